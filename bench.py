@@ -1,0 +1,180 @@
+"""Benchmark of the fused routed-expert MoE layer on one MI355X.
+
+Default workload (the headline config): int8 experts, decode M = 1 row, hidden 2048, expert FFN 768, 128 experts,
+top-8 softmax routing from N(0, 1) router logits, per-row int8 activations, bf16 output; 48 distinct layer tables
+(29 GB, far beyond the 256 MB Infinity Cache), the layers chained as a decode step chains them (each layer's output
+is the next one's input). A step is one token through the 48 layers; four HIP graphs hold four tokens with their own
+routing and are replayed in turn.
+
+    python bench.py [--steps K] [--warmup W] [--format int8|w4a8|w6a8|fp8] [--rows M] [--layers L]
+
+Prints one JSON line: metric (expert-weight GB/s), tokens/s, the roofline of the fused kernel (algorithmic bytes per
+launch / average launch time from HIP events on the replay stream, against 8 TB/s HBM) and the reference's CPU path
+timed on a bounded sample of the same workload on this host.
+"""
+import argparse
+import json
+import os
+import pathlib
+import sys
+import time
+
+ROOT = pathlib.Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "comfyui-drama3_amd"))
+
+import torch  # noqa: E402
+
+from drama3 import formats, moe  # noqa: E402
+
+METRIC = "MoE-layer expert-weight HBM GB/s (% of peak) at M=1; decode tokens/s"
+PEAK_GBS = 8000.0
+FORMATS = {"int8": formats.FMT_I8, "w4a8": formats.FMT_W4, "w6a8": formats.FMT_W6, "fp8": formats.FMT_F8}
+H, I, E, TOPK = 2048, 768, 128, 8
+GRAPH_TOKENS = 4
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def make_layers(fmt, layers, device, seed=0):
+    gen = torch.Generator(device=device).manual_seed(seed)
+    banks = []
+    for _ in range(layers):
+        gu = torch.randn((E, 2 * I, H), generator=gen, device=device) * 0.02
+        gate_up = formats.quantize(gu, fmt)
+        del gu
+        dn = torch.randn((E, H, I), generator=gen, device=device) * 0.02
+        down = formats.quantize(dn, fmt)
+        del dn
+        banks.append((gate_up, down))
+    return banks
+
+
+def expert_bytes(gate_up, down):
+    return gate_up.expert_bytes() + down.expert_bytes()
+
+
+def cpu_baseline(banks, fmt, logits, x, budget_s=12.0):
+    """The reference's CPU path (oracle/cpu_path.py) on this host: bf16 matmuls from the quantized banks per routed
+    expert, one row, over a sample of the same layers and routing; GB/s over the same algorithmic bytes."""
+    from oracle import cpu_path
+    threads = min(16, len(os.sched_getaffinity(0)))
+    torch.set_num_threads(threads)
+    sample_layers = min(2, len(banks))
+    host = [tuple((b.weight.cpu(), b.scale.cpu()) for b in pair) for pair in banks[:sample_layers]]
+    per_layer_bytes = TOPK * expert_bytes(*banks[0]) + 2 * H * 2 + E * 2
+    xs = x[0, :1].cpu()
+    lg = logits.cpu()
+    done, started = 0, time.perf_counter()
+    tokens = lg.shape[0]
+    while time.perf_counter() - started < budget_s:
+        t, layer = done % tokens, done % sample_layers
+        w, ids = torch.softmax(lg[t, layer, 0].float(), -1).topk(TOPK)
+        w = (w / w.sum()).to(torch.bfloat16)
+        cpu_path.layer(xs, ids, w, host[layer][0], host[layer][1], fmt, H, I)
+        done += 1
+    elapsed = time.perf_counter() - started
+    return {"value": round(per_layer_bytes * done / elapsed / 1e9, 3), "unit": "GB/s", "cores": threads,
+            "kind": "port", "tokens_per_s": round(done / elapsed / len(banks), 3),
+            "sample": f"{done} layer passes (M=1, top-8) over {sample_layers} of the layers, {elapsed:.1f} s, "
+                      f"torch {threads} threads: _weight_int8pack_mm / dequantize-then-linear per expert"}
+
+
+def main():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=100)
+    p.add_argument("--warmup", type=int, default=8)
+    p.add_argument("--format", default="int8", choices=sorted(FORMATS))
+    p.add_argument("--rows", type=int, default=1)
+    p.add_argument("--layers", type=int, default=48)
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    args = p.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: the routed-expert path runs on one MI355X (see DESIGN.md for how it would "
+              "shard); run it with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+    fmt = FORMATS[args.format]
+    device = torch.device("cuda:0")
+    torch.cuda.set_device(device)
+    M, L = args.rows, args.layers
+
+    log(f"building {L} layers of {args.format} experts")
+    banks = make_layers(fmt, L, device)
+    gen = torch.Generator(device=device).manual_seed(1)
+    logits = torch.randn((GRAPH_TOKENS, L, M, E), generator=gen, device=device).to(torch.bfloat16)
+    x0 = torch.randn((GRAPH_TOKENS, M, H), generator=gen, device=device).to(torch.bfloat16)
+
+    # routing of every (token, layer), for the exact count of experts each launch reads
+    unique = []
+    for t in range(GRAPH_TOKENS):
+        x = x0[t]
+        for layer, (gate_up, down) in enumerate(banks):
+            x, ids, _ = moe.moe_layer(x, logits[t, layer], gate_up, down, TOPK, routing=True)
+            unique.append(len(torch.unique(ids)))
+    torch.cuda.synchronize()
+    per_expert = expert_bytes(*banks[0])
+    act_bytes = M * (2 * H * 2 + E * 2)
+    bytes_per_token = [sum(unique[t * L:(t + 1) * L]) * per_expert + L * act_bytes for t in range(GRAPH_TOKENS)]
+
+    stream = torch.cuda.Stream(device)
+    stream.wait_stream(torch.cuda.current_stream(device))
+    graphs, outs = [], []
+    with torch.cuda.stream(stream):
+        moe.prepare(device, H, I, stream)
+        bufs = [x0[t].clone() for t in range(GRAPH_TOKENS)]
+        for t in range(GRAPH_TOKENS):
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=stream):
+                x = bufs[t]
+                for layer, (gate_up, down) in enumerate(banks):
+                    x = moe.moe_layer(x, logits[t, layer], gate_up, down, TOPK)
+            graphs.append(g)
+            outs.append(x)
+        for i in range(args.warmup):
+            graphs[i % GRAPH_TOKENS].replay()
+        stream.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        for i in range(args.steps):
+            graphs[i % GRAPH_TOKENS].replay()
+        end.record(stream)
+        end.synchronize()
+    torch.cuda.synchronize()
+    status = moe.status(device, H, I, stream)
+    if status:
+        raise RuntimeError(f"fused layer reported status {status}")
+    ms = start.elapsed_time(end)
+    total_bytes = sum(bytes_per_token[i % GRAPH_TOKENS] for i in range(args.steps))
+    gbs = total_bytes / (ms * 1e-3) / 1e9
+    launches = args.steps * L
+    launch_us = ms * 1e3 / launches
+    bytes_per_launch = total_bytes / launches
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("timing the reference's CPU path")
+        cpu = cpu_baseline(banks, fmt, logits, x0)
+
+    line = {
+        "metric": METRIC, "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms / args.steps, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": {"int8": "int8", "w4a8": "int4xint8", "w6a8": "int6xint8", "fp8": "fp8e4m3"}[args.format],
+        "data": "synthetic: weights N(0, 0.02) quantized, activations and router logits N(0, 1), seeded",
+        "config": {"workload": f"routed-expert MoE layer, {args.format} experts, decode M={M}, hidden {H}, FFN {I}, "
+                               f"{E} experts top-{TOPK}, {L} layers chained per token",
+                   "rows": M, "layers": L, "tokens_per_s": round(args.steps * M / (ms * 1e-3), 2),
+                   "pct_of_peak_hbm": round(100 * gbs / PEAK_GBS, 2),
+                   "unique_experts_per_launch": round(sum(unique) / len(unique), 2),
+                   "bytes_per_launch": int(bytes_per_launch)},
+        "roofline": {"bound": "hbm", "achieved": round(bytes_per_launch / (launch_us * 1e-6) / 1e9, 1),
+                     "peak": PEAK_GBS, "unit": "GB/s", "frac": round(bytes_per_launch / (launch_us * 1e-6) / 1e9 / PEAK_GBS, 4),
+                     "traffic": None, "kernel": "d3::moe_a8_kernel", "launch_us": round(launch_us, 3)},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

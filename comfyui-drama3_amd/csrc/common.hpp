@@ -1,0 +1,138 @@
+// Device helpers shared by every kernel of the routed-expert path: bfloat16 and float8 conversions, wave64
+// reductions over DPP, and the MFMA step types. gfx950 (CDNA4) only.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef int i32x2 __attribute__((ext_vector_type(2)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+#define D3_INLINE __device__ __forceinline__
+
+// ---------------------------------------------------------------------------------------------------------------
+// bfloat16 <-> float. The narrowing rounds to nearest, ties to even, as a cast does (kernels.py:33-37 rounds the same
+// way); NaN stays NaN.
+D3_INLINE float bf16_to_f32(uint32_t b) { return __uint_as_float(b << 16); }
+D3_INLINE uint32_t f32_to_bf16(float v) {
+  uint32_t b = __float_as_uint(v);
+  if ((b & 0x7FFFFFFFu) > 0x7F800000u) return (b >> 16) | 0x40u;
+  return (b + 0x7FFFu + ((b >> 16) & 1u)) >> 16;
+}
+D3_INLINE float bf16_round(float v) { return bf16_to_f32(f32_to_bf16(v)); }
+
+// float8 e4m3fn -> float through the hardware converter (OCP e4m3fn on gfx950: 0x7F / 0xFF are NaN). `word` holds
+// four codes; HI picks bytes 2-3 instead of 0-1.
+template <bool HI> D3_INLINE f32x2 fp8x2_to_f32(uint32_t word) { return __builtin_amdgcn_cvt_pk_f32_fp8((int)word, HI); }
+
+// float -> float8 e4m3fn, to nearest and ties to even, saturating at +-448. Written from the format's definition
+// (1 sign, 4 exponent bits biased by 7, 3 mantissa bits, no infinities): the value is rounded on the e4m3 grid of its
+// binade (step 2^(e-3), or 2^-9 below 2^-6), which rintf does exactly after scaling by a power of two.
+D3_INLINE uint32_t f32_to_fp8(float v) {
+  uint32_t sign = (__float_as_uint(v) >> 24) & 0x80u;
+  float a = fabsf(v);
+  if (!(a == a)) return sign | 0x7Fu;   // NaN
+  if (a >= 464.0f) return sign | 0x7Eu; // saturate (448 is the largest finite; 464 is the midpoint to 512)
+  int e = (int)((__float_as_uint(a) >> 23) & 0xFFu) - 127;  // a's binade
+  if (e < -6) e = -6;                                        // subnormal range shares 2^-6's step
+  float inv_step = __uint_as_float((uint32_t)(3 - e + 127) << 23);  // 2^(3-e)
+  float m = rintf(a * inv_step);  // exact scaling by a power of two, then round half to even
+  // m in [8, 16] for normals (16 means a carry into the next binade), [0, 8] for subnormals
+  uint32_t code;
+  if (m >= 16.0f) { e += 1; m = 8.0f; }
+  if (m < 8.0f) {
+    code = (uint32_t)m;  // subnormal (e == -6): exponent field 0
+  } else {
+    code = ((uint32_t)(e + 7) << 3) | ((uint32_t)m - 8u);
+  }
+  if (code > 0x7Eu) code = 0x7Eu;
+  return sign | code;
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// Wave64 reductions. DPP within each row of 16 lanes (quad swaps, half-row and row mirrors), then the four row results
+// read into scalars. Every lane gets the result; the order of combination is fixed, so float sums are deterministic.
+D3_INLINE int dpp_i32(int v, int ctrl) {
+  switch (ctrl) {
+    case 0xB1: return __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false);
+    case 0x4E: return __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false);
+    case 0x141: return __builtin_amdgcn_update_dpp(0, v, 0x141, 0xF, 0xF, false);
+    default: return __builtin_amdgcn_update_dpp(0, v, 0x140, 0xF, 0xF, false);
+  }
+}
+
+D3_INLINE uint32_t wave_max_u32(uint32_t v) {
+  v = max(v, (uint32_t)dpp_i32((int)v, 0xB1));   // quad_perm [1,0,3,2]
+  v = max(v, (uint32_t)dpp_i32((int)v, 0x4E));   // quad_perm [2,3,0,1]
+  v = max(v, (uint32_t)dpp_i32((int)v, 0x141));  // row_half_mirror
+  v = max(v, (uint32_t)dpp_i32((int)v, 0x140));  // row_mirror
+  uint32_t a = __builtin_amdgcn_readlane((int)v, 0), b = __builtin_amdgcn_readlane((int)v, 16);
+  uint32_t c = __builtin_amdgcn_readlane((int)v, 32), d = __builtin_amdgcn_readlane((int)v, 48);
+  return max(max(a, b), max(c, d));
+}
+
+D3_INLINE float wave_max_f32(float v) {
+  v = fmaxf(v, __int_as_float(dpp_i32(__float_as_int(v), 0xB1)));
+  v = fmaxf(v, __int_as_float(dpp_i32(__float_as_int(v), 0x4E)));
+  v = fmaxf(v, __int_as_float(dpp_i32(__float_as_int(v), 0x141)));
+  v = fmaxf(v, __int_as_float(dpp_i32(__float_as_int(v), 0x140)));
+  float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+  float c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+  float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+  return fmaxf(fmaxf(a, b), fmaxf(c, d));
+}
+
+D3_INLINE float wave_sum_f32(float v) {
+  v += __int_as_float(dpp_i32(__float_as_int(v), 0xB1));
+  v += __int_as_float(dpp_i32(__float_as_int(v), 0x4E));
+  v += __int_as_float(dpp_i32(__float_as_int(v), 0x141));
+  v += __int_as_float(dpp_i32(__float_as_int(v), 0x140));
+  float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+  float c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+  float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+  return (a + b) + (c + d);
+}
+
+D3_INLINE int wave_sum_i32(int v) {
+  v += dpp_i32(v, 0xB1);
+  v += dpp_i32(v, 0x4E);
+  v += dpp_i32(v, 0x141);
+  v += dpp_i32(v, 0x140);
+  return __builtin_amdgcn_readlane(v, 0) + __builtin_amdgcn_readlane(v, 16) + __builtin_amdgcn_readlane(v, 32) +
+         __builtin_amdgcn_readlane(v, 48);
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// Device-scope signalling between workgroups of one launch (the fused layer's gate_up -> down hand-off). Producers
+// publish with a release add; consumers poll with relaxed loads, then acquire. Waits are bounded: past `limit` polls
+// the consumer records an error in `status` and goes on, so a broken hand-off can never hang the device.
+D3_INLINE void signal_add(uint32_t* counter, uint32_t v) {
+  __hip_atomic_fetch_add(counter, v, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+}
+D3_INLINE uint32_t signal_add_acq_rel(uint32_t* counter, uint32_t v) {
+  return __hip_atomic_fetch_add(counter, v, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+}
+D3_INLINE uint32_t signal_load(const uint32_t* counter) {
+  return __hip_atomic_load(counter, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+D3_INLINE void signal_store(uint32_t* counter, uint32_t v) {
+  __hip_atomic_store(counter, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+D3_INLINE bool wait_at_least(const uint32_t* counter, uint32_t target, uint32_t* status, uint32_t limit) {
+  uint32_t polls = 0;
+  while (signal_load(counter) < target) {
+    // after one timeout in this launch the rest give up at once: a broken hand-off costs one bounded wait, not many
+    if (signal_load(status) != 0u) return false;
+    __builtin_amdgcn_s_sleep(2);
+    if (++polls > limit) {
+      __hip_atomic_fetch_or(status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      return false;
+    }
+  }
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  return true;
+}

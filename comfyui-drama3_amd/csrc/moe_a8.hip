@@ -1,0 +1,707 @@
+// The fused routed-expert MoE layer for A8 expert banks (int8, W4, W6 or FP8 weights; int8 or e4m3 activations
+// quantized per row): route -> gate_up -> SiLU(gate) * up -> down -> routing-weighted sum, in one launch.
+//
+// This replaces the reference's chain of launches for one decode row (drama3/offload.py:108-123: rotate, gemv,
+// rotate(swiglu), gemv, weighted_sum, after kernels.route at drama3/model.py:116-118) and its row-by-row loop over
+// batched lines (drama3/model.py:111-113): M rows share one launch and every expert any of them routes to is read
+// once.
+//
+// Work decomposition. Every workgroup (4 waves) first routes all M rows (top-k of the router logits, softmax over the
+// k, bf16-rounded weights: kernels.py:39-67's semantics), builds the sorted union of their experts (U of them) and
+// groups it into down chunks of at most 8 experts and 32 (expert, row) pairs. It quantizes the activations into LDS.
+// Then it takes work items round-robin (item, item + gridDim, ...):
+//   gate_up item (u, tile): gate rows 8 tile .. 8 tile + 7 and the matching up rows of expert u, one 16-row MFMA tile
+//     over K = H (the 4 waves split K); the expert's rows are the MFMA columns. The epilogue applies the scales and
+//     SiLU(gate) * up, writes 8 hidden units per row to `hidden`, and counts the tile done for expert u.
+//   down item (chunk c, block b): output rows 8 b .. 8 b + 7 of every expert of the chunk, over K = I. Each wave packs
+//     two experts into one 16-row MFMA tile (rows 0-7 and 8-15) with both experts' rows as columns. It loads its
+//     weights first, then waits until every gate_up tile of its chunk is done, quantizes the chunk's hidden rows into
+//     LDS and runs. When the chunk holds every expert (always for M = 1) it writes the weighted sum straight to `out`;
+//     otherwise it stores its outputs in `parts`, and the last chunk to finish block b sums them.
+// Items are ordered gate_up(chunk 0), gate_up(chunk 1), down(chunk 0), gate_up(chunk 2), down(chunk 1), ...: every
+// wait is on items of lower index. The grid is at most what the device holds at once, so every workgroup is resident
+// and the lowest unfinished item can always run: no wait can block forever. Waits are bounded anyway (spin_limit),
+// and a timeout sets sync[SYNC_STATUS].
+//
+// Synchronisation state lives in `sync` (zeroed once by the caller); the last down item to pass its wait and the last
+// finisher of each block put it back to zero, so consecutive launches on one stream (or graph replays) reuse it.
+// Launches that overlap on one `sync` race.
+#include "formats.hpp"
+#include "../../include/drama3_moe.h"
+
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <string>
+#include <tuple>
+
+namespace d3 {
+
+enum : int { SYNC_DONE = 0, SYNC_HBLOCK = 256, SYNC_PASSED = 512, SYNC_STATUS = 513, SYNC_WORDS = 1024 };
+constexpr int MAX_M = 16, MAX_K = 8, MAX_E = 256, MAX_PAIRS = MAX_M * MAX_K;
+constexpr int CHUNK_EXPERTS = 8, CHUNK_PAIRS = 32;
+
+struct MoeA8Args {
+  const uint16_t* x;
+  const uint16_t* logits;
+  const uint8_t* gu_w;
+  const uint16_t* gu_s;
+  const uint8_t* dn_w;
+  const uint16_t* dn_s;
+  uint16_t* out;
+  int64_t* ids_out;
+  float* weights_out;
+  float* hidden;
+  float* parts;
+  uint32_t* sync;
+  int M, E, topk;
+  uint32_t spin_limit;
+};
+
+// LDS carve-up (bytes), shared by host (launch size) and device.
+struct Lds {
+  int xq, sx, rt_id, rt_w, emask, ulist, ucount, utok, upair, chunk_first, misc, red, hq, hs, lparts, slot_pair,
+      pair_slot, slot_first, total;
+  __host__ __device__ Lds(int M, int H, int I) {
+    int o = 0;
+    auto take = [&](int bytes) { int at = o; o += (bytes + 15) & ~15; return at; };
+    xq = take(M * H);
+    sx = take(MAX_M * 4);
+    rt_id = take(MAX_M * MAX_K * 4);
+    rt_w = take(MAX_M * MAX_K * 4);
+    emask = take(MAX_E * 4);
+    ulist = take(MAX_E * 4);
+    ucount = take(MAX_E * 4);
+    utok = take(MAX_PAIRS * MAX_M);
+    upair = take(MAX_PAIRS * MAX_M);
+    chunk_first = take((MAX_PAIRS + 1) * 4);
+    misc = take(64);
+    red = take(2 * 4 * 256 * 4);
+    hq = take(CHUNK_PAIRS * I);
+    hs = take(CHUNK_PAIRS * 4);
+    lparts = take(CHUNK_PAIRS * 8 * 4);
+    slot_pair = take(CHUNK_PAIRS * 4);
+    pair_slot = take(MAX_PAIRS * 4);
+    slot_first = take((CHUNK_EXPERTS + 1) * 4);
+    total = o;
+  }
+};
+
+template <int F> __host__ __device__ constexpr float act_qmax() { return F == FMT_F8 ? 448.0f : 127.0f; }
+
+// quantize 8 activations with `inv`, store them in the format's storage order
+template <int F> D3_INLINE void store_act8(uint8_t* dst, const float* v, float inv) {
+  uint32_t b[8];
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    if constexpr (F == FMT_F8) {
+      b[i] = f32_to_fp8(v[i] * inv);
+    } else {
+      float r = rintf(v[i] * inv);
+      r = fminf(fmaxf(r, -127.0f), 127.0f);
+      b[i] = (uint32_t)((int)r) & 0xFFu;
+    }
+  }
+  uint32_t lo, hi;
+  if constexpr (F == FMT_W4) {
+    lo = b[0] | (b[2] << 8) | (b[4] << 16) | (b[6] << 24);
+    hi = b[1] | (b[3] << 8) | (b[5] << 16) | (b[7] << 24);
+  } else {
+    lo = b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24);
+    hi = b[4] | (b[5] << 8) | (b[6] << 16) | (b[7] << 24);
+  }
+  *(i32x2*)dst = i32x2{(int)lo, (int)hi};
+}
+
+// What a workgroup knows after its prologue.
+struct Ctx {
+  const MoeA8Args* a;
+  uint8_t* xq;
+  float* sx;
+  int* rt_id;
+  float* rt_w;
+  int* ulist;
+  int* ucount;
+  uint8_t* utok;
+  uint8_t* upair;
+  int* chunk_first;
+  int* misc;
+  float* red;
+  uint8_t* hq;
+  float* hs;
+  float* lparts;
+  int* slot_pair;
+  int* pair_slot;
+  int* slot_first;
+  int U, nch, n_dn;
+};
+
+// gate_up tile: gate rows 8 tile .. 8 tile + 7 and up rows I + 8 tile .. of expert u
+template <int F, int H, int I>
+D3_INLINE void gate_up_item(const Ctx& cx, int u, int tile, int parity) {
+  constexpr int SPW = H / 512;  // steps per wave
+  constexpr int RB = row_bytes(F, H);
+  constexpr int SHIFT = unpack_shift(F);
+  const MoeA8Args& a = *cx.a;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, q = lane >> 4, col = lane & 15;
+  const int e = cx.ulist[u], nu = cx.ucount[u];
+  const int ra = lane & 15;
+  const uint8_t* wp = a.gu_w + ((size_t)e * (2 * I) + (ra < 8 ? 8 * tile + ra : I + 8 * tile + ra - 8)) * RB;
+  Raw<F> raw[SPW];
+#pragma unroll
+  for (int s = 0; s < SPW; s++) load_step<F>(raw[s], wp, w * SPW + s, q);
+  float sc[SPW][4];
+  if constexpr (group_scaled(F)) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int rc = 4 * q + i;
+      const size_t srow = (size_t)e * (2 * I) + (rc < 8 ? 8 * tile + rc : I + 8 * tile + rc - 8);
+#pragma unroll
+      for (int s = 0; s < SPW; s++) sc[s][i] = bf16_to_f32(a.gu_s[srow * (H / 128) + w * SPW + s]);
+    }
+  }
+  const bool active = col < nu;
+  const uint8_t* xp = cx.xq + (size_t)(active ? cx.utok[u * MAX_M + col] : 0) * H;
+  i32x4 iacc = {0, 0, 0, 0};
+  f32x4 facc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int s = 0; s < SPW; s++) {
+    i32x4 xlo = {0, 0, 0, 0}, xhi = {0, 0, 0, 0};
+    if (active) {
+      const uint8_t* p = xp + 128 * (w * SPW + s) + 32 * q;
+      xlo = *(const i32x4*)p;
+      xhi = *(const i32x4*)(p + 16);
+    }
+    if constexpr (F == FMT_I8) {
+      iacc = step_i8<F>(raw[s], xlo, xhi, iacc);
+    } else if constexpr (F == FMT_F8) {
+      facc = step_f8(raw[s], xlo, xhi, facc);
+    } else {
+      const i32x4 g = step_i8<F>(raw[s], xlo, xhi, i32x4{0, 0, 0, 0});
+#pragma unroll
+      for (int i = 0; i < 4; i++) facc[i] += (float)(g[i] >> SHIFT) * sc[s][i];
+    }
+  }
+  float* rd = cx.red + parity * 1024;
+#pragma unroll
+  for (int i = 0; i < 4; i++) rd[w * 256 + (4 * q + i) * 16 + col] = F == FMT_I8 ? __int_as_float(iacc[i]) : facc[i];
+  __syncthreads();
+  if (w == 0) {
+    for (int idx = lane; idx < 8 * nu; idx += 64) {
+      const int n = idx >> 3, j = idx & 7;
+      float g, up;
+      if constexpr (F == FMT_I8) {
+        int gi = 0, ui = 0;
+#pragma unroll
+        for (int ww = 0; ww < 4; ww++) {
+          gi += __float_as_int(rd[ww * 256 + j * 16 + n]);
+          ui += __float_as_int(rd[ww * 256 + (8 + j) * 16 + n]);
+        }
+        g = (float)gi;
+        up = (float)ui;
+      } else {
+        g = 0.0f;
+        up = 0.0f;
+#pragma unroll
+        for (int ww = 0; ww < 4; ww++) {
+          g += rd[ww * 256 + j * 16 + n];
+          up += rd[ww * 256 + (8 + j) * 16 + n];
+        }
+      }
+      if constexpr (!group_scaled(F)) {
+        g *= bf16_to_f32(a.gu_s[(size_t)e * (2 * I) + 8 * tile + j]);
+        up *= bf16_to_f32(a.gu_s[(size_t)e * (2 * I) + I + 8 * tile + j]);
+      }
+      const float s = cx.sx[cx.utok[u * MAX_M + n]];
+      g *= s;
+      up *= s;
+      a.hidden[(size_t)cx.upair[u * MAX_M + n] * I + 8 * tile + j] = g / (1.0f + __expf(-g)) * up;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    if (lane == 0) signal_add(&a.sync[SYNC_DONE + u], 1u);
+  }
+}
+
+// down block: output rows 8 hb .. 8 hb + 7 of the experts of chunk c
+template <int F, int H, int I>
+D3_INLINE void down_item(const Ctx& cx, int c, int hb) {
+  constexpr int T = I / 8;
+  constexpr int STEPS = I / 128;
+  constexpr int RB = row_bytes(F, I);
+  constexpr int SHIFT = unpack_shift(F);
+  constexpr float QMAX = act_qmax<F>();
+  const MoeA8Args& a = *cx.a;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, q = lane >> 4, col = lane & 15;
+  const int M = a.M, K8 = a.topk;
+  const int u0 = cx.chunk_first[c], ne = cx.chunk_first[c + 1] - u0;
+  int* slot_first = cx.slot_first;
+  __syncthreads();  // the previous item's readers of the slot tables and partial outputs are done
+
+  // this lane's weight row: local expert 2w + (row / 8), output row 8 hb + row % 8
+  const int ra = lane & 15;
+  const int lj_a = 2 * w + (ra >> 3);
+  Raw<F> raw[STEPS] = {};
+  if (lj_a < ne) {
+    const int e = cx.ulist[u0 + lj_a];
+    const uint8_t* wp = a.dn_w + ((size_t)e * H + 8 * hb + (ra & 7)) * RB;
+#pragma unroll
+    for (int s = 0; s < STEPS; s++) load_step<F>(raw[s], wp, s, q);
+  }
+  // scales of this lane's accumulator rows 4q + i: local expert 2w + q / 2, output row 8 hb + 4 (q % 2) + i
+  const int lj_c = 2 * w + (q >> 1);
+  const int e_c = lj_c < ne ? cx.ulist[u0 + lj_c] : 0;
+  float sc[STEPS][4];
+  if constexpr (group_scaled(F)) {
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+      for (int s = 0; s < STEPS; s++)
+        sc[s][i] = lj_c < ne ? bf16_to_f32(a.dn_s[((size_t)e_c * H + 8 * hb + 4 * (q & 1) + i) * (I / 128) + s]) : 0.0f;
+  }
+  if (tid == 0) {
+    int slot = 0;
+    for (int lj = 0; lj < ne; lj++) {
+      const int uu = u0 + lj;
+      slot_first[lj] = slot;
+      for (int n = 0; n < cx.ucount[uu]; n++) {
+        const int p = cx.upair[uu * MAX_M + n];
+        cx.slot_pair[slot] = p;
+        cx.pair_slot[p] = slot;
+        slot++;
+      }
+    }
+    slot_first[ne] = slot;
+    for (int lj = 0; lj < ne; lj++)
+      wait_at_least(&a.sync[SYNC_DONE + u0 + lj], (uint32_t)T, &a.sync[SYNC_STATUS], a.spin_limit);
+    const uint32_t passed = signal_add_acq_rel(&a.sync[SYNC_PASSED], 1u);
+    if (passed == (uint32_t)cx.n_dn - 1u) {
+      // every down item is past its wait: clear the counters for the next launch
+      for (int uu = 0; uu < cx.U; uu++) signal_store(&a.sync[SYNC_DONE + uu], 0u);
+      signal_store(&a.sync[SYNC_PASSED], 0u);
+    }
+  }
+  __syncthreads();
+  const int P = slot_first[ne];
+  // the chunk's hidden rows, quantized per (expert, row) pair into LDS: one wave per pair
+  constexpr int G8 = I / 8;
+  for (int slot = w; slot < P; slot += 4) {
+    const float* hp = a.hidden + (size_t)cx.slot_pair[slot] * I;
+    float v[(G8 + 63) / 64][8];
+    float amax = 0.0f;
+#pragma unroll
+    for (int k = 0; k < (G8 + 63) / 64; k++) {
+      const int g8 = lane + 64 * k;
+      if (g8 < G8) {
+        const f32x4 p0 = *(const f32x4*)(hp + 8 * g8), p1 = *(const f32x4*)(hp + 8 * g8 + 4);
+        v[k][0] = p0.x; v[k][1] = p0.y; v[k][2] = p0.z; v[k][3] = p0.w;
+        v[k][4] = p1.x; v[k][5] = p1.y; v[k][6] = p1.z; v[k][7] = p1.w;
+#pragma unroll
+        for (int i = 0; i < 8; i++) amax = fmaxf(amax, fabsf(v[k][i]));
+      }
+    }
+    amax = wave_max_f32(amax);
+    const float inv = amax > 0.0f ? QMAX / amax : 0.0f;
+#pragma unroll
+    for (int k = 0; k < (G8 + 63) / 64; k++) {
+      const int g8 = lane + 64 * k;
+      if (g8 < G8) store_act8<F>(cx.hq + (size_t)slot * I + 8 * g8, v[k], inv);
+    }
+    if (lane == 0) cx.hs[slot] = amax / QMAX;
+  }
+  __syncthreads();
+  if (2 * w < ne) {
+    const int la = 2 * w, lb = 2 * w + 1;
+    const int na = slot_first[la + 1] - slot_first[la];
+    const int nb = lb < ne ? slot_first[lb + 1] - slot_first[lb] : 0;
+    const bool one_pass = na + nb <= 16;
+    const bool rows_b = q >= 2;
+    for (int pass = 0; pass < (one_pass ? 1 : 2); pass++) {
+      // columns: pass 0 = a's pairs (then b's, in one pass); pass 1 = b's pairs
+      int slot = -1;
+      if (pass == 0) {
+        if (col < na) slot = slot_first[la] + col;
+        else if (one_pass && col < na + nb) slot = slot_first[lb] + col - na;
+      } else if (col < nb) {
+        slot = slot_first[lb] + col;
+      }
+      const uint8_t* xp = cx.hq + (size_t)(slot >= 0 ? slot : 0) * I;
+      i32x4 iacc = {0, 0, 0, 0};
+      f32x4 facc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int s = 0; s < STEPS; s++) {
+        i32x4 xlo = {0, 0, 0, 0}, xhi = {0, 0, 0, 0};
+        if (slot >= 0) {
+          xlo = *(const i32x4*)(xp + 128 * s + 32 * q);
+          xhi = *(const i32x4*)(xp + 128 * s + 32 * q + 16);
+        }
+        if constexpr (F == FMT_I8) {
+          iacc = step_i8<F>(raw[s], xlo, xhi, iacc);
+        } else if constexpr (F == FMT_F8) {
+          facc = step_f8(raw[s], xlo, xhi, facc);
+        } else {
+          const i32x4 g = step_i8<F>(raw[s], xlo, xhi, i32x4{0, 0, 0, 0});
+#pragma unroll
+          for (int i = 0; i < 4; i++) facc[i] += (float)(g[i] >> SHIFT) * sc[s][i];
+        }
+      }
+      // this lane's accumulator rows belong to expert a (q < 2) or b (q >= 2); keep the products of matching columns
+      const bool valid = slot >= 0 && (one_pass ? (rows_b ? col >= na : col < na) : (pass == 0 ? !rows_b : rows_b));
+      if (valid) {
+        const float hsc = cx.hs[slot];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          const int r = 4 * (q & 1) + i;
+          float y;
+          if constexpr (F == FMT_I8) y = (float)iacc[i] * bf16_to_f32(a.dn_s[(size_t)e_c * H + 8 * hb + r]);
+          else if constexpr (F == FMT_F8) y = facc[i] * bf16_to_f32(a.dn_s[(size_t)e_c * H + 8 * hb + r]);
+          else y = facc[i];
+          cx.lparts[slot * 8 + r] = y * hsc;
+        }
+      }
+    }
+  }
+  __syncthreads();
+  if (cx.nch == 1) {
+    // every row's experts are in this chunk
+    for (int idx = tid; idx < M * 8; idx += 256) {
+      const int t = idx >> 3, r = idx & 7;
+      float acc = 0.0f;
+      for (int j = 0; j < K8; j++) acc = fmaf(cx.lparts[cx.pair_slot[t * K8 + j] * 8 + r], cx.rt_w[t * MAX_K + j], acc);
+      a.out[(size_t)t * H + 8 * hb + r] = (uint16_t)f32_to_bf16(acc);
+    }
+  } else {
+    for (int idx = tid; idx < P * 8; idx += 256) {
+      const int slot = idx >> 3, r = idx & 7;
+      a.parts[(size_t)cx.slot_pair[slot] * H + 8 * hb + r] = cx.lparts[slot * 8 + r];
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    __syncthreads();
+    if (tid == 0) {
+      const uint32_t old = signal_add_acq_rel(&a.sync[SYNC_HBLOCK + hb], 1u);
+      const int last = old == (uint32_t)cx.nch - 1u;
+      if (last) signal_store(&a.sync[SYNC_HBLOCK + hb], 0u);
+      cx.misc[2] = last;
+    }
+    __syncthreads();
+    if (cx.misc[2]) {
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+      for (int idx = tid; idx < M * 8; idx += 256) {
+        const int t = idx >> 3, r = idx & 7;
+        float acc = 0.0f;
+        for (int j = 0; j < K8; j++) acc = fmaf(a.parts[(size_t)(t * K8 + j) * H + 8 * hb + r], cx.rt_w[t * MAX_K + j], acc);
+        a.out[(size_t)t * H + 8 * hb + r] = (uint16_t)f32_to_bf16(acc);
+      }
+    }
+  }
+}
+
+template <int F, int H, int I>
+__global__ void __launch_bounds__(256, 4) moe_a8_kernel(MoeA8Args a) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  constexpr int T = I / 8;
+  constexpr int NHB = H / 8;
+  constexpr float QMAX = act_qmax<F>();
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int M = a.M, E = a.E, K8 = a.topk;
+  const Lds L(M, H, I);
+  Ctx cx;
+  cx.a = &a;
+  cx.xq = lds + L.xq;
+  cx.sx = (float*)(lds + L.sx);
+  cx.rt_id = (int*)(lds + L.rt_id);
+  cx.rt_w = (float*)(lds + L.rt_w);
+  uint32_t* emask = (uint32_t*)(lds + L.emask);
+  cx.ulist = (int*)(lds + L.ulist);
+  cx.ucount = (int*)(lds + L.ucount);
+  cx.utok = lds + L.utok;
+  cx.upair = lds + L.upair;
+  cx.chunk_first = (int*)(lds + L.chunk_first);
+  cx.misc = (int*)(lds + L.misc);
+  cx.red = (float*)(lds + L.red);
+  cx.hq = lds + L.hq;
+  cx.hs = (float*)(lds + L.hs);
+  cx.lparts = (float*)(lds + L.lparts);
+  cx.slot_pair = (int*)(lds + L.slot_pair);
+  cx.pair_slot = (int*)(lds + L.pair_slot);
+  cx.slot_first = (int*)(lds + L.slot_first);
+
+  // ---- routing: one wave per row
+  for (int t = w; t < M; t += 4) {
+    const uint16_t* lg = a.logits + (size_t)t * E;
+    uint32_t key[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const int e = lane + 64 * j;
+      uint32_t k = 0;
+      if (e < E) {
+        uint32_t b = lg[e];
+        if (b == 0x8000u) b = 0;  // -0 ranks as +0
+        const uint32_t ord = (b & 0x8000u) ? (~b & 0xFFFFu) : (b | 0x8000u);
+        k = (ord << 16) | (0xFFFFu - (uint32_t)e);  // larger logit first, then lower index
+      }
+      key[j] = k;
+    }
+    float top[MAX_K];
+    int ids[MAX_K];
+#pragma unroll
+    for (int r = 0; r < MAX_K; r++) {
+      top[r] = 0.0f;
+      ids[r] = 0;
+      if (r < K8) {
+        const uint32_t m = wave_max_u32(max(max(key[0], key[1]), max(key[2], key[3])));
+#pragma unroll
+        for (int j = 0; j < 4; j++) key[j] = key[j] == m ? 0u : key[j];
+        ids[r] = (int)(0xFFFFu - (m & 0xFFFFu));
+        const uint32_t ord = m >> 16;
+        top[r] = bf16_to_f32((ord & 0x8000u) ? (ord & 0x7FFFu) : (~ord & 0xFFFFu));
+      }
+    }
+    float total = 0.0f;
+#pragma unroll
+    for (int r = 0; r < MAX_K; r++)
+      if (r < K8) total += expf(top[r] - top[0]);
+#pragma unroll
+    for (int r = 0; r < MAX_K; r++) {
+      if (r < K8 && lane == r) {
+        cx.rt_id[t * MAX_K + r] = ids[r];
+        cx.rt_w[t * MAX_K + r] = bf16_round(expf(top[r] - top[0]) / total);
+      }
+    }
+  }
+  for (int e = tid; e < MAX_E; e += 256) emask[e] = 0;
+
+  // ---- activations: one wave per row, quantized per row (absmax / QMAX) into LDS
+  for (int t = w; t < M; t += 4) {
+    const uint16_t* xr = a.x + (size_t)t * H;
+    float v[H / 512][8];
+    float amax = 0.0f;
+#pragma unroll
+    for (int k = 0; k < H / 512; k++) {
+      const i32x4 raw = *(const i32x4*)(xr + 512 * k + 8 * lane);
+      const uint32_t wv[4] = {(uint32_t)raw.x, (uint32_t)raw.y, (uint32_t)raw.z, (uint32_t)raw.w};
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        v[k][2 * i] = bf16_to_f32(wv[i] & 0xFFFFu);
+        v[k][2 * i + 1] = bf16_to_f32(wv[i] >> 16);
+        amax = fmaxf(amax, fmaxf(fabsf(v[k][2 * i]), fabsf(v[k][2 * i + 1])));
+      }
+    }
+    amax = wave_max_f32(amax);
+    const float inv = amax > 0.0f ? QMAX / amax : 0.0f;
+#pragma unroll
+    for (int k = 0; k < H / 512; k++) store_act8<F>(cx.xq + (size_t)t * H + 512 * k + 8 * lane, v[k], inv);
+    if (lane == 0) cx.sx[t] = amax / QMAX;
+  }
+  __syncthreads();
+
+  // ---- union of the rows' experts, ascending
+  for (int i = tid; i < M * K8; i += 256) atomicOr(&emask[cx.rt_id[(i / K8) * MAX_K + i % K8]], 1u << (i / K8));
+  __syncthreads();
+  if (w == 0) {
+    int base = 0;
+    for (int k = 0; k < MAX_E / 64; k++) {
+      const int e = 64 * k + lane;
+      const uint32_t m = e < E ? emask[e] : 0u;
+      const uint64_t ball = __ballot(m != 0u);
+      const int pos = base + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(ball >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)ball, 0u));
+      if (m != 0u) cx.ulist[pos] = e;
+      base += __popcll(ball);
+    }
+    if (lane == 0) cx.misc[0] = base;
+  }
+  __syncthreads();
+  const int U = cx.misc[0];
+  for (int u = tid; u < U; u += 256) {
+    const int e = cx.ulist[u];
+    const uint32_t m = emask[e];
+    int n = 0;
+    for (int t = 0; t < M; t++) {
+      if (!((m >> t) & 1u)) continue;
+      int j = 0;
+      for (int jj = 0; jj < K8; jj++)
+        if (cx.rt_id[t * MAX_K + jj] == e) j = jj;
+      cx.utok[u * MAX_M + n] = (uint8_t)t;
+      cx.upair[u * MAX_M + n] = (uint8_t)(t * K8 + j);
+      n++;
+    }
+    cx.ucount[u] = n;
+  }
+  if (blockIdx.x == 0) {
+    for (int i = tid; i < M * K8; i += 256) {
+      if (a.ids_out) a.ids_out[i] = cx.rt_id[(i / K8) * MAX_K + i % K8];
+      if (a.weights_out) a.weights_out[i] = cx.rt_w[(i / K8) * MAX_K + i % K8];
+    }
+  }
+  __syncthreads();
+  // down chunks: consecutive experts, at most CHUNK_EXPERTS of them and CHUNK_PAIRS pairs
+  if (tid == 0) {
+    int nch = 0, ne = 0, np = 0;
+    cx.chunk_first[0] = 0;
+    for (int u = 0; u < U; u++) {
+      const int n = cx.ucount[u];
+      if (ne == CHUNK_EXPERTS || np + n > CHUNK_PAIRS) {
+        cx.chunk_first[++nch] = u;
+        ne = 0;
+        np = 0;
+      }
+      ne++;
+      np += n;
+    }
+    cx.chunk_first[++nch] = U;
+    cx.misc[1] = nch;
+  }
+  __syncthreads();
+  cx.U = U;
+  cx.nch = cx.misc[1];
+  cx.n_dn = cx.nch * NHB;
+  const int n_items = U * T + cx.n_dn;
+  int parity = 0;
+  for (int item = blockIdx.x; item < n_items; item += gridDim.x) {
+    // segments: gate_up(chunk c), then down(chunk c - 1)
+    int base = 0;
+    for (int c = 0; c <= cx.nch; c++) {
+      if (c < cx.nch) {
+        const int u0 = cx.chunk_first[c], ne = cx.chunk_first[c + 1] - u0;
+        if (item < base + ne * T) {
+          gate_up_item<F, H, I>(cx, u0 + (item - base) / T, (item - base) % T, parity);
+          parity ^= 1;
+          break;
+        }
+        base += ne * T;
+      }
+      if (c >= 1) {
+        if (item < base + NHB) {
+          down_item<F, H, I>(cx, c - 1, item - base);
+          break;
+        }
+        base += NHB;
+      }
+    }
+  }
+}
+
+}  // namespace d3
+
+
+// =====================================================================================================================
+// Host side
+namespace d3 {
+
+thread_local std::string g_error;
+int fail(const std::string& msg) {
+  g_error = msg;
+  return D3_EINVAL;
+}
+int hip_fail(hipError_t err, const char* what) {
+  g_error = std::string(what) + ": " + hipGetErrorString(err);
+  return (int)err;
+}
+
+int64_t moe_a8_workspace_bytes(int M, int topk, int H, int I) {
+  const int64_t pairs = (int64_t)M * topk;
+  return SYNC_WORDS * 4 + pairs * I * 4 + pairs * H * 4;
+}
+
+using KernelFn = void (*)(MoeA8Args);
+
+template <int F, int H, int I> KernelFn kernel_of() { return moe_a8_kernel<F, H, I>; }
+
+KernelFn pick_kernel(int fmt, int H, int I) {
+#define D3_CASE(F, HH, II) \
+  if (fmt == F && H == HH && I == II) return kernel_of<F, HH, II>();
+#define D3_SHAPES(F) D3_CASE(F, 2048, 768) D3_CASE(F, 2048, 512)
+  D3_SHAPES(FMT_I8) D3_SHAPES(FMT_W4) D3_SHAPES(FMT_W6) D3_SHAPES(FMT_F8)
+#undef D3_SHAPES
+#undef D3_CASE
+  return nullptr;
+}
+
+// workgroups the device holds at once for a kernel and LDS size (cached per device)
+int resident_capacity(KernelFn fn, int lds_bytes, int* err) {
+  static std::mutex mu;
+  static std::map<std::tuple<int, void*, int>, int> cache;
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) { *err = hip_fail(e, "hipGetDevice"); return 0; }
+  std::lock_guard<std::mutex> lock(mu);
+  auto key = std::make_tuple(dev, (void*)fn, lds_bytes);
+  auto it = cache.find(key);
+  if (it != cache.end()) return it->second;
+  int per_cu = 0, cus = 0;
+  e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void*)fn, 256, lds_bytes);
+  if (e != hipSuccess) { *err = hip_fail(e, "hipOccupancyMaxActiveBlocksPerMultiprocessor"); return 0; }
+  e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  if (e != hipSuccess) { *err = hip_fail(e, "hipDeviceGetAttribute"); return 0; }
+  int cap = per_cu * cus;
+  cache[key] = cap;
+  return cap;
+}
+
+int launch_moe_a8(const d3_moe_a8_desc* d, hipStream_t stream) {
+  if (!d) return fail("d3_moe_a8: null descriptor");
+  if (d->M < 1 || d->M > MAX_M) return fail("d3_moe_a8: M must be 1..16");
+  if (d->topk < 1 || d->topk > MAX_K) return fail("d3_moe_a8: topk must be 1..8");
+  if (d->E < d->topk || d->E > MAX_E) return fail("d3_moe_a8: E must be topk..256");
+  KernelFn fn = pick_kernel(d->format, d->H, d->I);
+  if (!fn) return fail("d3_moe_a8: no kernel for this format and shape (H 2048; I 512 or 768)");
+  if (!d->x || !d->logits || !d->gate_up || !d->gate_up_scale || !d->down || !d->down_scale || !d->out || !d->workspace)
+    return fail("d3_moe_a8: null pointer");
+  const int64_t need = moe_a8_workspace_bytes(d->M, d->topk, d->H, d->I);
+  if (d->workspace_bytes < need) return fail("d3_moe_a8: workspace too small");
+  const Lds L(d->M, d->H, d->I);
+  int err = 0;
+  const int cap = resident_capacity(fn, L.total, &err);
+  if (err) return err;
+  if (cap < 1) return fail("d3_moe_a8: the kernel does not fit on a compute unit");
+  const int umax = d->M * d->topk < d->E ? d->M * d->topk : d->E;
+  // chunks hold up to 8 experts and 32 pairs; a chunk per expert bounds their count
+  const int nch = umax;
+  const int items = umax * (d->I / 8) + nch * (d->H / 8);
+  int grid = items < cap ? items : cap;
+  if (d->grid > 0) grid = d->grid < grid ? d->grid : grid;
+
+  MoeA8Args a;
+  a.x = (const uint16_t*)d->x;
+  a.logits = (const uint16_t*)d->logits;
+  a.gu_w = (const uint8_t*)d->gate_up;
+  a.gu_s = (const uint16_t*)d->gate_up_scale;
+  a.dn_w = (const uint8_t*)d->down;
+  a.dn_s = (const uint16_t*)d->down_scale;
+  a.out = (uint16_t*)d->out;
+  a.ids_out = d->ids_out;
+  a.weights_out = d->weights_out;
+  uint8_t* ws = (uint8_t*)d->workspace;
+  a.sync = (uint32_t*)ws;
+  a.hidden = (float*)(ws + SYNC_WORDS * 4);
+  a.parts = a.hidden + (size_t)d->M * d->topk * d->I;
+  a.M = d->M;
+  a.E = d->E;
+  a.topk = d->topk;
+  a.spin_limit = d->spin_limit ? d->spin_limit : (1u << 20);
+  hipLaunchKernelGGL(fn, dim3(grid), dim3(256), L.total, stream, a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return hip_fail(e, "d3_moe_a8 launch");
+  return 0;
+}
+
+}  // namespace d3
+
+extern "C" {
+
+const char* d3_last_error(void) { return d3::g_error.c_str(); }
+int d3_version(void) { return 1; }
+
+int64_t d3_moe_a8_workspace_bytes(int32_t M, int32_t topk, int32_t H, int32_t I) {
+  return d3::moe_a8_workspace_bytes(M, topk, H, I);
+}
+
+int d3_moe_a8(const d3_moe_a8_desc* desc, void* stream) { return d3::launch_moe_a8(desc, (hipStream_t)stream); }
+
+int d3_moe_a8_status(const void* workspace, uint32_t* status) {
+  if (!workspace || !status) return d3::fail("d3_moe_a8_status: null pointer");
+  hipError_t e = hipMemcpy(status, (const uint8_t*)workspace + d3::SYNC_STATUS * 4, 4, hipMemcpyDeviceToHost);
+  if (e != hipSuccess) return d3::hip_fail(e, "d3_moe_a8_status");
+  return 0;
+}
+
+}  // extern "C"

@@ -1,0 +1,110 @@
+"""The fused routed-expert MoE layer on A8 banks: one launch per layer for M <= 16 rows.
+
+`moe_layer(x, logits, gate_up, down, topk)` does what the reference's SparseMoeBlock.forward does for its routed
+experts (drama3/model.py:107-122: router softmax / top-k / renormalization, then Experts.forward ->
+offload.resident_decode, drama3/offload.py:108-123), for every row of a batch of decode lines at once, in one kernel
+(include/drama3_moe.h, d3_moe_a8). The shared expert and the router's linear stay with the caller, as in the
+reference (model.py:115,123).
+
+Each (device, stream) pair gets a workspace, zeroed once; the kernel leaves it zeroed after every launch, so launches
+on one stream and graph replays reuse it. Allocate it before capturing a graph (`prepare`).
+"""
+import ctypes
+import threading
+
+import torch
+
+from . import _lib
+from .formats import A8Bank
+
+MAX_ROWS = 16
+MAX_TOPK = 8
+_workspaces = {}
+_lock = threading.Lock()
+
+
+def _workspace_bytes(H, I):
+    return int(_lib.lib().d3_moe_a8_workspace_bytes(MAX_ROWS, MAX_TOPK, H, I))
+
+
+def workspace(device, H, I, stream=None):
+    """The zeroed workspace for (device, stream); created on first use, outside graph capture."""
+    device = torch.device(device)
+    stream = stream if stream is not None else torch.cuda.current_stream(device)
+    key = (device.index, stream.cuda_stream, H, I)
+    with _lock:
+        ws = _workspaces.get(key)
+        if ws is None:
+            if torch.cuda.is_current_stream_capturing():
+                raise RuntimeError("drama3.moe: call prepare() before capturing a graph (the workspace must exist)")
+            with torch.cuda.stream(stream):
+                ws = torch.zeros(_workspace_bytes(H, I), dtype=torch.uint8, device=device)
+            _workspaces[key] = ws
+    return ws
+
+
+def prepare(device, H, I, stream=None):
+    """Create the workspace for `stream` (default: the current one) ahead of graph capture."""
+    workspace(device, H, I, stream)
+
+
+def status(device, H, I, stream=None):
+    """The workspace's status word (synchronizes): 0, or bit 0 when a wait hit its bound."""
+    ws = workspace(device, H, I, stream)
+    torch.cuda.synchronize(ws.device)
+    value = ctypes.c_uint32(0)
+    _lib.check(_lib.lib().d3_moe_a8_status(ctypes.c_void_p(ws.data_ptr()), ctypes.byref(value)), "d3_moe_a8_status")
+    return value.value
+
+
+def moe_layer(x, logits, gate_up: A8Bank, down: A8Bank, topk, *, routing=False, spin_limit=0, grid=0, out=None):
+    """x [M, H] bf16 and router logits [M, E] bf16 (M <= 16) through the routed experts: [M, H] bf16, and with
+    `routing` also (ids [M, topk] int64 in descending logit order, weights [M, topk] float32)."""
+    if x.dtype != torch.bfloat16 or logits.dtype != torch.bfloat16:
+        raise TypeError("x and logits must be bfloat16")
+    if x.dim() != 2 or logits.dim() != 2 or x.shape[0] != logits.shape[0]:
+        raise ValueError("x [M, H] and logits [M, E] expected")
+    M, H = x.shape
+    E = logits.shape[1]
+    if gate_up.fmt != down.fmt or gate_up.experts != E or down.experts != E:
+        raise ValueError("banks must share the format and hold one expert per logit")
+    if gate_up.cols != H or down.rows != H or gate_up.rows != 2 * down.cols:
+        raise ValueError("gate_up [E * 2I, H] and down [E * H, I] expected")
+    I = down.cols
+    device = x.device
+    x = x.contiguous()
+    logits = logits.contiguous()
+    if out is None:
+        out = torch.empty((M, H), dtype=torch.bfloat16, device=device)
+    ids = torch.empty((M, topk), dtype=torch.int64, device=device) if routing else None
+    weights = torch.empty((M, topk), dtype=torch.float32, device=device) if routing else None
+    ws = workspace(device, H, I)
+    desc = _lib.MoeA8Desc(
+        x=x.data_ptr(), logits=logits.data_ptr(), gate_up=gate_up.weight.data_ptr(),
+        gate_up_scale=gate_up.scale.data_ptr(), down=down.weight.data_ptr(), down_scale=down.scale.data_ptr(),
+        out=out.data_ptr(), ids_out=_lib.ptr(ids), weights_out=_lib.ptr(weights), workspace=ws.data_ptr(),
+        workspace_bytes=ws.numel(), format=gate_up.fmt, M=M, H=H, I=I, E=E, topk=topk, spin_limit=spin_limit,
+        grid=grid)
+    _lib.check(_lib.lib().d3_moe_a8(ctypes.byref(desc), _lib.stream_of(device)), "d3_moe_a8")
+    return (out, ids, weights) if routing else out
+
+
+def gemv_groups(bank_rows, fmt, cols, act):
+    """Exact per-group dot products of packed rows [R, row_bytes] with act [C, cols] (int8, or e4m3 bytes for F8):
+    [R, cols / 128, C] int32 (float32 for F8). Runs the fused layer's MFMA step on its own."""
+    R = bank_rows.shape[0]
+    C = act.shape[0]
+    dtype = torch.float32 if fmt == 3 else torch.int32
+    acc = torch.empty((R, cols // 128, C), dtype=dtype, device=bank_rows.device)
+    _lib.check(_lib.lib().d3_gemv_a8_groups(fmt, bank_rows.data_ptr(), R, cols, act.contiguous().data_ptr(), C,
+                                            acc.data_ptr(), _lib.stream_of(bank_rows.device)), "d3_gemv_a8_groups")
+    return acc
+
+
+def unpack_rows(bank_rows, fmt, cols):
+    """The int8 codes [R, cols] the fused layer's W4 / W6 unpacking feeds the MFMA."""
+    R = bank_rows.shape[0]
+    codes = torch.empty((R, cols), dtype=torch.int8, device=bank_rows.device)
+    _lib.check(_lib.lib().d3_unpack_rows(fmt, bank_rows.data_ptr(), R, cols, codes.data_ptr(),
+                                         _lib.stream_of(bank_rows.device)), "d3_unpack_rows")
+    return codes
