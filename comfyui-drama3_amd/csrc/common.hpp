@@ -107,14 +107,23 @@ D3_INLINE int wave_sum_i32(int v) {
 }
 
 // ---------------------------------------------------------------------------------------------------------------
-// Device-scope signalling between workgroups of one launch (the fused layer's gate_up -> down hand-off). Producers
-// publish with a release add; consumers poll with relaxed loads, then acquire. Waits are bounded: past `limit` polls
-// the consumer records an error in `status` and goes on, so a broken hand-off can never hang the device.
-D3_INLINE void signal_add(uint32_t* counter, uint32_t v) {
-  __hip_atomic_fetch_add(counter, v, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+// Device-scope hand-off between workgroups of one launch (the fused layer's hidden rows and partial outputs).
+// Each exchanged float travels as one 64-bit word, its bits and the launch's epoch, written and read with relaxed
+// device-scope atomics. The compiler issues those as device-coherent (sc1) accesses, which go past the per-XCD L2s, so
+// no L2-wide writeback or invalidate (what an agent-scope release / acquire fence costs) is needed, and a word carries
+// its own validity: a consumer polls the words it needs until all show the current epoch, with no flag or counter in
+// between. Polls are bounded: past `limit` the consumer records an error in `status` and goes on, so a broken hand-off
+// can never hang the device.
+D3_INLINE void put_tagged(uint64_t* p, float v, uint32_t epoch) {
+  __hip_atomic_store(p, (uint64_t)__float_as_uint(v) | ((uint64_t)epoch << 32), __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
 }
-D3_INLINE uint32_t signal_add_acq_rel(uint32_t* counter, uint32_t v) {
-  return __hip_atomic_fetch_add(counter, v, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+D3_INLINE uint64_t get_tagged(const uint64_t* p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+D3_INLINE bool tag_is(uint64_t word, uint32_t epoch) { return (uint32_t)(word >> 32) == epoch; }
+D3_INLINE float tagged_value(uint64_t word) { return __uint_as_float((uint32_t)word); }
+
+D3_INLINE uint32_t signal_add_ret(uint32_t* counter, uint32_t v) {
+  return __hip_atomic_fetch_add(counter, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 D3_INLINE uint32_t signal_load(const uint32_t* counter) {
   return __hip_atomic_load(counter, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -122,17 +131,27 @@ D3_INLINE uint32_t signal_load(const uint32_t* counter) {
 D3_INLINE void signal_store(uint32_t* counter, uint32_t v) {
   __hip_atomic_store(counter, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-D3_INLINE bool wait_at_least(const uint32_t* counter, uint32_t target, uint32_t* status, uint32_t limit) {
-  uint32_t polls = 0;
-  while (signal_load(counter) < target) {
-    // after one timeout in this launch the rest give up at once: a broken hand-off costs one bounded wait, not many
-    if (signal_load(status) != 0u) return false;
-    __builtin_amdgcn_s_sleep(2);
-    if (++polls > limit) {
-      __hip_atomic_fetch_or(status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      return false;
-    }
+// one more poll allowed? Records a timeout in `status` (and stops every later wait of the launch at once).
+D3_INLINE bool keep_polling(uint32_t& polls, uint32_t* status, uint32_t limit) {
+  if (signal_load(status) != 0u) return false;
+  if (++polls > limit) {
+    __hip_atomic_fetch_or(status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return false;
   }
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  __builtin_amdgcn_s_sleep(1);
   return true;
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// Routing keys: a bf16 logit and its expert index as one 32-bit integer whose order is "larger logit first, then lower
+// index" (the order route_experts ranks by, kernels.py:50-55); -0 ranks as +0. Top-k is then k rounds of a wave max.
+D3_INLINE uint32_t route_key(uint32_t logit_bits, int index) {
+  uint32_t b = logit_bits == 0x8000u ? 0u : logit_bits;
+  const uint32_t ord = (b & 0x8000u) ? (~b & 0xFFFFu) : (b | 0x8000u);
+  return (ord << 16) | (0xFFFFu - (uint32_t)index);
+}
+D3_INLINE int route_key_index(uint32_t key) { return (int)(0xFFFFu - (key & 0xFFFFu)); }
+D3_INLINE float route_key_value(uint32_t key) {
+  const uint32_t ord = key >> 16;
+  return bf16_to_f32((ord & 0x8000u) ? (ord & 0x7FFFu) : (~ord & 0xFFFFu));
 }

@@ -12,20 +12,21 @@
 // Then it takes work items round-robin (item, item + gridDim, ...):
 //   gate_up item (u, tile): gate rows 8 tile .. 8 tile + 7 and the matching up rows of expert u, one 16-row MFMA tile
 //     over K = H (the 4 waves split K); the expert's rows are the MFMA columns. The epilogue applies the scales and
-//     SiLU(gate) * up, writes 8 hidden units per row to `hidden`, and counts the tile done for expert u.
+//     SiLU(gate) * up and publishes 8 hidden units per row.
 //   down item (chunk c, block b): output rows 8 b .. 8 b + 7 of every expert of the chunk, over K = I. Each wave packs
 //     two experts into one 16-row MFMA tile (rows 0-7 and 8-15) with both experts' rows as columns. It loads its
-//     weights first, then waits until every gate_up tile of its chunk is done, quantizes the chunk's hidden rows into
-//     LDS and runs. When the chunk holds every expert (always for M = 1) it writes the weighted sum straight to `out`;
-//     otherwise it stores its outputs in `parts`, and the last chunk to finish block b sums them.
+//     weights first, then collects the chunk's hidden rows as they are published, quantizes them into LDS and runs.
+//     When the chunk holds every expert (always for M = 1) it writes the weighted sum straight to `out`; otherwise it
+//     publishes its partial outputs and the last chunk's item for block b sums them.
 // Items are ordered gate_up(chunk 0), gate_up(chunk 1), down(chunk 0), gate_up(chunk 2), down(chunk 1), ...: every
 // wait is on items of lower index. The grid is at most what the device holds at once, so every workgroup is resident
 // and the lowest unfinished item can always run: no wait can block forever. Waits are bounded anyway (spin_limit),
 // and a timeout sets sync[SYNC_STATUS].
 //
-// Synchronisation state lives in `sync` (zeroed once by the caller); the last down item to pass its wait and the last
-// finisher of each block put it back to zero, so consecutive launches on one stream (or graph replays) reuse it.
-// Launches that overlap on one `sync` race.
+// Hand-off: hidden units and partial outputs are 64-bit words (value, epoch) written and polled with device-coherent
+// accesses (common.hpp), so a consumer waits on the data itself. The epoch is the workspace's launch count + 1: every
+// workgroup reads the count on entry, and the last down item advances it, after every item of the launch has read it.
+// Launches that overlap on one workspace race.
 #include "formats.hpp"
 #include "../../include/drama3_moe.h"
 
@@ -37,7 +38,8 @@
 
 namespace d3 {
 
-enum : int { SYNC_DONE = 0, SYNC_HBLOCK = 256, SYNC_PASSED = 512, SYNC_STATUS = 513, SYNC_WORDS = 1024 };
+// sync words, 256 bytes apart
+enum : int { SYNC_SEQ = 0, SYNC_PASSED = 64, SYNC_STATUS = 128, SYNC_WORDS = 256 };
 constexpr int MAX_M = 16, MAX_K = 8, MAX_E = 256, MAX_PAIRS = MAX_M * MAX_K;
 constexpr int CHUNK_EXPERTS = 8, CHUNK_PAIRS = 32;
 
@@ -51,8 +53,8 @@ struct MoeA8Args {
   uint16_t* out;
   int64_t* ids_out;
   float* weights_out;
-  float* hidden;
-  float* parts;
+  uint64_t* hidden;  // [M * topk, I] tagged
+  uint64_t* parts;   // [M * topk, H] tagged
   uint32_t* sync;
   int M, E, topk;
   uint32_t spin_limit;
@@ -61,10 +63,12 @@ struct MoeA8Args {
 // LDS carve-up (bytes), shared by host (launch size) and device.
 struct Lds {
   int xq, sx, rt_id, rt_w, emask, ulist, ucount, utok, upair, chunk_first, misc, red, hq, hs, lparts, slot_pair,
-      pair_slot, slot_first, total;
-  __host__ __device__ Lds(int M, int H, int I) {
+      pair_slot, slot_first, fparts, total;
+  __host__ __device__ Lds(int M, int topk, int H, int I) {
     int o = 0;
     auto take = [&](int bytes) { int at = o; o += (bytes + 15) & ~15; return at; };
+    const int pairs = M * topk;
+    const int pmax = pairs < CHUNK_PAIRS ? pairs : CHUNK_PAIRS;
     xq = take(M * H);
     sx = take(MAX_M * 4);
     rt_id = take(MAX_M * MAX_K * 4);
@@ -77,12 +81,13 @@ struct Lds {
     chunk_first = take((MAX_PAIRS + 1) * 4);
     misc = take(64);
     red = take(2 * 4 * 256 * 4);
-    hq = take(CHUNK_PAIRS * I);
-    hs = take(CHUNK_PAIRS * 4);
-    lparts = take(CHUNK_PAIRS * 8 * 4);
-    slot_pair = take(CHUNK_PAIRS * 4);
+    hq = take(pmax * I);
+    hs = take(pmax * 4);
+    lparts = take(pmax * 8 * 4);
+    slot_pair = take(pmax * 4);
     pair_slot = take(MAX_PAIRS * 4);
     slot_first = take((CHUNK_EXPERTS + 1) * 4);
+    fparts = take(pairs * 8 * 4);  // every pair's 8 partial outputs of a block (chunks exceed one at 9 experts)
     total = o;
   }
 };
@@ -133,7 +138,9 @@ struct Ctx {
   int* slot_pair;
   int* pair_slot;
   int* slot_first;
+  float* fparts;
   int U, nch, n_dn;
+  uint32_t epoch;
 };
 
 // gate_up tile: gate rows 8 tile .. 8 tile + 7 and up rows I + 8 tile .. of expert u
@@ -215,21 +222,20 @@ D3_INLINE void gate_up_item(const Ctx& cx, int u, int tile, int parity) {
       const float s = cx.sx[cx.utok[u * MAX_M + n]];
       g *= s;
       up *= s;
-      a.hidden[(size_t)cx.upair[u * MAX_M + n] * I + 8 * tile + j] = g / (1.0f + __expf(-g)) * up;
+      put_tagged(a.hidden + (size_t)cx.upair[u * MAX_M + n] * I + 8 * tile + j, g / (1.0f + __expf(-g)) * up, cx.epoch);
     }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-    if (lane == 0) signal_add(&a.sync[SYNC_DONE + u], 1u);
   }
 }
 
 // down block: output rows 8 hb .. 8 hb + 7 of the experts of chunk c
 template <int F, int H, int I>
 D3_INLINE void down_item(const Ctx& cx, int c, int hb) {
-  constexpr int T = I / 8;
   constexpr int STEPS = I / 128;
   constexpr int RB = row_bytes(F, I);
   constexpr int SHIFT = unpack_shift(F);
   constexpr float QMAX = act_qmax<F>();
+  constexpr int G8 = I / 8;  // 8-column groups of a hidden row
+  constexpr int GPL = (G8 + 63) / 64;
   const MoeA8Args& a = *cx.a;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, q = lane >> 4, col = lane & 15;
   const int M = a.M, K8 = a.topk;
@@ -271,38 +277,45 @@ D3_INLINE void down_item(const Ctx& cx, int c, int hb) {
       }
     }
     slot_first[ne] = slot;
-    for (int lj = 0; lj < ne; lj++)
-      wait_at_least(&a.sync[SYNC_DONE + u0 + lj], (uint32_t)T, &a.sync[SYNC_STATUS], a.spin_limit);
-    const uint32_t passed = signal_add_acq_rel(&a.sync[SYNC_PASSED], 1u);
-    if (passed == (uint32_t)cx.n_dn - 1u) {
-      // every down item is past its wait: clear the counters for the next launch
-      for (int uu = 0; uu < cx.U; uu++) signal_store(&a.sync[SYNC_DONE + uu], 0u);
-      signal_store(&a.sync[SYNC_PASSED], 0u);
-    }
   }
   __syncthreads();
   const int P = slot_first[ne];
-  // the chunk's hidden rows, quantized per (expert, row) pair into LDS: one wave per pair
-  constexpr int G8 = I / 8;
+  // the chunk's hidden rows, collected as the gate_up tiles publish them and quantized per pair into LDS
   for (int slot = w; slot < P; slot += 4) {
-    const float* hp = a.hidden + (size_t)cx.slot_pair[slot] * I;
-    float v[(G8 + 63) / 64][8];
+    const uint64_t* hp = a.hidden + (size_t)cx.slot_pair[slot] * I;
+    uint64_t word[GPL][8];
+    uint32_t polls = 0;
+    while (true) {
+      bool fresh = true;
+#pragma unroll
+      for (int k = 0; k < GPL; k++) {
+        const int g8 = lane + 64 * k;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+          if (g8 < G8) {
+            word[k][i] = get_tagged(hp + 8 * g8 + i);
+            fresh = fresh && tag_is(word[k][i], cx.epoch);
+          } else {
+            word[k][i] = 0;
+          }
+        }
+      }
+      if (__all(fresh)) break;
+      if (!keep_polling(polls, a.sync + SYNC_STATUS, a.spin_limit)) break;
+    }
+    float v[GPL][8];
     float amax = 0.0f;
 #pragma unroll
-    for (int k = 0; k < (G8 + 63) / 64; k++) {
-      const int g8 = lane + 64 * k;
-      if (g8 < G8) {
-        const f32x4 p0 = *(const f32x4*)(hp + 8 * g8), p1 = *(const f32x4*)(hp + 8 * g8 + 4);
-        v[k][0] = p0.x; v[k][1] = p0.y; v[k][2] = p0.z; v[k][3] = p0.w;
-        v[k][4] = p1.x; v[k][5] = p1.y; v[k][6] = p1.z; v[k][7] = p1.w;
+    for (int k = 0; k < GPL; k++)
 #pragma unroll
-        for (int i = 0; i < 8; i++) amax = fmaxf(amax, fabsf(v[k][i]));
+      for (int i = 0; i < 8; i++) {
+        v[k][i] = tagged_value(word[k][i]);
+        amax = fmaxf(amax, fabsf(v[k][i]));
       }
-    }
     amax = wave_max_f32(amax);
     const float inv = amax > 0.0f ? QMAX / amax : 0.0f;
 #pragma unroll
-    for (int k = 0; k < (G8 + 63) / 64; k++) {
+    for (int k = 0; k < GPL; k++) {
       const int g8 = lane + 64 * k;
       if (g8 < G8) store_act8<F>(cx.hq + (size_t)slot * I + 8 * g8, v[k], inv);
     }
@@ -372,25 +385,33 @@ D3_INLINE void down_item(const Ctx& cx, int c, int hb) {
   } else {
     for (int idx = tid; idx < P * 8; idx += 256) {
       const int slot = idx >> 3, r = idx & 7;
-      a.parts[(size_t)cx.slot_pair[slot] * H + 8 * hb + r] = cx.lparts[slot * 8 + r];
+      put_tagged(a.parts + (size_t)cx.slot_pair[slot] * H + 8 * hb + r, cx.lparts[slot * 8 + r], cx.epoch);
     }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-    __syncthreads();
-    if (tid == 0) {
-      const uint32_t old = signal_add_acq_rel(&a.sync[SYNC_HBLOCK + hb], 1u);
-      const int last = old == (uint32_t)cx.nch - 1u;
-      if (last) signal_store(&a.sync[SYNC_HBLOCK + hb], 0u);
-      cx.misc[2] = last;
-    }
-    __syncthreads();
-    if (cx.misc[2]) {
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    if (c == cx.nch - 1) {
+      // the last chunk's item gathers every pair's partial outputs of this block
+      for (int idx = tid; idx < M * K8 * 8; idx += 256) {
+        const int p = idx >> 3, r = idx & 7;
+        const uint64_t* src = a.parts + (size_t)p * H + 8 * hb + r;
+        uint64_t word = get_tagged(src);
+        uint32_t polls = 0;
+        while (!tag_is(word, cx.epoch) && keep_polling(polls, a.sync + SYNC_STATUS, a.spin_limit)) word = get_tagged(src);
+        cx.fparts[idx] = tagged_value(word);
+      }
+      __syncthreads();
       for (int idx = tid; idx < M * 8; idx += 256) {
         const int t = idx >> 3, r = idx & 7;
         float acc = 0.0f;
-        for (int j = 0; j < K8; j++) acc = fmaf(a.parts[(size_t)(t * K8 + j) * H + 8 * hb + r], cx.rt_w[t * MAX_K + j], acc);
+        for (int j = 0; j < K8; j++) acc = fmaf(cx.fparts[(t * K8 + j) * 8 + r], cx.rt_w[t * MAX_K + j], acc);
         a.out[(size_t)t * H + 8 * hb + r] = (uint16_t)f32_to_bf16(acc);
       }
+    }
+  }
+  if (tid == 0) {
+    // the launch's last down item advances the epoch for the next launch
+    const uint32_t passed = signal_add_ret(a.sync + SYNC_PASSED, 1u);
+    if (passed == (uint32_t)cx.n_dn - 1u) {
+      signal_store(a.sync + SYNC_PASSED, 0u);
+      signal_store(a.sync + SYNC_SEQ, cx.epoch);
     }
   }
 }
@@ -403,7 +424,7 @@ __global__ void __launch_bounds__(256, 4) moe_a8_kernel(MoeA8Args a) {
   constexpr float QMAX = act_qmax<F>();
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int M = a.M, E = a.E, K8 = a.topk;
-  const Lds L(M, H, I);
+  const Lds L(M, K8, H, I);
   Ctx cx;
   cx.a = &a;
   cx.xq = lds + L.xq;
@@ -424,23 +445,22 @@ __global__ void __launch_bounds__(256, 4) moe_a8_kernel(MoeA8Args a) {
   cx.slot_pair = (int*)(lds + L.slot_pair);
   cx.pair_slot = (int*)(lds + L.pair_slot);
   cx.slot_first = (int*)(lds + L.slot_first);
+  cx.fparts = (float*)(lds + L.fparts);
+  cx.epoch = signal_load(a.sync + SYNC_SEQ) + 1u;
 
-  // ---- routing: one wave per row
+  // ---- per row (one wave each): its logits and activations are loaded together, then routed and quantized
   for (int t = w; t < M; t += 4) {
     const uint16_t* lg = a.logits + (size_t)t * E;
+    const uint16_t* xr = a.x + (size_t)t * H;
+    uint32_t lb[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) lb[j] = lane + 64 * j < E ? lg[lane + 64 * j] : 0u;
+    i32x4 xraw[H / 512];
+#pragma unroll
+    for (int k = 0; k < H / 512; k++) xraw[k] = *(const i32x4*)(xr + 512 * k + 8 * lane);
     uint32_t key[4];
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-      const int e = lane + 64 * j;
-      uint32_t k = 0;
-      if (e < E) {
-        uint32_t b = lg[e];
-        if (b == 0x8000u) b = 0;  // -0 ranks as +0
-        const uint32_t ord = (b & 0x8000u) ? (~b & 0xFFFFu) : (b | 0x8000u);
-        k = (ord << 16) | (0xFFFFu - (uint32_t)e);  // larger logit first, then lower index
-      }
-      key[j] = k;
-    }
+    for (int j = 0; j < 4; j++) key[j] = lane + 64 * j < E ? route_key(lb[j], lane + 64 * j) : 0u;
     float top[MAX_K];
     int ids[MAX_K];
 #pragma unroll
@@ -451,9 +471,8 @@ __global__ void __launch_bounds__(256, 4) moe_a8_kernel(MoeA8Args a) {
         const uint32_t m = wave_max_u32(max(max(key[0], key[1]), max(key[2], key[3])));
 #pragma unroll
         for (int j = 0; j < 4; j++) key[j] = key[j] == m ? 0u : key[j];
-        ids[r] = (int)(0xFFFFu - (m & 0xFFFFu));
-        const uint32_t ord = m >> 16;
-        top[r] = bf16_to_f32((ord & 0x8000u) ? (ord & 0x7FFFu) : (~ord & 0xFFFFu));
+        ids[r] = route_key_index(m);
+        top[r] = route_key_value(m);
       }
     }
     float total = 0.0f;
@@ -467,18 +486,11 @@ __global__ void __launch_bounds__(256, 4) moe_a8_kernel(MoeA8Args a) {
         cx.rt_w[t * MAX_K + r] = bf16_round(expf(top[r] - top[0]) / total);
       }
     }
-  }
-  for (int e = tid; e < MAX_E; e += 256) emask[e] = 0;
-
-  // ---- activations: one wave per row, quantized per row (absmax / QMAX) into LDS
-  for (int t = w; t < M; t += 4) {
-    const uint16_t* xr = a.x + (size_t)t * H;
     float v[H / 512][8];
     float amax = 0.0f;
 #pragma unroll
     for (int k = 0; k < H / 512; k++) {
-      const i32x4 raw = *(const i32x4*)(xr + 512 * k + 8 * lane);
-      const uint32_t wv[4] = {(uint32_t)raw.x, (uint32_t)raw.y, (uint32_t)raw.z, (uint32_t)raw.w};
+      const uint32_t wv[4] = {(uint32_t)xraw[k].x, (uint32_t)xraw[k].y, (uint32_t)xraw[k].z, (uint32_t)xraw[k].w};
 #pragma unroll
       for (int i = 0; i < 4; i++) {
         v[k][2 * i] = bf16_to_f32(wv[i] & 0xFFFFu);
@@ -492,6 +504,7 @@ __global__ void __launch_bounds__(256, 4) moe_a8_kernel(MoeA8Args a) {
     for (int k = 0; k < H / 512; k++) store_act8<F>(cx.xq + (size_t)t * H + 512 * k + 8 * lane, v[k], inv);
     if (lane == 0) cx.sx[t] = amax / QMAX;
   }
+  for (int e = tid; e < MAX_E; e += 256) emask[e] = 0;
   __syncthreads();
 
   // ---- union of the rows' experts, ascending
@@ -582,7 +595,6 @@ __global__ void __launch_bounds__(256, 4) moe_a8_kernel(MoeA8Args a) {
 
 }  // namespace d3
 
-
 // =====================================================================================================================
 // Host side
 namespace d3 {
@@ -599,7 +611,7 @@ int hip_fail(hipError_t err, const char* what) {
 
 int64_t moe_a8_workspace_bytes(int M, int topk, int H, int I) {
   const int64_t pairs = (int64_t)M * topk;
-  return SYNC_WORDS * 4 + pairs * I * 4 + pairs * H * 4;
+  return SYNC_WORDS * 4 + pairs * I * 8 + pairs * H * 8;
 }
 
 using KernelFn = void (*)(MoeA8Args);
@@ -648,7 +660,7 @@ int launch_moe_a8(const d3_moe_a8_desc* d, hipStream_t stream) {
     return fail("d3_moe_a8: null pointer");
   const int64_t need = moe_a8_workspace_bytes(d->M, d->topk, d->H, d->I);
   if (d->workspace_bytes < need) return fail("d3_moe_a8: workspace too small");
-  const Lds L(d->M, d->H, d->I);
+  const Lds L(d->M, d->topk, d->H, d->I);
   int err = 0;
   const int cap = resident_capacity(fn, L.total, &err);
   if (err) return err;
@@ -672,7 +684,7 @@ int launch_moe_a8(const d3_moe_a8_desc* d, hipStream_t stream) {
   a.weights_out = d->weights_out;
   uint8_t* ws = (uint8_t*)d->workspace;
   a.sync = (uint32_t*)ws;
-  a.hidden = (float*)(ws + SYNC_WORDS * 4);
+  a.hidden = (uint64_t*)(ws + SYNC_WORDS * 4);
   a.parts = a.hidden + (size_t)d->M * d->topk * d->I;
   a.M = d->M;
   a.E = d->E;

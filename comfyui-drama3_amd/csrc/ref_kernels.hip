@@ -1,0 +1,590 @@
+// Kernels of the reference's own expert formats, behind drama3/kernels.py's call surface (kernels.py:590-724):
+// routing, the ConvRot rotation, the weighted sum, and the decode GEMVs / prefill grouped products over int8 ConvRot
+// banks (per-row float scale), FP8 banks (float scale per 128 x 128 block) and W4A8 / W6A8 code banks (nibble plane,
+// 2-bit high plane for 6 bits, e4m3 scale per 16 columns, float scale per row, 16-entry codebook for 4 bits).
+// Activations stay float32, as in the reference. The slot-cache semantics of the decode GEMVs are kept: plan[e] =
+// (slot, code), code 0 reads the slot, 1 reads the bank (host memory) and fills the slot if it has one, 2 is the CPU's
+// (zeros, or, with `late` and took_over set, read from the bank) (kernels.py:274-314).
+//
+// Design for gfx950, not a translation: a wave holds a row's columns across its 64 lanes (each lane a fixed slice, so
+// the activation slice stays in registers across rows), int8 bytes become floats through one unsigned conversion after
+// flipping the sign bit (sum u x - 128 sum x), FP8 bytes through the hardware e4m3 converter with the block scale
+// folded into the activation slice, and wave sums go through DPP. The rotation runs in registers: H256 is the 4-fold
+// Kronecker power of h4, whose row r is +1 except -1 at column 3 - r, so each of the four base-4 digits of the column
+// index is one step y = (sum of the 4 values) - 2 * (the value at the mirrored digit), exchanged within a lane, a quad
+// (DPP), a row (DPP rotate / mirror) and the wave (shuffles).
+#include "common.hpp"
+#include "../../include/drama3_moe.h"
+
+#include <string>
+
+namespace d3 {
+int fail(const std::string& msg);
+int hip_fail(hipError_t err, const char* what);
+
+constexpr int RPB = 16;  // output rows per workgroup of the GEMVs (kernels.py:590 ROWS_PER_BLOCK: N % 16 == 0)
+
+template <int CTRL> D3_INLINE float dpp_f32(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
+// ---------------------------------------------------------------------------------------------------------- route
+// kernels.py:39-67: the k (<= 32) largest of n (<= 1024) bf16 logits, descending, ties to the lower index; weights
+// softmax over those k, rounded to bf16. One wave per row.
+__global__ void __launch_bounds__(256) route_kernel(const uint16_t* logits, int rows, int n, int k, int64_t* ids,
+                                                    float* weights) {
+  const int lane = threadIdx.x & 63, row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const uint16_t* lg = logits + (size_t)row * n;
+  uint32_t key[16];
+#pragma unroll
+  for (int j = 0; j < 16; j++) {
+    const int e = lane + 64 * j;
+    key[j] = e < n ? route_key(lg[e], e) : 0u;
+  }
+  float top[32];
+  int id[32];
+#pragma unroll
+  for (int r = 0; r < 32; r++) {
+    top[r] = 0.0f;
+    id[r] = 0;
+    if (r < k) {
+      uint32_t m = key[0];
+#pragma unroll
+      for (int j = 1; j < 16; j++) m = max(m, key[j]);
+      m = wave_max_u32(m);
+#pragma unroll
+      for (int j = 0; j < 16; j++) key[j] = key[j] == m ? 0u : key[j];
+      id[r] = route_key_index(m);
+      top[r] = route_key_value(m);
+    }
+  }
+  float total = 0.0f;
+#pragma unroll
+  for (int r = 0; r < 32; r++)
+    if (r < k) total += expf(top[r] - top[0]);
+#pragma unroll
+  for (int r = 0; r < 32; r++) {
+    if (r < k && lane == r) {
+      ids[(size_t)row * k + r] = id[r];
+      weights[(size_t)row * k + r] = bf16_round(expf(top[r] - top[0]) / total);
+    }
+  }
+}
+
+// -------------------------------------------------------------------------------------------------- weighted sum
+// kernels.py:69-76: out[h] = bf16(sum_e parts[e, h] * w[e]), e in order.
+__global__ void __launch_bounds__(256) weighted_sum_kernel(const float* parts, const float* w, int k, int H,
+                                                           uint16_t* out) {
+  const int h = blockIdx.x * 256 + threadIdx.x;
+  if (h >= H) return;
+  float acc = 0.0f;
+  for (int e = 0; e < k; e++) acc = fmaf(parts[(size_t)e * H + h], w[e], acc);
+  out[h] = (uint16_t)f32_to_bf16(acc);
+}
+
+// -------------------------------------------------------------------------------------------------------- rotate
+// kernels.py:222-258: per row, optional SwiGLU (float [rows, 2K] gate | up), then H256 on every 256 columns, / 16.
+// MODE 0: float rows, 1: bf16 rows, 2: SwiGLU. Does nothing unless only_if[0].
+template <int MODE>
+__global__ void __launch_bounds__(256) rotate_kernel(const void* x, int K, float* out, const int* only_if) {
+  if (!only_if[0]) return;
+  const int row = blockIdx.x, lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  for (int g = w; g < K / 256; g += 4) {
+    const int c0 = 256 * g + 4 * lane;
+    float v[4];
+    if constexpr (MODE == 0) {
+      const f32x4 a = *(const f32x4*)((const float*)x + (size_t)row * K + c0);
+      v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+    } else if constexpr (MODE == 1) {
+      const i32x2 a = *(const i32x2*)((const uint16_t*)x + (size_t)row * K + c0);
+      v[0] = bf16_to_f32((uint32_t)a.x & 0xFFFFu); v[1] = bf16_to_f32((uint32_t)a.x >> 16);
+      v[2] = bf16_to_f32((uint32_t)a.y & 0xFFFFu); v[3] = bf16_to_f32((uint32_t)a.y >> 16);
+    } else {
+      const float* f = (const float*)x + (size_t)row * 2 * K;
+      const f32x4 gt = *(const f32x4*)(f + c0), up = *(const f32x4*)(f + K + c0);
+      const float gg[4] = {gt.x, gt.y, gt.z, gt.w}, uu[4] = {up.x, up.y, up.z, up.w};
+#pragma unroll
+      for (int j = 0; j < 4; j++) v[j] = gg[j] / (1.0f + __expf(-gg[j])) * uu[j];
+    }
+    // digit 0: the lane's own four columns
+    {
+      const float s = (v[0] + v[1]) + (v[2] + v[3]);
+      const float y0 = s - 2.0f * v[3], y1 = s - 2.0f * v[2], y2 = s - 2.0f * v[1], y3 = s - 2.0f * v[0];
+      v[0] = y0; v[1] = y1; v[2] = y2; v[3] = y3;
+    }
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      // digit 1: the four lanes of a quad; mirrored digit = lane ^ 3
+      float s = v[j] + dpp_f32<0xB1>(v[j]);
+      s = s + dpp_f32<0x4E>(s);
+      v[j] = s - 2.0f * dpp_f32<0x1B>(v[j]);
+      // digit 2: the four quads of a row (rotate by 8 and 4); mirrored digit = lane ^ 12 (row mirror, then quad mirror)
+      s = v[j] + dpp_f32<0x128>(v[j]);
+      s = s + dpp_f32<0x124>(s);
+      v[j] = s - 2.0f * dpp_f32<0x1B>(dpp_f32<0x140>(v[j]));
+      // digit 3: the four rows of the wave; mirrored digit = lane ^ 48
+      s = v[j] + __shfl_xor(v[j], 16);
+      s = s + __shfl_xor(s, 32);
+      v[j] = (s - 2.0f * __shfl_xor(v[j], 48)) * 0.0625f;
+    }
+    *(f32x4*)(out + (size_t)row * K + c0) = f32x4{v[0], v[1], v[2], v[3]};
+  }
+}
+
+// ---------------------------------------------------------------------------------------------------- decode GEMVs
+// Which source an expert's rows come from, and whether this launch computes them at all (kernels.py:284-295).
+struct Source {
+  bool zero, fill;
+  int slot;
+  size_t id;
+};
+D3_INLINE Source source_of(const int64_t* ids, const int* plan, const int* took_over, int late, int e, bool cpu_code) {
+  Source s;
+  const int code = plan[2 * e + 1];
+  s.slot = plan[2 * e];
+  s.id = (size_t)ids[e];
+  s.zero = cpu_code && (late ? (code != 2 || !took_over[0]) : code == 2);
+  s.fill = code == 1 && s.slot >= 0;
+  return s;
+}
+
+// lane's CPL activation floats (columns lane * CPL ..), and their sum
+template <int CPL> D3_INLINE float load_slice(const float* xr, int lane, float* xv) {
+  float sum = 0.0f;
+#pragma unroll
+  for (int i = 0; i < CPL / 4; i++) {
+    const f32x4 a = *(const f32x4*)(xr + lane * CPL + 4 * i);
+    xv[4 * i] = a.x; xv[4 * i + 1] = a.y; xv[4 * i + 2] = a.z; xv[4 * i + 3] = a.w;
+    sum += (a.x + a.y) + (a.z + a.w);
+  }
+  return sum;
+}
+
+// sum over the lane's int8 columns of w * x, with w's sign bit flipped into an unsigned byte: sum (w + 128) x - 128 sum x
+template <int CPL> D3_INLINE float dot_i8(const uint32_t* wd, const float* xv, float xsum) {
+  float acc = 0.0f;
+#pragma unroll
+  for (int i = 0; i < CPL / 4; i++) {
+    const uint32_t u = wd[i] ^ 0x80808080u;
+#pragma unroll
+    for (int b = 0; b < 4; b++) acc = fmaf((float)((u >> (8 * b)) & 0xFFu), xv[4 * i + b], acc);
+  }
+  return fmaf(-128.0f, xsum, acc);
+}
+
+template <int CPL> D3_INLINE float dot_f8(const uint32_t* wd, const float* xv) {
+  float acc = 0.0f;
+#pragma unroll
+  for (int i = 0; i < CPL / 4; i++) {
+    const f32x2 lo = fp8x2_to_f32<false>(wd[i]), hi = fp8x2_to_f32<true>(wd[i]);
+    acc = fmaf(lo.x, xv[4 * i], acc);
+    acc = fmaf(lo.y, xv[4 * i + 1], acc);
+    acc = fmaf(hi.x, xv[4 * i + 2], acc);
+    acc = fmaf(hi.y, xv[4 * i + 3], acc);
+  }
+  return acc;
+}
+
+template <int CPL> D3_INLINE void load_words(const uint8_t* p, uint32_t* wd) {
+#pragma unroll
+  for (int i = 0; i < CPL / 4; i++) wd[i] = ((const uint32_t*)p)[i];
+}
+template <int CPL> D3_INLINE void store_words(uint8_t* p, const uint32_t* wd) {
+#pragma unroll
+  for (int i = 0; i < CPL / 4; i++) ((uint32_t*)p)[i] = wd[i];
+}
+
+// kernels.py:274-314: out[e, n] = (int8 row n of expert e) . x[e or 0] * row scale. Grid (N / 16, k), 256 threads.
+template <int K>
+__global__ void __launch_bounds__(256) gemv_int8_kernel(const float* x, int x_rows, const int64_t* ids, const int* plan,
+                                                        const int* took_over, int late, uint8_t* slot_w, float* slot_s,
+                                                        const uint8_t* host_w, const float* host_s, float* out, int N) {
+  constexpr int CPL = K / 64;
+  const int e = blockIdx.y, lane = threadIdx.x & 63, w = threadIdx.x >> 6, n0 = blockIdx.x * RPB;
+  const Source src = source_of(ids, plan, took_over, late, e, true);
+  if (src.zero) {
+    if (threadIdx.x < RPB) out[(size_t)e * N + n0 + threadIdx.x] = 0.0f;
+    return;
+  }
+  const bool host = plan[2 * e + 1] != 0;
+  float xv[CPL];
+  const float xsum = load_slice<CPL>(x + (size_t)(x_rows == 1 ? 0 : e) * K, lane, xv);
+  const uint8_t* wsrc = host ? host_w + src.id * N * K : slot_w + (size_t)src.slot * N * K;
+  const float* ssrc = host ? host_s + src.id * N : slot_s + (size_t)src.slot * N;
+#pragma unroll
+  for (int r = 0; r < RPB / 4; r++) {
+    const int n = n0 + w * (RPB / 4) + r;
+    uint32_t wd[CPL / 4];
+    load_words<CPL>(wsrc + (size_t)n * K + lane * CPL, wd);
+    if (src.fill) store_words<CPL>(slot_w + ((size_t)src.slot * N + n) * K + lane * CPL, wd);
+    const float acc = wave_sum_f32(dot_i8<CPL>(wd, xv, xsum));
+    if (lane == 0) {
+      const float s = ssrc[n];
+      out[(size_t)e * N + n] = acc * s;
+      if (src.fill) slot_s[(size_t)src.slot * N + n] = s;
+    }
+  }
+}
+
+// kernels.py:316-363: out[e, n] = (e4m3 row n) . x with the 128 x 128 block scales [N / 128, K / 128] folded into the
+// activation slice of the block's rows.
+template <int K>
+__global__ void __launch_bounds__(256) gemv_fp8_kernel(const float* x, int x_rows, const int64_t* ids, const int* plan,
+                                                       uint8_t* slot_w, float* slot_s, const uint8_t* host_w,
+                                                       const float* host_s, float* out, int N) {
+  constexpr int CPL = K / 64, SC = K / 128;
+  const int e = blockIdx.y, lane = threadIdx.x & 63, w = threadIdx.x >> 6, n0 = blockIdx.x * RPB;
+  const int slot = plan[2 * e];
+  const bool host = plan[2 * e + 1] != 0, fill = host && slot >= 0;
+  const size_t id = (size_t)ids[e];
+  const size_t srows = (size_t)(N / 128) * SC;
+  const float* sblock = (host ? host_s + id * srows : slot_s + (size_t)slot * srows) + (size_t)(n0 / 128) * SC;
+  if (fill && n0 % 128 == 0 && threadIdx.x < SC) slot_s[(size_t)slot * srows + (size_t)(n0 / 128) * SC + threadIdx.x] = sblock[threadIdx.x];
+  float xv[CPL];
+  load_slice<CPL>(x + (size_t)(x_rows == 1 ? 0 : e) * K, lane, xv);
+#pragma unroll
+  for (int j = 0; j < CPL; j++) xv[j] *= sblock[(lane * CPL + j) / 128];
+  const uint8_t* wsrc = host ? host_w + id * N * K : slot_w + (size_t)slot * N * K;
+#pragma unroll
+  for (int r = 0; r < RPB / 4; r++) {
+    const int n = n0 + w * (RPB / 4) + r;
+    uint32_t wd[CPL / 4];
+    load_words<CPL>(wsrc + (size_t)n * K + lane * CPL, wd);
+    if (fill) store_words<CPL>(slot_w + ((size_t)slot * N + n) * K + lane * CPL, wd);
+    const float acc = wave_sum_f32(dot_f8<CPL>(wd, xv));
+    if (lane == 0) out[(size_t)e * N + n] = acc;
+  }
+}
+
+// W4A8 / W6A8 code decoding to the int8 grid (kernels.py:466-483): 16 columns (group v) of a row; code = nibble (and
+// two high bits from the plane after the K/2 nibble bytes at 6 bits); value = codebook[code] or code - 32; q =
+// clamp(rint(value * e4m3(scale byte)), -127, 127).
+template <int BITS>
+D3_INLINE void decode_group(uint32_t lo, uint32_t hi, uint32_t high, uint32_t scale_byte, const float* lut, float* q) {
+  const float s = fp8x2_to_f32<false>(scale_byte).x;
+#pragma unroll
+  for (int j = 0; j < 16; j++) {
+    const uint32_t code = ((j < 8 ? lo : hi) >> (4 * (j & 7))) & 0xFu;
+    float value;
+    if constexpr (BITS == 6) value = (float)(code | (((high >> (2 * j)) & 3u) << 4)) - 32.0f;
+    else value = lut[code];
+    q[j] = fminf(fmaxf(rintf(value * s), -127.0f), 127.0f);
+  }
+}
+
+// kernels.py:495-536: code rows against x, times the row's channel scale. Lane l takes 16-column groups l, l + 64.
+template <int K, int BITS>
+__global__ void __launch_bounds__(256) gemv_codes_kernel(const float* x, int x_rows, const int64_t* ids, const int* plan,
+                                                         uint8_t* slot_w, uint8_t* slot_r, float* slot_c,
+                                                         const uint8_t* host_w, const uint8_t* host_r, const float* host_c,
+                                                         const float* codebook, float* out, int N) {
+  constexpr int RB = K * BITS / 8, G = K / 16, GPL = (G + 63) / 64;
+  __shared__ float xs[K];
+  __shared__ float lut[16];
+  const int e = blockIdx.y, lane = threadIdx.x & 63, w = threadIdx.x >> 6, n0 = blockIdx.x * RPB;
+  const float* xr = x + (size_t)(x_rows == 1 ? 0 : e) * K;
+  for (int i = threadIdx.x; i < K; i += 256) xs[i] = xr[i];
+  if (BITS == 4 && threadIdx.x < 16) lut[threadIdx.x] = codebook[threadIdx.x];
+  __syncthreads();
+  const int slot = plan[2 * e];
+  const bool host = plan[2 * e + 1] != 0, fill = host && slot >= 0;
+  const size_t id = (size_t)ids[e];
+  const uint8_t* wsrc = host ? host_w + id * N * RB : slot_w + (size_t)slot * N * RB;
+  const uint8_t* rsrc = host ? host_r + id * N * G : slot_r + (size_t)slot * N * G;
+  const float* csrc = host ? host_c + id * N : slot_c + (size_t)slot * N;
+#pragma unroll
+  for (int r = 0; r < RPB / 4; r++) {
+    const int n = n0 + w * (RPB / 4) + r;
+    const uint8_t* row = wsrc + (size_t)n * RB;
+    const uint8_t* rs = rsrc + (size_t)n * G;
+    float acc = 0.0f;
+#pragma unroll
+    for (int i = 0; i < GPL; i++) {
+      const int v = lane + 64 * i;
+      if (v < G) {
+        const i32x2 lw = *(const i32x2*)(row + 8 * v);
+        const uint32_t high = BITS == 6 ? *(const uint32_t*)(row + K / 2 + 4 * v) : 0u;
+        const uint32_t sb = rs[v];
+        if (fill) {
+          uint8_t* drow = slot_w + ((size_t)slot * N + n) * RB;
+          *(i32x2*)(drow + 8 * v) = lw;
+          if (BITS == 6) *(uint32_t*)(drow + K / 2 + 4 * v) = high;
+          slot_r[((size_t)slot * N + n) * G + v] = (uint8_t)sb;
+        }
+        float q[16];
+        decode_group<BITS>((uint32_t)lw.x, (uint32_t)lw.y, high, sb, lut, q);
+#pragma unroll
+        for (int j = 0; j < 16; j++) acc = fmaf(q[j], xs[16 * v + j], acc);
+      }
+    }
+    acc = wave_sum_f32(acc);
+    if (lane == 0) {
+      const float c = csrc[n];
+      out[(size_t)e * N + n] = acc * c;
+      if (fill) slot_c[(size_t)slot * N + n] = c;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------- grouped (prefill)
+// kernels.py:365-464,538-587: rows of x sorted by expert; group g = (expert, slot, fill, first, rows); out[t, n] = row
+// n of the group's expert . x[t] (* its scale). The group reads its slot, or the bank when it has no slot or fills it.
+// Each wave holds 4 weight rows in registers and walks the group's activation rows.
+template <int KIND, int K>  // KIND 0 int8, 1 fp8, 4 / 6 codes
+__global__ void __launch_bounds__(256) grouped_kernel(const float* x, const int* groups, uint8_t* slot_w, void* slot_s,
+                                                      void* slot_c, const uint8_t* host_w, const void* host_s,
+                                                      const void* host_c, const float* codebook, float* out, int N) {
+  constexpr int CPL = K / 64;  // int8 / fp8: bytes per lane per row
+  const int* gp = groups + 5 * blockIdx.y;
+  const int expert = gp[0], slot = gp[1], fill = gp[2], first = gp[3], rows = gp[4];
+  const bool host = slot < 0 || fill;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, n0 = blockIdx.x * RPB;
+  __shared__ float lut[16];
+  if (KIND == 4 && threadIdx.x < 16) lut[threadIdx.x] = codebook[threadIdx.x];
+  __syncthreads();
+  if constexpr (KIND == 0 || KIND == 1) {
+    const uint8_t* wsrc = host ? host_w + (size_t)expert * N * K : slot_w + (size_t)slot * N * K;
+    uint32_t wd[RPB / 4][CPL / 4];
+    float rs[RPB / 4];
+    float sb[CPL];  // fp8: block scale of each of the lane's columns
+    const int SC = K / 128;
+    const size_t srows = (size_t)(N / 128) * SC;
+    if constexpr (KIND == 1) {
+      const float* s = (const float*)host_s;
+      const float* sblock = (host ? s + (size_t)expert * srows : (const float*)slot_s + (size_t)slot * srows) + (size_t)(n0 / 128) * SC;
+      if (fill && n0 % 128 == 0 && threadIdx.x < SC) ((float*)slot_s)[(size_t)slot * srows + (size_t)(n0 / 128) * SC + threadIdx.x] = sblock[threadIdx.x];
+#pragma unroll
+      for (int j = 0; j < CPL; j++) sb[j] = sblock[(lane * CPL + j) / 128];
+    }
+#pragma unroll
+    for (int r = 0; r < RPB / 4; r++) {
+      const int n = n0 + w * (RPB / 4) + r;
+      load_words<CPL>(wsrc + (size_t)n * K + lane * CPL, wd[r]);
+      if (fill) store_words<CPL>(slot_w + ((size_t)slot * N + n) * K + lane * CPL, wd[r]);
+      if constexpr (KIND == 0) {
+        const float* s = host ? (const float*)host_s + (size_t)expert * N : (const float*)slot_s + (size_t)slot * N;
+        rs[r] = s[n];
+        if (fill && lane == 0) ((float*)slot_s)[(size_t)slot * N + n] = rs[r];
+      }
+    }
+    for (int t = first; t < first + rows; t++) {
+      float xv[CPL];
+      const float xsum = load_slice<CPL>(x + (size_t)t * K, lane, xv);
+      if constexpr (KIND == 1) {
+#pragma unroll
+        for (int j = 0; j < CPL; j++) xv[j] *= sb[j];
+      }
+#pragma unroll
+      for (int r = 0; r < RPB / 4; r++) {
+        const int n = n0 + w * (RPB / 4) + r;
+        float acc = KIND == 0 ? dot_i8<CPL>(wd[r], xv, xsum) : dot_f8<CPL>(wd[r], xv);
+        acc = wave_sum_f32(acc);
+        if (lane == 0) out[(size_t)t * N + n] = KIND == 0 ? acc * rs[r] : acc;
+      }
+    }
+  } else {
+    constexpr int BITS = KIND, RB = K * BITS / 8, G = K / 16, GPL = (G + 63) / 64;
+    const uint8_t* wsrc = host ? host_w + (size_t)expert * N * RB : slot_w + (size_t)slot * N * RB;
+    const uint8_t* rsrc = host ? (const uint8_t*)host_s + (size_t)expert * N * G : (const uint8_t*)slot_s + (size_t)slot * N * G;
+    const float* csrc = host ? (const float*)host_c + (size_t)expert * N : (const float*)slot_c + (size_t)slot * N;
+    // decoded int8-grid rows, packed 4 per word as (q + 128) bytes, and each row's channel scale
+    uint32_t qd[RPB / 4][GPL * 4];
+    float cs[RPB / 4];
+#pragma unroll
+    for (int r = 0; r < RPB / 4; r++) {
+      const int n = n0 + w * (RPB / 4) + r;
+      const uint8_t* row = wsrc + (size_t)n * RB;
+#pragma unroll
+      for (int i = 0; i < GPL; i++) {
+        const int v = lane + 64 * i;
+#pragma unroll
+        for (int c = 0; c < 4; c++) qd[r][4 * i + c] = 0x80808080u;
+        if (v < G) {
+          const i32x2 lw = *(const i32x2*)(row + 8 * v);
+          const uint32_t high = BITS == 6 ? *(const uint32_t*)(row + K / 2 + 4 * v) : 0u;
+          const uint32_t sbyte = rsrc[(size_t)n * G + v];
+          if (fill) {
+            uint8_t* drow = slot_w + ((size_t)slot * N + n) * RB;
+            *(i32x2*)(drow + 8 * v) = lw;
+            if (BITS == 6) *(uint32_t*)(drow + K / 2 + 4 * v) = high;
+            ((uint8_t*)slot_s)[((size_t)slot * N + n) * G + v] = (uint8_t)sbyte;
+          }
+          float q[16];
+          decode_group<BITS>((uint32_t)lw.x, (uint32_t)lw.y, high, sbyte, lut, q);
+#pragma unroll
+          for (int c = 0; c < 4; c++) {
+            uint32_t word = 0;
+#pragma unroll
+            for (int b = 0; b < 4; b++) word |= ((uint32_t)((int)q[4 * c + b] + 128) & 0xFFu) << (8 * b);
+            qd[r][4 * i + c] = word;
+          }
+        }
+      }
+      cs[r] = csrc[n];
+      if (fill && lane == 0) ((float*)slot_c)[(size_t)slot * N + n] = cs[r];
+    }
+    for (int t = first; t < first + rows; t++) {
+      const float* xr = x + (size_t)t * K;
+      float acc[RPB / 4];
+#pragma unroll
+      for (int r = 0; r < RPB / 4; r++) acc[r] = 0.0f;
+#pragma unroll
+      for (int i = 0; i < GPL; i++) {
+        const int v = lane + 64 * i;
+        if (v < G) {
+          float xv[16];
+          float xsum = 0.0f;
+#pragma unroll
+          for (int c = 0; c < 4; c++) {
+            const f32x4 a = *(const f32x4*)(xr + 16 * v + 4 * c);
+            xv[4 * c] = a.x; xv[4 * c + 1] = a.y; xv[4 * c + 2] = a.z; xv[4 * c + 3] = a.w;
+            xsum += (a.x + a.y) + (a.z + a.w);
+          }
+#pragma unroll
+          for (int r = 0; r < RPB / 4; r++) {
+            float part = 0.0f;
+#pragma unroll
+            for (int c = 0; c < 4; c++)
+#pragma unroll
+              for (int b = 0; b < 4; b++) part = fmaf((float)((qd[r][4 * i + c] >> (8 * b)) & 0xFFu), xv[4 * c + b], part);
+            acc[r] += fmaf(-128.0f, xsum, part);
+          }
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < RPB / 4; r++) {
+        const float s = wave_sum_f32(acc[r]);
+        if (lane == 0) out[(size_t)t * N + n0 + w * (RPB / 4) + r] = s * cs[r];
+      }
+    }
+  }
+}
+
+}  // namespace d3
+
+// ============================================================================================================ C ABI
+using namespace d3;
+
+namespace {
+template <template <int> class KT> struct None {};
+
+hipError_t last() { return hipGetLastError(); }
+int done(const char* what) {
+  const hipError_t e = last();
+  return e == hipSuccess ? 0 : hip_fail(e, what);
+}
+bool supported_k(int K) { return K == 256 || K == 512 || K == 768 || K == 1024 || K == 1536 || K == 2048; }
+}  // namespace
+
+#define D3_K_SWITCH(K, CALL)                          \
+  switch (K) {                                        \
+    case 256: { constexpr int KK = 256; CALL; } break;  \
+    case 512: { constexpr int KK = 512; CALL; } break;  \
+    case 768: { constexpr int KK = 768; CALL; } break;  \
+    case 1024: { constexpr int KK = 1024; CALL; } break; \
+    case 1536: { constexpr int KK = 1536; CALL; } break; \
+    case 2048: { constexpr int KK = 2048; CALL; } break; \
+    default: break;                                   \
+  }
+
+extern "C" {
+
+int d3_route(const void* logits, int32_t rows, int32_t n, int32_t k, int64_t* ids, float* weights, void* stream) {
+  if (!logits || !ids || !weights) return fail("d3_route: null pointer");
+  if (rows < 1 || n < 1 || n > 1024 || k < 1 || k > 32 || k > n) return fail("d3_route: n <= 1024, 1 <= k <= min(32, n)");
+  hipLaunchKernelGGL(route_kernel, dim3((rows + 3) / 4), dim3(256), 0, (hipStream_t)stream, (const uint16_t*)logits,
+                     rows, n, k, ids, weights);
+  return done("d3_route");
+}
+
+int d3_weighted_sum(const float* parts, const float* weights, int32_t k, int32_t H, void* out, void* stream) {
+  if (!parts || !weights || !out) return fail("d3_weighted_sum: null pointer");
+  if (k < 1 || H < 1) return fail("d3_weighted_sum: k, H >= 1");
+  hipLaunchKernelGGL(weighted_sum_kernel, dim3((H + 255) / 256), dim3(256), 0, (hipStream_t)stream, parts, weights, k, H,
+                     (uint16_t*)out);
+  return done("d3_weighted_sum");
+}
+
+int d3_rotate(const void* x, int32_t mode, int32_t rows, int32_t K, float* out, const int32_t* only_if, void* stream) {
+  if (!x || !out || !only_if) return fail("d3_rotate: null pointer");
+  if (rows < 1 || K < 256 || K % 256 || K > 4096) return fail("d3_rotate: K % 256 == 0, K <= 4096");
+  const hipStream_t s = (hipStream_t)stream;
+  switch (mode) {
+    case 0: hipLaunchKernelGGL(rotate_kernel<0>, dim3(rows), dim3(256), 0, s, x, K, out, only_if); break;
+    case 1: hipLaunchKernelGGL(rotate_kernel<1>, dim3(rows), dim3(256), 0, s, x, K, out, only_if); break;
+    case 2: hipLaunchKernelGGL(rotate_kernel<2>, dim3(rows), dim3(256), 0, s, x, K, out, only_if); break;
+    default: return fail("d3_rotate: mode 0 (float), 1 (bf16) or 2 (swiglu)");
+  }
+  return done("d3_rotate");
+}
+
+int d3_gemv_int8(const float* x, int32_t x_rows, const int64_t* ids, const int32_t* plan, const int32_t* took_over,
+                 int32_t late, void* slot_w, float* slot_s, const void* host_w, const float* host_s, float* out,
+                 int32_t k, int32_t N, int32_t K, void* stream) {
+  if (!x || !ids || !plan || !took_over || !slot_w || !slot_s || !host_w || !host_s || !out)
+    return fail("d3_gemv_int8: null pointer");
+  if (k < 1 || N < RPB || N % RPB || !supported_k(K)) return fail("d3_gemv_int8: N % 16 == 0, K in {256..2048}");
+  const dim3 grid(N / RPB, k);
+  D3_K_SWITCH(K, hipLaunchKernelGGL(gemv_int8_kernel<KK>, grid, dim3(256), 0, (hipStream_t)stream, x, x_rows, ids, plan,
+                                    took_over, late, (uint8_t*)slot_w, slot_s, (const uint8_t*)host_w, host_s, out, N));
+  return done("d3_gemv_int8");
+}
+
+int d3_gemv_fp8(const float* x, int32_t x_rows, const int64_t* ids, const int32_t* plan, void* slot_w, float* slot_s,
+                const void* host_w, const float* host_s, float* out, int32_t k, int32_t N, int32_t K, void* stream) {
+  if (!x || !ids || !plan || !slot_w || !slot_s || !host_w || !host_s || !out) return fail("d3_gemv_fp8: null pointer");
+  if (k < 1 || N < 128 || N % 128 || !supported_k(K)) return fail("d3_gemv_fp8: N % 128 == 0, K in {256..2048}");
+  const dim3 grid(N / RPB, k);
+  D3_K_SWITCH(K, hipLaunchKernelGGL(gemv_fp8_kernel<KK>, grid, dim3(256), 0, (hipStream_t)stream, x, x_rows, ids, plan,
+                                    (uint8_t*)slot_w, slot_s, (const uint8_t*)host_w, host_s, out, N));
+  return done("d3_gemv_fp8");
+}
+
+int d3_gemv_codes(const float* x, int32_t x_rows, const int64_t* ids, const int32_t* plan, void* slot_w, void* slot_r,
+                  float* slot_c, const void* host_w, const void* host_r, const float* host_c, const float* codebook,
+                  int32_t bits, float* out, int32_t k, int32_t N, int32_t K, void* stream) {
+  if (!x || !ids || !plan || !slot_w || !slot_r || !slot_c || !host_w || !host_r || !host_c || !out)
+    return fail("d3_gemv_codes: null pointer");
+  if (bits == 4 && !codebook) return fail("d3_gemv_codes: 4 bits need a codebook");
+  if (k < 1 || N < RPB || N % RPB || !supported_k(K) || (bits != 4 && bits != 6))
+    return fail("d3_gemv_codes: N % 16 == 0, K in {256..2048}, bits 4 or 6");
+  const dim3 grid(N / RPB, k);
+  const hipStream_t s = (hipStream_t)stream;
+  if (bits == 4) {
+    D3_K_SWITCH(K, hipLaunchKernelGGL((gemv_codes_kernel<KK, 4>), grid, dim3(256), 0, s, x, x_rows, ids, plan,
+                                      (uint8_t*)slot_w, (uint8_t*)slot_r, slot_c, (const uint8_t*)host_w,
+                                      (const uint8_t*)host_r, host_c, codebook, out, N));
+  } else {
+    D3_K_SWITCH(K, hipLaunchKernelGGL((gemv_codes_kernel<KK, 6>), grid, dim3(256), 0, s, x, x_rows, ids, plan,
+                                      (uint8_t*)slot_w, (uint8_t*)slot_r, slot_c, (const uint8_t*)host_w,
+                                      (const uint8_t*)host_r, host_c, codebook, out, N));
+  }
+  return done("d3_gemv_codes");
+}
+
+// kind: 0 int8 (scale float [E * N]), 1 fp8 (scale float [E * N / 128, K / 128]), 4 / 6 codes (scale e4m3 [E * N, K / 16],
+// channel float [E * N])
+int d3_grouped(int32_t kind, const float* x, const int32_t* groups, int32_t n_groups, void* slot_w, void* slot_s,
+               void* slot_c, const void* host_w, const void* host_s, const void* host_c, const float* codebook,
+               float* out, int32_t N, int32_t K, void* stream) {
+  if (!x || !groups || !slot_w || !slot_s || !host_w || !host_s || !out) return fail("d3_grouped: null pointer");
+  if ((kind == 4 || kind == 6) && (!slot_c || !host_c)) return fail("d3_grouped: codes need channel scales");
+  if (kind == 4 && !codebook) return fail("d3_grouped: 4 bits need a codebook");
+  if (n_groups < 1) return 0;
+  if (N < 128 || N % 128 || !supported_k(K)) return fail("d3_grouped: N % 128 == 0, K in {256..2048}");
+  const dim3 grid(N / RPB, n_groups);
+  const hipStream_t s = (hipStream_t)stream;
+  const uint8_t* hw = (const uint8_t*)host_w;
+  uint8_t* sw = (uint8_t*)slot_w;
+  switch (kind) {
+    case 0: D3_K_SWITCH(K, hipLaunchKernelGGL((grouped_kernel<0, KK>), grid, dim3(256), 0, s, x, groups, sw, slot_s, slot_c, hw, host_s, host_c, codebook, out, N)); break;
+    case 1: D3_K_SWITCH(K, hipLaunchKernelGGL((grouped_kernel<1, KK>), grid, dim3(256), 0, s, x, groups, sw, slot_s, slot_c, hw, host_s, host_c, codebook, out, N)); break;
+    case 4: D3_K_SWITCH(K, hipLaunchKernelGGL((grouped_kernel<4, KK>), grid, dim3(256), 0, s, x, groups, sw, slot_s, slot_c, hw, host_s, host_c, codebook, out, N)); break;
+    case 6: D3_K_SWITCH(K, hipLaunchKernelGGL((grouped_kernel<6, KK>), grid, dim3(256), 0, s, x, groups, sw, slot_s, slot_c, hw, host_s, host_c, codebook, out, N)); break;
+    default: return fail("d3_grouped: kind 0, 1, 4 or 6");
+  }
+  return done("d3_grouped");
+}
+
+}  // extern "C"

@@ -1,0 +1,144 @@
+"""gfx950 kernels for a layer's routed experts, with the reference's call surface (drama3/kernels.py:590-724).
+
+The reference compiles CUDA source with NVRTC at first use and launches it on torch's current stream
+(kernels.py:593-601). Here the kernels are HIP for gfx950, compiled ahead of time into libdrama3_moe.so and launched
+through its C ABI (include/drama3_moe.h) on the same stream; every function below keeps the reference's name,
+arguments, output shape / dtype and allocation (torch.empty on the input's device, so graph capture works), and
+nothing waits on the host.
+
+Differences from the reference, by design: float sums run in a different order (results agree within float
+tolerance, not bit for bit), and FP8 bytes are decoded by the hardware e4m3fn converter, so the two NaN codes 0x7F /
+0xFF read as NaN where the reference's bit trick reads +-480 (kernels.py:25-29); quantized checkpoints never hold
+them.
+"""
+import functools
+
+import torch
+
+from . import _lib
+
+ROWS_PER_BLOCK = 16
+
+
+@functools.cache
+def _gfx950(index):
+    return torch.cuda.get_device_properties(index).gcnArchName.split(":")[0] == "gfx950"
+
+
+def available(device):
+    """Whether the kernels run on `device`: a gfx950 GPU. On such a device a missing library is an error, not a
+    fallback."""
+    if device.type != "cuda" or not torch.cuda.is_available():
+        return False
+    if not _gfx950(device.index if device.index is not None else torch.cuda.current_device()):
+        return False
+    _lib.lib()  # raises if libdrama3_moe.so was not built
+    return True
+
+
+def _stream(t):
+    return _lib.stream_of(t.device)
+
+
+def _p(t):
+    return None if t is None else t.data_ptr()
+
+
+def _call(name, *args):
+    _lib.check(getattr(_lib.lib(), name)(*args), name)
+
+
+def route(logits, k):
+    """(ids [1, k] int64, weights [1, k] float32) of one row of router logits [1, n] (bfloat16): the k largest, by
+    descending logit (ties to the lower index), and their softmax weights renormalized over them, rounded to
+    bfloat16."""
+    rows, n = logits.shape
+    logits = logits.contiguous()
+    ids = torch.empty((rows, k), dtype=torch.int64, device=logits.device)
+    weights = torch.empty((rows, k), dtype=torch.float32, device=logits.device)
+    _call("d3_route", _p(logits), rows, n, k, _p(ids), _p(weights), _stream(logits))
+    return ids, weights
+
+
+def weighted_sum(parts, weights):
+    """[1, H] bfloat16: parts [k, H] (float32) summed by weights [k] (float32)."""
+    parts = parts.contiguous()
+    weights = weights.contiguous()
+    out = torch.empty((1, parts.shape[1]), dtype=torch.bfloat16, device=parts.device)
+    _call("d3_weighted_sum", _p(parts), _p(weights), parts.shape[0], parts.shape[1], _p(out), _stream(parts))
+    return out
+
+
+def rotate(x, only_if, swiglu=False):
+    """Rows of x [rows, K] (float32 or bfloat16; float32 [rows, 2K] gate | up with `swiglu`, SiLU(gate) * up first) in
+    the ConvRot basis: float32 [rows, K]. Only when `only_if` (an int32 on the GPU) is set; otherwise the output is
+    left unset."""
+    rows, width = x.shape
+    k = width // 2 if swiglu else width
+    x = x.contiguous()
+    if swiglu and x.dtype != torch.float32:
+        raise TypeError("rotate(swiglu=True) takes float32 gate | up rows")
+    mode = 2 if swiglu else 1 if x.dtype == torch.bfloat16 else 0
+    if mode == 0 and x.dtype != torch.float32:
+        x = x.float()
+    out = torch.empty((rows, k), dtype=torch.float32, device=x.device)
+    _call("d3_rotate", _p(x), mode, rows, k, _p(out), _p(only_if), _stream(x))
+    return out
+
+
+def gemv_int8(x, ids, plan, took_over, late, slot_fields, host_fields, n):
+    """[k, n] float32: each expert's int8 rows against x [1 or k, K] (float32, rotated); fields are {"_qdata",
+    "scale"}."""
+    k, width = ids.shape[0], x.shape[1]
+    x = x.contiguous()
+    out = torch.empty((k, n), dtype=torch.float32, device=x.device)
+    _call("d3_gemv_int8", _p(x), x.shape[0], _p(ids), _p(plan), _p(took_over), int(late), _p(slot_fields["_qdata"]),
+          _p(slot_fields["scale"]), _p(host_fields["_qdata"]), _p(host_fields["scale"]), _p(out), k, n, width,
+          _stream(x))
+    return out
+
+
+def gemv_fp8(x, ids, plan, slot_fields, host_fields, n):
+    """[k, n] float32: each expert's float8 rows against x [1 or k, K] float32; fields are {"weight", "scale"}."""
+    k, width = ids.shape[0], x.shape[1]
+    x = x.contiguous()
+    out = torch.empty((k, n), dtype=torch.float32, device=x.device)
+    _call("d3_gemv_fp8", _p(x), x.shape[0], _p(ids), _p(plan), _p(slot_fields["weight"]), _p(slot_fields["scale"]),
+          _p(host_fields["weight"]), _p(host_fields["scale"]), _p(out), k, n, width, _stream(x))
+    return out
+
+
+def gemv_codes(x, ids, plan, slot_fields, host_fields, codebook, bits, n):
+    """gemv_int8 for W4A8/W6A8 banks; fields are {"_qdata", "scale" (e4m3), "s_channel"}, codebook [16] at 4 bits."""
+    k, width = ids.shape[0], x.shape[1]
+    x = x.contiguous()
+    out = torch.empty((k, n), dtype=torch.float32, device=x.device)
+    _call("d3_gemv_codes", _p(x), x.shape[0], _p(ids), _p(plan), _p(slot_fields["_qdata"]), _p(slot_fields["scale"]),
+          _p(slot_fields["s_channel"]), _p(host_fields["_qdata"]), _p(host_fields["scale"]),
+          _p(host_fields["s_channel"]), _p(codebook), int(bits), _p(out), k, n, width, _stream(x))
+    return out
+
+
+def _grouped(kind, x, groups, slot_fields, host_fields, codebook, n, wkey):
+    x = x.contiguous()
+    out = torch.empty((x.shape[0], n), dtype=torch.float32, device=x.device)
+    _call("d3_grouped", kind, _p(x), _p(groups), groups.shape[0], _p(slot_fields[wkey]), _p(slot_fields["scale"]),
+          _p(slot_fields.get("s_channel")), _p(host_fields[wkey]), _p(host_fields["scale"]),
+          _p(host_fields.get("s_channel")), _p(codebook), _p(out), n, x.shape[1], _stream(x))
+    return out
+
+
+def grouped_int8(x, groups, slot_fields, host_fields, n):
+    """[rows, n] float32 for x's rows (float32, rotated, sorted by expert) through their experts; groups [g, 5] int32
+    (expert, slot, fill, first row, rows). Rows outside every group are left unset."""
+    return _grouped(0, x, groups, slot_fields, host_fields, None, n, "_qdata")
+
+
+def grouped_fp8(x, groups, slot_fields, host_fields, n):
+    """grouped_int8 for float8 experts, against float32 rows x."""
+    return _grouped(1, x, groups, slot_fields, host_fields, None, n, "weight")
+
+
+def grouped_codes(x, groups, slot_fields, host_fields, codebook, bits, n):
+    """grouped_int8 for W4A8/W6A8 banks (see gemv_codes)."""
+    return _grouped(int(bits), x, groups, slot_fields, host_fields, codebook, n, "_qdata")
