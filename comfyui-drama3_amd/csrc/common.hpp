@@ -119,8 +119,58 @@ D3_INLINE void put_tagged(uint64_t* p, float v, uint32_t epoch) {
                      __HIP_MEMORY_SCOPE_AGENT);
 }
 D3_INLINE uint64_t get_tagged(const uint64_t* p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+// A first read that may be served by this XCD's caches: one workgroup's miss brings the line in for the others. A
+// stale line (read before the producer's store landed) shows an old epoch, and the word is then read with get_tagged.
+D3_INLINE uint64_t get_tagged_cached(const uint64_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
 D3_INLINE bool tag_is(uint64_t word, uint32_t epoch) { return (uint32_t)(word >> 32) == epoch; }
 D3_INLINE float tagged_value(uint64_t word) { return __uint_as_float((uint32_t)word); }
+
+// N tagged words at p[0..N) (stride `stride`): all loads issued at once, then the stale ones (not yet landed) read
+// again until they carry `epoch` (bounded by keep_polling). Values go to v.
+template <int N>
+D3_INLINE void gather_tagged(const uint64_t* p, int stride, uint32_t epoch, float* v, uint32_t* status, uint32_t limit) {
+  uint64_t w[N];
+#pragma unroll
+  for (int i = 0; i < N; i++) w[i] = get_tagged_cached(p + i * stride);
+  bool fresh = true;
+#pragma unroll
+  for (int i = 0; i < N; i++) fresh = fresh && tag_is(w[i], epoch);
+  if (!fresh) {
+    uint32_t polls = 0;
+    while (true) {
+      bool all = true;
+#pragma unroll
+      for (int i = 0; i < N; i++) {
+        if (!tag_is(w[i], epoch)) w[i] = get_tagged(p + i * stride);
+        all = all && tag_is(w[i], epoch);
+      }
+      if (all) break;
+      // keep_polling's limit counts rounds; it also records the timeout
+      uint32_t st = __hip_atomic_load(status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (st != 0u || ++polls > limit) {
+        if (st == 0u) __hip_atomic_fetch_or(status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < N; i++) v[i] = tagged_value(w[i]);
+}
+
+// The dispatch's ID: the HSA queue's packet index of this launch, the same for every workgroup, larger for every later
+// dispatch on the queue (graph replays included). LLVM's intrinsic, which clang does not expose as a builtin.
+extern "C" __device__ uint64_t d3_dispatch_id() __asm("llvm.amdgcn.dispatch.id");
+D3_INLINE uint32_t launch_epoch() {
+  const uint32_t e = (uint32_t)d3_dispatch_id() + 1u;
+  return e == 0u ? 1u : e;
+}
+D3_INLINE uint64_t signal_load64(const uint64_t* p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+
+// every memory access of this wave so far has completed (its LDS writes are visible to its own lanes)
+D3_INLINE void settle() { __builtin_amdgcn_s_waitcnt(0); }
 
 D3_INLINE uint32_t signal_add_ret(uint32_t* counter, uint32_t v) {
   return __hip_atomic_fetch_add(counter, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -131,9 +181,10 @@ D3_INLINE uint32_t signal_load(const uint32_t* counter) {
 D3_INLINE void signal_store(uint32_t* counter, uint32_t v) {
   __hip_atomic_store(counter, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-// one more poll allowed? Records a timeout in `status` (and stops every later wait of the launch at once).
+// one more poll allowed? Records a timeout in `status`; every 32 polls it also checks `status`, so after one timeout
+// the launch's other waits stop soon.
 D3_INLINE bool keep_polling(uint32_t& polls, uint32_t* status, uint32_t limit) {
-  if (signal_load(status) != 0u) return false;
+  if ((polls & 31u) == 31u && signal_load(status) != 0u) return false;
   if (++polls > limit) {
     __hip_atomic_fetch_or(status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     return false;

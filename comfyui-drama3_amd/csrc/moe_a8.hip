@@ -10,9 +10,9 @@
 // k, bf16-rounded weights: kernels.py:39-67's semantics), builds the sorted union of their experts (U of them) and
 // groups it into down chunks of at most 8 experts and 32 (expert, row) pairs. It quantizes the activations into LDS.
 // Then it takes work items round-robin (item, item + gridDim, ...):
-//   gate_up item (u, tile): gate rows 8 tile .. 8 tile + 7 and the matching up rows of expert u, one 16-row MFMA tile
-//     over K = H (the 4 waves split K); the expert's rows are the MFMA columns. The epilogue applies the scales and
-//     SiLU(gate) * up and publishes 8 hidden units per row.
+//   gate_up item (u, tile): gate rows 16 tile .. 16 tile + 15 and the matching up rows of expert u, two 16-row MFMA
+//     tiles over K = H (the 4 waves split K); the expert's rows are the MFMA columns. The epilogue applies the scales
+//     and SiLU(gate) * up and publishes 16 hidden units per row.
 //   down item (chunk c, block b): output rows 8 b .. 8 b + 7 of every expert of the chunk, over K = I. Each wave packs
 //     two experts into one 16-row MFMA tile (rows 0-7 and 8-15) with both experts' rows as columns. It loads its
 //     weights first, then collects the chunk's hidden rows as they are published, quantizes them into LDS and runs.
@@ -23,10 +23,12 @@
 // and the lowest unfinished item can always run: no wait can block forever. Waits are bounded anyway (spin_limit),
 // and a timeout sets sync[SYNC_STATUS].
 //
-// Hand-off: hidden units and partial outputs are 64-bit words (value, epoch) written and polled with device-coherent
-// accesses (common.hpp), so a consumer waits on the data itself. The epoch is the workspace's launch count + 1: every
-// workgroup reads the count on entry, and the last down item advances it, after every item of the launch has read it.
-// Launches that overlap on one workspace race.
+// Hand-off: hidden units, each gate_up item's absmax and partial outputs are 64-bit words (value, epoch) written and
+// read with device-coherent accesses (common.hpp); a gate_up item also counts itself done in its expert's counter (no
+// wait for its stores: a word that has not landed yet is told apart by its epoch and read again). Down items poll only
+// those counters. The epoch is the dispatch ID + 1, which grows with every dispatch on a queue, so a workspace carries
+// over from launch to launch (and graph replay to replay) with nothing to clear; it must stay on one stream (queue),
+// and launches that overlap on one workspace race.
 #include "formats.hpp"
 #include "../../include/drama3_moe.h"
 
@@ -38,8 +40,8 @@
 
 namespace d3 {
 
-// sync words, 256 bytes apart
-enum : int { SYNC_SEQ = 0, SYNC_PASSED = 64, SYNC_STATUS = 128, SYNC_WORDS = 256 };
+// sync words (32-bit), 256 bytes apart: status, then per expert slot a 64-bit (epoch, gate_up items done) counter
+enum : int { SYNC_STATUS = 0, SYNC_DONE = 64, SYNC_WORDS = 64 + 64 * 128 };
 constexpr int MAX_M = 16, MAX_K = 8, MAX_E = 256, MAX_PAIRS = MAX_M * MAX_K;
 constexpr int CHUNK_EXPERTS = 8, CHUNK_PAIRS = 32;
 
@@ -54,10 +56,12 @@ struct MoeA8Args {
   int64_t* ids_out;
   float* weights_out;
   uint64_t* hidden;  // [M * topk, I] tagged
+  uint64_t* tmax;    // [M * topk, I / 16] tagged: absmax of each gate_up item's 16 hidden units
   uint64_t* parts;   // [M * topk, H] tagged
   uint32_t* sync;
   int M, E, topk;
   uint32_t spin_limit;
+  int dn_start;  // down items load their weights once this many 256ths of their chunk's gate_up tiles are done
 };
 
 // LDS carve-up (bytes), shared by host (launch size) and device.
@@ -80,7 +84,7 @@ struct Lds {
     upair = take(MAX_PAIRS * MAX_M);
     chunk_first = take((MAX_PAIRS + 1) * 4);
     misc = take(64);
-    red = take(2 * 4 * 256 * 4);
+    red = take(2 * 2 * 4 * 256 * 4);
     hq = take(pmax * I);
     hs = take(pmax * 4);
     lparts = take(pmax * 8 * 4);
@@ -91,6 +95,11 @@ struct Lds {
     total = o;
   }
 };
+
+// Per-expert-slot counter of finished gate_up items: (epoch << 32) | count. An item raises it to (epoch, 0) when it
+// starts (atomic max: a stale count of an earlier launch is replaced, this launch's count is kept) and adds 1 when it
+// has published; the down items wait for (epoch, T). Nothing needs clearing between launches.
+D3_INLINE uint64_t* done_counter(uint32_t* sync, int u) { return (uint64_t*)(sync + SYNC_DONE + 64 * u); }
 
 template <int F> __host__ __device__ constexpr float act_qmax() { return F == FMT_F8 ? 448.0f : 127.0f; }
 
@@ -143,7 +152,8 @@ struct Ctx {
   uint32_t epoch;
 };
 
-// gate_up tile: gate rows 8 tile .. 8 tile + 7 and up rows I + 8 tile .. of expert u
+// gate_up item: hidden units 16 tile .. 16 tile + 15 of expert u, i.e. two 16-row MFMA tiles (sub-tile s: gate rows
+// 16 tile + 8 s .. + 7 as rows 0-7, the matching up rows as rows 8-15)
 template <int F, int H, int I>
 D3_INLINE void gate_up_item(const Ctx& cx, int u, int tile, int parity) {
   constexpr int SPW = H / 512;  // steps per wave
@@ -152,57 +162,76 @@ D3_INLINE void gate_up_item(const Ctx& cx, int u, int tile, int parity) {
   const MoeA8Args& a = *cx.a;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, q = lane >> 4, col = lane & 15;
   const int e = cx.ulist[u], nu = cx.ucount[u];
+  uint64_t raised = 0;
+  if (tid == 0)
+    raised = __hip_atomic_fetch_max(done_counter(a.sync, u), (uint64_t)cx.epoch << 32, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   const int ra = lane & 15;
-  const uint8_t* wp = a.gu_w + ((size_t)e * (2 * I) + (ra < 8 ? 8 * tile + ra : I + 8 * tile + ra - 8)) * RB;
-  Raw<F> raw[SPW];
+  auto row_of = [&](int sub, int r) {
+    return (size_t)e * (2 * I) + (r < 8 ? 16 * tile + 8 * sub + r : I + 16 * tile + 8 * sub + r - 8);
+  };
+  Raw<F> raw[2][SPW];
 #pragma unroll
-  for (int s = 0; s < SPW; s++) load_step<F>(raw[s], wp, w * SPW + s, q);
-  float sc[SPW][4];
+  for (int sub = 0; sub < 2; sub++)
+#pragma unroll
+    for (int s = 0; s < SPW; s++) load_step<F>(raw[sub][s], a.gu_w + row_of(sub, ra) * RB, w * SPW + s, q);
+  float sc[2][SPW][4];
   if constexpr (group_scaled(F)) {
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const int rc = 4 * q + i;
-      const size_t srow = (size_t)e * (2 * I) + (rc < 8 ? 8 * tile + rc : I + 8 * tile + rc - 8);
+    for (int sub = 0; sub < 2; sub++)
 #pragma unroll
-      for (int s = 0; s < SPW; s++) sc[s][i] = bf16_to_f32(a.gu_s[srow * (H / 128) + w * SPW + s]);
+      for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int s = 0; s < SPW; s++) sc[sub][s][i] = bf16_to_f32(a.gu_s[row_of(sub, 4 * q + i) * (H / 128) + w * SPW + s]);
+  }
+  // row scales for the epilogue (wave 0, unit j = lane & 15), fetched with the rows
+  float gs = 1.0f, us = 1.0f;
+  if constexpr (!group_scaled(F)) {
+    if (w == 0) {
+      gs = bf16_to_f32(a.gu_s[(size_t)e * (2 * I) + 16 * tile + (lane & 15)]);
+      us = bf16_to_f32(a.gu_s[(size_t)e * (2 * I) + I + 16 * tile + (lane & 15)]);
     }
   }
   const bool active = col < nu;
   const uint8_t* xp = cx.xq + (size_t)(active ? cx.utok[u * MAX_M + col] : 0) * H;
-  i32x4 iacc = {0, 0, 0, 0};
-  f32x4 facc = {0.0f, 0.0f, 0.0f, 0.0f};
+  float* rd = cx.red + parity * 2048;
 #pragma unroll
-  for (int s = 0; s < SPW; s++) {
-    i32x4 xlo = {0, 0, 0, 0}, xhi = {0, 0, 0, 0};
-    if (active) {
-      const uint8_t* p = xp + 128 * (w * SPW + s) + 32 * q;
-      xlo = *(const i32x4*)p;
-      xhi = *(const i32x4*)(p + 16);
-    }
-    if constexpr (F == FMT_I8) {
-      iacc = step_i8<F>(raw[s], xlo, xhi, iacc);
-    } else if constexpr (F == FMT_F8) {
-      facc = step_f8(raw[s], xlo, xhi, facc);
-    } else {
-      const i32x4 g = step_i8<F>(raw[s], xlo, xhi, i32x4{0, 0, 0, 0});
+  for (int sub = 0; sub < 2; sub++) {
+    i32x4 iacc = {0, 0, 0, 0};
+    f32x4 facc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-      for (int i = 0; i < 4; i++) facc[i] += (float)(g[i] >> SHIFT) * sc[s][i];
+    for (int s = 0; s < SPW; s++) {
+      i32x4 xlo = {0, 0, 0, 0}, xhi = {0, 0, 0, 0};
+      if (active) {
+        const uint8_t* p = xp + 128 * (w * SPW + s) + 32 * q;
+        xlo = *(const i32x4*)p;
+        xhi = *(const i32x4*)(p + 16);
+      }
+      if constexpr (F == FMT_I8) {
+        iacc = step_i8<F>(raw[sub][s], xlo, xhi, iacc);
+      } else if constexpr (F == FMT_F8) {
+        facc = step_f8(raw[sub][s], xlo, xhi, facc);
+      } else {
+        const i32x4 g = step_i8<F>(raw[sub][s], xlo, xhi, i32x4{0, 0, 0, 0});
+#pragma unroll
+        for (int i = 0; i < 4; i++) facc[i] += (float)(g[i] >> SHIFT) * sc[sub][s][i];
+      }
     }
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+      rd[sub * 1024 + w * 256 + (4 * q + i) * 16 + col] = F == FMT_I8 ? __int_as_float(iacc[i]) : facc[i];
   }
-  float* rd = cx.red + parity * 1024;
-#pragma unroll
-  for (int i = 0; i < 4; i++) rd[w * 256 + (4 * q + i) * 16 + col] = F == FMT_I8 ? __int_as_float(iacc[i]) : facc[i];
   __syncthreads();
   if (w == 0) {
-    for (int idx = lane; idx < 8 * nu; idx += 64) {
-      const int n = idx >> 3, j = idx & 7;
+    for (int idx = lane; idx < 16 * nu; idx += 64) {
+      const int n = idx >> 4, j = idx & 15, sub = j >> 3, jj = j & 7;
+      const float* rs = rd + sub * 1024;
       float g, up;
       if constexpr (F == FMT_I8) {
         int gi = 0, ui = 0;
 #pragma unroll
         for (int ww = 0; ww < 4; ww++) {
-          gi += __float_as_int(rd[ww * 256 + j * 16 + n]);
-          ui += __float_as_int(rd[ww * 256 + (8 + j) * 16 + n]);
+          gi += __float_as_int(rs[ww * 256 + jj * 16 + n]);
+          ui += __float_as_int(rs[ww * 256 + (8 + jj) * 16 + n]);
         }
         g = (float)gi;
         up = (float)ui;
@@ -211,18 +240,33 @@ D3_INLINE void gate_up_item(const Ctx& cx, int u, int tile, int parity) {
         up = 0.0f;
 #pragma unroll
         for (int ww = 0; ww < 4; ww++) {
-          g += rd[ww * 256 + j * 16 + n];
-          up += rd[ww * 256 + (8 + j) * 16 + n];
+          g += rs[ww * 256 + jj * 16 + n];
+          up += rs[ww * 256 + (8 + jj) * 16 + n];
         }
       }
       if constexpr (!group_scaled(F)) {
-        g *= bf16_to_f32(a.gu_s[(size_t)e * (2 * I) + 8 * tile + j]);
-        up *= bf16_to_f32(a.gu_s[(size_t)e * (2 * I) + I + 8 * tile + j]);
+        g *= gs;
+        up *= us;
       }
       const float s = cx.sx[cx.utok[u * MAX_M + n]];
       g *= s;
       up *= s;
-      put_tagged(a.hidden + (size_t)cx.upair[u * MAX_M + n] * I + 8 * tile + j, g / (1.0f + __expf(-g)) * up, cx.epoch);
+      const float h = g / (1.0f + __expf(-g)) * up;
+      const int p = cx.upair[u * MAX_M + n];
+      put_tagged(a.hidden + (size_t)p * I + 16 * tile + j, h, cx.epoch);
+      // absmax of the row's 16 units: lanes 16n .. 16n + 15 (quad swaps, half-row and row mirrors)
+      float m = fabsf(h);
+      m = fmaxf(m, __int_as_float(dpp_i32(__float_as_int(m), 0xB1)));
+      m = fmaxf(m, __int_as_float(dpp_i32(__float_as_int(m), 0x4E)));
+      m = fmaxf(m, __int_as_float(dpp_i32(__float_as_int(m), 0x141)));
+      m = fmaxf(m, __int_as_float(dpp_i32(__float_as_int(m), 0x140)));
+      if (j == 0) put_tagged(a.tmax + (size_t)p * (I / 16) + tile, m, cx.epoch);
+    }
+    if (lane == 0) {
+      // the raise has returned (its value is used), so the add lands after it; a counter of a later epoch means the
+      // workspace was used on another queue: flag it
+      if ((uint32_t)(raised >> 32) > cx.epoch) __hip_atomic_fetch_or(a.sync + SYNC_STATUS, 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_fetch_add(done_counter(a.sync, u), (uint64_t)1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
 }
@@ -235,7 +279,6 @@ D3_INLINE void down_item(const Ctx& cx, int c, int hb) {
   constexpr int SHIFT = unpack_shift(F);
   constexpr float QMAX = act_qmax<F>();
   constexpr int G8 = I / 8;  // 8-column groups of a hidden row
-  constexpr int GPL = (G8 + 63) / 64;
   const MoeA8Args& a = *cx.a;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, q = lane >> 4, col = lane & 15;
   const int M = a.M, K8 = a.topk;
@@ -243,6 +286,22 @@ D3_INLINE void down_item(const Ctx& cx, int c, int hb) {
   int* slot_first = cx.slot_first;
   __syncthreads();  // the previous item's readers of the slot tables and partial outputs are done
 
+  // The down weights queue behind the chunk's gate_up weights: the item loads them once dn_start / 256 of the chunk's
+  // gate_up tiles are done, so the gate_up rows arrive first and the hand-off overlaps the down rows' arrival.
+  if (tid == 0 && a.dn_start > 0) {
+    const uint32_t want = (uint32_t)((ne * (I / 16) * a.dn_start) >> 8);
+    uint32_t polls = 0;
+    while (true) {
+      uint64_t n[CHUNK_EXPERTS];
+#pragma unroll
+      for (int lj = 0; lj < CHUNK_EXPERTS; lj++) n[lj] = lj < ne ? signal_load64(done_counter(a.sync, u0 + lj)) : 0;
+      uint32_t total = 0;
+#pragma unroll
+      for (int lj = 0; lj < CHUNK_EXPERTS; lj++) total += (uint32_t)(n[lj] >> 32) == cx.epoch ? (uint32_t)n[lj] : 0u;
+      if (total >= want || !keep_polling(polls, a.sync + SYNC_STATUS, a.spin_limit)) break;
+    }
+  }
+  __syncthreads();
   // this lane's weight row: local expert 2w + (row / 8), output row 8 hb + row % 8
   const int ra = lane & 15;
   const int lj_a = 2 * w + (ra >> 3);
@@ -257,12 +316,16 @@ D3_INLINE void down_item(const Ctx& cx, int c, int hb) {
   const int lj_c = 2 * w + (q >> 1);
   const int e_c = lj_c < ne ? cx.ulist[u0 + lj_c] : 0;
   float sc[STEPS][4];
+  float rs[4] = {0.0f, 0.0f, 0.0f, 0.0f};
   if constexpr (group_scaled(F)) {
 #pragma unroll
     for (int i = 0; i < 4; i++)
 #pragma unroll
       for (int s = 0; s < STEPS; s++)
         sc[s][i] = lj_c < ne ? bf16_to_f32(a.dn_s[((size_t)e_c * H + 8 * hb + 4 * (q & 1) + i) * (I / 128) + s]) : 0.0f;
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; i++) rs[i] = lj_c < ne ? bf16_to_f32(a.dn_s[(size_t)e_c * H + 8 * hb + 4 * (q & 1) + i]) : 0.0f;
   }
   if (tid == 0) {
     int slot = 0;
@@ -280,52 +343,103 @@ D3_INLINE void down_item(const Ctx& cx, int c, int hb) {
   }
   __syncthreads();
   const int P = slot_first[ne];
-  // the chunk's hidden rows, collected as the gate_up tiles publish them and quantized per pair into LDS
-  for (int slot = w; slot < P; slot += 4) {
-    const uint64_t* hp = a.hidden + (size_t)cx.slot_pair[slot] * I;
-    uint64_t word[GPL][8];
-    uint32_t polls = 0;
-    while (true) {
+  constexpr int T = I / 16;             // gate_up tiles per expert
+  constexpr int GPH = (G8 + 31) / 32;   // 8-column groups per lane of a half-wave
+  constexpr int TPH = (T + 31) / 32;    // tile maxima per lane of a half-wave
+  if (2 * w < ne) {
+    // Each wave serves its two experts on its own: waits for their gate_up tiles (lane 0 polls their counters), then
+    // gathers their pairs' hidden rows two at a time (a pair per half-wave: the tiles' maxima and the values in one
+    // round trip; words whose store has not landed yet are read again), quantizes them into its LDS slots and runs.
+    const int la = 2 * w, lb = 2 * w + 1;
+    const bool has_b = lb < ne;
+    if (lane == 0) {
+      uint32_t polls = 0;
+      while (true) {
+        const uint64_t want = ((uint64_t)cx.epoch << 32) | (uint32_t)T;
+        const uint64_t na = signal_load64(done_counter(a.sync, u0 + la));
+        const uint64_t nb = has_b ? signal_load64(done_counter(a.sync, u0 + lb)) : want;
+        if ((na == want && nb == want) || !keep_polling(polls, a.sync + SYNC_STATUS, a.spin_limit)) break;
+      }
+    }
+    const int s0 = slot_first[la], s1 = slot_first[has_b ? lb + 1 : la + 1];
+    const int half = lane >> 5, hl = lane & 31;
+    for (int sp = s0; sp < s1; sp += 2) {
+      const int slot = sp + half;
+      const bool on = slot < s1;
+      const int p = cx.slot_pair[on ? slot : s0];
+      uint64_t mw[TPH], vw[GPH][8];
+#pragma unroll
+      for (int k = 0; k < TPH; k++) {
+        const int t = hl + 32 * k;
+        mw[k] = on && t < T ? get_tagged_cached(a.tmax + (size_t)p * T + t) : 0;
+      }
+#pragma unroll
+      for (int k = 0; k < GPH; k++) {
+        const int g8 = hl + 32 * k;
+#pragma unroll
+        for (int i = 0; i < 8; i++) vw[k][i] = on && g8 < G8 ? get_tagged_cached(a.hidden + (size_t)p * I + 8 * g8 + i) : 0;
+      }
+      // words not yet landed: read again, coherently
       bool fresh = true;
 #pragma unroll
-      for (int k = 0; k < GPL; k++) {
-        const int g8 = lane + 64 * k;
+      for (int k = 0; k < TPH; k++) fresh = fresh && (!on || hl + 32 * k >= T || tag_is(mw[k], cx.epoch));
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-          if (g8 < G8) {
-            word[k][i] = get_tagged(hp + 8 * g8 + i);
-            fresh = fresh && tag_is(word[k][i], cx.epoch);
-          } else {
-            word[k][i] = 0;
+      for (int k = 0; k < GPH; k++)
+#pragma unroll
+        for (int i = 0; i < 8; i++) fresh = fresh && (!on || hl + 32 * k >= G8 || tag_is(vw[k][i], cx.epoch));
+      if (!__all(fresh)) {
+        uint32_t polls = 0;
+        while (true) {
+          bool ok = true;
+#pragma unroll
+          for (int k = 0; k < TPH; k++) {
+            const int t = hl + 32 * k;
+            if (on && t < T && !tag_is(mw[k], cx.epoch)) mw[k] = get_tagged(a.tmax + (size_t)p * T + t);
+            ok = ok && (!on || t >= T || tag_is(mw[k], cx.epoch));
           }
+#pragma unroll
+          for (int k = 0; k < GPH; k++) {
+            const int g8 = hl + 32 * k;
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+              if (on && g8 < G8 && !tag_is(vw[k][i], cx.epoch)) vw[k][i] = get_tagged(a.hidden + (size_t)p * I + 8 * g8 + i);
+              ok = ok && (!on || g8 >= G8 || tag_is(vw[k][i], cx.epoch));
+            }
+          }
+          if (__all(ok) || !keep_polling(polls, a.sync + SYNC_STATUS, a.spin_limit)) break;
         }
       }
-      if (__all(fresh)) break;
-      if (!keep_polling(polls, a.sync + SYNC_STATUS, a.spin_limit)) break;
-    }
-    float v[GPL][8];
-    float amax = 0.0f;
+      // the pair's absmax over its tiles' maxima: a half-wave reduction (rows 0-1 or 2-3 of the wave)
+      float m = 0.0f;
 #pragma unroll
-    for (int k = 0; k < GPL; k++)
+      for (int k = 0; k < TPH; k++) m = fmaxf(m, tagged_value(mw[k]));
+      m = fmaxf(m, __int_as_float(dpp_i32(__float_as_int(m), 0xB1)));
+      m = fmaxf(m, __int_as_float(dpp_i32(__float_as_int(m), 0x4E)));
+      m = fmaxf(m, __int_as_float(dpp_i32(__float_as_int(m), 0x141)));
+      m = fmaxf(m, __int_as_float(dpp_i32(__float_as_int(m), 0x140)));
+      const float m0 = fmaxf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 0)),
+                             __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 16)));
+      const float m1 = fmaxf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 32)),
+                             __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 48)));
+      const float amax = half ? m1 : m0;
+      const float inv = amax > 0.0f ? QMAX / amax : 0.0f;
+      if (on) {
 #pragma unroll
-      for (int i = 0; i < 8; i++) {
-        v[k][i] = tagged_value(word[k][i]);
-        amax = fmaxf(amax, fabsf(v[k][i]));
+        for (int k = 0; k < GPH; k++) {
+          const int g8 = hl + 32 * k;
+          if (g8 < G8) {
+            float v[8];
+#pragma unroll
+            for (int i = 0; i < 8; i++) v[i] = tagged_value(vw[k][i]);
+            store_act8<F>(cx.hq + (size_t)slot * I + 8 * g8, v, inv);
+          }
+        }
+        if (hl == 0) cx.hs[slot] = amax / QMAX;
       }
-    amax = wave_max_f32(amax);
-    const float inv = amax > 0.0f ? QMAX / amax : 0.0f;
-#pragma unroll
-    for (int k = 0; k < GPL; k++) {
-      const int g8 = lane + 64 * k;
-      if (g8 < G8) store_act8<F>(cx.hq + (size_t)slot * I + 8 * g8, v[k], inv);
     }
-    if (lane == 0) cx.hs[slot] = amax / QMAX;
-  }
-  __syncthreads();
-  if (2 * w < ne) {
-    const int la = 2 * w, lb = 2 * w + 1;
+    settle();  // this wave's LDS slots are written before its lanes read each other's
     const int na = slot_first[la + 1] - slot_first[la];
-    const int nb = lb < ne ? slot_first[lb + 1] - slot_first[lb] : 0;
+    const int nb = has_b ? slot_first[lb + 1] - slot_first[lb] : 0;
     const bool one_pass = na + nb <= 16;
     const bool rows_b = q >= 2;
     for (int pass = 0; pass < (one_pass ? 1 : 2); pass++) {
@@ -365,8 +479,8 @@ D3_INLINE void down_item(const Ctx& cx, int c, int hb) {
         for (int i = 0; i < 4; i++) {
           const int r = 4 * (q & 1) + i;
           float y;
-          if constexpr (F == FMT_I8) y = (float)iacc[i] * bf16_to_f32(a.dn_s[(size_t)e_c * H + 8 * hb + r]);
-          else if constexpr (F == FMT_F8) y = facc[i] * bf16_to_f32(a.dn_s[(size_t)e_c * H + 8 * hb + r]);
+          if constexpr (F == FMT_I8) y = (float)iacc[i] * rs[i];
+          else if constexpr (F == FMT_F8) y = facc[i] * rs[i];
           else y = facc[i];
           cx.lparts[slot * 8 + r] = y * hsc;
         }
@@ -392,7 +506,7 @@ D3_INLINE void down_item(const Ctx& cx, int c, int hb) {
       for (int idx = tid; idx < M * K8 * 8; idx += 256) {
         const int p = idx >> 3, r = idx & 7;
         const uint64_t* src = a.parts + (size_t)p * H + 8 * hb + r;
-        uint64_t word = get_tagged(src);
+        uint64_t word = get_tagged_cached(src);
         uint32_t polls = 0;
         while (!tag_is(word, cx.epoch) && keep_polling(polls, a.sync + SYNC_STATUS, a.spin_limit)) word = get_tagged(src);
         cx.fparts[idx] = tagged_value(word);
@@ -406,20 +520,12 @@ D3_INLINE void down_item(const Ctx& cx, int c, int hb) {
       }
     }
   }
-  if (tid == 0) {
-    // the launch's last down item advances the epoch for the next launch
-    const uint32_t passed = signal_add_ret(a.sync + SYNC_PASSED, 1u);
-    if (passed == (uint32_t)cx.n_dn - 1u) {
-      signal_store(a.sync + SYNC_PASSED, 0u);
-      signal_store(a.sync + SYNC_SEQ, cx.epoch);
-    }
-  }
 }
 
 template <int F, int H, int I>
-__global__ void __launch_bounds__(256, 4) moe_a8_kernel(MoeA8Args a) {
+__global__ void __launch_bounds__(256, 3) moe_a8_kernel(MoeA8Args a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-  constexpr int T = I / 8;
+  constexpr int T = I / 16;
   constexpr int NHB = H / 8;
   constexpr float QMAX = act_qmax<F>();
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
@@ -431,7 +537,6 @@ __global__ void __launch_bounds__(256, 4) moe_a8_kernel(MoeA8Args a) {
   cx.sx = (float*)(lds + L.sx);
   cx.rt_id = (int*)(lds + L.rt_id);
   cx.rt_w = (float*)(lds + L.rt_w);
-  uint32_t* emask = (uint32_t*)(lds + L.emask);
   cx.ulist = (int*)(lds + L.ulist);
   cx.ucount = (int*)(lds + L.ucount);
   cx.utok = lds + L.utok;
@@ -446,7 +551,7 @@ __global__ void __launch_bounds__(256, 4) moe_a8_kernel(MoeA8Args a) {
   cx.pair_slot = (int*)(lds + L.pair_slot);
   cx.slot_first = (int*)(lds + L.slot_first);
   cx.fparts = (float*)(lds + L.fparts);
-  cx.epoch = signal_load(a.sync + SYNC_SEQ) + 1u;
+  cx.epoch = launch_epoch();
 
   // ---- per row (one wave each): its logits and activations are loaded together, then routed and quantized
   for (int t = w; t < M; t += 4) {
@@ -504,40 +609,61 @@ __global__ void __launch_bounds__(256, 4) moe_a8_kernel(MoeA8Args a) {
     for (int k = 0; k < H / 512; k++) store_act8<F>(cx.xq + (size_t)t * H + 512 * k + 8 * lane, v[k], inv);
     if (lane == 0) cx.sx[t] = amax / QMAX;
   }
-  for (int e = tid; e < MAX_E; e += 256) emask[e] = 0;
   __syncthreads();
 
-  // ---- union of the rows' experts, ascending
-  for (int i = tid; i < M * K8; i += 256) atomicOr(&emask[cx.rt_id[(i / K8) * MAX_K + i % K8]], 1u << (i / K8));
-  __syncthreads();
+  // ---- union of the rows' experts, ascending, built by wave 0: lane l owns experts l, l + 64, l + 128, l + 192
   if (w == 0) {
+    uint32_t m[4] = {0u, 0u, 0u, 0u};
+    for (int t = 0; t < M; t++)
+      for (int j = 0; j < K8; j++) {
+        const int e = cx.rt_id[t * MAX_K + j];
+#pragma unroll
+        for (int k = 0; k < 4; k++) m[k] |= (e == lane + 64 * k ? 1u : 0u) << t;
+      }
     int base = 0;
-    for (int k = 0; k < MAX_E / 64; k++) {
-      const int e = 64 * k + lane;
-      const uint32_t m = e < E ? emask[e] : 0u;
-      const uint64_t ball = __ballot(m != 0u);
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      const int e = lane + 64 * k;
+      const uint64_t ball = __ballot(m[k] != 0u);
       const int pos = base + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(ball >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)ball, 0u));
-      if (m != 0u) cx.ulist[pos] = e;
+      if (m[k] != 0u) {
+        cx.ulist[pos] = e;
+        cx.ucount[pos] = __popc(m[k]);
+        int n = 0;
+        for (int t = 0; t < M; t++) {
+          if (!((m[k] >> t) & 1u)) continue;
+          int j = 0;
+          for (int jj = 0; jj < K8; jj++) j = cx.rt_id[t * MAX_K + jj] == e ? jj : j;
+          cx.utok[pos * MAX_M + n] = (uint8_t)t;
+          cx.upair[pos * MAX_M + n] = (uint8_t)(t * K8 + j);
+          n++;
+        }
+      }
       base += __popcll(ball);
     }
-    if (lane == 0) cx.misc[0] = base;
-  }
-  __syncthreads();
-  const int U = cx.misc[0];
-  for (int u = tid; u < U; u += 256) {
-    const int e = cx.ulist[u];
-    const uint32_t m = emask[e];
-    int n = 0;
-    for (int t = 0; t < M; t++) {
-      if (!((m >> t) & 1u)) continue;
-      int j = 0;
-      for (int jj = 0; jj < K8; jj++)
-        if (cx.rt_id[t * MAX_K + jj] == e) j = jj;
-      cx.utok[u * MAX_M + n] = (uint8_t)t;
-      cx.upair[u * MAX_M + n] = (uint8_t)(t * K8 + j);
-      n++;
+    // down chunks: consecutive experts, at most CHUNK_EXPERTS of them and CHUNK_PAIRS pairs; with M * topk <= 32
+    // pairs that is simply 8 experts each
+    if (M * K8 <= CHUNK_PAIRS) {
+      const int nch = (base + CHUNK_EXPERTS - 1) / CHUNK_EXPERTS;
+      for (int c = lane; c <= nch; c += 64) cx.chunk_first[c] = min(c * CHUNK_EXPERTS, base);
+      if (lane == 0) cx.misc[1] = nch;
+    } else if (lane == 0) {
+      int nch = 0, ne = 0, np = 0;
+      cx.chunk_first[0] = 0;
+      for (int u = 0; u < base; u++) {
+        const int n = cx.ucount[u];
+        if (ne == CHUNK_EXPERTS || np + n > CHUNK_PAIRS) {
+          cx.chunk_first[++nch] = u;
+          ne = 0;
+          np = 0;
+        }
+        ne++;
+        np += n;
+      }
+      cx.chunk_first[++nch] = base;
+      cx.misc[1] = nch;
     }
-    cx.ucount[u] = n;
+    if (lane == 0) cx.misc[0] = base;
   }
   if (blockIdx.x == 0) {
     for (int i = tid; i < M * K8; i += 256) {
@@ -546,24 +672,7 @@ __global__ void __launch_bounds__(256, 4) moe_a8_kernel(MoeA8Args a) {
     }
   }
   __syncthreads();
-  // down chunks: consecutive experts, at most CHUNK_EXPERTS of them and CHUNK_PAIRS pairs
-  if (tid == 0) {
-    int nch = 0, ne = 0, np = 0;
-    cx.chunk_first[0] = 0;
-    for (int u = 0; u < U; u++) {
-      const int n = cx.ucount[u];
-      if (ne == CHUNK_EXPERTS || np + n > CHUNK_PAIRS) {
-        cx.chunk_first[++nch] = u;
-        ne = 0;
-        np = 0;
-      }
-      ne++;
-      np += n;
-    }
-    cx.chunk_first[++nch] = U;
-    cx.misc[1] = nch;
-  }
-  __syncthreads();
+  const int U = cx.misc[0];
   cx.U = U;
   cx.nch = cx.misc[1];
   cx.n_dn = cx.nch * NHB;
@@ -611,7 +720,7 @@ int hip_fail(hipError_t err, const char* what) {
 
 int64_t moe_a8_workspace_bytes(int M, int topk, int H, int I) {
   const int64_t pairs = (int64_t)M * topk;
-  return SYNC_WORDS * 4 + pairs * I * 8 + pairs * H * 8;
+  return SYNC_WORDS * 4 + pairs * I * 8 + pairs * (I / 16) * 8 + pairs * H * 8;
 }
 
 using KernelFn = void (*)(MoeA8Args);
@@ -668,7 +777,7 @@ int launch_moe_a8(const d3_moe_a8_desc* d, hipStream_t stream) {
   const int umax = d->M * d->topk < d->E ? d->M * d->topk : d->E;
   // chunks hold up to 8 experts and 32 pairs; a chunk per expert bounds their count
   const int nch = umax;
-  const int items = umax * (d->I / 8) + nch * (d->H / 8);
+  const int items = umax * (d->I / 16) + nch * (d->H / 8);
   int grid = items < cap ? items : cap;
   if (d->grid > 0) grid = d->grid < grid ? d->grid : grid;
 
@@ -685,11 +794,13 @@ int launch_moe_a8(const d3_moe_a8_desc* d, hipStream_t stream) {
   uint8_t* ws = (uint8_t*)d->workspace;
   a.sync = (uint32_t*)ws;
   a.hidden = (uint64_t*)(ws + SYNC_WORDS * 4);
-  a.parts = a.hidden + (size_t)d->M * d->topk * d->I;
+  a.tmax = a.hidden + (size_t)d->M * d->topk * d->I;
+  a.parts = a.tmax + (size_t)d->M * d->topk * (d->I / 16);
   a.M = d->M;
   a.E = d->E;
   a.topk = d->topk;
   a.spin_limit = d->spin_limit ? d->spin_limit : (1u << 20);
+  a.dn_start = d->dn_start < 0 ? 0 : d->dn_start > 256 ? 256 : d->dn_start;
   hipLaunchKernelGGL(fn, dim3(grid), dim3(256), L.total, stream, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return hip_fail(e, "d3_moe_a8 launch");

@@ -57,7 +57,11 @@ def status(device, H, I, stream=None):
     return value.value
 
 
-def moe_layer(x, logits, gate_up: A8Bank, down: A8Bank, topk, *, routing=False, spin_limit=0, grid=0, out=None):
+DN_START = 0
+
+
+def moe_layer(x, logits, gate_up: A8Bank, down: A8Bank, topk, *, routing=False, spin_limit=0, grid=0, out=None,
+              dn_start=None):
     """x [M, H] bf16 and router logits [M, E] bf16 (M <= 16) through the routed experts: [M, H] bf16, and with
     `routing` also (ids [M, topk] int64 in descending logit order, weights [M, topk] float32)."""
     if x.dtype != torch.bfloat16 or logits.dtype != torch.bfloat16:
@@ -84,7 +88,7 @@ def moe_layer(x, logits, gate_up: A8Bank, down: A8Bank, topk, *, routing=False, 
         gate_up_scale=gate_up.scale.data_ptr(), down=down.weight.data_ptr(), down_scale=down.scale.data_ptr(),
         out=out.data_ptr(), ids_out=_lib.ptr(ids), weights_out=_lib.ptr(weights), workspace=ws.data_ptr(),
         workspace_bytes=ws.numel(), format=gate_up.fmt, M=M, H=H, I=I, E=E, topk=topk, spin_limit=spin_limit,
-        grid=grid)
+        grid=grid, dn_start=DN_START if dn_start is None else dn_start)
     _lib.check(_lib.lib().d3_moe_a8(ctypes.byref(desc), _lib.stream_of(device)), "d3_moe_a8")
     return (out, ids, weights) if routing else out
 
