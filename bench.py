@@ -27,6 +27,9 @@ import torch  # noqa: E402
 from drama3 import formats, moe  # noqa: E402
 
 METRIC = "MoE-layer expert-weight HBM GB/s (% of peak) at M=1; decode tokens/s"
+# HBM bytes per launch of the fused kernel, from rocprofv3 FETCH_SIZE / WRITE_SIZE passes scaled by the same counters
+# on a plain copy kernel of known size (`--calibrate-copy`); keyed by (format, rows)
+TRAFFIC_PROFILES = {("int8", 1): ROOT / "profiles" / "moe_a8_int8_m1.md"}
 PEAK_GBS = 8000.0
 FORMATS = {"int8": formats.FMT_I8, "w4a8": formats.FMT_W4, "w6a8": formats.FMT_W6, "fp8": formats.FMT_F8}
 H, I, E, TOPK = 2048, 768, 128, 8
@@ -81,6 +84,30 @@ def cpu_baseline(banks, fmt, logits, x, budget_s=12.0):
                       f"torch {threads} threads: _weight_int8pack_mm / dequantize-then-linear per expert"}
 
 
+def measured_traffic(fmt_name, rows):
+    """HBM bytes per launch recorded in the workload's profile summary (line `traffic_bytes_per_launch: N`), or
+    None."""
+    path = TRAFFIC_PROFILES.get((fmt_name, rows))
+    if path is None or not path.exists():
+        return None
+    for line in path.read_text().splitlines():
+        if line.strip().startswith("traffic_bytes_per_launch:"):
+            return int(line.split(":", 1)[1].strip())
+    return None
+
+
+def calibrate_copy(device):
+    """A plain elementwise kernel of known traffic for scaling the PMC byte counters: three launches that each read
+    and write 256 MiB (float32 x * 1.0)."""
+    a = torch.ones(64 << 20, dtype=torch.float32, device=device)
+    b = torch.empty_like(a)
+    for _ in range(3):
+        torch.mul(a, 1.0, out=b)
+    torch.cuda.synchronize()
+    print(json.dumps({"calibration": "elementwise mul", "launches": 3, "read_bytes": a.numel() * 4,
+                      "write_bytes": b.numel() * 4}), flush=True)
+
+
 def main():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
@@ -90,6 +117,7 @@ def main():
     p.add_argument("--rows", type=int, default=1)
     p.add_argument("--layers", type=int, default=48)
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--calibrate-copy", action="store_true", help="only run the copy kernel that scales PMC counters")
     args = p.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: the routed-expert path runs on one MI355X (see DESIGN.md for how it would "
@@ -98,6 +126,9 @@ def main():
     fmt = FORMATS[args.format]
     device = torch.device("cuda:0")
     torch.cuda.set_device(device)
+    if args.calibrate_copy:
+        calibrate_copy(device)
+        return
     M, L = args.rows, args.layers
 
     log(f"building {L} layers of {args.format} experts")
@@ -170,7 +201,8 @@ def main():
                    "bytes_per_launch": int(bytes_per_launch)},
         "roofline": {"bound": "hbm", "achieved": round(bytes_per_launch / (launch_us * 1e-6) / 1e9, 1),
                      "peak": PEAK_GBS, "unit": "GB/s", "frac": round(bytes_per_launch / (launch_us * 1e-6) / 1e9 / PEAK_GBS, 4),
-                     "traffic": None, "kernel": "d3::moe_a8_kernel", "launch_us": round(launch_us, 3)},
+                     "traffic": measured_traffic(args.format, M), "kernel": "d3::moe_a8_kernel",
+                     "launch_us": round(launch_us, 3)},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
