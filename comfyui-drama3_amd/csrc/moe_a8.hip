@@ -553,66 +553,86 @@ __global__ void __launch_bounds__(256, 3) moe_a8_kernel(MoeA8Args a) {
   cx.fparts = (float*)(lds + L.fparts);
   cx.epoch = launch_epoch();
 
-  // ---- per row (one wave each): its logits and activations are loaded together, then routed and quantized
-  for (int t = w; t < M; t += 4) {
-    const uint16_t* lg = a.logits + (size_t)t * E;
-    const uint16_t* xr = a.x + (size_t)t * H;
+  // ---- per row: routed by wave t % 4 and its activations quantized by wave (t + 1) % 4, so that with one row the
+  // two loads and what follows them overlap; each wave issues its loads before using any of them
+  for (int i = 0; 4 * i < M; i++) {
+    const int tr = 4 * i + w, tq = 4 * i + ((w + 3) & 3);
+    const bool do_route = tr < M, do_quant = tq < M;
+    const uint16_t* lg = a.logits + (size_t)(do_route ? tr : 0) * E;
+    const uint16_t* xr = a.x + (size_t)(do_quant ? tq : 0) * H;
     uint32_t lb[4];
 #pragma unroll
-    for (int j = 0; j < 4; j++) lb[j] = lane + 64 * j < E ? lg[lane + 64 * j] : 0u;
+    for (int j = 0; j < 4; j++) lb[j] = do_route && lane + 64 * j < E ? lg[lane + 64 * j] : 0u;
     i32x4 xraw[H / 512];
 #pragma unroll
-    for (int k = 0; k < H / 512; k++) xraw[k] = *(const i32x4*)(xr + 512 * k + 8 * lane);
-    uint32_t key[4];
+    for (int k = 0; k < H / 512; k++) xraw[k] = do_quant ? *(const i32x4*)(xr + 512 * k + 8 * lane) : i32x4{0, 0, 0, 0};
+    if (do_route) {
+      uint32_t key[4];
 #pragma unroll
-    for (int j = 0; j < 4; j++) key[j] = lane + 64 * j < E ? route_key(lb[j], lane + 64 * j) : 0u;
-    float top[MAX_K];
-    int ids[MAX_K];
+      for (int j = 0; j < 4; j++) key[j] = lane + 64 * j < E ? route_key(lb[j], lane + 64 * j) : 0u;
+      float top[MAX_K];
+      int ids[MAX_K];
 #pragma unroll
-    for (int r = 0; r < MAX_K; r++) {
-      top[r] = 0.0f;
-      ids[r] = 0;
-      if (r < K8) {
-        const uint32_t m = wave_max_u32(max(max(key[0], key[1]), max(key[2], key[3])));
+      for (int r = 0; r < MAX_K; r++) {
+        top[r] = 0.0f;
+        ids[r] = 0;
+        if (r < K8) {
+          const uint32_t m = wave_max_u32(max(max(key[0], key[1]), max(key[2], key[3])));
 #pragma unroll
-        for (int j = 0; j < 4; j++) key[j] = key[j] == m ? 0u : key[j];
-        ids[r] = route_key_index(m);
-        top[r] = route_key_value(m);
+          for (int j = 0; j < 4; j++) key[j] = key[j] == m ? 0u : key[j];
+          ids[r] = route_key_index(m);
+          top[r] = route_key_value(m);
+        }
+      }
+      float total = 0.0f;
+#pragma unroll
+      for (int r = 0; r < MAX_K; r++)
+        if (r < K8) total += expf(top[r] - top[0]);
+#pragma unroll
+      for (int r = 0; r < MAX_K; r++) {
+        if (r < K8 && lane == r) {
+          cx.rt_id[tr * MAX_K + r] = ids[r];
+          cx.rt_w[tr * MAX_K + r] = bf16_round(expf(top[r] - top[0]) / total);
+          if (M == 1) {
+            // one row: its experts in routing order are the union, one pair each, all in one down chunk
+            cx.ulist[r] = ids[r];
+            cx.ucount[r] = 1;
+            cx.utok[r * MAX_M] = 0;
+            cx.upair[r * MAX_M] = (uint8_t)r;
+          }
+        }
+      }
+      if (M == 1 && lane == 0) {
+        cx.chunk_first[0] = 0;
+        cx.chunk_first[1] = K8;
+        cx.misc[0] = K8;
+        cx.misc[1] = 1;
       }
     }
-    float total = 0.0f;
+    if (do_quant) {
+      float v[H / 512][8];
+      float amax = 0.0f;
 #pragma unroll
-    for (int r = 0; r < MAX_K; r++)
-      if (r < K8) total += expf(top[r] - top[0]);
+      for (int k = 0; k < H / 512; k++) {
+        const uint32_t wv[4] = {(uint32_t)xraw[k].x, (uint32_t)xraw[k].y, (uint32_t)xraw[k].z, (uint32_t)xraw[k].w};
 #pragma unroll
-    for (int r = 0; r < MAX_K; r++) {
-      if (r < K8 && lane == r) {
-        cx.rt_id[t * MAX_K + r] = ids[r];
-        cx.rt_w[t * MAX_K + r] = bf16_round(expf(top[r] - top[0]) / total);
+        for (int i = 0; i < 4; i++) {
+          v[k][2 * i] = bf16_to_f32(wv[i] & 0xFFFFu);
+          v[k][2 * i + 1] = bf16_to_f32(wv[i] >> 16);
+          amax = fmaxf(amax, fmaxf(fabsf(v[k][2 * i]), fabsf(v[k][2 * i + 1])));
+        }
       }
+      amax = wave_max_f32(amax);
+      const float inv = amax > 0.0f ? QMAX / amax : 0.0f;
+#pragma unroll
+      for (int k = 0; k < H / 512; k++) store_act8<F>(cx.xq + (size_t)tq * H + 512 * k + 8 * lane, v[k], inv);
+      if (lane == 0) cx.sx[tq] = amax / QMAX;
     }
-    float v[H / 512][8];
-    float amax = 0.0f;
-#pragma unroll
-    for (int k = 0; k < H / 512; k++) {
-      const uint32_t wv[4] = {(uint32_t)xraw[k].x, (uint32_t)xraw[k].y, (uint32_t)xraw[k].z, (uint32_t)xraw[k].w};
-#pragma unroll
-      for (int i = 0; i < 4; i++) {
-        v[k][2 * i] = bf16_to_f32(wv[i] & 0xFFFFu);
-        v[k][2 * i + 1] = bf16_to_f32(wv[i] >> 16);
-        amax = fmaxf(amax, fmaxf(fabsf(v[k][2 * i]), fabsf(v[k][2 * i + 1])));
-      }
-    }
-    amax = wave_max_f32(amax);
-    const float inv = amax > 0.0f ? QMAX / amax : 0.0f;
-#pragma unroll
-    for (int k = 0; k < H / 512; k++) store_act8<F>(cx.xq + (size_t)t * H + 512 * k + 8 * lane, v[k], inv);
-    if (lane == 0) cx.sx[t] = amax / QMAX;
   }
   __syncthreads();
 
   // ---- union of the rows' experts, ascending, built by wave 0: lane l owns experts l, l + 64, l + 128, l + 192
-  if (w == 0) {
+  if (M > 1 && w == 0) {
     uint32_t m[4] = {0u, 0u, 0u, 0u};
     for (int t = 0; t < M; t++)
       for (int j = 0; j < K8; j++) {
@@ -671,7 +691,7 @@ __global__ void __launch_bounds__(256, 3) moe_a8_kernel(MoeA8Args a) {
       if (a.weights_out) a.weights_out[i] = cx.rt_w[(i / K8) * MAX_K + i % K8];
     }
   }
-  __syncthreads();
+  if (M > 1) __syncthreads();
   const int U = cx.misc[0];
   cx.U = U;
   cx.nch = cx.misc[1];
