@@ -343,6 +343,7 @@ __global__ void __launch_bounds__(256) grouped_kernel(const float* x, const int*
   __shared__ float lut[16];
   if (KIND == 4 && threadIdx.x < 16) lut[threadIdx.x] = codebook[threadIdx.x];
   __syncthreads();
+  if (rows <= 0) return;  // an empty group reads nothing (groups built on the device list every expert)
   if constexpr (KIND == 0 || KIND == 1) {
     const uint8_t* wsrc = host ? host_w + (size_t)expert * N * K : slot_w + (size_t)slot * N * K;
     uint32_t wd[RPB / 4][CPL / 4];
@@ -461,6 +462,26 @@ __global__ void __launch_bounds__(256) grouped_kernel(const float* x, const int*
   }
 }
 
+// Check of the decode above on its own: one thread per (row, 16-column group) writes the int8-grid values.
+template <int BITS>
+__global__ void __launch_bounds__(256) decode_codes_kernel(const uint8_t* rows, const uint8_t* scales,
+                                                           const float* codebook, int R, int K, int8_t* out) {
+  __shared__ float lut[16];
+  if (BITS == 4 && threadIdx.x < 16) lut[threadIdx.x] = codebook[threadIdx.x];
+  __syncthreads();
+  const int G = K / 16;
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (int64_t)R * G) return;
+  const int r = (int)(idx / G), v = (int)(idx % G);
+  const uint8_t* row = rows + (size_t)r * (K * BITS / 8);
+  const i32x2 lw = *(const i32x2*)(row + 8 * v);
+  const uint32_t high = BITS == 6 ? *(const uint32_t*)(row + K / 2 + 4 * v) : 0u;
+  float q[16];
+  decode_group<BITS>((uint32_t)lw.x, (uint32_t)lw.y, high, scales[(size_t)r * G + v], lut, q);
+#pragma unroll
+  for (int j = 0; j < 16; j++) out[(size_t)r * K + 16 * v + j] = (int8_t)(int)q[j];
+}
+
 }  // namespace d3
 
 // ============================================================================================================ C ABI
@@ -572,7 +593,8 @@ int d3_grouped(int32_t kind, const float* x, const int32_t* groups, int32_t n_gr
   if ((kind == 4 || kind == 6) && (!slot_c || !host_c)) return fail("d3_grouped: codes need channel scales");
   if (kind == 4 && !codebook) return fail("d3_grouped: 4 bits need a codebook");
   if (n_groups < 1) return 0;
-  if (N < 128 || N % 128 || !supported_k(K)) return fail("d3_grouped: N % 128 == 0, K in {256..2048}");
+  if (N < RPB || N % (kind == 1 ? 128 : RPB) || !supported_k(K))
+    return fail("d3_grouped: N % 16 == 0 (N % 128 == 0 for fp8), K in {256..2048}");
   const dim3 grid(N / RPB, n_groups);
   const hipStream_t s = (hipStream_t)stream;
   const uint8_t* hw = (const uint8_t*)host_w;
@@ -585,6 +607,22 @@ int d3_grouped(int32_t kind, const float* x, const int32_t* groups, int32_t n_gr
     default: return fail("d3_grouped: kind 0, 1, 4 or 6");
   }
   return done("d3_grouped");
+}
+
+int d3_decode_codes(int32_t bits, const void* rows, const void* scales, const float* codebook, int32_t R, int32_t K,
+                    void* out, void* stream) {
+  if (!rows || !scales || !out) return fail("d3_decode_codes: null pointer");
+  if (bits == 4 && !codebook) return fail("d3_decode_codes: 4 bits need a codebook");
+  if ((bits != 4 && bits != 6) || R < 1 || K < 32 || K % 32) return fail("d3_decode_codes: bits 4 or 6, K % 32 == 0");
+  const int64_t threads = (int64_t)R * (K / 16);
+  const dim3 grid((unsigned)((threads + 255) / 256));
+  if (bits == 4)
+    hipLaunchKernelGGL(decode_codes_kernel<4>, grid, dim3(256), 0, (hipStream_t)stream, (const uint8_t*)rows,
+                       (const uint8_t*)scales, codebook, R, K, (int8_t*)out);
+  else
+    hipLaunchKernelGGL(decode_codes_kernel<6>, grid, dim3(256), 0, (hipStream_t)stream, (const uint8_t*)rows,
+                       (const uint8_t*)scales, codebook, R, K, (int8_t*)out);
+  return done("d3_decode_codes");
 }
 
 }  // extern "C"

@@ -40,6 +40,18 @@ SIGNATURES = {
     "d3_moe_a8_status": (c_int32, [c_void_p, ctypes.POINTER(c_uint32)]),
     "d3_gemv_a8_groups": (c_int32, [c_int32, c_void_p, c_int32, c_int32, c_void_p, c_int32, c_void_p, c_void_p]),
     "d3_unpack_rows": (c_int32, [c_int32, c_void_p, c_int32, c_int32, c_void_p, c_void_p]),
+    "d3_route": (c_int32, [c_void_p, c_int32, c_int32, c_int32, c_void_p, c_void_p, c_void_p]),
+    "d3_weighted_sum": (c_int32, [c_void_p, c_void_p, c_int32, c_int32, c_void_p, c_void_p]),
+    "d3_rotate": (c_int32, [c_void_p, c_int32, c_int32, c_int32, c_void_p, c_void_p, c_void_p]),
+    "d3_gemv_int8": (c_int32, [c_void_p, c_int32, c_void_p, c_void_p, c_void_p, c_int32, c_void_p, c_void_p, c_void_p,
+                               c_void_p, c_void_p, c_int32, c_int32, c_int32, c_void_p]),
+    "d3_gemv_fp8": (c_int32, [c_void_p, c_int32, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+                              c_int32, c_int32, c_int32, c_void_p]),
+    "d3_gemv_codes": (c_int32, [c_void_p, c_int32, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+                                c_void_p, c_void_p, c_int32, c_void_p, c_int32, c_int32, c_int32, c_void_p]),
+    "d3_grouped": (c_int32, [c_int32, c_void_p, c_void_p, c_int32, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+                             c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_void_p]),
+    "d3_decode_codes": (c_int32, [c_int32, c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_void_p, c_void_p]),
 }
 
 _lock = threading.Lock()

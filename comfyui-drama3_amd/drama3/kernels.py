@@ -142,3 +142,14 @@ def grouped_fp8(x, groups, slot_fields, host_fields, n):
 def grouped_codes(x, groups, slot_fields, host_fields, codebook, bits, n):
     """grouped_int8 for W4A8/W6A8 banks (see gemv_codes)."""
     return _grouped(int(bits), x, groups, slot_fields, host_fields, codebook, n, "_qdata")
+
+
+def decode_codes(qdata, scale, codebook, bits):
+    """int8 [R, K]: W4A8 / W6A8 rows decoded to the int8 grid exactly as gemv_codes / grouped_codes decode them
+    (a check of kernels.py:466-483's decode_codes; no counterpart in the reference's call surface)."""
+    R = qdata.shape[0]
+    K = qdata.shape[1] * 8 // bits
+    out = torch.empty((R, K), dtype=torch.int8, device=qdata.device)
+    _call("d3_decode_codes", int(bits), _p(qdata.contiguous()), _p(scale.contiguous()), _p(codebook), R, K, _p(out),
+          _stream(qdata))
+    return out

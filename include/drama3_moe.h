@@ -75,6 +75,59 @@ int d3_gemv_a8_groups(int32_t format, const void* rows, int32_t R, int32_t K, co
                       void* stream);
 int d3_unpack_rows(int32_t format, const void* rows, int32_t R, int32_t K, void* codes, void* stream);
 
+/* ---- The reference's own formats, one kernel per reference kernel (drama3/kernels.py SOURCE) -------------------
+ * Float32 activations as in the reference. Slot-cache plans as there: plan [k, 2] int32 = (slot, code) per expert;
+ * code 0 reads the slot fields, 1 reads the host (bank) fields and copies the expert into its slot when slot >= 0,
+ * 2 (gemv_int8 only) is the CPU's: zeros, or with `late` the only experts run, from the host fields, when took_over[0].
+ * "Host" fields may be device memory (an HBM-resident table: slot e = expert e and plan (e, 0)) or pinned host memory.
+ * K is one of 256, 512, 768, 1024, 1536, 2048; N % 16 == 0 (N % 128 == 0 for FP8). */
+
+/* route_experts (kernels.py:39-67, wrapper route kernels.py:647-653): per row of bf16 logits [rows, n] (n <= 1024),
+ * ids [rows, k] int64 of the k (<= 32) largest in descending order (ties to the lower index) and weights [rows, k]
+ * float32 = bf16(exp(l - l_max) / sum over the k). One wave per row. */
+int d3_route(const void* logits, int32_t rows, int32_t n, int32_t k, int64_t* ids, float* weights, void* stream);
+
+/* weighted_sum (kernels.py:69-76, wrapper kernels.py:656-661): out [H] bf16 = sum_e parts[e, h] * weights[e]. */
+int d3_weighted_sum(const float* parts, const float* weights, int32_t k, int32_t H, void* out, void* stream);
+
+/* rotate_rows (kernels.py:222-258, wrapper rotate kernels.py:636-644): mode 0 float rows [rows, K], 1 bf16 rows,
+ * 2 SwiGLU of float [rows, 2K] gate | up; out [rows, K] float32 = rows times H256 on each 256 columns (K % 256 == 0).
+ * Writes nothing unless only_if[0] (device int32) is non-zero. */
+int d3_rotate(const void* x, int32_t mode, int32_t rows, int32_t K, float* out, const int32_t* only_if, void* stream);
+
+/* gemv_int8 (kernels.py:260-314, wrapper kernels.py:664-671): out [k, N] float32 = (int8 row of the expert . x[e or 0])
+ * * row scale, x [x_rows (1 or k), K] float32 (ConvRot basis); fields _qdata int8 [E * N, K], scale float32 [E * N]. */
+int d3_gemv_int8(const float* x, int32_t x_rows, const int64_t* ids, const int32_t* plan, const int32_t* took_over,
+                 int32_t late, void* slot_w, float* slot_s, const void* host_w, const float* host_s, float* out,
+                 int32_t k, int32_t N, int32_t K, void* stream);
+
+/* gemv_fp8 (kernels.py:316-363, wrapper kernels.py:674-681): out [k, N] = sum over columns of e4m3(W) * x * the
+ * 128 x 128 block scale; fields weight uint8 [E * N, K], scale float32 [E * N / 128, K / 128]. The hardware e4m3fn
+ * decode reads the NaN codes 0x7F / 0xFF as NaN (the reference's bit trick reads +-480). */
+int d3_gemv_fp8(const float* x, int32_t x_rows, const int64_t* ids, const int32_t* plan, void* slot_w, float* slot_s,
+                const void* host_w, const float* host_s, float* out, int32_t k, int32_t N, int32_t K, void* stream);
+
+/* gemv_codes (kernels.py:466-536, wrapper kernels.py:703-713): W4A8 / W6A8 rows decoded to the int8 grid
+ * (clamp(rint(value * e4m3 group scale), +-127), value = codebook[code] at 4 bits or code - 32 at 6 bits) . x, times
+ * s_channel; fields _qdata uint8 [E * N, K * bits / 8] (nibble plane, then the 2-bit high planes at 6 bits), scale
+ * e4m3 [E * N, K / 16], s_channel float32 [E * N]; codebook float32 [16] (4 bits) or NULL. */
+int d3_gemv_codes(const float* x, int32_t x_rows, const int64_t* ids, const int32_t* plan, void* slot_w, void* slot_r,
+                  float* slot_c, const void* host_w, const void* host_r, const float* host_c, const float* codebook,
+                  int32_t bits, float* out, int32_t k, int32_t N, int32_t K, void* stream);
+
+/* grouped_int8 / grouped_fp8 / grouped_codes (kernels.py:365-464,538-587, wrappers kernels.py:684-700,716-724):
+ * kind 0 int8, 1 fp8, 4 / 6 codes. x [T, K] float32 rows sorted by expert; groups [n_groups, 5] int32 = (expert, slot,
+ * fill, first row, rows); a group reads its slot, or the host fields when slot < 0 or fill (then copying the expert
+ * into the slot). out [T, N] float32 rows of the groups (others untouched); a group with 0 rows reads nothing. */
+int d3_grouped(int32_t kind, const float* x, const int32_t* groups, int32_t n_groups, void* slot_w, void* slot_s,
+               void* slot_c, const void* host_w, const void* host_s, const void* host_c, const float* codebook,
+               float* out, int32_t N, int32_t K, void* stream);
+
+/* Check of the W4A8 / W6A8 decode on its own (kernels.py:466-483 decode_codes; no entry point of its own there):
+ * codes [R, K] int8 of rows [R, K * bits / 8] with scales [R, K / 16]; K % 32 == 0. */
+int d3_decode_codes(int32_t bits, const void* rows, const void* scales, const float* codebook, int32_t R, int32_t K,
+                    void* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

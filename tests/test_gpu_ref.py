@@ -1,0 +1,409 @@
+"""Parity of the reference-format kernels (kernels.py surface -> libdrama3_moe.so) and the layer entry points of
+offload.py with the oracle (oracle/reference.py) on the same seeded inputs.
+
+Bars: routing ids exact and weights within one bf16 step; decoded int8-grid codes bit-exact; float32 GEMV / grouped
+outputs within 3e-5 of each output's sum of |w x| (float32 sums in another order than the oracle's float64);
+bf16 layer outputs within one bf16 step plus 1e-5 of the row's largest value. FP8 codes 0x7F / 0xFF are left out of
+the inputs: the hardware e4m3fn decode reads them as NaN where the reference reads +-480."""
+import numpy as np
+import pytest
+import torch
+
+from drama3 import _lib, kernels, offload
+from oracle import numerics
+from oracle import reference as ref
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda:0")
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+
+
+def pinned(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).pin_memory()
+
+
+def fields_on(fields, where=dev):
+    return {n: where(v) for n, v in fields.items()}
+
+
+def assert_dot_close(got, expect, abs_sum, tol=3e-5):
+    got = got.detach().cpu().numpy().astype(np.float64)
+    bound = tol * abs_sum + 1e-30
+    err = np.abs(got - expect)
+    assert np.all(err <= bound), (err / bound).max()
+
+
+def assert_bf16_close(got_bits, expect_bits):
+    a = numerics.bf16_bits_to_f32(np.asarray(got_bits)).astype(np.float64)
+    b = numerics.bf16_bits_to_f32(np.asarray(expect_bits)).astype(np.float64)
+    assert np.all(np.isfinite(a))
+    bound = 2.0 ** -7 * np.abs(b) + 1e-5 * np.abs(b).max()
+    assert np.all(np.abs(a - b) <= bound), np.abs(a - b).max()
+
+
+def bits_of(t):
+    return t.detach().cpu().view(torch.int16).numpy().view(np.uint16)
+
+
+def no_nan_fp8(rng, shape):
+    w = rng.integers(0, 256, size=shape).astype(np.uint8)
+    w[(w & 0x7F) == 0x7F] = 0x7E
+    return w
+
+
+# ---------------------------------------------------------------------------------------------------------- route
+@pytest.mark.parametrize("n,k,rows", [(128, 8, 1), (256, 8, 1), (1024, 32, 3), (64, 1, 5)])
+def test_route(n, k, rows):
+    rng = np.random.default_rng(n + k)
+    v = (rng.integers(-6, 6, size=(rows, n)) * 0.37).astype(np.float32)  # ties on purpose
+    bits = numerics.f32_to_bf16_bits(v)
+    ids, w = kernels.route(dev(bits).view(torch.bfloat16), k)
+    rid, rw = ref.route_ref(bits, k)
+    assert np.array_equal(ids.cpu().numpy(), rid)
+    got = w.cpu().numpy()
+    assert np.all(np.abs(got - rw) <= 2.0 ** -8 * rw + 1e-7)
+
+
+def test_weighted_sum():
+    rng = np.random.default_rng(1)
+    parts = rng.standard_normal((8, 2048)).astype(np.float32)
+    w = rng.uniform(0, 1, 8).astype(np.float32)
+    out = kernels.weighted_sum(dev(parts), dev(w))
+    assert out.shape == (1, 2048) and out.dtype == torch.bfloat16
+    assert_bf16_close(bits_of(out), ref.weighted_sum_ref(parts, w))
+
+
+# --------------------------------------------------------------------------------------------------------- rotate
+@pytest.mark.parametrize("mode,rows,K", [("f32", 3, 2048), ("bf16", 1, 2048), ("bf16", 2, 768), ("swiglu", 8, 768),
+                                         ("swiglu", 8, 512)])
+def test_rotate(mode, rows, K):
+    rng = np.random.default_rng(K + rows)
+    always = torch.ones(1, dtype=torch.int32, device=DEV)
+    if mode == "swiglu":
+        x = rng.standard_normal((rows, 2 * K)).astype(np.float32)
+        got = kernels.rotate(dev(x), always, swiglu=True)
+        expect = ref.rotate_ref(x, swiglu=True)
+    elif mode == "bf16":
+        bits = numerics.f32_to_bf16_bits(rng.standard_normal((rows, K)).astype(np.float32))
+        got = kernels.rotate(dev(bits).view(torch.bfloat16), always)
+        expect = ref.rotate_ref(numerics.bf16_bits_to_f32(bits))
+    else:
+        x = rng.standard_normal((rows, K)).astype(np.float32)
+        got = kernels.rotate(dev(x), always)
+        expect = ref.rotate_ref(x)
+    err = np.abs(got.cpu().numpy() - expect).max() / np.abs(expect).max()
+    assert err < 2e-6, err
+
+
+def test_rotate_only_if_zero_writes_nothing():
+    x = torch.randn(2, 512, device=DEV)
+    out = torch.full((2, 512), 7.0, device=DEV)
+    never = torch.zeros(1, dtype=torch.int32, device=DEV)
+    _lib.check(_lib.lib().d3_rotate(x.data_ptr(), 0, 2, 512, out.data_ptr(), never.data_ptr(),
+                                    _lib.stream_of(DEV)), "d3_rotate")
+    assert torch.all(out == 7.0)
+
+
+# ----------------------------------------------------------------------------------------------------- decode
+@pytest.mark.parametrize("bits", [4, 6])
+def test_decode_codes_bit_exact_exhaustive(bits):
+    """Every (code, scale byte) pair, and random rows, decode to the oracle's int8 grid bit for bit."""
+    codebook = ref.default_codebook()
+    ncodes = 1 << bits
+    K = 16 * 256
+    codes = np.tile(np.arange(ncodes), K // ncodes + 1)[:K]
+    code = np.stack([np.roll(codes, 16 * s) for s in range(max(1, ncodes // 16))]).astype(np.uint32)
+    scale = np.tile(np.arange(256, dtype=np.uint8), (code.shape[0], 1))
+    q = ref.pack_codes(code, bits)
+    got = kernels.decode_codes(dev(q), dev(scale), dev(codebook), bits).cpu().numpy()
+    expect = ref.decode_codes_ref(q, scale, bits, codebook)
+    finite = np.repeat((scale & 0x7F) != 0x7F, 16, axis=1)
+    assert np.array_equal(got[finite], expect[finite])
+    rng = np.random.default_rng(bits)
+    qr = rng.integers(0, 256, size=(64, 2048 * bits // 8)).astype(np.uint8)
+    sr = no_nan_fp8(rng, (64, 2048 // 16))
+    got = kernels.decode_codes(dev(qr), dev(sr), dev(codebook), bits).cpu().numpy()
+    assert np.array_equal(got, ref.decode_codes_ref(qr, sr, bits, codebook))
+
+
+# ------------------------------------------------------------------------------------------------------ GEMVs
+def int8_bank(rng, E, N, K):
+    return {"_qdata": rng.integers(-127, 128, size=(E * N, K), dtype=np.int8),
+            "scale": rng.uniform(1e-3, 1e-2, size=E * N).astype(np.float32)}
+
+
+def abs_sum_int8(bank, ids, x, N):
+    out = []
+    for j, e in enumerate(ids):
+        w = np.abs(bank["_qdata"][e * N:(e + 1) * N].astype(np.float64)) * bank["scale"][e * N:(e + 1) * N, None]
+        out.append(w @ np.abs(x[0 if x.shape[0] == 1 else j]))
+    return np.stack(out)
+
+
+@pytest.mark.parametrize("N,K,x_rows", [(1536, 2048, 1), (2048, 768, 8), (1024, 2048, 1), (2048, 512, 8)])
+def test_gemv_int8_resident(N, K, x_rows):
+    rng = np.random.default_rng(N + K)
+    E = 8
+    bank = int8_bank(rng, E, N, K)
+    ids = np.array([5, 1, 7, 0, 2, 6, 3, 4])
+    plan = np.stack([ids, np.zeros_like(ids)], 1).astype(np.int32)
+    x = rng.standard_normal((x_rows, K)).astype(np.float32)
+    took = torch.zeros(1, dtype=torch.int32, device=DEV)
+    f = fields_on(bank)
+    got = kernels.gemv_int8(dev(x), dev(ids), dev(plan), took, False, f, f, N)
+    expect = ref.gemv_int8_ref(x, ids, plan, False, False, bank, bank, N)
+    assert_dot_close(got, expect, abs_sum_int8(bank, ids, x, N))
+
+
+@pytest.mark.parametrize("host_where", ["device", "pinned"])
+def test_gemv_int8_slot_plan(host_where):
+    """Cached, filling, slot-less and CPU experts in one launch; then the late launch for the CPU's expert."""
+    rng = np.random.default_rng(3)
+    E, N, K, slots = 6, 256, 512, 4
+    host = int8_bank(rng, E, N, K)
+    slot = {"_qdata": np.zeros((slots * N, K), np.int8), "scale": np.zeros(slots * N, np.float32)}
+    slot["_qdata"][N:2 * N] = host["_qdata"][4 * N:5 * N]
+    slot["scale"][N:2 * N] = host["scale"][4 * N:5 * N]
+    ids = np.array([4, 2, 5, 0])
+    plan = np.array([[1, 0], [2, 1], [-1, 1], [0, 2]], np.int32)
+    x = rng.standard_normal((1, K)).astype(np.float32)
+    hf = fields_on(host, dev if host_where == "device" else pinned)
+    sf = fields_on(slot)
+    for late, took in ((False, 0), (True, 0), (True, 1)):
+        slot_np = {n: v.copy() for n, v in slot.items()}
+        sf = fields_on(slot_np)
+        took_t = torch.full((1,), took, dtype=torch.int32, device=DEV)
+        got = kernels.gemv_int8(dev(x), dev(ids), dev(plan), took_t, late, sf, hf, N)
+        expect = ref.gemv_int8_ref(x, ids, plan, bool(took), late, slot_np, host, N)
+        assert_dot_close(got, expect, abs_sum_int8(host, ids, x, N) + 1e-12)
+        for n in slot_np:
+            assert np.array_equal(sf[n].cpu().numpy(), slot_np[n]), n
+
+
+def fp8_bank(rng, E, N, K):
+    return {"weight": no_nan_fp8(rng, (E * N, K)),
+            "scale": rng.uniform(1e-4, 1e-3, size=(E * N // 128, K // 128)).astype(np.float32)}
+
+
+def abs_sum_fp8(bank, ids, x, N):
+    vals = np.abs(ref.fp8_rows(bank["weight"], bank["scale"]))
+    return np.stack([vals[e * N:(e + 1) * N] @ np.abs(x[0 if x.shape[0] == 1 else j]) for j, e in enumerate(ids)])
+
+
+@pytest.mark.parametrize("N,K,x_rows", [(1536, 2048, 1), (2048, 768, 8)])
+def test_gemv_fp8(N, K, x_rows):
+    rng = np.random.default_rng(N)
+    E = 8
+    bank = fp8_bank(rng, E, N, K)
+    ids = np.array([3, 0, 6, 1, 7, 2, 5, 4])
+    plan = np.stack([ids, np.zeros_like(ids)], 1).astype(np.int32)
+    x = rng.standard_normal((x_rows, K)).astype(np.float32)
+    f = fields_on(bank)
+    got = kernels.gemv_fp8(dev(x), dev(ids), dev(plan), f, f, N)
+    expect = ref.gemv_fp8_ref(x, ids, plan, bank, bank, N)
+    assert_dot_close(got, expect, abs_sum_fp8(bank, ids, x, N))
+
+
+def test_gemv_fp8_fill():
+    rng = np.random.default_rng(9)
+    E, N, K, slots = 4, 256, 512, 3
+    host = fp8_bank(rng, E, N, K)
+    slot = {"weight": np.zeros((slots * N, K), np.uint8), "scale": np.zeros((slots * N // 128, K // 128), np.float32)}
+    ids = np.array([3, 1])
+    plan = np.array([[2, 1], [-1, 1]], np.int32)
+    x = rng.standard_normal((1, K)).astype(np.float32)
+    sf, hf = fields_on(slot), fields_on(host, pinned)
+    got = kernels.gemv_fp8(dev(x), dev(ids), dev(plan), sf, hf, N)
+    expect = ref.gemv_fp8_ref(x, ids, plan, slot, host, N)
+    assert_dot_close(got, expect, abs_sum_fp8(host, ids, x, N))
+    for n in slot:
+        assert np.array_equal(sf[n].cpu().numpy(), slot[n]), n
+
+
+def codes_bank(rng, E, N, K, bits):
+    return {"_qdata": rng.integers(0, 256, size=(E * N, K * bits // 8)).astype(np.uint8),
+            "scale": rng.integers(0x20, 0x40, size=(E * N, K // 16)).astype(np.uint8),
+            "s_channel": rng.uniform(1e-4, 1e-3, size=E * N).astype(np.float32)}
+
+
+def abs_sum_codes(bank, ids, x, N, bits, codebook):
+    q = np.abs(ref.decode_codes_ref(bank["_qdata"], bank["scale"], bits, codebook).astype(np.float64))
+    q *= bank["s_channel"][:, None]
+    return np.stack([q[e * N:(e + 1) * N] @ np.abs(x[0 if x.shape[0] == 1 else j]) for j, e in enumerate(ids)])
+
+
+@pytest.mark.parametrize("bits", [4, 6])
+@pytest.mark.parametrize("N,K,x_rows", [(1536, 2048, 1), (2048, 768, 8)])
+def test_gemv_codes(bits, N, K, x_rows):
+    rng = np.random.default_rng(bits * N)
+    E = 8
+    bank = codes_bank(rng, E, N, K, bits)
+    cb = ref.default_codebook()
+    ids = np.array([2, 7, 0, 5, 1, 3, 6, 4])
+    plan = np.stack([ids, np.zeros_like(ids)], 1).astype(np.int32)
+    x = rng.standard_normal((x_rows, K)).astype(np.float32)
+    f = fields_on(bank)
+    got = kernels.gemv_codes(dev(x), dev(ids), dev(plan), f, f, dev(cb) if bits == 4 else None, bits, N)
+    expect = ref.gemv_codes_ref(x, ids, plan, bank, bank, cb, bits, N)
+    assert_dot_close(got, expect, abs_sum_codes(bank, ids, x, N, bits, cb))
+
+
+@pytest.mark.parametrize("bits", [4, 6])
+def test_gemv_codes_fill(bits):
+    rng = np.random.default_rng(20 + bits)
+    E, N, K, slots = 4, 128, 512, 2
+    host = codes_bank(rng, E, N, K, bits)
+    slot = {n: np.zeros((slots * N, *v.shape[1:]), v.dtype) for n, v in host.items()}
+    cb = ref.default_codebook()
+    ids = np.array([3, 2])
+    plan = np.array([[1, 1], [-1, 1]], np.int32)
+    x = rng.standard_normal((1, K)).astype(np.float32)
+    sf, hf = fields_on(slot), fields_on(host, pinned)
+    got = kernels.gemv_codes(dev(x), dev(ids), dev(plan), sf, hf, dev(cb) if bits == 4 else None, bits, N)
+    expect = ref.gemv_codes_ref(x, ids, plan, slot, host, cb, bits, N)
+    assert_dot_close(got, expect, abs_sum_codes(host, ids, x, N, bits, cb))
+    for n in slot:
+        assert np.array_equal(sf[n].cpu().numpy(), slot[n]), n
+
+
+# --------------------------------------------------------------------------------------------------- grouped
+@pytest.mark.parametrize("kind", ["int8", "fp8", "w4", "w6"])
+def test_grouped(kind):
+    rng = np.random.default_rng(len(kind) + 40)
+    E, N, K, slots = 6, 256, 768, 3
+    if kind == "int8":
+        host = int8_bank(rng, E, N, K)
+    elif kind == "fp8":
+        host = fp8_bank(rng, E, N, K)
+    else:
+        host = codes_bank(rng, E, N, K, int(kind[1]))
+    slot = {n: np.zeros(((slots * v.shape[0]) // E, *v.shape[1:]), v.dtype) for n, v in host.items()}
+    for n, v in host.items():  # expert 2 cached in slot 0
+        r = v.shape[0] // E
+        slot[n][0:r] = v[2 * r:3 * r]
+    cb = ref.default_codebook()
+    # (expert, slot, fill, first, rows): cached, filling slot 2, slot-less, empty, cached again with fill 0
+    groups = np.array([[2, 0, 0, 0, 5], [4, 2, 1, 5, 7], [1, -1, 0, 12, 3], [5, 1, 0, 15, 0], [0, -1, 0, 15, 9]],
+                      np.int32)
+    T = 24
+    x = rng.standard_normal((T, K)).astype(np.float32)
+    sf, hf = fields_on(slot), fields_on(host)
+    out = kernels._grouped({"int8": 0, "fp8": 1, "w4": 4, "w6": 6}[kind], dev(x), dev(groups), sf, hf,
+                           dev(cb) if kind == "w4" else None, N, "weight" if kind == "fp8" else "_qdata")
+    expect = ref.grouped_ref(kind, x, groups, slot, host, cb, N)
+    if kind == "int8":
+        absw = np.abs(host["_qdata"].astype(np.float64)) * host["scale"][:, None]
+    elif kind == "fp8":
+        absw = np.abs(ref.fp8_rows(host["weight"], host["scale"]))
+    else:
+        absw = np.abs(ref.decode_codes_ref(host["_qdata"], host["scale"], int(kind[1]), cb).astype(np.float64))
+        absw *= host["s_channel"][:, None]
+    got = out.cpu().numpy().astype(np.float64)
+    for e, _, _, first, rows in groups:
+        for t in range(first, first + rows):
+            bound = 3e-5 * (absw[e * N:(e + 1) * N] @ np.abs(x[t])) + 1e-30
+            assert np.all(np.abs(got[t] - expect[t]) <= bound), (kind, e, t)
+    for n in slot:
+        assert np.array_equal(sf[n].cpu().numpy(), slot[n]), n
+
+
+# ---------------------------------------------------------------------------------------------- the layer
+H, I, E = 2048, 768, 8
+
+
+def layer_banks(kind, seed):
+    rng = np.random.default_rng(seed)
+    gu = rng.standard_normal((E, 2 * I, H)).astype(np.float32) * 0.02
+    dn = rng.standard_normal((E, H, I)).astype(np.float32) * 0.02
+    if kind == "int8":
+        return (ref.quantize_int8_convrot(gu), ref.quantize_int8_convrot(dn)), (None, None)
+    if kind == "fp8":
+        return (ref.quantize_fp8_block(gu), ref.quantize_fp8_block(dn)), (None, None)
+    (a, ca), (b, cb) = ref.quantize_codes(gu, int(kind[1])), ref.quantize_codes(dn, int(kind[1]))
+    return (a, b), (ca, cb)
+
+
+@pytest.fixture(scope="module", params=["int8", "fp8", "w4", "w6"])
+def layer(request):
+    banks, cbs = layer_banks(request.param, 70 + len(request.param))
+    dbanks = [fields_on(b) for b in banks]
+    dcbs = tuple(None if c is None else dev(c) for c in cbs)
+    return request.param, banks, cbs, dbanks, dcbs
+
+
+def test_resident_decode(layer):
+    kind, banks, cbs, dbanks, dcbs = layer
+    rng = np.random.default_rng(5)
+    x = numerics.f32_to_bf16_bits(rng.standard_normal((1, H)).astype(np.float32))
+    ids = np.array([6, 2, 0, 7])
+    w = numerics.bf16_round(np.array([0.4, 0.3, 0.2, 0.1], np.float32))
+    got = offload.resident_decode(dev(x).view(torch.bfloat16), dev(ids), dev(w), dbanks, (2 * I, H), kind, dcbs)
+    assert got.shape == (1, H) and got.dtype == torch.bfloat16
+    assert_bf16_close(bits_of(got), ref.resident_decode_ref(x, ids, w, banks, (2 * I, H), kind, cbs))
+
+
+def test_resident_prefill(layer):
+    kind, banks, cbs, dbanks, dcbs = layer
+    rng = np.random.default_rng(6)
+    T, k = 12, 4
+    x = numerics.f32_to_bf16_bits(rng.standard_normal((T, H)).astype(np.float32))
+    idx = np.stack([rng.choice(E, k, replace=False) for _ in range(T)])
+    w = numerics.bf16_round(rng.dirichlet(np.ones(k), T).astype(np.float32))
+    got = offload.resident_prefill(dev(x).view(torch.bfloat16), dev(idx), dev(w).to(torch.bfloat16), dbanks,
+                                   (2 * I, H), kind, dcbs, E)
+    assert got.shape == (T, H) and got.dtype == torch.bfloat16
+    assert_bf16_close(bits_of(got), ref.resident_prefill_ref(x, idx, w, banks, (2 * I, H), kind, cbs))
+
+
+def test_expert_groups_without_host_sync():
+    idx = torch.tensor([[3, 1], [1, 0], [3, 3]], device=DEV)
+    order, groups = offload.expert_groups(idx, 5)
+    g = groups.cpu().numpy()
+    assert g[:, 4].tolist() == [1, 2, 0, 3, 0] and g[:, 3].tolist() == [0, 1, 3, 3, 6]
+    assert idx.reshape(-1)[order].cpu().tolist() == [0, 1, 1, 3, 3, 3]
+
+
+def test_fp8_experts_module():
+    banks, _ = layer_banks("fp8", 90)
+    mod = offload.FP8Experts(E, H, I, device=DEV, dtype=torch.bfloat16)
+    with torch.no_grad():
+        for name, b in zip(("gate_up", "down"), banks):
+            rows = b["weight"].shape[0] // E
+            getattr(mod, f"{name}_weight").copy_(dev(b["weight"]).view(E, rows, -1).view(torch.float8_e4m3fn))
+            getattr(mod, f"{name}_scale").copy_(dev(b["scale"]).view(E, rows // 128, -1))
+    rng = np.random.default_rng(8)
+    x = numerics.f32_to_bf16_bits(rng.standard_normal((1, H)).astype(np.float32))
+    idx = np.array([[1, 4, 6]])
+    w = numerics.bf16_round(np.array([[0.5, 0.3, 0.2]], np.float32))
+    got = mod(dev(x).view(torch.bfloat16), dev(idx), dev(w).to(torch.bfloat16))
+    assert_bf16_close(bits_of(got), ref.resident_decode_ref(x, idx[0], w[0], banks, (2 * I, H), "fp8", (None, None)))
+
+
+def test_resident_decode_graph_replays(layer):
+    """A decode layer captured in a HIP graph gives the eager result on every replay, with new inputs in place."""
+    kind, banks, cbs, dbanks, dcbs = layer
+    rng = np.random.default_rng(11)
+    xs = [numerics.f32_to_bf16_bits(rng.standard_normal((1, H)).astype(np.float32)) for _ in range(3)]
+    ids_all = [rng.choice(E, 4, replace=False) for _ in range(3)]
+    w = dev(numerics.bf16_round(np.full(4, 0.25, np.float32)))
+    x_buf = dev(xs[0]).view(torch.bfloat16).clone()
+    ids_buf = dev(ids_all[0]).clone()
+    offload.resident_decode(x_buf, ids_buf, w, dbanks, (2 * I, H), kind, dcbs)  # constants exist before capture
+    stream = torch.cuda.Stream(DEV)
+    stream.wait_stream(torch.cuda.current_stream(DEV))
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        with torch.cuda.graph(g, stream=stream):
+            out = offload.resident_decode(x_buf, ids_buf, w, dbanks, (2 * I, H), kind, dcbs)
+    torch.cuda.current_stream(DEV).wait_stream(stream)
+    for x, ids in zip(xs, ids_all):
+        x_buf.copy_(dev(x).view(torch.bfloat16))
+        ids_buf.copy_(dev(ids))
+        g.replay()
+        torch.cuda.synchronize()
+        eager = offload.resident_decode(x_buf, ids_buf, w, dbanks, (2 * I, H), kind, dcbs)
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)
