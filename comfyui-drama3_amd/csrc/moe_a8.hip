@@ -101,32 +101,6 @@ struct Lds {
 // has published; the down items wait for (epoch, T). Nothing needs clearing between launches.
 D3_INLINE uint64_t* done_counter(uint32_t* sync, int u) { return (uint64_t*)(sync + SYNC_DONE + 64 * u); }
 
-template <int F> __host__ __device__ constexpr float act_qmax() { return F == FMT_F8 ? 448.0f : 127.0f; }
-
-// quantize 8 activations with `inv`, store them in the format's storage order
-template <int F> D3_INLINE void store_act8(uint8_t* dst, const float* v, float inv) {
-  uint32_t b[8];
-#pragma unroll
-  for (int i = 0; i < 8; i++) {
-    if constexpr (F == FMT_F8) {
-      b[i] = f32_to_fp8(v[i] * inv);
-    } else {
-      float r = rintf(v[i] * inv);
-      r = fminf(fmaxf(r, -127.0f), 127.0f);
-      b[i] = (uint32_t)((int)r) & 0xFFu;
-    }
-  }
-  uint32_t lo, hi;
-  if constexpr (F == FMT_W4) {
-    lo = b[0] | (b[2] << 8) | (b[4] << 16) | (b[6] << 24);
-    hi = b[1] | (b[3] << 8) | (b[5] << 16) | (b[7] << 24);
-  } else {
-    lo = b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24);
-    hi = b[4] | (b[5] << 8) | (b[6] << 16) | (b[7] << 24);
-  }
-  *(i32x2*)dst = i32x2{(int)lo, (int)hi};
-}
-
 // What a workgroup knows after its prologue.
 struct Ctx {
   const MoeA8Args* a;

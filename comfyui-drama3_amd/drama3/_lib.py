@@ -31,6 +31,16 @@ class MoeA8Desc(ctypes.Structure):
     ]
 
 
+class MoeA8PrefillDesc(ctypes.Structure):
+    """d3_moe_a8_prefill_desc (include/drama3_moe.h)."""
+    _fields_ = [
+        ("x", c_void_p), ("logits", c_void_p), ("ids_in", c_void_p), ("weights_in", c_void_p), ("gate_up", c_void_p),
+        ("gate_up_scale", c_void_p), ("down", c_void_p), ("down_scale", c_void_p), ("out", c_void_p),
+        ("ids_out", c_void_p), ("weights_out", c_void_p), ("workspace", c_void_p), ("workspace_bytes", c_int64),
+        ("format", c_int32), ("T", c_int32), ("H", c_int32), ("I", c_int32), ("E", c_int32), ("topk", c_int32),
+    ]
+
+
 # name -> (restype, argtypes)
 SIGNATURES = {
     "d3_last_error": (ctypes.c_char_p, []),
@@ -38,6 +48,8 @@ SIGNATURES = {
     "d3_moe_a8_workspace_bytes": (c_int64, [c_int32, c_int32, c_int32, c_int32]),
     "d3_moe_a8": (c_int32, [ctypes.POINTER(MoeA8Desc), c_void_p]),
     "d3_moe_a8_status": (c_int32, [c_void_p, ctypes.POINTER(c_uint32)]),
+    "d3_moe_a8_prefill_workspace_bytes": (c_int64, [c_int32, c_int32, c_int32, c_int32, c_int32]),
+    "d3_moe_a8_prefill": (c_int32, [ctypes.POINTER(MoeA8PrefillDesc), c_void_p]),
     "d3_gemv_a8_groups": (c_int32, [c_int32, c_void_p, c_int32, c_int32, c_void_p, c_int32, c_void_p, c_void_p]),
     "d3_unpack_rows": (c_int32, [c_int32, c_void_p, c_int32, c_int32, c_void_p, c_void_p]),
     "d3_route": (c_int32, [c_void_p, c_int32, c_int32, c_int32, c_void_p, c_void_p, c_void_p]),

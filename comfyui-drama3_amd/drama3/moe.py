@@ -93,6 +93,50 @@ def moe_layer(x, logits, gate_up: A8Bank, down: A8Bank, topk, *, routing=False, 
     return (out, ids, weights) if routing else out
 
 
+def moe_prefill(x, gate_up: A8Bank, down: A8Bank, topk, *, logits=None, topk_idx=None, topk_weight=None,
+                routing=False, out=None):
+    """Many rows x [T, H] bf16 through the routed experts of A8 banks: [T, H] bf16 (d3_moe_a8_prefill). Routing from
+    router `logits` [T, E] bf16 (as moe_layer; with `routing` also returns ids and weights), or given as `topk_idx`
+    [T, k] int64 with `topk_weight` [T, k] (as Experts.forward receives them, drama3/model.py:73). The (row, expert)
+    pairs are grouped by expert on the device; nothing waits on the host."""
+    if x.dtype != torch.bfloat16 or x.dim() != 2:
+        raise TypeError("x must be bfloat16 [T, H]")
+    T, H = x.shape
+    E = gate_up.experts
+    if gate_up.fmt != down.fmt or down.experts != E:
+        raise ValueError("banks must share the format and the expert count")
+    if gate_up.cols != H or down.rows != H or gate_up.rows != 2 * down.cols:
+        raise ValueError("gate_up [E * 2I, H] and down [E * H, I] expected")
+    I = down.cols
+    device = x.device
+    x = x.contiguous()
+    if logits is not None:
+        if logits.dtype != torch.bfloat16 or logits.shape != (T, E):
+            raise ValueError("logits [T, E] bfloat16 expected")
+        logits = logits.contiguous()
+        ids_in = weights_in = None
+    else:
+        if topk_idx is None or topk_weight is None:
+            raise ValueError("logits, or topk_idx and topk_weight")
+        ids_in = topk_idx.to(torch.int64).contiguous()
+        weights_in = topk_weight.to(torch.float32).contiguous()
+        if ids_in.shape != (T, topk) or weights_in.shape != (T, topk):
+            raise ValueError("topk_idx / topk_weight [T, topk] expected")
+    if out is None:
+        out = torch.empty((T, H), dtype=torch.bfloat16, device=device)
+    ids = torch.empty((T, topk), dtype=torch.int64, device=device) if routing and logits is not None else None
+    weights = torch.empty((T, topk), dtype=torch.float32, device=device) if ids is not None else None
+    nbytes = int(_lib.lib().d3_moe_a8_prefill_workspace_bytes(T, topk, H, I, E))
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=device)
+    desc = _lib.MoeA8PrefillDesc(
+        x=x.data_ptr(), logits=_lib.ptr(logits), ids_in=_lib.ptr(ids_in), weights_in=_lib.ptr(weights_in),
+        gate_up=gate_up.weight.data_ptr(), gate_up_scale=gate_up.scale.data_ptr(), down=down.weight.data_ptr(),
+        down_scale=down.scale.data_ptr(), out=out.data_ptr(), ids_out=_lib.ptr(ids), weights_out=_lib.ptr(weights),
+        workspace=ws.data_ptr(), workspace_bytes=nbytes, format=gate_up.fmt, T=T, H=H, I=I, E=E, topk=topk)
+    _lib.check(_lib.lib().d3_moe_a8_prefill(ctypes.byref(desc), _lib.stream_of(device)), "d3_moe_a8_prefill")
+    return (out, ids, weights) if ids is not None else out
+
+
 def gemv_groups(bank_rows, fmt, cols, act):
     """Exact per-group dot products of packed rows [R, row_bytes] with act [C, cols] (int8, or e4m3 bytes for F8):
     [R, cols / 128, C] int32 (float32 for F8). Runs the fused layer's MFMA step on its own."""

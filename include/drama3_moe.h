@@ -66,6 +66,39 @@ int d3_moe_a8(const d3_moe_a8_desc* desc, void* stream);
  * `status` receives it (synchronous copy). */
 int d3_moe_a8_status(const void* workspace, uint32_t* status);
 
+/* ---- MoE layer for many rows on A8 banks (prefill, many decode lines) --------------------------------------------
+ * Replaces offload.resident_prefill (drama3/offload.py:139-149 -> grouped_int8 / grouped_fp8 / grouped_codes,
+ * kernels.py:365-464,538-587) and FP8Experts.forward's prompt branch (offload.py:775-802) for A8 banks: the rows'
+ * (row, expert) pairs are grouped by expert on the device (no host sync, unlike offload.py:142's bincount().tolist())
+ * and each expert's weights are read once for all its rows by grouped MFMA products. Same layer as d3_moe_a8:
+ *   out[t] = bf16( sum_j w[t, j] * down_e( SiLU(gate_e(x[t])) * up_e(x[t]) ) ),  e = ids[t, j]
+ * Routing from logits (as d3_moe_a8) or given (ids_in [T, topk] int64 with weights_in [T, topk] float32, as
+ * Experts.forward receives topk_idx / topk_weight, model.py:73). Several launches on `stream`; graph-capturable. */
+typedef struct d3_moe_a8_prefill_desc {
+  const void* x;             /* [T, H] bf16 */
+  const void* logits;        /* [T, E] bf16, or NULL with ids_in / weights_in */
+  const int64_t* ids_in;     /* [T, topk] */
+  const float* weights_in;   /* [T, topk] */
+  const void* gate_up;       /* A8 bank [E * 2I, row_bytes(H)] */
+  const void* gate_up_scale;
+  const void* down;          /* [E * H, row_bytes(I)] */
+  const void* down_scale;
+  void* out;                 /* [T, H] bf16 */
+  int64_t* ids_out;          /* [T, topk] or NULL (routing from logits only) */
+  float* weights_out;        /* [T, topk] or NULL */
+  void* workspace;           /* d3_moe_a8_prefill_workspace_bytes(...) bytes; no initialization needed */
+  int64_t workspace_bytes;
+  int32_t format;            /* D3_FMT_* */
+  int32_t T;                 /* rows */
+  int32_t H;                 /* 2048 */
+  int32_t I;                 /* 512 or 768 */
+  int32_t E;                 /* experts, <= 1024 */
+  int32_t topk;              /* <= 32 */
+} d3_moe_a8_prefill_desc;
+
+int64_t d3_moe_a8_prefill_workspace_bytes(int32_t T, int32_t topk, int32_t H, int32_t I, int32_t E);
+int d3_moe_a8_prefill(const d3_moe_a8_prefill_desc* desc, void* stream);
+
 /* ---- Checks of the A8 step (no reference counterpart: they expose the fused kernels' inner operations) --------
  * d3_gemv_a8_groups: rows [R, row_bytes(K)] of a bank in `format` against C <= 16 activation rows act [C, K] (int8;
  * e4m3 codes for F8). acc[R, K / 128, C]: the exact int32 dot product of each 128-column group (I8, W4, W6), or its

@@ -1,0 +1,141 @@
+"""GPU parity of the many-rows layer (d3_moe_a8_prefill: on-device grouping, grouped MFMA products) against the
+oracle's layer (oracle/a8.py moe_layer), for all four A8 formats.
+
+Bars as for the fused decode layer: routing ids exact and weights within one bf16 ulp; outputs (bf16) within max-abs
+2e-2 * max|ref| and rel-L2 1e-2 (SiLU(gate) * up in float32 with a fast exp before its quantization, the oracle in
+float64: a hidden code on a rounding boundary can differ by one step)."""
+import numpy as np
+import pytest
+import torch
+
+from drama3 import formats, moe
+from oracle import a8
+from oracle.numerics import bf16_bits_to_f32
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda:0")
+FMTS = [formats.FMT_I8, formats.FMT_W4, formats.FMT_W6, formats.FMT_F8]
+H, I = 2048, 768
+
+_banks = {}
+
+
+def banks(fmt, E=16, inter=I, seed=0):
+    key = (fmt, E, inter, seed)
+    if key not in _banks:
+        _banks.clear()
+        gen = torch.Generator(device=DEV).manual_seed(seed)
+        gate_up = formats.quantize(torch.randn((E, 2 * inter, H), generator=gen, device=DEV) * 0.02, fmt)
+        down = formats.quantize(torch.randn((E, H, inter), generator=gen, device=DEV) * 0.02, fmt)
+        _banks[key] = (gate_up, down)
+    return _banks[key]
+
+
+def bits(t):
+    return t.detach().contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+def fetcher(gate_up, down):
+    cache = {}
+
+    def fetch(bank, e):
+        if (bank, e) not in cache:
+            b = gate_up if bank == "gate_up" else down
+            rows = slice(e * b.rows, (e + 1) * b.rows)
+            cache[bank, e] = (b.weight[rows].cpu().numpy(),
+                              b.scale[rows].contiguous().view(torch.int16).cpu().numpy().view(np.uint16))
+        return cache[bank, e]
+    return fetch
+
+
+def check(fmt, x, logits, gate_up, down, topk=8):
+    out, ids, w = moe.moe_prefill(x, gate_up, down, topk, logits=logits, routing=True)
+    want, want_ids, want_w, _ = a8.moe_layer(bits(x), bits(logits), (gate_up.rows, gate_up.cols),
+                                             (down.rows, down.cols), fmt, topk, fetcher(gate_up, down))
+    assert np.array_equal(ids.cpu().numpy(), want_ids)
+    assert np.all(np.abs(w.cpu().numpy() - want_w) <= np.abs(want_w) * 2.0 ** -8 + 1e-30)
+    got = bf16_bits_to_f32(bits(out)).astype(np.float64)
+    ref = bf16_bits_to_f32(want).astype(np.float64)
+    assert np.all(np.isfinite(got))
+    err = np.abs(got - ref)
+    assert err.max() <= 2e-2 * np.abs(ref).max(), (err.max(), np.abs(ref).max())
+    assert np.linalg.norm(got - ref) <= 1e-2 * np.linalg.norm(ref)
+    return out, ids, w
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+def test_prefill_matches_oracle(fmt):
+    gate_up, down = banks(fmt)
+    gen = torch.Generator(device=DEV).manual_seed(20 + fmt)
+    x = torch.randn((24, H), generator=gen, device=DEV).to(torch.bfloat16)
+    logits = torch.randn((24, 16), generator=gen, device=DEV).to(torch.bfloat16)
+    check(fmt, x, logits, gate_up, down)
+
+
+@pytest.mark.parametrize("fmt", [formats.FMT_I8, formats.FMT_F8])
+def test_prefill_hot_experts_many_tiles(fmt):
+    """48 rows all routed to the same 8 experts: 48 pairs per expert, three 16-pair tiles each; 8 experts unused."""
+    gate_up, down = banks(fmt)
+    gen = torch.Generator(device=DEV).manual_seed(31)
+    x = torch.randn((48, H), generator=gen, device=DEV).to(torch.bfloat16)
+    logits = torch.randn((48, 16), generator=gen, device=DEV)
+    logits[:, 3:11] += 20.0
+    check(fmt, x, logits.to(torch.bfloat16), gate_up, down)
+
+
+def test_prefill_single_row_and_reference_shape():
+    """One row, and the reference model's shape (256 experts, FFN 512)."""
+    gate_up, down = banks(formats.FMT_W4, E=256, inter=512, seed=5)
+    gen = torch.Generator(device=DEV).manual_seed(32)
+    for T in (1, 5):
+        x = torch.randn((T, H), generator=gen, device=DEV).to(torch.bfloat16)
+        logits = torch.randn((T, 256), generator=gen, device=DEV).to(torch.bfloat16)
+        check(formats.FMT_W4, x, logits, gate_up, down)
+
+
+@pytest.mark.parametrize("fmt", [formats.FMT_I8, formats.FMT_W6])
+def test_given_routing_equals_logits_routing(fmt):
+    """topk_idx / topk_weight handed in (as Experts.forward gets them) give the same output as routing inside."""
+    gate_up, down = banks(fmt)
+    gen = torch.Generator(device=DEV).manual_seed(33)
+    x = torch.randn((20, H), generator=gen, device=DEV).to(torch.bfloat16)
+    logits = torch.randn((20, 16), generator=gen, device=DEV).to(torch.bfloat16)
+    out, ids, w = moe.moe_prefill(x, gate_up, down, 8, logits=logits, routing=True)
+    again = moe.moe_prefill(x, gate_up, down, 8, topk_idx=ids, topk_weight=w)
+    assert torch.equal(out, again)
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+def test_prefill_close_to_fused_decode(fmt):
+    """The same rows through the fused decode kernel and the prefill path: the same layer, other summation orders."""
+    gate_up, down = banks(fmt)
+    gen = torch.Generator(device=DEV).manual_seed(34)
+    x = torch.randn((8, H), generator=gen, device=DEV).to(torch.bfloat16)
+    logits = torch.randn((8, 16), generator=gen, device=DEV).to(torch.bfloat16)
+    a = moe.moe_prefill(x, gate_up, down, 8, logits=logits).float()
+    b = moe.moe_layer(x, logits, gate_up, down, 8).float()
+    assert torch.linalg.norm(a - b) <= 1e-2 * torch.linalg.norm(b)
+
+
+def test_prefill_graph_replays():
+    gate_up, down = banks(formats.FMT_F8)
+    gen = torch.Generator(device=DEV).manual_seed(35)
+    xs = [torch.randn((16, H), generator=gen, device=DEV).to(torch.bfloat16) for _ in range(3)]
+    lgs = [torch.randn((16, 16), generator=gen, device=DEV).to(torch.bfloat16) for _ in range(3)]
+    x_buf, lg_buf = xs[0].clone(), lgs[0].clone()
+    stream = torch.cuda.Stream(DEV)
+    stream.wait_stream(torch.cuda.current_stream(DEV))
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        moe.moe_prefill(x_buf, gate_up, down, 8, logits=lg_buf)
+        with torch.cuda.graph(g, stream=stream):
+            out = moe.moe_prefill(x_buf, gate_up, down, 8, logits=lg_buf)
+    torch.cuda.current_stream(DEV).wait_stream(stream)
+    for x, lg in zip(xs, lgs):
+        x_buf.copy_(x)
+        lg_buf.copy_(lg)
+        g.replay()
+        torch.cuda.synchronize()
+        eager = moe.moe_prefill(x_buf, gate_up, down, 8, logits=lg_buf)
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)
