@@ -1,19 +1,27 @@
-"""Benchmark of the fused routed-expert MoE layer on one MI355X.
+"""Benchmark of the routed-expert MoE layer on one MI355X.
 
 Default workload (the headline config): int8 experts, decode M = 1 row, hidden 2048, expert FFN 768, 128 experts,
 top-8 softmax routing from N(0, 1) router logits, per-row int8 activations, bf16 output; 48 distinct layer tables
 (29 GB, far beyond the 256 MB Infinity Cache), the layers chained as a decode step chains them (each layer's output
 is the next one's input). A step is one token through the 48 layers; four HIP graphs hold four tokens with their own
-routing and are replayed in turn.
+routing and are replayed in turn. The fused layer kernel (d3_moe_a8) runs each layer in one launch.
 
-    python bench.py [--steps K] [--warmup W] [--format int8|w4a8|w6a8|fp8] [--rows M] [--layers L]
+Other workloads of the same layer shape:
+    --format w4a8 --rows 4                      W4A8 experts, 4 decode lines batched (uniform routing)
+    --format w6a8 --routing zipf                W6A8 over 48 layers, experts per layer drawn from Zipf(1.1)
+    --mode prefill                              FP8 experts, 256 rows at once, Zipf(1.1) routing: the grouped
+                                                MFMA path (d3_moe_a8_prefill), 16 layers chained
 
-Prints one JSON line: metric (expert-weight GB/s), tokens/s, the roofline of the fused kernel (algorithmic bytes per
-launch / average launch time from HIP events on the replay stream, against 8 TB/s HBM) and the reference's CPU path
-timed on a bounded sample of the same workload on this host.
+    python bench.py [--steps K] [--warmup W] [--mode decode|prefill] [--format int8|w4a8|w6a8|fp8] [--rows M]
+                    [--layers L] [--routing normal|zipf] [--no-cpu-baseline] [--calibrate-copy]
+
+Prints one JSON line: metric (expert-weight GB/s), tokens/s, the roofline of the layer (algorithmic bytes per launch
+/ average launch time from HIP events on the replay stream, against 8 TB/s HBM) and the reference's CPU path timed on
+a bounded sample of the same workload on this host.
 """
 import argparse
 import json
+import math
 import os
 import pathlib
 import sys
@@ -28,12 +36,15 @@ from drama3 import formats, moe  # noqa: E402
 
 METRIC = "MoE-layer expert-weight HBM GB/s (% of peak) at M=1; decode tokens/s"
 # HBM bytes per launch of the fused kernel, from rocprofv3 FETCH_SIZE / WRITE_SIZE passes scaled by the same counters
-# on a plain copy kernel of known size (`--calibrate-copy`); keyed by (format, rows)
-TRAFFIC_PROFILES = {("int8", 1): ROOT / "profiles" / "moe_a8_int8_m1.md"}
+# on a plain copy kernel of known size (`--calibrate-copy`); keyed by (mode, format, rows)
+TRAFFIC_PROFILES = {("decode", "int8", 1): ROOT / "profiles" / "moe_a8_int8_m1.md"}
 PEAK_GBS = 8000.0
+PEAK_FP8_TFLOPS = 5000.0
 FORMATS = {"int8": formats.FMT_I8, "w4a8": formats.FMT_W4, "w6a8": formats.FMT_W6, "fp8": formats.FMT_F8}
+DTYPES = {"int8": "int8", "w4a8": "int4xint8", "w6a8": "int6xint8", "fp8": "fp8e4m3"}
 H, I, E, TOPK = 2048, 768, 128, 8
 GRAPH_TOKENS = 4
+ZIPF_S = 1.1
 
 
 def log(msg):
@@ -54,40 +65,67 @@ def make_layers(fmt, layers, device, seed=0):
     return banks
 
 
+def make_logits(routing, tokens, layers, rows, device, seed=1):
+    """Router logits [tokens, layers, rows, E] bf16. normal: N(0, 1). zipf: log p(rank) + Gumbel noise with
+    p(rank) ~ rank^-1.1 over a per-layer permutation of the experts, so the top-8 is a draw of 8 distinct experts
+    without replacement from Zipf(1.1) (Gumbel-top-k)."""
+    gen = torch.Generator(device=device).manual_seed(seed)
+    if routing == "normal":
+        return torch.randn((tokens, layers, rows, E), generator=gen, device=device).to(torch.bfloat16)
+    ranks = torch.arange(1, E + 1, device=device, dtype=torch.float32)
+    logp = -ZIPF_S * torch.log(ranks)
+    out = torch.empty((tokens, layers, rows, E), device=device)
+    for layer in range(layers):
+        perm = torch.randperm(E, generator=gen, device=device)
+        base = torch.empty(E, device=device)
+        base[perm] = logp
+        u = torch.rand((tokens, rows, E), generator=gen, device=device).clamp_(1e-12, 1 - 1e-7)
+        out[:, layer] = base - torch.log(-torch.log(u))
+    return out.to(torch.bfloat16)
+
+
 def expert_bytes(gate_up, down):
     return gate_up.expert_bytes() + down.expert_bytes()
 
 
-def cpu_baseline(banks, fmt, logits, x, budget_s=12.0):
+def cpu_baseline(banks, fmt, logits, x, grouped=False, budget_s=12.0):
     """The reference's CPU path (oracle/cpu_path.py) on this host: bf16 matmuls from the quantized banks per routed
-    expert, one row, over a sample of the same layers and routing; GB/s over the same algorithmic bytes."""
+    expert, over a sample of the same layers and routing; GB/s over the same algorithmic bytes (each routed expert's
+    weights once per layer pass)."""
     from oracle import cpu_path
     threads = min(16, len(os.sched_getaffinity(0)))
     torch.set_num_threads(threads)
     sample_layers = min(2, len(banks))
     host = [tuple((b.weight.cpu(), b.scale.cpu()) for b in pair) for pair in banks[:sample_layers]]
-    per_layer_bytes = TOPK * expert_bytes(*banks[0]) + 2 * H * 2 + E * 2
-    xs = x[0, :1].cpu()
+    per_expert = expert_bytes(*banks[0])
     lg = logits.cpu()
-    done, started = 0, time.perf_counter()
+    xs = x.cpu()
+    done, moved, started = 0, 0, time.perf_counter()
     tokens = lg.shape[0]
     while time.perf_counter() - started < budget_s:
         t, layer = done % tokens, done % sample_layers
-        w, ids = torch.softmax(lg[t, layer, 0].float(), -1).topk(TOPK)
-        w = (w / w.sum()).to(torch.bfloat16)
-        cpu_path.layer(xs, ids, w, host[layer][0], host[layer][1], fmt, H, I)
+        w, ids = torch.softmax(lg[t, layer].float(), -1).topk(TOPK, dim=-1)
+        w = (w / w.sum(-1, keepdim=True)).to(torch.bfloat16)
+        if grouped:
+            cpu_path.grouped_layer(xs[t], ids, w, host[layer][0], host[layer][1], fmt, H, I)
+            moved += len(torch.unique(ids)) * per_expert + xs[t].shape[0] * (2 * H * 2 + E * 2)
+        else:
+            cpu_path.layer(xs[t, :1], ids[0], w[0], host[layer][0], host[layer][1], fmt, H, I)
+            moved += TOPK * per_expert + 2 * H * 2 + E * 2
         done += 1
     elapsed = time.perf_counter() - started
-    return {"value": round(per_layer_bytes * done / elapsed / 1e9, 3), "unit": "GB/s", "cores": threads,
-            "kind": "port", "tokens_per_s": round(done / elapsed / len(banks), 3),
-            "sample": f"{done} layer passes (M=1, top-8) over {sample_layers} of the layers, {elapsed:.1f} s, "
-                      f"torch {threads} threads: _weight_int8pack_mm / dequantize-then-linear per expert"}
+    rows = xs.shape[1] if grouped else 1
+    what = "cpu_path.grouped_layer" if grouped else "cpu_path.layer"
+    return {"value": round(moved / elapsed / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "tokens_per_s": round(done * rows / elapsed / len(banks), 3),
+            "sample": f"{done} layer passes ({rows} rows, top-8) over {sample_layers} of the layers, {elapsed:.1f} s, "
+                      f"torch {threads} threads, {what}: _weight_int8pack_mm / dequantize-then-linear per expert"}
 
 
-def measured_traffic(fmt_name, rows):
+def measured_traffic(mode, fmt_name, rows):
     """HBM bytes per launch recorded in the workload's profile summary (line `traffic_bytes_per_launch: N`), or
     None."""
-    path = TRAFFIC_PROFILES.get((fmt_name, rows))
+    path = TRAFFIC_PROFILES.get((mode, fmt_name, rows))
     if path is None or not path.exists():
         return None
     for line in path.read_text().splitlines():
@@ -108,33 +146,25 @@ def calibrate_copy(device):
                       "write_bytes": b.numel() * 4}), flush=True)
 
 
-def main():
-    p = argparse.ArgumentParser()
-    p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=100)
-    p.add_argument("--warmup", type=int, default=8)
-    p.add_argument("--format", default="int8", choices=sorted(FORMATS))
-    p.add_argument("--rows", type=int, default=1)
-    p.add_argument("--layers", type=int, default=48)
-    p.add_argument("--no-cpu-baseline", action="store_true")
-    p.add_argument("--calibrate-copy", action="store_true", help="only run the copy kernel that scales PMC counters")
-    args = p.parse_args()
-    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print("bench.py measures one GPU: the routed-expert path runs on one MI355X (see DESIGN.md for how it would "
-              "shard); run it with --gpus 1", file=sys.stderr)
-        sys.exit(2)
-    fmt = FORMATS[args.format]
-    device = torch.device("cuda:0")
-    torch.cuda.set_device(device)
-    if args.calibrate_copy:
-        calibrate_copy(device)
-        return
-    M, L = args.rows, args.layers
+def timed_replays(graphs, stream, steps, warmup):
+    for i in range(warmup):
+        graphs[i % len(graphs)].replay()
+    stream.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for i in range(steps):
+        graphs[i % len(graphs)].replay()
+    end.record(stream)
+    end.synchronize()
+    return start.elapsed_time(end)
 
+
+def run_decode(args, fmt, device):
+    M, L = args.rows, args.layers
     log(f"building {L} layers of {args.format} experts")
     banks = make_layers(fmt, L, device)
-    gen = torch.Generator(device=device).manual_seed(1)
-    logits = torch.randn((GRAPH_TOKENS, L, M, E), generator=gen, device=device).to(torch.bfloat16)
+    logits = make_logits(args.routing, GRAPH_TOKENS, L, M, device)
+    gen = torch.Generator(device=device).manual_seed(2)
     x0 = torch.randn((GRAPH_TOKENS, M, H), generator=gen, device=device).to(torch.bfloat16)
 
     # routing of every (token, layer), for the exact count of experts each launch reads
@@ -151,7 +181,7 @@ def main():
 
     stream = torch.cuda.Stream(device)
     stream.wait_stream(torch.cuda.current_stream(device))
-    graphs, outs = [], []
+    graphs = []
     with torch.cuda.stream(stream):
         moe.prepare(device, H, I, stream)
         bufs = [x0[t].clone() for t in range(GRAPH_TOKENS)]
@@ -162,49 +192,117 @@ def main():
                 for layer, (gate_up, down) in enumerate(banks):
                     x = moe.moe_layer(x, logits[t, layer], gate_up, down, TOPK)
             graphs.append(g)
-            outs.append(x)
-        for i in range(args.warmup):
-            graphs[i % GRAPH_TOKENS].replay()
-        stream.synchronize()
-        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        start.record(stream)
-        for i in range(args.steps):
-            graphs[i % GRAPH_TOKENS].replay()
-        end.record(stream)
-        end.synchronize()
+        ms = timed_replays(graphs, stream, args.steps, args.warmup)
     torch.cuda.synchronize()
     status = moe.status(device, H, I, stream)
     if status:
         raise RuntimeError(f"fused layer reported status {status}")
-    ms = start.elapsed_time(end)
     total_bytes = sum(bytes_per_token[i % GRAPH_TOKENS] for i in range(args.steps))
-    gbs = total_bytes / (ms * 1e-3) / 1e9
     launches = args.steps * L
-    launch_us = ms * 1e3 / launches
-    bytes_per_launch = total_bytes / launches
-
     cpu = None
     if not args.no_cpu_baseline:
         log("timing the reference's CPU path")
-        cpu = cpu_baseline(banks, fmt, logits, x0)
+        cpu = cpu_baseline(banks, fmt, logits[:, :, :1], x0[:, :1])
+    config = {"workload": f"routed-expert MoE layer, {args.format} experts, decode M={M}, hidden {H}, FFN {I}, "
+                          f"{E} experts top-{TOPK} ({args.routing} routing), {L} layers chained per token",
+              "rows": M, "layers": L, "unique_experts_per_launch": round(sum(unique) / len(unique), 2)}
+    return ms, total_bytes, launches, args.steps * M, config, "d3::moe_a8_kernel", cpu
 
+
+def run_prefill(args, fmt, device):
+    T, L = args.rows, args.layers
+    log(f"building {L} layers of {args.format} experts")
+    banks = make_layers(fmt, L, device)
+    logits = make_logits(args.routing, 1, L, T, device)[0]
+    gen = torch.Generator(device=device).manual_seed(2)
+    x0 = torch.randn((T, H), generator=gen, device=device).to(torch.bfloat16)
+    unique = []
+    x = x0
+    for layer, (gate_up, down) in enumerate(banks):
+        x, ids, _ = moe.moe_prefill(x, gate_up, down, TOPK, logits=logits[layer], routing=True)
+        unique.append(len(torch.unique(ids)))
+    torch.cuda.synchronize()
+    per_expert = expert_bytes(*banks[0])
+    step_bytes = sum(unique) * per_expert + L * T * (2 * H * 2 + E * 2)
+    stream = torch.cuda.Stream(device)
+    stream.wait_stream(torch.cuda.current_stream(device))
+    with torch.cuda.stream(stream):
+        buf = x0.clone()
+        moe.moe_prefill(buf, *banks[0], TOPK, logits=logits[0])  # warm the allocator on this stream
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream):
+            x = buf
+            for layer, (gate_up, down) in enumerate(banks):
+                x = moe.moe_prefill(x, gate_up, down, TOPK, logits=logits[layer])
+        ms = timed_replays([g], stream, args.steps, args.warmup)
+    torch.cuda.synchronize()
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("timing the reference's CPU path")
+        sample = min(T, 32)
+        cpu = cpu_baseline(banks, fmt, logits[None, :, :sample], x0[None, :sample], grouped=True)
+    flops = 2 * TOPK * T * (2 * I * H + H * I)
+    config = {"workload": f"routed-expert MoE layer, {args.format} experts, {T} rows at once (prefill), hidden {H}, "
+                          f"FFN {I}, {E} experts top-{TOPK} ({args.routing} routing), {L} layers chained",
+              "rows": T, "layers": L, "unique_experts_per_launch": round(sum(unique) / len(unique), 2),
+              "mfma_tflops": round(flops * L * args.steps / (ms * 1e-3) / 1e12, 2),
+              "mfma_frac_fp8_peak": round(flops * L * args.steps / (ms * 1e-3) / 1e12 / PEAK_FP8_TFLOPS, 5)}
+    return ms, step_bytes * args.steps, args.steps * L, args.steps * T, config, "d3_moe_a8_prefill (7 launches)", cpu
+
+
+def main():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=None)
+    p.add_argument("--warmup", type=int, default=None)
+    p.add_argument("--mode", default="decode", choices=["decode", "prefill"])
+    p.add_argument("--format", default=None, choices=sorted(FORMATS))
+    p.add_argument("--rows", type=int, default=None)
+    p.add_argument("--layers", type=int, default=None)
+    p.add_argument("--routing", default=None, choices=["normal", "zipf"])
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--calibrate-copy", action="store_true", help="only run the copy kernel that scales PMC counters")
+    args = p.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: the routed-expert path runs on one MI355X (see DESIGN.md for how it would "
+              "shard); run it with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+    prefill = args.mode == "prefill"
+    args.format = args.format or ("fp8" if prefill else "int8")
+    args.rows = args.rows or (256 if prefill else 1)
+    args.layers = args.layers or (16 if prefill else 48)
+    args.routing = args.routing or ("zipf" if prefill else "normal")
+    args.steps = args.steps or (20 if prefill else 100)
+    args.warmup = args.warmup if args.warmup is not None else (3 if prefill else 8)
+    fmt = FORMATS[args.format]
+    device = torch.device("cuda:0")
+    torch.cuda.set_device(device)
+    if args.calibrate_copy:
+        calibrate_copy(device)
+        return
+
+    run = run_prefill if prefill else run_decode
+    ms, total_bytes, launches, tokens, config, kernel, cpu = run(args, fmt, device)
+    gbs = total_bytes / (ms * 1e-3) / 1e9
+    launch_us = ms * 1e3 / launches
+    bytes_per_launch = total_bytes / launches
+    config.update({"tokens_per_s": round(tokens / (ms * 1e-3), 2), "pct_of_peak_hbm": round(100 * gbs / PEAK_GBS, 2),
+                   "bytes_per_launch": int(bytes_per_launch)})
+    achieved = bytes_per_launch / (launch_us * 1e-6) / 1e9
     line = {
         "metric": METRIC, "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms / args.steps, 4), "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": {"int8": "int8", "w4a8": "int4xint8", "w6a8": "int6xint8", "fp8": "fp8e4m3"}[args.format],
-        "data": "synthetic: weights N(0, 0.02) quantized, activations and router logits N(0, 1), seeded",
-        "config": {"workload": f"routed-expert MoE layer, {args.format} experts, decode M={M}, hidden {H}, FFN {I}, "
-                               f"{E} experts top-{TOPK}, {L} layers chained per token",
-                   "rows": M, "layers": L, "tokens_per_s": round(args.steps * M / (ms * 1e-3), 2),
-                   "pct_of_peak_hbm": round(100 * gbs / PEAK_GBS, 2),
-                   "unique_experts_per_launch": round(sum(unique) / len(unique), 2),
-                   "bytes_per_launch": int(bytes_per_launch)},
-        "roofline": {"bound": "hbm", "achieved": round(bytes_per_launch / (launch_us * 1e-6) / 1e9, 1),
-                     "peak": PEAK_GBS, "unit": "GB/s", "frac": round(bytes_per_launch / (launch_us * 1e-6) / 1e9 / PEAK_GBS, 4),
-                     "traffic": measured_traffic(args.format, M), "kernel": "d3::moe_a8_kernel",
-                     "launch_us": round(launch_us, 3)},
+        "vs_baseline": None, "dtype": DTYPES[args.format],
+        "data": f"synthetic: weights N(0, 0.02) quantized, activations N(0, 1), router logits "
+                f"{'N(0, 1)' if args.routing == 'normal' else 'Zipf(1.1) Gumbel-top-k'}, seeded",
+        "config": config,
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / PEAK_GBS, 4), "traffic": measured_traffic(args.mode, args.format, args.rows),
+                     "kernel": kernel, "launch_us": round(launch_us, 3)},
         "cpu_baseline": cpu,
     }
+    if not math.isfinite(gbs):
+        raise RuntimeError("no time measured")
     print(json.dumps(line), flush=True)
 
 

@@ -9,7 +9,7 @@
 // Launches, all stream-ordered and graph-capturable (no host sync; the grouping happens on the device):
 //   route      top-k per row (d3_route's kernel), unless the caller hands ids / weights in
 //   group      one workgroup: per-expert counts (LDS atomics), offsets, and the pairs in expert order
-//   quantize   activations per row, in the format's storage order
+//   quantize   activations per pair, straight into the pairs' expert order, in the format's storage order
 //   gate_up    grid (I / 16, E): 16 hidden units of one expert (16 gate + 16 up rows), K split over 4 waves per
 //              tile, the weights held in registers while the expert's pairs go by 16 at a time; SiLU(gate) * up
 //   quantize   the hidden rows, per pair
@@ -21,6 +21,7 @@
 #include "formats.hpp"
 #include "../../include/drama3_moe.h"
 
+#include <algorithm>
 #include <string>
 
 namespace d3 {
@@ -30,6 +31,7 @@ int hip_fail(hipError_t err, const char* what);
 namespace {
 
 constexpr int MAX_EXPERTS = 1024;
+constexpr int UNIT_PAIRS = 64;  // pairs per work unit: bounds an item's time, so hot experts spread over workgroups
 
 struct PrefillArgs {
   const int64_t* ids;     // [P] pair p = t * k + j -> expert
@@ -37,8 +39,8 @@ struct PrefillArgs {
   const int* counts;      // [E]
   const int* offsets;     // [E + 1]
   const int* perm;        // [P] sorted position -> pair
-  const uint8_t* xq;      // [T, H] storage order
-  const float* xs;        // [T]
+  const uint8_t* xq;      // [P, H] storage order, by sorted position (row perm[s] / k of x)
+  const float* xs;        // [P]
   float* h;               // [P, I] by sorted position
   const uint8_t* hq;      // [P, I]
   const float* hs;        // [P]
@@ -47,39 +49,83 @@ struct PrefillArgs {
   const uint16_t* gu_s;
   const uint8_t* dn_w;
   const uint16_t* dn_s;
+  const int4* units;      // (expert, first position, pairs <= UNIT_PAIRS, 0): the experts' pairs in runs of at
+                          // most UNIT_PAIRS, experts with most pairs first
+  const int* meta;        // [0]: units
   int k;
   int inter;              // I
 };
 
 // ---------------------------------------------------------------------------------------------------------- group
+// Per-expert pair counts (LDS atomics), their offsets, the pairs in expert order, and the work units: each expert's
+// pairs in runs of at most UNIT_PAIRS, experts with most pairs first (ties: lower id first), the order the product
+// kernels take their work in (long work starts first).
+D3_INLINE int wave_exclusive_scan(int v, int lane, int& total) {
+  int incl = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int t = __shfl_up(incl, o);
+    if (lane >= o) incl += t;
+  }
+  total = __shfl(incl, 63);
+  return incl - v;
+}
+
 __global__ void __launch_bounds__(1024) group_kernel(const int64_t* ids, int P, int E, int* counts, int* offsets,
-                                                     int* perm) {
-  __shared__ int cnt[MAX_EXPERTS], cur[MAX_EXPERTS];
+                                                     int* perm, int4* units, int* meta) {
+  __shared__ int cnt[MAX_EXPERTS], cur[MAX_EXPERTS], by_rank[MAX_EXPERTS], rank_base[MAX_EXPERTS];
+  __shared__ int used;
   const int tid = threadIdx.x;
   for (int e = tid; e < E; e += 1024) cnt[e] = 0;
+  if (tid == 0) used = 0;
   __syncthreads();
   // ids outside [0, E) (a caller's error) count as the nearest expert instead of reaching outside the tables
   for (int p = tid; p < P; p += 1024) atomicAdd(&cnt[(int)min<int64_t>(max<int64_t>(ids[p], 0), E - 1)], 1);
   __syncthreads();
   if (tid < 64) {
-    // exclusive scan by wave 0: each lane sums a contiguous run of experts, then the runs are scanned
+    // exclusive scan of the counts by wave 0, each lane over a contiguous run of experts
     const int per = (E + 63) / 64, lo = tid * per, hi = min(E, lo + per);
     int run = 0;
     for (int e = lo; e < hi; e++) run += cnt[e];
-    int incl = run;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      const int v = __shfl_up(incl, o);
-      if (tid >= o) incl += v;
-    }
-    int at = incl - run;
+    int total;
+    int at = wave_exclusive_scan(run, tid, total);
     for (int e = lo; e < hi; e++) {
       cur[e] = at;
       offsets[e] = at;
       counts[e] = cnt[e];
       at += cnt[e];
     }
-    if (tid == 63) offsets[E] = incl;
+    if (tid == 0) offsets[E] = total;
+  }
+  // each used expert's rank (most pairs first), and its unit count at that rank
+  for (int e = tid; e < E; e += 1024) {
+    const int c = cnt[e];
+    if (c > 0) {
+      atomicAdd(&used, 1);
+      int rank = 0;
+      for (int f = 0; f < E; f++) rank += cnt[f] > c || (cnt[f] == c && f < e);
+      by_rank[rank] = e;
+    }
+  }
+  __syncthreads();
+  const int U = used;
+  if (tid < 64) {
+    const int per = (U + 63) / 64, lo = tid * per, hi = min(U, lo + per);
+    int run = 0;
+    for (int r = lo; r < hi; r++) run += (cnt[by_rank[r]] + UNIT_PAIRS - 1) / UNIT_PAIRS;
+    int total;
+    int at = wave_exclusive_scan(run, tid, total);
+    for (int r = lo; r < hi; r++) {
+      rank_base[r] = at;
+      at += (cnt[by_rank[r]] + UNIT_PAIRS - 1) / UNIT_PAIRS;
+    }
+    if (tid == 0) meta[0] = total;
+  }
+  __syncthreads();
+  for (int r = tid; r < U; r += 1024) {
+    const int e = by_rank[r], c = cnt[e], first = cur[e];
+    for (int u = 0; u * UNIT_PAIRS < c; u++)
+      units[rank_base[r] + u] = int4{e, first + u * UNIT_PAIRS, min(UNIT_PAIRS, c - u * UNIT_PAIRS), 0};
   }
   __syncthreads();
   for (int p = tid; p < P; p += 1024) perm[atomicAdd(&cur[(int)min<int64_t>(max<int64_t>(ids[p], 0), E - 1)], 1)] = p;
@@ -90,10 +136,11 @@ __global__ void __launch_bounds__(1024) group_kernel(const int64_t* ids, int P, 
 // row's scale.
 template <int F, bool BF16>
 __global__ void __launch_bounds__(256) quantize_rows_kernel(const void* src, int rows, int width, uint8_t* q,
-                                                            float* scale) {
+                                                            float* scale, const int* rowmap, int k) {
   constexpr float QMAX = act_qmax<F>();
-  const int lane = threadIdx.x & 63, row = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (row >= rows) return;
+  const int lane = threadIdx.x & 63, out_row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (out_row >= rows) return;
+  const int row = rowmap ? rowmap[out_row] / k : out_row;  // source row
   const int chunks = width / 8;
   float amax = 0.0f;
   for (int c = lane; c < chunks; c += 64) {
@@ -125,22 +172,35 @@ __global__ void __launch_bounds__(256) quantize_rows_kernel(const void* src, int
       const f32x4 b = *(const f32x4*)((const float*)src + (size_t)row * width + 8 * c + 4);
       v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
     }
-    store_act8<F>(q + (size_t)row * width + 8 * c, v, inv);
+    store_act8<F>(q + (size_t)out_row * width + 8 * c, v, inv);
   }
-  if (lane == 0) scale[row] = amax / QMAX;
+  if (lane == 0) scale[out_row] = amax / QMAX;
 }
 
 // ------------------------------------------------------------------------------------------- grouped MFMA products
-// A workgroup computes TILES 16-row tiles of one expert's bank against all of the expert's pairs. Its KS * TILES
-// waves split the work: wave w takes tile w / KS and the K-slice w % KS (SW = K / 128 / KS steps of 128 columns), whose
-// weight bytes it holds in registers while it walks the pairs 16 at a time; the KS partial products of a tile meet in
-// LDS. Per MFMA, lane l reads weight row l % 16 and pair l % 16, lane group l / 16 covers 32 columns of a step.
-//   MODE 0 (gate_up): TILES = 2 = 16 gate rows and the matching 16 up rows (hidden units 16 bx ..), epilogue
-//                     SiLU(gate) * up into h[sorted position].
-//   MODE 1 (down):    TILES 16-row tiles of output rows (TILES * 16 bx ..), epilogue scaled by the pair's hidden scale
-//                     and routing weight into parts[pair].
-template <int F, int SW> struct Slice {
-  Raw<F> raw[SW];
+// The grouped products, persistent: a work item is (unit, tile): a run of at most UNIT_PAIRS of one expert's pairs
+// against the expert's 16 hidden units (gate_up: its 16 gate and 16 up rows) or 64 output rows (down). A workgroup
+// walks items i, i + grid, ... (experts with most pairs first), loading the next item's weights while it computes
+// the current one. Its 4 waves split K into KS
+// slices (SW steps of 128 columns each) and 16-row tile pairs: a wave holds its two tiles' bytes of its slice in
+// registers and walks the expert's pairs 16 at a time (one MFMA per tile and step; lane l reads weight row l % 16
+// and pair l % 16, lane group l / 16 covers 32 columns of a step); the slices' partial products meet in LDS.
+//   MODE 0 (gate_up): K = H, 4 slices, tiles = gate and up rows of units 16 it .. 16 it + 15; epilogue SiLU(gate) *
+//                     up into h[sorted position].
+//   MODE 1 (down):    K = I, 2 slices, 2 tile pairs = output rows 64 it .. 64 it + 63; epilogue scaled by the pair's
+//                     hidden scale and routing weight into parts[pair].
+template <int F, int H, int I, int MODE> struct Geometry {
+  static constexpr int K = MODE == 0 ? H : I;
+  static constexpr int KS = MODE == 0 ? 4 : 2;
+  static constexpr int TILES = MODE == 0 ? 2 : 4;
+  static constexpr int SW = K / 128 / KS;
+  static constexpr int PER_EXPERT = MODE == 0 ? I / 16 : H / 64;  // items per expert
+  static constexpr int RB = row_bytes(F, K);
+};
+
+template <int F, int SW> struct Weights {
+  Raw<F> raw[2][SW];
+  float rs[2][4];  // I8 / F8: the accumulator rows' scales, per tile
 };
 
 // one lane's 32 activation bytes of step `st`
@@ -153,117 +213,162 @@ D3_INLINE void load_act(const uint8_t* act, int st, int q, bool valid, i32x4& lo
   }
 }
 
-template <int F, int K, int KS, int TILES, int MODE>
-__global__ void __launch_bounds__(64 * KS * TILES) grouped_kernel(PrefillArgs a) {
-  constexpr int SW = K / 128 / KS;
-  constexpr int SHIFT = unpack_shift(F);
-  constexpr int RB = row_bytes(F, K);
-  constexpr int H = 2048;
-  const int bx = blockIdx.x, e = blockIdx.y;
-  const int n = a.counts[e];
-  if (n == 0) return;
-  const int first = a.offsets[e];
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, q = lane >> 4, col = lane & 15;
-  const int tile = w / KS, ks = w % KS, st0 = ks * SW;
-  // bank rows of this wave's tile
-  size_t row0;
-  const uint8_t* bank;
-  const uint16_t* sbank;
-  if constexpr (MODE == 0) {
-    row0 = (size_t)e * 2 * a.inter + (tile ? a.inter : 0) + 16 * bx;
-    bank = a.gu_w;
-    sbank = a.gu_s;
-  } else {
-    row0 = (size_t)e * H + 16 * (TILES * bx + tile);
-    bank = a.dn_w;
-    sbank = a.dn_s;
-  }
-  Slice<F, SW> sl;
-  {
-    const uint8_t* row = bank + (row0 + col) * RB;
+template <int F, int H, int I, int MODE>
+D3_INLINE size_t tile_row0(const PrefillArgs& a, int e, int it, int tile) {
+  if constexpr (MODE == 0) return (size_t)e * 2 * I + (tile ? I : 0) + 16 * it;
+  else return (size_t)e * H + 64 * it + 16 * tile;
+}
+
+template <int F, int H, int I, int MODE>
+D3_INLINE void load_weights(Weights<F, Geometry<F, H, I, MODE>::SW>& wt, const PrefillArgs& a, int e, int it,
+                            int tp, int ks, int lane) {
+  using G = Geometry<F, H, I, MODE>;
+  const int q = lane >> 4;
+  const uint8_t* bank = MODE == 0 ? a.gu_w : a.dn_w;
+  const uint16_t* sb = MODE == 0 ? a.gu_s : a.dn_s;
 #pragma unroll
-    for (int j = 0; j < SW; j++) load_step<F>(sl.raw[j], row, st0 + j, q);
-  }
-  // scales of the accumulator rows 4q + i: per row (I8, F8) or per (row, step) (W4, W6)
-  float rs[4], gsc[SW][4];
+  for (int t = 0; t < 2; t++) {
+    const size_t row0 = tile_row0<F, H, I, MODE>(a, e, it, 2 * tp + t);
+    const uint8_t* row = bank + (row0 + (lane & 15)) * G::RB;
 #pragma unroll
-  for (int i = 0; i < 4; i++) {
-    if constexpr (group_scaled(F)) {
+    for (int j = 0; j < G::SW; j++) load_step<F>(wt.raw[t][j], row, ks * G::SW + j, q);
+    if constexpr (!group_scaled(F)) {
 #pragma unroll
-      for (int j = 0; j < SW; j++) gsc[j][i] = bf16_to_f32(sbank[(row0 + 4 * q + i) * (K / 128) + st0 + j]);
-      rs[i] = 1.0f;
-    } else {
-      rs[i] = bf16_to_f32(sbank[row0 + 4 * q + i]);
+      for (int i = 0; i < 4; i++) wt.rs[t][i] = bf16_to_f32(sb[row0 + 4 * q + i]);
     }
   }
-  __shared__ float part[TILES][KS][16][17];
-  const uint8_t* acts = MODE == 0 ? a.xq : a.hq;
+}
+
+// colv / colp: per column (pair) of a 16-pair tile, its epilogue scale and (down) its pair index, staged in LDS by
+// wave 0 while the products run
+template <int F, int H, int I, int MODE>
+D3_INLINE void compute_item(const PrefillArgs& a, const Weights<F, Geometry<F, H, I, MODE>::SW>& wt, int4 unit,
+                            int it, float* gs, float (*part)[Geometry<F, H, I, MODE>::KS][16][17], float* colv,
+                            int* colp) {
+  using G = Geometry<F, H, I, MODE>;
+  constexpr int SW = G::SW, KS = G::KS, K = G::K, STEPS = K / 128;
+  constexpr int SHIFT = unpack_shift(F);
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, q = lane >> 4, col = lane & 15;
+  const int ks = w % KS, tp = w / KS;
+  const int e = unit.x, first = unit.y, n = unit.z;
+  if constexpr (group_scaled(F)) {
+    // group scales of the item's rows: gs[tile][row][step]
+    const uint16_t* sb = MODE == 0 ? a.gu_s : a.dn_s;
+    for (int o = tid; o < G::TILES * 16 * STEPS; o += 256) {
+      const int t = o / (16 * STEPS), r = (o / STEPS) % 16, st = o % STEPS;
+      gs[o] = bf16_to_f32(sb[(tile_row0<F, H, I, MODE>(a, e, it, t) + r) * STEPS + st]);
+    }
+    __syncthreads();
+  }
   for (int c0 = 0; c0 < n; c0 += 16) {
     const bool valid = c0 + col < n;
     const int sp = first + c0 + (valid ? col : 0);
-    const uint8_t* act;
-    if constexpr (MODE == 0) act = acts + (size_t)(a.perm[sp] / a.k) * K;
-    else act = acts + (size_t)sp * K;
+    if (w == 0 && lane < 16) {
+      if constexpr (MODE == 0) {
+        colv[col] = valid ? a.xs[sp] : 0.0f;
+      } else {
+        const int pr = valid ? a.perm[sp] : 0;
+        colp[col] = pr;
+        colv[col] = valid ? a.hs[sp] * a.weights[pr] : 0.0f;
+      }
+    }
+    const uint8_t* act = (MODE == 0 ? a.xq : a.hq) + (size_t)sp * K;
     i32x4 lo[SW], hi[SW];
 #pragma unroll
-    for (int j = 0; j < SW; j++) load_act(act, st0 + j, q, valid, lo[j], hi[j]);
-    f32x4 y;
-    if constexpr (F == FMT_F8) {
-      f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int j = 0; j < SW; j++) load_act(act, ks * SW + j, q, valid, lo[j], hi[j]);
 #pragma unroll
-      for (int j = 0; j < SW; j++) acc = step_f8(sl.raw[j], lo[j], hi[j], acc);
-      y = acc;
-    } else if constexpr (F == FMT_I8) {
-      i32x4 acc = {0, 0, 0, 0};
+    for (int t = 0; t < 2; t++) {
+      f32x4 y;
+      if constexpr (F == FMT_F8) {
+        f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-      for (int j = 0; j < SW; j++) acc = step_i8<F>(sl.raw[j], lo[j], hi[j], acc);
+        for (int j = 0; j < SW; j++) acc = step_f8(wt.raw[t][j], lo[j], hi[j], acc);
 #pragma unroll
-      for (int i = 0; i < 4; i++) y[i] = (float)acc[i];
-    } else {
-      f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (int i = 0; i < 4; i++) y[i] = acc[i] * wt.rs[t][i];
+      } else if constexpr (F == FMT_I8) {
+        i32x4 acc = {0, 0, 0, 0};
 #pragma unroll
-      for (int j = 0; j < SW; j++) {
-        const i32x4 g = step_i8<F>(sl.raw[j], lo[j], hi[j], i32x4{0, 0, 0, 0});
+        for (int j = 0; j < SW; j++) acc = step_i8<F>(wt.raw[t][j], lo[j], hi[j], acc);
 #pragma unroll
-        for (int i = 0; i < 4; i++) acc[i] += (float)(g[i] >> SHIFT) * gsc[j][i];
+        for (int i = 0; i < 4; i++) y[i] = (float)acc[i] * wt.rs[t][i];
+      } else {
+        const float* g = gs + (2 * tp + t) * 16 * STEPS;
+        f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int j = 0; j < SW; j++) {
+          const i32x4 d = step_i8<F>(wt.raw[t][j], lo[j], hi[j], i32x4{0, 0, 0, 0});
+#pragma unroll
+          for (int i = 0; i < 4; i++) acc[i] += (float)(d[i] >> SHIFT) * g[(4 * q + i) * STEPS + ks * SW + j];
+        }
+        y = acc;
       }
-      y = acc;
-    }
 #pragma unroll
-    for (int i = 0; i < 4; i++) part[tile][ks][4 * q + i][col] = y[i] * rs[i];
+      for (int i = 0; i < 4; i++) part[2 * tp + t][ks][4 * q + i][col] = y[i];
+    }
     __syncthreads();
     if constexpr (MODE == 0) {
-      // 16 units x 16 pairs, one per thread of the first 256
-      if (tid < 256) {
-        const int u = tid & 15, j = tid >> 4;
-        if (c0 + j < n) {
-          float g = 0.0f, up = 0.0f;
+      // 16 units x 16 pairs, one per thread
+      const int u = tid & 15, j = tid >> 4;
+      if (c0 + j < n) {
+        float gv = 0.0f, uv = 0.0f;
 #pragma unroll
-          for (int k2 = 0; k2 < KS; k2++) {
-            g += part[0][k2][u][j];
-            up += part[1][k2][u][j];
-          }
-          const float xs = a.xs[a.perm[first + c0 + j] / a.k];
-          g *= xs;
-          up *= xs;
-          a.h[(size_t)(first + c0 + j) * a.inter + 16 * bx + u] = g / (1.0f + __expf(-g)) * up;
+        for (int k2 = 0; k2 < KS; k2++) {
+          gv += part[0][k2][u][j];
+          uv += part[1][k2][u][j];
         }
+        const float xs = colv[j];
+        gv *= xs;
+        uv *= xs;
+        a.h[(size_t)(first + c0 + j) * I + 16 * it + u] = gv / (1.0f + __expf(-gv)) * uv;
       }
     } else {
-      // TILES * 16 rows x 16 pairs
-      for (int o = tid; o < TILES * 256; o += 64 * KS * TILES) {
-        const int r = o & (16 * TILES - 1), j = o / (16 * TILES);
+      // 64 rows x 16 pairs, four per thread
+#pragma unroll
+      for (int r4 = 0; r4 < 4; r4++) {
+        const int o = tid + 256 * r4, r = o & 63, j = o >> 6;
         if (c0 + j < n) {
-          const int t2 = r >> 4, rr = r & 15;
           float v = 0.0f;
 #pragma unroll
-          for (int k2 = 0; k2 < KS; k2++) v += part[t2][k2][rr][j];
-          const int sp2 = first + c0 + j, pair = a.perm[sp2];
-          a.parts[(size_t)pair * H + 16 * TILES * bx + r] = v * a.hs[sp2] * a.weights[pair];
+          for (int k2 = 0; k2 < KS; k2++) v += part[r >> 4][k2][r & 15][j];
+          a.parts[(size_t)colp[j] * H + 64 * it + r] = v * colv[j];
         }
       }
     }
     __syncthreads();
+  }
+}
+
+template <int F, int H, int I, int MODE>
+__global__ void __launch_bounds__(256) grouped_kernel(PrefillArgs a) {
+  using G = Geometry<F, H, I, MODE>;
+  __shared__ float part[G::TILES][G::KS][16][17];
+  __shared__ float gs[group_scaled(F) ? G::TILES * 16 * (G::K / 128) : 1];
+  __shared__ float colv[16];
+  __shared__ int colp[16];
+  const int n_items = a.meta[0] * G::PER_EXPERT;
+  int i = blockIdx.x;
+  if (i >= n_items) return;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, ks = w % G::KS, tp = w / G::KS;
+  int4 item = a.units[i / G::PER_EXPERT];
+  int it = i % G::PER_EXPERT;
+  Weights<F, G::SW> cur, nxt;
+  load_weights<F, H, I, MODE>(cur, a, item.x, it, tp, ks, lane);
+  while (true) {
+    const int in = i + (int)gridDim.x;
+    const bool more = in < n_items;
+    int4 item_n = item;
+    int it_n = 0;
+    if (more) {
+      item_n = a.units[in / G::PER_EXPERT];
+      it_n = in % G::PER_EXPERT;
+      load_weights<F, H, I, MODE>(nxt, a, item_n.x, it_n, tp, ks, lane);
+    }
+    compute_item<F, H, I, MODE>(a, cur, item, it, gs, part, colv, colp);
+    if (!more) break;
+    cur = nxt;
+    item = item_n;
+    it = it_n;
+    i = in;
   }
 }
 
@@ -283,7 +388,7 @@ __global__ void __launch_bounds__(256) reduce_kernel(const float* parts, int T, 
 
 // ------------------------------------------------------------------------------------------------------- host side
 struct Layout {
-  size_t ids, weights, counts, offsets, perm, xq, xs, h, hq, hs, parts, total;
+  size_t ids, weights, counts, offsets, perm, units, meta, xq, xs, h, hq, hs, parts, total;
 };
 size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 Layout layout(int64_t T, int64_t k, int64_t H, int64_t I, int64_t E) {
@@ -296,8 +401,10 @@ Layout layout(int64_t T, int64_t k, int64_t H, int64_t I, int64_t E) {
   L.counts = take(E * 4);
   L.offsets = take((E + 1) * 4);
   L.perm = take(P * 4);
-  L.xq = take(T * H);
-  L.xs = take(T * 4);
+  L.units = take((E + P / UNIT_PAIRS + 1) * 16);
+  L.meta = take(16);
+  L.xq = take(P * H);
+  L.xs = take(P * 4);
   L.h = take(P * I * 4);
   L.hq = take(P * I);
   L.hs = take(P * 4);
@@ -306,28 +413,47 @@ Layout layout(int64_t T, int64_t k, int64_t H, int64_t I, int64_t E) {
   return L;
 }
 
-// gate_up: K = H = 2048 in 4 slices of 4 steps, 2 tiles (gate, up) -> 8 waves; down: K = I in 2 slices, 2 tiles
-template <int F, int H, int I> void launch_products(const PrefillArgs& pa, int E, hipStream_t s) {
-  hipLaunchKernelGGL((grouped_kernel<F, H, 4, 2, 0>), dim3(I / 16, E), dim3(512), 0, s, pa);
+// Persistent grids: as many workgroups as the device holds at once (the kernels stop at the item count).
+template <int F, int H, int I, int MODE> int resident_grid() {
+  static int grid = 0;
+  if (grid == 0) {
+    int dev = 0, cus = 0, per = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, grouped_kernel<F, H, I, MODE>, 256, 0) != hipSuccess ||
+        per < 1)
+      return 1024;
+    grid = cus * per;
+  }
+  return grid;
 }
-template <int F, int H, int I> void launch_down(const PrefillArgs& pa, int E, hipStream_t s) {
-  hipLaunchKernelGGL((grouped_kernel<F, I, (I / 128) % 2 == 0 ? 2 : 1, 2, 1>), dim3(H / 32, E), dim3((I / 128) % 2 == 0 ? 256 : 128), 0, s, pa);
+template <int F, int H, int I> void launch_products(const PrefillArgs& pa, int max_units, hipStream_t s) {
+  const int grid = std::min(resident_grid<F, H, I, 0>(), max_units * (I / 16));
+  hipLaunchKernelGGL((grouped_kernel<F, H, I, 0>), dim3(grid), dim3(256), 0, s, pa);
+}
+template <int F, int H, int I> void launch_down(const PrefillArgs& pa, int max_units, hipStream_t s) {
+  const int grid = std::min(resident_grid<F, H, I, 1>(), max_units * (H / 64));
+  hipLaunchKernelGGL((grouped_kernel<F, H, I, 1>), dim3(grid), dim3(256), 0, s, pa);
 }
 
 template <int F> void launch_quantize(const void* src, bool bf16, int rows, int width, uint8_t* q, float* scale,
-                                      hipStream_t s) {
+                                      const int* rowmap, int k, hipStream_t s) {
   const dim3 grid((rows + 3) / 4);
-  if (bf16) hipLaunchKernelGGL((quantize_rows_kernel<F, true>), grid, dim3(256), 0, s, src, rows, width, q, scale);
-  else hipLaunchKernelGGL((quantize_rows_kernel<F, false>), grid, dim3(256), 0, s, src, rows, width, q, scale);
+  if (bf16)
+    hipLaunchKernelGGL((quantize_rows_kernel<F, true>), grid, dim3(256), 0, s, src, rows, width, q, scale, rowmap, k);
+  else
+    hipLaunchKernelGGL((quantize_rows_kernel<F, false>), grid, dim3(256), 0, s, src, rows, width, q, scale, rowmap, k);
 }
 
 template <int F, int H, int I> void run(const PrefillArgs& pa, const d3_moe_a8_prefill_desc& d, const Layout& L,
                                         uint8_t* ws, hipStream_t s) {
   const int P = d.T * d.topk;
-  launch_quantize<F>(d.x, true, d.T, H, ws + L.xq, (float*)(ws + L.xs), s);
-  launch_products<F, H, I>(pa, d.E, s);
-  launch_quantize<F>(ws + L.h, false, P, I, ws + L.hq, (float*)(ws + L.hs), s);
-  launch_down<F, H, I>(pa, d.E, s);
+  const int max_units = std::min(d.E, P) + P / UNIT_PAIRS;
+  // activations quantized straight into the pairs' sorted order (row perm[s] / k of x for position s)
+  launch_quantize<F>(d.x, true, P, H, ws + L.xq, (float*)(ws + L.xs), pa.perm, d.topk, s);
+  launch_products<F, H, I>(pa, max_units, s);
+  launch_quantize<F>(ws + L.h, false, P, I, ws + L.hq, (float*)(ws + L.hs), nullptr, 1, s);
+  launch_down<F, H, I>(pa, max_units, s);
 }
 
 }  // namespace
@@ -375,7 +501,7 @@ int d3_moe_a8_prefill(const d3_moe_a8_prefill_desc* d, void* stream) {
     if (err != hipSuccess) return hip_fail(err, "d3_moe_a8_prefill: copy routing out");
   }
   hipLaunchKernelGGL(group_kernel, dim3(1), dim3(1024), 0, s, (const int64_t*)ids, P, d->E, (int*)(ws + L.counts),
-                     (int*)(ws + L.offsets), (int*)(ws + L.perm));
+                     (int*)(ws + L.offsets), (int*)(ws + L.perm), (int4*)(ws + L.units), (int*)(ws + L.meta));
   PrefillArgs pa;
   pa.ids = ids;
   pa.weights = weights;
@@ -392,6 +518,8 @@ int d3_moe_a8_prefill(const d3_moe_a8_prefill_desc* d, void* stream) {
   pa.gu_s = (const uint16_t*)d->gate_up_scale;
   pa.dn_w = (const uint8_t*)d->down;
   pa.dn_s = (const uint16_t*)d->down_scale;
+  pa.units = (const int4*)(ws + L.units);
+  pa.meta = (const int*)(ws + L.meta);
   pa.k = d->topk;
   pa.inter = d->I;
   const bool i768 = d->I == 768;

@@ -45,3 +45,24 @@ def layer(x, ids, weights, gate_up, down, fmt, H, I):
             hidden = _swiglu(torch.nn.functional.linear(x, dequantize_rows(gw, gs, fmt, H)).float()).to(torch.bfloat16)
             outs.append(torch.nn.functional.linear(hidden, dequantize_rows(dw, ds, fmt, I)).float())
     return weights.float() @ torch.cat(outs)
+
+
+def grouped_layer(x, ids, weights, gate_up, down, fmt, H, I):
+    """Many rows x [T, H] bf16 through their experts ids [T, k] on the CPU, one expert at a time over the rows that
+    chose it, as FP8Experts.forward's prompt branch runs (drama3/offload.py:783-802): [T, H] float32."""
+    T, k = ids.shape
+    flat = ids.reshape(-1)
+    out = torch.zeros((T * k, H), dtype=torch.float32)
+    for e in torch.unique(flat).tolist():
+        sel = (flat == e).nonzero().flatten()
+        rows = x[sel // k]
+        gw, gs = expert_rows(*gate_up, 2 * I, e)
+        dw, ds = expert_rows(*down, H, e)
+        if fmt == 0:
+            hidden = _swiglu(torch._weight_int8pack_mm(rows, gw.view(torch.int8), gs).float()).to(torch.bfloat16)
+            y = torch._weight_int8pack_mm(hidden, dw.view(torch.int8), ds).float()
+        else:
+            hidden = _swiglu(torch.nn.functional.linear(rows, dequantize_rows(gw, gs, fmt, H)).float()).to(torch.bfloat16)
+            y = torch.nn.functional.linear(hidden, dequantize_rows(dw, ds, fmt, I)).float()
+        out[sel] = y * weights.reshape(-1)[sel].float()[:, None]
+    return out.view(T, k, H).sum(1)
