@@ -206,7 +206,8 @@ def run_decode(args, fmt, device):
     config = {"workload": f"routed-expert MoE layer, {args.format} experts, decode M={M}, hidden {H}, FFN {I}, "
                           f"{E} experts top-{TOPK} ({args.routing} routing), {L} layers chained per token",
               "rows": M, "layers": L, "unique_experts_per_launch": round(sum(unique) / len(unique), 2)}
-    return ms, total_bytes, launches, args.steps * M, config, "d3::moe_a8_kernel", cpu
+    kernel = "d3::moe_a8_kernel" if M < moe.GROUPED_FROM_ROWS else "d3_moe_a8_prefill (7 launches)"
+    return ms, total_bytes, launches, args.steps * M, config, kernel, cpu
 
 
 def run_prefill(args, fmt, device):

@@ -43,7 +43,7 @@ struct PrefillArgs {
   const float* xs;        // [P]
   float* h;               // [P, I] by sorted position
   const uint8_t* hq;      // [P, I]
-  const float* hs;        // [P]
+  const float* hs;        // [P] the hidden row's scale times the pair's routing weight
   float* parts;           // [P, H] by pair
   const uint8_t* gu_w;
   const uint16_t* gu_s;
@@ -132,49 +132,52 @@ __global__ void __launch_bounds__(1024) group_kernel(const int64_t* ids, int P, 
 }
 
 // ------------------------------------------------------------------------------------------------------- quantize
-// One wave per row of `width` floats (bf16 with BF16): absmax, then codes in the format's storage order and the
-// row's scale.
-template <int F, bool BF16>
-__global__ void __launch_bounds__(256) quantize_rows_kernel(const void* src, int rows, int width, uint8_t* q,
-                                                            float* scale, const int* rowmap, int k) {
+// One wave per output row of WIDTH values (float, or bf16 with BF16), read once into registers: absmax, then codes in
+// the format's storage order and the row's scale. With a row map, output row s reads source row rowmap[s] / k; with
+// pair weights, the scale is multiplied by pair_weight[rowmap2[s]] (the down products then need no other factor).
+template <int F, bool BF16, int WIDTH>
+__global__ void __launch_bounds__(256) quantize_rows_kernel(const void* src, int rows, uint8_t* q, float* scale,
+                                                            const int* rowmap, int k, const float* pair_weight,
+                                                            const int* rowmap2) {
   constexpr float QMAX = act_qmax<F>();
+  constexpr int CHUNKS = WIDTH / 8, CPL = (CHUNKS + 63) / 64;  // 8-value chunks, per lane
   const int lane = threadIdx.x & 63, out_row = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (out_row >= rows) return;
   const int row = rowmap ? rowmap[out_row] / k : out_row;  // source row
-  const int chunks = width / 8;
+  float v[CPL][8];
   float amax = 0.0f;
-  for (int c = lane; c < chunks; c += 64) {
-    float v[8];
-    if constexpr (BF16) {
-      const i32x4 r = *(const i32x4*)((const uint16_t*)src + (size_t)row * width + 8 * c);
-      const uint32_t w4[4] = {(uint32_t)r.x, (uint32_t)r.y, (uint32_t)r.z, (uint32_t)r.w};
 #pragma unroll
-      for (int i = 0; i < 4; i++) { v[2 * i] = bf16_to_f32(w4[i] & 0xFFFFu); v[2 * i + 1] = bf16_to_f32(w4[i] >> 16); }
-    } else {
-      const f32x4 a = *(const f32x4*)((const float*)src + (size_t)row * width + 8 * c);
-      const f32x4 b = *(const f32x4*)((const float*)src + (size_t)row * width + 8 * c + 4);
-      v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+  for (int i = 0; i < CPL; i++) {
+    const int c = lane + 64 * i;
+#pragma unroll
+    for (int j = 0; j < 8; j++) v[i][j] = 0.0f;
+    if (c < CHUNKS) {
+      if constexpr (BF16) {
+        const i32x4 r = *(const i32x4*)((const uint16_t*)src + (size_t)row * WIDTH + 8 * c);
+        const uint32_t w4[4] = {(uint32_t)r.x, (uint32_t)r.y, (uint32_t)r.z, (uint32_t)r.w};
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          v[i][2 * j] = bf16_to_f32(w4[j] & 0xFFFFu);
+          v[i][2 * j + 1] = bf16_to_f32(w4[j] >> 16);
+        }
+      } else {
+        const f32x4 a = *(const f32x4*)((const float*)src + (size_t)row * WIDTH + 8 * c);
+        const f32x4 b = *(const f32x4*)((const float*)src + (size_t)row * WIDTH + 8 * c + 4);
+        v[i][0] = a.x; v[i][1] = a.y; v[i][2] = a.z; v[i][3] = a.w;
+        v[i][4] = b.x; v[i][5] = b.y; v[i][6] = b.z; v[i][7] = b.w;
+      }
     }
 #pragma unroll
-    for (int i = 0; i < 8; i++) amax = fmaxf(amax, fabsf(v[i]));
+    for (int j = 0; j < 8; j++) amax = fmaxf(amax, fabsf(v[i][j]));
   }
   amax = wave_max_f32(amax);
   const float inv = amax > 0.0f ? QMAX / amax : 0.0f;
-  for (int c = lane; c < chunks; c += 64) {
-    float v[8];
-    if constexpr (BF16) {
-      const i32x4 r = *(const i32x4*)((const uint16_t*)src + (size_t)row * width + 8 * c);
-      const uint32_t w4[4] = {(uint32_t)r.x, (uint32_t)r.y, (uint32_t)r.z, (uint32_t)r.w};
 #pragma unroll
-      for (int i = 0; i < 4; i++) { v[2 * i] = bf16_to_f32(w4[i] & 0xFFFFu); v[2 * i + 1] = bf16_to_f32(w4[i] >> 16); }
-    } else {
-      const f32x4 a = *(const f32x4*)((const float*)src + (size_t)row * width + 8 * c);
-      const f32x4 b = *(const f32x4*)((const float*)src + (size_t)row * width + 8 * c + 4);
-      v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
-    }
-    store_act8<F>(q + (size_t)out_row * width + 8 * c, v, inv);
+  for (int i = 0; i < CPL; i++) {
+    const int c = lane + 64 * i;
+    if (c < CHUNKS) store_act8<F>(q + (size_t)out_row * WIDTH + 8 * c, v[i], inv);
   }
-  if (lane == 0) scale[out_row] = amax / QMAX;
+  if (lane == 0) scale[out_row] = amax / QMAX * (pair_weight ? pair_weight[rowmap2[out_row]] : 1.0f);
 }
 
 // ------------------------------------------------------------------------------------------- grouped MFMA products
@@ -239,136 +242,160 @@ D3_INLINE void load_weights(Weights<F, Geometry<F, H, I, MODE>::SW>& wt, const P
   }
 }
 
-// colv / colp: per column (pair) of a 16-pair tile, its epilogue scale and (down) its pair index, staged in LDS by
-// wave 0 while the products run
+// One item: the unit's pairs 16 at a time against the weights in `wt`. The next item's weights go into `pref` in the
+// last tile, after that tile's own loads, unconditionally (the current item's rows again when there is no next item,
+// which the cache serves): a wave's vector loads complete in issue order and the compiler counts them per path, so
+// a load issued after the prefetch, or a prefetch on one path only, would make the products wait for it. For the
+// same reason activation rows are read without a branch (columns past the unit's pairs read its first pair and their
+// products are never stored). colv / colp: per column (pair) of a tile, its epilogue scale and (down) its pair index,
+// staged in LDS by wave 0.
 template <int F, int H, int I, int MODE>
-D3_INLINE void compute_item(const PrefillArgs& a, const Weights<F, Geometry<F, H, I, MODE>::SW>& wt, int4 unit,
-                            int it, float* gs, float (*part)[Geometry<F, H, I, MODE>::KS][16][17], float* colv,
+D3_INLINE void compute_tile(const PrefillArgs& a, const Weights<F, Geometry<F, H, I, MODE>::SW>& wt,
+                            Weights<F, Geometry<F, H, I, MODE>::SW>* pref, int4 unit_n, int it_n, int4 unit, int it,
+                            int c0, const float* gs, float (*part)[Geometry<F, H, I, MODE>::KS][16][17], float* colv,
                             int* colp) {
   using G = Geometry<F, H, I, MODE>;
   constexpr int SW = G::SW, KS = G::KS, K = G::K, STEPS = K / 128;
   constexpr int SHIFT = unpack_shift(F);
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, q = lane >> 4, col = lane & 15;
   const int ks = w % KS, tp = w / KS;
-  const int e = unit.x, first = unit.y, n = unit.z;
+  const int first = unit.y, n = unit.z;
+  const bool valid = c0 + col < n;
+  const int sp = first + (valid ? c0 + col : 0);
+  const uint8_t* act = (MODE == 0 ? a.xq : a.hq) + (size_t)sp * K + 32 * q;
+  i32x4 lo[SW], hi[SW];
+#pragma unroll
+  for (int j = 0; j < SW; j++) {
+    lo[j] = *(const i32x4*)(act + 128 * (ks * SW + j));
+    hi[j] = *(const i32x4*)(act + 128 * (ks * SW + j) + 16);
+  }
+  if (w == 0 && lane < 16) {
+    colv[col] = valid ? (MODE == 0 ? a.xs[sp] : a.hs[sp]) : 0.0f;
+    if constexpr (MODE == 1) colp[col] = valid ? a.perm[sp] : 0;
+  }
+  if (pref) load_weights<F, H, I, MODE>(*pref, a, unit_n.x, it_n, tp, ks, lane);
+#pragma unroll
+  for (int t = 0; t < 2; t++) {
+    f32x4 y;
+    if constexpr (F == FMT_F8) {
+      f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int j = 0; j < SW; j++) acc = step_f8(wt.raw[t][j], lo[j], hi[j], acc);
+#pragma unroll
+      for (int i = 0; i < 4; i++) y[i] = acc[i] * wt.rs[t][i];
+    } else if constexpr (F == FMT_I8) {
+      i32x4 acc = {0, 0, 0, 0};
+#pragma unroll
+      for (int j = 0; j < SW; j++) acc = step_i8<F>(wt.raw[t][j], lo[j], hi[j], acc);
+#pragma unroll
+      for (int i = 0; i < 4; i++) y[i] = (float)acc[i] * wt.rs[t][i];
+    } else {
+      const float* g = gs + (2 * tp + t) * 16 * STEPS;
+      f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int j = 0; j < SW; j++) {
+        const i32x4 d = step_i8<F>(wt.raw[t][j], lo[j], hi[j], i32x4{0, 0, 0, 0});
+#pragma unroll
+        for (int i = 0; i < 4; i++) acc[i] += (float)(d[i] >> SHIFT) * g[(4 * q + i) * STEPS + ks * SW + j];
+      }
+      y = acc;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++) part[2 * tp + t][ks][4 * q + i][col] = y[i];
+  }
+  __syncthreads();
+  if constexpr (MODE == 0) {
+    // 16 units x 16 pairs, one per thread
+    const int u = tid & 15, j = tid >> 4;
+    if (c0 + j < n) {
+      float gv = 0.0f, uv = 0.0f;
+#pragma unroll
+      for (int k2 = 0; k2 < KS; k2++) {
+        gv += part[0][k2][u][j];
+        uv += part[1][k2][u][j];
+      }
+      const float xs = colv[j];
+      gv *= xs;
+      uv *= xs;
+      a.h[(size_t)(first + c0 + j) * I + 16 * it + u] = gv / (1.0f + __expf(-gv)) * uv;
+    }
+  } else {
+    // 64 rows x 16 pairs, four per thread; hs carries the pair's routing weight
+#pragma unroll
+    for (int r4 = 0; r4 < 4; r4++) {
+      const int o = tid + 256 * r4, r = o & 63, j = o >> 6;
+      if (c0 + j < n) {
+        float v = 0.0f;
+#pragma unroll
+        for (int k2 = 0; k2 < KS; k2++) v += part[r >> 4][k2][r & 15][j];
+        a.parts[(size_t)colp[j] * H + 64 * it + r] = v * colv[j];
+      }
+    }
+  }
+  __syncthreads();
+}
+
+template <int F, int H, int I, int MODE>
+D3_INLINE void compute_item(const PrefillArgs& a, const Weights<F, Geometry<F, H, I, MODE>::SW>& wt,
+                            Weights<F, Geometry<F, H, I, MODE>::SW>& pref, int4 unit_n, int it_n, int4 unit, int it,
+                            float* gs, float (*part)[Geometry<F, H, I, MODE>::KS][16][17], float* colv, int* colp) {
+  using G = Geometry<F, H, I, MODE>;
+  constexpr int STEPS = G::K / 128;
+  const int tid = threadIdx.x;
   if constexpr (group_scaled(F)) {
     // group scales of the item's rows: gs[tile][row][step]
     const uint16_t* sb = MODE == 0 ? a.gu_s : a.dn_s;
     for (int o = tid; o < G::TILES * 16 * STEPS; o += 256) {
       const int t = o / (16 * STEPS), r = (o / STEPS) % 16, st = o % STEPS;
-      gs[o] = bf16_to_f32(sb[(tile_row0<F, H, I, MODE>(a, e, it, t) + r) * STEPS + st]);
+      gs[o] = bf16_to_f32(sb[(tile_row0<F, H, I, MODE>(a, unit.x, it, t) + r) * STEPS + st]);
     }
     __syncthreads();
   }
-  for (int c0 = 0; c0 < n; c0 += 16) {
-    const bool valid = c0 + col < n;
-    const int sp = first + c0 + (valid ? col : 0);
-    if (w == 0 && lane < 16) {
-      if constexpr (MODE == 0) {
-        colv[col] = valid ? a.xs[sp] : 0.0f;
-      } else {
-        const int pr = valid ? a.perm[sp] : 0;
-        colp[col] = pr;
-        colv[col] = valid ? a.hs[sp] * a.weights[pr] : 0.0f;
-      }
-    }
-    const uint8_t* act = (MODE == 0 ? a.xq : a.hq) + (size_t)sp * K;
-    i32x4 lo[SW], hi[SW];
-#pragma unroll
-    for (int j = 0; j < SW; j++) load_act(act, ks * SW + j, q, valid, lo[j], hi[j]);
-#pragma unroll
-    for (int t = 0; t < 2; t++) {
-      f32x4 y;
-      if constexpr (F == FMT_F8) {
-        f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-        for (int j = 0; j < SW; j++) acc = step_f8(wt.raw[t][j], lo[j], hi[j], acc);
-#pragma unroll
-        for (int i = 0; i < 4; i++) y[i] = acc[i] * wt.rs[t][i];
-      } else if constexpr (F == FMT_I8) {
-        i32x4 acc = {0, 0, 0, 0};
-#pragma unroll
-        for (int j = 0; j < SW; j++) acc = step_i8<F>(wt.raw[t][j], lo[j], hi[j], acc);
-#pragma unroll
-        for (int i = 0; i < 4; i++) y[i] = (float)acc[i] * wt.rs[t][i];
-      } else {
-        const float* g = gs + (2 * tp + t) * 16 * STEPS;
-        f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-        for (int j = 0; j < SW; j++) {
-          const i32x4 d = step_i8<F>(wt.raw[t][j], lo[j], hi[j], i32x4{0, 0, 0, 0});
-#pragma unroll
-          for (int i = 0; i < 4; i++) acc[i] += (float)(d[i] >> SHIFT) * g[(4 * q + i) * STEPS + ks * SW + j];
-        }
-        y = acc;
-      }
-#pragma unroll
-      for (int i = 0; i < 4; i++) part[2 * tp + t][ks][4 * q + i][col] = y[i];
-    }
-    __syncthreads();
-    if constexpr (MODE == 0) {
-      // 16 units x 16 pairs, one per thread
-      const int u = tid & 15, j = tid >> 4;
-      if (c0 + j < n) {
-        float gv = 0.0f, uv = 0.0f;
-#pragma unroll
-        for (int k2 = 0; k2 < KS; k2++) {
-          gv += part[0][k2][u][j];
-          uv += part[1][k2][u][j];
-        }
-        const float xs = colv[j];
-        gv *= xs;
-        uv *= xs;
-        a.h[(size_t)(first + c0 + j) * I + 16 * it + u] = gv / (1.0f + __expf(-gv)) * uv;
-      }
-    } else {
-      // 64 rows x 16 pairs, four per thread
-#pragma unroll
-      for (int r4 = 0; r4 < 4; r4++) {
-        const int o = tid + 256 * r4, r = o & 63, j = o >> 6;
-        if (c0 + j < n) {
-          float v = 0.0f;
-#pragma unroll
-          for (int k2 = 0; k2 < KS; k2++) v += part[r >> 4][k2][r & 15][j];
-          a.parts[(size_t)colp[j] * H + 64 * it + r] = v * colv[j];
-        }
-      }
-    }
-    __syncthreads();
-  }
+  const int last = (unit.z - 1) & ~15;
+  for (int c0 = 0; c0 < last; c0 += 16)
+    compute_tile<F, H, I, MODE>(a, wt, nullptr, unit_n, it_n, unit, it, c0, gs, part, colv, colp);
+  compute_tile<F, H, I, MODE>(a, wt, &pref, unit_n, it_n, unit, it, last, gs, part, colv, colp);
 }
 
+// units / meta come as separate read-only kernel arguments so that their (uniform) loads are scalar loads: those
+// complete apart from the waves' vector loads, so reading the next unit never waits for a weight prefetch.
 template <int F, int H, int I, int MODE>
-__global__ void __launch_bounds__(256) grouped_kernel(PrefillArgs a) {
+__global__ void __launch_bounds__(256) grouped_kernel(PrefillArgs a, const int4* __restrict__ units,
+                                                      const int* __restrict__ meta) {
   using G = Geometry<F, H, I, MODE>;
   __shared__ float part[G::TILES][G::KS][16][17];
   __shared__ float gs[group_scaled(F) ? G::TILES * 16 * (G::K / 128) : 1];
   __shared__ float colv[16];
   __shared__ int colp[16];
-  const int n_items = a.meta[0] * G::PER_EXPERT;
+  const int n_items = meta[0] * G::PER_EXPERT;
   int i = blockIdx.x;
   if (i >= n_items) return;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, ks = w % G::KS, tp = w / G::KS;
-  int4 item = a.units[i / G::PER_EXPERT];
+  int4 unit = units[i / G::PER_EXPERT];
   int it = i % G::PER_EXPERT;
-  Weights<F, G::SW> cur, nxt;
-  load_weights<F, H, I, MODE>(cur, a, item.x, it, tp, ks, lane);
+  // two weight buffers in turn (no copy between them, so nothing waits for a prefetch before its data is needed)
+  Weights<F, G::SW> buf0, buf1;
+  load_weights<F, H, I, MODE>(buf0, a, unit.x, it, tp, ks, lane);
   while (true) {
-    const int in = i + (int)gridDim.x;
-    const bool more = in < n_items;
-    int4 item_n = item;
-    int it_n = 0;
-    if (more) {
-      item_n = a.units[in / G::PER_EXPERT];
-      it_n = in % G::PER_EXPERT;
-      load_weights<F, H, I, MODE>(nxt, a, item_n.x, it_n, tp, ks, lane);
-    }
-    compute_item<F, H, I, MODE>(a, cur, item, it, gs, part, colv, colp);
+    // the next item (this one again at the end: its rows are in the cache)
+    int in = i + (int)gridDim.x;
+    bool more = in < n_items;
+    int4 unit_n = units[(more ? in : i) / G::PER_EXPERT];
+    int it_n = (more ? in : i) % G::PER_EXPERT;
+    compute_item<F, H, I, MODE>(a, buf0, buf1, unit_n, it_n, unit, it, gs, part, colv, colp);
     if (!more) break;
-    cur = nxt;
-    item = item_n;
-    it = it_n;
     i = in;
+    unit = unit_n;
+    it = it_n;
+    in = i + (int)gridDim.x;
+    more = in < n_items;
+    unit_n = units[(more ? in : i) / G::PER_EXPERT];
+    it_n = (more ? in : i) % G::PER_EXPERT;
+    compute_item<F, H, I, MODE>(a, buf1, buf0, unit_n, it_n, unit, it, gs, part, colv, colp);
+    if (!more) break;
+    i = in;
+    unit = unit_n;
+    it = it_n;
   }
 }
 
@@ -429,20 +456,18 @@ template <int F, int H, int I, int MODE> int resident_grid() {
 }
 template <int F, int H, int I> void launch_products(const PrefillArgs& pa, int max_units, hipStream_t s) {
   const int grid = std::min(resident_grid<F, H, I, 0>(), max_units * (I / 16));
-  hipLaunchKernelGGL((grouped_kernel<F, H, I, 0>), dim3(grid), dim3(256), 0, s, pa);
+  hipLaunchKernelGGL((grouped_kernel<F, H, I, 0>), dim3(grid), dim3(256), 0, s, pa, pa.units, pa.meta);
 }
 template <int F, int H, int I> void launch_down(const PrefillArgs& pa, int max_units, hipStream_t s) {
   const int grid = std::min(resident_grid<F, H, I, 1>(), max_units * (H / 64));
-  hipLaunchKernelGGL((grouped_kernel<F, H, I, 1>), dim3(grid), dim3(256), 0, s, pa);
+  hipLaunchKernelGGL((grouped_kernel<F, H, I, 1>), dim3(grid), dim3(256), 0, s, pa, pa.units, pa.meta);
 }
 
-template <int F> void launch_quantize(const void* src, bool bf16, int rows, int width, uint8_t* q, float* scale,
-                                      const int* rowmap, int k, hipStream_t s) {
-  const dim3 grid((rows + 3) / 4);
-  if (bf16)
-    hipLaunchKernelGGL((quantize_rows_kernel<F, true>), grid, dim3(256), 0, s, src, rows, width, q, scale, rowmap, k);
-  else
-    hipLaunchKernelGGL((quantize_rows_kernel<F, false>), grid, dim3(256), 0, s, src, rows, width, q, scale, rowmap, k);
+template <int F, bool BF16, int WIDTH> void launch_quantize(const void* src, int rows, uint8_t* q, float* scale,
+                                                             const int* rowmap, int k, const float* pair_weight,
+                                                             const int* rowmap2, hipStream_t s) {
+  hipLaunchKernelGGL((quantize_rows_kernel<F, BF16, WIDTH>), dim3((rows + 3) / 4), dim3(256), 0, s, src, rows, q,
+                     scale, rowmap, k, pair_weight, rowmap2);
 }
 
 template <int F, int H, int I> void run(const PrefillArgs& pa, const d3_moe_a8_prefill_desc& d, const Layout& L,
@@ -450,9 +475,9 @@ template <int F, int H, int I> void run(const PrefillArgs& pa, const d3_moe_a8_p
   const int P = d.T * d.topk;
   const int max_units = std::min(d.E, P) + P / UNIT_PAIRS;
   // activations quantized straight into the pairs' sorted order (row perm[s] / k of x for position s)
-  launch_quantize<F>(d.x, true, P, H, ws + L.xq, (float*)(ws + L.xs), pa.perm, d.topk, s);
+  launch_quantize<F, true, H>(d.x, P, ws + L.xq, (float*)(ws + L.xs), pa.perm, d.topk, nullptr, nullptr, s);
   launch_products<F, H, I>(pa, max_units, s);
-  launch_quantize<F>(ws + L.h, false, P, I, ws + L.hq, (float*)(ws + L.hs), nullptr, 1, s);
+  launch_quantize<F, false, I>(ws + L.h, P, ws + L.hq, (float*)(ws + L.hs), nullptr, 1, pa.weights, pa.perm, s);
   launch_down<F, H, I>(pa, max_units, s);
 }
 

@@ -58,12 +58,22 @@ def status(device, H, I, stream=None):
 
 
 DN_START = 0
+# From this many rows on, moe_layer runs the grouped path (d3_moe_a8_prefill): its persistent grouped products read
+# each expert once for all rows and keep the memory busy, where the fused kernel's items for several rows queue up
+# behind each other (measured on MI355X, W4A8: 4 rows 54 vs 61 us, 16 rows 92 vs 215 us).
+GROUPED_FROM_ROWS = 4
 
 
 def moe_layer(x, logits, gate_up: A8Bank, down: A8Bank, topk, *, routing=False, spin_limit=0, grid=0, out=None,
-              dn_start=None):
+              dn_start=None, fused=None):
     """x [M, H] bf16 and router logits [M, E] bf16 (M <= 16) through the routed experts: [M, H] bf16, and with
-    `routing` also (ids [M, topk] int64 in descending logit order, weights [M, topk] float32)."""
+    `routing` also (ids [M, topk] int64 in descending logit order, weights [M, topk] float32). Fewer than
+    GROUPED_FROM_ROWS rows run the fused one-launch kernel (d3_moe_a8), more the grouped path (moe_prefill); `fused`
+    forces either."""
+    if fused is None:
+        fused = x.shape[0] < GROUPED_FROM_ROWS
+    if not fused:
+        return moe_prefill(x, gate_up, down, topk, logits=logits, routing=routing, out=out)
     if x.dtype != torch.bfloat16 or logits.dtype != torch.bfloat16:
         raise TypeError("x and logits must be bfloat16")
     if x.dim() != 2 or logits.dim() != 2 or x.shape[0] != logits.shape[0]:

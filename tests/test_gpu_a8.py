@@ -88,8 +88,8 @@ def fetcher(gate_up, down):
     return fetch
 
 
-def check_layer(fmt, x, logits, gate_up, down, topk=8):
-    out, ids, w = moe.moe_layer(x, logits, gate_up, down, topk, routing=True)
+def check_layer(fmt, x, logits, gate_up, down, topk=8, fused=True):
+    out, ids, w = moe.moe_layer(x, logits, gate_up, down, topk, routing=True, fused=fused)
     torch.cuda.synchronize()
     assert moe.status(DEV, x.shape[1], down.cols) == 0
     want, want_ids, want_w, _ = a8.moe_layer(bits(x), bits(logits), (gate_up.rows, gate_up.cols), (down.rows, down.cols),
@@ -106,7 +106,7 @@ def check_layer(fmt, x, logits, gate_up, down, topk=8):
 
 
 @pytest.mark.parametrize("fmt", FMTS)
-@pytest.mark.parametrize("M", [1, 4, 16])
+@pytest.mark.parametrize("M", [1, 2, 4, 16])
 def test_layer_matches_oracle(fmt, M):
     gate_up, down = layer_banks(fmt)
     gen = torch.Generator(device=DEV).manual_seed(100 + M)
@@ -142,9 +142,9 @@ def test_repeated_launches_are_identical():
     gen = torch.Generator(device=DEV).manual_seed(9)
     x = torch.randn((4, 2048), generator=gen, device=DEV).to(torch.bfloat16)
     logits = torch.randn((4, 128), generator=gen, device=DEV).to(torch.bfloat16)
-    first = moe.moe_layer(x, logits, gate_up, down, 8)
+    first = moe.moe_layer(x, logits, gate_up, down, 8, fused=True)
     for _ in range(5):
-        again = moe.moe_layer(x, logits, gate_up, down, 8)
+        again = moe.moe_layer(x, logits, gate_up, down, 8, fused=True)
         assert torch.equal(first, again)
     assert moe.status(DEV, 2048, 768) == 0
 
@@ -178,3 +178,14 @@ def test_graph_replay_matches_eager():
         assert torch.equal(static_out, eager)
         _ = chain(x0.clone())  # eager work between replays
     assert moe.status(DEV, 2048, 768, stream) == 0
+
+
+@pytest.mark.parametrize("M", [1, 3, 4, 16])
+def test_layer_dispatch_matches_oracle(M):
+    """moe_layer's own choice of path (fused below GROUPED_FROM_ROWS rows, grouped from there on) against the
+    oracle."""
+    gate_up, down = layer_banks(formats.FMT_W4)
+    gen = torch.Generator(device=DEV).manual_seed(200 + M)
+    x = torch.randn((M, 2048), generator=gen, device=DEV).to(torch.bfloat16)
+    logits = torch.randn((M, 128), generator=gen, device=DEV).to(torch.bfloat16)
+    check_layer(formats.FMT_W4, x, logits, gate_up, down, fused=None)
