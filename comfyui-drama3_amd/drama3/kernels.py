@@ -69,6 +69,26 @@ def weighted_sum(parts, weights):
     return out
 
 
+def resolve(ids, layer, layers, num_experts, half_life, cpu, admit, table, owner, score, at, pending, clock, budget,
+            reads, step, share):
+    """plan [k, 2] int32 for the row's experts `ids` [k] (int64) of `layer`: the slot cache's lookup and decayed-LFU
+    eviction on the device, state tensors updated in place (kernels.py:78-191)."""
+    plan = torch.empty((ids.shape[0], 2), dtype=torch.int32, device=ids.device)
+    _call("d3_resolve", _p(ids.contiguous()), ids.shape[0], int(layer), int(layers), int(num_experts), _p(table),
+          _p(owner), _p(score), _p(at), _p(pending), owner.shape[0], _p(clock), _p(budget), _p(plan), _p(reads),
+          _p(step), _p(share), float(half_life), int(cpu), float(admit), _stream(ids))
+    return plan
+
+
+def await_cpu(plan, flag, step, result, timeout_us, took_over):
+    """[1, H] float32: the host's result for the experts `plan` left to the CPU, or zeros when the host is late (then
+    took_over is set; kernels.py:193-220). flag and result live in pinned host memory."""
+    out = torch.empty((1, result.shape[-1]), dtype=torch.float32, device=plan.device)
+    _call("d3_await_cpu", _p(plan), plan.shape[0], _p(flag), _p(step), _p(result), int(timeout_us), _p(out),
+          _p(took_over), result.shape[-1], _stream(plan))
+    return out
+
+
 def rotate(x, only_if, swiglu=False):
     """Rows of x [rows, K] (float32 or bfloat16; float32 [rows, 2K] gate | up with `swiglu`, SiLU(gate) * up first) in
     the ConvRot basis: float32 [rows, K]. Only when `only_if` (an int32 on the GPU) is set; otherwise the output is

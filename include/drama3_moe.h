@@ -156,6 +156,26 @@ int d3_grouped(int32_t kind, const float* x, const int32_t* groups, int32_t n_gr
                void* slot_c, const void* host_w, const void* host_s, const void* host_c, const float* codebook,
                float* out, int32_t N, int32_t K, void* stream);
 
+/* resolve_experts (kernels.py:78-191, wrapper resolve kernels.py:617-625): the slot cache's lookup and eviction for
+ * one decode row's experts ids [k] (int64, k <= 32) of `layer`, on the device. State (device memory, updated in
+ * place): table [layers * experts] (slot, -1, or -2 - slot while the host copies into it), owner [count] (key or -1),
+ * score / at [layers * experts] (decayed use count, as of step at), pending [count], clock [1] (passes), budget [2]
+ * (reservations left this step, per layer), reads [3] (hits, GPU fills, CPU experts), step [1] (this layer's step).
+ * share [1] float: the GPU's share of the missed experts with `cpu`. plan [k, 2] int32 out = (slot, code): 0 cached,
+ * 1 read from the bank and fill the slot, 2 left to the CPU (slot reserved for the host's copy, or -1). One
+ * workgroup. */
+int d3_resolve(const int64_t* ids, int32_t k, int32_t layer, int32_t layers, int32_t experts, int32_t* table,
+               int32_t* owner, float* score, int32_t* at, int32_t* pending, int32_t count, int32_t* clock,
+               int32_t* budget, int32_t* plan, int32_t* reads, int32_t* step, const float* share, double half_life,
+               int32_t cpu, double admit, void* stream);
+
+/* await_cpu (kernels.py:193-220, wrapper kernels.py:628-633): when plan [k, 2] leaves experts to the CPU, waits up to
+ * timeout_us for the host flag (pinned host memory) to reach step[0], then out [H] float32 = the host's bf16 result
+ * (pinned host memory); a late host gives zeros and took_over[0] = 1 (the GEMVs' `late` launch then runs those
+ * experts). Without CPU experts it returns at once (zeros, took_over 0). */
+int d3_await_cpu(const int32_t* plan, int32_t k, const int32_t* flag, const int32_t* step, const void* result,
+                 int32_t timeout_us, float* out, int32_t* took_over, int32_t H, void* stream);
+
 /* Check of the W4A8 / W6A8 decode on its own (kernels.py:466-483 decode_codes; no entry point of its own there):
  * codes [R, K] int8 of rows [R, K * bits / 8] with scales [R, K / 16]; K % 32 == 0. */
 int d3_decode_codes(int32_t bits, const void* rows, const void* scales, const float* codebook, int32_t R, int32_t K,

@@ -1,0 +1,97 @@
+"""Pins of oracle/slots.py (the slot cache's resolve and the wait for the host, drama3/kernels.py:78-220) through the
+invariants a decayed-LFU slot cache must keep and hand-built cases of its CPU / GPU split. CPU only."""
+import numpy as np
+import pytest
+
+from oracle import slots
+
+
+def check_consistent(st):
+    for s, key in enumerate(st["owner"]):
+        if key >= 0:
+            assert st["table"][key] in (s, -2 - s)
+    for key, t in enumerate(st["table"]):
+        if t >= 0:
+            assert st["owner"][t] == key and not st["pending"][t]
+        elif t <= -2:
+            assert st["owner"][-2 - t] == key and st["pending"][-2 - t]
+
+
+@pytest.mark.parametrize("cpu", [0, 1])
+def test_random_trace_keeps_invariants_and_evicts_the_least_used(cpu):
+    rng = np.random.default_rng(cpu)
+    L, E, S, k = 3, 16, 6, 4
+    st = slots.new_state(L, E, S, budget=(2, 1))
+    half_life = 2.0
+    log2_decay = np.float32(-1.0) / np.float32(np.float32(half_life) * np.float32(L))
+    for step in range(12):
+        for layer in range(L):
+            st["budget"][0] = 2  # the step's reservations
+            ids = rng.choice(E, k, replace=False)
+            before = {key: dict(table=int(st["table"][key])) for key in range(L * E)}
+            owner_before = st["owner"].copy()
+            pending_before = st["pending"].copy()
+            plan = slots.resolve_ref(ids, layer, L, E, half_life, cpu, 3.0, st, 0.5)
+            now = int(st["step"][0])
+            assert now == int(st["clock"][0]) * L + layer
+            check_consistent(st)
+            for e, (slot, code) in enumerate(plan):
+                key = layer * E + int(ids[e])
+                if before[key]["table"] >= 0:  # cached: keeps its slot
+                    assert code == 0 and slot == before[key]["table"]
+                assert st["at"][key] == now
+            # victims: slots whose owner changed were free, or held an expert neither used now nor pending
+            for s in range(S):
+                if owner_before[s] != st["owner"][s] and owner_before[s] >= 0:
+                    assert not pending_before[s]
+                    assert st["table"][owner_before[s]] == -1
+            # brute force: every slot taken from an earlier owner was a minimum of the decayed counts among the
+            # candidates at that time (free slots count -1); checked for the first fill of the call
+            fills = [(e, int(s)) for e, (s, c) in enumerate(plan) if c in (1, 2) and s >= 0
+                     and before[layer * E + int(ids[e])]["table"] < 0]
+            if fills:
+                _, s0 = fills[0]
+                vals = []
+                for s in range(S):
+                    key = owner_before[s]
+                    if key < 0:
+                        vals.append(-1.0)
+                    elif pending_before[s] or (st["at"][key] == now and st["owner"][s] == key):
+                        vals.append(np.inf)
+                    else:
+                        vals.append(float(slots.decayed(st["score"][key], st["at"][key], now, log2_decay)))
+                assert vals[s0] == min(vals) and s0 == int(np.argmin(vals))
+            # settle the host's copies: pending slots become cached (SlotPool.settle)
+            for s in range(S):
+                if st["pending"][s]:
+                    st["pending"][s] = 0
+                    st["table"][st["owner"][s]] = s
+
+
+def test_split_between_gpu_and_cpu():
+    """Four missed experts, share 0.5: the GPU takes the int(4 * 0.5 + 0.25) = 2 most used; of the CPU's, the ones used
+    admit times or more reserve a slot while the budget lasts (here 1), the rest get none."""
+    L, E, S = 1, 8, 8
+    st = slots.new_state(L, E, S, budget=(1, 4))
+    st["score"][:4] = [5.0, 4.0, 3.0, 2.5]
+    st["at"][:4] = 0
+    st["clock"][0] = 0  # this call makes the pass 1, step 1: one step of decay
+    plan = slots.resolve_ref([3, 2, 1, 0], 0, L, E, 1e9, 1, 2.0, st, 0.5)
+    codes = {int(e): tuple(p) for e, p in zip([3, 2, 1, 0], plan)}
+    assert codes[0][1] == 1 and codes[1][1] == 1          # the two most used: GPU fills
+    assert codes[2][1] == 2 and codes[2][0] >= 0          # next: CPU, reserves (uses 4 >= admit, budget 1)
+    assert codes[3] == (-1, 2)                           # budget spent: CPU without a slot
+    assert st["budget"][0] == 0 and list(st["reads"]) == [0, 2, 2]
+    assert st["table"][2] == -2 - codes[2][0] and st["pending"][codes[2][0]] == 1
+
+
+def test_await_ref():
+    plan_cpu = np.array([[0, 0], [-1, 2]])
+    plan_gpu = np.array([[0, 0], [1, 1]])
+    res = np.array([0x3F80, 0xC000], np.uint16)  # 1.0, -2.0
+    out, took = slots.await_ref(plan_cpu, 7, 7, res)
+    assert list(out[0]) == [1.0, -2.0] and took == 0
+    out, took = slots.await_ref(plan_cpu, 6, 7, res)
+    assert np.all(out == 0) and took == 1
+    out, took = slots.await_ref(plan_gpu, 6, 7, res)
+    assert np.all(out == 0) and took == 0
