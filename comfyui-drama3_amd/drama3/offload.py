@@ -15,6 +15,7 @@ comfy's QuantizedTensor (comfy.quant_ops) is used when it is importable; without
 any object with the same `_qdata`, `_params`, `_layout_cls` attributes.
 """
 import dataclasses
+import time
 
 import torch
 import torch.nn as nn
@@ -22,8 +23,12 @@ import torch.nn as nn
 from . import kernels
 
 FP8_BLOCK = 128             # offload.py:36
+CPU_EXPERT_US, CPU_ROW_US = 60, 13   # offload.py:37-38: the CPU's cost of one int8 expert, first estimate
+PCIE_BYTES_PER_US = 12e3    # offload.py:39
 HALF_LIFE = 128             # offload.py:44
 MAX_EXPERTS_PER_ROW = 8     # offload.py:46
+RESERVE_START, RESERVE_MIN, RESERVE_MAX = 32, 8, 256   # offload.py:49
+ADMIT = 6.0                 # offload.py:51
 AWAIT_US = 5000             # offload.py:53
 
 try:  # optional: ComfyUI's quantized tensor type
@@ -277,6 +282,209 @@ class FP8HostBank(HostBank):
 
     def weight(self, fields, device):
         return dequantize_fp8(fields["weight"].view(torch.float8_e4m3fn), fields["scale"], torch.bfloat16)
+
+
+class SlotPool:
+    """offload.py:560-700, the device part: `count` expert slots in HBM filled from host banks, the least used expert
+    out first. table [L * E] maps a key (layer * E + expert) to its slot, -1, or -2 - slot while the host copies it in
+    (pending); owner [count] maps a slot to its key. The state lives on the device, where kernels.resolve keeps it
+    (`device_state`); `promote` copies the slots decode steps reserved for the CPU's experts between steps."""
+
+    def __init__(self, banks, count, device):
+        self.banks = banks
+        self.device = torch.device(device)
+        self.layers, self.num_experts = len(banks), banks[0][0].num_experts
+        self.rows = [{n: bank.rows(n) for n in bank.fields} for bank in banks[0]]
+        self.expert_bytes = sum(t[:bank.rows(n)].nbytes for bank in banks[0] for n, t in bank.fields.items())
+        self.count = max(8, min(self.layers * self.num_experts, int(count)))
+        self.fields = [{n: torch.zeros((self.count * bank.rows(n), *t.shape[1:]), dtype=t.dtype, device=self.device)
+                        for n, t in bank.fields.items()} for bank in banks[0]]
+        keys = self.layers * self.num_experts
+        dev = self.device
+        self.table = torch.full((keys,), -1, dtype=torch.int32, device=dev)
+        self.owner = torch.full((self.count,), -1, dtype=torch.int32, device=dev)
+        self.score = torch.zeros((keys,), dtype=torch.float32, device=dev)
+        self.at = torch.full((keys,), -1, dtype=torch.int32, device=dev)
+        self.pending = torch.zeros((self.count,), dtype=torch.int32, device=dev)
+        self.clock = torch.zeros((1,), dtype=torch.int32, device=dev)
+        self.reads = torch.zeros((3,), dtype=torch.int32, device=dev)
+        self.reserve = RESERVE_START
+        self.budget = torch.tensor(self._budget(), dtype=torch.int32, device=dev)
+        # a layer's step, whether the GPU took over the CPU's experts, a set flag, the GPU's share of missed experts
+        self.step, self.took_over, self.always = torch.tensor([[0], [0], [1]], dtype=torch.int32, device=dev)
+        self.share = torch.zeros((1,), dtype=torch.float32, device=dev)
+        self.reserved, self.copying = [], []
+        self.copy_stream = None
+
+    def device_state(self):
+        """(table, owner, score, at, pending, clock, budget, reads, step, share) for kernels.resolve."""
+        return (self.table, self.owner, self.score, self.at, self.pending, self.clock, self.budget, self.reads,
+                self.step, self.share)
+
+    def _budget(self):
+        """[slots a decode step may reserve, at most per layer] (offload.py:644-646)."""
+        return [self.reserve, max(1, -(-2 * self.reserve // self.layers))]
+
+    def _fill(self, slot, sources):
+        for fields, rows, source in zip(self.fields, self.rows, sources):
+            for name, target in fields.items():
+                target[slot * rows[name]:(slot + 1) * rows[name]].copy_(source[name], non_blocking=True)
+
+    def _map(self, pairs):
+        if pairs:
+            keys, slots = zip(*pairs)
+            keys = torch.tensor(keys, dtype=torch.long, device=self.device)
+            slots = torch.tensor(slots, dtype=torch.long, device=self.device)
+            self.table[keys] = slots.to(torch.int32)
+            self.pending[slots] = 0
+
+    def promote(self):
+        """offload.py:624-642: map the slots whose copies landed, copy the experts reserved since the last call into
+        theirs on a copy stream, and let the next step reserve as many as the copies kept up with."""
+        landed = []
+        while self.copying and self.copying[0][0].query():
+            landed += self.copying.pop(0)[1]
+        self._map(landed)
+        lagging = bool(self.copying)
+        if self.reserved:
+            if self.copy_stream is None:
+                self.copy_stream = torch.cuda.Stream(self.device)
+            self.copy_stream.wait_stream(torch.cuda.current_stream(self.device))
+            with torch.cuda.stream(self.copy_stream):
+                for layer, expert, slot in self.reserved:
+                    self._fill(slot, [bank.take(bank.fields, expert, expert + 1) for bank in self.banks[layer]])
+                event = torch.cuda.Event()
+                event.record()
+            self.copying.append((event, [(layer * self.num_experts + expert, slot)
+                                         for layer, expert, slot in self.reserved]))
+            self.reserved = []
+        self.reserve = max(RESERVE_MIN, self.reserve * 3 // 4) if lagging else min(RESERVE_MAX, self.reserve * 5 // 4 + 1)
+        self.budget.copy_(torch.tensor(self._budget(), dtype=torch.int32), non_blocking=True)
+
+    def settle(self):
+        """Every reserved slot copied in and mapped."""
+        self.promote()
+        if self.copy_stream is not None:
+            self.copy_stream.synchronize()
+        self._map([pair for _, pairs in self.copying for pair in pairs])
+        self.copying = []
+
+
+class CpuSide:
+    """offload.py:276-299: where a decode step's layers hand experts to the CPU. A layer copies its plan, routing,
+    rotated row and step here (pinned host memory) and records posted[layer], then waits on the device
+    (kernels.await_cpu) for flag[layer] to reach that step; the host (HostExperts.after_layer) runs the experts and
+    writes result[layer], then the flag."""
+
+    def __init__(self, layers, k, hidden):
+        self.plan = torch.empty((layers, k, 2), dtype=torch.int32, pin_memory=True)
+        self.ids = torch.empty((layers, k), dtype=torch.long, pin_memory=True)
+        self.weights = torch.empty((layers, k), dtype=torch.float32, pin_memory=True)
+        self.rows = torch.empty((layers, 1, hidden), dtype=torch.bfloat16, pin_memory=True)
+        self.step = torch.zeros((layers,), dtype=torch.int32, pin_memory=True)
+        self.flag = torch.zeros((layers,), dtype=torch.int32, pin_memory=True)
+        self.result = torch.empty((layers, hidden), dtype=torch.bfloat16, pin_memory=True)
+        self.posted = [torch.cuda.Event() for _ in range(layers)]
+
+    def post(self, layer, plan, ids, weights, rows, step):
+        for target, source in ((self.plan[layer], plan), (self.ids[layer], ids), (self.weights[layer], weights),
+                               (self.rows[layer], rows), (self.step[layer:layer + 1], step)):
+            target.copy_(source, non_blocking=True)
+        self.posted[layer].record()
+
+    def wait(self, layer, plan, step, took_over):
+        return kernels.await_cpu(plan, self.flag[layer:layer + 1], step, self.result[layer], AWAIT_US, took_over)
+
+
+class HostExperts:
+    """The host-offload option (offload.py:302-452, ExpertStore's decode): every layer's banks in pinned host memory,
+    a SlotPool of `slots` experts in HBM. A decode row resolves its experts on the device (kernels.resolve), the GEMVs
+    read cached ones from their slots and missed ones straight from host memory, filling their slots on the way; with
+    `cpu_side` (int8 banks) the CPU runs part of the missed experts meanwhile (`after_layer` on the host, bounded by
+    kernels.await_cpu on the device). Nothing on the device waits on the host beyond AWAIT_US."""
+
+    def __init__(self, kind, layer_banks, num_experts, slots, device, codebooks=None, cpu_side=False, pin=True):
+        self.kind = kind
+        if kind == "fp8":
+            self.banks = [tuple(_FieldBank(num_experts, "fp8", f, pin) for f in banks) for banks in layer_banks]
+        else:
+            self.banks = [tuple(QuantHostBank(num_experts, kind, f, pin) for f in banks) for banks in layer_banks]
+        self.codebooks = [tuple(None if c is None else c.to(device) for c in cb) for cb in codebooks] \
+            if codebooks is not None else [(None, None)] * len(self.banks)
+        self.cache = SlotPool(self.banks, slots, device)
+        self.cpu_side = None
+        if cpu_side:
+            if kind != "int8":
+                raise ValueError("the CPU side runs int8 experts (torch._weight_int8pack_mm)")
+            hidden = self.banks[0][0].fields["_qdata"].shape[1]
+            self.cpu_side = CpuSide(len(self.banks), MAX_EXPERTS_PER_ROW, hidden)
+        self.rotation = hadamard(256)
+        self.cpu_expert_us = CPU_EXPERT_US + CPU_ROW_US
+
+    def between_steps(self):
+        """offload.py:386-391: copy the experts the CPU ran into their reserved slots; give the GPU the share of
+        missed experts that lets both sides finish together."""
+        self.cache.promote()
+        pcie = self.cache.expert_bytes / PCIE_BYTES_PER_US
+        self.cache.share.fill_(self.cpu_expert_us / (self.cpu_expert_us + pcie))
+
+    def decode(self, layer, x, ids, weights):
+        """offload.py:403-432: one row x [1, H] through its experts `ids` [k]: [1, H] in x's dtype."""
+        gate_up, down = self.banks[layer]
+        cache, side = self.cache, self.cpu_side
+        plan = kernels.resolve(ids, layer, len(self.banks), gate_up.num_experts, HALF_LIFE, side is not None, ADMIT,
+                               *cache.device_state())
+        slots_gate_up, slots_down = cache.fields
+        weights = weights.float()
+        if self.kind == "fp8":
+            gate, up = kernels.gemv_fp8(x.float(), ids, plan, slots_gate_up, gate_up.fields,
+                                        gate_up.rows("weight")).chunk(2, dim=-1)
+            out = kernels.gemv_fp8(nn.functional.silu(gate) * up, ids, plan, slots_down, down.fields,
+                                   down.rows("weight"))
+            return kernels.weighted_sum(out, weights)
+        cb_gu, cb_dn = self.codebooks[layer]
+
+        def experts(late):
+            hidden = quantized_gemv(self.kind, rotated, ids, plan, cache.took_over, late, slots_gate_up,
+                                    gate_up.fields, gate_up.rows("_qdata"), cb_gu)
+            hidden = kernels.rotate(hidden, cache.took_over if late else cache.always, swiglu=True)
+            return quantized_gemv(self.kind, hidden, ids, plan, cache.took_over, late, slots_down, down.fields,
+                                  down.rows("_qdata"), cb_dn)
+
+        rotated = kernels.rotate(x, cache.always)
+        if side is None:
+            return kernels.weighted_sum(experts(False), weights)
+        side.post(layer, plan, ids, weights, rotated.to(torch.bfloat16), cache.step)
+        out = weights @ experts(False) + side.wait(layer, plan, cache.step, cache.took_over)
+        return (out + weights @ experts(True)).to(x.dtype)
+
+    def after_layer(self, layer):
+        """offload.py:434-452: the host's part of decode layer `layer`, already launched: wait for its routing, run
+        the experts it left to the CPU, and hand the result to the layer."""
+        side = self.cpu_side
+        side.posted[layer].synchronize()
+        plan = side.plan[layer].tolist()
+        on_cpu = [e for e, (_, code) in enumerate(plan) if code == 2]
+        if not on_cpu:
+            return
+        ids = side.ids[layer].tolist()
+        for e in on_cpu:
+            if plan[e][0] >= 0:
+                self.cache.reserved.append((layer, ids[e], plan[e][0]))
+        started = time.perf_counter()
+        out = experts_on_cpu(self.banks[layer], [ids[e] for e in on_cpu], [1] * len(on_cpu),
+                             side.rows[layer].expand(len(on_cpu), -1), self.rotation)
+        side.result[layer].copy_(side.weights[layer, on_cpu] @ out)
+        side.flag[layer] = int(side.step[layer])
+        self.cpu_expert_us = 0.9 * self.cpu_expert_us + 0.1 * 1e6 * (time.perf_counter() - started) / len(on_cpu)
+
+
+class _FieldBank(HostBank):
+    """A host bank given as its field dict (FP8 {"weight", "scale"} with block scales)."""
+
+    def __init__(self, num_experts, kind, fields, pin):
+        super().__init__(num_experts, fields, pin)
+        self.kernel = kind
 
 
 class ExpertTable:
