@@ -11,6 +11,8 @@ Other workloads of the same layer shape:
     --format w6a8 --routing zipf                W6A8 over 48 layers, experts per layer drawn from Zipf(1.1)
     --mode prefill                              FP8 experts, 256 rows at once, Zipf(1.1) routing: the grouped
                                                 MFMA path (d3_moe_a8_prefill), 16 layers chained
+    --mode resident --format fp8                the reference's own layouts and float activations (kernels.route +
+                                                offload.resident_decode), the drop-in path for converted files
 
     python bench.py [--steps K] [--warmup W] [--mode decode|prefill] [--format int8|w4a8|w6a8|fp8] [--rows M]
                     [--layers L] [--routing normal|zipf] [--no-cpu-baseline] [--calibrate-copy]
@@ -251,12 +253,89 @@ def run_prefill(args, fmt, device):
     return ms, step_bytes * args.steps, args.steps * L, args.steps * T, config, "d3_moe_a8_prefill (7 launches)", cpu
 
 
+def make_reference_banks(fmt_name, layers, device, seed=3):
+    """Banks in the reference's own layouts (offload.py:72-90, 264-273) with random codes and scales of the right
+    shapes and ranges: int8 rows with float32 row scales, FP8 rows with 128 x 128 float32 block scales, W4A8 / W6A8
+    code rows with e4m3 group-16 scales, float32 channel scales and a codebook at 4 bits."""
+    gen = torch.Generator(device=device).manual_seed(seed)
+    kind = {"int8": "int8", "fp8": "fp8", "w4a8": "w4", "w6a8": "w6"}[fmt_name]
+    out = []
+    for _ in range(layers):
+        banks = []
+        for n, k in ((2 * I, H), (H, I)):
+            if kind == "int8":
+                f = {"_qdata": torch.randint(-127, 128, (E * n, k), generator=gen, device=device, dtype=torch.int8),
+                     "scale": torch.rand((E * n,), generator=gen, device=device) * 1e-3}
+            elif kind == "fp8":
+                w = torch.randint(0, 0x7E, (E * n, k), generator=gen, device=device, dtype=torch.uint8)
+                w |= torch.randint(0, 2, (E * n, k), generator=gen, device=device, dtype=torch.uint8) << 7
+                f = {"weight": w, "scale": torch.rand((E * n // 128, k // 128), generator=gen, device=device) * 1e-2}
+            else:
+                bits = int(kind[1])
+                f = {"_qdata": torch.randint(0, 256, (E * n, k * bits // 8), generator=gen, device=device,
+                                             dtype=torch.uint8),
+                     "scale": torch.randint(0x28, 0x38, (E * n, k // 16), generator=gen, device=device,
+                                            dtype=torch.uint8),
+                     "s_channel": torch.rand((E * n,), generator=gen, device=device) * 1e-3}
+            banks.append(f)
+        cb = (torch.linspace(-8, 7, 16, device=device),) * 2 if kind == "w4" else (None, None)
+        out.append((kind, tuple(banks), cb))
+    return out
+
+
+def bank_bytes(fields):
+    return sum(t.numel() * t.element_size() for t in fields.values()) // E
+
+
+def run_resident(args, fmt, device):
+    """The reference-format decode path (kernels.route + offload.resident_decode: rotate, gemv, rotate(SwiGLU),
+    gemv, weighted sum; FP8 without the rotations), one row, layers chained in HIP graphs."""
+    from drama3 import kernels, offload
+    L = args.layers
+    log(f"building {L} layers of {args.format} experts in the reference's layouts")
+    layers = make_reference_banks(args.format, L, device)
+    logits = make_logits(args.routing, GRAPH_TOKENS, L, 1, device)
+    gen = torch.Generator(device=device).manual_seed(2)
+    x0 = torch.randn((GRAPH_TOKENS, 1, H), generator=gen, device=device).to(torch.bfloat16)
+    rows = (2 * I, H)
+
+    def layer_step(x, lg, layer):
+        kind, banks, cbs = layers[layer]
+        ids, w = kernels.route(lg, TOPK)
+        return offload.resident_decode(x, ids[0], w[0], banks, rows, kind, cbs)
+
+    per_expert = sum(bank_bytes(f) for f in layers[0][1])
+    layer_bytes = TOPK * per_expert + 2 * H * 2 + E * 2
+    stream = torch.cuda.Stream(device)
+    stream.wait_stream(torch.cuda.current_stream(device))
+    graphs = []
+    with torch.cuda.stream(stream):
+        x = x0[0]
+        for layer in range(L):  # constants and allocator pools before capture
+            x = layer_step(x, logits[0, layer], layer)
+        bufs = [x0[t].clone() for t in range(GRAPH_TOKENS)]
+        for t in range(GRAPH_TOKENS):
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=stream):
+                x = bufs[t]
+                for layer in range(L):
+                    x = layer_step(x, logits[t, layer], layer)
+            graphs.append(g)
+        ms = timed_replays(graphs, stream, args.steps, args.warmup)
+    torch.cuda.synchronize()
+    config = {"workload": f"routed-expert MoE layer in the reference's {args.format} layout (float activations, "
+                          f"route + resident_decode), decode M=1, hidden {H}, FFN {I}, {E} experts top-{TOPK}, "
+                          f"{L} layers chained per token", "rows": 1, "layers": L, "unique_experts_per_launch": TOPK}
+    return (ms, layer_bytes * L * args.steps, args.steps * L, args.steps, config,
+            "route + resident_decode (3 launches: route, gate_up, down)", None)
+
+
 def main():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=None)
     p.add_argument("--warmup", type=int, default=None)
-    p.add_argument("--mode", default="decode", choices=["decode", "prefill"])
+    p.add_argument("--mode", default="decode", choices=["decode", "prefill", "resident"])
     p.add_argument("--format", default=None, choices=sorted(FORMATS))
     p.add_argument("--rows", type=int, default=None)
     p.add_argument("--layers", type=int, default=None)
@@ -282,7 +361,7 @@ def main():
         calibrate_copy(device)
         return
 
-    run = run_prefill if prefill else run_decode
+    run = run_prefill if prefill else run_resident if args.mode == "resident" else run_decode
     ms, total_bytes, launches, tokens, config, kernel, cpu = run(args, fmt, device)
     gbs = total_bytes / (ms * 1e-3) / 1e9
     launch_us = ms * 1e3 / launches

@@ -31,16 +31,19 @@ template <int CTRL> D3_INLINE float dpp_f32(float v) {
 // ---------------------------------------------------------------------------------------------------------- route
 // kernels.py:39-67: the k (<= 32) largest of n (<= 1024) bf16 logits, descending, ties to the lower index; weights
 // softmax over those k, rounded to bf16. One wave per row.
+template <int KPL>  // logits per lane: n <= 64 * KPL
 __global__ void __launch_bounds__(256) route_kernel(const uint16_t* logits, int rows, int n, int k, int64_t* ids,
                                                     float* weights) {
   const int lane = threadIdx.x & 63, row = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= rows) return;
   const uint16_t* lg = logits + (size_t)row * n;
-  uint32_t key[16];
+  uint32_t raw[KPL], key[KPL];
 #pragma unroll
-  for (int j = 0; j < 16; j++) {
+  for (int j = 0; j < KPL; j++) raw[j] = lg[min(lane + 64 * j, n - 1)];  // branch-free: all loads in flight together
+#pragma unroll
+  for (int j = 0; j < KPL; j++) {
     const int e = lane + 64 * j;
-    key[j] = e < n ? route_key(lg[e], e) : 0u;
+    key[j] = e < n ? route_key(raw[j], e) : 0u;
   }
   float top[32];
   int id[32];
@@ -51,10 +54,10 @@ __global__ void __launch_bounds__(256) route_kernel(const uint16_t* logits, int 
     if (r < k) {
       uint32_t m = key[0];
 #pragma unroll
-      for (int j = 1; j < 16; j++) m = max(m, key[j]);
+      for (int j = 1; j < KPL; j++) m = max(m, key[j]);
       m = wave_max_u32(m);
 #pragma unroll
-      for (int j = 0; j < 16; j++) key[j] = key[j] == m ? 0u : key[j];
+      for (int j = 0; j < KPL; j++) key[j] = key[j] == m ? 0u : key[j];
       id[r] = route_key_index(m);
       top[r] = route_key_value(m);
     }
@@ -84,6 +87,31 @@ __global__ void __launch_bounds__(256) weighted_sum_kernel(const float* parts, c
 }
 
 // -------------------------------------------------------------------------------------------------------- rotate
+// H256 / 16 of one 256-column chunk held by a wave, lane l holding columns 4l .. 4l + 3 (all 64 lanes active).
+D3_INLINE void fwht256(float* v) {
+  // digit 0: the lane's own four columns
+  {
+    const float s = (v[0] + v[1]) + (v[2] + v[3]);
+    const float y0 = s - 2.0f * v[3], y1 = s - 2.0f * v[2], y2 = s - 2.0f * v[1], y3 = s - 2.0f * v[0];
+    v[0] = y0; v[1] = y1; v[2] = y2; v[3] = y3;
+  }
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    // digit 1: the four lanes of a quad; mirrored digit = lane ^ 3
+    float s = v[j] + dpp_f32<0xB1>(v[j]);
+    s = s + dpp_f32<0x4E>(s);
+    v[j] = s - 2.0f * dpp_f32<0x1B>(v[j]);
+    // digit 2: the four quads of a row (rotate by 8 and 4); mirrored digit = lane ^ 12 (row mirror, then quad mirror)
+    s = v[j] + dpp_f32<0x128>(v[j]);
+    s = s + dpp_f32<0x124>(s);
+    v[j] = s - 2.0f * dpp_f32<0x1B>(dpp_f32<0x140>(v[j]));
+    // digit 3: the four rows of the wave; mirrored digit = lane ^ 48
+    s = v[j] + __shfl_xor(v[j], 16);
+    s = s + __shfl_xor(s, 32);
+    v[j] = (s - 2.0f * __shfl_xor(v[j], 48)) * 0.0625f;
+  }
+}
+
 // kernels.py:222-258: per row, optional SwiGLU (float [rows, 2K] gate | up), then H256 on every 256 columns, / 16.
 // MODE 0: float rows, 1: bf16 rows, 2: SwiGLU. Does nothing unless only_if[0].
 template <int MODE>
@@ -107,27 +135,7 @@ __global__ void __launch_bounds__(256) rotate_kernel(const void* x, int K, float
 #pragma unroll
       for (int j = 0; j < 4; j++) v[j] = gg[j] / (1.0f + __expf(-gg[j])) * uu[j];
     }
-    // digit 0: the lane's own four columns
-    {
-      const float s = (v[0] + v[1]) + (v[2] + v[3]);
-      const float y0 = s - 2.0f * v[3], y1 = s - 2.0f * v[2], y2 = s - 2.0f * v[1], y3 = s - 2.0f * v[0];
-      v[0] = y0; v[1] = y1; v[2] = y2; v[3] = y3;
-    }
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-      // digit 1: the four lanes of a quad; mirrored digit = lane ^ 3
-      float s = v[j] + dpp_f32<0xB1>(v[j]);
-      s = s + dpp_f32<0x4E>(s);
-      v[j] = s - 2.0f * dpp_f32<0x1B>(v[j]);
-      // digit 2: the four quads of a row (rotate by 8 and 4); mirrored digit = lane ^ 12 (row mirror, then quad mirror)
-      s = v[j] + dpp_f32<0x128>(v[j]);
-      s = s + dpp_f32<0x124>(s);
-      v[j] = s - 2.0f * dpp_f32<0x1B>(dpp_f32<0x140>(v[j]));
-      // digit 3: the four rows of the wave; mirrored digit = lane ^ 48
-      s = v[j] + __shfl_xor(v[j], 16);
-      s = s + __shfl_xor(s, 32);
-      v[j] = (s - 2.0f * __shfl_xor(v[j], 48)) * 0.0625f;
-    }
+    fwht256(v);
     *(f32x4*)(out + (size_t)row * K + c0) = f32x4{v[0], v[1], v[2], v[3]};
   }
 }
@@ -462,6 +470,178 @@ __global__ void __launch_bounds__(256) grouped_kernel(const float* x, const int*
   }
 }
 
+// ------------------------------------------------------------------------------------ fused resident decode
+// offload.py:108-123 resident_decode in two launches instead of five (rotate, gemv, rotate(SwiGLU), gemv,
+// weighted_sum): banks held whole on the device (expert e in slot e), KIND 0 int8 (ConvRot), 1 fp8 (128 x 128 block
+// scales), 4 / 6 codes (ConvRot). The same arithmetic per row as the separate kernels; the rotations move into the
+// products' prologues (every workgroup rotates the row it needs, from L2, which costs far less than a launch).
+//
+// gate_up: grid (N / 16, k), workgroup (rows n0 .. n0 + 15, expert j): its rows' bytes are loaded first, then x
+// (bf16) goes into LDS as float, rotated per 256 columns unless fp8, then 4 rows per wave: gu[j, n] = row . x (* row
+// scale / channel scale; fp8 block scales folded into the activation slice).
+// One lane's share of a row for the row-slice products: int8 / fp8 bytes (CPL per lane), or for codes the lane's
+// 16-column groups (GPL of them: nibble words, 2-bit plane word, e4m3 scale byte). Loaded before anything the
+// products wait for, so the weight stream starts at once.
+template <int KIND, int K> struct RowBytes {
+  static constexpr int CPL = K / 64, G = K / 16, GPL = (G + 63) / 64;
+  uint32_t wd[KIND <= 1 ? CPL / 4 : 1];
+  i32x2 lw[KIND <= 1 ? 1 : GPL];
+  uint32_t high[KIND <= 1 ? 1 : GPL];
+  uint32_t sb[KIND <= 1 ? 1 : GPL];
+};
+
+template <int KIND, int K>
+D3_INLINE void load_row(RowBytes<KIND, K>& rb, const uint8_t* bw, const uint8_t* bs, size_t row, int lane) {
+  using R = RowBytes<KIND, K>;
+  if constexpr (KIND <= 1) {
+    load_words<R::CPL>(bw + row * K + lane * R::CPL, rb.wd);
+  } else {
+    constexpr int RB = K * KIND / 8;
+    const uint8_t* p = bw + row * RB;
+#pragma unroll
+    for (int i = 0; i < R::GPL; i++) {
+      // lanes past the row's groups read its last group (branch-free loads; row_dot skips them)
+      const int v = min(lane + 64 * i, R::G - 1);
+      rb.lw[i] = *(const i32x2*)(p + 8 * v);
+      rb.high[i] = KIND == 6 ? *(const uint32_t*)(p + K / 2 + 4 * v) : 0u;
+      rb.sb[i] = bs[row * R::G + v];
+    }
+  }
+}
+
+// row . xs (LDS, K floats) for a row loaded by load_row; fp8 block scales of the row's 128-row block in `sblock`.
+template <int KIND, int K>
+D3_INLINE float row_dot(const RowBytes<KIND, K>& rb, const float* xs, const float* sblock, const float* lut,
+                        int lane) {
+  using R = RowBytes<KIND, K>;
+  if constexpr (KIND <= 1) {
+    float xv[R::CPL];
+    const float xsum = load_slice<R::CPL>(xs, lane, xv);
+    if constexpr (KIND == 1) {
+#pragma unroll
+      for (int i = 0; i < R::CPL; i++) xv[i] *= sblock[(lane * R::CPL + i) / 128];
+      return dot_f8<R::CPL>(rb.wd, xv);
+    } else {
+      return dot_i8<R::CPL>(rb.wd, xv, xsum);
+    }
+  } else {
+    float acc = 0.0f;
+#pragma unroll
+    for (int i = 0; i < R::GPL; i++) {
+      const int v = lane + 64 * i;
+      if (v < R::G) {
+        float q[16];
+        decode_group<KIND>((uint32_t)rb.lw[i].x, (uint32_t)rb.lw[i].y, rb.high[i], rb.sb[i], lut, q);
+#pragma unroll
+        for (int t = 0; t < 16; t++) acc = fmaf(q[t], xs[16 * v + t], acc);
+      }
+    }
+    return acc;
+  }
+}
+
+// the row's scale applied after the sum: int8 row scale, codes channel scale, fp8 none (folded into x)
+template <int KIND> D3_INLINE float row_scale(const void* bs, const float* bc, size_t row) {
+  if constexpr (KIND == 0) return ((const float*)bs)[row];
+  else if constexpr (KIND == 1) return 1.0f;
+  else return bc[row];
+}
+
+template <int KIND, int K>
+__global__ void __launch_bounds__(256) resident_gu_kernel(const uint16_t* x, const int64_t* ids, const uint8_t* bw,
+                                                          const void* bs, const float* bc, const float* codebook,
+                                                          float* gu, int N) {
+  constexpr int RW = RPB / 4;  // rows per wave
+  __shared__ float xs[K];
+  __shared__ float lut[16];
+  const int j = blockIdx.y, lane = threadIdx.x & 63, w = threadIdx.x >> 6, n0 = blockIdx.x * RPB;
+  const size_t e = (size_t)ids[j];
+  RowBytes<KIND, K> rb[RW];
+  float sc[RW];
+#pragma unroll
+  for (int r = 0; r < RW; r++) {
+    const size_t row = e * N + n0 + w * RW + r;
+    load_row<KIND, K>(rb[r], bw, (const uint8_t*)bs, row, lane);
+    sc[r] = row_scale<KIND>(bs, bc, row);
+  }
+  for (int g = w; g < K / 256; g += 4) {
+    const int c0 = 256 * g + 4 * lane;
+    const i32x2 raw = *(const i32x2*)(x + c0);
+    float v[4] = {bf16_to_f32((uint32_t)raw.x & 0xFFFFu), bf16_to_f32((uint32_t)raw.x >> 16),
+                  bf16_to_f32((uint32_t)raw.y & 0xFFFFu), bf16_to_f32((uint32_t)raw.y >> 16)};
+    if constexpr (KIND != 1) fwht256(v);
+    *(f32x4*)(xs + c0) = f32x4{v[0], v[1], v[2], v[3]};
+  }
+  if (KIND == 4 && threadIdx.x < 16) lut[threadIdx.x] = codebook[threadIdx.x];
+  __syncthreads();
+  const float* sblock = KIND == 1 ? (const float*)bs + ((e * N + n0) / 128) * (K / 128) : nullptr;
+#pragma unroll
+  for (int r = 0; r < RW; r++) {
+    const float acc = wave_sum_f32(row_dot<KIND, K>(rb[r], xs, sblock, lut, lane));
+    if (lane == 0) gu[(size_t)j * N + n0 + w * RW + r] = acc * sc[r];
+  }
+}
+
+// down: grid (H / 8), workgroup (output rows m0 .. m0 + 7) for all k experts, so the routing-weighted sum stays in the
+// workgroup. The rows' bytes for every expert are loaded first; then each expert's hidden row h_j = SiLU(gate) * up
+// of gu[j] (rotated per 256 unless fp8) goes into LDS, and 2 rows per wave give out[m] = bf16(sum_j w_j *
+// (row . h_j) * scale), experts in order as weighted_sum sums them.
+constexpr int DN_ROWS = 8, MAX_K_RES = 8;
+template <int KIND, int K>
+__global__ void __launch_bounds__(256) resident_dn_kernel(const float* gu, const int64_t* ids, const float* wts, int k,
+                                                          const uint8_t* bw, const void* bs, const float* bc,
+                                                          const float* codebook, uint16_t* out, int H) {
+  constexpr int RW = DN_ROWS / 4;
+  __shared__ float hs[MAX_K_RES][K];
+  __shared__ float lut[16];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, m0 = blockIdx.x * DN_ROWS;
+  RowBytes<KIND, K> rb[RW][MAX_K_RES];
+  float sc[RW][MAX_K_RES];
+  size_t ex[MAX_K_RES];
+  // every expert slot up to MAX_K_RES loads a valid row (the last expert's again past k), without branches, so all
+  // of a wave's loads are in flight together; the products skip the slots past k
+#pragma unroll
+  for (int j = 0; j < MAX_K_RES; j++) ex[j] = (size_t)ids[min(j, k - 1)];
+#pragma unroll
+  for (int r = 0; r < RW; r++)
+#pragma unroll
+    for (int j = 0; j < MAX_K_RES; j++) {
+      const size_t row = ex[j] * H + m0 + w * RW + r;
+      load_row<KIND, K>(rb[r][j], bw, (const uint8_t*)bs, row, lane);
+      sc[r][j] = row_scale<KIND>(bs, bc, row);
+    }
+  for (int c = w; c < k * (K / 256); c += 4) {
+    const int jj = c / (K / 256), c0 = 256 * (c % (K / 256)) + 4 * lane;
+    const f32x4 g = *(const f32x4*)(gu + (size_t)jj * 2 * K + c0), u = *(const f32x4*)(gu + (size_t)jj * 2 * K + K + c0);
+    const float gg[4] = {g.x, g.y, g.z, g.w}, uu[4] = {u.x, u.y, u.z, u.w};
+    float v[4];
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+      // fp8: torch's silu as offload.py:115 applies it; the others: rotate_rows' SwiGLU (kernels.py:236)
+      const float sig = KIND == 1 ? 1.0f + expf(-gg[t]) : 1.0f + __expf(-gg[t]);
+      v[t] = gg[t] / sig * uu[t];
+    }
+    if constexpr (KIND != 1) fwht256(v);
+    *(f32x4*)(&hs[jj][c0]) = f32x4{v[0], v[1], v[2], v[3]};
+  }
+  if (KIND == 4 && threadIdx.x < 16) lut[threadIdx.x] = codebook[threadIdx.x];
+  __syncthreads();
+#pragma unroll
+  for (int r = 0; r < RW; r++) {
+    const int m = m0 + w * RW + r;
+    float total = 0.0f;
+#pragma unroll
+    for (int j = 0; j < MAX_K_RES; j++) {
+      if (j < k) {
+        const float* sblock = KIND == 1 ? (const float*)bs + ((ex[j] * H + m) / 128) * (K / 128) : nullptr;
+        const float y = wave_sum_f32(row_dot<KIND, K>(rb[r][j], hs[j], sblock, lut, lane)) * sc[r][j];
+        total = fmaf(y, wts[j], total);
+      }
+    }
+    if (lane == 0) out[m] = (uint16_t)f32_to_bf16(total);
+  }
+}
+
 // Check of the decode above on its own: one thread per (row, 16-column group) writes the int8-grid values.
 template <int BITS>
 __global__ void __launch_bounds__(256) decode_codes_kernel(const uint8_t* rows, const uint8_t* scales,
@@ -514,8 +694,14 @@ extern "C" {
 int d3_route(const void* logits, int32_t rows, int32_t n, int32_t k, int64_t* ids, float* weights, void* stream) {
   if (!logits || !ids || !weights) return fail("d3_route: null pointer");
   if (rows < 1 || n < 1 || n > 1024 || k < 1 || k > 32 || k > n) return fail("d3_route: n <= 1024, 1 <= k <= min(32, n)");
-  hipLaunchKernelGGL(route_kernel, dim3((rows + 3) / 4), dim3(256), 0, (hipStream_t)stream, (const uint16_t*)logits,
-                     rows, n, k, ids, weights);
+  const dim3 grid((rows + 3) / 4);
+  const hipStream_t s = (hipStream_t)stream;
+  const uint16_t* lg = (const uint16_t*)logits;
+  if (n <= 64) hipLaunchKernelGGL(route_kernel<1>, grid, dim3(256), 0, s, lg, rows, n, k, ids, weights);
+  else if (n <= 128) hipLaunchKernelGGL(route_kernel<2>, grid, dim3(256), 0, s, lg, rows, n, k, ids, weights);
+  else if (n <= 256) hipLaunchKernelGGL(route_kernel<4>, grid, dim3(256), 0, s, lg, rows, n, k, ids, weights);
+  else if (n <= 512) hipLaunchKernelGGL(route_kernel<8>, grid, dim3(256), 0, s, lg, rows, n, k, ids, weights);
+  else hipLaunchKernelGGL(route_kernel<16>, grid, dim3(256), 0, s, lg, rows, n, k, ids, weights);
   return done("d3_route");
 }
 
@@ -607,6 +793,46 @@ int d3_grouped(int32_t kind, const float* x, const int32_t* groups, int32_t n_gr
     default: return fail("d3_grouped: kind 0, 1, 4 or 6");
   }
   return done("d3_grouped");
+}
+
+int d3_resident_decode(int32_t kind, const void* x, const int64_t* ids, const float* weights, int32_t k,
+                       const void* gu_w, const void* gu_s, const float* gu_c, const void* dn_w, const void* dn_s,
+                       const float* dn_c, const float* gu_codebook, const float* dn_codebook, float* gu, void* out,
+                       int32_t H, int32_t I, void* stream) {
+  if (!x || !ids || !weights || !gu_w || !gu_s || !dn_w || !dn_s || !gu || !out)
+    return fail("d3_resident_decode: null pointer");
+  if ((kind == 4 || kind == 6) && (!gu_c || !dn_c)) return fail("d3_resident_decode: codes need channel scales");
+  if (kind == 4 && (!gu_codebook || !dn_codebook)) return fail("d3_resident_decode: 4 bits need codebooks");
+  if (k < 1 || k > MAX_K_RES) return fail("d3_resident_decode: 1 <= k <= 8");
+  if ((H != 2048 && H != 1024) || (I != 512 && I != 768 && I != 1024) || H % DN_ROWS)
+    return fail("d3_resident_decode: H 1024 or 2048, I 512, 768 or 1024");
+  const hipStream_t s = (hipStream_t)stream;
+  const dim3 ggrid(2 * I / RPB, k), dgrid(H / DN_ROWS);
+  const uint16_t* xb = (const uint16_t*)x;
+  const uint8_t *gw = (const uint8_t*)gu_w, *dw = (const uint8_t*)dn_w;
+  uint16_t* o = (uint16_t*)out;
+#define D3_RES(KIND)                                                                                                 \
+  do {                                                                                                               \
+    if (H == 2048) hipLaunchKernelGGL((resident_gu_kernel<KIND, 2048>), ggrid, dim3(256), 0, s, xb, ids, gw, gu_s,   \
+                                      gu_c, gu_codebook, gu, 2 * I);                                                 \
+    else hipLaunchKernelGGL((resident_gu_kernel<KIND, 1024>), ggrid, dim3(256), 0, s, xb, ids, gw, gu_s, gu_c,       \
+                            gu_codebook, gu, 2 * I);                                                                 \
+    if (I == 768) hipLaunchKernelGGL((resident_dn_kernel<KIND, 768>), dgrid, dim3(256), 0, s, gu, ids, weights, k,  \
+                                     dw, dn_s, dn_c, dn_codebook, o, H);                                             \
+    else if (I == 512) hipLaunchKernelGGL((resident_dn_kernel<KIND, 512>), dgrid, dim3(256), 0, s, gu, ids, weights, \
+                                          k, dw, dn_s, dn_c, dn_codebook, o, H);                                     \
+    else hipLaunchKernelGGL((resident_dn_kernel<KIND, 1024>), dgrid, dim3(256), 0, s, gu, ids, weights, k, dw, dn_s, \
+                            dn_c, dn_codebook, o, H);                                                                \
+  } while (0)
+  switch (kind) {
+    case 0: D3_RES(0); break;
+    case 1: D3_RES(1); break;
+    case 4: D3_RES(4); break;
+    case 6: D3_RES(6); break;
+    default: return fail("d3_resident_decode: kind 0, 1, 4 or 6");
+  }
+#undef D3_RES
+  return done("d3_resident_decode");
 }
 
 int d3_decode_codes(int32_t bits, const void* rows, const void* scales, const float* codebook, int32_t R, int32_t K,

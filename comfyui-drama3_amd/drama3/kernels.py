@@ -164,6 +164,24 @@ def grouped_codes(x, groups, slot_fields, host_fields, codebook, bits, n):
     return _grouped(int(bits), x, groups, slot_fields, host_fields, codebook, n, "_qdata")
 
 
+_RESIDENT_KINDS = {"int8": (0, "_qdata"), "fp8": (1, "weight"), "w4": (4, "_qdata"), "w6": (6, "_qdata")}
+
+
+def resident_decode(x, ids, weights, banks, kind, codebooks, H, I):
+    """[1, H] bfloat16: offload.resident_decode's product in two launches (gate_up with x rotated in its prologue;
+    down with SiLU(gate) * up rotated in its prologue and the routing-weighted sum), banks resident, expert e in slot
+    e. weights float32 [k]."""
+    code, wkey = _RESIDENT_KINDS[kind]
+    gate_up, down = banks
+    k = ids.shape[0]
+    gu = torch.empty((k, 2 * I), dtype=torch.float32, device=x.device)
+    out = torch.empty((1, H), dtype=torch.bfloat16, device=x.device)
+    _call("d3_resident_decode", code, _p(x.contiguous()), _p(ids.contiguous()), _p(weights.contiguous()), k,
+          _p(gate_up[wkey]), _p(gate_up["scale"]), _p(gate_up.get("s_channel")), _p(down[wkey]), _p(down["scale"]),
+          _p(down.get("s_channel")), _p(codebooks[0]), _p(codebooks[1]), _p(gu), _p(out), H, I, _stream(x))
+    return out
+
+
 def decode_codes(qdata, scale, codebook, bits):
     """int8 [R, K]: W4A8 / W6A8 rows decoded to the int8 grid exactly as gemv_codes / grouped_codes decode them
     (a check of kernels.py:466-483's decode_codes; no counterpart in the reference's call surface)."""

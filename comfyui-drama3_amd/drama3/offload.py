@@ -118,10 +118,23 @@ def _constants(device):
     return _consts[key]
 
 
+_FUSED_KINDS = {"int8": 0, "fp8": 1, "w4": 4, "w6": 6}
+
+
 def resident_decode(x, ids, weights, banks, rows, kind, codebooks):
     """offload.py:108-123: one row x [1, H] through experts `ids` [k] of banks held whole on the GPU (expert e in
     slot e, `rows` per expert): fp8 -> gemv, SiLU(gate) * up, gemv; int8 / w4 / w6 -> rotate, gemv, rotate(swiglu),
-    gemv; then the routing-weighted sum, bf16 [1, H]. Nothing waits on the host."""
+    gemv; then the routing-weighted sum, bf16 [1, H]. Nothing waits on the host. Two launches
+    (kernels.resident_decode) where the shapes allow, else the reference's five."""
+    (gate_up, down), (gate_up_rows, down_rows) = banks, rows
+    H, I = down_rows, gate_up_rows // 2
+    if H in (1024, 2048) and I in (512, 768, 1024) and ids.shape[0] <= 8 and x.dtype == torch.bfloat16:
+        return kernels.resident_decode(x, ids, weights.float(), banks, kind, codebooks, H, I)
+    return resident_decode_unfused(x, ids, weights, banks, rows, kind, codebooks)
+
+
+def resident_decode_unfused(x, ids, weights, banks, rows, kind, codebooks):
+    """resident_decode as the reference launches it: rotate, gemv, rotate(SwiGLU), gemv, weighted_sum."""
     (gate_up, down), (gate_up_rows, down_rows) = banks, rows
     plan = torch.stack((ids.to(torch.int32), torch.zeros_like(ids, dtype=torch.int32)), dim=-1)
     if kind == "fp8":
