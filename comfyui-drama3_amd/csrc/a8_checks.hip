@@ -69,6 +69,19 @@ __global__ void unpack_kernel(const uint8_t* rows, int R, int K, int8_t* codes) 
 
 }  // namespace d3
 
+namespace d3 {
+// float -> e4m3fn codes, pairs per thread, by the hardware converter (1) or the format-definition one (0)
+// (both halves of the packed converter: a pair into the low half-word, the next pair into the high one)
+__global__ void __launch_bounds__(256) cvt_fp8_kernel(const float* in, int quads, uint8_t* out, int hardware) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i >= quads) return;
+  const float a = in[4 * i], b = in[4 * i + 1], c = in[4 * i + 2], d = in[4 * i + 3];
+  const uint32_t r = hardware ? f32x4_to_fp8x4(a, b, c, d)
+                              : (f32_to_fp8(a) | (f32_to_fp8(b) << 8) | (f32_to_fp8(c) << 16) | (f32_to_fp8(d) << 24));
+  for (int j = 0; j < 4; j++) out[4 * i + j] = (uint8_t)(r >> (8 * j));
+}
+}  // namespace d3
+
 extern "C" {
 
 int d3_gemv_a8_groups(int32_t format, const void* rows, int32_t R, int32_t K, const void* act, int32_t C, void* acc,
@@ -106,6 +119,16 @@ int d3_unpack_rows(int32_t format, const void* rows, int32_t R, int32_t K, void*
   }
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? 0 : hip_fail(e, "d3_unpack_rows launch");
+}
+
+int d3_cvt_fp8(const float* in, int32_t n, void* out, int32_t hardware, void* stream) {
+  using namespace d3;
+  if (!in || !out) return fail("d3_cvt_fp8: null pointer");
+  if (n < 4 || n % 4) return fail("d3_cvt_fp8: n a positive multiple of 4");
+  hipLaunchKernelGGL(cvt_fp8_kernel, dim3((n / 4 + 255) / 256), dim3(256), 0, (hipStream_t)stream, in, n / 4,
+                     (uint8_t*)out, hardware);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? 0 : hip_fail(e, "d3_cvt_fp8 launch");
 }
 
 }  // extern "C"

@@ -51,6 +51,17 @@ D3_INLINE uint32_t f32_to_fp8(float v) {
   return sign | code;
 }
 
+// two floats -> two float8 e4m3fn codes (byte 0: a, byte 1: b) through the hardware converter, to nearest and ties to
+// even; for |v| < 464 (the kernels feed it |v| <= 448) it agrees with f32_to_fp8 bit for bit.
+D3_INLINE uint32_t f32x2_to_fp8x2(float a, float b) {
+  return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false) & 0xFFFFu;
+}
+// four floats -> four codes, byte i from value i (the second pair goes to the high half-word)
+D3_INLINE uint32_t f32x4_to_fp8x4(float a, float b, float c, float d) {
+  const int lo = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+  return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(c, d, lo, true);
+}
+
 // ---------------------------------------------------------------------------------------------------------------
 // Wave64 reductions. DPP within each row of 16 lanes (quad swaps, half-row and row mirrors), then the four row results
 // read into scalars. Every lane gets the result; the order of combination is fixed, so float sums are deterministic.

@@ -123,16 +123,18 @@ template <int F> __host__ __device__ constexpr float act_qmax() { return F == FM
 
 // quantize 8 activations with `inv`, store them in the format's storage order
 template <int F> D3_INLINE void store_act8(uint8_t* dst, const float* v, float inv) {
+  if constexpr (F == FMT_F8) {  // |v * inv| <= 448 (inv = 448 / amax): the packed converter, exact on that range
+    const uint32_t lo = f32x4_to_fp8x4(v[0] * inv, v[1] * inv, v[2] * inv, v[3] * inv);
+    const uint32_t hi = f32x4_to_fp8x4(v[4] * inv, v[5] * inv, v[6] * inv, v[7] * inv);
+    *(i32x2*)dst = i32x2{(int)lo, (int)hi};
+    return;
+  }
   uint32_t b[8];
 #pragma unroll
   for (int i = 0; i < 8; i++) {
-    if constexpr (F == FMT_F8) {
-      b[i] = f32_to_fp8(v[i] * inv);
-    } else {
-      float r = rintf(v[i] * inv);
-      r = fminf(fmaxf(r, -127.0f), 127.0f);
-      b[i] = (uint32_t)((int)r) & 0xFFu;
-    }
+    float r = rintf(v[i] * inv);
+    r = fminf(fmaxf(r, -127.0f), 127.0f);
+    b[i] = (uint32_t)((int)r) & 0xFFu;
   }
   uint32_t lo, hi;
   if constexpr (F == FMT_W4) {

@@ -52,6 +52,7 @@ SIGNATURES = {
     "d3_moe_a8_prefill": (c_int32, [ctypes.POINTER(MoeA8PrefillDesc), c_void_p]),
     "d3_gemv_a8_groups": (c_int32, [c_int32, c_void_p, c_int32, c_int32, c_void_p, c_int32, c_void_p, c_void_p]),
     "d3_unpack_rows": (c_int32, [c_int32, c_void_p, c_int32, c_int32, c_void_p, c_void_p]),
+    "d3_cvt_fp8": (c_int32, [c_void_p, c_int32, c_void_p, c_int32, c_void_p]),
     "d3_route": (c_int32, [c_void_p, c_int32, c_int32, c_int32, c_void_p, c_void_p, c_void_p]),
     "d3_weighted_sum": (c_int32, [c_void_p, c_void_p, c_int32, c_int32, c_void_p, c_void_p]),
     "d3_rotate": (c_int32, [c_void_p, c_int32, c_int32, c_int32, c_void_p, c_void_p, c_void_p]),

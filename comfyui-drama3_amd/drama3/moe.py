@@ -159,6 +159,17 @@ def gemv_groups(bank_rows, fmt, cols, act):
     return acc
 
 
+def cvt_fp8(values, hardware=True):
+    """float32 -> float8 e4m3fn codes (uint8) by the converter the kernels quantize activations with (hardware) or by
+    the format's definition, round to nearest, ties to even."""
+    values = values.contiguous()
+    n = values.numel()
+    out = torch.empty(n, dtype=torch.uint8, device=values.device)
+    _lib.check(_lib.lib().d3_cvt_fp8(values.data_ptr(), n, out.data_ptr(), int(hardware),
+                                     _lib.stream_of(values.device)), "d3_cvt_fp8")
+    return out
+
+
 def unpack_rows(bank_rows, fmt, cols):
     """The int8 codes [R, cols] the fused layer's W4 / W6 unpacking feeds the MFMA."""
     R = bank_rows.shape[0]

@@ -107,6 +107,9 @@ int d3_moe_a8_prefill(const d3_moe_a8_prefill_desc* desc, void* stream);
 int d3_gemv_a8_groups(int32_t format, const void* rows, int32_t R, int32_t K, const void* act, int32_t C, void* acc,
                       void* stream);
 int d3_unpack_rows(int32_t format, const void* rows, int32_t R, int32_t K, void* codes, void* stream);
+/* d3_cvt_fp8: float -> float8 e4m3fn codes (n a multiple of 4), by the hardware converter the kernels quantize with (hardware 1)
+ * or the format-definition conversion (0); round to nearest, ties to even. */
+int d3_cvt_fp8(const float* in, int32_t n, void* out, int32_t hardware, void* stream);
 
 /* ---- The reference's own formats, one kernel per reference kernel (drama3/kernels.py SOURCE) -------------------
  * Float32 activations as in the reference. Slot-cache plans as there: plan [k, 2] int32 = (slot, code) per expert;

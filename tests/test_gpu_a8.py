@@ -12,7 +12,7 @@ import torch
 
 from drama3 import formats, moe
 from oracle import a8
-from oracle.numerics import bf16_bits_to_f32
+from oracle.numerics import bf16_bits_to_f32, e4m3_decode, e4m3_encode
 
 pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda:0")
@@ -29,6 +29,25 @@ def random_rows(fmt, R, K, gen):
     if fmt == formats.FMT_F8:
         raw = torch.where((raw & 0x7F) == 0x7F, torch.full_like(raw, 0x38), raw)  # no NaN codes
     return raw
+
+
+@pytest.mark.parametrize("hardware", [True, False])
+def test_fp8_conversion_bit_exact(hardware):
+    """Both float -> e4m3fn converters agree with the format's round-to-nearest-even definition on every e4m3 value,
+    every midpoint between neighbours (the ties), points just either side of them and a dense random sweep of
+    |v| < 464, both signs; the packed words keep their order (value i in byte i, both half-words)."""
+    grid = np.unique(np.abs(e4m3_decode(np.arange(127, dtype=np.uint8)).astype(np.float64)))
+    mids = (grid[1:] + grid[:-1]) / 2
+    pts = np.concatenate([grid, mids, np.nextafter(mids.astype(np.float32), np.float32(0)),
+                          np.nextafter(mids.astype(np.float32), np.float32(1e9)), [460.0, 463.9]]).astype(np.float32)
+    rng = np.random.default_rng(5)
+    sweep = (rng.uniform(-1, 1, 1 << 20) * np.exp2(rng.uniform(-12, np.log2(463.9), 1 << 20))).astype(np.float32)
+    v = np.concatenate([pts, -pts, sweep, rng.standard_normal(1 << 16).astype(np.float32)])
+    v = v[: v.size // 4 * 4]
+    got = moe.cvt_fp8(torch.from_numpy(v).to(DEV), hardware).cpu().numpy()
+    want = e4m3_encode(v)
+    bad = np.nonzero(got != want)[0]
+    assert bad.size == 0, (v[bad[:4]], got[bad[:4]], want[bad[:4]])
 
 
 @pytest.mark.parametrize("fmt", [formats.FMT_W4, formats.FMT_W6])
