@@ -84,6 +84,19 @@ D3_INLINE uint32_t wave_max_u32(uint32_t v) {
   return max(max(a, b), max(c, d));
 }
 
+// the same maximum left in every lane's register (rows of 16 by DPP, then the row pairs and halves exchanged with
+// permlane16 / permlane32 swaps): no scalar round trip, so a chain of reductions stays on the vector unit
+D3_INLINE uint32_t wave_max_u32_v(uint32_t v) {
+  v = max(v, (uint32_t)dpp_i32((int)v, 0xB1));
+  v = max(v, (uint32_t)dpp_i32((int)v, 0x4E));
+  v = max(v, (uint32_t)dpp_i32((int)v, 0x141));
+  v = max(v, (uint32_t)dpp_i32((int)v, 0x140));
+  const auto r16 = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+  v = max((uint32_t)r16[0], (uint32_t)r16[1]);
+  const auto r32 = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  return max((uint32_t)r32[0], (uint32_t)r32[1]);
+}
+
 D3_INLINE float wave_max_f32(float v) {
   v = fmaxf(v, __int_as_float(dpp_i32(__float_as_int(v), 0xB1)));
   v = fmaxf(v, __int_as_float(dpp_i32(__float_as_int(v), 0x4E)));

@@ -321,20 +321,29 @@ D3_INLINE void down_item(const Ctx& cx, int c, int hb) {
   constexpr int GPH = (G8 + 31) / 32;   // 8-column groups per lane of a half-wave
   constexpr int TPH = (T + 31) / 32;    // tile maxima per lane of a half-wave
   if (2 * w < ne) {
-    // Each wave serves its two experts on its own: waits for their gate_up tiles (lane 0 polls their counters), then
-    // gathers their pairs' hidden rows two at a time (a pair per half-wave: the tiles' maxima and the values in one
-    // round trip; words whose store has not landed yet are read again), quantizes them into its LDS slots and runs.
+    // Each wave serves its two experts on its own: gathers their pairs' hidden rows two at a time (a pair per
+    // half-wave: the tiles' maxima and the values in one round trip), quantizes them into its LDS slots and runs.
+    // The gather is issued once the wave's weight rows have arrived (its loads complete in order, so anything issued
+    // earlier would be read early and come back no sooner); the words carry their epoch, so a gather that finds every
+    // word current needs nothing else. Otherwise lane 0 waits for the experts' counters and the stale words are read
+    // again.
     const int la = 2 * w, lb = 2 * w + 1;
     const bool has_b = lb < ne;
-    if (lane == 0) {
-      uint32_t polls = 0;
-      while (true) {
-        const uint64_t want = ((uint64_t)cx.epoch << 32) | (uint32_t)T;
-        const uint64_t na = signal_load64(done_counter(a.sync, u0 + la));
-        const uint64_t nb = has_b ? signal_load64(done_counter(a.sync, u0 + lb)) : want;
-        if ((na == want && nb == want) || !keep_polling(polls, a.sync + SYNC_STATUS, a.spin_limit)) break;
+    bool counted = false;
+    auto await_counters = [&]() {
+      if (counted) return;
+      counted = true;
+      if (lane == 0) {
+        uint32_t polls = 0;
+        while (true) {
+          const uint64_t want = ((uint64_t)cx.epoch << 32) | (uint32_t)T;
+          const uint64_t na = signal_load64(done_counter(a.sync, u0 + la));
+          const uint64_t nb = has_b ? signal_load64(done_counter(a.sync, u0 + lb)) : want;
+          if ((na == want && nb == want) || !keep_polling(polls, a.sync + SYNC_STATUS, a.spin_limit)) break;
+        }
       }
-    }
+    };
+    settle();
     const int s0 = slot_first[la], s1 = slot_first[has_b ? lb + 1 : la + 1];
     const int half = lane >> 5, hl = lane & 31;
     for (int sp = s0; sp < s1; sp += 2) {
@@ -362,6 +371,7 @@ D3_INLINE void down_item(const Ctx& cx, int c, int hb) {
 #pragma unroll
         for (int i = 0; i < 8; i++) fresh = fresh && (!on || hl + 32 * k >= G8 || tag_is(vw[k][i], cx.epoch));
       if (!__all(fresh)) {
+        await_counters();
         uint32_t polls = 0;
         while (true) {
           bool ok = true;
@@ -496,6 +506,34 @@ D3_INLINE void down_item(const Ctx& cx, int c, int hb) {
   }
 }
 
+// Top-k of a row's router logits (bf16 bits lb[j] for experts lane + 64 j, KPL of them per lane): k rounds of a
+// wave-wide max over each lane's largest remaining key; lane r < k returns the r-th largest key, descending, ties to
+// the lower index (kernels.py:50-55).
+template <int KPL>
+D3_INLINE uint32_t top_keys(const uint32_t* lb, int lane, int E, int k) {
+  uint32_t key[KPL];
+#pragma unroll
+  for (int j = 0; j < KPL; j++) key[j] = lane + 64 * j < E ? route_key(lb[j], lane + 64 * j) : 0u;
+  uint32_t lm = key[0];
+#pragma unroll
+  for (int j = 1; j < KPL; j++) lm = max(lm, key[j]);
+  uint32_t mine = 0u;
+#pragma unroll
+  for (int r = 0; r < MAX_K; r++) {
+    if (r < k) {
+      const uint32_t m = wave_max_u32_v(lm);
+      mine = lane == r ? m : mine;
+      lm = 0u;
+#pragma unroll
+      for (int j = 0; j < KPL; j++) {
+        key[j] = key[j] == m ? 0u : key[j];
+        lm = max(lm, key[j]);
+      }
+    }
+  }
+  return mine;
+}
+
 template <int F, int H, int I>
 __global__ void __launch_bounds__(256, 3) moe_a8_kernel(MoeA8Args a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
@@ -541,39 +579,24 @@ __global__ void __launch_bounds__(256, 3) moe_a8_kernel(MoeA8Args a) {
 #pragma unroll
     for (int k = 0; k < H / 512; k++) xraw[k] = do_quant ? *(const i32x4*)(xr + 512 * k + 8 * lane) : i32x4{0, 0, 0, 0};
     if (do_route) {
-      uint32_t key[4];
-#pragma unroll
-      for (int j = 0; j < 4; j++) key[j] = lane + 64 * j < E ? route_key(lb[j], lane + 64 * j) : 0u;
-      float top[MAX_K];
-      int ids[MAX_K];
-#pragma unroll
-      for (int r = 0; r < MAX_K; r++) {
-        top[r] = 0.0f;
-        ids[r] = 0;
-        if (r < K8) {
-          const uint32_t m = wave_max_u32(max(max(key[0], key[1]), max(key[2], key[3])));
-#pragma unroll
-          for (int j = 0; j < 4; j++) key[j] = key[j] == m ? 0u : key[j];
-          ids[r] = route_key_index(m);
-          top[r] = route_key_value(m);
-        }
-      }
+      const uint32_t mine = E <= 128 ? top_keys<2>(lb, lane, E, K8) : top_keys<4>(lb, lane, E, K8);
+      // softmax over the k, the exponentials in parallel and their sum in rank order (kernels.py:57-61)
+      const float top0 = route_key_value((uint32_t)__builtin_amdgcn_readlane((int)mine, 0));
+      const float ex = lane < K8 ? expf(route_key_value(mine) - top0) : 0.0f;
       float total = 0.0f;
 #pragma unroll
       for (int r = 0; r < MAX_K; r++)
-        if (r < K8) total += expf(top[r] - top[0]);
-#pragma unroll
-      for (int r = 0; r < MAX_K; r++) {
-        if (r < K8 && lane == r) {
-          cx.rt_id[tr * MAX_K + r] = ids[r];
-          cx.rt_w[tr * MAX_K + r] = bf16_round(expf(top[r] - top[0]) / total);
-          if (M == 1) {
-            // one row: its experts in routing order are the union, one pair each, all in one down chunk
-            cx.ulist[r] = ids[r];
-            cx.ucount[r] = 1;
-            cx.utok[r * MAX_M] = 0;
-            cx.upair[r * MAX_M] = (uint8_t)r;
-          }
+        if (r < K8) total += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ex), r));
+      if (lane < K8) {
+        const int id = route_key_index(mine);
+        cx.rt_id[tr * MAX_K + lane] = id;
+        cx.rt_w[tr * MAX_K + lane] = bf16_round(ex / total);
+        if (M == 1) {
+          // one row: its experts in routing order are the union, one pair each, all in one down chunk
+          cx.ulist[lane] = id;
+          cx.ucount[lane] = 1;
+          cx.utok[lane * MAX_M] = 0;
+          cx.upair[lane * MAX_M] = (uint8_t)lane;
         }
       }
       if (M == 1 && lane == 0) {
