@@ -33,7 +33,8 @@ __global__ void __launch_bounds__(64) gemv_groups_kernel(const uint8_t* rows, in
       xhi = *(const i32x4*)(xs + col * K + 128 * s + 32 * q + 16);
     }
     if constexpr (F == FMT_F8) {
-      const f32x4 f = step_f8(raw, xlo, xhi, f32x4{0.0f, 0.0f, 0.0f, 0.0f});
+      const i32x8 fa = f8_operand(raw), fb = f8_operand(xlo, xhi);
+      const f32x4 f = mfma_f8_chain<1>(&fa, &fb);
       if (col < C)
         for (int i = 0; i < 4; i++)
           ((float*)acc)[((size_t)(blockIdx.x * 16 + 4 * q + i) * groups + s) * C + col] = f[i];

@@ -195,6 +195,9 @@ D3_INLINE uint64_t signal_load64(const uint64_t* p) { return __hip_atomic_load(p
 
 // every memory access of this wave so far has completed (its LDS writes are visible to its own lanes)
 D3_INLINE void settle() { __builtin_amdgcn_s_waitcnt(0); }
+// this wave's LDS accesses (and scalar loads) have completed; its vector loads may still be in flight
+// (s_waitcnt lgkmcnt(0) with vmcnt and expcnt left at their maxima: 0xC07F in the gfx9 encoding)
+D3_INLINE void lds_settle() { __builtin_amdgcn_s_waitcnt(0xC07F); }
 
 D3_INLINE uint32_t signal_add_ret(uint32_t* counter, uint32_t v) {
   return __hip_atomic_fetch_add(counter, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

@@ -95,12 +95,7 @@ template <int F> D3_INLINE void operand_i8(const Raw<F>& r, i32x4& lo, i32x4& hi
 // A step against 32 activation bytes (int8, or e4m3 for F8) of this lane's column.
 //   I8: acc (int32) += the step's dot products.
 //   W4/W6: returns the step's int32 dot products scaled by 16 / 4 (the caller applies the group scale).
-//   F8: facc (float) += the step's dot products.
 D3_INLINE i32x4 mfma_i8(i32x4 a, i32x4 b, i32x4 c) { return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0); }
-D3_INLINE f32x4 mfma_f8(i32x8 a, i32x8 b, f32x4 c) {
-  // E8M0 block scales of 127 are 2^0: a plain e4m3 x e4m3 product with float accumulation
-  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 127, 0, 127);
-}
 
 template <int F> D3_INLINE i32x4 step_i8(const Raw<F>& r, const i32x4& xlo, const i32x4& xhi, i32x4 acc) {
   i32x4 lo, hi;
@@ -108,10 +103,86 @@ template <int F> D3_INLINE i32x4 step_i8(const Raw<F>& r, const i32x4& xlo, cons
   acc = mfma_i8(lo, xlo, acc);
   return mfma_i8(hi, xhi, acc);
 }
-D3_INLINE f32x4 step_f8(const Raw<FMT_F8>& r, const i32x4& xlo, const i32x4& xhi, f32x4 acc) {
-  i32x8 a = i32x8{(int)r.d[0], (int)r.d[1], (int)r.d[2], (int)r.d[3], (int)r.d[4], (int)r.d[5], (int)r.d[6], (int)r.d[7]};
-  i32x8 b = i32x8{xlo.x, xlo.y, xlo.z, xlo.w, xhi.x, xhi.y, xhi.z, xhi.w};
-  return mfma_f8(a, b, acc);
+// F8: e4m3 x e4m3 -> float32 on the f8f6f4 MFMA (16 x 16 x 128 per step), acc = sum over steps k of A[k] . B[k] (A: 8
+// registers of a weight row's 32 columns per lane group, B: the activations', lane layout as the int8 MFMA). The whole
+// chain is one asm statement: every A and B operand keeps its registers until the chain has finished and the
+// accumulator is both source and destination. With the compiler's own register choices for this instruction (an
+// accumulator overlapping an operand or another accumulator, operand registers rewritten right after issue while the
+// 16-pass instruction still reads its 8-register operands) layer outputs came out wrong on MI355X, depending on the
+// surrounding code. The wait states before (operands written just before) and after (the result read just after)
+// cover the instruction's own hazards, which the compiler does not see inside the statement.
+template <int N> D3_INLINE f32x4 mfma_f8_chain(const i32x8* A, const i32x8* B);
+template <> D3_INLINE f32x4 mfma_f8_chain<1>(const i32x8* A, const i32x8* B) {
+  f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  const int one = 127;  // E8M0 block scale 2^0: a plain e4m3 x e4m3 product
+  asm volatile(
+      "s_nop 4\n"
+      "v_mfma_scale_f32_16x16x128_f8f6f4 %0, %1, %2, %0, %3, %3 op_sel_hi:[0,0,0]\n"
+      "s_nop 7\n s_nop 7\n s_nop 7\n"
+      : "+v"(acc)
+      : "v"(A[0]), "v"(B[0]), "v"(one));
+  return acc;
+}
+template <> D3_INLINE f32x4 mfma_f8_chain<2>(const i32x8* A, const i32x8* B) {
+  f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  const int one = 127;  // E8M0 block scale 2^0: a plain e4m3 x e4m3 product
+  asm volatile(
+      "s_nop 4\n"
+      "v_mfma_scale_f32_16x16x128_f8f6f4 %0, %1, %3, %0, %5, %5 op_sel_hi:[0,0,0]\n"
+      "v_mfma_scale_f32_16x16x128_f8f6f4 %0, %2, %4, %0, %5, %5 op_sel_hi:[0,0,0]\n"
+      "s_nop 7\n s_nop 7\n s_nop 7\n"
+      : "+v"(acc)
+      : "v"(A[0]), "v"(A[1]), "v"(B[0]), "v"(B[1]), "v"(one));
+  return acc;
+}
+template <> D3_INLINE f32x4 mfma_f8_chain<3>(const i32x8* A, const i32x8* B) {
+  f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  const int one = 127;  // E8M0 block scale 2^0: a plain e4m3 x e4m3 product
+  asm volatile(
+      "s_nop 4\n"
+      "v_mfma_scale_f32_16x16x128_f8f6f4 %0, %1, %4, %0, %7, %7 op_sel_hi:[0,0,0]\n"
+      "v_mfma_scale_f32_16x16x128_f8f6f4 %0, %2, %5, %0, %7, %7 op_sel_hi:[0,0,0]\n"
+      "v_mfma_scale_f32_16x16x128_f8f6f4 %0, %3, %6, %0, %7, %7 op_sel_hi:[0,0,0]\n"
+      "s_nop 7\n s_nop 7\n s_nop 7\n"
+      : "+v"(acc)
+      : "v"(A[0]), "v"(A[1]), "v"(A[2]), "v"(B[0]), "v"(B[1]), "v"(B[2]), "v"(one));
+  return acc;
+}
+template <> D3_INLINE f32x4 mfma_f8_chain<4>(const i32x8* A, const i32x8* B) {
+  f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  const int one = 127;  // E8M0 block scale 2^0: a plain e4m3 x e4m3 product
+  asm volatile(
+      "s_nop 4\n"
+      "v_mfma_scale_f32_16x16x128_f8f6f4 %0, %1, %5, %0, %9, %9 op_sel_hi:[0,0,0]\n"
+      "v_mfma_scale_f32_16x16x128_f8f6f4 %0, %2, %6, %0, %9, %9 op_sel_hi:[0,0,0]\n"
+      "v_mfma_scale_f32_16x16x128_f8f6f4 %0, %3, %7, %0, %9, %9 op_sel_hi:[0,0,0]\n"
+      "v_mfma_scale_f32_16x16x128_f8f6f4 %0, %4, %8, %0, %9, %9 op_sel_hi:[0,0,0]\n"
+      "s_nop 7\n s_nop 7\n s_nop 7\n"
+      : "+v"(acc)
+      : "v"(A[0]), "v"(A[1]), "v"(A[2]), "v"(A[3]), "v"(B[0]), "v"(B[1]), "v"(B[2]), "v"(B[3]), "v"(one));
+  return acc;
+}
+template <> D3_INLINE f32x4 mfma_f8_chain<6>(const i32x8* A, const i32x8* B) {
+  f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  const int one = 127;  // E8M0 block scale 2^0: a plain e4m3 x e4m3 product
+  asm volatile(
+      "s_nop 4\n"
+      "v_mfma_scale_f32_16x16x128_f8f6f4 %0, %1, %7, %0, %13, %13 op_sel_hi:[0,0,0]\n"
+      "v_mfma_scale_f32_16x16x128_f8f6f4 %0, %2, %8, %0, %13, %13 op_sel_hi:[0,0,0]\n"
+      "v_mfma_scale_f32_16x16x128_f8f6f4 %0, %3, %9, %0, %13, %13 op_sel_hi:[0,0,0]\n"
+      "v_mfma_scale_f32_16x16x128_f8f6f4 %0, %4, %10, %0, %13, %13 op_sel_hi:[0,0,0]\n"
+      "v_mfma_scale_f32_16x16x128_f8f6f4 %0, %5, %11, %0, %13, %13 op_sel_hi:[0,0,0]\n"
+      "v_mfma_scale_f32_16x16x128_f8f6f4 %0, %6, %12, %0, %13, %13 op_sel_hi:[0,0,0]\n"
+      "s_nop 7\n s_nop 7\n s_nop 7\n"
+      : "+v"(acc)
+      : "v"(A[0]), "v"(A[1]), "v"(A[2]), "v"(A[3]), "v"(A[4]), "v"(A[5]), "v"(B[0]), "v"(B[1]), "v"(B[2]), "v"(B[3]), "v"(B[4]), "v"(B[5]), "v"(one));
+  return acc;
+}
+D3_INLINE i32x8 f8_operand(const Raw<FMT_F8>& r) {
+  return i32x8{(int)r.d[0], (int)r.d[1], (int)r.d[2], (int)r.d[3], (int)r.d[4], (int)r.d[5], (int)r.d[6], (int)r.d[7]};
+}
+D3_INLINE i32x8 f8_operand(const i32x4& lo, const i32x4& hi) {
+  return i32x8{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
 }
 
 // Activation storage order: W4 keeps each 8 columns as [0,2,4,6,1,3,5,7]; the others keep column order. Position of

@@ -61,7 +61,6 @@ struct MoeA8Args {
   uint32_t* sync;
   int M, E, topk;
   uint32_t spin_limit;
-  int dn_start;  // down items load their weights once this many 256ths of their chunk's gate_up tiles are done
 };
 
 // LDS carve-up (bytes), shared by host (launch size) and device.
@@ -128,14 +127,15 @@ struct Ctx {
 
 // gate_up item: hidden units 16 tile .. 16 tile + 15 of expert u, i.e. two 16-row MFMA tiles (sub-tile s: gate rows
 // 16 tile + 8 s .. + 7 as rows 0-7, the matching up rows as rows 8-15)
-template <int F, int H, int I>
-D3_INLINE void gate_up_item(const Ctx& cx, int u, int tile, int parity) {
+// (`between` runs once the item's weight rows are on their way, before it reads the slot tables or x; `after` once its
+// products are done, before its reduction)
+template <int F, int H, int I, typename Between, typename After>
+D3_INLINE void gate_up_item(const Ctx& cx, int u, int tile, int parity, int e, int nu, Between between, After after) {
   constexpr int SPW = H / 512;  // steps per wave
   constexpr int RB = row_bytes(F, H);
   constexpr int SHIFT = unpack_shift(F);
   const MoeA8Args& a = *cx.a;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, q = lane >> 4, col = lane & 15;
-  const int e = cx.ulist[u], nu = cx.ucount[u];
   uint64_t raised = 0;
   if (tid == 0)
     raised = __hip_atomic_fetch_max(done_counter(a.sync, u), (uint64_t)cx.epoch << 32, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -165,6 +165,7 @@ D3_INLINE void gate_up_item(const Ctx& cx, int u, int tile, int parity) {
       us = bf16_to_f32(a.gu_s[(size_t)e * (2 * I) + I + 16 * tile + (lane & 15)]);
     }
   }
+  between();
   const bool active = col < nu;
   const uint8_t* xp = cx.xq + (size_t)(active ? cx.utok[u * MAX_M + col] : 0) * H;
   float* rd = cx.red + parity * 2048;
@@ -172,6 +173,7 @@ D3_INLINE void gate_up_item(const Ctx& cx, int u, int tile, int parity) {
   for (int sub = 0; sub < 2; sub++) {
     i32x4 iacc = {0, 0, 0, 0};
     f32x4 facc = {0.0f, 0.0f, 0.0f, 0.0f};
+    i32x8 fa[SPW], fb[SPW];
 #pragma unroll
     for (int s = 0; s < SPW; s++) {
       i32x4 xlo = {0, 0, 0, 0}, xhi = {0, 0, 0, 0};
@@ -183,17 +185,20 @@ D3_INLINE void gate_up_item(const Ctx& cx, int u, int tile, int parity) {
       if constexpr (F == FMT_I8) {
         iacc = step_i8<F>(raw[sub][s], xlo, xhi, iacc);
       } else if constexpr (F == FMT_F8) {
-        facc = step_f8(raw[sub][s], xlo, xhi, facc);
+        fa[s] = f8_operand(raw[sub][s]);
+        fb[s] = f8_operand(xlo, xhi);
       } else {
         const i32x4 g = step_i8<F>(raw[sub][s], xlo, xhi, i32x4{0, 0, 0, 0});
 #pragma unroll
         for (int i = 0; i < 4; i++) facc[i] += (float)(g[i] >> SHIFT) * sc[sub][s][i];
       }
     }
+    if constexpr (F == FMT_F8) facc = mfma_f8_chain<SPW>(fa, fb);
 #pragma unroll
     for (int i = 0; i < 4; i++)
       rd[sub * 1024 + w * 256 + (4 * q + i) * 16 + col] = F == FMT_I8 ? __int_as_float(iacc[i]) : facc[i];
   }
+  after();
   __syncthreads();
   if (w == 0) {
     for (int idx = lane; idx < 16 * nu; idx += 64) {
@@ -245,11 +250,118 @@ D3_INLINE void gate_up_item(const Ctx& cx, int u, int tile, int parity) {
   }
 }
 
-// down block: output rows 8 hb .. 8 hb + 7 of the experts of chunk c
+// Top-k of a row's router logits (bf16 bits lb[j] for experts lane + 64 j, KPL of them per lane), one round at a time:
+// round r takes the wave-wide max over each lane's largest remaining key and lane r keeps it, so after k rounds lanes
+// 0 .. k-1 hold the k largest keys, descending, ties to the lower index (kernels.py:50-55).
+template <int KPL>
+struct TopKeys {
+  uint32_t key[KPL], lm, mine;
+  D3_INLINE TopKeys(const uint32_t* lb, int lane, int E) : lm(0u), mine(0u) {
+#pragma unroll
+    for (int j = 0; j < KPL; j++) {
+      key[j] = lane + 64 * j < E ? route_key(lb[j], lane + 64 * j) : 0u;
+      lm = max(lm, key[j]);
+    }
+  }
+  // rounds from .. to - 1 (to <= MAX_K)
+  D3_INLINE void rounds(int lane, int from, int to) {
+#pragma unroll
+    for (int r = 0; r < MAX_K; r++) {
+      if (r >= from && r < to) {
+        const uint32_t m = wave_max_u32_v(lm);
+        mine = lane == r ? m : mine;
+        lm = 0u;
+#pragma unroll
+        for (int j = 0; j < KPL; j++) {
+          key[j] = key[j] == m ? 0u : key[j];
+          lm = max(lm, key[j]);
+        }
+      }
+    }
+  }
+};
+template <int KPL>
+D3_INLINE uint32_t top_keys(const uint32_t* lb, int lane, int E, int k) {
+  TopKeys<KPL> t(lb, lane, E);
+  t.rounds(lane, 0, k);
+  return t.mine;
+}
+
+// The softmax over a row's k routed logits (lanes 0 .. k-1 hold the keys, descending): this lane's weight, the
+// exponentials in parallel and their sum in rank order (kernels.py:57-61), bf16-rounded.
+D3_INLINE float route_weight(uint32_t mine, int lane, int k) {
+  const float top0 = route_key_value((uint32_t)__builtin_amdgcn_readlane((int)mine, 0));
+  const float ex = lane < k ? expf(route_key_value(mine) - top0) : 0.0f;
+  float total = 0.0f;
+#pragma unroll
+  for (int r = 0; r < MAX_K; r++)
+    if (r < k) total += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ex), r));
+  return bf16_round(ex / total);
+}
+
+// A down item's weight rows (this lane's: local expert 2w + (row / 8), output row 8 hb + row % 8) and the scales of
+// its accumulator rows, held in registers from their loads to the item's products.
+template <int F, int I>
+struct DownRows {
+  static constexpr int STEPS = I / 128;
+  Raw<F> raw[STEPS];
+  // scales as loaded (bf16 pairs, converted where the products use them, so that nothing waits for the loads
+  // before then): W4 / W6 the 4 rows' group scales, row-major [4][STEPS]; I8 / F8 the 4 row scales
+  uint32_t sw[group_scaled(F) ? 2 * STEPS : 2];
+  D3_INLINE float scale(int i, int s) const {  // group scale of row i, step s (W4 / W6)
+    const int k = i * STEPS + s;
+    return bf16_to_f32((k & 1) ? sw[k >> 1] >> 16 : sw[k >> 1] & 0xFFFFu);
+  }
+  D3_INLINE float row_scale(int i) const {  // I8 / F8
+    return bf16_to_f32((i & 1) ? sw[i >> 1] >> 16 : sw[i >> 1] & 0xFFFFu);
+  }
+};
+
+// issue the loads of down item (c, hb): output rows 8 hb .. 8 hb + 7 of the experts of chunk c
 template <int F, int H, int I>
-D3_INLINE void down_item(const Ctx& cx, int c, int hb) {
+D3_INLINE void down_load(const Ctx& cx, int c, int hb, DownRows<F, I>& d) {
   constexpr int STEPS = I / 128;
   constexpr int RB = row_bytes(F, I);
+  const MoeA8Args& a = *cx.a;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, q = lane >> 4;
+  const int u0 = cx.chunk_first[c], ne = cx.chunk_first[c + 1] - u0;
+  const int ra = lane & 15;
+  const int lj_a = 2 * w + (ra >> 3);
+#pragma unroll
+  for (int s = 0; s < STEPS; s++) d.raw[s] = Raw<F>{};
+  if (lj_a < ne) {
+    const int e = cx.ulist[u0 + lj_a];
+    const uint8_t* wp = a.dn_w + ((size_t)e * H + 8 * hb + (ra & 7)) * RB;
+#pragma unroll
+    for (int s = 0; s < STEPS; s++) load_step<F>(d.raw[s], wp, s, q);
+  }
+  // scales of this lane's accumulator rows 4q + i: local expert 2w + q / 2, output row 8 hb + 4 (q % 2) + i (the 4
+  // rows' scales are contiguous: 8 bytes, or 4 * STEPS * 2 bytes of group scales, aligned to their size's 8 / 16)
+  const int lj_c = 2 * w + (q >> 1);
+  const int e_c = cx.ulist[u0 + min(lj_c, ne - 1)];
+  const uint16_t* sp = a.dn_s + ((size_t)e_c * H + 8 * hb + 4 * (q & 1)) * (group_scaled(F) ? STEPS : 1);
+  if constexpr (group_scaled(F)) {
+    static_assert(STEPS % 2 == 0, "whole 16-byte groups of scales");
+#pragma unroll
+    for (int k = 0; k < STEPS / 2; k++) {
+      const i32x4 v = *(const i32x4*)(sp + 8 * k);
+      d.sw[4 * k] = (uint32_t)v.x;
+      d.sw[4 * k + 1] = (uint32_t)v.y;
+      d.sw[4 * k + 2] = (uint32_t)v.z;
+      d.sw[4 * k + 3] = (uint32_t)v.w;
+    }
+  } else {
+    const i32x2 v = *(const i32x2*)sp;
+    d.sw[0] = (uint32_t)v.x;
+    d.sw[1] = (uint32_t)v.y;
+  }
+}
+
+// the rest of down item (c, hb) once its loads are out: collect the chunk's hidden rows, quantize, multiply, and write
+// the weighted sum (one chunk) or the partial outputs
+template <int F, int H, int I>
+D3_INLINE void down_finish(const Ctx& cx, int c, int hb, const DownRows<F, I>& d) {
+  constexpr int STEPS = I / 128;
   constexpr int SHIFT = unpack_shift(F);
   constexpr float QMAX = act_qmax<F>();
   constexpr int G8 = I / 8;  // 8-column groups of a hidden row
@@ -258,49 +370,6 @@ D3_INLINE void down_item(const Ctx& cx, int c, int hb) {
   const int M = a.M, K8 = a.topk;
   const int u0 = cx.chunk_first[c], ne = cx.chunk_first[c + 1] - u0;
   int* slot_first = cx.slot_first;
-  __syncthreads();  // the previous item's readers of the slot tables and partial outputs are done
-
-  // The down weights queue behind the chunk's gate_up weights: the item loads them once dn_start / 256 of the chunk's
-  // gate_up tiles are done, so the gate_up rows arrive first and the hand-off overlaps the down rows' arrival.
-  if (tid == 0 && a.dn_start > 0) {
-    const uint32_t want = (uint32_t)((ne * (I / 16) * a.dn_start) >> 8);
-    uint32_t polls = 0;
-    while (true) {
-      uint64_t n[CHUNK_EXPERTS];
-#pragma unroll
-      for (int lj = 0; lj < CHUNK_EXPERTS; lj++) n[lj] = lj < ne ? signal_load64(done_counter(a.sync, u0 + lj)) : 0;
-      uint32_t total = 0;
-#pragma unroll
-      for (int lj = 0; lj < CHUNK_EXPERTS; lj++) total += (uint32_t)(n[lj] >> 32) == cx.epoch ? (uint32_t)n[lj] : 0u;
-      if (total >= want || !keep_polling(polls, a.sync + SYNC_STATUS, a.spin_limit)) break;
-    }
-  }
-  __syncthreads();
-  // this lane's weight row: local expert 2w + (row / 8), output row 8 hb + row % 8
-  const int ra = lane & 15;
-  const int lj_a = 2 * w + (ra >> 3);
-  Raw<F> raw[STEPS] = {};
-  if (lj_a < ne) {
-    const int e = cx.ulist[u0 + lj_a];
-    const uint8_t* wp = a.dn_w + ((size_t)e * H + 8 * hb + (ra & 7)) * RB;
-#pragma unroll
-    for (int s = 0; s < STEPS; s++) load_step<F>(raw[s], wp, s, q);
-  }
-  // scales of this lane's accumulator rows 4q + i: local expert 2w + q / 2, output row 8 hb + 4 (q % 2) + i
-  const int lj_c = 2 * w + (q >> 1);
-  const int e_c = lj_c < ne ? cx.ulist[u0 + lj_c] : 0;
-  float sc[STEPS][4];
-  float rs[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-  if constexpr (group_scaled(F)) {
-#pragma unroll
-    for (int i = 0; i < 4; i++)
-#pragma unroll
-      for (int s = 0; s < STEPS; s++)
-        sc[s][i] = lj_c < ne ? bf16_to_f32(a.dn_s[((size_t)e_c * H + 8 * hb + 4 * (q & 1) + i) * (I / 128) + s]) : 0.0f;
-  } else {
-#pragma unroll
-    for (int i = 0; i < 4; i++) rs[i] = lj_c < ne ? bf16_to_f32(a.dn_s[(size_t)e_c * H + 8 * hb + 4 * (q & 1) + i]) : 0.0f;
-  }
   if (tid == 0) {
     int slot = 0;
     for (int lj = 0; lj < ne; lj++) {
@@ -438,6 +507,7 @@ D3_INLINE void down_item(const Ctx& cx, int c, int hb) {
       const uint8_t* xp = cx.hq + (size_t)(slot >= 0 ? slot : 0) * I;
       i32x4 iacc = {0, 0, 0, 0};
       f32x4 facc = {0.0f, 0.0f, 0.0f, 0.0f};
+      i32x8 fa[STEPS], fb[STEPS];
 #pragma unroll
       for (int s = 0; s < STEPS; s++) {
         i32x4 xlo = {0, 0, 0, 0}, xhi = {0, 0, 0, 0};
@@ -446,15 +516,17 @@ D3_INLINE void down_item(const Ctx& cx, int c, int hb) {
           xhi = *(const i32x4*)(xp + 128 * s + 32 * q + 16);
         }
         if constexpr (F == FMT_I8) {
-          iacc = step_i8<F>(raw[s], xlo, xhi, iacc);
+          iacc = step_i8<F>(d.raw[s], xlo, xhi, iacc);
         } else if constexpr (F == FMT_F8) {
-          facc = step_f8(raw[s], xlo, xhi, facc);
+          fa[s] = f8_operand(d.raw[s]);
+          fb[s] = f8_operand(xlo, xhi);
         } else {
-          const i32x4 g = step_i8<F>(raw[s], xlo, xhi, i32x4{0, 0, 0, 0});
+          const i32x4 g = step_i8<F>(d.raw[s], xlo, xhi, i32x4{0, 0, 0, 0});
 #pragma unroll
-          for (int i = 0; i < 4; i++) facc[i] += (float)(g[i] >> SHIFT) * sc[s][i];
+          for (int i = 0; i < 4; i++) facc[i] += (float)(g[i] >> SHIFT) * d.scale(i, s);
         }
       }
+      if constexpr (F == FMT_F8) facc = mfma_f8_chain<STEPS>(fa, fb);
       // this lane's accumulator rows belong to expert a (q < 2) or b (q >= 2); keep the products of matching columns
       const bool valid = slot >= 0 && (one_pass ? (rows_b ? col >= na : col < na) : (pass == 0 ? !rows_b : rows_b));
       if (valid) {
@@ -463,8 +535,8 @@ D3_INLINE void down_item(const Ctx& cx, int c, int hb) {
         for (int i = 0; i < 4; i++) {
           const int r = 4 * (q & 1) + i;
           float y;
-          if constexpr (F == FMT_I8) y = (float)iacc[i] * rs[i];
-          else if constexpr (F == FMT_F8) y = facc[i] * rs[i];
+          if constexpr (F == FMT_I8) y = (float)iacc[i] * d.row_scale(i);
+          else if constexpr (F == FMT_F8) y = facc[i] * d.row_scale(i);
           else y = facc[i];
           cx.lparts[slot * 8 + r] = y * hsc;
         }
@@ -506,32 +578,99 @@ D3_INLINE void down_item(const Ctx& cx, int c, int hb) {
   }
 }
 
-// Top-k of a row's router logits (bf16 bits lb[j] for experts lane + 64 j, KPL of them per lane): k rounds of a
-// wave-wide max over each lane's largest remaining key; lane r < k returns the r-th largest key, descending, ties to
-// the lower index (kernels.py:50-55).
-template <int KPL>
-D3_INLINE uint32_t top_keys(const uint32_t* lb, int lane, int E, int k) {
-  uint32_t key[KPL];
+// down item (c, hb)
+template <int F, int H, int I>
+D3_INLINE void down_item(const Ctx& cx, int c, int hb) {
+  __syncthreads();  // the previous item's readers of the slot tables and partial outputs are done
+  DownRows<F, I> d;
+  down_load<F, H, I>(cx, c, hb, d);
+  down_finish<F, H, I>(cx, c, hb, d);
+}
+
+// One row (M = 1) with a workgroup for each gate_up tile: workgroup i computes gate_up tile i % T of the expert at
+// routing rank i / T and, for i < H / 8, down block i, so the down rows are requested only once the workgroup's
+// gate_up rows have arrived and the gate_up rows, which the hand-off waits for, are not queued behind them.
+// Every wave routes the row itself and its gate_up rows go out after the rounds that name their expert (no workgroup
+// barrier before them); the remaining rounds, the softmax, the x slice its MFMA steps read (H = 2048: wave w reads x
+// chunk w) and the slot tables are written while they are in flight. Every wave writes the same values, so nothing
+// waits for another wave until the gate_up reduction.
+template <int F, int H, int I, int KPL>
+D3_INLINE void one_row_layer(Ctx& cx, int i) {
+  static_assert(H == 2048, "wave w's K slice is x chunk w");
+  constexpr int T = I / 16, NHB = H / 8;
+  constexpr float QMAX = act_qmax<F>();
+  const MoeA8Args& a = *cx.a;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int E = a.E, K8 = a.topk;
+  const int u = i / T, tile = i % T;
+  const bool has_down = i < NHB;
+  uint32_t lb[KPL];
 #pragma unroll
-  for (int j = 0; j < KPL; j++) key[j] = lane + 64 * j < E ? route_key(lb[j], lane + 64 * j) : 0u;
-  uint32_t lm = key[0];
+  for (int j = 0; j < KPL; j++) lb[j] = a.logits[min(lane + 64 * j, E - 1)];
+  i32x4 xraw[H / 512];
 #pragma unroll
-  for (int j = 1; j < KPL; j++) lm = max(lm, key[j]);
-  uint32_t mine = 0u;
+  for (int k = 0; k < H / 512; k++) xraw[k] = *(const i32x4*)(a.x + 512 * k + 8 * lane);
+  TopKeys<KPL> tk(lb, lane, E);
+  tk.rounds(lane, 0, u + 1);
+  const int e = route_key_index((uint32_t)__builtin_amdgcn_readlane((int)tk.mine, u));
+  cx.U = K8;
+  cx.nch = 1;
+  cx.n_dn = NHB;
+  DownRows<F, I> d;
+  gate_up_item<F, H, I>(
+      cx, u, tile, 0, e, 1,
+      [&]() {
+        if (has_down) {
+          tk.rounds(lane, u + 1, K8);
+          const float wt = route_weight(tk.mine, lane, K8);
+          if (lane < K8) {
+            const int id = route_key_index(tk.mine);
+            cx.rt_id[lane] = id;
+            cx.rt_w[lane] = wt;
+            cx.ulist[lane] = id;
+            cx.ucount[lane] = 1;
+            cx.utok[lane * MAX_M] = 0;
+            cx.upair[lane * MAX_M] = (uint8_t)lane;
+            if (i == 0 && w == 0) {
+              if (a.ids_out) a.ids_out[lane] = id;
+              if (a.weights_out) a.weights_out[lane] = wt;
+            }
+          }
+          if (lane == 0) {
+            cx.chunk_first[0] = 0;
+            cx.chunk_first[1] = K8;
+            cx.misc[0] = K8;
+            cx.misc[1] = 1;
+          }
+        }
+        float v[H / 512][8];
+        float amax = 0.0f;
 #pragma unroll
-  for (int r = 0; r < MAX_K; r++) {
-    if (r < k) {
-      const uint32_t m = wave_max_u32_v(lm);
-      mine = lane == r ? m : mine;
-      lm = 0u;
+        for (int k = 0; k < H / 512; k++) {
+          const uint32_t wv[4] = {(uint32_t)xraw[k].x, (uint32_t)xraw[k].y, (uint32_t)xraw[k].z, (uint32_t)xraw[k].w};
 #pragma unroll
-      for (int j = 0; j < KPL; j++) {
-        key[j] = key[j] == m ? 0u : key[j];
-        lm = max(lm, key[j]);
-      }
-    }
-  }
-  return mine;
+          for (int j = 0; j < 4; j++) {
+            v[k][2 * j] = bf16_to_f32(wv[j] & 0xFFFFu);
+            v[k][2 * j + 1] = bf16_to_f32(wv[j] >> 16);
+            amax = fmaxf(amax, fmaxf(fabsf(v[k][2 * j]), fabsf(v[k][2 * j + 1])));
+          }
+        }
+        amax = wave_max_f32(amax);
+        const float inv = amax > 0.0f ? QMAX / amax : 0.0f;
+#pragma unroll
+        for (int k = 0; k < H / 512; k++)
+          if (k == w) store_act8<F>(cx.xq + 512 * k + 8 * lane, v[k], inv);
+        if (lane == 0) {
+          cx.sx[0] = amax / QMAX;
+          cx.utok[u * MAX_M] = 0;
+          cx.upair[u * MAX_M] = (uint8_t)u;
+        }
+        lds_settle();
+      },
+      [&]() {
+        if (has_down) down_load<F, H, I>(cx, 0, i, d);
+      });
+  if (has_down) down_finish<F, H, I>(cx, 0, i, d);
 }
 
 template <int F, int H, int I>
@@ -564,6 +703,12 @@ __global__ void __launch_bounds__(256, 3) moe_a8_kernel(MoeA8Args a) {
   cx.slot_first = (int*)(lds + L.slot_first);
   cx.fparts = (float*)(lds + L.fparts);
   cx.epoch = launch_epoch();
+  // one row with a workgroup per gate_up tile (the grid the host picks for it): see one_row_layer
+  if (M == 1 && K8 * T >= NHB && (int)gridDim.x == K8 * T) {
+    if (E <= 128) one_row_layer<F, H, I, 2>(cx, (int)blockIdx.x);
+    else one_row_layer<F, H, I, 4>(cx, (int)blockIdx.x);
+    return;
+  }
 
   // ---- per row: routed by wave t % 4 and its activations quantized by wave (t + 1) % 4, so that with one row the
   // two loads and what follows them overlap; each wave issues its loads before using any of them
@@ -702,7 +847,8 @@ __global__ void __launch_bounds__(256, 3) moe_a8_kernel(MoeA8Args a) {
       if (c < cx.nch) {
         const int u0 = cx.chunk_first[c], ne = cx.chunk_first[c + 1] - u0;
         if (item < base + ne * T) {
-          gate_up_item<F, H, I>(cx, u0 + (item - base) / T, (item - base) % T, parity);
+          const int u = u0 + (item - base) / T;
+          gate_up_item<F, H, I>(cx, u, (item - base) % T, parity, cx.ulist[u], cx.ucount[u], [] {}, [] {});
           parity ^= 1;
           break;
         }
@@ -784,6 +930,8 @@ int launch_moe_a8(const d3_moe_a8_desc* d, hipStream_t stream) {
   if (!fn) return fail("d3_moe_a8: no kernel for this format and shape (H 2048; I 512 or 768)");
   if (!d->x || !d->logits || !d->gate_up || !d->gate_up_scale || !d->down || !d->down_scale || !d->out || !d->workspace)
     return fail("d3_moe_a8: null pointer");
+  if (((uintptr_t)d->gate_up_scale | (uintptr_t)d->down_scale) & 15u)
+    return fail("d3_moe_a8: scale tensors must be 16-byte aligned");
   const int64_t need = moe_a8_workspace_bytes(d->M, d->topk, d->H, d->I);
   if (d->workspace_bytes < need) return fail("d3_moe_a8: workspace too small");
   const Lds L(d->M, d->topk, d->H, d->I);
@@ -796,7 +944,11 @@ int launch_moe_a8(const d3_moe_a8_desc* d, hipStream_t stream) {
   const int nch = umax;
   const int items = umax * (d->I / 16) + nch * (d->H / 8);
   int grid = items < cap ? items : cap;
+  // one row: a workgroup per gate_up tile, the first H / 8 of them also taking a down block (one_row_layer), when the
+  // device holds them all at once
+  const int tiles = d->topk * (d->I / 16);
   if (d->grid > 0) grid = d->grid < grid ? d->grid : grid;
+  else if (d->M == 1 && tiles >= d->H / 8 && tiles <= cap) grid = tiles;
 
   MoeA8Args a;
   a.x = (const uint16_t*)d->x;
@@ -817,7 +969,6 @@ int launch_moe_a8(const d3_moe_a8_desc* d, hipStream_t stream) {
   a.E = d->E;
   a.topk = d->topk;
   a.spin_limit = d->spin_limit ? d->spin_limit : (1u << 20);
-  a.dn_start = d->dn_start < 0 ? 0 : d->dn_start > 256 ? 256 : d->dn_start;
   hipLaunchKernelGGL(fn, dim3(grid), dim3(256), L.total, stream, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return hip_fail(e, "d3_moe_a8 launch");

@@ -278,9 +278,14 @@ D3_INLINE void compute_tile(const PrefillArgs& a, const Weights<F, Geometry<F, H
   for (int t = 0; t < 2; t++) {
     f32x4 y;
     if constexpr (F == FMT_F8) {
-      f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+      f32x4 acc;
+      i32x8 fa[SW], fb[SW];
 #pragma unroll
-      for (int j = 0; j < SW; j++) acc = step_f8(wt.raw[t][j], lo[j], hi[j], acc);
+      for (int j = 0; j < SW; j++) {
+        fa[j] = f8_operand(wt.raw[t][j]);
+        fb[j] = f8_operand(lo[j], hi[j]);
+      }
+      acc = mfma_f8_chain<SW>(fa, fb);
 #pragma unroll
       for (int i = 0; i < 4; i++) y[i] = acc[i] * wt.rs[t][i];
     } else if constexpr (F == FMT_I8) {

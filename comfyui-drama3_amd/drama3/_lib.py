@@ -27,7 +27,7 @@ class MoeA8Desc(ctypes.Structure):
         ("down", c_void_p), ("down_scale", c_void_p), ("out", c_void_p), ("ids_out", c_void_p),
         ("weights_out", c_void_p), ("workspace", c_void_p), ("workspace_bytes", c_int64), ("format", c_int32),
         ("M", c_int32), ("H", c_int32), ("I", c_int32), ("E", c_int32), ("topk", c_int32), ("spin_limit", c_uint32),
-        ("grid", c_int32), ("dn_start", c_int32),
+        ("grid", c_int32),
     ]
 
 

@@ -57,7 +57,6 @@ def status(device, H, I, stream=None):
     return value.value
 
 
-DN_START = 0
 # From this many rows on, moe_layer runs the grouped path (d3_moe_a8_prefill): its persistent grouped products read
 # each expert once for all rows and keep the memory busy, where the fused kernel's items for several rows queue up
 # behind each other (measured on MI355X, W4A8: 4 rows 54 vs 61 us, 16 rows 92 vs 215 us).
@@ -65,7 +64,7 @@ GROUPED_FROM_ROWS = 4
 
 
 def moe_layer(x, logits, gate_up: A8Bank, down: A8Bank, topk, *, routing=False, spin_limit=0, grid=0, out=None,
-              dn_start=None, fused=None):
+              fused=None):
     """x [M, H] bf16 and router logits [M, E] bf16 (M <= 16) through the routed experts: [M, H] bf16, and with
     `routing` also (ids [M, topk] int64 in descending logit order, weights [M, topk] float32). Fewer than
     GROUPED_FROM_ROWS rows run the fused one-launch kernel (d3_moe_a8), more the grouped path (moe_prefill); `fused`
@@ -98,7 +97,7 @@ def moe_layer(x, logits, gate_up: A8Bank, down: A8Bank, topk, *, routing=False, 
         gate_up_scale=gate_up.scale.data_ptr(), down=down.weight.data_ptr(), down_scale=down.scale.data_ptr(),
         out=out.data_ptr(), ids_out=_lib.ptr(ids), weights_out=_lib.ptr(weights), workspace=ws.data_ptr(),
         workspace_bytes=ws.numel(), format=gate_up.fmt, M=M, H=H, I=I, E=E, topk=topk, spin_limit=spin_limit,
-        grid=grid, dn_start=DN_START if dn_start is None else dn_start)
+        grid=grid)
     _lib.check(_lib.lib().d3_moe_a8(ctypes.byref(desc), _lib.stream_of(device)), "d3_moe_a8")
     return (out, ids, weights) if routing else out
 

@@ -41,7 +41,7 @@ typedef struct d3_moe_a8_desc {
   const void* x;           /* [M, H] bf16 */
   const void* logits;      /* [M, E] bf16 router logits */
   const void* gate_up;     /* [E * 2I, row_bytes(H)] packed weights */
-  const void* gate_up_scale; /* bf16 scales (see formats) */
+  const void* gate_up_scale; /* bf16 scales (see formats); this and down_scale 16-byte aligned */
   const void* down;        /* [E * H, row_bytes(I)] */
   const void* down_scale;
   void* out;               /* [M, H] bf16 */
@@ -57,7 +57,6 @@ typedef struct d3_moe_a8_desc {
   int32_t topk;            /* <= 8 */
   uint32_t spin_limit;     /* bound on a workgroup's wait for another's result (0: default) */
   int32_t grid;            /* workgroups (0: as many as the device holds at once, capped by the work) */
-  int32_t dn_start;        /* down weights load once this many 256ths of gate_up is done (0: at once) */
 } d3_moe_a8_desc;
 
 int64_t d3_moe_a8_workspace_bytes(int32_t M, int32_t topk, int32_t H, int32_t I);

@@ -107,8 +107,8 @@ def fetcher(gate_up, down):
     return fetch
 
 
-def check_layer(fmt, x, logits, gate_up, down, topk=8, fused=True):
-    out, ids, w = moe.moe_layer(x, logits, gate_up, down, topk, routing=True, fused=fused)
+def check_layer(fmt, x, logits, gate_up, down, topk=8, fused=True, grid=0):
+    out, ids, w = moe.moe_layer(x, logits, gate_up, down, topk, routing=True, fused=fused, grid=grid)
     torch.cuda.synchronize()
     assert moe.status(DEV, x.shape[1], down.cols) == 0
     want, want_ids, want_w, _ = a8.moe_layer(bits(x), bits(logits), (gate_up.rows, gate_up.cols), (down.rows, down.cols),
@@ -133,6 +133,19 @@ def test_layer_matches_oracle(fmt, M):
     logits = torch.randn((M, 128), generator=gen, device=DEV).to(torch.bfloat16)
     check_layer(fmt, x, logits, gate_up, down)
 
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+def test_one_row_paths_agree(fmt):
+    """One row runs a workgroup per gate_up tile by default (gate_up tiles with the down blocks behind them); an
+    explicit grid of one workgroup per item runs the general schedule. Both match the oracle."""
+    gate_up, down = layer_banks(fmt)
+    gen = torch.Generator(device=DEV).manual_seed(21)
+    x = torch.randn((1, 2048), generator=gen, device=DEV).to(torch.bfloat16)
+    logits = torch.randn((1, 128), generator=gen, device=DEV).to(torch.bfloat16)
+    a = check_layer(fmt, x, logits, gate_up, down)
+    b = check_layer(fmt, x, logits, gate_up, down, grid=8 * 48 + 2048 // 8)
+    assert torch.equal(a, b)
 
 @pytest.mark.parametrize("fmt", [formats.FMT_I8, formats.FMT_W4])
 def test_layer_shared_experts(fmt):
