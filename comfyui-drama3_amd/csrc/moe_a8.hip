@@ -61,6 +61,18 @@ struct MoeA8Args {
   uint32_t* sync;
   int M, E, topk;
   uint32_t spin_limit;
+  // the block around the routed experts (one row): the router's weights [E, H] bf16 (logits computed in the launch
+  // instead of read), its logits out [E] bf16; the shared expert (one A8 expert of the layer's format and shape) and
+  // its gate [H] bf16
+  const uint16_t* router;
+  uint16_t* logits_out;
+  const uint8_t* sh_gu_w;
+  const uint16_t* sh_gu_s;
+  const uint8_t* sh_dn_w;
+  const uint16_t* sh_dn_s;
+  const uint16_t* sh_gate;
+  uint64_t* logitw;   // [E] tagged logits (router)
+  uint64_t* sharedw;  // [H] tagged: the shared expert's gated output, bf16-rounded
 };
 
 // LDS carve-up (bytes), shared by host (launch size) and device.
@@ -130,15 +142,18 @@ struct Ctx {
 // (`between` runs once the item's weight rows are on their way, before it reads the slot tables or x; `after` once its
 // products are done, before its reduction)
 template <int F, int H, int I, typename Between, typename After>
-D3_INLINE void gate_up_item(const Ctx& cx, int u, int tile, int parity, int e, int nu, Between between, After after) {
+D3_INLINE uint64_t gate_up_item(const Ctx& cx, int u, int tile, int parity, int e, int nu, Between between,
+                                After after, const uint8_t* gu_w, const uint16_t* gu_s) {
   constexpr int SPW = H / 512;  // steps per wave
   constexpr int RB = row_bytes(F, H);
   constexpr int SHIFT = unpack_shift(F);
   const MoeA8Args& a = *cx.a;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, q = lane >> 4, col = lane & 15;
-  uint64_t raised = 0;
+  // raise the expert's counter to (epoch, 0) with an atomic that returns nothing: waiting for its value here would
+  // hold the weight rows back by its round trip (loads complete in order)
+  uint64_t before = 0;
   if (tid == 0)
-    raised = __hip_atomic_fetch_max(done_counter(a.sync, u), (uint64_t)cx.epoch << 32, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_fetch_max(done_counter(a.sync, u), (uint64_t)cx.epoch << 32, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   const int ra = lane & 15;
   auto row_of = [&](int sub, int r) {
     return (size_t)e * (2 * I) + (r < 8 ? 16 * tile + 8 * sub + r : I + 16 * tile + 8 * sub + r - 8);
@@ -147,7 +162,7 @@ D3_INLINE void gate_up_item(const Ctx& cx, int u, int tile, int parity, int e, i
 #pragma unroll
   for (int sub = 0; sub < 2; sub++)
 #pragma unroll
-    for (int s = 0; s < SPW; s++) load_step<F>(raw[sub][s], a.gu_w + row_of(sub, ra) * RB, w * SPW + s, q);
+    for (int s = 0; s < SPW; s++) load_step<F>(raw[sub][s], gu_w + row_of(sub, ra) * RB, w * SPW + s, q);
   float sc[2][SPW][4];
   if constexpr (group_scaled(F)) {
 #pragma unroll
@@ -155,14 +170,14 @@ D3_INLINE void gate_up_item(const Ctx& cx, int u, int tile, int parity, int e, i
 #pragma unroll
       for (int i = 0; i < 4; i++)
 #pragma unroll
-        for (int s = 0; s < SPW; s++) sc[sub][s][i] = bf16_to_f32(a.gu_s[row_of(sub, 4 * q + i) * (H / 128) + w * SPW + s]);
+        for (int s = 0; s < SPW; s++) sc[sub][s][i] = bf16_to_f32(gu_s[row_of(sub, 4 * q + i) * (H / 128) + w * SPW + s]);
   }
   // row scales for the epilogue (wave 0, unit j = lane & 15), fetched with the rows
   float gs = 1.0f, us = 1.0f;
   if constexpr (!group_scaled(F)) {
     if (w == 0) {
-      gs = bf16_to_f32(a.gu_s[(size_t)e * (2 * I) + 16 * tile + (lane & 15)]);
-      us = bf16_to_f32(a.gu_s[(size_t)e * (2 * I) + I + 16 * tile + (lane & 15)]);
+      gs = bf16_to_f32(gu_s[(size_t)e * (2 * I) + 16 * tile + (lane & 15)]);
+      us = bf16_to_f32(gu_s[(size_t)e * (2 * I) + I + 16 * tile + (lane & 15)]);
     }
   }
   between();
@@ -242,12 +257,18 @@ D3_INLINE void gate_up_item(const Ctx& cx, int u, int tile, int parity, int e, i
       if (j == 0) put_tagged(a.tmax + (size_t)p * (I / 16) + tile, m, cx.epoch);
     }
     if (lane == 0) {
-      // the raise has returned (its value is used), so the add lands after it; a counter of a later epoch means the
-      // workspace was used on another queue: flag it
-      if ((uint32_t)(raised >> 32) > cx.epoch) __hip_atomic_fetch_or(a.sync + SYNC_STATUS, 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_fetch_add(done_counter(a.sync, u), (uint64_t)1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      // the add follows the raise to the same word from the same lane, so it lands after it. The count before the add
+      // goes back to the caller, who checks it once the workgroup's work is done (flag_later_epoch): a later epoch
+      // means the workspace was used on another queue.
+      before = __hip_atomic_fetch_add(done_counter(a.sync, u), (uint64_t)1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
+  return before;
+}
+
+// status bit 1 when a gate_up item found its expert's counter raised by a later launch (see gate_up_item)
+D3_INLINE void flag_later_epoch(const MoeA8Args& a, uint64_t before, uint32_t epoch) {
+  if ((uint32_t)(before >> 32) > epoch) __hip_atomic_fetch_or(a.sync + SYNC_STATUS, 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Top-k of a row's router logits (bf16 bits lb[j] for experts lane + 64 j, KPL of them per lane), one round at a time:
@@ -550,6 +571,14 @@ D3_INLINE void down_finish(const Ctx& cx, int c, int hb, const DownRows<F, I>& d
       const int t = idx >> 3, r = idx & 7;
       float acc = 0.0f;
       for (int j = 0; j < K8; j++) acc = fmaf(cx.lparts[cx.pair_slot[t * K8 + j] * 8 + r], cx.rt_w[t * MAX_K + j], acc);
+      if (a.sh_dn_w) {
+        // the shared expert's gated output of this row (one row): the block's sum of two bf16 tensors
+        const uint64_t* src = a.sharedw + 8 * hb + r;
+        uint64_t word = get_tagged_cached(src);
+        uint32_t polls = 0;
+        while (!tag_is(word, cx.epoch) && keep_polling(polls, a.sync + SYNC_STATUS, a.spin_limit)) word = get_tagged(src);
+        acc = bf16_round(acc) + tagged_value(word);
+      }
       a.out[(size_t)t * H + 8 * hb + r] = (uint16_t)f32_to_bf16(acc);
     }
   } else {
@@ -587,13 +616,204 @@ D3_INLINE void down_item(const Ctx& cx, int c, int hb) {
   down_finish<F, H, I>(cx, c, hb, d);
 }
 
-// One row (M = 1) with a workgroup for each gate_up tile: workgroup i computes gate_up tile i % T of the expert at
-// routing rank i / T and, for i < H / 8, down block i, so the down rows are requested only once the workgroup's
+// The router's logit e for one row: bf16(x . router[e]) with float sums (model.py:115), x as every wave holds it
+// (lane l: columns 512 k + 8 l .. + 7 of chunk k); published as a tagged word (its bf16 bits) for every routing wave.
+template <int H>
+D3_INLINE void router_logit(const MoeA8Args& a, uint32_t epoch, int e, const i32x4* xraw, int lane) {
+  const uint16_t* wr = a.router + (size_t)e * H;
+  float acc = 0.0f;
+#pragma unroll
+  for (int k = 0; k < H / 512; k++) {
+    const i32x4 wv = *(const i32x4*)(wr + 512 * k + 8 * lane);
+    const uint32_t xs[4] = {(uint32_t)xraw[k].x, (uint32_t)xraw[k].y, (uint32_t)xraw[k].z, (uint32_t)xraw[k].w};
+    const uint32_t ws[4] = {(uint32_t)wv.x, (uint32_t)wv.y, (uint32_t)wv.z, (uint32_t)wv.w};
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      acc = fmaf(bf16_to_f32(xs[j] & 0xFFFFu), bf16_to_f32(ws[j] & 0xFFFFu), acc);
+      acc = fmaf(bf16_to_f32(xs[j] >> 16), bf16_to_f32(ws[j] >> 16), acc);
+    }
+  }
+  const uint32_t bits = f32_to_bf16(wave_sum_f32(acc));
+  if (lane == 0) {
+    put_tagged(a.logitw + e, __uint_as_float(bits), epoch);
+    if (a.logits_out) a.logits_out[e] = (uint16_t)bits;
+  }
+}
+
+// The router's logits as bf16 bits for experts lane + 64 j, once every one is published (reads of words not yet
+// landed are repeated, bounded by spin_limit).
+template <int KPL>
+D3_INLINE void gather_logits(const MoeA8Args& a, uint32_t epoch, int lane, uint32_t* lb) {
+  uint64_t wv[KPL];
+#pragma unroll
+  for (int j = 0; j < KPL; j++) wv[j] = get_tagged_cached(a.logitw + min(lane + 64 * j, a.E - 1));
+  bool fresh = true;
+#pragma unroll
+  for (int j = 0; j < KPL; j++) fresh = fresh && tag_is(wv[j], epoch);
+  if (!__all(fresh)) {
+    uint32_t polls = 0;
+    while (true) {
+      bool ok = true;
+#pragma unroll
+      for (int j = 0; j < KPL; j++) {
+        if (!tag_is(wv[j], epoch)) wv[j] = get_tagged(a.logitw + min(lane + 64 * j, a.E - 1));
+        ok = ok && tag_is(wv[j], epoch);
+      }
+      if (__all(ok) || !keep_polling(polls, a.sync + SYNC_STATUS, a.spin_limit)) break;
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < KPL; j++) lb[j] = (uint32_t)wv[j] & 0xFFFFu;
+}
+
+// A block of 64 output rows of the shared expert for one row (wave w: rows 64 b + 16 w .. + 15, one 16-row MFMA tile
+// against the shared hidden row as column 0): its gated output bf16(bf16(sigmoid(bf16(x . gate))) * bf16(y)), as
+// model.py:123 rounds it, published as tagged words for the routed down blocks to add.
+template <int F, int H, int I>
+D3_INLINE void shared_down_block(const Ctx& cx, int b, const i32x4* xraw) {
+  constexpr int STEPS = I / 128;
+  constexpr int RB = row_bytes(F, I);
+  constexpr int SHIFT = unpack_shift(F);
+  constexpr float QMAX = act_qmax<F>();
+  constexpr int T = I / 16, G8 = I / 8, GPL = (G8 + 63) / 64;
+  static_assert(T <= 64, "a tile maximum per lane");
+  const MoeA8Args& a = *cx.a;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, q = lane >> 4, col = lane & 15;
+  const int K8 = a.topk;
+  const int r0 = 64 * b + 16 * w;
+  Raw<F> raw[STEPS];
+#pragma unroll
+  for (int s = 0; s < STEPS; s++) load_step<F>(raw[s], a.sh_dn_w + (size_t)(r0 + (lane & 15)) * RB, s, q);
+  // scales of accumulator rows r0 + 4q + i, as loaded (see DownRows)
+  uint32_t sw[group_scaled(F) ? 2 * STEPS : 2];
+  const uint16_t* sp = a.sh_dn_s + (size_t)(r0 + 4 * q) * (group_scaled(F) ? STEPS : 1);
+  if constexpr (group_scaled(F)) {
+#pragma unroll
+    for (int k = 0; k < STEPS / 2; k++) {
+      const i32x4 v = *(const i32x4*)(sp + 8 * k);
+      sw[4 * k] = (uint32_t)v.x;
+      sw[4 * k + 1] = (uint32_t)v.y;
+      sw[4 * k + 2] = (uint32_t)v.z;
+      sw[4 * k + 3] = (uint32_t)v.w;
+    }
+  } else {
+    const i32x2 v = *(const i32x2*)sp;
+    sw[0] = (uint32_t)v.x;
+    sw[1] = (uint32_t)v.y;
+  }
+  auto half = [&](int k) { return bf16_to_f32((k & 1) ? sw[k >> 1] >> 16 : sw[k >> 1] & 0xFFFFu); };
+  // the gate: x . shared_gate (model.py:123), then its sigmoid, each rounded to bf16 as the block's ops round them
+  float gsum = 0.0f;
+#pragma unroll
+  for (int k = 0; k < H / 512; k++) {
+    const i32x4 gv = *(const i32x4*)(a.sh_gate + 512 * k + 8 * lane);
+    const uint32_t xs[4] = {(uint32_t)xraw[k].x, (uint32_t)xraw[k].y, (uint32_t)xraw[k].z, (uint32_t)xraw[k].w};
+    const uint32_t gs[4] = {(uint32_t)gv.x, (uint32_t)gv.y, (uint32_t)gv.z, (uint32_t)gv.w};
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      gsum = fmaf(bf16_to_f32(xs[j] & 0xFFFFu), bf16_to_f32(gs[j] & 0xFFFFu), gsum);
+      gsum = fmaf(bf16_to_f32(xs[j] >> 16), bf16_to_f32(gs[j] >> 16), gsum);
+    }
+  }
+  const float gate = bf16_round(wave_sum_f32(gsum));
+  const float gw = bf16_round(1.0f / (1.0f + expf(-gate)));
+  // the shared hidden row (pair K8), gathered once this wave's rows have landed; words not yet published are read
+  // again after the expert's counter shows all its tiles
+  settle();
+  const uint64_t* hrow = a.hidden + (size_t)K8 * I;
+  const uint64_t* trow = a.tmax + (size_t)K8 * T;
+  uint64_t mw = get_tagged_cached(trow + min(lane, T - 1));
+  uint64_t vw[GPL][8];
+#pragma unroll
+  for (int k = 0; k < GPL; k++)
+#pragma unroll
+    for (int j = 0; j < 8; j++) vw[k][j] = get_tagged_cached(hrow + 8 * min(lane + 64 * k, G8 - 1) + j);
+  bool fresh = tag_is(mw, cx.epoch);
+#pragma unroll
+  for (int k = 0; k < GPL; k++)
+#pragma unroll
+    for (int j = 0; j < 8; j++) fresh = fresh && tag_is(vw[k][j], cx.epoch);
+  if (!__all(fresh)) {
+    if (lane == 0) {
+      uint32_t polls = 0;
+      const uint64_t want = ((uint64_t)cx.epoch << 32) | (uint32_t)T;
+      while (signal_load64(done_counter(a.sync, K8)) != want && keep_polling(polls, a.sync + SYNC_STATUS, a.spin_limit)) {
+      }
+    }
+    uint32_t polls = 0;
+    while (true) {
+      if (!tag_is(mw, cx.epoch)) mw = get_tagged(trow + min(lane, T - 1));
+      bool ok = tag_is(mw, cx.epoch);
+#pragma unroll
+      for (int k = 0; k < GPL; k++)
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+          if (!tag_is(vw[k][j], cx.epoch)) vw[k][j] = get_tagged(hrow + 8 * min(lane + 64 * k, G8 - 1) + j);
+          ok = ok && tag_is(vw[k][j], cx.epoch);
+        }
+      if (__all(ok) || !keep_polling(polls, a.sync + SYNC_STATUS, a.spin_limit)) break;
+    }
+  }
+  const float amax = wave_max_f32(tagged_value(mw));
+  const float inv = amax > 0.0f ? QMAX / amax : 0.0f;
+  uint8_t* hq = cx.hq + (size_t)w * I;  // this wave's own copy of the quantized row
+#pragma unroll
+  for (int k = 0; k < GPL; k++) {
+    const int g8 = lane + 64 * k;
+    if (g8 < G8) {
+      float v[8];
+#pragma unroll
+      for (int j = 0; j < 8; j++) v[j] = tagged_value(vw[k][j]);
+      store_act8<F>(hq + 8 * g8, v, inv);
+    }
+  }
+  lds_settle();
+  // rows r0 + 4q + i against the row (column 0)
+  i32x4 iacc = {0, 0, 0, 0};
+  f32x4 facc = {0.0f, 0.0f, 0.0f, 0.0f};
+  i32x8 fa[STEPS], fb[STEPS];
+#pragma unroll
+  for (int s = 0; s < STEPS; s++) {
+    i32x4 xlo = {0, 0, 0, 0}, xhi = {0, 0, 0, 0};
+    if (col == 0) {
+      xlo = *(const i32x4*)(hq + 128 * s + 32 * q);
+      xhi = *(const i32x4*)(hq + 128 * s + 32 * q + 16);
+    }
+    if constexpr (F == FMT_I8) {
+      iacc = step_i8<F>(raw[s], xlo, xhi, iacc);
+    } else if constexpr (F == FMT_F8) {
+      fa[s] = f8_operand(raw[s]);
+      fb[s] = f8_operand(xlo, xhi);
+    } else {
+      const i32x4 g = step_i8<F>(raw[s], xlo, xhi, i32x4{0, 0, 0, 0});
+#pragma unroll
+      for (int i = 0; i < 4; i++) facc[i] += (float)(g[i] >> SHIFT) * half(i * STEPS + s);
+    }
+  }
+  if constexpr (F == FMT_F8) facc = mfma_f8_chain<STEPS>(fa, fb);
+  if (col == 0) {
+    const float hs = amax / QMAX;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      float y;
+      if constexpr (F == FMT_I8) y = (float)iacc[i] * half(i);
+      else if constexpr (F == FMT_F8) y = facc[i] * half(i);
+      else y = facc[i];
+      put_tagged(a.sharedw + r0 + 4 * q + i, bf16_round(gw * bf16_round(y * hs)), cx.epoch);
+    }
+  }
+}
+
+// One row (M = 1) with a workgroup for each gate_up tile: workgroup i < k T computes gate_up tile i % T of the expert
+// at routing rank i / T and, for i < H / 8, down block i, so the down rows are requested only once the workgroup's
 // gate_up rows have arrived and the gate_up rows, which the hand-off waits for, are not queued behind them.
 // Every wave routes the row itself and its gate_up rows go out after the rounds that name their expert (no workgroup
 // barrier before them); the remaining rounds, the softmax, the x slice its MFMA steps read (H = 2048: wave w reads x
 // chunk w) and the slot tables are written while they are in flight. Every wave writes the same values, so nothing
 // waits for another wave until the gate_up reduction.
+// The block around the experts: with a router, workgroups 0 .. E-1 first compute one logit each and every routing
+// wave gathers them; with a shared expert, workgroups k T .. k T + T - 1 compute its gate_up tiles (hidden row k)
+// and the next H / 64 its output in blocks of 64 rows, which the down blocks add to the routed sum.
 template <int F, int H, int I, int KPL>
 D3_INLINE void one_row_layer(Ctx& cx, int i) {
   static_assert(H == 2048, "wave w's K slice is x chunk w");
@@ -602,22 +822,35 @@ D3_INLINE void one_row_layer(Ctx& cx, int i) {
   const MoeA8Args& a = *cx.a;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int E = a.E, K8 = a.topk;
-  const int u = i / T, tile = i % T;
-  const bool has_down = i < NHB;
+  const int routed = K8 * T;
+  const bool is_shared = i >= routed;
+  // given logits go out first: routing waits for them, and a wave's loads complete in order
   uint32_t lb[KPL];
 #pragma unroll
-  for (int j = 0; j < KPL; j++) lb[j] = a.logits[min(lane + 64 * j, E - 1)];
+  for (int j = 0; j < KPL; j++) lb[j] = 0u;
+  if (!a.router && !is_shared) {
+#pragma unroll
+    for (int j = 0; j < KPL; j++) lb[j] = a.logits[min(lane + 64 * j, E - 1)];
+  }
   i32x4 xraw[H / 512];
 #pragma unroll
   for (int k = 0; k < H / 512; k++) xraw[k] = *(const i32x4*)(a.x + 512 * k + 8 * lane);
+  if (a.router && i < E && w == 0) router_logit<H>(a, cx.epoch, i, xraw, lane);
+  if (i >= routed + T) {
+    shared_down_block<F, H, I>(cx, i - routed - T, xraw);
+    return;
+  }
+  const int u = is_shared ? K8 : i / T, tile = is_shared ? i - routed : i % T;
+  const bool has_down = i < NHB;
+  if (a.router && !is_shared) gather_logits<KPL>(a, cx.epoch, lane, lb);
   TopKeys<KPL> tk(lb, lane, E);
-  tk.rounds(lane, 0, u + 1);
-  const int e = route_key_index((uint32_t)__builtin_amdgcn_readlane((int)tk.mine, u));
+  if (!is_shared) tk.rounds(lane, 0, u + 1);
+  const int e = is_shared ? 0 : route_key_index((uint32_t)__builtin_amdgcn_readlane((int)tk.mine, u));
   cx.U = K8;
   cx.nch = 1;
   cx.n_dn = NHB;
   DownRows<F, I> d;
-  gate_up_item<F, H, I>(
+  const uint64_t before = gate_up_item<F, H, I>(
       cx, u, tile, 0, e, 1,
       [&]() {
         if (has_down) {
@@ -669,19 +902,15 @@ D3_INLINE void one_row_layer(Ctx& cx, int i) {
       },
       [&]() {
         if (has_down) down_load<F, H, I>(cx, 0, i, d);
-      });
+      },
+      is_shared ? a.sh_gu_w : a.gu_w, is_shared ? a.sh_gu_s : a.gu_s);
   if (has_down) down_finish<F, H, I>(cx, 0, i, d);
+  flag_later_epoch(a, before, cx.epoch);
 }
 
-template <int F, int H, int I>
-__global__ void __launch_bounds__(256, 3) moe_a8_kernel(MoeA8Args a) {
-  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-  constexpr int T = I / 16;
-  constexpr int NHB = H / 8;
-  constexpr float QMAX = act_qmax<F>();
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int M = a.M, E = a.E, K8 = a.topk;
-  const Lds L(M, K8, H, I);
+// a workgroup's view of its LDS and the launch
+D3_INLINE Ctx make_ctx(const MoeA8Args& a, uint8_t* lds, int H, int I) {
+  const Lds L(a.M, a.topk, H, I);
   Ctx cx;
   cx.a = &a;
   cx.xq = lds + L.xq;
@@ -703,12 +932,28 @@ __global__ void __launch_bounds__(256, 3) moe_a8_kernel(MoeA8Args a) {
   cx.slot_first = (int*)(lds + L.slot_first);
   cx.fparts = (float*)(lds + L.fparts);
   cx.epoch = launch_epoch();
-  // one row with a workgroup per gate_up tile (the grid the host picks for it): see one_row_layer
-  if (M == 1 && K8 * T >= NHB && (int)gridDim.x == K8 * T) {
-    if (E <= 128) one_row_layer<F, H, I, 2>(cx, (int)blockIdx.x);
-    else one_row_layer<F, H, I, 4>(cx, (int)blockIdx.x);
-    return;
-  }
+  return cx;
+}
+
+// The one-row schedule as its own kernel: at most k I / 16 + I / 16 + H / 64 workgroups, fewer than two per CU, so
+// it is compiled for two per CU (256 registers a lane) and keeps its weight rows, routing state and x in registers.
+template <int F, int H, int I>
+__global__ void __launch_bounds__(256, 2) moe_a8_one_row_kernel(MoeA8Args a) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  Ctx cx = make_ctx(a, lds, H, I);
+  if (a.E <= 128) one_row_layer<F, H, I, 2>(cx, (int)blockIdx.x);
+  else one_row_layer<F, H, I, 4>(cx, (int)blockIdx.x);
+}
+
+template <int F, int H, int I>
+__global__ void __launch_bounds__(256, 3) moe_a8_kernel(MoeA8Args a) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  constexpr int T = I / 16;
+  constexpr int NHB = H / 8;
+  constexpr float QMAX = act_qmax<F>();
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int M = a.M, E = a.E, K8 = a.topk;
+  Ctx cx = make_ctx(a, lds, H, I);
 
   // ---- per row: routed by wave t % 4 and its activations quantized by wave (t + 1) % 4, so that with one row the
   // two loads and what follows them overlap; each wave issues its loads before using any of them
@@ -848,7 +1093,10 @@ __global__ void __launch_bounds__(256, 3) moe_a8_kernel(MoeA8Args a) {
         const int u0 = cx.chunk_first[c], ne = cx.chunk_first[c + 1] - u0;
         if (item < base + ne * T) {
           const int u = u0 + (item - base) / T;
-          gate_up_item<F, H, I>(cx, u, (item - base) % T, parity, cx.ulist[u], cx.ucount[u], [] {}, [] {});
+          flag_later_epoch(a,
+                           gate_up_item<F, H, I>(cx, u, (item - base) % T, parity, cx.ulist[u], cx.ucount[u], [] {},
+                                                 [] {}, a.gu_w, a.gu_s),
+                           cx.epoch);
           parity ^= 1;
           break;
         }
@@ -881,18 +1129,22 @@ int hip_fail(hipError_t err, const char* what) {
   return (int)err;
 }
 
+// sync words, then (pairs + 1 for the shared expert) hidden rows and tile maxima, the pairs' partial outputs, and for
+// the block's router and shared expert MAX_E logit words and H output words
 int64_t moe_a8_workspace_bytes(int M, int topk, int H, int I) {
   const int64_t pairs = (int64_t)M * topk;
-  return SYNC_WORDS * 4 + pairs * I * 8 + pairs * (I / 16) * 8 + pairs * H * 8;
+  return SYNC_WORDS * 4 + (pairs + 1) * I * 8 + (pairs + 1) * (I / 16) * 8 + pairs * H * 8 + (MAX_E + H) * 8;
 }
 
 using KernelFn = void (*)(MoeA8Args);
 
-template <int F, int H, int I> KernelFn kernel_of() { return moe_a8_kernel<F, H, I>; }
+template <int F, int H, int I> KernelFn kernel_of(bool one_row) {
+  return one_row ? moe_a8_one_row_kernel<F, H, I> : moe_a8_kernel<F, H, I>;
+}
 
-KernelFn pick_kernel(int fmt, int H, int I) {
+KernelFn pick_kernel(int fmt, int H, int I, bool one_row = false) {
 #define D3_CASE(F, HH, II) \
-  if (fmt == F && H == HH && I == II) return kernel_of<F, HH, II>();
+  if (fmt == F && H == HH && I == II) return kernel_of<F, HH, II>(one_row);
 #define D3_SHAPES(F) D3_CASE(F, 2048, 768) D3_CASE(F, 2048, 512)
   D3_SHAPES(FMT_I8) D3_SHAPES(FMT_W4) D3_SHAPES(FMT_W6) D3_SHAPES(FMT_F8)
 #undef D3_SHAPES
@@ -928,9 +1180,15 @@ int launch_moe_a8(const d3_moe_a8_desc* d, hipStream_t stream) {
   if (d->E < d->topk || d->E > MAX_E) return fail("d3_moe_a8: E must be topk..256");
   KernelFn fn = pick_kernel(d->format, d->H, d->I);
   if (!fn) return fail("d3_moe_a8: no kernel for this format and shape (H 2048; I 512 or 768)");
-  if (!d->x || !d->logits || !d->gate_up || !d->gate_up_scale || !d->down || !d->down_scale || !d->out || !d->workspace)
+  if (!d->x || !(d->logits || d->router) || !d->gate_up || !d->gate_up_scale || !d->down || !d->down_scale || !d->out ||
+      !d->workspace)
     return fail("d3_moe_a8: null pointer");
   if (((uintptr_t)d->gate_up_scale | (uintptr_t)d->down_scale) & 15u)
+    return fail("d3_moe_a8: scale tensors must be 16-byte aligned");
+  const bool shared = d->shared_gate_up != nullptr;
+  if (shared && (!d->shared_gate_up_scale || !d->shared_down || !d->shared_down_scale || !d->shared_gate))
+    return fail("d3_moe_a8: the shared expert needs gate_up, down, their scales and its gate");
+  if (shared && (((uintptr_t)d->shared_gate_up_scale | (uintptr_t)d->shared_down_scale) & 15u))
     return fail("d3_moe_a8: scale tensors must be 16-byte aligned");
   const int64_t need = moe_a8_workspace_bytes(d->M, d->topk, d->H, d->I);
   if (d->workspace_bytes < need) return fail("d3_moe_a8: workspace too small");
@@ -946,9 +1204,16 @@ int launch_moe_a8(const d3_moe_a8_desc* d, hipStream_t stream) {
   int grid = items < cap ? items : cap;
   // one row: a workgroup per gate_up tile, the first H / 8 of them also taking a down block (one_row_layer), when the
   // device holds them all at once
-  const int tiles = d->topk * (d->I / 16);
+  const int tiles = d->topk * (d->I / 16) + (shared ? d->I / 16 + d->H / 64 : 0);
+  KernelFn fn1 = pick_kernel(d->format, d->H, d->I, true);
+  const int cap1 = resident_capacity(fn1, L.total, &err);
+  if (err) return err;
+  const bool one_row = d->grid <= 0 && d->M == 1 && d->topk * (d->I / 16) >= d->H / 8 && tiles <= cap1 &&
+                       (!d->router || tiles >= d->E);
   if (d->grid > 0) grid = d->grid < grid ? d->grid : grid;
-  else if (d->M == 1 && tiles >= d->H / 8 && tiles <= cap) grid = tiles;
+  else if (one_row) grid = tiles;
+  if ((d->router || shared) && !one_row)
+    return fail("d3_moe_a8: the router and the shared expert run in the one-row schedule (M = 1, grid 0)");
 
   MoeA8Args a;
   a.x = (const uint16_t*)d->x;
@@ -962,14 +1227,24 @@ int launch_moe_a8(const d3_moe_a8_desc* d, hipStream_t stream) {
   a.weights_out = d->weights_out;
   uint8_t* ws = (uint8_t*)d->workspace;
   a.sync = (uint32_t*)ws;
+  const size_t pairs = (size_t)d->M * d->topk;
   a.hidden = (uint64_t*)(ws + SYNC_WORDS * 4);
-  a.tmax = a.hidden + (size_t)d->M * d->topk * d->I;
-  a.parts = a.tmax + (size_t)d->M * d->topk * (d->I / 16);
+  a.tmax = a.hidden + (pairs + 1) * d->I;
+  a.parts = a.tmax + (pairs + 1) * (d->I / 16);
+  a.logitw = a.parts + pairs * d->H;
+  a.sharedw = a.logitw + MAX_E;
   a.M = d->M;
   a.E = d->E;
   a.topk = d->topk;
   a.spin_limit = d->spin_limit ? d->spin_limit : (1u << 20);
-  hipLaunchKernelGGL(fn, dim3(grid), dim3(256), L.total, stream, a);
+  a.router = (const uint16_t*)d->router;
+  a.logits_out = (uint16_t*)d->logits_out;
+  a.sh_gu_w = (const uint8_t*)d->shared_gate_up;
+  a.sh_gu_s = (const uint16_t*)d->shared_gate_up_scale;
+  a.sh_dn_w = (const uint8_t*)d->shared_down;
+  a.sh_dn_s = (const uint16_t*)d->shared_down_scale;
+  a.sh_gate = (const uint16_t*)d->shared_gate;
+  hipLaunchKernelGGL(one_row ? fn1 : fn, dim3(grid), dim3(256), L.total, stream, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return hip_fail(e, "d3_moe_a8 launch");
   return 0;

@@ -27,7 +27,9 @@ class MoeA8Desc(ctypes.Structure):
         ("down", c_void_p), ("down_scale", c_void_p), ("out", c_void_p), ("ids_out", c_void_p),
         ("weights_out", c_void_p), ("workspace", c_void_p), ("workspace_bytes", c_int64), ("format", c_int32),
         ("M", c_int32), ("H", c_int32), ("I", c_int32), ("E", c_int32), ("topk", c_int32), ("spin_limit", c_uint32),
-        ("grid", c_int32),
+        ("grid", c_int32), ("router", c_void_p), ("logits_out", c_void_p), ("shared_gate_up", c_void_p),
+        ("shared_gate_up_scale", c_void_p), ("shared_down", c_void_p), ("shared_down_scale", c_void_p),
+        ("shared_gate", c_void_p),
     ]
 
 

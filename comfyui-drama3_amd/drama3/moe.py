@@ -102,6 +102,67 @@ def moe_layer(x, logits, gate_up: A8Bank, down: A8Bank, topk, *, routing=False, 
     return (out, ids, weights) if routing else out
 
 
+def moe_block(x, gate_up: A8Bank, down: A8Bank, topk, *, router=None, logits=None, shared=None, shared_gate=None,
+              routing=False, return_logits=False, out=None):
+    """SparseMoeBlock.forward for one decode row (drama3/model.py:107-124) in one launch: x [1, H] bf16 -> [1, H] bf16.
+
+    The router: `router` [E, H] bf16 (its logits computed in the launch, model.py:115) or given `logits` [1, E] bf16.
+    The shared expert: `shared` = (gate_up, down) A8Banks of one expert in the layer's format and shape, and
+    `shared_gate` [H] bf16; it is added as model.py:123 does (both terms bf16). With `routing` also returns ids and
+    weights, with `return_logits` the router's logits [1, E] bf16."""
+    if x.dtype != torch.bfloat16 or x.dim() != 2 or x.shape[0] != 1:
+        raise ValueError("x [1, H] bfloat16 expected: the block runs one row")
+    H = x.shape[1]
+    E = gate_up.experts
+    if gate_up.fmt != down.fmt or down.experts != E or gate_up.cols != H or down.rows != H or gate_up.rows != 2 * down.cols:
+        raise ValueError("gate_up [E * 2I, H] and down [E * H, I] of one format expected")
+    I = down.cols
+    device = x.device
+    if (router is None) == (logits is None):
+        raise ValueError("router or logits, one of them")
+    if router is not None:
+        if router.dtype != torch.bfloat16 or router.shape != (E, H):
+            raise ValueError("router [E, H] bfloat16 expected")
+        router = router.contiguous()
+    else:
+        if logits.dtype != torch.bfloat16 or logits.shape != (1, E):
+            raise ValueError("logits [1, E] bfloat16 expected")
+        logits = logits.contiguous()
+    sg = sd = None
+    if shared is not None:
+        sg, sd = shared
+        if (sg.fmt, sd.fmt) != (gate_up.fmt, gate_up.fmt) or sg.experts != 1 or sd.experts != 1 or \
+                (sg.rows, sg.cols, sd.rows, sd.cols) != (2 * I, H, H, I):
+            raise ValueError("the shared expert: one expert of the layer's format and shape")
+        if shared_gate is None or shared_gate.dtype != torch.bfloat16 or shared_gate.numel() != H:
+            raise ValueError("shared_gate [H] bfloat16 expected")
+        shared_gate = shared_gate.contiguous()
+    x = x.contiguous()
+    if out is None:
+        out = torch.empty((1, H), dtype=torch.bfloat16, device=device)
+    ids = torch.empty((1, topk), dtype=torch.int64, device=device) if routing else None
+    weights = torch.empty((1, topk), dtype=torch.float32, device=device) if routing else None
+    lg_out = torch.empty((1, E), dtype=torch.bfloat16, device=device) if return_logits else None
+    ws = workspace(device, H, I)
+    desc = _lib.MoeA8Desc(
+        x=x.data_ptr(), logits=_lib.ptr(logits), gate_up=gate_up.weight.data_ptr(),
+        gate_up_scale=gate_up.scale.data_ptr(), down=down.weight.data_ptr(), down_scale=down.scale.data_ptr(),
+        out=out.data_ptr(), ids_out=_lib.ptr(ids), weights_out=_lib.ptr(weights), workspace=ws.data_ptr(),
+        workspace_bytes=ws.numel(), format=gate_up.fmt, M=1, H=H, I=I, E=E, topk=topk, spin_limit=0, grid=0,
+        router=_lib.ptr(router), logits_out=_lib.ptr(lg_out),
+        shared_gate_up=_lib.ptr(sg.weight if sg is not None else None),
+        shared_gate_up_scale=_lib.ptr(sg.scale if sg is not None else None),
+        shared_down=_lib.ptr(sd.weight if sd is not None else None),
+        shared_down_scale=_lib.ptr(sd.scale if sd is not None else None), shared_gate=_lib.ptr(shared_gate))
+    _lib.check(_lib.lib().d3_moe_a8(ctypes.byref(desc), _lib.stream_of(device)), "d3_moe_a8")
+    res = (out,)
+    if routing:
+        res += (ids, weights)
+    if return_logits:
+        res += (lg_out,)
+    return res if len(res) > 1 else out
+
+
 def moe_prefill(x, gate_up: A8Bank, down: A8Bank, topk, *, logits=None, topk_idx=None, topk_weight=None,
                 routing=False, out=None):
     """Many rows x [T, H] bf16 through the routed experts of A8 banks: [T, H] bf16 (d3_moe_a8_prefill). Routing from

@@ -57,6 +57,17 @@ typedef struct d3_moe_a8_desc {
   int32_t topk;            /* <= 8 */
   uint32_t spin_limit;     /* bound on a workgroup's wait for another's result (0: default) */
   int32_t grid;            /* workgroups (0: as many as the device holds at once, capped by the work) */
+  /* The block around the routed experts, SparseMoeBlock.forward (drama3/model.py:107-124), for one row (M = 1, grid
+   * 0): with `router` the logits are computed in the launch, bf16(x . router[e]) (model.py:115), and `logits` may be
+   * NULL; with the shared expert, out = bf16(experts + bf16(bf16(sigmoid(bf16(x . shared_gate))) * bf16(shared(x))))
+   * as model.py:123 rounds it. NULL: not used. */
+  const void* router;        /* [E, H] bf16 */
+  void* logits_out;          /* [E] bf16 router logits, or NULL */
+  const void* shared_gate_up;        /* [2I, row_bytes(H)]: one expert in the layer's format */
+  const void* shared_gate_up_scale;
+  const void* shared_down;           /* [H, row_bytes(I)] */
+  const void* shared_down_scale;
+  const void* shared_gate;           /* [H] bf16 (shared_expert_gate, one output) */
 } d3_moe_a8_desc;
 
 int64_t d3_moe_a8_workspace_bytes(int32_t M, int32_t topk, int32_t H, int32_t I);

@@ -171,6 +171,16 @@ def project(packed, scale_bits, fmt, act_codes, act_scale):
 
 
 # ------------------------------------------------------------------------------------------------------------ layer
+def expert_output(xq, xs, gu, dn, fmt, I):
+    """One expert on one row's quantized activations (xq [1, H] codes, xs [1] scale): gate_up, SiLU(gate) * up, the
+    hidden row quantized per row, down. gu / dn = (packed rows, scale bits). Returns (out float64 [H], hidden [I])."""
+    y = project(gu[0], gu[1], fmt, xq, xs)[0]  # [2I]
+    g, u = y[:I], y[I:]
+    h = g / (1.0 + np.exp(-g)) * u
+    hq, hs = quantize_act(h.astype(np.float32)[None, :], fmt)
+    return project(dn[0], dn[1], fmt, hq, hs)[0], h
+
+
 def moe_layer(x_bits, logits_bits, gate_up, down, fmt, topk, fetch):
     """The fused layer for rows x [M, H] (bf16 bits) and logits [M, E] (bf16 bits).
 
@@ -188,14 +198,35 @@ def moe_layer(x_bits, logits_bits, gate_up, down, fmt, topk, fetch):
         acc = 0.0
         for j in range(topk):
             e = int(ids[m, j])
-            gu_w, gu_s = fetch("gate_up", e)
-            y = project(gu_w, gu_s, fmt, xq[m:m + 1], xs[m:m + 1])[0]  # [2I]
-            g, u = y[:I], y[I:]
-            h = g / (1.0 + np.exp(-g)) * u
-            hidden[m, j] = h
-            hq, hs = quantize_act(h.astype(np.float32)[None, :], fmt)
-            dn_w, dn_s = fetch("down", e)
-            part = project(dn_w, dn_s, fmt, hq, hs)[0]  # [H]
+            part, hidden[m, j] = expert_output(xq[m:m + 1], xs[m:m + 1], fetch("gate_up", e), fetch("down", e), fmt, I)
             acc = acc + float(w[m, j]) * part
         out[m] = acc
     return f32_to_bf16_bits(out.astype(np.float32)), ids, w, hidden
+
+
+# ------------------------------------------------------------------------------------------------------------ block
+def router_logits(x_bits, router_bits):
+    """The router's linear (model.py:115): bf16(x . router[e]) [M, E], from float64 sums."""
+    x = bf16_bits_to_f32(x_bits).astype(np.float64)
+    w = bf16_bits_to_f32(router_bits).astype(np.float64)
+    return f32_to_bf16_bits((x @ w.T).astype(np.float32))
+
+
+def moe_block(x_bits, gate_up, down, fmt, topk, fetch, logits_bits, shared=None, shared_gate_bits=None):
+    """SparseMoeBlock.forward for one row (model.py:107-124) on A8 banks: the routed experts as moe_layer, then with
+    `shared` = ((gate_up packed, scale bits), (down packed, scale bits)) of one expert and its gate [H] (bf16 bits)
+    the sum the block forms from bf16 tensors: out = bf16(experts + bf16(bf16(sigmoid(bf16(x . gate))) *
+    bf16(shared(x)))) (model.py:123). Returns (out bf16 bits [1, H], ids, weights)."""
+    out_bits, ids, w, _ = moe_layer(x_bits, logits_bits, gate_up, down, fmt, topk, fetch)
+    if shared is None:
+        return out_bits, ids, w
+    x = bf16_bits_to_f32(x_bits)
+    xq, xs = quantize_act(x, fmt)
+    y, _ = expert_output(xq[0:1], xs[0:1], shared[0], shared[1], fmt, down[1])
+    y = bf16_round(y.astype(np.float32))
+    g = bf16_bits_to_f32(shared_gate_bits).astype(np.float64).reshape(-1)
+    gate = float(np.asarray(bf16_round(np.float32(x[0].astype(np.float64) @ g))).reshape(-1)[0])
+    gw = float(np.asarray(bf16_round(np.float32(1.0 / (1.0 + np.exp(-gate))))).reshape(-1)[0])
+    prod = bf16_round((np.float32(gw) * y).astype(np.float32))
+    out = bf16_bits_to_f32(out_bits).astype(np.float32) + prod
+    return f32_to_bf16_bits(out.astype(np.float32)), ids, w

@@ -221,3 +221,49 @@ def test_layer_dispatch_matches_oracle(M):
     x = torch.randn((M, 2048), generator=gen, device=DEV).to(torch.bfloat16)
     logits = torch.randn((M, 128), generator=gen, device=DEV).to(torch.bfloat16)
     check_layer(formats.FMT_W4, x, logits, gate_up, down, fused=None)
+
+
+def block_inputs(fmt, seed):
+    gate_up, down = layer_banks(fmt)
+    gen = torch.Generator(device=DEV).manual_seed(seed)
+    x = torch.randn((1, 2048), generator=gen, device=DEV).to(torch.bfloat16)
+    router = (torch.randn((128, 2048), generator=gen, device=DEV) * 0.02).to(torch.bfloat16)
+    sg = formats.quantize(torch.randn((1, 2 * 768, 2048), generator=gen, device=DEV) * 0.02, fmt)
+    sd = formats.quantize(torch.randn((1, 2048, 768), generator=gen, device=DEV) * 0.02, fmt)
+    g = (torch.randn((2048,), generator=gen, device=DEV) * 0.05).to(torch.bfloat16)
+    return gate_up, down, x, router, (sg, sd), g
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+def test_block_router_and_shared_expert(fmt):
+    """SparseMoeBlock.forward for one row in one launch (model.py:107-124): the router's logits within one bf16 step
+    of its float64 sums (the kernel sums in float32), the routing from those logits exact, the output against the
+    oracle's block from the same logits within the layer's bar (the shared term adds two bf16 roundings)."""
+    gate_up, down, x, router, (sg, sd), g = block_inputs(fmt, 31)
+    out, ids, w, lg = moe.moe_block(x, gate_up, down, 8, router=router, shared=(sg, sd), shared_gate=g, routing=True,
+                                    return_logits=True)
+    torch.cuda.synchronize()
+    assert moe.status(DEV, 2048, 768) == 0
+    got_lg = bf16_bits_to_f32(bits(lg)).astype(np.float64)
+    ref_lg = bf16_bits_to_f32(a8.router_logits(bits(x), bits(router))).astype(np.float64)
+    assert np.all(np.abs(got_lg - ref_lg) <= np.abs(ref_lg) * 2.0 ** -7 + 1e-6)
+    shared = tuple((b.weight.cpu().numpy(), b.scale.contiguous().view(torch.int16).cpu().numpy().view(np.uint16))
+                   for b in (sg, sd))
+    want, want_ids, want_w = a8.moe_block(bits(x), (gate_up.rows, gate_up.cols), (down.rows, down.cols), fmt, 8,
+                                          fetcher(gate_up, down), bits(lg), shared, bits(g))
+    assert np.array_equal(ids.cpu().numpy(), want_ids)
+    assert np.all(np.abs(w.cpu().numpy() - want_w) <= np.abs(want_w) * 2.0 ** -8 + 1e-30)
+    got = bf16_bits_to_f32(bits(out)).astype(np.float64)
+    ref = bf16_bits_to_f32(want).astype(np.float64)
+    err = np.abs(got - ref)
+    assert err.max() <= 2e-2 * np.abs(ref).max(), (err.max(), np.abs(ref).max())
+    assert np.linalg.norm(got - ref) <= 1e-2 * np.linalg.norm(ref)
+    # the same block from the logits given: identical; the router alone: the layer on its logits, identical
+    assert torch.equal(moe.moe_block(x, gate_up, down, 8, logits=lg, shared=(sg, sd), shared_gate=g), out)
+    assert torch.equal(moe.moe_block(x, gate_up, down, 8, router=router), moe.moe_layer(x, lg, gate_up, down, 8))
+
+
+def test_block_rejects_more_rows():
+    gate_up, down, x, router, shared, g = block_inputs(formats.FMT_I8, 32)
+    with pytest.raises(ValueError):
+        moe.moe_block(torch.cat([x, x]), gate_up, down, 8, router=router)
