@@ -53,14 +53,14 @@ def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
 
-def make_layers(fmt, layers, device, seed=0):
+def make_layers(fmt, layers, device, seed=0, experts=E):
     gen = torch.Generator(device=device).manual_seed(seed)
     banks = []
     for _ in range(layers):
-        gu = torch.randn((E, 2 * I, H), generator=gen, device=device) * 0.02
+        gu = torch.randn((experts, 2 * I, H), generator=gen, device=device) * 0.02
         gate_up = formats.quantize(gu, fmt)
         del gu
-        dn = torch.randn((E, H, I), generator=gen, device=device) * 0.02
+        dn = torch.randn((experts, H, I), generator=gen, device=device) * 0.02
         down = formats.quantize(dn, fmt)
         del dn
         banks.append((gate_up, down))
@@ -208,8 +208,58 @@ def run_decode(args, fmt, device):
     config = {"workload": f"routed-expert MoE layer, {args.format} experts, decode M={M}, hidden {H}, FFN {I}, "
                           f"{E} experts top-{TOPK} ({args.routing} routing), {L} layers chained per token",
               "rows": M, "layers": L, "unique_experts_per_launch": round(sum(unique) / len(unique), 2)}
-    kernel = "d3::moe_a8_kernel" if M < moe.GROUPED_FROM_ROWS else "d3_moe_a8_prefill (7 launches)"
+    kernel = "d3::moe_a8_one_row_kernel" if M == 1 else "d3::moe_a8_kernel" if M < moe.GROUPED_FROM_ROWS else \
+        "d3_moe_a8_prefill (7 launches)"
     return ms, total_bytes, launches, args.steps * M, config, kernel, cpu
+
+
+def run_block(args, fmt, device):
+    """SparseMoeBlock.forward for one decode row in one launch (moe.moe_block): the router's logits from its bf16
+    weights [E, H], the routed experts, and a shared expert of the layer's format and shape with its gate, per layer.
+    Algorithmic bytes: the routed experts read, the shared expert, the router and gate rows, x and out."""
+    L = args.layers
+    log(f"building {L} layers of {args.format} experts, routers and shared experts")
+    banks = make_layers(fmt, L, device)
+    shared = make_layers(fmt, L, device, seed=5, experts=1)
+    gen = torch.Generator(device=device).manual_seed(4)
+    routers = [(torch.randn((E, H), generator=gen, device=device) * 0.02).to(torch.bfloat16) for _ in range(L)]
+    gates = [(torch.randn((H,), generator=gen, device=device) * 0.05).to(torch.bfloat16) for _ in range(L)]
+    x0 = torch.randn((GRAPH_TOKENS, 1, H), generator=gen, device=device).to(torch.bfloat16)
+    unique = []
+    for t in range(GRAPH_TOKENS):
+        x = x0[t]
+        for layer, (gate_up, down) in enumerate(banks):
+            x, ids, _ = moe.moe_block(x, gate_up, down, TOPK, router=routers[layer], shared=shared[layer],
+                                      shared_gate=gates[layer], routing=True)
+            unique.append(len(torch.unique(ids)))
+    torch.cuda.synchronize()
+    per_expert = expert_bytes(*banks[0])
+    fixed = expert_bytes(*shared[0]) + E * H * 2 + H * 2 + 2 * H * 2
+    bytes_per_token = [sum(unique[t * L:(t + 1) * L]) * per_expert + L * fixed for t in range(GRAPH_TOKENS)]
+    stream = torch.cuda.Stream(device)
+    stream.wait_stream(torch.cuda.current_stream(device))
+    graphs = []
+    with torch.cuda.stream(stream):
+        moe.prepare(device, H, I, stream)
+        bufs = [x0[t].clone() for t in range(GRAPH_TOKENS)]
+        for t in range(GRAPH_TOKENS):
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=stream):
+                x = bufs[t]
+                for layer, (gate_up, down) in enumerate(banks):
+                    x = moe.moe_block(x, gate_up, down, TOPK, router=routers[layer], shared=shared[layer],
+                                      shared_gate=gates[layer])
+            graphs.append(g)
+        ms = timed_replays(graphs, stream, args.steps, args.warmup)
+    torch.cuda.synchronize()
+    status = moe.status(device, H, I, stream)
+    if status:
+        raise RuntimeError(f"fused layer reported status {status}")
+    total_bytes = sum(bytes_per_token[i % GRAPH_TOKENS] for i in range(args.steps))
+    config = {"workload": f"MoE block (router {E}x{H} bf16, routed {args.format} experts top-{TOPK}, shared expert "
+                          f"of FFN {I} with its gate), decode M=1, hidden {H}, FFN {I}, {L} layers chained per token",
+              "rows": 1, "layers": L, "unique_experts_per_launch": round(sum(unique) / len(unique), 2)}
+    return ms, total_bytes, args.steps * L, args.steps, config, "d3::moe_a8_one_row_kernel (block)", None
 
 
 def run_prefill(args, fmt, device):
@@ -335,7 +385,7 @@ def main():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=None)
     p.add_argument("--warmup", type=int, default=None)
-    p.add_argument("--mode", default="decode", choices=["decode", "prefill", "resident"])
+    p.add_argument("--mode", default="decode", choices=["decode", "prefill", "resident", "block"])
     p.add_argument("--format", default=None, choices=sorted(FORMATS))
     p.add_argument("--rows", type=int, default=None)
     p.add_argument("--layers", type=int, default=None)
@@ -361,7 +411,7 @@ def main():
         calibrate_copy(device)
         return
 
-    run = run_prefill if prefill else run_resident if args.mode == "resident" else run_decode
+    run = {"prefill": run_prefill, "resident": run_resident, "block": run_block}.get(args.mode, run_decode)
     ms, total_bytes, launches, tokens, config, kernel, cpu = run(args, fmt, device)
     gbs = total_bytes / (ms * 1e-3) / 1e9
     launch_us = ms * 1e3 / launches
