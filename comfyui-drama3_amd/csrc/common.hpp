@@ -233,3 +233,52 @@ D3_INLINE float route_key_value(uint32_t key) {
   const uint32_t ord = key >> 16;
   return bf16_to_f32((ord & 0x8000u) ? (ord & 0x7FFFu) : (~ord & 0xFFFFu));
 }
+
+// Top-k of a row's router logits (bf16 bits lb[j] for experts lane + 64 j, KPL of them per lane), one round at a time:
+// round r takes the wave-wide max over each lane's largest remaining key and lane r keeps it, so after k rounds lanes
+// 0 .. k-1 hold the k largest keys, descending, ties to the lower index (kernels.py:50-55).
+template <int KPL>
+struct TopKeys {
+  uint32_t key[KPL], lm, mine;
+  D3_INLINE TopKeys(const uint32_t* lb, int lane, int E) : lm(0u), mine(0u) {
+#pragma unroll
+    for (int j = 0; j < KPL; j++) {
+      key[j] = lane + 64 * j < E ? route_key(lb[j], lane + 64 * j) : 0u;
+      lm = max(lm, key[j]);
+    }
+  }
+  // rounds from .. to - 1 (to <= 8)
+  D3_INLINE void rounds(int lane, int from, int to) {
+#pragma unroll
+    for (int r = 0; r < 8; r++) {
+      if (r >= from && r < to) {
+        const uint32_t m = wave_max_u32_v(lm);
+        mine = lane == r ? m : mine;
+        lm = 0u;
+#pragma unroll
+        for (int j = 0; j < KPL; j++) {
+          key[j] = key[j] == m ? 0u : key[j];
+          lm = max(lm, key[j]);
+        }
+      }
+    }
+  }
+};
+template <int KPL>
+D3_INLINE uint32_t top_keys(const uint32_t* lb, int lane, int E, int k) {
+  TopKeys<KPL> t(lb, lane, E);
+  t.rounds(lane, 0, k);
+  return t.mine;
+}
+
+// The softmax over a row's k routed logits (lanes 0 .. k-1 hold the keys, descending): this lane's weight, the
+// exponentials in parallel and their sum in rank order (kernels.py:57-61), bf16-rounded.
+D3_INLINE float route_weight(uint32_t mine, int lane, int k) {
+  const float top0 = route_key_value((uint32_t)__builtin_amdgcn_readlane((int)mine, 0));
+  const float ex = lane < k ? expf(route_key_value(mine) - top0) : 0.0f;
+  float total = 0.0f;
+#pragma unroll
+  for (int r = 0; r < 8; r++)
+    if (r < k) total += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ex), r));
+  return bf16_round(ex / total);
+}

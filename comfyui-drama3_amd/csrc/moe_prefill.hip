@@ -71,8 +71,9 @@ D3_INLINE int wave_exclusive_scan(int v, int lane, int& total) {
   return incl - v;
 }
 
-__global__ void __launch_bounds__(1024) group_kernel(const int64_t* ids, int P, int E, int* counts, int* offsets,
-                                                     int* perm, int4* units, int* meta) {
+// (a workgroup of 1024 threads; ids may be in LDS or device memory; perm_lds, if given, gets a copy of perm)
+D3_INLINE void group_pairs(const int64_t* ids, int P, int E, int* counts, int* offsets, int* perm, int4* units,
+                           int* meta, int* perm_lds = nullptr) {
   __shared__ int cnt[MAX_EXPERTS], cur[MAX_EXPERTS], by_rank[MAX_EXPERTS], rank_base[MAX_EXPERTS];
   __shared__ int used;
   const int tid = threadIdx.x;
@@ -128,7 +129,110 @@ __global__ void __launch_bounds__(1024) group_kernel(const int64_t* ids, int P, 
       units[rank_base[r] + u] = int4{e, first + u * UNIT_PAIRS, min(UNIT_PAIRS, c - u * UNIT_PAIRS), 0};
   }
   __syncthreads();
-  for (int p = tid; p < P; p += 1024) perm[atomicAdd(&cur[(int)min<int64_t>(max<int64_t>(ids[p], 0), E - 1)], 1)] = p;
+  for (int p = tid; p < P; p += 1024) {
+    const int at = atomicAdd(&cur[(int)min<int64_t>(max<int64_t>(ids[p], 0), E - 1)], 1);
+    perm[at] = p;
+    if (perm_lds) perm_lds[at] = p;
+  }
+}
+
+__global__ void __launch_bounds__(1024) group_kernel(const int64_t* ids, int P, int E, int* counts, int* offsets,
+                                                     int* perm, int4* units, int* meta) {
+  group_pairs(ids, P, E, counts, offsets, perm, units, meta);
+}
+
+// ----------------------------------------------------------------------------------------- few rows, one launch
+// T <= 16 rows in one workgroup of 16 waves, the steps route, group and quantize x of the many-row path in one
+// launch: wave t routes row t (the fused layer's TopKeys, kernels.py:39-67's rule; or copies the given ids and
+// weights), the workgroup groups the pairs (group_pairs), then quantizes x into the pairs' sorted order, a row per
+// wave in turn.
+struct SmallPrepArgs {
+  const uint16_t* logits;   // [T, E] bf16, or null with ids_in / weights_in
+  const int64_t* ids_in;
+  const float* weights_in;
+  const uint16_t* x;        // [T, H] bf16
+  int T, E, k;
+  int64_t* ids;             // [P]
+  float* weights;           // [P]
+  int64_t* ids_out;         // optional
+  float* weights_out;       // optional
+  int* counts;
+  int* offsets;
+  int* perm;
+  int4* units;
+  int* meta;
+  uint8_t* xq;              // [P, H] by sorted position
+  float* xs;                // [P]
+};
+
+template <int F, int H, int KPL>
+__global__ void __launch_bounds__(1024) small_prep_kernel(SmallPrepArgs a) {
+  constexpr float QMAX = act_qmax<F>();
+  __shared__ int64_t lids[16 * 8];
+  __shared__ int lperm[16 * 8];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int T = a.T, E = a.E, k = a.k, P = T * k;
+  if (w < T) {
+    if (a.logits) {
+      uint32_t lb[KPL];
+#pragma unroll
+      for (int j = 0; j < KPL; j++) lb[j] = a.logits[(size_t)w * E + min(lane + 64 * j, E - 1)];
+      TopKeys<KPL> tk(lb, lane, E);
+      tk.rounds(lane, 0, k);
+      const float wt = route_weight(tk.mine, lane, k);
+      if (lane < k) {
+        const int64_t id = route_key_index(tk.mine);
+        lids[w * k + lane] = id;
+        a.ids[w * k + lane] = id;
+        a.weights[w * k + lane] = wt;
+        if (a.ids_out) a.ids_out[w * k + lane] = id;
+        if (a.weights_out) a.weights_out[w * k + lane] = wt;
+      }
+    } else if (lane < k) {
+      const int64_t id = a.ids_in[w * k + lane];
+      lids[w * k + lane] = id;
+      a.ids[w * k + lane] = id;
+      a.weights[w * k + lane] = a.weights_in[w * k + lane];
+    }
+  }
+  __syncthreads();
+  group_pairs(lids, P, E, a.counts, a.offsets, a.perm, a.units, a.meta, lperm);
+  __syncthreads();
+  // sorted position sp = w + 16 i: each wave loads four rows of x at once (clamped, so every load is issued), then
+  // quantizes them
+  constexpr int RB = 4;
+  for (int i0 = 0; w + 16 * i0 < P; i0 += RB) {
+    i32x4 r[RB][H / 512];
+#pragma unroll
+    for (int b = 0; b < RB; b++) {
+      const int sp = min(w + 16 * (i0 + b), P - 1);
+      const int row = lperm[sp] / k;
+#pragma unroll
+      for (int c = 0; c < H / 512; c++) r[b][c] = *(const i32x4*)(a.x + (size_t)row * H + 512 * c + 8 * lane);
+    }
+#pragma unroll
+    for (int b = 0; b < RB; b++) {
+      const int sp = w + 16 * (i0 + b);
+      if (sp >= P) break;
+      float v[H / 512][8];
+      float amax = 0.0f;
+#pragma unroll
+      for (int c = 0; c < H / 512; c++) {
+        const uint32_t w4[4] = {(uint32_t)r[b][c].x, (uint32_t)r[b][c].y, (uint32_t)r[b][c].z, (uint32_t)r[b][c].w};
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          v[c][2 * j] = bf16_to_f32(w4[j] & 0xFFFFu);
+          v[c][2 * j + 1] = bf16_to_f32(w4[j] >> 16);
+          amax = fmaxf(amax, fmaxf(fabsf(v[c][2 * j]), fabsf(v[c][2 * j + 1])));
+        }
+      }
+      amax = wave_max_f32(amax);
+      const float inv = amax > 0.0f ? QMAX / amax : 0.0f;
+#pragma unroll
+      for (int c = 0; c < H / 512; c++) store_act8<F>(a.xq + (size_t)sp * H + 512 * c + 8 * lane, v[c], inv);
+      if (lane == 0) a.xs[sp] = amax / QMAX;
+    }
+  }
 }
 
 // ------------------------------------------------------------------------------------------------------- quantize
@@ -468,6 +572,10 @@ template <int F, int H, int I> void launch_down(const PrefillArgs& pa, int max_u
   hipLaunchKernelGGL((grouped_kernel<F, H, I, 1>), dim3(grid), dim3(256), 0, s, pa, pa.units, pa.meta);
 }
 
+template <int F, int KPL> void launch_small(const SmallPrepArgs& sa, hipStream_t s) {
+  hipLaunchKernelGGL((small_prep_kernel<F, 2048, KPL>), dim3(1), dim3(1024), 0, s, sa);
+}
+
 template <int F, bool BF16, int WIDTH> void launch_quantize(const void* src, int rows, uint8_t* q, float* scale,
                                                              const int* rowmap, int k, const float* pair_weight,
                                                              const int* rowmap2, hipStream_t s) {
@@ -476,11 +584,12 @@ template <int F, bool BF16, int WIDTH> void launch_quantize(const void* src, int
 }
 
 template <int F, int H, int I> void run(const PrefillArgs& pa, const d3_moe_a8_prefill_desc& d, const Layout& L,
-                                        uint8_t* ws, hipStream_t s) {
+                                        uint8_t* ws, hipStream_t s, bool x_done) {
   const int P = d.T * d.topk;
   const int max_units = std::min(d.E, P) + P / UNIT_PAIRS;
   // activations quantized straight into the pairs' sorted order (row perm[s] / k of x for position s)
-  launch_quantize<F, true, H>(d.x, P, ws + L.xq, (float*)(ws + L.xs), pa.perm, d.topk, nullptr, nullptr, s);
+  if (!x_done)
+    launch_quantize<F, true, H>(d.x, P, ws + L.xq, (float*)(ws + L.xs), pa.perm, d.topk, nullptr, nullptr, s);
   launch_products<F, H, I>(pa, max_units, s);
   launch_quantize<F, false, I>(ws + L.h, P, ws + L.hq, (float*)(ws + L.hs), nullptr, 1, pa.weights, pa.perm, s);
   launch_down<F, H, I>(pa, max_units, s);
@@ -516,7 +625,39 @@ int d3_moe_a8_prefill(const d3_moe_a8_prefill_desc* d, void* stream) {
   const int P = d->T * d->topk;
   int64_t* ids = (int64_t*)(ws + L.ids);
   float* weights = (float*)(ws + L.weights);
-  if (d->logits) {
+  // few rows: routing, grouping and x's quantization in one launch. One
+  // workgroup quantizes every sorted row, so past 6 rows (48 pairs at top-8)
+  // the three wide launches it replaces are quicker (measured on a
+  // 2048 x 768, 128-expert W4A8 layer: 1.7 us saved at 5 rows, even at 6-7).
+  const bool small = d->T <= 6 && d->topk <= 8 && d->E <= 256;
+  if (small) {
+    SmallPrepArgs sa;
+    sa.logits = (const uint16_t*)d->logits;
+    sa.ids_in = d->ids_in;
+    sa.weights_in = d->weights_in;
+    sa.x = (const uint16_t*)d->x;
+    sa.T = d->T;
+    sa.E = d->E;
+    sa.k = d->topk;
+    sa.ids = ids;
+    sa.weights = weights;
+    sa.ids_out = d->logits ? d->ids_out : nullptr;
+    sa.weights_out = d->logits ? d->weights_out : nullptr;
+    sa.counts = (int*)(ws + L.counts);
+    sa.offsets = (int*)(ws + L.offsets);
+    sa.perm = (int*)(ws + L.perm);
+    sa.units = (int4*)(ws + L.units);
+    sa.meta = (int*)(ws + L.meta);
+    sa.xq = ws + L.xq;
+    sa.xs = (float*)(ws + L.xs);
+    const bool kpl2 = d->E <= 128;
+    switch (d->format) {
+      case D3_FMT_I8: kpl2 ? launch_small<FMT_I8, 2>(sa, s) : launch_small<FMT_I8, 4>(sa, s); break;
+      case D3_FMT_W4: kpl2 ? launch_small<FMT_W4, 2>(sa, s) : launch_small<FMT_W4, 4>(sa, s); break;
+      case D3_FMT_W6: kpl2 ? launch_small<FMT_W6, 2>(sa, s) : launch_small<FMT_W6, 4>(sa, s); break;
+      default: kpl2 ? launch_small<FMT_F8, 2>(sa, s) : launch_small<FMT_F8, 4>(sa, s); break;
+    }
+  } else if (d->logits) {
     const int rc = d3_route(d->logits, d->T, d->E, d->topk, ids, weights, stream);
     if (rc) return rc;
   } else {
@@ -524,14 +665,15 @@ int d3_moe_a8_prefill(const d3_moe_a8_prefill_desc* d, void* stream) {
     if (err == hipSuccess) err = hipMemcpyAsync(weights, d->weights_in, (size_t)P * 4, hipMemcpyDeviceToDevice, s);
     if (err != hipSuccess) return hip_fail(err, "d3_moe_a8_prefill: copy routing");
   }
-  if (d->ids_out && d->logits) {
+  if (d->ids_out && d->logits && !small) {
     hipError_t err = hipMemcpyAsync(d->ids_out, ids, (size_t)P * 8, hipMemcpyDeviceToDevice, s);
     if (err == hipSuccess && d->weights_out)
       err = hipMemcpyAsync(d->weights_out, weights, (size_t)P * 4, hipMemcpyDeviceToDevice, s);
     if (err != hipSuccess) return hip_fail(err, "d3_moe_a8_prefill: copy routing out");
   }
-  hipLaunchKernelGGL(group_kernel, dim3(1), dim3(1024), 0, s, (const int64_t*)ids, P, d->E, (int*)(ws + L.counts),
-                     (int*)(ws + L.offsets), (int*)(ws + L.perm), (int4*)(ws + L.units), (int*)(ws + L.meta));
+  if (!small)
+    hipLaunchKernelGGL(group_kernel, dim3(1), dim3(1024), 0, s, (const int64_t*)ids, P, d->E, (int*)(ws + L.counts),
+                       (int*)(ws + L.offsets), (int*)(ws + L.perm), (int4*)(ws + L.units), (int*)(ws + L.meta));
   PrefillArgs pa;
   pa.ids = ids;
   pa.weights = weights;
@@ -554,10 +696,10 @@ int d3_moe_a8_prefill(const d3_moe_a8_prefill_desc* d, void* stream) {
   pa.inter = d->I;
   const bool i768 = d->I == 768;
   switch (d->format) {
-    case D3_FMT_I8: i768 ? run<FMT_I8, 2048, 768>(pa, *d, L, ws, s) : run<FMT_I8, 2048, 512>(pa, *d, L, ws, s); break;
-    case D3_FMT_W4: i768 ? run<FMT_W4, 2048, 768>(pa, *d, L, ws, s) : run<FMT_W4, 2048, 512>(pa, *d, L, ws, s); break;
-    case D3_FMT_W6: i768 ? run<FMT_W6, 2048, 768>(pa, *d, L, ws, s) : run<FMT_W6, 2048, 512>(pa, *d, L, ws, s); break;
-    default: i768 ? run<FMT_F8, 2048, 768>(pa, *d, L, ws, s) : run<FMT_F8, 2048, 512>(pa, *d, L, ws, s); break;
+    case D3_FMT_I8: i768 ? run<FMT_I8, 2048, 768>(pa, *d, L, ws, s, small) : run<FMT_I8, 2048, 512>(pa, *d, L, ws, s, small); break;
+    case D3_FMT_W4: i768 ? run<FMT_W4, 2048, 768>(pa, *d, L, ws, s, small) : run<FMT_W4, 2048, 512>(pa, *d, L, ws, s, small); break;
+    case D3_FMT_W6: i768 ? run<FMT_W6, 2048, 768>(pa, *d, L, ws, s, small) : run<FMT_W6, 2048, 512>(pa, *d, L, ws, s, small); break;
+    default: i768 ? run<FMT_F8, 2048, 768>(pa, *d, L, ws, s, small) : run<FMT_F8, 2048, 512>(pa, *d, L, ws, s, small); break;
   }
   const int64_t threads = (int64_t)d->T * (d->H / 2);
   hipLaunchKernelGGL(reduce_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s, (const float*)pa.parts,

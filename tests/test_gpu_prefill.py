@@ -93,6 +93,22 @@ def test_prefill_single_row_and_reference_shape():
         check(formats.FMT_W4, x, logits, gate_up, down)
 
 
+@pytest.mark.parametrize("fmt", FMTS)
+def test_few_rows_prep_in_one_launch(fmt):
+    """Up to 6 rows route, group and quantize x in one launch; 7 rows take the three wide launches. Each output row
+    depends on its own row only, so 6 rows and the first 6 of 7 agree bit for bit; 1, 3 and 6 rows match the
+    oracle, with the routing given as well as computed."""
+    gate_up, down = banks(fmt)
+    gen = torch.Generator(device=DEV).manual_seed(40 + fmt)
+    x = torch.randn((7, H), generator=gen, device=DEV).to(torch.bfloat16)
+    logits = torch.randn((7, 16), generator=gen, device=DEV).to(torch.bfloat16)
+    seven = moe.moe_prefill(x, gate_up, down, 8, logits=logits)
+    for T in (1, 3, 6):
+        out, ids, w = check(fmt, x[:T].contiguous(), logits[:T].contiguous(), gate_up, down)
+        assert torch.equal(out, seven[:T])
+        assert torch.equal(moe.moe_prefill(x[:T].contiguous(), gate_up, down, 8, topk_idx=ids, topk_weight=w), out)
+
+
 @pytest.mark.parametrize("fmt", [formats.FMT_I8, formats.FMT_W6])
 def test_given_routing_equals_logits_routing(fmt):
     """topk_idx / topk_weight handed in (as Experts.forward gets them) give the same output as routing inside."""
@@ -117,11 +133,12 @@ def test_prefill_close_to_fused_decode(fmt):
     assert torch.linalg.norm(a - b) <= 1e-2 * torch.linalg.norm(b)
 
 
-def test_prefill_graph_replays():
+@pytest.mark.parametrize("rows", [16, 4])
+def test_prefill_graph_replays(rows):
     gate_up, down = banks(formats.FMT_F8)
     gen = torch.Generator(device=DEV).manual_seed(35)
-    xs = [torch.randn((16, H), generator=gen, device=DEV).to(torch.bfloat16) for _ in range(3)]
-    lgs = [torch.randn((16, 16), generator=gen, device=DEV).to(torch.bfloat16) for _ in range(3)]
+    xs = [torch.randn((rows, H), generator=gen, device=DEV).to(torch.bfloat16) for _ in range(3)]
+    lgs = [torch.randn((rows, 16), generator=gen, device=DEV).to(torch.bfloat16) for _ in range(3)]
     x_buf, lg_buf = xs[0].clone(), lgs[0].clone()
     stream = torch.cuda.Stream(DEV)
     stream.wait_stream(torch.cuda.current_stream(DEV))
