@@ -218,4 +218,14 @@ template <int F> D3_INLINE void store_act8(uint8_t* dst, const float* v, float i
   *(i32x2*)dst = i32x2{(int)lo, (int)hi};
 }
 
+// one activation quantized as store_act8 does it, and the byte offset store_act8 gives column c of a row
+template <int F> D3_INLINE uint32_t act8_byte(float v, float inv) {
+  if constexpr (F == FMT_F8) return f32x2_to_fp8x2(v * inv, 0.0f) & 0xFFu;
+  const float r = fminf(fmaxf(rintf(v * inv), -127.0f), 127.0f);
+  return (uint32_t)((int)r) & 0xFFu;
+}
+template <int F> __host__ __device__ constexpr int act8_pos(int c) {
+  return F == FMT_W4 ? (c & ~7) + ((c & 1) ? 4 : 0) + ((c & 7) >> 1) : c;
+}
+
 }  // namespace d3

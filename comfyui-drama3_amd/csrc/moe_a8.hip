@@ -337,7 +337,6 @@ D3_INLINE void down_finish(const Ctx& cx, int c, int hb, const DownRows<F, I>& d
   constexpr int STEPS = I / 128;
   constexpr int SHIFT = unpack_shift(F);
   constexpr float QMAX = act_qmax<F>();
-  constexpr int G8 = I / 8;  // 8-column groups of a hidden row
   const MoeA8Args& a = *cx.a;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, q = lane >> 4, col = lane & 15;
   const int M = a.M, K8 = a.topk;
@@ -360,7 +359,8 @@ D3_INLINE void down_finish(const Ctx& cx, int c, int hb, const DownRows<F, I>& d
   __syncthreads();
   const int P = slot_first[ne];
   constexpr int T = I / 16;             // gate_up tiles per expert
-  constexpr int GPH = (G8 + 31) / 32;   // 8-column groups per lane of a half-wave
+  constexpr int HPL = I / 32;           // hidden words per lane of a half-wave
+  static_assert(I % 32 == 0, "whole words per lane");
   constexpr int TPH = (T + 31) / 32;    // tile maxima per lane of a half-wave
   if (2 * w < ne) {
     // Each wave serves its two experts on its own: gathers their pairs' hidden rows two at a time (a pair per
@@ -392,26 +392,22 @@ D3_INLINE void down_finish(const Ctx& cx, int c, int hb, const DownRows<F, I>& d
       const int slot = sp + half;
       const bool on = slot < s1;
       const int p = cx.slot_pair[on ? slot : s0];
-      uint64_t mw[TPH], vw[GPH][8];
+      // lane hl reads words hl + 32 j: every load covers 256 contiguous bytes of the half-wave's row
+      const uint64_t* hrow = a.hidden + (size_t)p * I + hl;
+      uint64_t mw[TPH], vw[HPL];
 #pragma unroll
       for (int k = 0; k < TPH; k++) {
         const int t = hl + 32 * k;
         mw[k] = on && t < T ? get_tagged_cached(a.tmax + (size_t)p * T + t) : 0;
       }
 #pragma unroll
-      for (int k = 0; k < GPH; k++) {
-        const int g8 = hl + 32 * k;
-#pragma unroll
-        for (int i = 0; i < 8; i++) vw[k][i] = on && g8 < G8 ? get_tagged_cached(a.hidden + (size_t)p * I + 8 * g8 + i) : 0;
-      }
+      for (int j = 0; j < HPL; j++) vw[j] = on ? get_tagged_cached(hrow + 32 * j) : 0;
       // words not yet landed: read again, coherently
       bool fresh = true;
 #pragma unroll
       for (int k = 0; k < TPH; k++) fresh = fresh && (!on || hl + 32 * k >= T || tag_is(mw[k], cx.epoch));
 #pragma unroll
-      for (int k = 0; k < GPH; k++)
-#pragma unroll
-        for (int i = 0; i < 8; i++) fresh = fresh && (!on || hl + 32 * k >= G8 || tag_is(vw[k][i], cx.epoch));
+      for (int j = 0; j < HPL; j++) fresh = fresh && (!on || tag_is(vw[j], cx.epoch));
       if (!__all(fresh)) {
         await_counters();
         uint32_t polls = 0;
@@ -424,13 +420,9 @@ D3_INLINE void down_finish(const Ctx& cx, int c, int hb, const DownRows<F, I>& d
             ok = ok && (!on || t >= T || tag_is(mw[k], cx.epoch));
           }
 #pragma unroll
-          for (int k = 0; k < GPH; k++) {
-            const int g8 = hl + 32 * k;
-#pragma unroll
-            for (int i = 0; i < 8; i++) {
-              if (on && g8 < G8 && !tag_is(vw[k][i], cx.epoch)) vw[k][i] = get_tagged(a.hidden + (size_t)p * I + 8 * g8 + i);
-              ok = ok && (!on || g8 >= G8 || tag_is(vw[k][i], cx.epoch));
-            }
+          for (int j = 0; j < HPL; j++) {
+            if (on && !tag_is(vw[j], cx.epoch)) vw[j] = get_tagged(hrow + 32 * j);
+            ok = ok && (!on || tag_is(vw[j], cx.epoch));
           }
           if (__all(ok) || !keep_polling(polls, a.sync + SYNC_STATUS, a.spin_limit)) break;
         }
@@ -450,16 +442,9 @@ D3_INLINE void down_finish(const Ctx& cx, int c, int hb, const DownRows<F, I>& d
       const float amax = half ? m1 : m0;
       const float inv = amax > 0.0f ? QMAX / amax : 0.0f;
       if (on) {
+        uint8_t* hrow_q = cx.hq + (size_t)slot * I;
 #pragma unroll
-        for (int k = 0; k < GPH; k++) {
-          const int g8 = hl + 32 * k;
-          if (g8 < G8) {
-            float v[8];
-#pragma unroll
-            for (int i = 0; i < 8; i++) v[i] = tagged_value(vw[k][i]);
-            store_act8<F>(cx.hq + (size_t)slot * I + 8 * g8, v, inv);
-          }
-        }
+        for (int j = 0; j < HPL; j++) hrow_q[act8_pos<F>(hl + 32 * j)] = (uint8_t)act8_byte<F>(tagged_value(vw[j]), inv);
         if (hl == 0) cx.hs[slot] = amax / QMAX;
       }
     }
@@ -627,8 +612,8 @@ D3_INLINE void shared_down_block(const Ctx& cx, int b, const i32x4* xraw) {
   constexpr int RB = row_bytes(F, I);
   constexpr int SHIFT = unpack_shift(F);
   constexpr float QMAX = act_qmax<F>();
-  constexpr int T = I / 16, G8 = I / 8, GPL = (G8 + 63) / 64;
-  static_assert(T <= 64, "a tile maximum per lane");
+  constexpr int T = I / 16, HPW = I / 64;  // hidden words per lane (lane l reads words l + 64 j)
+  static_assert(T <= 64 && I % 64 == 0, "a tile maximum per lane, whole words per lane");
   const MoeA8Args& a = *cx.a;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, q = lane >> 4, col = lane & 15;
   const int K8 = a.topk;
@@ -675,16 +660,12 @@ D3_INLINE void shared_down_block(const Ctx& cx, int b, const i32x4* xraw) {
   const uint64_t* hrow = a.hidden + (size_t)K8 * I;
   const uint64_t* trow = a.tmax + (size_t)K8 * T;
   uint64_t mw = get_tagged_cached(trow + min(lane, T - 1));
-  uint64_t vw[GPL][8];
+  uint64_t vw[HPW];
 #pragma unroll
-  for (int k = 0; k < GPL; k++)
-#pragma unroll
-    for (int j = 0; j < 8; j++) vw[k][j] = get_tagged_cached(hrow + 8 * min(lane + 64 * k, G8 - 1) + j);
+  for (int j = 0; j < HPW; j++) vw[j] = get_tagged_cached(hrow + lane + 64 * j);
   bool fresh = tag_is(mw, cx.epoch);
 #pragma unroll
-  for (int k = 0; k < GPL; k++)
-#pragma unroll
-    for (int j = 0; j < 8; j++) fresh = fresh && tag_is(vw[k][j], cx.epoch);
+  for (int j = 0; j < HPW; j++) fresh = fresh && tag_is(vw[j], cx.epoch);
   if (!__all(fresh)) {
     if (lane == 0) {
       uint32_t polls = 0;
@@ -697,12 +678,10 @@ D3_INLINE void shared_down_block(const Ctx& cx, int b, const i32x4* xraw) {
       if (!tag_is(mw, cx.epoch)) mw = get_tagged(trow + min(lane, T - 1));
       bool ok = tag_is(mw, cx.epoch);
 #pragma unroll
-      for (int k = 0; k < GPL; k++)
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-          if (!tag_is(vw[k][j], cx.epoch)) vw[k][j] = get_tagged(hrow + 8 * min(lane + 64 * k, G8 - 1) + j);
-          ok = ok && tag_is(vw[k][j], cx.epoch);
-        }
+      for (int j = 0; j < HPW; j++) {
+        if (!tag_is(vw[j], cx.epoch)) vw[j] = get_tagged(hrow + lane + 64 * j);
+        ok = ok && tag_is(vw[j], cx.epoch);
+      }
       if (__all(ok) || !keep_polling(polls, a.sync + SYNC_STATUS, a.spin_limit)) break;
     }
   }
@@ -710,15 +689,7 @@ D3_INLINE void shared_down_block(const Ctx& cx, int b, const i32x4* xraw) {
   const float inv = amax > 0.0f ? QMAX / amax : 0.0f;
   uint8_t* hq = cx.hq + (size_t)w * I;  // this wave's own copy of the quantized row
 #pragma unroll
-  for (int k = 0; k < GPL; k++) {
-    const int g8 = lane + 64 * k;
-    if (g8 < G8) {
-      float v[8];
-#pragma unroll
-      for (int j = 0; j < 8; j++) v[j] = tagged_value(vw[k][j]);
-      store_act8<F>(hq + 8 * g8, v, inv);
-    }
-  }
+  for (int j = 0; j < HPW; j++) hq[act8_pos<F>(lane + 64 * j)] = (uint8_t)act8_byte<F>(tagged_value(vw[j]), inv);
   lds_settle();
   // rows r0 + 4q + i against the row (column 0)
   i32x4 iacc = {0, 0, 0, 0};
@@ -897,8 +868,11 @@ __global__ void __launch_bounds__(256, 2) moe_a8_one_row_kernel(MoeA8Args a) {
   else one_row_layer<F, H, I, 4>(cx, (int)blockIdx.x);
 }
 
-template <int F, int H, int I>
-__global__ void __launch_bounds__(256, 3) moe_a8_kernel(MoeA8Args a) {
+// The general schedule, persistent: compiled for WPC workgroups per CU, the grid being as many as fit. Two rows run
+// faster with two per CU (the registers of 256 a lane hold a down item's gathered rows without spills), three rows and
+// more with three (more workgroups on the items).
+template <int F, int H, int I, int WPC>
+__global__ void __launch_bounds__(256, WPC) moe_a8_kernel(MoeA8Args a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   constexpr int T = I / 16;
   constexpr int NHB = H / 8;
@@ -1090,13 +1064,14 @@ int64_t moe_a8_workspace_bytes(int M, int topk, int H, int I) {
 
 using KernelFn = void (*)(MoeA8Args);
 
-template <int F, int H, int I> KernelFn kernel_of(bool one_row) {
-  return one_row ? moe_a8_one_row_kernel<F, H, I> : moe_a8_kernel<F, H, I>;
+template <int F, int H, int I> KernelFn kernel_of(bool one_row, int M) {
+  return one_row ? moe_a8_one_row_kernel<F, H, I> : M == 2 ? moe_a8_kernel<F, H, I, 2> : moe_a8_kernel<F, H, I, 3>;
 }
 
-KernelFn pick_kernel(int fmt, int H, int I, bool one_row = false) {
+// the fused layer's kernel for a format, shape and row count (one_row: the one-row schedule)
+KernelFn pick_kernel(int fmt, int H, int I, int M, bool one_row = false) {
 #define D3_CASE(F, HH, II) \
-  if (fmt == F && H == HH && I == II) return kernel_of<F, HH, II>(one_row);
+  if (fmt == F && H == HH && I == II) return kernel_of<F, HH, II>(one_row, M);
 #define D3_SHAPES(F) D3_CASE(F, 2048, 768) D3_CASE(F, 2048, 512)
   D3_SHAPES(FMT_I8) D3_SHAPES(FMT_W4) D3_SHAPES(FMT_W6) D3_SHAPES(FMT_F8)
 #undef D3_SHAPES
@@ -1130,7 +1105,7 @@ int launch_moe_a8(const d3_moe_a8_desc* d, hipStream_t stream) {
   if (d->M < 1 || d->M > MAX_M) return fail("d3_moe_a8: M must be 1..16");
   if (d->topk < 1 || d->topk > MAX_K) return fail("d3_moe_a8: topk must be 1..8");
   if (d->E < d->topk || d->E > MAX_E) return fail("d3_moe_a8: E must be topk..256");
-  KernelFn fn = pick_kernel(d->format, d->H, d->I);
+  KernelFn fn = pick_kernel(d->format, d->H, d->I, d->M);
   if (!fn) return fail("d3_moe_a8: no kernel for this format and shape (H 2048; I 512 or 768)");
   if (!d->x || !(d->logits || d->router) || !d->gate_up || !d->gate_up_scale || !d->down || !d->down_scale || !d->out ||
       !d->workspace)
@@ -1157,7 +1132,7 @@ int launch_moe_a8(const d3_moe_a8_desc* d, hipStream_t stream) {
   // one row: a workgroup per gate_up tile, the first H / 8 of them also taking a down block (one_row_layer), when the
   // device holds them all at once
   const int tiles = d->topk * (d->I / 16) + (shared ? d->I / 16 + d->H / 64 : 0);
-  KernelFn fn1 = pick_kernel(d->format, d->H, d->I, true);
+  KernelFn fn1 = pick_kernel(d->format, d->H, d->I, d->M, true);
   const int cap1 = resident_capacity(fn1, L.total, &err);
   if (err) return err;
   const bool one_row = d->grid <= 0 && d->M == 1 && d->topk * (d->I / 16) >= d->H / 8 && tiles <= cap1 &&
