@@ -612,8 +612,8 @@ D3_INLINE void shared_down_block(const Ctx& cx, int b, const i32x4* xraw) {
   constexpr int RB = row_bytes(F, I);
   constexpr int SHIFT = unpack_shift(F);
   constexpr float QMAX = act_qmax<F>();
-  constexpr int T = I / 16, HPW = I / 64;  // hidden words per lane (lane l reads words l + 64 j)
-  static_assert(T <= 64 && I % 64 == 0, "a tile maximum per lane, whole words per lane");
+  constexpr int T = I / 16, G8 = I / 8, GPL = (G8 + 63) / 64;
+  static_assert(T <= 64, "a tile maximum per lane");
   const MoeA8Args& a = *cx.a;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, q = lane >> 4, col = lane & 15;
   const int K8 = a.topk;
@@ -655,17 +655,23 @@ D3_INLINE void shared_down_block(const Ctx& cx, int b, const i32x4* xraw) {
   const float gate = bf16_round(wave_sum_f32(gsum));
   const float gw = bf16_round(1.0f / (1.0f + expf(-gate)));
   // the shared hidden row (pair K8), gathered once this wave's rows have landed; words not yet published are read
-  // again after the expert's counter shows all its tiles
+  // again after the expert's counter shows all its tiles. Lane l reads the 8 words of column group l (and l + 64):
+  // per block, this order measured faster than the routed down items' lane-contiguous one for int8 (0.75 us), FP8
+  // (0.8 us) and W6 (0.2 us), slower for W4 (0.8 us).
   settle();
   const uint64_t* hrow = a.hidden + (size_t)K8 * I;
   const uint64_t* trow = a.tmax + (size_t)K8 * T;
   uint64_t mw = get_tagged_cached(trow + min(lane, T - 1));
-  uint64_t vw[HPW];
+  uint64_t vw[GPL][8];
 #pragma unroll
-  for (int j = 0; j < HPW; j++) vw[j] = get_tagged_cached(hrow + lane + 64 * j);
+  for (int k = 0; k < GPL; k++)
+#pragma unroll
+    for (int j = 0; j < 8; j++) vw[k][j] = get_tagged_cached(hrow + 8 * min(lane + 64 * k, G8 - 1) + j);
   bool fresh = tag_is(mw, cx.epoch);
 #pragma unroll
-  for (int j = 0; j < HPW; j++) fresh = fresh && tag_is(vw[j], cx.epoch);
+  for (int k = 0; k < GPL; k++)
+#pragma unroll
+    for (int j = 0; j < 8; j++) fresh = fresh && tag_is(vw[k][j], cx.epoch);
   if (!__all(fresh)) {
     if (lane == 0) {
       uint32_t polls = 0;
@@ -678,10 +684,12 @@ D3_INLINE void shared_down_block(const Ctx& cx, int b, const i32x4* xraw) {
       if (!tag_is(mw, cx.epoch)) mw = get_tagged(trow + min(lane, T - 1));
       bool ok = tag_is(mw, cx.epoch);
 #pragma unroll
-      for (int j = 0; j < HPW; j++) {
-        if (!tag_is(vw[j], cx.epoch)) vw[j] = get_tagged(hrow + lane + 64 * j);
-        ok = ok && tag_is(vw[j], cx.epoch);
-      }
+      for (int k = 0; k < GPL; k++)
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+          if (!tag_is(vw[k][j], cx.epoch)) vw[k][j] = get_tagged(hrow + 8 * min(lane + 64 * k, G8 - 1) + j);
+          ok = ok && tag_is(vw[k][j], cx.epoch);
+        }
       if (__all(ok) || !keep_polling(polls, a.sync + SYNC_STATUS, a.spin_limit)) break;
     }
   }
@@ -689,7 +697,15 @@ D3_INLINE void shared_down_block(const Ctx& cx, int b, const i32x4* xraw) {
   const float inv = amax > 0.0f ? QMAX / amax : 0.0f;
   uint8_t* hq = cx.hq + (size_t)w * I;  // this wave's own copy of the quantized row
 #pragma unroll
-  for (int j = 0; j < HPW; j++) hq[act8_pos<F>(lane + 64 * j)] = (uint8_t)act8_byte<F>(tagged_value(vw[j]), inv);
+  for (int k = 0; k < GPL; k++) {
+    const int g8 = lane + 64 * k;
+    if (g8 < G8) {
+      float v[8];
+#pragma unroll
+      for (int j = 0; j < 8; j++) v[j] = tagged_value(vw[k][j]);
+      store_act8<F>(hq + 8 * g8, v, inv);
+    }
+  }
   lds_settle();
   // rows r0 + 4q + i against the row (column 0)
   i32x4 iacc = {0, 0, 0, 0};
