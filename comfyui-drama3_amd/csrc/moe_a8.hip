@@ -56,7 +56,7 @@ struct MoeA8Args {
   int64_t* ids_out;
   float* weights_out;
   uint64_t* hidden;  // [M * topk, I] tagged
-  uint64_t* tmax;    // [M * topk, I / 16] tagged: absmax of each gate_up item's 16 hidden units
+  uint64_t* tmax;    // [M * topk + 1, I / UT] tagged: absmax of each gate_up item's UT (8 or 16) hidden units
   uint64_t* parts;   // [M * topk, H] tagged
   uint32_t* sync;
   int M, E, topk;
@@ -137,13 +137,15 @@ struct Ctx {
   uint32_t epoch;
 };
 
-// gate_up item: hidden units 16 tile .. 16 tile + 15 of expert u, i.e. two 16-row MFMA tiles (sub-tile s: gate rows
-// 16 tile + 8 s .. + 7 as rows 0-7, the matching up rows as rows 8-15)
+// gate_up item: hidden units UT tile .. UT tile + UT - 1 (UT = 8 NSUB) of expert u, i.e. NSUB 16-row MFMA tiles
+// (sub-tile s: gate rows UT tile + 8 s .. + 7 as rows 0-7, the matching up rows as rows 8-15)
 // (`between` runs once the item's weight rows are on their way, before it reads the slot tables or x; `after` once its
 // products are done, before its reduction)
-template <int F, int H, int I, typename Between, typename After>
+template <int F, int H, int I, int NSUB = 2, typename Between, typename After>
 D3_INLINE uint64_t gate_up_item(const Ctx& cx, int u, int tile, int parity, int e, int nu, Between between,
                                 After after, const uint8_t* gu_w, const uint16_t* gu_s) {
+  static_assert(NSUB == 1 || NSUB == 2, "8 or 16 hidden units per item");
+  constexpr int UT = 8 * NSUB, T = I / UT;  // hidden units per item, items per expert
   constexpr int SPW = H / 512;  // steps per wave
   constexpr int RB = row_bytes(F, H);
   constexpr int SHIFT = unpack_shift(F);
@@ -156,17 +158,17 @@ D3_INLINE uint64_t gate_up_item(const Ctx& cx, int u, int tile, int parity, int 
     __hip_atomic_fetch_max(done_counter(a.sync, u), (uint64_t)cx.epoch << 32, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   const int ra = lane & 15;
   auto row_of = [&](int sub, int r) {
-    return (size_t)e * (2 * I) + (r < 8 ? 16 * tile + 8 * sub + r : I + 16 * tile + 8 * sub + r - 8);
+    return (size_t)e * (2 * I) + (r < 8 ? UT * tile + 8 * sub + r : I + UT * tile + 8 * sub + r - 8);
   };
-  Raw<F> raw[2][SPW];
+  Raw<F> raw[NSUB][SPW];
 #pragma unroll
-  for (int sub = 0; sub < 2; sub++)
+  for (int sub = 0; sub < NSUB; sub++)
 #pragma unroll
     for (int s = 0; s < SPW; s++) load_step<F>(raw[sub][s], gu_w + row_of(sub, ra) * RB, w * SPW + s, q);
-  float sc[2][SPW][4];
+  float sc[NSUB][SPW][4];
   if constexpr (group_scaled(F)) {
 #pragma unroll
-    for (int sub = 0; sub < 2; sub++)
+    for (int sub = 0; sub < NSUB; sub++)
 #pragma unroll
       for (int i = 0; i < 4; i++)
 #pragma unroll
@@ -176,8 +178,8 @@ D3_INLINE uint64_t gate_up_item(const Ctx& cx, int u, int tile, int parity, int 
   float gs = 1.0f, us = 1.0f;
   if constexpr (!group_scaled(F)) {
     if (w == 0) {
-      gs = bf16_to_f32(gu_s[(size_t)e * (2 * I) + 16 * tile + (lane & 15)]);
-      us = bf16_to_f32(gu_s[(size_t)e * (2 * I) + I + 16 * tile + (lane & 15)]);
+      gs = bf16_to_f32(gu_s[(size_t)e * (2 * I) + UT * tile + (lane & (UT - 1))]);
+      us = bf16_to_f32(gu_s[(size_t)e * (2 * I) + I + UT * tile + (lane & (UT - 1))]);
     }
   }
   between();
@@ -185,7 +187,7 @@ D3_INLINE uint64_t gate_up_item(const Ctx& cx, int u, int tile, int parity, int 
   const uint8_t* xp = cx.xq + (size_t)(active ? cx.utok[u * MAX_M + col] : 0) * H;
   float* rd = cx.red + parity * 2048;
 #pragma unroll
-  for (int sub = 0; sub < 2; sub++) {
+  for (int sub = 0; sub < NSUB; sub++) {
     i32x4 iacc = {0, 0, 0, 0};
     f32x4 facc = {0.0f, 0.0f, 0.0f, 0.0f};
     i32x8 fa[SPW], fb[SPW];
@@ -217,7 +219,9 @@ D3_INLINE uint64_t gate_up_item(const Ctx& cx, int u, int tile, int parity, int 
   __syncthreads();
   if (w == 0) {
     for (int idx = lane; idx < 16 * nu; idx += 64) {
-      const int n = idx >> 4, j = idx & 15, sub = j >> 3, jj = j & 7;
+      // lanes 16 n + j, j < UT: unit j of the item for its n-th row (with UT = 8, lanes j >= 8 publish nothing)
+      const int n = idx >> 4, j = idx & 15, sub = (j >> 3) & (NSUB - 1), jj = j & 7;
+      const bool unit = j < UT;
       const float* rs = rd + sub * 1024;
       float g, up;
       if constexpr (F == FMT_I8) {
@@ -247,14 +251,14 @@ D3_INLINE uint64_t gate_up_item(const Ctx& cx, int u, int tile, int parity, int 
       up *= s;
       const float h = g / (1.0f + __expf(-g)) * up;
       const int p = cx.upair[u * MAX_M + n];
-      put_tagged(a.hidden + (size_t)p * I + 16 * tile + j, h, cx.epoch);
-      // absmax of the row's 16 units: lanes 16n .. 16n + 15 (quad swaps, half-row and row mirrors)
-      float m = fabsf(h);
+      if (unit) put_tagged(a.hidden + (size_t)p * I + UT * tile + j, h, cx.epoch);
+      // absmax of the row's UT units: lanes 16n .. 16n + 15 (quad swaps, half-row and row mirrors)
+      float m = unit ? fabsf(h) : 0.0f;
       m = fmaxf(m, __int_as_float(dpp_i32(__float_as_int(m), 0xB1)));
       m = fmaxf(m, __int_as_float(dpp_i32(__float_as_int(m), 0x4E)));
       m = fmaxf(m, __int_as_float(dpp_i32(__float_as_int(m), 0x141)));
       m = fmaxf(m, __int_as_float(dpp_i32(__float_as_int(m), 0x140)));
-      if (j == 0) put_tagged(a.tmax + (size_t)p * (I / 16) + tile, m, cx.epoch);
+      if (j == 0) put_tagged(a.tmax + (size_t)p * T + tile, m, cx.epoch);
     }
     if (lane == 0) {
       // the add follows the raise to the same word from the same lane, so it lands after it. The count before the add
@@ -332,7 +336,7 @@ D3_INLINE void down_load(const Ctx& cx, int c, int hb, DownRows<F, I>& d) {
 
 // the rest of down item (c, hb) once its loads are out: collect the chunk's hidden rows, quantize, multiply, and write
 // the weighted sum (one chunk) or the partial outputs
-template <int F, int H, int I>
+template <int F, int H, int I, int NSUB = 2>
 D3_INLINE void down_finish(const Ctx& cx, int c, int hb, const DownRows<F, I>& d) {
   constexpr int STEPS = I / 128;
   constexpr int SHIFT = unpack_shift(F);
@@ -358,7 +362,7 @@ D3_INLINE void down_finish(const Ctx& cx, int c, int hb, const DownRows<F, I>& d
   }
   __syncthreads();
   const int P = slot_first[ne];
-  constexpr int T = I / 16;             // gate_up tiles per expert
+  constexpr int T = I / (8 * NSUB);     // gate_up items per expert
   constexpr int HPL = I / 32;           // hidden words per lane of a half-wave
   static_assert(I % 32 == 0, "whole words per lane");
   constexpr int TPH = (T + 31) / 32;    // tile maxima per lane of a half-wave
@@ -606,14 +610,14 @@ D3_INLINE void gather_logits(const MoeA8Args& a, uint32_t epoch, int lane, uint3
 // A block of 64 output rows of the shared expert for one row (wave w: rows 64 b + 16 w .. + 15, one 16-row MFMA tile
 // against the shared hidden row as column 0): its gated output bf16(bf16(sigmoid(bf16(x . gate))) * bf16(y)), as
 // model.py:123 rounds it, published as tagged words for the routed down blocks to add.
-template <int F, int H, int I>
+template <int F, int H, int I, int NSUB>
 D3_INLINE void shared_down_block(const Ctx& cx, int b, const i32x4* xraw) {
   constexpr int STEPS = I / 128;
   constexpr int RB = row_bytes(F, I);
   constexpr int SHIFT = unpack_shift(F);
   constexpr float QMAX = act_qmax<F>();
-  constexpr int T = I / 16, G8 = I / 8, GPL = (G8 + 63) / 64;
-  static_assert(T <= 64, "a tile maximum per lane");
+  constexpr int T = I / (8 * NSUB), G8 = I / 8, GPL = (G8 + 63) / 64;
+  constexpr int TPW = (T + 63) / 64;  // item maxima per lane
   const MoeA8Args& a = *cx.a;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, q = lane >> 4, col = lane & 15;
   const int K8 = a.topk;
@@ -661,13 +665,17 @@ D3_INLINE void shared_down_block(const Ctx& cx, int b, const i32x4* xraw) {
   settle();
   const uint64_t* hrow = a.hidden + (size_t)K8 * I;
   const uint64_t* trow = a.tmax + (size_t)K8 * T;
-  uint64_t mw = get_tagged_cached(trow + min(lane, T - 1));
+  uint64_t mw[TPW];
+#pragma unroll
+  for (int k = 0; k < TPW; k++) mw[k] = get_tagged_cached(trow + min(lane + 64 * k, T - 1));
   uint64_t vw[GPL][8];
 #pragma unroll
   for (int k = 0; k < GPL; k++)
 #pragma unroll
     for (int j = 0; j < 8; j++) vw[k][j] = get_tagged_cached(hrow + 8 * min(lane + 64 * k, G8 - 1) + j);
-  bool fresh = tag_is(mw, cx.epoch);
+  bool fresh = true;
+#pragma unroll
+  for (int k = 0; k < TPW; k++) fresh = fresh && tag_is(mw[k], cx.epoch);
 #pragma unroll
   for (int k = 0; k < GPL; k++)
 #pragma unroll
@@ -681,8 +689,12 @@ D3_INLINE void shared_down_block(const Ctx& cx, int b, const i32x4* xraw) {
     }
     uint32_t polls = 0;
     while (true) {
-      if (!tag_is(mw, cx.epoch)) mw = get_tagged(trow + min(lane, T - 1));
-      bool ok = tag_is(mw, cx.epoch);
+      bool ok = true;
+#pragma unroll
+      for (int k = 0; k < TPW; k++) {
+        if (!tag_is(mw[k], cx.epoch)) mw[k] = get_tagged(trow + min(lane + 64 * k, T - 1));
+        ok = ok && tag_is(mw[k], cx.epoch);
+      }
 #pragma unroll
       for (int k = 0; k < GPL; k++)
 #pragma unroll
@@ -693,7 +705,10 @@ D3_INLINE void shared_down_block(const Ctx& cx, int b, const i32x4* xraw) {
       if (__all(ok) || !keep_polling(polls, a.sync + SYNC_STATUS, a.spin_limit)) break;
     }
   }
-  const float amax = wave_max_f32(tagged_value(mw));
+  float tm = 0.0f;
+#pragma unroll
+  for (int k = 0; k < TPW; k++) tm = fmaxf(tm, tagged_value(mw[k]));
+  const float amax = wave_max_f32(tm);
   const float inv = amax > 0.0f ? QMAX / amax : 0.0f;
   uint8_t* hq = cx.hq + (size_t)w * I;  // this wave's own copy of the quantized row
 #pragma unroll
@@ -753,10 +768,10 @@ D3_INLINE void shared_down_block(const Ctx& cx, int b, const i32x4* xraw) {
 // The block around the experts: with a router, workgroups 0 .. E-1 first compute one logit each and every routing
 // wave gathers them; with a shared expert, workgroups k T .. k T + T - 1 compute its gate_up tiles (hidden row k)
 // and the next H / 64 its output in blocks of 64 rows, which the down blocks add to the routed sum.
-template <int F, int H, int I, int KPL>
+template <int F, int H, int I, int NSUB, int KPL>
 D3_INLINE void one_row_layer(Ctx& cx, int i) {
   static_assert(H == 2048, "wave w's K slice is x chunk w");
-  constexpr int T = I / 16, NHB = H / 8;
+  constexpr int T = I / (8 * NSUB), NHB = H / 8;  // gate_up items per expert, down blocks
   constexpr float QMAX = act_qmax<F>();
   const MoeA8Args& a = *cx.a;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
@@ -776,7 +791,7 @@ D3_INLINE void one_row_layer(Ctx& cx, int i) {
   for (int k = 0; k < H / 512; k++) xraw[k] = *(const i32x4*)(a.x + 512 * k + 8 * lane);
   if (a.router && i < E && w == 0) router_logit<H>(a, cx.epoch, i, xraw, lane);
   if (i >= routed + T) {
-    shared_down_block<F, H, I>(cx, i - routed - T, xraw);
+    shared_down_block<F, H, I, NSUB>(cx, i - routed - T, xraw);
     return;
   }
   const int u = is_shared ? K8 : i / T, tile = is_shared ? i - routed : i % T;
@@ -789,7 +804,7 @@ D3_INLINE void one_row_layer(Ctx& cx, int i) {
   cx.nch = 1;
   cx.n_dn = NHB;
   DownRows<F, I> d;
-  const uint64_t before = gate_up_item<F, H, I>(
+  const uint64_t before = gate_up_item<F, H, I, NSUB>(
       cx, u, tile, 0, e, 1,
       [&]() {
         if (has_down) {
@@ -843,7 +858,7 @@ D3_INLINE void one_row_layer(Ctx& cx, int i) {
         if (has_down) down_load<F, H, I>(cx, 0, i, d);
       },
       is_shared ? a.sh_gu_w : a.gu_w, is_shared ? a.sh_gu_s : a.gu_s);
-  if (has_down) down_finish<F, H, I>(cx, 0, i, d);
+  if (has_down) down_finish<F, H, I, NSUB>(cx, 0, i, d);
   flag_later_epoch(a, before, cx.epoch);
 }
 
@@ -874,14 +889,15 @@ D3_INLINE Ctx make_ctx(const MoeA8Args& a, uint8_t* lds, int H, int I) {
   return cx;
 }
 
-// The one-row schedule as its own kernel: at most k I / 16 + I / 16 + H / 64 workgroups, fewer than two per CU, so
-// it is compiled for two per CU (256 registers a lane) and keeps its weight rows, routing state and x in registers.
-template <int F, int H, int I>
+// The one-row schedule as its own kernel: k I / UT + I / UT + H / 64 workgroups (UT = 8 NSUB hidden units per
+// gate_up item). With UT = 16 that is fewer than two per CU, so it is compiled for two per CU (256 registers a lane)
+// and keeps its weight rows, routing state and x in registers.
+template <int F, int H, int I, int NSUB>
 __global__ void __launch_bounds__(256, 2) moe_a8_one_row_kernel(MoeA8Args a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   Ctx cx = make_ctx(a, lds, H, I);
-  if (a.E <= 128) one_row_layer<F, H, I, 2>(cx, (int)blockIdx.x);
-  else one_row_layer<F, H, I, 4>(cx, (int)blockIdx.x);
+  if (a.E <= 128) one_row_layer<F, H, I, NSUB, 2>(cx, (int)blockIdx.x);
+  else one_row_layer<F, H, I, NSUB, 4>(cx, (int)blockIdx.x);
 }
 
 // The general schedule, persistent: compiled for WPC workgroups per CU, the grid being as many as fit. Two rows run
@@ -1075,19 +1091,22 @@ int hip_fail(hipError_t err, const char* what) {
 // the block's router and shared expert MAX_E logit words and H output words
 int64_t moe_a8_workspace_bytes(int M, int topk, int H, int I) {
   const int64_t pairs = (int64_t)M * topk;
-  return SYNC_WORDS * 4 + (pairs + 1) * I * 8 + (pairs + 1) * (I / 16) * 8 + pairs * H * 8 + (MAX_E + H) * 8;
+  return SYNC_WORDS * 4 + (pairs + 1) * I * 8 + (pairs + 1) * (I / 8) * 8 + pairs * H * 8 + (MAX_E + H) * 8;
 }
 
 using KernelFn = void (*)(MoeA8Args);
 
-template <int F, int H, int I> KernelFn kernel_of(bool one_row, int M) {
-  return one_row ? moe_a8_one_row_kernel<F, H, I> : M == 2 ? moe_a8_kernel<F, H, I, 2> : moe_a8_kernel<F, H, I, 3>;
+template <int F, int H, int I> KernelFn kernel_of(int unit, int M) {
+  if (unit == 8) return moe_a8_one_row_kernel<F, H, I, 1>;
+  if (unit == 16) return moe_a8_one_row_kernel<F, H, I, 2>;
+  return M == 2 ? moe_a8_kernel<F, H, I, 2> : moe_a8_kernel<F, H, I, 3>;
 }
 
-// the fused layer's kernel for a format, shape and row count (one_row: the one-row schedule)
-KernelFn pick_kernel(int fmt, int H, int I, int M, bool one_row = false) {
+// the fused layer's kernel for a format, shape and row count: the general schedule (unit 0) or the one-row schedule
+// with gate_up items of `unit` (8 or 16) hidden units
+KernelFn pick_kernel(int fmt, int H, int I, int M, int unit = 0) {
 #define D3_CASE(F, HH, II) \
-  if (fmt == F && H == HH && I == II) return kernel_of<F, HH, II>(one_row, M);
+  if (fmt == F && H == HH && I == II) return kernel_of<F, HH, II>(unit, M);
 #define D3_SHAPES(F) D3_CASE(F, 2048, 768) D3_CASE(F, 2048, 512)
   D3_SHAPES(FMT_I8) D3_SHAPES(FMT_W4) D3_SHAPES(FMT_W6) D3_SHAPES(FMT_F8)
 #undef D3_SHAPES
@@ -1145,18 +1164,33 @@ int launch_moe_a8(const d3_moe_a8_desc* d, hipStream_t stream) {
   const int nch = umax;
   const int items = umax * (d->I / 16) + nch * (d->H / 8);
   int grid = items < cap ? items : cap;
-  // one row: a workgroup per gate_up tile, the first H / 8 of them also taking a down block (one_row_layer), when the
-  // device holds them all at once
-  const int tiles = d->topk * (d->I / 16) + (shared ? d->I / 16 + d->H / 64 : 0);
-  KernelFn fn1 = pick_kernel(d->format, d->H, d->I, d->M, true);
-  const int cap1 = resident_capacity(fn1, L.total, &err);
-  if (err) return err;
-  const bool one_row = d->grid <= 0 && d->M == 1 && d->topk * (d->I / 16) >= d->H / 8 && tiles <= cap1 &&
-                       (!d->router || tiles >= d->E);
+  // one row: a workgroup per gate_up item, the first H / 8 of them also taking a down block (one_row_layer), when the
+  // device holds them all at once. Items of 8 hidden units first: k I / 8 workgroups (768 at k 8, I 768) put the
+  // same gate_up bytes on every CU, where 16-unit items (384) put two on half the CUs, which then finish last.
+  if (d->item_units != 0 && d->item_units != 8 && d->item_units != 16)
+    return fail("d3_moe_a8: item_units must be 0, 8 or 16");
+  KernelFn fn1 = nullptr;
+  int tiles = 0;
+  for (int unit = 8; d->grid <= 0 && d->M == 1 && unit <= 16 && !fn1; unit += 8) {
+    if (d->item_units != 0 && unit != d->item_units) continue;
+    const int t = d->topk * (d->I / unit) + (shared ? d->I / unit + d->H / 64 : 0);
+    if (d->topk * (d->I / unit) < d->H / 8 || (d->router && t < d->E)) continue;
+    KernelFn f = pick_kernel(d->format, d->H, d->I, d->M, unit);
+    const int cap1 = resident_capacity(f, L.total, &err);
+    if (err) return err;
+    if (t <= cap1) {
+      fn1 = f;
+      tiles = t;
+    }
+  }
+  const bool one_row = fn1 != nullptr;
   if (d->grid > 0) grid = d->grid < grid ? d->grid : grid;
   else if (one_row) grid = tiles;
   if ((d->router || shared) && !one_row)
     return fail("d3_moe_a8: the router and the shared expert run in the one-row schedule (M = 1, grid 0)");
+  if (d->item_units != 0 && !one_row)
+    return fail("d3_moe_a8: item_units applies to the one-row schedule (M = 1, grid 0), whose workgroups must all fit "
+                "on the device at once");
 
   MoeA8Args a;
   a.x = (const uint16_t*)d->x;
@@ -1173,7 +1207,7 @@ int launch_moe_a8(const d3_moe_a8_desc* d, hipStream_t stream) {
   const size_t pairs = (size_t)d->M * d->topk;
   a.hidden = (uint64_t*)(ws + SYNC_WORDS * 4);
   a.tmax = a.hidden + (pairs + 1) * d->I;
-  a.parts = a.tmax + (pairs + 1) * (d->I / 16);
+  a.parts = a.tmax + (pairs + 1) * (d->I / 8);
   a.logitw = a.parts + pairs * d->H;
   a.sharedw = a.logitw + MAX_E;
   a.M = d->M;

@@ -64,11 +64,11 @@ GROUPED_FROM_ROWS = 4
 
 
 def moe_layer(x, logits, gate_up: A8Bank, down: A8Bank, topk, *, routing=False, spin_limit=0, grid=0, out=None,
-              fused=None):
+              fused=None, item_units=0):
     """x [M, H] bf16 and router logits [M, E] bf16 (M <= 16) through the routed experts: [M, H] bf16, and with
     `routing` also (ids [M, topk] int64 in descending logit order, weights [M, topk] float32). Fewer than
     GROUPED_FROM_ROWS rows run the fused one-launch kernel (d3_moe_a8), more the grouped path (moe_prefill); `fused`
-    forces either."""
+    forces either. `item_units` (8 or 16; 0 picks) sets the one-row schedule's hidden units per gate_up workgroup."""
     if fused is None:
         fused = x.shape[0] < GROUPED_FROM_ROWS
     if not fused:
@@ -97,19 +97,19 @@ def moe_layer(x, logits, gate_up: A8Bank, down: A8Bank, topk, *, routing=False, 
         gate_up_scale=gate_up.scale.data_ptr(), down=down.weight.data_ptr(), down_scale=down.scale.data_ptr(),
         out=out.data_ptr(), ids_out=_lib.ptr(ids), weights_out=_lib.ptr(weights), workspace=ws.data_ptr(),
         workspace_bytes=ws.numel(), format=gate_up.fmt, M=M, H=H, I=I, E=E, topk=topk, spin_limit=spin_limit,
-        grid=grid)
+        grid=grid, item_units=item_units)
     _lib.check(_lib.lib().d3_moe_a8(ctypes.byref(desc), _lib.stream_of(device)), "d3_moe_a8")
     return (out, ids, weights) if routing else out
 
 
 def moe_block(x, gate_up: A8Bank, down: A8Bank, topk, *, router=None, logits=None, shared=None, shared_gate=None,
-              routing=False, return_logits=False, out=None):
+              routing=False, return_logits=False, out=None, item_units=0):
     """SparseMoeBlock.forward for one decode row (drama3/model.py:107-124) in one launch: x [1, H] bf16 -> [1, H] bf16.
 
     The router: `router` [E, H] bf16 (its logits computed in the launch, model.py:115) or given `logits` [1, E] bf16.
     The shared expert: `shared` = (gate_up, down) A8Banks of one expert in the layer's format and shape, and
     `shared_gate` [H] bf16; it is added as model.py:123 does (both terms bf16). With `routing` also returns ids and
-    weights, with `return_logits` the router's logits [1, E] bf16."""
+    weights, with `return_logits` the router's logits [1, E] bf16. `item_units` as for moe_layer."""
     if x.dtype != torch.bfloat16 or x.dim() != 2 or x.shape[0] != 1:
         raise ValueError("x [1, H] bfloat16 expected: the block runs one row")
     H = x.shape[1]
@@ -153,7 +153,8 @@ def moe_block(x, gate_up: A8Bank, down: A8Bank, topk, *, router=None, logits=Non
         shared_gate_up=_lib.ptr(sg.weight if sg is not None else None),
         shared_gate_up_scale=_lib.ptr(sg.scale if sg is not None else None),
         shared_down=_lib.ptr(sd.weight if sd is not None else None),
-        shared_down_scale=_lib.ptr(sd.scale if sd is not None else None), shared_gate=_lib.ptr(shared_gate))
+        shared_down_scale=_lib.ptr(sd.scale if sd is not None else None), shared_gate=_lib.ptr(shared_gate),
+        item_units=item_units)
     _lib.check(_lib.lib().d3_moe_a8(ctypes.byref(desc), _lib.stream_of(device)), "d3_moe_a8")
     res = (out,)
     if routing:

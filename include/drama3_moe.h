@@ -68,6 +68,9 @@ typedef struct d3_moe_a8_desc {
   const void* shared_down;           /* [H, row_bytes(I)] */
   const void* shared_down_scale;
   const void* shared_gate;           /* [H] bf16 (shared_expert_gate, one output) */
+  /* One-row schedule (M = 1, grid 0): hidden units per gate_up workgroup, 8 or 16 (0: 8 when the device holds k I / 8
+   * workgroups at once, else 16). Both give the same output, bit for bit. */
+  int32_t item_units;
 } d3_moe_a8_desc;
 
 int64_t d3_moe_a8_workspace_bytes(int32_t M, int32_t topk, int32_t H, int32_t I);

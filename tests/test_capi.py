@@ -3,6 +3,7 @@ launched), and the Python binding knows each of them."""
 import ctypes
 import pathlib
 import re
+import subprocess
 
 import pytest
 
@@ -41,3 +42,24 @@ def test_host_only_calls():
     # argument errors come back as D3_EINVAL with a message, without touching a device
     rc = lib.d3_moe_a8(None, None)
     assert rc == -1 and b"null" in lib.d3_last_error()
+
+
+@pytest.mark.parametrize("struct,cname", [(_lib.MoeA8Desc, "d3_moe_a8_desc"),
+                                          (_lib.MoeA8PrefillDesc, "d3_moe_a8_prefill_desc")])
+def test_descriptor_layout_matches_header(struct, cname, tmp_path):
+    """Every field of the ctypes descriptor sits at the offset the C compiler gives it in the header, and the sizes
+    agree: a field added to one side only shifts the rest and is caught here."""
+    fields = [f[0] for f in struct._fields_]
+    prog = tmp_path / "layout.c"
+    lines = ["#include <stdio.h>", "#include <stddef.h>", f'#include "{HEADER}"', "int main(void) {",
+             f'  printf("size %zu\\n", sizeof({cname}));']
+    lines += [f'  printf("{f} %zu\\n", offsetof({cname}, {f}));' for f in fields]
+    lines += ["  return 0;", "}"]
+    prog.write_text("\n".join(lines) + "\n")
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c11", "-o", str(exe), str(prog)], check=True, capture_output=True)
+    got = dict(line.split() for line in subprocess.run([str(exe)], check=True, capture_output=True,
+                                                       text=True).stdout.splitlines())
+    assert int(got["size"]) == ctypes.sizeof(struct)
+    for f in fields:
+        assert int(got[f]) == getattr(struct, f).offset, f

@@ -107,8 +107,9 @@ def fetcher(gate_up, down):
     return fetch
 
 
-def check_layer(fmt, x, logits, gate_up, down, topk=8, fused=True, grid=0):
-    out, ids, w = moe.moe_layer(x, logits, gate_up, down, topk, routing=True, fused=fused, grid=grid)
+def check_layer(fmt, x, logits, gate_up, down, topk=8, fused=True, grid=0, item_units=0):
+    out, ids, w = moe.moe_layer(x, logits, gate_up, down, topk, routing=True, fused=fused, grid=grid,
+                                item_units=item_units)
     torch.cuda.synchronize()
     assert moe.status(DEV, x.shape[1], down.cols) == 0
     want, want_ids, want_w, _ = a8.moe_layer(bits(x), bits(logits), (gate_up.rows, gate_up.cols), (down.rows, down.cols),
@@ -137,15 +138,28 @@ def test_layer_matches_oracle(fmt, M):
 
 @pytest.mark.parametrize("fmt", FMTS)
 def test_one_row_paths_agree(fmt):
-    """One row runs a workgroup per gate_up tile by default (gate_up tiles with the down blocks behind them); an
-    explicit grid of one workgroup per item runs the general schedule. Both match the oracle."""
+    """One row runs a workgroup per gate_up item (8 hidden units by default, or 16), the down blocks behind the
+    items; an explicit grid of one workgroup per item runs the general schedule. All three match the oracle and each
+    other bit for bit: the items' size changes no sum's order."""
     gate_up, down = layer_banks(fmt)
     gen = torch.Generator(device=DEV).manual_seed(21)
     x = torch.randn((1, 2048), generator=gen, device=DEV).to(torch.bfloat16)
     logits = torch.randn((1, 128), generator=gen, device=DEV).to(torch.bfloat16)
     a = check_layer(fmt, x, logits, gate_up, down)
+    a8_ = check_layer(fmt, x, logits, gate_up, down, item_units=8)
+    a16 = check_layer(fmt, x, logits, gate_up, down, item_units=16)
     b = check_layer(fmt, x, logits, gate_up, down, grid=8 * 48 + 2048 // 8)
-    assert torch.equal(a, b)
+    assert torch.equal(a, a8_) and torch.equal(a, a16) and torch.equal(a, b)
+
+
+def test_item_units_checked():
+    gate_up, down = layer_banks(formats.FMT_I8)
+    x = torch.zeros((2, 2048), device=DEV, dtype=torch.bfloat16)
+    logits = torch.zeros((2, 128), device=DEV, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="item_units must be"):
+        moe.moe_layer(x[:1], logits[:1], gate_up, down, 8, item_units=12)
+    with pytest.raises(RuntimeError, match="one-row schedule"):
+        moe.moe_layer(x, logits, gate_up, down, 8, item_units=8)
 
 @pytest.mark.parametrize("fmt", [formats.FMT_I8, formats.FMT_W4])
 def test_layer_shared_experts(fmt):
@@ -260,7 +274,11 @@ def test_block_router_and_shared_expert(fmt):
     assert np.linalg.norm(got - ref) <= 1e-2 * np.linalg.norm(ref)
     # the same block from the logits given: identical; the router alone: the layer on its logits, identical
     assert torch.equal(moe.moe_block(x, gate_up, down, 8, logits=lg, shared=(sg, sd), shared_gate=g), out)
-    assert torch.equal(moe.moe_block(x, gate_up, down, 8, router=router), moe.moe_layer(x, lg, gate_up, down, 8))
+    assert torch.equal(moe.moe_block(x, gate_up, down, 8, logits=lg, shared=(sg, sd), shared_gate=g, item_units=16),
+                       out)
+    layer = moe.moe_layer(x, lg, gate_up, down, 8)
+    for units in (0, 8, 16):
+        assert torch.equal(moe.moe_block(x, gate_up, down, 8, router=router, item_units=units), layer)
 
 
 def test_block_rejects_more_rows():
