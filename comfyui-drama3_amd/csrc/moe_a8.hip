@@ -371,24 +371,11 @@ D3_INLINE void down_finish(const Ctx& cx, int c, int hb, const DownRows<F, I>& d
     // half-wave: the tiles' maxima and the values in one round trip), quantizes them into its LDS slots and runs.
     // The gather is issued once the wave's weight rows have arrived (its loads complete in order, so anything issued
     // earlier would be read early and come back no sooner); the words carry their epoch, so a gather that finds every
-    // word current needs nothing else. Otherwise lane 0 waits for the experts' counters and the stale words are read
-    // again.
+    // word current needs nothing else. Otherwise the stale words are read again, coherently, until they are current.
+    // (Not the experts' counters first: every waiting wave would poll the same few words, and by the time a first
+    // gather is back the late items are mostly published.)
     const int la = 2 * w, lb = 2 * w + 1;
     const bool has_b = lb < ne;
-    bool counted = false;
-    auto await_counters = [&]() {
-      if (counted) return;
-      counted = true;
-      if (lane == 0) {
-        uint32_t polls = 0;
-        while (true) {
-          const uint64_t want = ((uint64_t)cx.epoch << 32) | (uint32_t)T;
-          const uint64_t na = signal_load64(done_counter(a.sync, u0 + la));
-          const uint64_t nb = has_b ? signal_load64(done_counter(a.sync, u0 + lb)) : want;
-          if ((na == want && nb == want) || !keep_polling(polls, a.sync + SYNC_STATUS, a.spin_limit)) break;
-        }
-      }
-    };
     settle();
     const int s0 = slot_first[la], s1 = slot_first[has_b ? lb + 1 : la + 1];
     const int half = lane >> 5, hl = lane & 31;
@@ -413,7 +400,6 @@ D3_INLINE void down_finish(const Ctx& cx, int c, int hb, const DownRows<F, I>& d
 #pragma unroll
       for (int j = 0; j < HPL; j++) fresh = fresh && (!on || tag_is(vw[j], cx.epoch));
       if (!__all(fresh)) {
-        await_counters();
         uint32_t polls = 0;
         while (true) {
           bool ok = true;
@@ -616,7 +602,7 @@ D3_INLINE void shared_down_block(const Ctx& cx, int b, const i32x4* xraw) {
   constexpr int RB = row_bytes(F, I);
   constexpr int SHIFT = unpack_shift(F);
   constexpr float QMAX = act_qmax<F>();
-  constexpr int T = I / (8 * NSUB), G8 = I / 8, GPL = (G8 + 63) / 64;
+  constexpr int T = I / (8 * NSUB);
   constexpr int TPW = (T + 63) / 64;  // item maxima per lane
   const MoeA8Args& a = *cx.a;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, q = lane >> 4, col = lane & 15;
@@ -659,34 +645,25 @@ D3_INLINE void shared_down_block(const Ctx& cx, int b, const i32x4* xraw) {
   const float gate = bf16_round(wave_sum_f32(gsum));
   const float gw = bf16_round(1.0f / (1.0f + expf(-gate)));
   // the shared hidden row (pair K8), gathered once this wave's rows have landed; words not yet published are read
-  // again after the expert's counter shows all its tiles. Lane l reads the 8 words of column group l (and l + 64):
-  // per block, this order measured faster than the routed down items' lane-contiguous one for int8 (0.75 us), FP8
-  // (0.8 us) and W6 (0.2 us), slower for W4 (0.8 us).
+  // again, coherently, until they carry the launch's epoch (polling the expert's counter first, as every waiting wave
+  // of these blocks would, cost 2-2.5 us per block). Lane l reads words l + 64 j, so each load covers 512 contiguous
+  // bytes.
   settle();
   const uint64_t* hrow = a.hidden + (size_t)K8 * I;
   const uint64_t* trow = a.tmax + (size_t)K8 * T;
   uint64_t mw[TPW];
 #pragma unroll
   for (int k = 0; k < TPW; k++) mw[k] = get_tagged_cached(trow + min(lane + 64 * k, T - 1));
-  uint64_t vw[GPL][8];
+  constexpr int HPW = I / 64;
+  uint64_t vw[HPW];
 #pragma unroll
-  for (int k = 0; k < GPL; k++)
-#pragma unroll
-    for (int j = 0; j < 8; j++) vw[k][j] = get_tagged_cached(hrow + 8 * min(lane + 64 * k, G8 - 1) + j);
+  for (int j = 0; j < HPW; j++) vw[j] = get_tagged_cached(hrow + lane + 64 * j);
   bool fresh = true;
 #pragma unroll
   for (int k = 0; k < TPW; k++) fresh = fresh && tag_is(mw[k], cx.epoch);
 #pragma unroll
-  for (int k = 0; k < GPL; k++)
-#pragma unroll
-    for (int j = 0; j < 8; j++) fresh = fresh && tag_is(vw[k][j], cx.epoch);
+  for (int j = 0; j < HPW; j++) fresh = fresh && tag_is(vw[j], cx.epoch);
   if (!__all(fresh)) {
-    if (lane == 0) {
-      uint32_t polls = 0;
-      const uint64_t want = ((uint64_t)cx.epoch << 32) | (uint32_t)T;
-      while (signal_load64(done_counter(a.sync, K8)) != want && keep_polling(polls, a.sync + SYNC_STATUS, a.spin_limit)) {
-      }
-    }
     uint32_t polls = 0;
     while (true) {
       bool ok = true;
@@ -696,12 +673,10 @@ D3_INLINE void shared_down_block(const Ctx& cx, int b, const i32x4* xraw) {
         ok = ok && tag_is(mw[k], cx.epoch);
       }
 #pragma unroll
-      for (int k = 0; k < GPL; k++)
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-          if (!tag_is(vw[k][j], cx.epoch)) vw[k][j] = get_tagged(hrow + 8 * min(lane + 64 * k, G8 - 1) + j);
-          ok = ok && tag_is(vw[k][j], cx.epoch);
-        }
+      for (int j = 0; j < HPW; j++) {
+        if (!tag_is(vw[j], cx.epoch)) vw[j] = get_tagged(hrow + lane + 64 * j);
+        ok = ok && tag_is(vw[j], cx.epoch);
+      }
       if (__all(ok) || !keep_polling(polls, a.sync + SYNC_STATUS, a.spin_limit)) break;
     }
   }
@@ -712,15 +687,7 @@ D3_INLINE void shared_down_block(const Ctx& cx, int b, const i32x4* xraw) {
   const float inv = amax > 0.0f ? QMAX / amax : 0.0f;
   uint8_t* hq = cx.hq + (size_t)w * I;  // this wave's own copy of the quantized row
 #pragma unroll
-  for (int k = 0; k < GPL; k++) {
-    const int g8 = lane + 64 * k;
-    if (g8 < G8) {
-      float v[8];
-#pragma unroll
-      for (int j = 0; j < 8; j++) v[j] = tagged_value(vw[k][j]);
-      store_act8<F>(hq + 8 * g8, v, inv);
-    }
-  }
+  for (int j = 0; j < HPW; j++) hq[act8_pos<F>(lane + 64 * j)] = (uint8_t)act8_byte<F>(tagged_value(vw[j]), inv);
   lds_settle();
   // rows r0 + 4q + i against the row (column 0)
   i32x4 iacc = {0, 0, 0, 0};
