@@ -867,9 +867,10 @@ __global__ void __launch_bounds__(256, 2) moe_a8_one_row_kernel(MoeA8Args a) {
   else one_row_layer<F, H, I, NSUB, 4>(cx, (int)blockIdx.x);
 }
 
-// The general schedule, persistent: compiled for WPC workgroups per CU, the grid being as many as fit. Two rows run
-// faster with two per CU (the registers of 256 a lane hold a down item's gathered rows without spills), three rows and
-// more with three (more workgroups on the items).
+// The general schedule, persistent: compiled for WPC workgroups per CU, the grid being as many as fit. Two, four and
+// five rows run faster with two per CU (the registers of 256 a lane hold a down item's gathered rows without spills),
+// three rows and six or more with three (more workgroups on the items). Measured (int8, us per layer, two / three per
+// CU): 2 rows 25.4 / 29.4, 3 rows 40.8 / 39.5, 4 rows 45.8 / 49.4, 5 rows 58.6 / 61.9.
 template <int F, int H, int I, int WPC>
 __global__ void __launch_bounds__(256, WPC) moe_a8_kernel(MoeA8Args a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
@@ -1066,7 +1067,7 @@ using KernelFn = void (*)(MoeA8Args);
 template <int F, int H, int I> KernelFn kernel_of(int unit, int M) {
   if (unit == 8) return moe_a8_one_row_kernel<F, H, I, 1>;
   if (unit == 16) return moe_a8_one_row_kernel<F, H, I, 2>;
-  return M == 2 ? moe_a8_kernel<F, H, I, 2> : moe_a8_kernel<F, H, I, 3>;
+  return (M == 2 || M == 4 || M == 5) ? moe_a8_kernel<F, H, I, 2> : moe_a8_kernel<F, H, I, 3>;
 }
 
 // the fused layer's kernel for a format, shape and row count: the general schedule (unit 0) or the one-row schedule

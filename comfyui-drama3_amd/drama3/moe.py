@@ -59,8 +59,9 @@ def status(device, H, I, stream=None):
 
 # From this many rows on, moe_layer runs the grouped path (d3_moe_a8_prefill): its persistent grouped products read
 # each expert once for all rows and keep the memory busy, where the fused kernel's items for several rows queue up
-# behind each other (measured on MI355X, W4A8: 4 rows 54 vs 61 us, 16 rows 92 vs 215 us).
-GROUPED_FROM_ROWS = 4
+# behind each other. Measured on MI355X (us per layer, fused / grouped): int8 4 rows 45.8 / 56.2, 5 rows 58.6 / 62.3,
+# 6 rows 70.0 / 67.4, 16 rows 193 / 99; W4A8 4 rows 40.4 / 46.0, 5 rows 50.4 / 50.4, 6 rows 57.6 / 53.6.
+GROUPED_FROM_ROWS = 6
 
 
 def moe_layer(x, logits, gate_up: A8Bank, down: A8Bank, topk, *, routing=False, spin_limit=0, grid=0, out=None,

@@ -126,7 +126,7 @@ def check_layer(fmt, x, logits, gate_up, down, topk=8, fused=True, grid=0, item_
 
 
 @pytest.mark.parametrize("fmt", FMTS)
-@pytest.mark.parametrize("M", [1, 2, 4, 16])
+@pytest.mark.parametrize("M", [1, 2, 4, 5, 16])
 def test_layer_matches_oracle(fmt, M):
     gate_up, down = layer_banks(fmt)
     gen = torch.Generator(device=DEV).manual_seed(100 + M)
@@ -226,7 +226,7 @@ def test_graph_replay_matches_eager():
     assert moe.status(DEV, 2048, 768, stream) == 0
 
 
-@pytest.mark.parametrize("M", [1, 3, 4, 16])
+@pytest.mark.parametrize("M", [1, 3, 4, 5, 6, 16])
 def test_layer_dispatch_matches_oracle(M):
     """moe_layer's own choice of path (fused below GROUPED_FROM_ROWS rows, grouped from there on) against the
     oracle."""
