@@ -1194,13 +1194,17 @@ int launch_moe_a8(const d3_moe_a8_desc* d, hipStream_t stream) {
   a.sh_gate = (const uint16_t*)d->shared_gate;
   // Which of the routed gate_up workgroups also take the down blocks: those routed at ranks 0-2 land their gate_up rows
   // first, and their down rows then compete with the later ranks' gate_up rows, which the hand-off waits for; from
-  // workgroup 256 on (ranks 2.7-5.3 with 8-unit items) they go out once most gate_up rows are in. W4A8's shorter
-  // stream favours the first workgroups. Measured, us per layer with the down blocks from workgroup 0 / 256: int8
-  // 15.5 / 14.5, FP8 15.6 / 14.5, W6A8 13.9 / 13.8, W4A8 11.6 / 12.2.
+  // workgroup 256 on (ranks 2.7-5.3 with 8-unit items) they go out once most gate_up rows are in. The shorter streams
+  // of the 4- and 6-bit formats favour the first workgroups (late down rows become the tail). Measured, us per layer,
+  // first down workgroup 0 / 256 with 8-unit items: int8 15.5 / 14.5, FP8 15.6 / 14.5, W6A8 13.9 / 13.8, W4A8 11.6 /
+  // 12.2; 0 / 128 with 16-unit items (block with a shared expert): int8 20.0 / 19.5, FP8 19.9 / 19.4, W6A8 18.6 /
+  // 19.6, W4A8 16.8 / 17.5.
   a.dn_first = 0;
-  if (one_row && unit_used == 8 && d->format != FMT_W4) {
-    const int routed = d->topk * (d->I / 8);
-    a.dn_first = routed - d->H / 8 < 256 ? routed - d->H / 8 : 256;
+  if (one_row) {
+    const int late = d->topk * (d->I / unit_used) - d->H / 8;  // the last workgroups that can take them all
+    const bool big = d->format == FMT_I8 || d->format == FMT_F8;
+    if (unit_used == 8 && d->format != FMT_W4) a.dn_first = late < 256 ? late : 256;
+    if (unit_used == 16 && big) a.dn_first = late < 128 ? late : 128;
   }
   hipLaunchKernelGGL(one_row ? fn1 : fn, dim3(grid), dim3(256), L.total, stream, a);
   hipError_t e = hipGetLastError();
