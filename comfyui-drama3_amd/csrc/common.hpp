@@ -149,6 +149,8 @@ D3_INLINE uint64_t get_tagged_cached(const uint64_t* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 D3_INLINE bool tag_is(uint64_t word, uint32_t epoch) { return (uint32_t)(word >> 32) == epoch; }
+// the bits in which a word's tag differs from `epoch`: OR them over many words and test once
+D3_INLINE uint32_t tag_diff(uint64_t word, uint32_t epoch) { return (uint32_t)(word >> 32) ^ epoch; }
 D3_INLINE float tagged_value(uint64_t word) { return __uint_as_float((uint32_t)word); }
 
 // N tagged words at p[0..N) (stride `stride`): all loads issued at once, then the stale ones (not yet landed) read

@@ -386,36 +386,50 @@ D3_INLINE void down_finish(const Ctx& cx, int c, int hb, const DownRows<F, I>& d
       const int p = cx.slot_pair[on ? slot : s0];
       // lane hl reads words hl + 32 j: every load covers 256 contiguous bytes of the half-wave's row
       const uint64_t* hrow = a.hidden + (size_t)p * I + hl;
+      // every lane loads (addresses clamped to a pair and an item of the unit), without a branch per load; lanes
+      // without a word of their own then hold a current word of value 0
+      const uint64_t* trow = a.tmax + (size_t)p * T;
+      const uint64_t cur = (uint64_t)cx.epoch << 32;
       uint64_t mw[TPH], vw[HPL];
 #pragma unroll
-      for (int k = 0; k < TPH; k++) {
-        const int t = hl + 32 * k;
-        mw[k] = on && t < T ? get_tagged_cached(a.tmax + (size_t)p * T + t) : 0;
-      }
+      for (int k = 0; k < TPH; k++) mw[k] = get_tagged_cached(trow + min(hl + 32 * k, T - 1));
 #pragma unroll
-      for (int j = 0; j < HPL; j++) vw[j] = on ? get_tagged_cached(hrow + 32 * j) : 0;
-      // words not yet landed: read again, coherently
-      bool fresh = true;
+      for (int j = 0; j < HPL; j++) vw[j] = get_tagged_cached(hrow + 32 * j);
 #pragma unroll
-      for (int k = 0; k < TPH; k++) fresh = fresh && (!on || hl + 32 * k >= T || tag_is(mw[k], cx.epoch));
+      for (int k = 0; k < TPH; k++)
+        if (!on || hl + 32 * k >= T) mw[k] = cur;
 #pragma unroll
-      for (int j = 0; j < HPL; j++) fresh = fresh && (!on || tag_is(vw[j], cx.epoch));
-      if (!__all(fresh)) {
+      for (int j = 0; j < HPL; j++)
+        if (!on) vw[j] = cur;
+      // words not yet current: read again, coherently. The check ORs the words' tag differences and compares once
+      // (a compare and a mask step per word made a serial chain of some 30 dependent steps)
+      uint32_t stale = 0;
+#pragma unroll
+      for (int k = 0; k < TPH; k++) stale |= tag_diff(mw[k], cx.epoch);
+#pragma unroll
+      for (int j = 0; j < HPL; j++) stale |= tag_diff(vw[j], cx.epoch);
+      if (!__all(stale == 0u)) {
+        // While waiting, only the item maxima are read again (TPH words a lane; an item stores its maximum after its
+        // hidden words): re-reading every stale hidden word each round cost as much memory traffic, over the down
+        // blocks, as their weight rows. Once the maxima are current, the hidden words still stale are read again.
         uint32_t polls = 0;
         while (true) {
-          bool ok = true;
+          uint32_t stale_m = 0;
 #pragma unroll
           for (int k = 0; k < TPH; k++) {
-            const int t = hl + 32 * k;
-            if (on && t < T && !tag_is(mw[k], cx.epoch)) mw[k] = get_tagged(a.tmax + (size_t)p * T + t);
-            ok = ok && (!on || t >= T || tag_is(mw[k], cx.epoch));
+            if (!tag_is(mw[k], cx.epoch)) mw[k] = get_tagged(trow + min(hl + 32 * k, T - 1));
+            stale_m |= tag_diff(mw[k], cx.epoch);
           }
+          if (__all(stale_m == 0u)) {
+            stale = 0;
 #pragma unroll
-          for (int j = 0; j < HPL; j++) {
-            if (on && !tag_is(vw[j], cx.epoch)) vw[j] = get_tagged(hrow + 32 * j);
-            ok = ok && (!on || tag_is(vw[j], cx.epoch));
+            for (int j = 0; j < HPL; j++) {
+              if (!tag_is(vw[j], cx.epoch)) vw[j] = get_tagged(hrow + 32 * j);
+              stale |= tag_diff(vw[j], cx.epoch);
+            }
+            if (__all(stale == 0u)) break;
           }
-          if (__all(ok) || !keep_polling(polls, a.sync + SYNC_STATUS, a.spin_limit)) break;
+          if (!keep_polling(polls, a.sync + SYNC_STATUS, a.spin_limit)) break;
         }
       }
       // the pair's absmax over its tiles' maxima: a half-wave reduction (rows 0-1 or 2-3 of the wave)
