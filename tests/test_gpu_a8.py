@@ -135,6 +135,18 @@ def test_layer_matches_oracle(fmt, M):
     check_layer(fmt, x, logits, gate_up, down)
 
 
+@pytest.mark.parametrize("fmt", [formats.FMT_I8, formats.FMT_W4])
+@pytest.mark.parametrize("topk", [1, 2, 4, 6])
+@pytest.mark.parametrize("M", [1, 3])
+def test_layer_other_topk(fmt, topk, M):
+    """Fewer than 8 experts per row. One row at k 4 and 6 runs a workgroup per 8-unit item (k * 96 >= 256 down
+    blocks); at k 1 and 2 the items are too few for the down blocks and the general schedule takes it."""
+    gate_up, down = layer_banks(fmt)
+    gen = torch.Generator(device=DEV).manual_seed(200 + 10 * topk + M)
+    x = torch.randn((M, 2048), generator=gen, device=DEV).to(torch.bfloat16)
+    logits = torch.randn((M, 128), generator=gen, device=DEV).to(torch.bfloat16)
+    check_layer(fmt, x, logits, gate_up, down, topk=topk)
+
 
 @pytest.mark.parametrize("fmt", FMTS)
 def test_one_row_paths_agree(fmt):

@@ -109,6 +109,18 @@ def test_few_rows_prep_in_one_launch(fmt):
         assert torch.equal(moe.moe_prefill(x[:T].contiguous(), gate_up, down, 8, topk_idx=ids, topk_weight=w), out)
 
 
+@pytest.mark.parametrize("fmt", [formats.FMT_I8, formats.FMT_W4])
+@pytest.mark.parametrize("topk,T", [(2, 5), (2, 24), (16, 3), (16, 24), (12, 9)])
+def test_prefill_other_topk(fmt, topk, T):
+    """k other than 8: k 2 in the few-rows launch (5 rows) and the wide one; k 12 and 16 (every expert of 16) take
+    the wide launches at any row count."""
+    gate_up, down = banks(fmt)
+    gen = torch.Generator(device=DEV).manual_seed(50 + topk + T)
+    x = torch.randn((T, H), generator=gen, device=DEV).to(torch.bfloat16)
+    logits = torch.randn((T, 16), generator=gen, device=DEV).to(torch.bfloat16)
+    check(fmt, x, logits, gate_up, down, topk=topk)
+
+
 @pytest.mark.parametrize("fmt", [formats.FMT_I8, formats.FMT_W6])
 def test_given_routing_equals_logits_routing(fmt):
     """topk_idx / topk_weight handed in (as Experts.forward gets them) give the same output as routing inside."""
