@@ -185,13 +185,16 @@ def test_layer_shared_experts(fmt):
     check_layer(fmt, x, logits.to(torch.bfloat16), gate_up, down)
 
 
-def test_layer_reference_shape_256_experts():
-    """The reference model's own shape: 256 experts, FFN 512 (drama3/fish/config.json)."""
-    gate_up, down = layer_banks(formats.FMT_I8, E=256, I=512, seed=3)
-    gen = torch.Generator(device=DEV).manual_seed(8)
-    x = torch.randn((3, 2048), generator=gen, device=DEV).to(torch.bfloat16)
-    logits = torch.randn((3, 256), generator=gen, device=DEV).to(torch.bfloat16)
-    check_layer(formats.FMT_I8, x, logits, gate_up, down)
+@pytest.mark.parametrize("fmt", FMTS)
+@pytest.mark.parametrize("M", [1, 3])
+def test_layer_reference_shape_256_experts(fmt, M):
+    """The reference model's own shape: 256 experts, FFN 512 (drama3/fish/config.json). One row runs 512 workgroups
+    of 8-unit items, 3 rows the general schedule."""
+    gate_up, down = layer_banks(fmt, E=256, I=512, seed=3)
+    gen = torch.Generator(device=DEV).manual_seed(8 + M)
+    x = torch.randn((M, 2048), generator=gen, device=DEV).to(torch.bfloat16)
+    logits = torch.randn((M, 256), generator=gen, device=DEV).to(torch.bfloat16)
+    check_layer(fmt, x, logits, gate_up, down)
 
 
 def test_repeated_launches_are_identical():
@@ -249,13 +252,13 @@ def test_layer_dispatch_matches_oracle(M):
     check_layer(formats.FMT_W4, x, logits, gate_up, down, fused=None)
 
 
-def block_inputs(fmt, seed):
-    gate_up, down = layer_banks(fmt)
+def block_inputs(fmt, seed, E=128, I=768):
+    gate_up, down = layer_banks(fmt, E=E, I=I)
     gen = torch.Generator(device=DEV).manual_seed(seed)
     x = torch.randn((1, 2048), generator=gen, device=DEV).to(torch.bfloat16)
-    router = (torch.randn((128, 2048), generator=gen, device=DEV) * 0.02).to(torch.bfloat16)
-    sg = formats.quantize(torch.randn((1, 2 * 768, 2048), generator=gen, device=DEV) * 0.02, fmt)
-    sd = formats.quantize(torch.randn((1, 2048, 768), generator=gen, device=DEV) * 0.02, fmt)
+    router = (torch.randn((E, 2048), generator=gen, device=DEV) * 0.02).to(torch.bfloat16)
+    sg = formats.quantize(torch.randn((1, 2 * I, 2048), generator=gen, device=DEV) * 0.02, fmt)
+    sd = formats.quantize(torch.randn((1, 2048, I), generator=gen, device=DEV) * 0.02, fmt)
     g = (torch.randn((2048,), generator=gen, device=DEV) * 0.05).to(torch.bfloat16)
     return gate_up, down, x, router, (sg, sd), g
 
@@ -291,6 +294,32 @@ def test_block_router_and_shared_expert(fmt):
     layer = moe.moe_layer(x, lg, gate_up, down, 8)
     for units in (0, 8, 16):
         assert torch.equal(moe.moe_block(x, gate_up, down, 8, router=router, item_units=units), layer)
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+def test_block_reference_shape(fmt):
+    """The block at the reference model's shape (256 experts, FFN 512): 256 router workgroups, 512 routed 8-unit
+    items, the shared expert's 64 items and 32 output blocks in one launch; against the oracle's block from the same
+    logits."""
+    gate_up, down, x, router, (sg, sd), g = block_inputs(fmt, 35, E=256, I=512)
+    out, ids, w, lg = moe.moe_block(x, gate_up, down, 8, router=router, shared=(sg, sd), shared_gate=g, routing=True,
+                                    return_logits=True)
+    torch.cuda.synchronize()
+    assert moe.status(DEV, 2048, 512) == 0
+    got_lg = bf16_bits_to_f32(bits(lg)).astype(np.float64)
+    ref_lg = bf16_bits_to_f32(a8.router_logits(bits(x), bits(router))).astype(np.float64)
+    assert np.all(np.abs(got_lg - ref_lg) <= np.abs(ref_lg) * 2.0 ** -7 + 1e-6)
+    shared = tuple((b.weight.cpu().numpy(), b.scale.contiguous().view(torch.int16).cpu().numpy().view(np.uint16))
+                   for b in (sg, sd))
+    want, want_ids, want_w = a8.moe_block(bits(x), (gate_up.rows, gate_up.cols), (down.rows, down.cols), fmt, 8,
+                                          fetcher(gate_up, down), bits(lg), shared, bits(g))
+    assert np.array_equal(ids.cpu().numpy(), want_ids)
+    assert np.all(np.abs(w.cpu().numpy() - want_w) <= np.abs(want_w) * 2.0 ** -8 + 1e-30)
+    got = bf16_bits_to_f32(bits(out)).astype(np.float64)
+    ref = bf16_bits_to_f32(want).astype(np.float64)
+    err = np.abs(got - ref)
+    assert err.max() <= 2e-2 * np.abs(ref).max(), (err.max(), np.abs(ref).max())
+    assert np.linalg.norm(got - ref) <= 1e-2 * np.linalg.norm(ref)
 
 
 def test_block_rejects_more_rows():
