@@ -14,8 +14,11 @@ Other workloads of the same layer shape:
     --mode resident --format fp8                the reference's own layouts and float activations (kernels.route +
                                                 offload.resident_decode), the drop-in path for converted files
 
-    python bench.py [--steps K] [--warmup W] [--mode decode|prefill] [--format int8|w4a8|w6a8|fp8] [--rows M]
-                    [--layers L] [--routing normal|zipf] [--no-cpu-baseline] [--calibrate-copy]
+    --shape model                               the reference model's own layer: 256 experts of FFN 512
+
+    python bench.py [--steps K] [--warmup W] [--mode decode|prefill|resident|block] [--format int8|w4a8|w6a8|fp8]
+                    [--rows M] [--layers L] [--routing normal|zipf] [--shape config|model] [--no-cpu-baseline]
+                    [--calibrate-copy]
 
 Prints one JSON line: metric (expert-weight GB/s), tokens/s, the roofline of the layer (algorithmic bytes per launch
 / average launch time from HIP events on the replay stream, against 8 TB/s HBM) and the reference's CPU path timed on
@@ -53,7 +56,8 @@ def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
 
-def make_layers(fmt, layers, device, seed=0, experts=E):
+def make_layers(fmt, layers, device, seed=0, experts=None):
+    experts = E if experts is None else experts
     gen = torch.Generator(device=device).manual_seed(seed)
     banks = []
     for _ in range(layers):
@@ -390,6 +394,9 @@ def main():
     p.add_argument("--rows", type=int, default=None)
     p.add_argument("--layers", type=int, default=None)
     p.add_argument("--routing", default=None, choices=["normal", "zipf"])
+    p.add_argument("--shape", default="config", choices=["config", "model"],
+                   help="config: 128 experts of FFN 768 (the headline layer); model: 256 experts of FFN 512, the "
+                        "reference model's own layer (drama3/fish/config.json)")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--calibrate-copy", action="store_true", help="only run the copy kernel that scales PMC counters")
     args = p.parse_args()
@@ -405,6 +412,9 @@ def main():
     args.steps = args.steps or (20 if prefill else 100)
     args.warmup = args.warmup if args.warmup is not None else (3 if prefill else 8)
     fmt = FORMATS[args.format]
+    global E, I
+    if args.shape == "model":
+        E, I = 256, 512
     device = torch.device("cuda:0")
     torch.cuda.set_device(device)
     if args.calibrate_copy:
@@ -427,7 +437,8 @@ def main():
                 f"{'N(0, 1)' if args.routing == 'normal' else 'Zipf(1.1) Gumbel-top-k'}, seeded",
         "config": config,
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / PEAK_GBS, 4), "traffic": measured_traffic(args.mode, args.format, args.rows),
+                     "frac": round(achieved / PEAK_GBS, 4), "traffic": measured_traffic(args.mode, args.format, args.rows)
+                     if args.shape == "config" else None,
                      "kernel": kernel, "launch_us": round(launch_us, 3)},
         "cpu_baseline": cpu,
     }
