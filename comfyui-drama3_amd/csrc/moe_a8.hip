@@ -79,7 +79,7 @@ struct MoeA8Args {
 // LDS carve-up (bytes), shared by host (launch size) and device.
 struct Lds {
   int xq, sx, rt_id, rt_w, emask, ulist, ucount, utok, upair, chunk_first, misc, red, hq, hs, lparts, slot_pair,
-      pair_slot, slot_first, fparts, total;
+      pair_slot, slot_first, fparts, gfirst, gpair, total;
   __host__ __device__ Lds(int M, int topk, int H, int I) {
     int o = 0;
     auto take = [&](int bytes) { int at = o; o += (bytes + 15) & ~15; return at; };
@@ -104,6 +104,8 @@ struct Lds {
     pair_slot = take(MAX_PAIRS * 4);
     slot_first = take((CHUNK_EXPERTS + 1) * 4);
     fparts = take(pairs * 8 * 4);  // every pair's 8 partial outputs of a block (chunks exceed one at 9 experts)
+    gfirst = take((MAX_PAIRS + 1) * 4);
+    gpair = take(MAX_PAIRS * 4);
     total = o;
   }
 };
@@ -134,6 +136,10 @@ struct Ctx {
   int* pair_slot;
   int* slot_first;
   float* fparts;
+  // the general schedule's slots, numbered over the whole union once per launch: union expert u's pairs hold slots
+  // gfirst[u] .. gfirst[u + 1] - 1, slot s holds pair gpair[s] (and pair_slot maps back)
+  int* gfirst;
+  int* gpair;
   int U, nch, n_dn;
   uint32_t epoch;
 };
@@ -336,8 +342,10 @@ D3_INLINE void down_load(const Ctx& cx, int c, int hb, DownRows<F, I>& d) {
 }
 
 // the rest of down item (c, hb) once its loads are out: collect the chunk's hidden rows, quantize, multiply, and write
-// the weighted sum (one chunk) or the partial outputs
-template <int F, int H, int I, int NSUB = 2>
+// the weighted sum (one chunk) or the partial outputs. GLOBAL: the slots come from the launch-wide tables (general
+// schedule) and the gather goes out behind the weight rows at once; otherwise thread 0 numbers the chunk's slots
+// first and the gather waits for the weight rows (one row: see one_row_layer).
+template <int F, int H, int I, int NSUB = 2, bool GLOBAL = false>
 D3_INLINE void down_finish(const Ctx& cx, int c, int hb, const DownRows<F, I>& d) {
   constexpr int STEPS = I / 128;
   constexpr int SHIFT = unpack_shift(F);
@@ -346,23 +354,28 @@ D3_INLINE void down_finish(const Ctx& cx, int c, int hb, const DownRows<F, I>& d
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, q = lane >> 4, col = lane & 15;
   const int M = a.M, K8 = a.topk;
   const int u0 = cx.chunk_first[c], ne = cx.chunk_first[c + 1] - u0;
-  int* slot_first = cx.slot_first;
-  if (tid == 0) {
-    int slot = 0;
-    for (int lj = 0; lj < ne; lj++) {
-      const int uu = u0 + lj;
-      slot_first[lj] = slot;
-      for (int n = 0; n < cx.ucount[uu]; n++) {
-        const int p = cx.upair[uu * MAX_M + n];
-        cx.slot_pair[slot] = p;
-        cx.pair_slot[p] = slot;
-        slot++;
+  const int* slot_first = GLOBAL ? cx.gfirst + u0 : cx.slot_first;
+  const int gb = GLOBAL ? cx.gfirst[u0] : 0;      // the chunk's first slot in the launch-wide numbering
+  const int* slot_pair = GLOBAL ? cx.gpair + gb : cx.slot_pair;
+  if (!GLOBAL) {
+    if (tid == 0) {
+      int slot = 0;
+      for (int lj = 0; lj < ne; lj++) {
+        const int uu = u0 + lj;
+        cx.slot_first[lj] = slot;
+        for (int n = 0; n < cx.ucount[uu]; n++) {
+          const int p = cx.upair[uu * MAX_M + n];
+          cx.slot_pair[slot] = p;
+          cx.pair_slot[p] = slot;
+          slot++;
+        }
       }
+      cx.slot_first[ne] = slot;
     }
-    slot_first[ne] = slot;
+    __syncthreads();
   }
-  __syncthreads();
-  const int P = slot_first[ne];
+  // slot_first[lj] - gb: the chunk's slots count from 0 (its LDS rows)
+  const int P = slot_first[ne] - gb;
   constexpr int T = I / (8 * NSUB);     // gate_up items per expert
   constexpr int HPL = I / 32;           // hidden words per lane of a half-wave
   static_assert(I % 32 == 0, "whole words per lane");
@@ -370,20 +383,20 @@ D3_INLINE void down_finish(const Ctx& cx, int c, int hb, const DownRows<F, I>& d
   if (2 * w < ne) {
     // Each wave serves its two experts on its own: gathers their pairs' hidden rows two at a time (a pair per
     // half-wave: the tiles' maxima and the values in one round trip), quantizes them into its LDS slots and runs.
-    // The gather is issued once the wave's weight rows have arrived (its loads complete in order, so anything issued
-    // earlier would be read early and come back no sooner); the words carry their epoch, so a gather that finds every
-    // word current needs nothing else. Otherwise the stale words are read again, coherently, until they are current.
+    // Without GLOBAL the gather is issued once the wave's weight rows have arrived (its loads complete in order, so
+    // anything issued earlier would be read early and come back no sooner); with GLOBAL it goes out behind them at
+    // once. The words carry their epoch, so a gather that finds every word current needs nothing else. Otherwise the stale words are read again, coherently, until they are current.
     // (Not the experts' counters first: every waiting wave would poll the same few words, and by the time a first
     // gather is back the late items are mostly published.)
     const int la = 2 * w, lb = 2 * w + 1;
     const bool has_b = lb < ne;
-    settle();
-    const int s0 = slot_first[la], s1 = slot_first[has_b ? lb + 1 : la + 1];
+    if (!GLOBAL) settle();
+    const int s0 = slot_first[la] - gb, s1 = slot_first[has_b ? lb + 1 : la + 1] - gb;
     const int half = lane >> 5, hl = lane & 31;
     for (int sp = s0; sp < s1; sp += 2) {
       const int slot = sp + half;
       const bool on = slot < s1;
-      const int p = cx.slot_pair[on ? slot : s0];
+      const int p = slot_pair[on ? slot : s0];
       // lane hl reads words hl + 32 j: every load covers 256 contiguous bytes of the half-wave's row
       const uint64_t* hrow = a.hidden + (size_t)p * I + hl;
       // every lane loads (addresses clamped to a pair and an item of the unit), without a branch per load; lanes
@@ -462,10 +475,10 @@ D3_INLINE void down_finish(const Ctx& cx, int c, int hb, const DownRows<F, I>& d
       // columns: pass 0 = a's pairs (then b's, in one pass); pass 1 = b's pairs
       int slot = -1;
       if (pass == 0) {
-        if (col < na) slot = slot_first[la] + col;
-        else if (one_pass && col < na + nb) slot = slot_first[lb] + col - na;
+        if (col < na) slot = slot_first[la] - gb + col;
+        else if (one_pass && col < na + nb) slot = slot_first[lb] - gb + col - na;
       } else if (col < nb) {
-        slot = slot_first[lb] + col;
+        slot = slot_first[lb] - gb + col;
       }
       const uint8_t* xp = cx.hq + (size_t)(slot >= 0 ? slot : 0) * I;
       i32x4 iacc = {0, 0, 0, 0};
@@ -526,7 +539,7 @@ D3_INLINE void down_finish(const Ctx& cx, int c, int hb, const DownRows<F, I>& d
   } else {
     for (int idx = tid; idx < P * 8; idx += 256) {
       const int slot = idx >> 3, r = idx & 7;
-      put_tagged(a.parts + (size_t)cx.slot_pair[slot] * H + 8 * hb + r, cx.lparts[slot * 8 + r], cx.epoch);
+      put_tagged(a.parts + (size_t)slot_pair[slot] * H + 8 * hb + r, cx.lparts[slot * 8 + r], cx.epoch);
     }
     if (c == cx.nch - 1) {
       // the last chunk's item gathers every pair's partial outputs of this block
@@ -549,13 +562,13 @@ D3_INLINE void down_finish(const Ctx& cx, int c, int hb, const DownRows<F, I>& d
   }
 }
 
-// down item (c, hb)
-template <int F, int H, int I>
+// down item (c, hb); GLOBAL as for down_finish
+template <int F, int H, int I, bool GLOBAL>
 D3_INLINE void down_item(const Ctx& cx, int c, int hb) {
   __syncthreads();  // the previous item's readers of the slot tables and partial outputs are done
   DownRows<F, I> d;
   down_load<F, H, I>(cx, c, hb, d);
-  down_finish<F, H, I>(cx, c, hb, d);
+  down_finish<F, H, I, 2, GLOBAL>(cx, c, hb, d);
 }
 
 // The router's logit e for one row: bf16(x . router[e]) with float sums (model.py:115), x as every wave holds it
@@ -867,6 +880,8 @@ D3_INLINE Ctx make_ctx(const MoeA8Args& a, uint8_t* lds, int H, int I) {
   cx.slot_pair = (int*)(lds + L.slot_pair);
   cx.pair_slot = (int*)(lds + L.pair_slot);
   cx.slot_first = (int*)(lds + L.slot_first);
+  cx.gfirst = (int*)(lds + L.gfirst);
+  cx.gpair = (int*)(lds + L.gpair);
   cx.fparts = (float*)(lds + L.fparts);
   cx.epoch = launch_epoch();
   return cx;
@@ -896,6 +911,9 @@ __global__ void __launch_bounds__(256, WPC) moe_a8_kernel(MoeA8Args a) {
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int M = a.M, E = a.E, K8 = a.topk;
   Ctx cx = make_ctx(a, lds, H, I);
+  // the down items' schedule (see the item loop): launch-wide slots and lag 2 for the 4- and 6-bit formats
+  constexpr bool EARLY = F == FMT_W4 || F == FMT_W6;
+  constexpr int LAG = EARLY ? 2 : 1;
 
   // ---- per row: routed by wave t % 4 and its activations quantized by wave (t + 1) % 4, so that with one row the
   // two loads and what follows them overlap; each wave issues its loads before using any of them
@@ -929,9 +947,15 @@ __global__ void __launch_bounds__(256, WPC) moe_a8_kernel(MoeA8Args a) {
           cx.ucount[lane] = 1;
           cx.utok[lane * MAX_M] = 0;
           cx.upair[lane * MAX_M] = (uint8_t)lane;
+          if constexpr (EARLY) {
+            cx.gfirst[lane] = lane;
+            cx.gpair[lane] = lane;
+            cx.pair_slot[lane] = lane;
+          }
         }
       }
       if (M == 1 && lane == 0) {
+        if constexpr (EARLY) cx.gfirst[K8] = K8;
         cx.chunk_first[0] = 0;
         cx.chunk_first[1] = K8;
         cx.misc[0] = K8;
@@ -969,27 +993,47 @@ __global__ void __launch_bounds__(256, WPC) moe_a8_kernel(MoeA8Args a) {
 #pragma unroll
         for (int k = 0; k < 4; k++) m[k] |= (e == lane + 64 * k ? 1u : 0u) << t;
       }
-    int base = 0;
+    // and, for the 4- and 6-bit formats, the launch-wide slots: union expert pos holds slots gfirst[pos] .. + its
+    // pair count - 1 (a scan of the counts over the lanes)
+    int base = 0, sbase = 0;
 #pragma unroll
     for (int k = 0; k < 4; k++) {
       const int e = lane + 64 * k;
       const uint64_t ball = __ballot(m[k] != 0u);
       const int pos = base + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(ball >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)ball, 0u));
+      const int cnt = __popc(m[k]);
+      int incl = cnt;
+      if constexpr (EARLY) {
+#pragma unroll
+        for (int dd = 1; dd < 64; dd <<= 1) {
+          const int v = __shfl_up(incl, dd);
+          if (lane >= dd) incl += v;
+        }
+      }
+      const int g0 = sbase + incl - cnt;
       if (m[k] != 0u) {
         cx.ulist[pos] = e;
-        cx.ucount[pos] = __popc(m[k]);
+        cx.ucount[pos] = cnt;
+        if constexpr (EARLY) cx.gfirst[pos] = g0;
         int n = 0;
         for (int t = 0; t < M; t++) {
           if (!((m[k] >> t) & 1u)) continue;
           int j = 0;
           for (int jj = 0; jj < K8; jj++) j = cx.rt_id[t * MAX_K + jj] == e ? jj : j;
+          const int pr = t * K8 + j;
           cx.utok[pos * MAX_M + n] = (uint8_t)t;
-          cx.upair[pos * MAX_M + n] = (uint8_t)(t * K8 + j);
+          cx.upair[pos * MAX_M + n] = (uint8_t)pr;
+          if constexpr (EARLY) {
+            cx.gpair[g0 + n] = pr;
+            cx.pair_slot[pr] = g0 + n;
+          }
           n++;
         }
       }
       base += __popcll(ball);
+      if constexpr (EARLY) sbase += __shfl(incl, 63);
     }
+    if (EARLY && lane == 0) cx.gfirst[base] = sbase;
     // down chunks: consecutive experts, at most CHUNK_EXPERTS of them and CHUNK_PAIRS pairs; with M * topk <= 32
     // pairs that is simply 8 experts each
     if (M * K8 <= CHUNK_PAIRS) {
@@ -1026,11 +1070,19 @@ __global__ void __launch_bounds__(256, WPC) moe_a8_kernel(MoeA8Args a) {
   cx.nch = cx.misc[1];
   cx.n_dn = cx.nch * NHB;
   const int n_items = U * T + cx.n_dn;
+  // When the down items of a chunk start. With the 8-bit formats the gate_up streams are the long part, and the
+  // chunk's down items follow the next chunk's gate_up items (lag 1), each numbering its slots first (thread 0), so
+  // that their gathers come once most words are published: gathers issued earlier compete with the streams. With
+  // the 4- and 6-bit formats the down items are the tail: they follow two chunks' gate_up items (lag 2) and gather
+  // behind their weight rows at once, from slots numbered once per launch. Measured, us per layer at 2 / 3 / 4 / 5
+  // rows: W4A8 21.6 / 30.9 / 38.9 / 48.4 with the 8-bit choice, 21.5 / 30.2 / 36.4 / 48.1 with this one; W6A8 at 4
+  // rows 45.9 / 43.5; int8 25.2 / 38.8 / 44.6 / 55.8 against 26.3 / 40.3 / 45.3 / 56.7 with the 4-bit choice.
+  // (EARLY and LAG are set at the top of the kernel.)
   int parity = 0;
   for (int item = blockIdx.x; item < n_items; item += gridDim.x) {
-    // segments: gate_up(chunk c), then down(chunk c - 1)
+    // segments: gate_up(chunk c), then down(chunk c - LAG)
     int base = 0;
-    for (int c = 0; c <= cx.nch; c++) {
+    for (int c = 0; c < cx.nch + LAG; c++) {
       if (c < cx.nch) {
         const int u0 = cx.chunk_first[c], ne = cx.chunk_first[c + 1] - u0;
         if (item < base + ne * T) {
@@ -1044,9 +1096,9 @@ __global__ void __launch_bounds__(256, WPC) moe_a8_kernel(MoeA8Args a) {
         }
         base += ne * T;
       }
-      if (c >= 1) {
+      if (c >= LAG) {
         if (item < base + NHB) {
-          down_item<F, H, I>(cx, c - 1, item - base);
+          down_item<F, H, I, EARLY>(cx, c - LAG, item - base);
           break;
         }
         base += NHB;
