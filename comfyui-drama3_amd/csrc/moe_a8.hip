@@ -128,6 +128,7 @@ struct Ctx {
   uint8_t* upair;
   int* chunk_first;
   int* misc;
+  uint32_t* emask;  // [MAX_E] the union's build: rows per expert, then (union position << 16 | rows)
   float* red;
   uint8_t* hq;
   float* hs;
@@ -873,6 +874,7 @@ D3_INLINE Ctx make_ctx(const MoeA8Args& a, uint8_t* lds, int H, int I) {
   cx.upair = lds + L.upair;
   cx.chunk_first = (int*)(lds + L.chunk_first);
   cx.misc = (int*)(lds + L.misc);
+  cx.emask = (uint32_t*)(lds + L.emask);
   cx.red = (float*)(lds + L.red);
   cx.hq = lds + L.hq;
   cx.hs = (float*)(lds + L.hs);
@@ -984,15 +986,22 @@ __global__ void __launch_bounds__(256, WPC) moe_a8_kernel(MoeA8Args a) {
   }
   __syncthreads();
 
-  // ---- union of the rows' experts, ascending, built by wave 0: lane l owns experts l, l + 64, l + 128, l + 192
+  // ---- union of the rows' experts, ascending, built by wave 0: lane l owns experts l, l + 64, l + 128, l + 192.
+  // Each expert's mask of rows comes from LDS atomics, one per (row, rank) pair; the experts are compacted by a
+  // ballot; each pair then finds its place among its expert's rows (rows ascending) from the expert's word.
   if (M > 1 && w == 0) {
-    uint32_t m[4] = {0u, 0u, 0u, 0u};
-    for (int t = 0; t < M; t++)
-      for (int j = 0; j < K8; j++) {
-        const int e = cx.rt_id[t * MAX_K + j];
+    const int npairs = M * K8;
 #pragma unroll
-        for (int k = 0; k < 4; k++) m[k] |= (e == lane + 64 * k ? 1u : 0u) << t;
-      }
+    for (int k = 0; k < 4; k++) cx.emask[lane + 64 * k] = 0u;
+    lds_settle();
+    for (int p = lane; p < npairs; p += 64) {
+      const int t = p / K8;
+      atomicOr(&cx.emask[cx.rt_id[t * MAX_K + p - t * K8]], 1u << t);
+    }
+    lds_settle();
+    uint32_t m[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) m[k] = lane + 64 * k < E ? cx.emask[lane + 64 * k] : 0u;
     // and, for the 4- and 6-bit formats, the launch-wide slots: union expert pos holds slots gfirst[pos] .. + its
     // pair count - 1 (a scan of the counts over the lanes)
     int base = 0, sbase = 0;
@@ -1015,25 +1024,24 @@ __global__ void __launch_bounds__(256, WPC) moe_a8_kernel(MoeA8Args a) {
         cx.ulist[pos] = e;
         cx.ucount[pos] = cnt;
         if constexpr (EARLY) cx.gfirst[pos] = g0;
-        int n = 0;
-        for (int t = 0; t < M; t++) {
-          if (!((m[k] >> t) & 1u)) continue;
-          int j = 0;
-          for (int jj = 0; jj < K8; jj++) j = cx.rt_id[t * MAX_K + jj] == e ? jj : j;
-          const int pr = t * K8 + j;
-          cx.utok[pos * MAX_M + n] = (uint8_t)t;
-          cx.upair[pos * MAX_M + n] = (uint8_t)pr;
-          if constexpr (EARLY) {
-            cx.gpair[g0 + n] = pr;
-            cx.pair_slot[pr] = g0 + n;
-          }
-          n++;
-        }
+        cx.emask[e] = (uint32_t)pos << 16 | m[k];  // rows < 16: the mask fits the low half
       }
       base += __popcll(ball);
       if constexpr (EARLY) sbase += __shfl(incl, 63);
     }
     if (EARLY && lane == 0) cx.gfirst[base] = sbase;
+    lds_settle();
+    for (int p = lane; p < npairs; p += 64) {
+      const int t = p / K8;
+      const uint32_t word = cx.emask[cx.rt_id[t * MAX_K + p - t * K8]];
+      const int pos = (int)(word >> 16), n = __popc(word & 0xFFFFu & ((1u << t) - 1u));
+      cx.utok[pos * MAX_M + n] = (uint8_t)t;
+      cx.upair[pos * MAX_M + n] = (uint8_t)p;
+      if constexpr (EARLY) {
+        cx.gpair[cx.gfirst[pos] + n] = p;
+        cx.pair_slot[p] = cx.gfirst[pos] + n;
+      }
+    }
     // down chunks: consecutive experts, at most CHUNK_EXPERTS of them and CHUNK_PAIRS pairs; with M * topk <= 32
     // pairs that is simply 8 experts each
     if (M * K8 <= CHUNK_PAIRS) {
