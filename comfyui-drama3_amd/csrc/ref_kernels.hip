@@ -55,7 +55,7 @@ __global__ void __launch_bounds__(256) route_kernel(const uint16_t* logits, int 
       uint32_t m = key[0];
 #pragma unroll
       for (int j = 1; j < KPL; j++) m = max(m, key[j]);
-      m = wave_max_u32(m);
+      m = wave_max_u32_v(m);  // on the vector unit: the k rounds form one dependent chain
 #pragma unroll
       for (int j = 0; j < KPL; j++) key[j] = key[j] == m ? 0u : key[j];
       id[r] = route_key_index(m);
@@ -582,11 +582,12 @@ __global__ void __launch_bounds__(256) resident_gu_kernel(const uint16_t* x, con
   }
 }
 
-// down: grid (H / 8), workgroup (output rows m0 .. m0 + 7) for all k experts, so the routing-weighted sum stays in the
+// down: grid (H / 4), workgroup (output rows m0 .. m0 + 3) for all k experts, so the routing-weighted sum stays in the
 // workgroup. The rows' bytes for every expert are loaded first; then each expert's hidden row h_j = SiLU(gate) * up
-// of gu[j] (rotated per 256 unless fp8) goes into LDS, and 2 rows per wave give out[m] = bf16(sum_j w_j *
-// (row . h_j) * scale), experts in order as weighted_sum sums them.
-constexpr int DN_ROWS = 8, MAX_K_RES = 8;
+// of gu[j] (rotated per 256 unless fp8) goes into LDS, and a row per wave gives out[m] = bf16(sum_j w_j *
+// (row . h_j) * scale), experts in order as weighted_sum sums them. (8 rows per workgroup, H / 8 = 256 of them,
+// left one workgroup per CU: int8 25.5 against 24.2 us per layer, W4A8 30.7 against 26.8, fp8 26.9 against 25.0.)
+constexpr int DN_ROWS = 4, MAX_K_RES = 8;
 template <int KIND, int K>
 __global__ void __launch_bounds__(256) resident_dn_kernel(const float* gu, const int64_t* ids, const float* wts, int k,
                                                           const uint8_t* bw, const void* bs, const float* bc,
