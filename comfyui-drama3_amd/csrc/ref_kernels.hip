@@ -586,7 +586,8 @@ __global__ void __launch_bounds__(256) resident_gu_kernel(const uint16_t* x, con
 // workgroup. The rows' bytes for every expert are loaded first; then each expert's hidden row h_j = SiLU(gate) * up
 // of gu[j] (rotated per 256 unless fp8) goes into LDS, and a row per wave gives out[m] = bf16(sum_j w_j *
 // (row . h_j) * scale), experts in order as weighted_sum sums them. (8 rows per workgroup, H / 8 = 256 of them,
-// left one workgroup per CU: int8 25.5 against 24.2 us per layer, W4A8 30.7 against 26.8, fp8 26.9 against 25.0.)
+// left one workgroup per CU: int8 25.5 against 24.2 us per layer, W4A8 30.7 against 26.8, fp8 26.9 against 25.0;
+// 2 rows, in workgroups of two waves that each recompute the hidden rows: int8 27.7, W4A8 30.3, fp8 27.6.)
 constexpr int DN_ROWS = 4, MAX_K_RES = 8;
 template <int KIND, int K>
 __global__ void __launch_bounds__(256) resident_dn_kernel(const float* gu, const int64_t* ids, const float* wts, int k,
