@@ -346,7 +346,7 @@ D3_INLINE void down_load(const Ctx& cx, int c, int hb, DownRows<F, I>& d) {
 // the weighted sum (one chunk) or the partial outputs. GLOBAL: the slots come from the launch-wide tables (general
 // schedule) and the gather goes out behind the weight rows at once; otherwise thread 0 numbers the chunk's slots
 // first and the gather waits for the weight rows (one row: see one_row_layer).
-template <int F, int H, int I, int NSUB = 2, bool GLOBAL = false>
+template <int F, int H, int I, int NSUB = 2, bool GLOBAL = false, bool SPREAD = false>
 D3_INLINE void down_finish(const Ctx& cx, int c, int hb, const DownRows<F, I>& d) {
   constexpr int STEPS = I / 128;
   constexpr int SHIFT = unpack_shift(F);
@@ -381,20 +381,24 @@ D3_INLINE void down_finish(const Ctx& cx, int c, int hb, const DownRows<F, I>& d
   constexpr int HPL = I / 32;           // hidden words per lane of a half-wave
   static_assert(I % 32 == 0, "whole words per lane");
   constexpr int TPH = (T + 31) / 32;    // tile maxima per lane of a half-wave
-  if (2 * w < ne) {
-    // Each wave serves its two experts on its own: gathers their pairs' hidden rows two at a time (a pair per
-    // half-wave: the tiles' maxima and the values in one round trip), quantizes them into its LDS slots and runs.
-    // Without GLOBAL the gather is issued once the wave's weight rows have arrived (its loads complete in order, so
-    // anything issued earlier would be read early and come back no sooner); with GLOBAL it goes out behind them at
-    // once. The words carry their epoch, so a gather that finds every word current needs nothing else. Otherwise the stale words are read again, coherently, until they are current.
-    // (Not the experts' counters first: every waiting wave would poll the same few words, and by the time a first
-    // gather is back the late items are mostly published.)
-    const int la = 2 * w, lb = 2 * w + 1;
-    const bool has_b = lb < ne;
+  // The pairs' hidden rows are gathered two at a time per wave (a pair per half-wave: the tiles' maxima and the
+  // values in one round trip) and quantized into LDS slots. Each wave gathers its own two experts' pairs, or with
+  // SPREAD the chunk's pairs go round the workgroup's 8 half-waves (one round trip for up to 8 pairs, where a wave
+  // whose experts hold 3 or more needed two). Without GLOBAL the gather is issued once the wave's weight rows have
+  // arrived (its loads complete in order, so anything issued earlier would be read early and come back no sooner);
+  // with GLOBAL it goes out behind them at once. The words carry their epoch, so a gather that finds every word
+  // current needs nothing else. Otherwise the stale words are read again, coherently, until they are current. (Not
+  // the experts' counters first: every waiting wave would poll the same few words, and by the time a first gather is
+  // back the late items are mostly published.)
+  const int la = 2 * w, lb = 2 * w + 1;
+  const bool has_b = lb < ne;
+  const bool gathers = SPREAD || la < ne;
+  const int s0 = SPREAD || !gathers ? 0 : slot_first[la] - gb;
+  const int s1 = SPREAD ? P : !gathers ? 0 : slot_first[has_b ? lb + 1 : la + 1] - gb;
+  if (gathers) {
     if (!GLOBAL) settle();
-    const int s0 = slot_first[la] - gb, s1 = slot_first[has_b ? lb + 1 : la + 1] - gb;
     const int half = lane >> 5, hl = lane & 31;
-    for (int sp = s0; sp < s1; sp += 2) {
+    for (int sp = SPREAD ? 2 * w : s0; sp < s1; sp += SPREAD ? 8 : 2) {
       const int slot = sp + half;
       const bool on = slot < s1;
       const int p = slot_pair[on ? slot : s0];
@@ -467,7 +471,11 @@ D3_INLINE void down_finish(const Ctx& cx, int c, int hb, const DownRows<F, I>& d
         if (hl == 0) cx.hs[slot] = amax / QMAX;
       }
     }
-    settle();  // this wave's LDS slots are written before its lanes read each other's
+  }
+  // the slots are in LDS before the products read them: this wave's own, or with SPREAD every wave's
+  if (SPREAD) __syncthreads();
+  else settle();
+  if (la < ne) {
     const int na = slot_first[la + 1] - slot_first[la];
     const int nb = has_b ? slot_first[lb + 1] - slot_first[lb] : 0;
     const bool one_pass = na + nb <= 16;
@@ -569,7 +577,7 @@ D3_INLINE void down_item(const Ctx& cx, int c, int hb) {
   __syncthreads();  // the previous item's readers of the slot tables and partial outputs are done
   DownRows<F, I> d;
   down_load<F, H, I>(cx, c, hb, d);
-  down_finish<F, H, I, 2, GLOBAL>(cx, c, hb, d);
+  down_finish<F, H, I, 2, GLOBAL, true>(cx, c, hb, d);
 }
 
 // The router's logit e for one row: bf16(x . router[e]) with float sums (model.py:115), x as every wave holds it
