@@ -71,9 +71,10 @@ D3_INLINE int wave_exclusive_scan(int v, int lane, int& total) {
   return incl - v;
 }
 
-// (a workgroup of 1024 threads; ids may be in LDS or device memory; perm_lds, if given, gets a copy of perm)
+// (a workgroup of 1024 threads; ids may be in LDS or device memory; inv_lds, if given, gets each pair's sorted
+// position)
 D3_INLINE void group_pairs(const int64_t* ids, int P, int E, int* counts, int* offsets, int* perm, int4* units,
-                           int* meta, int* perm_lds = nullptr) {
+                           int* meta, int* inv_lds = nullptr) {
   __shared__ int cnt[MAX_EXPERTS], cur[MAX_EXPERTS], by_rank[MAX_EXPERTS], rank_base[MAX_EXPERTS];
   __shared__ int used;
   const int tid = threadIdx.x;
@@ -132,7 +133,7 @@ D3_INLINE void group_pairs(const int64_t* ids, int P, int E, int* counts, int* o
   for (int p = tid; p < P; p += 1024) {
     const int at = atomicAdd(&cur[(int)min<int64_t>(max<int64_t>(ids[p], 0), E - 1)], 1);
     perm[at] = p;
-    if (perm_lds) perm_lds[at] = p;
+    if (inv_lds) inv_lds[p] = at;
   }
 }
 
@@ -144,8 +145,8 @@ __global__ void __launch_bounds__(1024) group_kernel(const int64_t* ids, int P, 
 // ----------------------------------------------------------------------------------------- few rows, one launch
 // T <= 16 rows in one workgroup of 16 waves, the steps route, group and quantize x of the many-row path in one
 // launch: wave t routes row t (the fused layer's TopKeys, kernels.py:39-67's rule; or copies the given ids and
-// weights), the workgroup groups the pairs (group_pairs), then quantizes x into the pairs' sorted order, a row per
-// wave in turn.
+// weights), the workgroup groups the pairs (group_pairs), then wave t quantizes row t once (loaded with the logits)
+// and stores its codes at each of its k pairs' sorted positions.
 struct SmallPrepArgs {
   const uint16_t* logits;   // [T, E] bf16, or null with ids_in / weights_in
   const int64_t* ids_in;
@@ -169,10 +170,13 @@ template <int F, int H, int KPL>
 __global__ void __launch_bounds__(1024) small_prep_kernel(SmallPrepArgs a) {
   constexpr float QMAX = act_qmax<F>();
   __shared__ int64_t lids[16 * 8];
-  __shared__ int lperm[16 * 8];
+  __shared__ int linv[16 * 8];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int T = a.T, E = a.E, k = a.k, P = T * k;
+  i32x4 xr[H / 512];
   if (w < T) {
+#pragma unroll
+    for (int c = 0; c < H / 512; c++) xr[c] = *(const i32x4*)(a.x + (size_t)w * H + 512 * c + 8 * lane);
     if (a.logits) {
       uint32_t lb[KPL];
 #pragma unroll
@@ -196,38 +200,25 @@ __global__ void __launch_bounds__(1024) small_prep_kernel(SmallPrepArgs a) {
     }
   }
   __syncthreads();
-  group_pairs(lids, P, E, a.counts, a.offsets, a.perm, a.units, a.meta, lperm);
+  group_pairs(lids, P, E, a.counts, a.offsets, a.perm, a.units, a.meta, linv);
   __syncthreads();
-  // sorted position sp = w + 16 i: each wave loads four rows of x at once (clamped, so every load is issued), then
-  // quantizes them
-  constexpr int RB = 4;
-  for (int i0 = 0; w + 16 * i0 < P; i0 += RB) {
-    i32x4 r[RB][H / 512];
+  if (w < T) {
+    float v[H / 512][8];
+    float amax = 0.0f;
 #pragma unroll
-    for (int b = 0; b < RB; b++) {
-      const int sp = min(w + 16 * (i0 + b), P - 1);
-      const int row = lperm[sp] / k;
+    for (int c = 0; c < H / 512; c++) {
+      const uint32_t w4[4] = {(uint32_t)xr[c].x, (uint32_t)xr[c].y, (uint32_t)xr[c].z, (uint32_t)xr[c].w};
 #pragma unroll
-      for (int c = 0; c < H / 512; c++) r[b][c] = *(const i32x4*)(a.x + (size_t)row * H + 512 * c + 8 * lane);
-    }
-#pragma unroll
-    for (int b = 0; b < RB; b++) {
-      const int sp = w + 16 * (i0 + b);
-      if (sp >= P) break;
-      float v[H / 512][8];
-      float amax = 0.0f;
-#pragma unroll
-      for (int c = 0; c < H / 512; c++) {
-        const uint32_t w4[4] = {(uint32_t)r[b][c].x, (uint32_t)r[b][c].y, (uint32_t)r[b][c].z, (uint32_t)r[b][c].w};
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-          v[c][2 * j] = bf16_to_f32(w4[j] & 0xFFFFu);
-          v[c][2 * j + 1] = bf16_to_f32(w4[j] >> 16);
-          amax = fmaxf(amax, fmaxf(fabsf(v[c][2 * j]), fabsf(v[c][2 * j + 1])));
-        }
+      for (int j = 0; j < 4; j++) {
+        v[c][2 * j] = bf16_to_f32(w4[j] & 0xFFFFu);
+        v[c][2 * j + 1] = bf16_to_f32(w4[j] >> 16);
+        amax = fmaxf(amax, fmaxf(fabsf(v[c][2 * j]), fabsf(v[c][2 * j + 1])));
       }
-      amax = wave_max_f32(amax);
-      const float inv = amax > 0.0f ? QMAX / amax : 0.0f;
+    }
+    amax = wave_max_f32(amax);
+    const float inv = amax > 0.0f ? QMAX / amax : 0.0f;
+    for (int j = 0; j < k; j++) {
+      const int sp = linv[w * k + j];
 #pragma unroll
       for (int c = 0; c < H / 512; c++) store_act8<F>(a.xq + (size_t)sp * H + 512 * c + 8 * lane, v[c], inv);
       if (lane == 0) a.xs[sp] = amax / QMAX;
@@ -625,11 +616,11 @@ int d3_moe_a8_prefill(const d3_moe_a8_prefill_desc* d, void* stream) {
   const int P = d->T * d->topk;
   int64_t* ids = (int64_t*)(ws + L.ids);
   float* weights = (float*)(ws + L.weights);
-  // few rows: routing, grouping and x's quantization in one launch. One
-  // workgroup quantizes every sorted row, so past 6 rows (48 pairs at top-8)
-  // the three wide launches it replaces are quicker (measured on a
-  // 2048 x 768, 128-expert W4A8 layer: 1.7 us saved at 5 rows, even at 6-7).
-  const bool small = d->T <= 6 && d->topk <= 8 && d->E <= 256;
+  // up to 16 rows: routing, grouping and x's quantization in one launch (one workgroup; each row quantized once and
+  // its codes stored at its k sorted positions). Measured on a 2048 x 768, 128-expert layer, us per layer against the
+  // three wide launches: int8 66.6 / 70.8 at 7 rows, 70.2 / 74.0 at 8, 84.2 / 87.1 at 12, 97.2 / 98.6 at 16; W4A8
+  // 52.1 / 56.6, 55.5 / 59.8, 64.3 / 67.3, 73.6 / 75.3.
+  const bool small = d->T <= 16 && d->topk <= 8 && d->E <= 256;
   if (small) {
     SmallPrepArgs sa;
     sa.logits = (const uint16_t*)d->logits;

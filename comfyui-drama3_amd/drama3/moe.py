@@ -59,8 +59,8 @@ def status(device, H, I, stream=None):
 
 # From this many rows on, moe_layer runs the grouped path (d3_moe_a8_prefill): its persistent grouped products read
 # each expert once for all rows and keep the memory busy, where the fused kernel's items for several rows queue up
-# behind each other. Measured on MI355X (us per layer, fused / grouped): int8 4 rows 45.8 / 56.2, 5 rows 58.6 / 62.3,
-# 6 rows 70.0 / 67.4, 16 rows 193 / 99; W4A8 4 rows 40.4 / 46.0, 5 rows 50.4 / 50.4, 6 rows 57.6 / 53.6.
+# behind each other. Measured on MI355X (us per layer, fused / grouped): int8 4 rows 42.1 / 52.8, 5 rows 52.5 / 58.3,
+# 6 rows 69.4 / 63.1, 16 rows 171 / 100; W4A8 4 rows 33.4 / 43.0, 5 rows 43.9 / 46.7, 6 rows 55.9 / 49.5.
 GROUPED_FROM_ROWS = 6
 
 

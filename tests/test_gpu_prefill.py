@@ -95,17 +95,18 @@ def test_prefill_single_row_and_reference_shape():
 
 @pytest.mark.parametrize("fmt", FMTS)
 def test_few_rows_prep_in_one_launch(fmt):
-    """Up to 6 rows route, group and quantize x in one launch; 7 rows take the three wide launches. Each output row
-    depends on its own row only, so 6 rows and the first 6 of 7 agree bit for bit; 1, 3 and 6 rows match the
-    oracle, with the routing given as well as computed."""
+    """Up to 16 rows route, group and quantize x in one launch (each row quantized once, its codes stored at its
+    pairs' sorted positions); 17 rows take the three wide launches. Each output row depends on its own row only, so
+    T rows and the first T of 17 agree bit for bit; 1, 3, 7 and 16 rows match the oracle, with the routing given as
+    well as computed."""
     gate_up, down = banks(fmt)
     gen = torch.Generator(device=DEV).manual_seed(40 + fmt)
-    x = torch.randn((7, H), generator=gen, device=DEV).to(torch.bfloat16)
-    logits = torch.randn((7, 16), generator=gen, device=DEV).to(torch.bfloat16)
-    seven = moe.moe_prefill(x, gate_up, down, 8, logits=logits)
-    for T in (1, 3, 6):
+    x = torch.randn((17, H), generator=gen, device=DEV).to(torch.bfloat16)
+    logits = torch.randn((17, 16), generator=gen, device=DEV).to(torch.bfloat16)
+    wide = moe.moe_prefill(x, gate_up, down, 8, logits=logits)
+    for T in (1, 3, 7, 16):
         out, ids, w = check(fmt, x[:T].contiguous(), logits[:T].contiguous(), gate_up, down)
-        assert torch.equal(out, seven[:T])
+        assert torch.equal(out, wide[:T])
         assert torch.equal(moe.moe_prefill(x[:T].contiguous(), gate_up, down, 8, topk_idx=ids, topk_weight=w), out)
 
 
@@ -145,7 +146,7 @@ def test_prefill_close_to_fused_decode(fmt):
     assert torch.linalg.norm(a - b) <= 1e-2 * torch.linalg.norm(b)
 
 
-@pytest.mark.parametrize("rows", [16, 4])
+@pytest.mark.parametrize("rows", [24, 16, 4])
 def test_prefill_graph_replays(rows):
     gate_up, down = banks(formats.FMT_F8)
     gen = torch.Generator(device=DEV).manual_seed(35)
