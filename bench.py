@@ -401,8 +401,9 @@ def main():
     p.add_argument("--calibrate-copy", action="store_true", help="only run the copy kernel that scales PMC counters")
     args = p.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print("bench.py measures one GPU: the routed-expert path runs on one MI355X (see DESIGN.md for how it would "
-              "shard); run it with --gpus 1", file=sys.stderr)
+        print("bench.py measures one GPU: the routed-expert path runs on one MI355X, each GPU holding every expert "
+              "of every layer (decode lines split across GPUs need no exchange); run it with --gpus 1",
+              file=sys.stderr)
         sys.exit(2)
     prefill = args.mode == "prefill"
     args.format = args.format or ("fp8" if prefill else "int8")
