@@ -355,6 +355,8 @@ def run_resident(args, fmt, device):
 
     def layer_step(x, lg, layer):
         kind, banks, cbs = layers[layer]
+        if args.routed:  # the routing in the gate_up launch's prologue
+            return offload.routed_decode(x, lg, TOPK, banks, rows, kind, cbs)[0]
         ids, w = kernels.route(lg, TOPK)
         return offload.resident_decode(x, ids[0], w[0], banks, rows, kind, cbs)
 
@@ -380,8 +382,9 @@ def run_resident(args, fmt, device):
     config = {"workload": f"routed-expert MoE layer in the reference's {args.format} layout (float activations, "
                           f"route + resident_decode), decode M=1, hidden {H}, FFN {I}, {E} experts top-{TOPK}, "
                           f"{L} layers chained per token", "rows": 1, "layers": L, "unique_experts_per_launch": TOPK}
-    return (ms, layer_bytes * L * args.steps, args.steps * L, args.steps, config,
-            "route + resident_decode (3 launches: route, gate_up, down)", None)
+    what = ("routed_decode (2 launches: gate_up with the routing, down)" if args.routed else
+            "route + resident_decode (3 launches: route, gate_up, down)")
+    return ms, layer_bytes * L * args.steps, args.steps * L, args.steps, config, what, None
 
 
 def main():
@@ -390,6 +393,7 @@ def main():
     p.add_argument("--steps", type=int, default=None)
     p.add_argument("--warmup", type=int, default=None)
     p.add_argument("--mode", default="decode", choices=["decode", "prefill", "resident", "block"])
+    p.add_argument("--routed", action="store_true", help="--mode resident: route inside the gate_up launch")
     p.add_argument("--format", default=None, choices=sorted(FORMATS))
     p.add_argument("--rows", type=int, default=None)
     p.add_argument("--layers", type=int, default=None)

@@ -547,15 +547,44 @@ template <int KIND> D3_INLINE float row_scale(const void* bs, const float* bc, s
   else return bc[row];
 }
 
-template <int KIND, int K>
-__global__ void __launch_bounds__(256) resident_gu_kernel(const uint16_t* x, const int64_t* ids, const uint8_t* bw,
-                                                          const void* bs, const float* bc, const float* codebook,
-                                                          float* gu, int N) {
+//
+// ROUTED: the row's routing (kernels.py:39-67 on logits [n <= 256] bf16) runs first in every workgroup, on wave 0:
+// the top-k keys and softmax weights as route_kernel computes them (the same key order, the same exponentials summed
+// in rank order), expert j from LDS; workgroup (0, 0) writes ids [k] and weights [k] for the down launch and the
+// caller. `ids` is then unused. This saves route's own launch for callers that pass the router's logits.
+constexpr int ROUTED_MAX_N = 256;
+template <int KIND, int K, bool ROUTED>
+__global__ void __launch_bounds__(256) resident_gu_kernel(const uint16_t* x, const int64_t* ids,
+                                                          const uint16_t* logits, int n, int k, int64_t* ids_out,
+                                                          float* w_out, const uint8_t* bw, const void* bs,
+                                                          const float* bc, const float* codebook, float* gu, int N) {
   constexpr int RW = RPB / 4;  // rows per wave
   __shared__ float xs[K];
   __shared__ float lut[16];
+  __shared__ int routed_id;
   const int j = blockIdx.y, lane = threadIdx.x & 63, w = threadIdx.x >> 6, n0 = blockIdx.x * RPB;
-  const size_t e = (size_t)ids[j];
+  size_t e;
+  if constexpr (ROUTED) {
+    if (w == 0) {
+      constexpr int KPL = ROUTED_MAX_N / 64;
+      uint32_t lb[KPL];
+#pragma unroll
+      for (int q = 0; q < KPL; q++) lb[q] = logits[min(lane + 64 * q, n - 1)];  // lanes past n masked by top_keys
+      const uint32_t mine = top_keys<KPL>(lb, lane, n, k);
+      if (lane == j) routed_id = route_key_index(mine);
+      if (blockIdx.x == 0 && j == 0) {  // uniform over the wave: route_weight reads lanes 0 .. k-1
+        const float wt = route_weight(mine, lane, k);
+        if (lane < k) {
+          ids_out[lane] = route_key_index(mine);
+          w_out[lane] = wt;
+        }
+      }
+    }
+    __syncthreads();
+    e = (size_t)routed_id;
+  } else {
+    e = (size_t)ids[j];
+  }
   RowBytes<KIND, K> rb[RW];
   float sc[RW];
 #pragma unroll
@@ -797,32 +826,44 @@ int d3_grouped(int32_t kind, const float* x, const int32_t* groups, int32_t n_gr
   return done("d3_grouped");
 }
 
-int d3_resident_decode(int32_t kind, const void* x, const int64_t* ids, const float* weights, int32_t k,
-                       const void* gu_w, const void* gu_s, const float* gu_c, const void* dn_w, const void* dn_s,
-                       const float* dn_c, const float* gu_codebook, const float* dn_codebook, float* gu, void* out,
-                       int32_t H, int32_t I, void* stream) {
-  if (!x || !ids || !weights || !gu_w || !gu_s || !dn_w || !dn_s || !gu || !out)
-    return fail("d3_resident_decode: null pointer");
-  if ((kind == 4 || kind == 6) && (!gu_c || !dn_c)) return fail("d3_resident_decode: codes need channel scales");
-  if (kind == 4 && (!gu_codebook || !dn_codebook)) return fail("d3_resident_decode: 4 bits need codebooks");
-  if (k < 1 || k > MAX_K_RES) return fail("d3_resident_decode: 1 <= k <= 8");
+}  // extern "C"
+
+// Both resident entries: gate_up (routed in its prologue when `logits` is given, else on `ids`), then down on the
+// ids and weights (for the routed entry, the ones gate_up wrote).
+static int resident_launch(const char* name, int32_t kind, const void* x, const int64_t* ids, const float* weights,
+                           const void* logits, int32_t n, int32_t k, const void* gu_w, const void* gu_s,
+                           const float* gu_c, const void* dn_w, const void* dn_s, const float* dn_c,
+                           const float* gu_codebook, const float* dn_codebook, float* gu, void* out, int32_t H,
+                           int32_t I, void* stream) {
+  if (!x || !ids || !weights || !gu_w || !gu_s || !dn_w || !dn_s || !gu || !out) return fail(std::string(name) + ": null pointer");
+  if ((kind == 4 || kind == 6) && (!gu_c || !dn_c)) return fail(std::string(name) + ": codes need channel scales");
+  if (kind == 4 && (!gu_codebook || !dn_codebook)) return fail(std::string(name) + ": 4 bits need codebooks");
+  if (k < 1 || k > MAX_K_RES) return fail(std::string(name) + ": 1 <= k <= 8");
+  if (logits && (n < k || n > ROUTED_MAX_N)) return fail(std::string(name) + ": k <= n <= 256 logits");
   if ((H != 2048 && H != 1024) || (I != 512 && I != 768 && I != 1024) || H % DN_ROWS)
-    return fail("d3_resident_decode: H 1024 or 2048, I 512, 768 or 1024");
+    return fail(std::string(name) + ": H 1024 or 2048, I 512, 768 or 1024");
   const hipStream_t s = (hipStream_t)stream;
   const dim3 ggrid(2 * I / RPB, k), dgrid(H / DN_ROWS);
-  const uint16_t* xb = (const uint16_t*)x;
+  const uint16_t *xb = (const uint16_t*)x, *lg = (const uint16_t*)logits;
   const uint8_t *gw = (const uint8_t*)gu_w, *dw = (const uint8_t*)dn_w;
+  int64_t* ids_out = const_cast<int64_t*>(ids);
+  float* w_out = const_cast<float*>(weights);
   uint16_t* o = (uint16_t*)out;
+#define D3_GU(KIND, K)                                                                                               \
+  do {                                                                                                               \
+    if (lg) hipLaunchKernelGGL((resident_gu_kernel<KIND, K, true>), ggrid, dim3(256), 0, s, xb, nullptr, lg, n, k,   \
+                               ids_out, w_out, gw, gu_s, gu_c, gu_codebook, gu, 2 * I);                              \
+    else hipLaunchKernelGGL((resident_gu_kernel<KIND, K, false>), ggrid, dim3(256), 0, s, xb, ids, nullptr, 0, k,    \
+                            nullptr, nullptr, gw, gu_s, gu_c, gu_codebook, gu, 2 * I);                               \
+  } while (0)
 #define D3_RES(KIND)                                                                                                 \
   do {                                                                                                               \
-    if (H == 2048) hipLaunchKernelGGL((resident_gu_kernel<KIND, 2048>), ggrid, dim3(256), 0, s, xb, ids, gw, gu_s,   \
-                                      gu_c, gu_codebook, gu, 2 * I);                                                 \
-    else hipLaunchKernelGGL((resident_gu_kernel<KIND, 1024>), ggrid, dim3(256), 0, s, xb, ids, gw, gu_s, gu_c,       \
-                            gu_codebook, gu, 2 * I);                                                                 \
+    if (H == 2048) D3_GU(KIND, 2048);                                                                                \
+    else D3_GU(KIND, 1024);                                                                                          \
     if (I == 768) hipLaunchKernelGGL((resident_dn_kernel<KIND, 768>), dgrid, dim3(256), 0, s, gu, ids, weights, k,  \
                                      dw, dn_s, dn_c, dn_codebook, o, H);                                             \
     else if (I == 512) hipLaunchKernelGGL((resident_dn_kernel<KIND, 512>), dgrid, dim3(256), 0, s, gu, ids, weights, \
-                                          k, dw, dn_s, dn_c, dn_codebook, o, H);                                     \
+                                          k, dw, dn_s, dn_c, dn_codebook, o, H);                                    \
     else hipLaunchKernelGGL((resident_dn_kernel<KIND, 1024>), dgrid, dim3(256), 0, s, gu, ids, weights, k, dw, dn_s, \
                             dn_c, dn_codebook, o, H);                                                                \
   } while (0)
@@ -831,10 +872,30 @@ int d3_resident_decode(int32_t kind, const void* x, const int64_t* ids, const fl
     case 1: D3_RES(1); break;
     case 4: D3_RES(4); break;
     case 6: D3_RES(6); break;
-    default: return fail("d3_resident_decode: kind 0, 1, 4 or 6");
+    default: return fail(std::string(name) + ": kind 0, 1, 4 or 6");
   }
 #undef D3_RES
-  return done("d3_resident_decode");
+#undef D3_GU
+  return done(name);
+}
+
+extern "C" {
+
+int d3_resident_decode(int32_t kind, const void* x, const int64_t* ids, const float* weights, int32_t k,
+                       const void* gu_w, const void* gu_s, const float* gu_c, const void* dn_w, const void* dn_s,
+                       const float* dn_c, const float* gu_codebook, const float* dn_codebook, float* gu, void* out,
+                       int32_t H, int32_t I, void* stream) {
+  return resident_launch("d3_resident_decode", kind, x, ids, weights, nullptr, 0, k, gu_w, gu_s, gu_c, dn_w, dn_s,
+                         dn_c, gu_codebook, dn_codebook, gu, out, H, I, stream);
+}
+
+int d3_resident_decode_routed(int32_t kind, const void* x, const void* logits, int32_t n, int32_t k, int64_t* ids,
+                              float* weights, const void* gu_w, const void* gu_s, const float* gu_c, const void* dn_w,
+                              const void* dn_s, const float* dn_c, const float* gu_codebook, const float* dn_codebook,
+                              float* gu, void* out, int32_t H, int32_t I, void* stream) {
+  if (!logits) return fail("d3_resident_decode_routed: null pointer");
+  return resident_launch("d3_resident_decode_routed", kind, x, ids, weights, logits, n, k, gu_w, gu_s, gu_c, dn_w,
+                         dn_s, dn_c, gu_codebook, dn_codebook, gu, out, H, I, stream);
 }
 
 int d3_decode_codes(int32_t bits, const void* rows, const void* scales, const float* codebook, int32_t R, int32_t K,

@@ -70,6 +70,9 @@ SIGNATURES = {
     "d3_resident_decode": (c_int32, [c_int32, c_void_p, c_void_p, c_void_p, c_int32, c_void_p, c_void_p, c_void_p,
                                      c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int32,
                                      c_int32, c_void_p]),
+    "d3_resident_decode_routed": (c_int32, [c_int32, c_void_p, c_void_p, c_int32, c_int32, c_void_p, c_void_p,
+                                            c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+                                            c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_void_p]),
     "d3_resolve": (c_int32, [c_void_p, c_int32, c_int32, c_int32, c_int32, c_void_p, c_void_p, c_void_p, c_void_p,
                              c_void_p, c_int32, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                              ctypes.c_double, c_int32, ctypes.c_double, c_void_p]),

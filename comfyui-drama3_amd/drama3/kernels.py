@@ -182,6 +182,23 @@ def resident_decode(x, ids, weights, banks, kind, codebooks, H, I):
     return out
 
 
+
+def resident_decode_routed(x, logits, k, banks, kind, codebooks, H, I):
+    """(out [1, H] bfloat16, ids [1, k] int64, weights [1, k] float32): route(logits, k) and resident_decode in two
+    launches, the routing in the gate_up launch's prologue (logits [n] or [1, n] bfloat16, k <= n <= 256). ids and
+    weights equal route's for the same logits."""
+    code, wkey = _RESIDENT_KINDS[kind]
+    gate_up, down = banks
+    lg = logits.reshape(-1).contiguous()
+    gu = torch.empty((k, 2 * I), dtype=torch.float32, device=x.device)
+    out = torch.empty((1, H), dtype=torch.bfloat16, device=x.device)
+    ids = torch.empty((1, k), dtype=torch.int64, device=x.device)
+    weights = torch.empty((1, k), dtype=torch.float32, device=x.device)
+    _call("d3_resident_decode_routed", code, _p(x.contiguous()), _p(lg), lg.shape[0], k, _p(ids), _p(weights),
+          _p(gate_up[wkey]), _p(gate_up["scale"]), _p(gate_up.get("s_channel")), _p(down[wkey]), _p(down["scale"]),
+          _p(down.get("s_channel")), _p(codebooks[0]), _p(codebooks[1]), _p(gu), _p(out), H, I, _stream(x))
+    return out, ids, weights
+
 def decode_codes(qdata, scale, codebook, bits):
     """int8 [R, K]: W4A8 / W6A8 rows decoded to the int8 grid exactly as gemv_codes / grouped_codes decode them
     (a check of kernels.py:466-483's decode_codes; no counterpart in the reference's call surface)."""

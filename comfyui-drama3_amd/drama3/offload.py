@@ -133,6 +133,19 @@ def resident_decode(x, ids, weights, banks, rows, kind, codebooks):
     return resident_decode_unfused(x, ids, weights, banks, rows, kind, codebooks)
 
 
+
+def routed_decode(x, logits, k, banks, rows, kind, codebooks):
+    """kernels.route(logits, k) then resident_decode (model.py:116-118 then offload.py:108-123) for one row:
+    (out [1, H] bf16, ids [1, k], weights [1, k]). Two launches where the shapes allow (the routing inside the
+    gate_up launch), else route's own launch and resident_decode."""
+    (gate_up, down), (gate_up_rows, down_rows) = banks, rows
+    H, I = down_rows, gate_up_rows // 2
+    if (H in (1024, 2048) and I in (512, 768, 1024) and k <= 8 and k <= logits.numel() <= 256
+            and x.dtype == torch.bfloat16 and logits.dtype == torch.bfloat16):
+        return kernels.resident_decode_routed(x, logits, k, banks, kind, codebooks, H, I)
+    ids, weights = kernels.route(logits.reshape(1, -1), k)
+    return resident_decode(x, ids[0], weights[0], banks, rows, kind, codebooks), ids, weights
+
 def resident_decode_unfused(x, ids, weights, banks, rows, kind, codebooks):
     """resident_decode as the reference launches it: rotate, gemv, rotate(SwiGLU), gemv, weighted_sum."""
     (gate_up, down), (gate_up_rows, down_rows) = banks, rows

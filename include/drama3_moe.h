@@ -201,6 +201,16 @@ int d3_resident_decode(int32_t kind, const void* x, const int64_t* ids, const fl
                        const float* dn_c, const float* gu_codebook, const float* dn_codebook, float* gu, void* out,
                        int32_t H, int32_t I, void* stream);
 
+/* kernels.route + resident_decode in two launches (kernels.py:39-67,647-653 route_experts / route, then
+ * offload.py:108-123 as d3_resident_decode): the row's routing runs in the gate_up launch's prologue, from the router's
+ * logits [n] bf16 (k <= n <= 256), with route's key order and bf16-rounded softmax weights. ids [k] int64 and
+ * weights [k] float32 are outputs (equal to d3_route's for the same logits); the other arguments as for
+ * d3_resident_decode. */
+int d3_resident_decode_routed(int32_t kind, const void* x, const void* logits, int32_t n, int32_t k, int64_t* ids,
+                              float* weights, const void* gu_w, const void* gu_s, const float* gu_c, const void* dn_w,
+                              const void* dn_s, const float* dn_c, const float* gu_codebook, const float* dn_codebook,
+                              float* gu, void* out, int32_t H, int32_t I, void* stream);
+
 /* Check of the W4A8 / W6A8 decode on its own (kernels.py:466-483 decode_codes; no entry point of its own there):
  * codes [R, K] int8 of rows [R, K * bits / 8] with scales [R, K / 16]; K % 32 == 0. */
 int d3_decode_codes(int32_t bits, const void* rows, const void* scales, const float* codebook, int32_t R, int32_t K,

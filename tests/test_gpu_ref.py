@@ -345,6 +345,32 @@ def test_resident_decode(layer):
     assert_bf16_close(bits_of(got), ref.resident_decode_ref(x, ids, w, banks, (2 * I, H), kind, cbs))
 
 
+
+@pytest.mark.parametrize("n,k,ties", [(E, 4, False), (E, 1, False), (E, 8, False), (E, 4, True), (256, 6, False),
+                                      (200, 8, True)])
+def test_resident_decode_routed(layer, n, k, ties):
+    """Routing inside the gate_up launch: ids and weights equal kernels.route's and the oracle's route_ref, and the
+    output equals route + resident_decode bitwise. Logits past the first E experts sit far below the rest, so the
+    banks' E experts are the ones routed to, while the launch still ranks all n."""
+    kind, banks, cbs, dbanks, dcbs = layer
+    rng = np.random.default_rng(13 + n + k)
+    x = numerics.f32_to_bf16_bits(rng.standard_normal((1, H)).astype(np.float32))
+    lf = rng.integers(-2, 3, n).astype(np.float32) if ties else rng.standard_normal(n).astype(np.float32)
+    lf[E:] = -30.0
+    logits = numerics.f32_to_bf16_bits(lf)
+    xd, lg = dev(x).view(torch.bfloat16), dev(logits).view(torch.bfloat16)
+    out, ids, w = offload.routed_decode(xd, lg, k, dbanks, (2 * I, H), kind, dcbs)
+    rid, rw = kernels.route(lg.view(1, n), k)
+    assert torch.equal(ids, rid) and torch.equal(w, rw)
+    want_ids, want_w = ref.route_ref(logits, k)
+    assert ids.cpu().numpy()[0].tolist() == np.asarray(want_ids).reshape(-1).tolist()
+    # the device's expf against numpy's exp: within one bf16 step, as for route itself
+    np.testing.assert_allclose(w.cpu().numpy()[0], np.asarray(want_w, np.float32).reshape(-1), rtol=2.0**-7, atol=0)
+    want = offload.resident_decode(xd, rid[0], rw[0], dbanks, (2 * I, H), kind, dcbs)
+    assert torch.equal(out.view(torch.int16), want.view(torch.int16))
+    assert_bf16_close(bits_of(out), ref.resident_decode_ref(x, ids.cpu().numpy()[0], w.cpu().numpy()[0], banks,
+                                                            (2 * I, H), kind, cbs))
+
 def test_resident_prefill(layer):
     kind, banks, cbs, dbanks, dcbs = layer
     rng = np.random.default_rng(6)
