@@ -13,6 +13,9 @@ Other workloads of the same layer shape:
                                                 MFMA path (d3_moe_a8_prefill), 16 layers chained
     --mode resident --format fp8                the reference's own layouts and float activations (kernels.route +
                                                 offload.resident_decode), the drop-in path for converted files
+    --mode gemv                                 one FP8 expert weight [1536, 2048] with a bf16 scale per output row
+                                                against one bf16 row, dequantize-then-matmul semantics
+                                                (kernels.fp8_linear): 128 distinct weights, one launch each
 
     --shape model                               the reference model's own layer: 256 experts of FFN 512
 
@@ -22,7 +25,8 @@ Other workloads of the same layer shape:
 
 Prints one JSON line: metric (expert-weight GB/s), tokens/s, the roofline of the layer (algorithmic bytes per launch
 / average launch time from HIP events on the replay stream, against 8 TB/s HBM) and the reference's CPU path timed on
-a bounded sample of the same workload on this host.
+a bounded sample of the same workload on this host. The default run (int8, one row) also times the other formats'
+one-row layers (W4A8 and FP8 with normal routing, W6A8 with Zipf routing) and reports them under config.other_formats.
 """
 import argparse
 import json
@@ -31,6 +35,8 @@ import os
 import pathlib
 import sys
 import time
+
+import numpy as np
 
 ROOT = pathlib.Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT / "comfyui-drama3_amd"))
@@ -42,7 +48,10 @@ from drama3 import formats, moe  # noqa: E402
 METRIC = "MoE-layer expert-weight HBM GB/s (% of peak) at M=1; decode tokens/s"
 # HBM bytes per launch of the fused kernel, from rocprofv3 FETCH_SIZE / WRITE_SIZE passes scaled by the same counters
 # on a plain copy kernel of known size (`--calibrate-copy`); keyed by (mode, format, rows)
-TRAFFIC_PROFILES = {("decode", "int8", 1): ROOT / "profiles" / "moe_a8_int8_m1.md"}
+TRAFFIC_PROFILES = {("decode", "int8", 1): ROOT / "profiles" / "moe_a8_int8_m1.md",
+                    ("decode", "w4a8", 1): ROOT / "profiles" / "moe_a8_w4a8_m1.md",
+                    ("decode", "fp8", 1): ROOT / "profiles" / "moe_a8_fp8_m1.md",
+                    ("decode", "w6a8", 1): ROOT / "profiles" / "moe_a8_w6a8_m1_zipf.md"}
 PEAK_GBS = 8000.0
 PEAK_FP8_TFLOPS = 5000.0
 FORMATS = {"int8": formats.FMT_I8, "w4a8": formats.FMT_W4, "w6a8": formats.FMT_W6, "fp8": formats.FMT_F8}
@@ -94,38 +103,61 @@ def expert_bytes(gate_up, down):
     return gate_up.expert_bytes() + down.expert_bytes()
 
 
-def cpu_baseline(banks, fmt, logits, x, grouped=False, budget_s=12.0):
+def cpu_threads():
+    """Threads for the CPU path: every core this process may run on, within the CPU share the job is given (the
+    OMP_NUM_THREADS the environment sets for it, when it sets one)."""
+    affinity = len(os.sched_getaffinity(0))
+    share = os.environ.get("OMP_NUM_THREADS")
+    return min(affinity, int(share)) if share and share.isdigit() and int(share) > 0 else affinity
+
+
+def cpu_baseline(banks, fmt, logits, x, grouped=False, budget_s=12.0, passes=None):
     """The reference's CPU path (oracle/cpu_path.py) on this host: bf16 matmuls from the quantized banks per routed
     expert, over a sample of the same layers and routing; GB/s over the same algorithmic bytes (each routed expert's
-    weights once per layer pass)."""
+    weights once per layer pass). The sample rotates over `passes` (token, layer) pairs of distinct layers, each with
+    its own routed experts copied to host memory, so that the working set (32 x 8 experts, 1.2 GB at int8) is far
+    larger than the host's last-level cache and every pass reads its experts from DRAM, as the reference's does."""
     from oracle import cpu_path
-    threads = min(16, len(os.sched_getaffinity(0)))
+    threads = cpu_threads()
     torch.set_num_threads(threads)
-    sample_layers = min(2, len(banks))
-    host = [tuple((b.weight.cpu(), b.scale.cpu()) for b in pair) for pair in banks[:sample_layers]]
+    passes = passes or (4 if grouped else 32)  # a prefill pass already reads ~126 experts (600 MB)
     per_expert = expert_bytes(*banks[0])
     lg = logits.cpu()
     xs = x.cpu()
-    done, moved, started = 0, 0, time.perf_counter()
-    tokens = lg.shape[0]
-    while time.perf_counter() - started < budget_s:
-        t, layer = done % tokens, done % sample_layers
+    tokens, layers = lg.shape[0], len(banks)
+    sample = []  # (token, layer, ids, weights, host banks of the routed experts only, ids renumbered)
+    for i in range(min(passes, tokens * layers)):
+        t, layer = i % tokens, (i * 7) % layers
         w, ids = torch.softmax(lg[t, layer].float(), -1).topk(TOPK, dim=-1)
         w = (w / w.sum(-1, keepdim=True)).to(torch.bfloat16)
+        used = torch.unique(ids)
+        local = torch.searchsorted(used, ids)
+        host = []
+        for b in banks[layer]:
+            rows = b.weight.view(b.experts, b.rows, -1)[used.to(b.weight.device)].reshape(-1, b.weight.shape[1])
+            scale = b.scale.view(b.experts, b.rows, *b.scale.shape[1:])[used.to(b.scale.device)]
+            host.append((rows.cpu(), scale.reshape(-1, *b.scale.shape[1:]).cpu()))
+        sample.append((t, local, w, host, len(used)))
+    done, moved, started = 0, 0, time.perf_counter()
+    while time.perf_counter() - started < budget_s:
+        t, ids, w, host, n_used = sample[done % len(sample)]
         if grouped:
-            cpu_path.grouped_layer(xs[t], ids, w, host[layer][0], host[layer][1], fmt, H, I)
-            moved += len(torch.unique(ids)) * per_expert + xs[t].shape[0] * (2 * H * 2 + E * 2)
+            cpu_path.grouped_layer(xs[t], ids, w, host[0], host[1], fmt, H, I)
+            moved += n_used * per_expert + xs[t].shape[0] * (2 * H * 2 + E * 2)
         else:
-            cpu_path.layer(xs[t, :1], ids[0], w[0], host[layer][0], host[layer][1], fmt, H, I)
+            cpu_path.layer(xs[t, :1], ids[0], w[0], host[0], host[1], fmt, H, I)
             moved += TOPK * per_expert + 2 * H * 2 + E * 2
         done += 1
     elapsed = time.perf_counter() - started
     rows = xs.shape[1] if grouped else 1
     what = "cpu_path.grouped_layer" if grouped else "cpu_path.layer"
     return {"value": round(moved / elapsed / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-            "tokens_per_s": round(done * rows / elapsed / len(banks), 3),
-            "sample": f"{done} layer passes ({rows} rows, top-8) over {sample_layers} of the layers, {elapsed:.1f} s, "
-                      f"torch {threads} threads, {what}: _weight_int8pack_mm / dequantize-then-linear per expert"}
+            "tokens_per_s": round(done * rows / elapsed / layers, 3),
+            "sample": f"{done} layer passes ({rows} rows, top-8) rotating over {len(sample)} (token, layer) pairs of "
+                      f"{len({(i * 7) % layers for i in range(len(sample))})} layers ({len(sample)} x their routed "
+                      f"experts in host memory), {elapsed:.1f} s, torch {threads} threads of "
+                      f"{len(os.sched_getaffinity(0))} in the affinity mask, {what}: _weight_int8pack_mm / "
+                      f"dequantize-then-linear per expert"}
 
 
 def measured_traffic(mode, fmt_name, rows):
@@ -201,7 +233,7 @@ def run_decode(args, fmt, device):
         ms = timed_replays(graphs, stream, args.steps, args.warmup)
     torch.cuda.synchronize()
     status = moe.status(device, H, I, stream)
-    if status:
+    if status & moe.STATUS_INVALID:
         raise RuntimeError(f"fused layer reported status {status}")
     total_bytes = sum(bytes_per_token[i % GRAPH_TOKENS] for i in range(args.steps))
     launches = args.steps * L
@@ -211,7 +243,8 @@ def run_decode(args, fmt, device):
         cpu = cpu_baseline(banks, fmt, logits[:, :, :1], x0[:, :1])
     config = {"workload": f"routed-expert MoE layer, {args.format} experts, decode M={M}, hidden {H}, FFN {I}, "
                           f"{E} experts top-{TOPK} ({args.routing} routing), {L} layers chained per token",
-              "rows": M, "layers": L, "unique_experts_per_launch": round(sum(unique) / len(unique), 2)}
+              "rows": M, "layers": L, "unique_experts_per_launch": round(sum(unique) / len(unique), 2),
+              "waits_recomputed": bool(status & moe.STATUS_RECOMPUTED)}
     kernel = "d3::moe_a8_one_row_kernel" if M == 1 else "d3::moe_a8_kernel" if M < moe.GROUPED_FROM_ROWS else \
         "d3_moe_a8_prefill (7 launches)"
     return ms, total_bytes, launches, args.steps * M, config, kernel, cpu
@@ -257,7 +290,7 @@ def run_block(args, fmt, device):
         ms = timed_replays(graphs, stream, args.steps, args.warmup)
     torch.cuda.synchronize()
     status = moe.status(device, H, I, stream)
-    if status:
+    if status & moe.STATUS_INVALID:
         raise RuntimeError(f"fused layer reported status {status}")
     total_bytes = sum(bytes_per_token[i % GRAPH_TOKENS] for i in range(args.steps))
     config = {"workload": f"MoE block (router {E}x{H} bf16, routed {args.format} experts top-{TOPK}, shared expert "
@@ -305,6 +338,85 @@ def run_prefill(args, fmt, device):
               "mfma_tflops": round(flops * L * args.steps / (ms * 1e-3) / 1e12, 2),
               "mfma_frac_fp8_peak": round(flops * L * args.steps / (ms * 1e-3) / 1e12 / PEAK_FP8_TFLOPS, 5)}
     return ms, step_bytes * args.steps, args.steps * L, args.steps * T, config, "d3_moe_a8_prefill (7 launches)", cpu
+
+
+def run_gemv(args, fmt, device):
+    """One FP8 expert weight [1536, 2048] with a bf16 scale per output row (absmax / 448) against one bf16 row,
+    dequantize-then-matmul semantics (kernels.fp8_linear, d3_gemv_fp8_rows): x ~ N(0, 1), weights ~ N(0, 0.02), seed
+    0. `layers` distinct weights (128: 400 MB, beyond the Infinity Cache), one launch each, in one graph; also the same
+    weights as one stacked matrix in one launch (how experts_decode's gate_up multiplies k experts at once). The CPU
+    leg times the reference's path, dequantize to bf16 then torch's bf16 linear, on the host."""
+    from drama3 import kernels
+    N, K, count = 2 * I, H, args.layers
+    gen = torch.Generator(device=device).manual_seed(0)
+    x = torch.randn((1, K), generator=gen, device=device).to(torch.bfloat16)
+    weights = torch.empty((count * N, K), dtype=torch.uint8, device=device)
+    scales = torch.empty((count * N,), dtype=torch.bfloat16, device=device)
+    for m in range(count):
+        bank = formats.quantize(torch.randn((1, N, K), generator=gen, device=device) * 0.02, formats.FMT_F8)
+        weights[m * N:(m + 1) * N] = bank.weight
+        scales[m * N:(m + 1) * N] = bank.scale
+    mats = [(weights[m * N:(m + 1) * N], scales[m * N:(m + 1) * N]) for m in range(count)]
+    bytes_per_call = N * K + N * 2 + K * 2 + N * 2  # weight bytes, row scales, x in, y out
+    stream = torch.cuda.Stream(device)
+    stream.wait_stream(torch.cuda.current_stream(device))
+    with torch.cuda.stream(stream):
+        outs = [kernels.fp8_linear(x, w, sc) for w, sc in mats]
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream):
+            outs = [kernels.fp8_linear(x, w, sc) for w, sc in mats]
+        ms = timed_replays([g], stream, args.steps, args.warmup)
+        kernels.fp8_linear(x, weights, scales)
+        gs = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gs, stream=stream):
+            stacked = kernels.fp8_linear(x, weights, scales)
+        ms_stacked = timed_replays([gs], stream, args.steps, args.warmup)
+    torch.cuda.synchronize()
+    if not torch.equal(stacked[0, :N], outs[0][0]):
+        raise RuntimeError("stacked and single launches differ")
+    launches = args.steps * count
+    stacked_gbs = (bytes_per_call - K * 2) * count * args.steps / (ms_stacked * 1e-3) / 1e9
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("timing the reference's CPU path")
+        from oracle import cpu_path
+        threads = cpu_threads()
+        torch.set_num_threads(threads)
+        host = [(w.cpu().view(torch.float8_e4m3fn), sc.cpu()) for w, sc in mats[:32]]  # 100 MB, beyond the LLC
+        xc = x.cpu()
+        done, started = 0, time.perf_counter()
+        while time.perf_counter() - started < 10.0:
+            w, sc = host[done % len(host)]
+            cpu_path.fp8_rows_linear(xc, w, sc)
+            done += 1
+        elapsed = time.perf_counter() - started
+        cpu = {"value": round(done * bytes_per_call / elapsed / 1e9, 3), "unit": "GB/s", "cores": threads,
+               "kind": "port", "us_per_call": round(elapsed / done * 1e6, 2),
+               "sample": f"{done} calls rotating over {len(host)} distinct weights in host memory, {elapsed:.1f} s, "
+                         f"torch {threads} threads of {len(os.sched_getaffinity(0))} in the affinity mask, "
+                         f"cpu_path.fp8_rows_linear: dequantize to bf16, then torch's bf16 linear"}
+    config = {"workload": f"FP8 expert weight [{N}, {K}] with a bf16 scale per output row, one bf16 row, dequantize "
+                          f"then matmul (fp8_linear), {count} distinct weights, one launch each",
+              "rows": 1, "weights": count, "us_per_call": round(ms * 1e3 / launches, 3),
+              "stacked_one_launch_gbs": round(stacked_gbs, 1),
+              "stacked_one_launch_us": round(ms_stacked * 1e3 / args.steps, 2)}
+    return ms, bytes_per_call * launches, launches, launches, config, "d3::gemv_fp8_rows_kernel", cpu
+
+
+def decode_summary(args, fmt_name, routing, device):
+    """One-row decode of another format (same shape, 48 layers), as run_decode measures it: a dict for
+    config.other_formats."""
+    sub = argparse.Namespace(**vars(args))
+    sub.format, sub.routing, sub.rows, sub.no_cpu_baseline = fmt_name, routing, 1, True
+    ms, total_bytes, launches, tokens, config, kernel, _ = run_decode(sub, FORMATS[fmt_name], device)
+    torch.cuda.empty_cache()
+    launch_us = ms * 1e3 / launches
+    gbs = total_bytes / launches / (launch_us * 1e-6) / 1e9
+    return {"format": fmt_name, "routing": routing, "us_per_layer": round(launch_us, 3), "gbs": round(gbs, 1),
+            "frac_of_peak": round(gbs / PEAK_GBS, 4), "tokens_per_s": round(tokens / (ms * 1e-3), 2),
+            "bytes_per_launch": int(total_bytes / launches),
+            "unique_experts_per_launch": config["unique_experts_per_launch"],
+            "traffic": measured_traffic("decode", fmt_name, 1)}
 
 
 def make_reference_banks(fmt_name, layers, device, seed=3):
@@ -379,11 +491,12 @@ def run_resident(args, fmt, device):
             graphs.append(g)
         ms = timed_replays(graphs, stream, args.steps, args.warmup)
     torch.cuda.synchronize()
-    config = {"workload": f"routed-expert MoE layer in the reference's {args.format} layout (float activations, "
-                          f"route + resident_decode), decode M=1, hidden {H}, FFN {I}, {E} experts top-{TOPK}, "
-                          f"{L} layers chained per token", "rows": 1, "layers": L, "unique_experts_per_launch": TOPK}
     what = ("routed_decode (2 launches: gate_up with the routing, down)" if args.routed else
             "route + resident_decode (3 launches: route, gate_up, down)")
+    config = {"workload": f"routed-expert MoE layer in the reference's {args.format} layout (float activations, "
+                          f"{'routed_decode' if args.routed else 'route + resident_decode'}), decode M=1, hidden {H}, "
+                          f"FFN {I}, {E} experts top-{TOPK}, {L} layers chained per token", "rows": 1, "layers": L,
+              "unique_experts_per_launch": TOPK}
     return ms, layer_bytes * L * args.steps, args.steps * L, args.steps, config, what, None
 
 
@@ -392,7 +505,7 @@ def main():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=None)
     p.add_argument("--warmup", type=int, default=None)
-    p.add_argument("--mode", default="decode", choices=["decode", "prefill", "resident", "block"])
+    p.add_argument("--mode", default="decode", choices=["decode", "prefill", "resident", "block", "gemv"])
     p.add_argument("--routed", action="store_true", help="--mode resident: route inside the gate_up launch")
     p.add_argument("--format", default=None, choices=sorted(FORMATS))
     p.add_argument("--rows", type=int, default=None)
@@ -403,6 +516,7 @@ def main():
                         "reference model's own layer (drama3/fish/config.json)")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--calibrate-copy", action="store_true", help="only run the copy kernel that scales PMC counters")
+    p.add_argument("--headline-only", action="store_true", help="the default run without the other formats' lines")
     args = p.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: the routed-expert path runs on one MI355X, each GPU holding every expert "
@@ -410,9 +524,10 @@ def main():
               file=sys.stderr)
         sys.exit(2)
     prefill = args.mode == "prefill"
-    args.format = args.format or ("fp8" if prefill else "int8")
+    default_run = args.mode == "decode" and args.format is None and args.rows is None and args.routing is None
+    args.format = args.format or ("fp8" if prefill or args.mode == "gemv" else "int8")
     args.rows = args.rows or (256 if prefill else 1)
-    args.layers = args.layers or (16 if prefill else 48)
+    args.layers = args.layers or (16 if prefill else 128 if args.mode == "gemv" else 48)
     args.routing = args.routing or ("zipf" if prefill else "normal")
     args.steps = args.steps or (20 if prefill else 100)
     args.warmup = args.warmup if args.warmup is not None else (3 if prefill else 8)
@@ -426,8 +541,15 @@ def main():
         calibrate_copy(device)
         return
 
-    run = {"prefill": run_prefill, "resident": run_resident, "block": run_block}.get(args.mode, run_decode)
+    run = {"prefill": run_prefill, "resident": run_resident, "block": run_block, "gemv": run_gemv}.get(args.mode,
+                                                                                                     run_decode)
     ms, total_bytes, launches, tokens, config, kernel, cpu = run(args, fmt, device)
+    if default_run and args.shape == "config" and not args.headline_only:
+        # the north star's target formats at one row, and the 48-layer Zipf sweep of W6A8
+        config["other_formats"] = []
+        for fmt_name, routing in (("w4a8", "normal"), ("fp8", "normal"), ("w6a8", "zipf")):
+            log(f"timing {fmt_name} one-row decode ({routing} routing)")
+            config["other_formats"].append(decode_summary(args, fmt_name, routing, device))
     gbs = total_bytes / (ms * 1e-3) / 1e9
     launch_us = ms * 1e3 / launches
     bytes_per_launch = total_bytes / launches

@@ -136,8 +136,8 @@ D3_INLINE int wave_sum_i32(int v) {
 // device-scope atomics. The compiler issues those as device-coherent (sc1) accesses, which go past the per-XCD L2s, so
 // no L2-wide writeback or invalidate (what an agent-scope release / acquire fence costs) is needed, and a word carries
 // its own validity: a consumer polls the words it needs until all show the current epoch, with no flag or counter in
-// between. Polls are bounded: past `limit` the consumer records an error in `status` and goes on, so a broken hand-off
-// can never hang the device.
+// between. Polls are bounded (keep_polling): past the bound the consumer computes what it waited for itself, so a
+// hand-off that never comes (a producer that is not resident) can never hang the device.
 D3_INLINE void put_tagged(uint64_t* p, float v, uint32_t epoch) {
   __hip_atomic_store(p, (uint64_t)__float_as_uint(v) | ((uint64_t)epoch << 32), __ATOMIC_RELAXED,
                      __HIP_MEMORY_SCOPE_AGENT);
@@ -153,44 +153,17 @@ D3_INLINE bool tag_is(uint64_t word, uint32_t epoch) { return (uint32_t)(word >>
 D3_INLINE uint32_t tag_diff(uint64_t word, uint32_t epoch) { return (uint32_t)(word >> 32) ^ epoch; }
 D3_INLINE float tagged_value(uint64_t word) { return __uint_as_float((uint32_t)word); }
 
-// N tagged words at p[0..N) (stride `stride`): all loads issued at once, then the stale ones (not yet landed) read
-// again until they carry `epoch` (bounded by keep_polling). Values go to v.
-template <int N>
-D3_INLINE void gather_tagged(const uint64_t* p, int stride, uint32_t epoch, float* v, uint32_t* status, uint32_t limit) {
-  uint64_t w[N];
-#pragma unroll
-  for (int i = 0; i < N; i++) w[i] = get_tagged_cached(p + i * stride);
-  bool fresh = true;
-#pragma unroll
-  for (int i = 0; i < N; i++) fresh = fresh && tag_is(w[i], epoch);
-  if (!fresh) {
-    uint32_t polls = 0;
-    while (true) {
-      bool all = true;
-#pragma unroll
-      for (int i = 0; i < N; i++) {
-        if (!tag_is(w[i], epoch)) w[i] = get_tagged(p + i * stride);
-        all = all && tag_is(w[i], epoch);
-      }
-      if (all) break;
-      // keep_polling's limit counts rounds; it also records the timeout
-      uint32_t st = __hip_atomic_load(status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (st != 0u || ++polls > limit) {
-        if (st == 0u) __hip_atomic_fetch_or(status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        break;
-      }
-      __builtin_amdgcn_s_sleep(1);
-    }
-  }
-#pragma unroll
-  for (int i = 0; i < N; i++) v[i] = tagged_value(w[i]);
-}
-
-// The dispatch's ID: the HSA queue's packet index of this launch, the same for every workgroup, larger for every later
-// dispatch on the queue (graph replays included). LLVM's intrinsic, which clang does not expose as a builtin.
+// The launch's epoch, the tag of every word it publishes: the dispatch's ID (the HSA queue's packet index of this
+// launch, the same for every workgroup and larger for every later dispatch on the queue, graph replays included; LLVM's
+// intrinsic, which clang does not expose as a builtin) plus a salt from the queue's address (a kernel argument the
+// hardware preloads). Two queues count their dispatches independently; with the salt, a launch on one queue does not
+// take the words another queue's launch left behind for its own, so a workspace may move between streams (a graph
+// replayed on a stream other than the one it was captured on included). Never 0, the tag of a zeroed workspace.
 extern "C" __device__ uint64_t d3_dispatch_id() __asm("llvm.amdgcn.dispatch.id");
 D3_INLINE uint32_t launch_epoch() {
-  const uint32_t e = (uint32_t)d3_dispatch_id() + 1u;
+  const uint64_t q = (uint64_t)__builtin_amdgcn_queue_ptr();
+  const uint32_t salt = (uint32_t)((q >> 6) ^ (q >> 32)) * 0x9E3779B1u;
+  const uint32_t e = (uint32_t)d3_dispatch_id() + 1u + salt;
   return e == 0u ? 1u : e;
 }
 D3_INLINE uint64_t signal_load64(const uint64_t* p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
@@ -210,12 +183,22 @@ D3_INLINE uint32_t signal_load(const uint32_t* counter) {
 D3_INLINE void signal_store(uint32_t* counter, uint32_t v) {
   __hip_atomic_store(counter, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-// one more poll allowed? Records a timeout in `status`; every 32 polls it also checks `status`, so after one timeout
-// the launch's other waits stop soon.
-D3_INLINE bool keep_polling(uint32_t& polls, uint32_t* status, uint32_t limit) {
-  if ((polls & 31u) == 31u && signal_load(status) != 0u) return false;
+// A launch's give-up word: (epoch << 32) | reason, stored by the first wait of that launch that stops waiting. Every
+// other wait of the same launch then stops soon too (the waiting workgroups compute what they waited for themselves);
+// the word of an earlier launch carries another epoch and stops nothing.
+D3_INLINE bool launch_gave_up(const uint64_t* status, uint32_t epoch) {
+  return (uint32_t)(signal_load64(status) >> 32) == epoch;
+}
+D3_INLINE void give_up(uint64_t* status, uint32_t epoch) {
+  __hip_atomic_store(status, ((uint64_t)epoch << 32) | 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// one more poll allowed? Past `limit` polls it records the launch's give-up; every 32 polls it also checks whether
+// another wait of the launch gave up (unless `alone`: a recovery's read-back of its own words, which must not stop
+// for that).
+D3_INLINE bool keep_polling(uint32_t& polls, uint64_t* status, uint32_t limit, uint32_t epoch, bool alone = false) {
+  if (!alone && (polls & 31u) == 31u && launch_gave_up(status, epoch)) return false;
   if (++polls > limit) {
-    __hip_atomic_fetch_or(status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    give_up(status, epoch);
     return false;
   }
   __builtin_amdgcn_s_sleep(1);

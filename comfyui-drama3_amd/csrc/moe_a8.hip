@@ -20,15 +20,18 @@
 //     publishes its partial outputs and the last chunk's item for block b sums them.
 // Items are ordered gate_up(chunk 0), gate_up(chunk 1), down(chunk 0), gate_up(chunk 2), down(chunk 1), ...: every
 // wait is on items of lower index. The grid is at most what the device holds at once, so every workgroup is resident
-// and the lowest unfinished item can always run: no wait can block forever. Waits are bounded anyway (spin_limit),
-// and a timeout sets sync[SYNC_STATUS].
+// and the lowest unfinished item can always run: no wait can block forever. Waits are bounded anyway (spin_limit).
+// A wait that gives up (a producer that is not resident, because another kernel holds part of the device, or a
+// spin_limit hit) does not leave the output wrong: its workgroup computes what it waited for itself, with the same
+// code on the same inputs, so the words it uses are the ones the producers would have published, bit for bit. The
+// launch's give-up word makes the launch's other waits stop soon and do the same; a sticky bit records that it
+// happened (d3_moe_a8_status).
 //
 // Hand-off: hidden units, each gate_up item's absmax and partial outputs are 64-bit words (value, epoch) written and
-// read with device-coherent accesses (common.hpp); a gate_up item also counts itself done in its expert's counter (no
-// wait for its stores: a word that has not landed yet is told apart by its epoch and read again). Down items poll only
-// those counters. The epoch is the dispatch ID + 1, which grows with every dispatch on a queue, so a workspace carries
-// over from launch to launch (and graph replay to replay) with nothing to clear; it must stay on one stream (queue),
-// and launches that overlap on one workspace race.
+// read with device-coherent accesses (common.hpp), with no counter or flag in between: a word that has not landed yet
+// is told apart by its epoch and read again. The epoch is the dispatch ID plus a salt from the queue's address
+// (launch_epoch), new for every dispatch, so a workspace carries over from launch to launch (and graph replay to
+// replay, on any stream) with nothing to clear. Launches that overlap on one workspace race.
 #include "formats.hpp"
 #include "../../include/drama3_moe.h"
 
@@ -40,8 +43,11 @@
 
 namespace d3 {
 
-// sync words (32-bit), 256 bytes apart: status, then per expert slot a 64-bit (epoch, gate_up items done) counter
-enum : int { SYNC_STATUS = 0, SYNC_DONE = 64, SYNC_WORDS = 64 + 64 * 128 };
+// workspace header (32-bit words, 256 bytes apart): the launch give-up word (64-bit: the epoch of the last launch in
+// which a wait gave up, and a reason), then the sticky bits d3_moe_a8_status reads (bit 0: a wait gave up and its
+// workgroup computed the missing values itself; bit 1: a wait still failed after that, the launch's output is not
+// valid)
+enum : int { SYNC_STATUS = 0, SYNC_STICKY = 64, SYNC_WORDS = 128 };
 constexpr int MAX_M = 16, MAX_K = 8, MAX_E = 256, MAX_PAIRS = MAX_M * MAX_K;
 constexpr int CHUNK_EXPERTS = 8, CHUNK_PAIRS = 32;
 
@@ -58,9 +64,10 @@ struct MoeA8Args {
   uint64_t* hidden;  // [M * topk, I] tagged
   uint64_t* tmax;    // [M * topk + 1, I / UT] tagged: absmax of each gate_up item's UT (8 or 16) hidden units
   uint64_t* parts;   // [M * topk, H] tagged
-  uint32_t* sync;
+  uint64_t* status;  // the launch give-up word
+  uint32_t* sticky;  // sticky status bits
   int M, E, topk;
-  uint32_t spin_limit;
+  uint32_t spin_limit;  // 0: every wait gives up at once (the descriptor's recompute_all)
   // the block around the routed experts (one row): the router's weights [E, H] bf16 (logits computed in the launch
   // instead of read), its logits out [E] bf16; the shared expert (one A8 expert of the layer's format and shape) and
   // its gate [H] bf16
@@ -110,10 +117,12 @@ struct Lds {
   }
 };
 
-// Per-expert-slot counter of finished gate_up items: (epoch << 32) | count. An item raises it to (epoch, 0) when it
-// starts (atomic max: a stale count of an earlier launch is replaced, this launch's count is kept) and adds 1 when it
-// has published; the down items wait for (epoch, T). Nothing needs clearing between launches.
-D3_INLINE uint64_t* done_counter(uint32_t* sync, int u) { return (uint64_t*)(sync + SYNC_DONE + 64 * u); }
+// Workgroup flags in LDS (misc[2 ..]): a wave that gave up a wait sets one; the workgroup reads it after its next
+// barrier and then computes what was missing itself (see down_compute).
+enum : int { FLAG_HIDDEN = 0, FLAG_SHARED = 1, FLAG_PARTS = 2, FLAG_SH_HIDDEN = 3, N_FLAGS = 4 };
+// polls allowed when reading back words the workgroup has just published itself (current at the first read that goes
+// past the caches)
+constexpr uint32_t RECOVER_LIMIT = 1u << 16;
 
 // What a workgroup knows after its prologue.
 struct Ctx {
@@ -141,16 +150,81 @@ struct Ctx {
   // gfirst[u] .. gfirst[u + 1] - 1, slot s holds pair gpair[s] (and pair_slot maps back)
   int* gfirst;
   int* gpair;
+  int* flags;  // [N_FLAGS] see FLAG_*
   int U, nch, n_dn;
   uint32_t epoch;
 };
+
+D3_INLINE void note_recovery(const MoeA8Args& a, uint32_t bit) {
+  __hip_atomic_fetch_or(a.sticky, bit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// The recovery paths are calls, not inlined, taking plain values only: their registers then do not count against the
+// kernels' fast paths (inlined, the fused kernels lost a workgroup per CU or spilled on their fast paths), and the
+// kernel's context stays in registers (a reference to it would put it in scratch memory, read back on the fast path).
+#define RECOVERY_FN __device__ __noinline__
+
+// the launch's dynamic LDS (every kernel here has one array, carved up by Lds)
+extern __shared__ __attribute__((aligned(16))) uint8_t d3_lds[];
+
+// a workgroup's view of its LDS and the launch (the flags are cleared by make_ctx only)
+D3_INLINE Ctx view_ctx(const MoeA8Args& a, int H, int I, uint32_t epoch) {
+  uint8_t* lds = d3_lds;
+  const Lds L(a.M, a.topk, H, I);
+  Ctx cx;
+  cx.a = &a;
+  cx.xq = lds + L.xq;
+  cx.sx = (float*)(lds + L.sx);
+  cx.rt_id = (int*)(lds + L.rt_id);
+  cx.rt_w = (float*)(lds + L.rt_w);
+  cx.ulist = (int*)(lds + L.ulist);
+  cx.ucount = (int*)(lds + L.ucount);
+  cx.utok = lds + L.utok;
+  cx.upair = lds + L.upair;
+  cx.chunk_first = (int*)(lds + L.chunk_first);
+  cx.misc = (int*)(lds + L.misc);
+  cx.emask = (uint32_t*)(lds + L.emask);
+  cx.red = (float*)(lds + L.red);
+  cx.hq = lds + L.hq;
+  cx.hs = (float*)(lds + L.hs);
+  cx.lparts = (float*)(lds + L.lparts);
+  cx.slot_pair = (int*)(lds + L.slot_pair);
+  cx.pair_slot = (int*)(lds + L.pair_slot);
+  cx.slot_first = (int*)(lds + L.slot_first);
+  cx.gfirst = (int*)(lds + L.gfirst);
+  cx.gpair = (int*)(lds + L.gpair);
+  cx.fparts = (float*)(lds + L.fparts);
+  cx.flags = cx.misc + 2;
+  cx.epoch = epoch;
+  return cx;
+}
+
+D3_INLINE Ctx make_ctx(const MoeA8Args& a, int H, int I) {
+  Ctx cx = view_ctx(a, H, I, launch_epoch());
+  if (threadIdx.x < N_FLAGS) cx.flags[threadIdx.x] = 0;
+  return cx;
+}
+
+// The launch's arguments where the kernel received them (its kernarg segment: the one argument, at offset 0), for the
+// recovery calls, which take this pointer as a parameter: then nothing of the kernel's own context has to go through
+// memory to reach them. Only inside a kernel: a called function's ABI does not carry the kernarg segment pointer.
+D3_INLINE const MoeA8Args* kernel_args() { return (const MoeA8Args*)__builtin_amdgcn_kernarg_segment_ptr(); }
+
+// The context of a recovery call: as make_ctx, with the union's size and chunk count the workgroup left in LDS
+D3_INLINE Ctx recovery_ctx(const MoeA8Args* args, int H, int I, uint32_t epoch) {
+  Ctx cx = view_ctx(*args, H, I, epoch);
+  cx.U = cx.misc[0];
+  cx.nch = cx.misc[1];
+  cx.n_dn = cx.nch * (H / 8);
+  return cx;
+}
 
 // gate_up item: hidden units UT tile .. UT tile + UT - 1 (UT = 8 NSUB) of expert u, i.e. NSUB 16-row MFMA tiles
 // (sub-tile s: gate rows UT tile + 8 s .. + 7 as rows 0-7, the matching up rows as rows 8-15)
 // (`between` runs once the item's weight rows are on their way, before it reads the slot tables or x; `after` once its
 // products are done, before its reduction)
 template <int F, int H, int I, int NSUB = 2, typename Between, typename After>
-D3_INLINE uint64_t gate_up_item(const Ctx& cx, int u, int tile, int parity, int e, int nu, Between between,
+D3_INLINE void gate_up_item(const Ctx& cx, int u, int tile, int parity, int e, int nu, Between between,
                                 After after, const uint8_t* gu_w, const uint16_t* gu_s) {
   static_assert(NSUB == 1 || NSUB == 2, "8 or 16 hidden units per item");
   constexpr int UT = 8 * NSUB, T = I / UT;  // hidden units per item, items per expert
@@ -159,11 +233,6 @@ D3_INLINE uint64_t gate_up_item(const Ctx& cx, int u, int tile, int parity, int 
   constexpr int SHIFT = unpack_shift(F);
   const MoeA8Args& a = *cx.a;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, q = lane >> 4, col = lane & 15;
-  // raise the expert's counter to (epoch, 0) with an atomic that returns nothing: waiting for its value here would
-  // hold the weight rows back by its round trip (loads complete in order)
-  uint64_t before = 0;
-  if (tid == 0)
-    __hip_atomic_fetch_max(done_counter(a.sync, u), (uint64_t)cx.epoch << 32, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   const int ra = lane & 15;
   auto row_of = [&](int sub, int r) {
     return (size_t)e * (2 * I) + (r < 8 ? UT * tile + 8 * sub + r : I + UT * tile + 8 * sub + r - 8);
@@ -268,19 +337,24 @@ D3_INLINE uint64_t gate_up_item(const Ctx& cx, int u, int tile, int parity, int 
       m = fmaxf(m, __int_as_float(dpp_i32(__float_as_int(m), 0x140)));
       if (j == 0) put_tagged(a.tmax + (size_t)p * T + tile, m, cx.epoch);
     }
-    if (lane == 0) {
-      // the add follows the raise to the same word from the same lane, so it lands after it. The count before the add
-      // goes back to the caller, who checks it once the workgroup's work is done (flag_later_epoch): a later epoch
-      // means the workspace was used on another queue.
-      before = __hip_atomic_fetch_add(done_counter(a.sync, u), (uint64_t)1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
   }
-  return before;
 }
 
-// status bit 1 when a gate_up item found its expert's counter raised by a later launch (see gate_up_item)
-D3_INLINE void flag_later_epoch(const MoeA8Args& a, uint64_t before, uint32_t epoch) {
-  if ((uint32_t)(before >> 32) > epoch) __hip_atomic_fetch_or(a.sync + SYNC_STATUS, 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+// Every gate_up item of chunk c's experts, computed and published by this workgroup: the recovery of a down item whose
+// wait for them gave up.
+template <int F, int H, int I, int NSUB>
+D3_INLINE void recompute_gate_up(const Ctx& cx, int c) {
+  constexpr int T = I / (8 * NSUB);
+  const MoeA8Args& a = *cx.a;
+  int parity = 0;
+#pragma unroll 1
+  for (int u = cx.chunk_first[c]; u < cx.chunk_first[c + 1]; u++) {
+#pragma unroll 1
+    for (int tile = 0; tile < T; tile++) {
+      gate_up_item<F, H, I, NSUB>(cx, u, tile, parity, cx.ulist[u], cx.ucount[u], [] {}, [] {}, a.gu_w, a.gu_s);
+      parity ^= 1;
+    }
+  }
 }
 
 
@@ -342,59 +416,37 @@ D3_INLINE void down_load(const Ctx& cx, int c, int hb, DownRows<F, I>& d) {
   }
 }
 
-// the rest of down item (c, hb) once its loads are out: collect the chunk's hidden rows, quantize, multiply, and write
-// the weighted sum (one chunk) or the partial outputs. GLOBAL: the slots come from the launch-wide tables (general
-// schedule) and the gather goes out behind the weight rows at once; otherwise thread 0 numbers the chunk's slots
-// first and the gather waits for the weight rows (one row: see one_row_layer).
-template <int F, int H, int I, int NSUB = 2, bool GLOBAL = false, bool SPREAD = false>
-D3_INLINE void down_finish(const Ctx& cx, int c, int hb, const DownRows<F, I>& d) {
-  constexpr int STEPS = I / 128;
-  constexpr int SHIFT = unpack_shift(F);
+// The gather of down item (c, hb): the chunk's pairs' hidden rows, quantized into LDS slots (hq, hs). Returns whether
+// this wave gave up waiting for words not yet published (wave-uniform).
+// The pairs' hidden rows are gathered two at a time per wave (a pair per half-wave: the tiles' maxima and the values
+// in one round trip). Each wave gathers its own two experts' pairs, or with SPREAD the chunk's pairs go round the
+// workgroup's 8 half-waves (one round trip for up to 8 pairs, where a wave whose experts hold 3 or more needed two).
+// Without GLOBAL the gather is issued once the wave's weight rows have arrived (its loads complete in order, so
+// anything issued earlier would be read early and come back no sooner); with GLOBAL it goes out behind them at once.
+// The words carry their epoch, so a gather that finds every word current needs nothing else. Otherwise the stale words
+// are read again, coherently, until they are current. (Not a counter of finished items first: every waiting wave would
+// poll the same few words, and by the time a first gather is back the late items are mostly published.)
+template <int F, int H, int I, int NSUB, bool GLOBAL, bool SPREAD>
+D3_INLINE bool down_gather(const Ctx& cx, int c, uint32_t limit) {
   constexpr float QMAX = act_qmax<F>();
   const MoeA8Args& a = *cx.a;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, q = lane >> 4, col = lane & 15;
-  const int M = a.M, K8 = a.topk;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int u0 = cx.chunk_first[c], ne = cx.chunk_first[c + 1] - u0;
   const int* slot_first = GLOBAL ? cx.gfirst + u0 : cx.slot_first;
   const int gb = GLOBAL ? cx.gfirst[u0] : 0;      // the chunk's first slot in the launch-wide numbering
   const int* slot_pair = GLOBAL ? cx.gpair + gb : cx.slot_pair;
-  if (!GLOBAL) {
-    if (tid == 0) {
-      int slot = 0;
-      for (int lj = 0; lj < ne; lj++) {
-        const int uu = u0 + lj;
-        cx.slot_first[lj] = slot;
-        for (int n = 0; n < cx.ucount[uu]; n++) {
-          const int p = cx.upair[uu * MAX_M + n];
-          cx.slot_pair[slot] = p;
-          cx.pair_slot[p] = slot;
-          slot++;
-        }
-      }
-      cx.slot_first[ne] = slot;
-    }
-    __syncthreads();
-  }
   // slot_first[lj] - gb: the chunk's slots count from 0 (its LDS rows)
   const int P = slot_first[ne] - gb;
   constexpr int T = I / (8 * NSUB);     // gate_up items per expert
   constexpr int HPL = I / 32;           // hidden words per lane of a half-wave
   static_assert(I % 32 == 0, "whole words per lane");
   constexpr int TPH = (T + 31) / 32;    // tile maxima per lane of a half-wave
-  // The pairs' hidden rows are gathered two at a time per wave (a pair per half-wave: the tiles' maxima and the
-  // values in one round trip) and quantized into LDS slots. Each wave gathers its own two experts' pairs, or with
-  // SPREAD the chunk's pairs go round the workgroup's 8 half-waves (one round trip for up to 8 pairs, where a wave
-  // whose experts hold 3 or more needed two). Without GLOBAL the gather is issued once the wave's weight rows have
-  // arrived (its loads complete in order, so anything issued earlier would be read early and come back no sooner);
-  // with GLOBAL it goes out behind them at once. The words carry their epoch, so a gather that finds every word
-  // current needs nothing else. Otherwise the stale words are read again, coherently, until they are current. (Not
-  // the experts' counters first: every waiting wave would poll the same few words, and by the time a first gather is
-  // back the late items are mostly published.)
   const int la = 2 * w, lb = 2 * w + 1;
   const bool has_b = lb < ne;
   const bool gathers = SPREAD || la < ne;
   const int s0 = SPREAD || !gathers ? 0 : slot_first[la] - gb;
   const int s1 = SPREAD ? P : !gathers ? 0 : slot_first[has_b ? lb + 1 : la + 1] - gb;
+  bool gave = false;
   if (gathers) {
     if (!GLOBAL) settle();
     const int half = lane >> 5, hl = lane & 31;
@@ -426,7 +478,9 @@ D3_INLINE void down_finish(const Ctx& cx, int c, int hb, const DownRows<F, I>& d
       for (int k = 0; k < TPH; k++) stale |= tag_diff(mw[k], cx.epoch);
 #pragma unroll
       for (int j = 0; j < HPL; j++) stale |= tag_diff(vw[j], cx.epoch);
-      if (!__all(stale == 0u)) {
+      if (limit == 0) {
+        gave = true;  // recompute_all: as if the producers never came
+      } else if (!__all(stale == 0u)) {
         // While waiting, only the item maxima are read again (TPH words a lane; an item stores its maximum after its
         // hidden words): re-reading every stale hidden word each round cost as much memory traffic, over the down
         // blocks, as their weight rows. Once the maxima are current, the hidden words still stale are read again.
@@ -447,7 +501,10 @@ D3_INLINE void down_finish(const Ctx& cx, int c, int hb, const DownRows<F, I>& d
             }
             if (__all(stale == 0u)) break;
           }
-          if (!keep_polling(polls, a.sync + SYNC_STATUS, a.spin_limit)) break;
+          if (!keep_polling(polls, a.status, limit, cx.epoch, limit == RECOVER_LIMIT)) {
+            gave = true;
+            break;
+          }
         }
       }
       // the pair's absmax over its tiles' maxima: a half-wave reduction (rows 0-1 or 2-3 of the wave)
@@ -472,9 +529,21 @@ D3_INLINE void down_finish(const Ctx& cx, int c, int hb, const DownRows<F, I>& d
       }
     }
   }
-  // the slots are in LDS before the products read them: this wave's own, or with SPREAD every wave's
-  if (SPREAD) __syncthreads();
-  else settle();
+  return gave;
+}
+
+// The products of down item (c, hb) against the gathered slots: each wave's two experts' 8 output rows, times the
+// slots' scales, into lparts [slot, 8].
+template <int F, int H, int I, bool GLOBAL>
+D3_INLINE void down_products(const Ctx& cx, int c, const DownRows<F, I>& d) {
+  constexpr int STEPS = I / 128;
+  constexpr int SHIFT = unpack_shift(F);
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, q = lane >> 4, col = lane & 15;
+  const int u0 = cx.chunk_first[c], ne = cx.chunk_first[c + 1] - u0;
+  const int* slot_first = GLOBAL ? cx.gfirst + u0 : cx.slot_first;
+  const int gb = GLOBAL ? cx.gfirst[u0] : 0;
+  const int la = 2 * w, lb = 2 * w + 1;
+  const bool has_b = lb < ne;
   if (la < ne) {
     const int na = slot_first[la + 1] - slot_first[la];
     const int nb = has_b ? slot_first[lb + 1] - slot_first[lb] : 0;
@@ -528,9 +597,80 @@ D3_INLINE void down_finish(const Ctx& cx, int c, int hb, const DownRows<F, I>& d
       }
     }
   }
+}
+
+// Down item (c, hb) up to its partial outputs (lparts) once its loads are out: the slot tables, the gather, the
+// products. GLOBAL: the slots come from the launch-wide tables (general schedule) and the gather goes out behind the
+// weight rows at once; otherwise thread 0 numbers the chunk's slots first and the gather waits for the weight rows
+// (one row: see one_row_layer). Returns false when a wave's wait gave up (the same in every thread).
+// RECOVERY: the item run again after such a give-up, computing everything it depends on itself: every gate_up item of
+// the chunk first (the same code on the same inputs, publishing the words the items would have published), its rows
+// loaded again, then the gather reads its own words back.
+template <int F, int H, int I, int NSUB, bool GLOBAL, bool SPREAD, bool RECOVERY>
+D3_INLINE bool down_compute(const Ctx& cx, int c, int hb, DownRows<F, I>& d) {
+  const int tid = threadIdx.x;
+  if (RECOVERY) {
+    recompute_gate_up<F, H, I, NSUB>(cx, c);
+    down_load<F, H, I>(cx, c, hb, d);
+    __syncthreads();  // the recomputed words are stored (the barrier waits for them) before anyone reads them back
+  }
+  if (!GLOBAL) {
+    if (tid == 0) {
+      const int u0 = cx.chunk_first[c], ne = cx.chunk_first[c + 1] - u0;
+      int slot = 0;
+      for (int lj = 0; lj < ne; lj++) {
+        const int uu = u0 + lj;
+        cx.slot_first[lj] = slot;
+        for (int n = 0; n < cx.ucount[uu]; n++) {
+          const int p = cx.upair[uu * MAX_M + n];
+          cx.slot_pair[slot] = p;
+          cx.pair_slot[p] = slot;
+          slot++;
+        }
+      }
+      cx.slot_first[ne] = slot;
+    }
+    __syncthreads();
+  }
+  const bool gave = down_gather<F, H, I, NSUB, GLOBAL, SPREAD>(cx, c, RECOVERY ? RECOVER_LIMIT : cx.a->spin_limit);
+  if (gave && (tid & 63) == 0) {
+    if (RECOVERY) note_recovery(*cx.a, 2u);
+    else cx.flags[FLAG_HIDDEN] = 1;
+  }
+  // the slots are in LDS before the products read them: this wave's own, or with SPREAD every wave's
+  if (SPREAD) __syncthreads();
+  else settle();
+  if (RECOVERY || (SPREAD ? cx.flags[FLAG_HIDDEN] == 0 : !gave)) down_products<F, H, I, GLOBAL>(cx, c, d);
   __syncthreads();
-  if (cx.nch == 1) {
+  return RECOVERY || cx.flags[FLAG_HIDDEN] == 0;
+}
+
+template <int F, int H, int I, int NSUB, bool RECOVERY>
+D3_INLINE bool shared_down_block(const Ctx& cx, int b, const i32x4* xraw);
+
+// the rest of down item (c, hb) once its loads are out: down_compute, then the weighted sum (one chunk: straight to
+// `out`, plus the shared expert's term in the block) or the partial outputs (MULTI: several chunks, the last chunk's
+// item sums them). Returns false when a wait gave up (the same in every thread); the caller then runs the item again
+// with RECOVERY, which computes everything the item depends on itself: the chunk's gate_up items, the shared expert's
+// block of output rows, the other chunks' partial outputs of this block.
+template <int F, int H, int I, int NSUB, bool GLOBAL, bool SPREAD, bool MULTI, bool RECOVERY>
+D3_INLINE bool down_finish(const Ctx& cx, int c, int hb, DownRows<F, I>& d) {
+  const MoeA8Args& a = *cx.a;
+  const int tid = threadIdx.x;
+  const int M = a.M, K8 = a.topk;
+  const uint32_t limit = RECOVERY ? RECOVER_LIMIT : a.spin_limit;
+  if (!down_compute<F, H, I, NSUB, GLOBAL, SPREAD, RECOVERY>(cx, c, hb, d)) return false;
+  if (!MULTI || cx.nch == 1) {
     // every row's experts are in this chunk
+    if (RECOVERY && a.sh_dn_w) {
+      // the shared expert's block of 64 output rows holding these 8, computed here
+      const int lane = tid & 63;
+      i32x4 xraw[H / 512];
+#pragma unroll
+      for (int k = 0; k < H / 512; k++) xraw[k] = *(const i32x4*)(a.x + 512 * k + 8 * lane);
+      shared_down_block<F, H, I, NSUB, true>(cx, hb >> 3, xraw);
+      __syncthreads();
+    }
     for (int idx = tid; idx < M * 8; idx += 256) {
       const int t = idx >> 3, r = idx & 7;
       float acc = 0.0f;
@@ -538,52 +678,107 @@ D3_INLINE void down_finish(const Ctx& cx, int c, int hb, const DownRows<F, I>& d
       if (a.sh_dn_w) {
         // the shared expert's gated output of this row (one row): the block's sum of two bf16 tensors
         const uint64_t* src = a.sharedw + 8 * hb + r;
-        uint64_t word = get_tagged_cached(src);
+        uint64_t word = RECOVERY ? get_tagged(src) : limit == 0 ? 0 : get_tagged_cached(src);
         uint32_t polls = 0;
-        while (!tag_is(word, cx.epoch) && keep_polling(polls, a.sync + SYNC_STATUS, a.spin_limit)) word = get_tagged(src);
+        while (!tag_is(word, cx.epoch) && keep_polling(polls, a.status, limit, cx.epoch, limit == RECOVER_LIMIT)) word = get_tagged(src);
+        if (!tag_is(word, cx.epoch)) {
+          if (RECOVERY) note_recovery(a, 2u);
+          else cx.flags[FLAG_SHARED] = 1;
+        }
         acc = bf16_round(acc) + tagged_value(word);
       }
       a.out[(size_t)t * H + 8 * hb + r] = (uint16_t)f32_to_bf16(acc);
     }
-  } else {
+    if (!RECOVERY && a.sh_dn_w) {
+      __syncthreads();
+      if (cx.flags[FLAG_SHARED] != 0) return false;
+    }
+    return true;
+  }
+  {
+    const int u0 = cx.chunk_first[c], ne = cx.chunk_first[c + 1] - u0;
+    const int* slot_first = GLOBAL ? cx.gfirst + u0 : cx.slot_first;
+    const int gb = GLOBAL ? cx.gfirst[u0] : 0;
+    const int* slot_pair = GLOBAL ? cx.gpair + gb : cx.slot_pair;
+    const int P = slot_first[ne] - gb;
     for (int idx = tid; idx < P * 8; idx += 256) {
       const int slot = idx >> 3, r = idx & 7;
       put_tagged(a.parts + (size_t)slot_pair[slot] * H + 8 * hb + r, cx.lparts[slot * 8 + r], cx.epoch);
     }
-    if (c == cx.nch - 1) {
-      // the last chunk's item gathers every pair's partial outputs of this block
-      for (int idx = tid; idx < M * K8 * 8; idx += 256) {
-        const int p = idx >> 3, r = idx & 7;
-        const uint64_t* src = a.parts + (size_t)p * H + 8 * hb + r;
-        uint64_t word = get_tagged_cached(src);
-        uint32_t polls = 0;
-        while (!tag_is(word, cx.epoch) && keep_polling(polls, a.sync + SYNC_STATUS, a.spin_limit)) word = get_tagged(src);
-        cx.fparts[idx] = tagged_value(word);
+  }
+  if (c != cx.nch - 1) return true;
+  if (RECOVERY) {
+    // the other chunks' items of this block, computed here
+    __syncthreads();  // lparts and the slot tables are rewritten by the next chunk
+#pragma unroll 1
+    for (int c2 = 0; c2 < cx.nch - 1; c2++) {
+      down_compute<F, H, I, NSUB, GLOBAL, SPREAD, true>(cx, c2, hb, d);
+      const int v0 = cx.chunk_first[c2], nv = cx.chunk_first[c2 + 1] - v0;
+      const int* sf2 = GLOBAL ? cx.gfirst + v0 : cx.slot_first;
+      const int gb2 = GLOBAL ? cx.gfirst[v0] : 0;
+      const int* sp2 = GLOBAL ? cx.gpair + gb2 : cx.slot_pair;
+      for (int idx = tid; idx < (sf2[nv] - gb2) * 8; idx += 256) {
+        const int slot = idx >> 3, r = idx & 7;
+        put_tagged(a.parts + (size_t)sp2[slot] * H + 8 * hb + r, cx.lparts[slot * 8 + r], cx.epoch);
       }
-      __syncthreads();
-      for (int idx = tid; idx < M * 8; idx += 256) {
-        const int t = idx >> 3, r = idx & 7;
-        float acc = 0.0f;
-        for (int j = 0; j < K8; j++) acc = fmaf(cx.fparts[(t * K8 + j) * 8 + r], cx.rt_w[t * MAX_K + j], acc);
-        a.out[(size_t)t * H + 8 * hb + r] = (uint16_t)f32_to_bf16(acc);
-      }
+      __syncthreads();  // stored before they are read back; lparts and the slot tables are rewritten next
     }
   }
+  // the last chunk's item gathers every pair's partial outputs of this block
+  for (int idx = tid; idx < M * K8 * 8; idx += 256) {
+    const int p = idx >> 3, r = idx & 7;
+    const uint64_t* src = a.parts + (size_t)p * H + 8 * hb + r;
+    uint64_t word = RECOVERY ? get_tagged(src) : limit == 0 ? 0 : get_tagged_cached(src);
+    uint32_t polls = 0;
+    while (!tag_is(word, cx.epoch) && keep_polling(polls, a.status, limit, cx.epoch, limit == RECOVER_LIMIT)) word = get_tagged(src);
+    if (!tag_is(word, cx.epoch)) {
+      if (RECOVERY) note_recovery(a, 2u);
+      else cx.flags[FLAG_PARTS] = 1;
+    }
+    cx.fparts[idx] = tagged_value(word);
+  }
+  __syncthreads();
+  if (!RECOVERY && cx.flags[FLAG_PARTS] != 0) return false;
+  for (int idx = tid; idx < M * 8; idx += 256) {
+    const int t = idx >> 3, r = idx & 7;
+    float acc = 0.0f;
+    for (int j = 0; j < K8; j++) acc = fmaf(cx.fparts[(t * K8 + j) * 8 + r], cx.rt_w[t * MAX_K + j], acc);
+    a.out[(size_t)t * H + 8 * hb + r] = (uint16_t)f32_to_bf16(acc);
+  }
+  return true;
 }
 
-// down item (c, hb); GLOBAL as for down_finish
+// After a recovery: the workgroup's flags cleared once every wave has read them (the caller's barriers since), and
+// the event recorded in the sticky bits
+D3_INLINE void end_recovery(const Ctx& cx) {
+  __syncthreads();
+  if (threadIdx.x < N_FLAGS) cx.flags[threadIdx.x] = 0;
+}
+
+// Down item (c, hb) run again with RECOVERY after a wait gave up (a call: see RECOVERY_FN).
+template <int F, int H, int I, int NSUB, bool GLOBAL, bool SPREAD, bool MULTI>
+RECOVERY_FN void recover_down(const MoeA8Args* args, uint32_t epoch, int c, int hb) {
+  const Ctx cx = recovery_ctx(args, H, I, epoch);
+  if (threadIdx.x == 0) note_recovery(*cx.a, 1u);
+  DownRows<F, I> d;
+  down_finish<F, H, I, NSUB, GLOBAL, SPREAD, MULTI, true>(cx, c, hb, d);
+  end_recovery(cx);
+}
+
+// down item (c, hb) of the general schedule (GLOBAL as for down_finish)
 template <int F, int H, int I, bool GLOBAL>
 D3_INLINE void down_item(const Ctx& cx, int c, int hb) {
   __syncthreads();  // the previous item's readers of the slot tables and partial outputs are done
   DownRows<F, I> d;
   down_load<F, H, I>(cx, c, hb, d);
-  down_finish<F, H, I, 2, GLOBAL, true>(cx, c, hb, d);
+  if (!down_finish<F, H, I, 2, GLOBAL, true, true, false>(cx, c, hb, d))
+    recover_down<F, H, I, 2, GLOBAL, true, true>(kernel_args(), cx.epoch, c, hb);
 }
 
-// The router's logit e for one row: bf16(x . router[e]) with float sums (model.py:115), x as every wave holds it
-// (lane l: columns 512 k + 8 l .. + 7 of chunk k); published as a tagged word (its bf16 bits) for every routing wave.
+// The router's logit e for one row, as bf16 bits: bf16(x . router[e]) with float sums (model.py:115), x as every wave
+// holds it (lane l: columns 512 k + 8 l .. + 7 of chunk k); the same in every lane.
 template <int H>
-D3_INLINE void router_logit(const MoeA8Args& a, uint32_t epoch, int e, const i32x4* xraw, int lane) {
+D3_INLINE uint32_t router_dot(const MoeA8Args& a, int e, const i32x4* xraw, int lane) {
   const uint16_t* wr = a.router + (size_t)e * H;
   float acc = 0.0f;
 #pragma unroll
@@ -597,7 +792,13 @@ D3_INLINE void router_logit(const MoeA8Args& a, uint32_t epoch, int e, const i32
       acc = fmaf(bf16_to_f32(xs[j] >> 16), bf16_to_f32(ws[j] >> 16), acc);
     }
   }
-  const uint32_t bits = f32_to_bf16(wave_sum_f32(acc));
+  return f32_to_bf16(wave_sum_f32(acc));
+}
+
+// router_dot published as a tagged word (its bf16 bits) for every routing wave
+template <int H>
+D3_INLINE void router_logit(const MoeA8Args& a, uint32_t epoch, int e, const i32x4* xraw, int lane) {
+  const uint32_t bits = router_dot<H>(a, e, xraw, lane);
   if (lane == 0) {
     put_tagged(a.logitw + e, __uint_as_float(bits), epoch);
     if (a.logits_out) a.logits_out[e] = (uint16_t)bits;
@@ -605,46 +806,144 @@ D3_INLINE void router_logit(const MoeA8Args& a, uint32_t epoch, int e, const i32
 }
 
 // The router's logits as bf16 bits for experts lane + 64 j, once every one is published (reads of words not yet
-// landed are repeated, bounded by spin_limit).
-template <int KPL>
-D3_INLINE void gather_logits(const MoeA8Args& a, uint32_t epoch, int lane, uint32_t* lb) {
+// landed are repeated, bounded by spin_limit). When the wait gives up, the wave computes the logits still missing
+// itself (router_dot: the value their workgroups would have published).
+template <int H, int KPL>
+D3_INLINE void gather_logits(const MoeA8Args& a, uint32_t epoch, int lane, uint32_t* lb, const i32x4* xraw) {
   uint64_t wv[KPL];
 #pragma unroll
   for (int j = 0; j < KPL; j++) wv[j] = get_tagged_cached(a.logitw + min(lane + 64 * j, a.E - 1));
-  bool fresh = true;
+  bool fresh = a.spin_limit != 0;  // recompute_all: as if no logit had come
 #pragma unroll
   for (int j = 0; j < KPL; j++) fresh = fresh && tag_is(wv[j], epoch);
   if (!__all(fresh)) {
     uint32_t polls = 0;
-    while (true) {
-      bool ok = true;
+    bool ok = false;
+    while (!ok && a.spin_limit != 0) {
+      ok = true;
 #pragma unroll
       for (int j = 0; j < KPL; j++) {
         if (!tag_is(wv[j], epoch)) wv[j] = get_tagged(a.logitw + min(lane + 64 * j, a.E - 1));
         ok = ok && tag_is(wv[j], epoch);
       }
-      if (__all(ok) || !keep_polling(polls, a.sync + SYNC_STATUS, a.spin_limit)) break;
+      ok = __all(ok);
+      if (!ok && !keep_polling(polls, a.status, a.spin_limit, epoch)) break;
+    }
+    if (!ok) {
+      if (lane == 0) note_recovery(a, 1u);
+#pragma unroll
+      for (int j = 0; j < KPL; j++) {
+        uint64_t missing = __ballot((a.spin_limit == 0 || !tag_is(wv[j], epoch)) && lane + 64 * j < a.E);
+        while (missing != 0u) {
+          const int l = __builtin_ctzll(missing);
+          missing &= missing - 1u;
+          const uint32_t bits = router_dot<H>(a, l + 64 * j, xraw, lane);
+          if (lane == l) wv[j] = bits;
+        }
+      }
     }
   }
 #pragma unroll
   for (int j = 0; j < KPL; j++) lb[j] = (uint32_t)wv[j] & 0xFFFFu;
 }
 
+// x (bf16, as every wave holds it) quantized per row into LDS (xq, sx[0]): wave w stores chunk w (H = 2048), the
+// columns its MFMA steps read
+template <int F, int H>
+D3_INLINE void quantize_x_lds(const Ctx& cx, const i32x4* xraw) {
+  constexpr float QMAX = act_qmax<F>();
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  float v[H / 512][8];
+  float amax = 0.0f;
+#pragma unroll
+  for (int k = 0; k < H / 512; k++) {
+    const uint32_t wv[4] = {(uint32_t)xraw[k].x, (uint32_t)xraw[k].y, (uint32_t)xraw[k].z, (uint32_t)xraw[k].w};
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      v[k][2 * j] = bf16_to_f32(wv[j] & 0xFFFFu);
+      v[k][2 * j + 1] = bf16_to_f32(wv[j] >> 16);
+      amax = fmaxf(amax, fmaxf(fabsf(v[k][2 * j]), fabsf(v[k][2 * j + 1])));
+    }
+  }
+  amax = wave_max_f32(amax);
+  const float inv = amax > 0.0f ? QMAX / amax : 0.0f;
+#pragma unroll
+  for (int k = 0; k < H / 512; k++)
+    if (k == w) store_act8<F>(cx.xq + 512 * k + 8 * lane, v[k], inv);
+  if (lane == 0) cx.sx[0] = amax / QMAX;
+}
+
+// The shared expert's hidden row (pair topk) and its items' maxima, lane l holding words l + 64 j (each load covers
+// 512 contiguous bytes); words not yet published are read again, coherently, until they carry the launch's epoch
+// (polling the expert's counter first, as every waiting wave of these blocks would, cost 2-2.5 us per block). Returns
+// whether the wave gave up.
+template <int I, int T, int TPW, int HPW>
+D3_INLINE bool shared_gather(const Ctx& cx, uint32_t limit, uint64_t* mw, uint64_t* vw, bool cached) {
+  const MoeA8Args& a = *cx.a;
+  const int lane = threadIdx.x & 63;
+  const uint64_t* hrow = a.hidden + (size_t)a.topk * I;
+  const uint64_t* trow = a.tmax + (size_t)a.topk * T;
+#pragma unroll
+  for (int k = 0; k < TPW; k++)
+    mw[k] = cached ? get_tagged_cached(trow + min(lane + 64 * k, T - 1)) : get_tagged(trow + min(lane + 64 * k, T - 1));
+#pragma unroll
+  for (int j = 0; j < HPW; j++) vw[j] = cached ? get_tagged_cached(hrow + lane + 64 * j) : get_tagged(hrow + lane + 64 * j);
+  bool fresh = true;
+#pragma unroll
+  for (int k = 0; k < TPW; k++) fresh = fresh && tag_is(mw[k], cx.epoch);
+#pragma unroll
+  for (int j = 0; j < HPW; j++) fresh = fresh && tag_is(vw[j], cx.epoch);
+  if (limit == 0) return true;  // recompute_all
+  if (__all(fresh)) return false;
+  uint32_t polls = 0;
+  while (true) {
+    bool ok = true;
+#pragma unroll
+    for (int k = 0; k < TPW; k++) {
+      if (!tag_is(mw[k], cx.epoch)) mw[k] = get_tagged(trow + min(lane + 64 * k, T - 1));
+      ok = ok && tag_is(mw[k], cx.epoch);
+    }
+#pragma unroll
+    for (int j = 0; j < HPW; j++) {
+      if (!tag_is(vw[j], cx.epoch)) vw[j] = get_tagged(hrow + lane + 64 * j);
+      ok = ok && tag_is(vw[j], cx.epoch);
+    }
+    if (__all(ok)) return false;
+    if (!keep_polling(polls, a.status, limit, cx.epoch, limit == RECOVER_LIMIT)) return true;
+  }
+}
+
 // A block of 64 output rows of the shared expert for one row (wave w: rows 64 b + 16 w .. + 15, one 16-row MFMA tile
 // against the shared hidden row as column 0): its gated output bf16(bf16(sigmoid(bf16(x . gate))) * bf16(y)), as
-// model.py:123 rounds it, published as tagged words for the routed down blocks to add.
-template <int F, int H, int I, int NSUB>
-D3_INLINE void shared_down_block(const Ctx& cx, int b, const i32x4* xraw) {
+// model.py:123 rounds it, published as tagged words for the routed down blocks to add. Every wave of the workgroup
+// calls it. Returns false when a wave's wait for the shared hidden row gave up (the same in every thread); RECOVERY
+// then runs it again computing the shared expert's gate_up items first (as recompute_gate_up does for the routed
+// experts).
+template <int F, int H, int I, int NSUB, bool RECOVERY>
+D3_INLINE bool shared_down_block(const Ctx& cx, int b, const i32x4* xraw) {
   constexpr int STEPS = I / 128;
   constexpr int RB = row_bytes(F, I);
   constexpr int SHIFT = unpack_shift(F);
   constexpr float QMAX = act_qmax<F>();
   constexpr int T = I / (8 * NSUB);
   constexpr int TPW = (T + 63) / 64;  // item maxima per lane
+  constexpr int HPW = I / 64;
   const MoeA8Args& a = *cx.a;
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, q = lane >> 4, col = lane & 15;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, q = lane >> 4, col = lane & 15;
   const int K8 = a.topk;
   const int r0 = 64 * b + 16 * w;
+  if (RECOVERY) {
+    if (tid == 0) {
+      cx.utok[K8 * MAX_M] = 0;
+      cx.upair[K8 * MAX_M] = (uint8_t)K8;
+    }
+    quantize_x_lds<F, H>(cx, xraw);
+    __syncthreads();
+#pragma unroll 1
+    for (int tile = 0; tile < T; tile++)
+      gate_up_item<F, H, I, NSUB>(cx, K8, tile, tile & 1, 0, 1, [] {}, [] {}, a.sh_gu_w, a.sh_gu_s);
+    __syncthreads();  // the recomputed words are stored before anyone reads them back
+  }
   Raw<F> raw[STEPS];
 #pragma unroll
   for (int s = 0; s < STEPS; s++) load_step<F>(raw[s], a.sh_dn_w + (size_t)(r0 + (lane & 15)) * RB, s, q);
@@ -681,41 +980,16 @@ D3_INLINE void shared_down_block(const Ctx& cx, int b, const i32x4* xraw) {
   }
   const float gate = bf16_round(wave_sum_f32(gsum));
   const float gw = bf16_round(1.0f / (1.0f + expf(-gate)));
-  // the shared hidden row (pair K8), gathered once this wave's rows have landed; words not yet published are read
-  // again, coherently, until they carry the launch's epoch (polling the expert's counter first, as every waiting wave
-  // of these blocks would, cost 2-2.5 us per block). Lane l reads words l + 64 j, so each load covers 512 contiguous
-  // bytes.
+  // the shared hidden row, gathered once this wave's rows have landed
   settle();
-  const uint64_t* hrow = a.hidden + (size_t)K8 * I;
-  const uint64_t* trow = a.tmax + (size_t)K8 * T;
-  uint64_t mw[TPW];
-#pragma unroll
-  for (int k = 0; k < TPW; k++) mw[k] = get_tagged_cached(trow + min(lane + 64 * k, T - 1));
-  constexpr int HPW = I / 64;
-  uint64_t vw[HPW];
-#pragma unroll
-  for (int j = 0; j < HPW; j++) vw[j] = get_tagged_cached(hrow + lane + 64 * j);
-  bool fresh = true;
-#pragma unroll
-  for (int k = 0; k < TPW; k++) fresh = fresh && tag_is(mw[k], cx.epoch);
-#pragma unroll
-  for (int j = 0; j < HPW; j++) fresh = fresh && tag_is(vw[j], cx.epoch);
-  if (!__all(fresh)) {
-    uint32_t polls = 0;
-    while (true) {
-      bool ok = true;
-#pragma unroll
-      for (int k = 0; k < TPW; k++) {
-        if (!tag_is(mw[k], cx.epoch)) mw[k] = get_tagged(trow + min(lane + 64 * k, T - 1));
-        ok = ok && tag_is(mw[k], cx.epoch);
-      }
-#pragma unroll
-      for (int j = 0; j < HPW; j++) {
-        if (!tag_is(vw[j], cx.epoch)) vw[j] = get_tagged(hrow + lane + 64 * j);
-        ok = ok && tag_is(vw[j], cx.epoch);
-      }
-      if (__all(ok) || !keep_polling(polls, a.sync + SYNC_STATUS, a.spin_limit)) break;
-    }
+  uint64_t mw[TPW], vw[HPW];
+  const bool gave = shared_gather<I, T, TPW, HPW>(cx, RECOVERY ? RECOVER_LIMIT : a.spin_limit, mw, vw, !RECOVERY);
+  if (RECOVERY) {
+    if (gave && lane == 0) note_recovery(a, 2u);
+  } else {
+    if (gave && lane == 0) cx.flags[FLAG_SH_HIDDEN] = 1;
+    __syncthreads();
+    if (cx.flags[FLAG_SH_HIDDEN] != 0) return false;
   }
   float tm = 0.0f;
 #pragma unroll
@@ -760,6 +1034,21 @@ D3_INLINE void shared_down_block(const Ctx& cx, int b, const i32x4* xraw) {
       put_tagged(a.sharedw + r0 + 4 * q + i, bf16_round(gw * bf16_round(y * hs)), cx.epoch);
     }
   }
+  return true;
+}
+
+// shared_down_block run again with RECOVERY after a wait gave up (a call: see RECOVERY_FN)
+template <int F, int H, int I, int NSUB>
+RECOVERY_FN void recover_shared(const MoeA8Args* args, uint32_t epoch, int b) {
+  const Ctx cx = recovery_ctx(args, H, I, epoch);
+  const MoeA8Args& a = *cx.a;
+  if (threadIdx.x == 0) note_recovery(a, 1u);
+  const int lane = threadIdx.x & 63;
+  i32x4 xraw[H / 512];
+#pragma unroll
+  for (int k = 0; k < H / 512; k++) xraw[k] = *(const i32x4*)(a.x + 512 * k + 8 * lane);
+  shared_down_block<F, H, I, NSUB, true>(cx, b, xraw);
+  end_recovery(cx);
 }
 
 // One row (M = 1) with a workgroup for each gate_up tile: workgroup i < k T computes gate_up tile i % T of the expert
@@ -776,7 +1065,6 @@ template <int F, int H, int I, int NSUB, int KPL>
 D3_INLINE void one_row_layer(Ctx& cx, int i) {
   static_assert(H == 2048, "wave w's K slice is x chunk w");
   constexpr int T = I / (8 * NSUB), NHB = H / 8;  // gate_up items per expert, down blocks
-  constexpr float QMAX = act_qmax<F>();
   const MoeA8Args& a = *cx.a;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int E = a.E, K8 = a.topk;
@@ -795,13 +1083,15 @@ D3_INLINE void one_row_layer(Ctx& cx, int i) {
   for (int k = 0; k < H / 512; k++) xraw[k] = *(const i32x4*)(a.x + 512 * k + 8 * lane);
   if (a.router && i < E && w == 0) router_logit<H>(a, cx.epoch, i, xraw, lane);
   if (i >= routed + T) {
-    shared_down_block<F, H, I, NSUB>(cx, i - routed - T, xraw);
+    __syncthreads();  // the LDS flags are cleared (make_ctx) before any wave sets one
+    if (!shared_down_block<F, H, I, NSUB, false>(cx, i - routed - T, xraw))
+      recover_shared<F, H, I, NSUB>(kernel_args(), cx.epoch, i - routed - T);
     return;
   }
   const int u = is_shared ? K8 : i / T, tile = is_shared ? i - routed : i % T;
   const int hb = i - a.dn_first;
   const bool has_down = hb >= 0 && hb < NHB && !is_shared;
-  if (a.router && !is_shared) gather_logits<KPL>(a, cx.epoch, lane, lb);
+  if (a.router && !is_shared) gather_logits<H, KPL>(a, cx.epoch, lane, lb, xraw);
   TopKeys<KPL> tk(lb, lane, E);
   if (!is_shared) tk.rounds(lane, 0, u + 1);
   const int e = is_shared ? 0 : route_key_index((uint32_t)__builtin_amdgcn_readlane((int)tk.mine, u));
@@ -809,7 +1099,7 @@ D3_INLINE void one_row_layer(Ctx& cx, int i) {
   cx.nch = 1;
   cx.n_dn = NHB;
   DownRows<F, I> d;
-  const uint64_t before = gate_up_item<F, H, I, NSUB>(
+  gate_up_item<F, H, I, NSUB>(
       cx, u, tile, 0, e, 1,
       [&]() {
         if (has_down) {
@@ -835,25 +1125,8 @@ D3_INLINE void one_row_layer(Ctx& cx, int i) {
             cx.misc[1] = 1;
           }
         }
-        float v[H / 512][8];
-        float amax = 0.0f;
-#pragma unroll
-        for (int k = 0; k < H / 512; k++) {
-          const uint32_t wv[4] = {(uint32_t)xraw[k].x, (uint32_t)xraw[k].y, (uint32_t)xraw[k].z, (uint32_t)xraw[k].w};
-#pragma unroll
-          for (int j = 0; j < 4; j++) {
-            v[k][2 * j] = bf16_to_f32(wv[j] & 0xFFFFu);
-            v[k][2 * j + 1] = bf16_to_f32(wv[j] >> 16);
-            amax = fmaxf(amax, fmaxf(fabsf(v[k][2 * j]), fabsf(v[k][2 * j + 1])));
-          }
-        }
-        amax = wave_max_f32(amax);
-        const float inv = amax > 0.0f ? QMAX / amax : 0.0f;
-#pragma unroll
-        for (int k = 0; k < H / 512; k++)
-          if (k == w) store_act8<F>(cx.xq + 512 * k + 8 * lane, v[k], inv);
+        quantize_x_lds<F, H>(cx, xraw);
         if (lane == 0) {
-          cx.sx[0] = amax / QMAX;
           cx.utok[u * MAX_M] = 0;
           cx.upair[u * MAX_M] = (uint8_t)u;
         }
@@ -863,47 +1136,17 @@ D3_INLINE void one_row_layer(Ctx& cx, int i) {
         if (has_down) down_load<F, H, I>(cx, 0, hb, d);
       },
       is_shared ? a.sh_gu_w : a.gu_w, is_shared ? a.sh_gu_s : a.gu_s);
-  if (has_down) down_finish<F, H, I, NSUB>(cx, 0, hb, d);
-  flag_later_epoch(a, before, cx.epoch);
-}
-
-// a workgroup's view of its LDS and the launch
-D3_INLINE Ctx make_ctx(const MoeA8Args& a, uint8_t* lds, int H, int I) {
-  const Lds L(a.M, a.topk, H, I);
-  Ctx cx;
-  cx.a = &a;
-  cx.xq = lds + L.xq;
-  cx.sx = (float*)(lds + L.sx);
-  cx.rt_id = (int*)(lds + L.rt_id);
-  cx.rt_w = (float*)(lds + L.rt_w);
-  cx.ulist = (int*)(lds + L.ulist);
-  cx.ucount = (int*)(lds + L.ucount);
-  cx.utok = lds + L.utok;
-  cx.upair = lds + L.upair;
-  cx.chunk_first = (int*)(lds + L.chunk_first);
-  cx.misc = (int*)(lds + L.misc);
-  cx.emask = (uint32_t*)(lds + L.emask);
-  cx.red = (float*)(lds + L.red);
-  cx.hq = lds + L.hq;
-  cx.hs = (float*)(lds + L.hs);
-  cx.lparts = (float*)(lds + L.lparts);
-  cx.slot_pair = (int*)(lds + L.slot_pair);
-  cx.pair_slot = (int*)(lds + L.pair_slot);
-  cx.slot_first = (int*)(lds + L.slot_first);
-  cx.gfirst = (int*)(lds + L.gfirst);
-  cx.gpair = (int*)(lds + L.gpair);
-  cx.fparts = (float*)(lds + L.fparts);
-  cx.epoch = launch_epoch();
-  return cx;
+  if (has_down && !down_finish<F, H, I, NSUB, false, false, false, false>(cx, 0, hb, d))
+    recover_down<F, H, I, NSUB, false, false, false>(kernel_args(), cx.epoch, 0, hb);
 }
 
 // The one-row schedule as its own kernel: k I / UT + I / UT + H / 64 workgroups (UT = 8 NSUB hidden units per
-// gate_up item). With UT = 16 that is fewer than two per CU, so it is compiled for two per CU (256 registers a lane)
-// and keeps its weight rows, routing state and x in registers.
+// gate_up item). Compiled for three workgroups per CU (168 registers a lane), which the 8-unit items need (768 of them
+// at k 8, I 768) and the 16-unit ones keep for latency; the recovery calls (recover_down, recover_shared) are held to
+// the same bound, so their registers cost the fast path nothing.
 template <int F, int H, int I, int NSUB>
-__global__ void __launch_bounds__(256, 2) moe_a8_one_row_kernel(MoeA8Args a) {
-  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-  Ctx cx = make_ctx(a, lds, H, I);
+__global__ void __launch_bounds__(256, 3) moe_a8_one_row_kernel(MoeA8Args a) {
+  Ctx cx = make_ctx(a, H, I);
   if (a.E <= 128) one_row_layer<F, H, I, NSUB, 2>(cx, (int)blockIdx.x);
   else one_row_layer<F, H, I, NSUB, 4>(cx, (int)blockIdx.x);
 }
@@ -914,13 +1157,12 @@ __global__ void __launch_bounds__(256, 2) moe_a8_one_row_kernel(MoeA8Args a) {
 // CU): 2 rows 25.4 / 29.4, 3 rows 40.8 / 39.5, 4 rows 45.8 / 49.4, 5 rows 58.6 / 61.9.
 template <int F, int H, int I, int WPC>
 __global__ void __launch_bounds__(256, WPC) moe_a8_kernel(MoeA8Args a) {
-  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   constexpr int T = I / 16;
   constexpr int NHB = H / 8;
   constexpr float QMAX = act_qmax<F>();
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int M = a.M, E = a.E, K8 = a.topk;
-  Ctx cx = make_ctx(a, lds, H, I);
+  Ctx cx = make_ctx(a, H, I);
   // the down items' schedule (see the item loop): launch-wide slots and lag 2 for the 4- and 6-bit formats
   constexpr bool EARLY = F == FMT_W4 || F == FMT_W6;
   constexpr int LAG = EARLY ? 2 : 1;
@@ -1103,10 +1345,8 @@ __global__ void __launch_bounds__(256, WPC) moe_a8_kernel(MoeA8Args a) {
         const int u0 = cx.chunk_first[c], ne = cx.chunk_first[c + 1] - u0;
         if (item < base + ne * T) {
           const int u = u0 + (item - base) / T;
-          flag_later_epoch(a,
-                           gate_up_item<F, H, I>(cx, u, (item - base) % T, parity, cx.ulist[u], cx.ucount[u], [] {},
-                                                 [] {}, a.gu_w, a.gu_s),
-                           cx.epoch);
+          gate_up_item<F, H, I>(cx, u, (item - base) % T, parity, cx.ulist[u], cx.ucount[u], [] {}, [] {}, a.gu_w,
+                                a.gu_s);
           parity ^= 1;
           break;
         }
@@ -1139,7 +1379,7 @@ int hip_fail(hipError_t err, const char* what) {
   return (int)err;
 }
 
-// sync words, then (pairs + 1 for the shared expert) hidden rows and tile maxima, the pairs' partial outputs, and for
+// the header, then (pairs + 1 for the shared expert) hidden rows and tile maxima, the pairs' partial outputs, and for
 // the block's router and shared expert MAX_E logit words and H output words
 int64_t moe_a8_workspace_bytes(int M, int topk, int H, int I) {
   const int64_t pairs = (int64_t)M * topk;
@@ -1256,7 +1496,8 @@ int launch_moe_a8(const d3_moe_a8_desc* d, hipStream_t stream) {
   a.ids_out = d->ids_out;
   a.weights_out = d->weights_out;
   uint8_t* ws = (uint8_t*)d->workspace;
-  a.sync = (uint32_t*)ws;
+  a.status = (uint64_t*)(ws + SYNC_STATUS * 4);
+  a.sticky = (uint32_t*)ws + SYNC_STICKY;
   const size_t pairs = (size_t)d->M * d->topk;
   a.hidden = (uint64_t*)(ws + SYNC_WORDS * 4);
   a.tmax = a.hidden + (pairs + 1) * d->I;
@@ -1266,7 +1507,8 @@ int launch_moe_a8(const d3_moe_a8_desc* d, hipStream_t stream) {
   a.M = d->M;
   a.E = d->E;
   a.topk = d->topk;
-  a.spin_limit = d->spin_limit ? d->spin_limit : (1u << 20);
+  // 0 inside the kernel: every wait gives up at once (recompute_all)
+  a.spin_limit = d->recompute_all ? 0u : d->spin_limit ? d->spin_limit : (1u << 20);
   a.router = (const uint16_t*)d->router;
   a.logits_out = (uint16_t*)d->logits_out;
   a.sh_gu_w = (const uint8_t*)d->shared_gate_up;
@@ -1307,9 +1549,13 @@ int64_t d3_moe_a8_workspace_bytes(int32_t M, int32_t topk, int32_t H, int32_t I)
 
 int d3_moe_a8(const d3_moe_a8_desc* desc, void* stream) { return d3::launch_moe_a8(desc, (hipStream_t)stream); }
 
-int d3_moe_a8_status(const void* workspace, uint32_t* status) {
+int d3_moe_a8_status(void* workspace, uint32_t* status) {
   if (!workspace || !status) return d3::fail("d3_moe_a8_status: null pointer");
-  hipError_t e = hipMemcpy(status, (const uint8_t*)workspace + d3::SYNC_STATUS * 4, 4, hipMemcpyDeviceToHost);
+  uint8_t* sticky = (uint8_t*)workspace + d3::SYNC_STICKY * 4;
+  hipError_t e = hipMemcpy(status, sticky, 4, hipMemcpyDeviceToHost);
+  if (e != hipSuccess) return d3::hip_fail(e, "d3_moe_a8_status");
+  const uint32_t zero = 0;
+  e = hipMemcpy(sticky, &zero, 4, hipMemcpyHostToDevice);
   if (e != hipSuccess) return d3::hip_fail(e, "d3_moe_a8_status");
   return 0;
 }

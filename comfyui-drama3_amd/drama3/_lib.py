@@ -29,7 +29,7 @@ class MoeA8Desc(ctypes.Structure):
         ("M", c_int32), ("H", c_int32), ("I", c_int32), ("E", c_int32), ("topk", c_int32), ("spin_limit", c_uint32),
         ("grid", c_int32), ("router", c_void_p), ("logits_out", c_void_p), ("shared_gate_up", c_void_p),
         ("shared_gate_up_scale", c_void_p), ("shared_down", c_void_p), ("shared_down_scale", c_void_p),
-        ("shared_gate", c_void_p), ("item_units", c_int32),
+        ("shared_gate", c_void_p), ("item_units", c_int32), ("recompute_all", c_int32),
     ]
 
 
@@ -55,6 +55,7 @@ SIGNATURES = {
     "d3_gemv_a8_groups": (c_int32, [c_int32, c_void_p, c_int32, c_int32, c_void_p, c_int32, c_void_p, c_void_p]),
     "d3_unpack_rows": (c_int32, [c_int32, c_void_p, c_int32, c_int32, c_void_p, c_void_p]),
     "d3_cvt_fp8": (c_int32, [c_void_p, c_int32, c_void_p, c_int32, c_void_p]),
+    "d3_gemv_fp8_rows": (c_int32, [c_void_p, c_int32, c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_void_p]),
     "d3_route": (c_int32, [c_void_p, c_int32, c_int32, c_int32, c_void_p, c_void_p, c_void_p]),
     "d3_weighted_sum": (c_int32, [c_void_p, c_void_p, c_int32, c_int32, c_void_p, c_void_p]),
     "d3_rotate": (c_int32, [c_void_p, c_int32, c_int32, c_int32, c_void_p, c_void_p, c_void_p]),

@@ -190,6 +190,10 @@ def resident_decode_routed(x, logits, k, banks, kind, codebooks, H, I):
     code, wkey = _RESIDENT_KINDS[kind]
     gate_up, down = banks
     lg = logits.reshape(-1).contiguous()
+    experts = gate_up[wkey].shape[0] // (2 * I)
+    if lg.shape[0] != experts or down[wkey].shape[0] != experts * H:
+        raise ValueError(f"{lg.shape[0]} logits for banks of {experts} experts: a routed id past the banks would be "
+                         f"read out of bounds")
     gu = torch.empty((k, 2 * I), dtype=torch.float32, device=x.device)
     out = torch.empty((1, H), dtype=torch.bfloat16, device=x.device)
     ids = torch.empty((1, k), dtype=torch.int64, device=x.device)
@@ -198,6 +202,24 @@ def resident_decode_routed(x, logits, k, banks, kind, codebooks, H, I):
           _p(gate_up[wkey]), _p(gate_up["scale"]), _p(gate_up.get("s_channel")), _p(down[wkey]), _p(down["scale"]),
           _p(down.get("s_channel")), _p(codebooks[0]), _p(codebooks[1]), _p(gu), _p(out), H, I, _stream(x))
     return out, ids, weights
+
+def fp8_linear(x, weight, scale):
+    """nn.functional.linear(x, dequantized weight) for an FP8 weight with one bf16 scale per output row, as the CPU
+    path computes it (offload.py:163-167 dequantize_fp8, then the bf16 linear): x [rows, K] bf16 (rows <= 4), weight
+    [N, K] float8_e4m3fn (or its bytes), scale [N] bf16 -> [rows, N] bf16. Each weight is rounded to bf16 after its
+    scale, as the dequantized matrix holds it; sums in float32."""
+    if x.dtype != torch.bfloat16 or scale.dtype != torch.bfloat16:
+        raise TypeError("x and scale must be bfloat16")
+    rows, K = x.shape
+    N = weight.shape[0]
+    if weight.shape != (N, K) or scale.numel() != N:
+        raise ValueError("weight [N, K] and scale [N] expected")
+    x = x.contiguous()
+    w = weight.contiguous().view(torch.uint8)
+    out = torch.empty((rows, N), dtype=torch.bfloat16, device=x.device)
+    _call("d3_gemv_fp8_rows", _p(x), rows, _p(w), _p(scale.contiguous()), _p(out), N, K, _stream(x))
+    return out
+
 
 def decode_codes(qdata, scale, codebook, bits):
     """int8 [R, K]: W4A8 / W6A8 rows decoded to the int8 grid exactly as gemv_codes / grouped_codes decode them

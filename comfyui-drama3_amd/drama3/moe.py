@@ -6,8 +6,14 @@ offload.resident_decode, drama3/offload.py:108-123), for every row of a batch of
 (include/drama3_moe.h, d3_moe_a8). The shared expert and the router's linear stay with the caller, as in the
 reference (model.py:115,123).
 
-Each (device, stream) pair gets a workspace, zeroed once; the kernel leaves it zeroed after every launch, so launches
-on one stream and graph replays reuse it. Allocate it before capturing a graph (`prepare`).
+Each (device, stream) pair gets a workspace, zeroed once and never cleared again: every word the kernel hands from one
+workgroup to another carries the launch's epoch (its dispatch ID plus a salt from its queue), so words a previous
+launch left behind are told apart without a reset, and a graph captured on one stream may be replayed on another.
+Launches that overlap on one workspace race. Allocate it before capturing a graph (`prepare`).
+
+A workgroup that waits for another's result past `spin_limit` polls (one that is not resident because another kernel
+holds part of the device, or a deliberately tiny limit) computes the result itself, bit for bit what the producer
+would have published, so the output stays exact; `status` reports that this happened.
 """
 import ctypes
 import threading
@@ -48,8 +54,13 @@ def prepare(device, H, I, stream=None):
     workspace(device, H, I, stream)
 
 
+STATUS_RECOMPUTED = 1   # a wait gave up and its workgroup computed the missing values itself (the output is exact)
+STATUS_INVALID = 2      # a wait still failed after that: the output of that launch is not valid
+
+
 def status(device, H, I, stream=None):
-    """The workspace's status word (synchronizes): 0, or bit 0 when a wait hit its bound."""
+    """The workspace's status bits since the last call (synchronizes, then clears them): 0, STATUS_RECOMPUTED,
+    STATUS_INVALID."""
     ws = workspace(device, H, I, stream)
     torch.cuda.synchronize(ws.device)
     value = ctypes.c_uint32(0)
@@ -65,11 +76,13 @@ GROUPED_FROM_ROWS = 6
 
 
 def moe_layer(x, logits, gate_up: A8Bank, down: A8Bank, topk, *, routing=False, spin_limit=0, grid=0, out=None,
-              fused=None, item_units=0):
+              fused=None, item_units=0, recompute_all=False):
     """x [M, H] bf16 and router logits [M, E] bf16 (M <= 16) through the routed experts: [M, H] bf16, and with
     `routing` also (ids [M, topk] int64 in descending logit order, weights [M, topk] float32). Fewer than
     GROUPED_FROM_ROWS rows run the fused one-launch kernel (d3_moe_a8), more the grouped path (moe_prefill); `fused`
-    forces either. `item_units` (8 or 16; 0 picks) sets the one-row schedule's hidden units per gate_up workgroup."""
+    forces either. `item_units` (8 or 16; 0 picks) sets the one-row schedule's hidden units per gate_up workgroup.
+    `spin_limit` bounds a workgroup's wait for another's result (0: the library's default; see the module's
+    docstring for what happens past it). `recompute_all` is a test hook: every such wait gives up at once."""
     if fused is None:
         fused = x.shape[0] < GROUPED_FROM_ROWS
     if not fused:
@@ -98,19 +111,20 @@ def moe_layer(x, logits, gate_up: A8Bank, down: A8Bank, topk, *, routing=False, 
         gate_up_scale=gate_up.scale.data_ptr(), down=down.weight.data_ptr(), down_scale=down.scale.data_ptr(),
         out=out.data_ptr(), ids_out=_lib.ptr(ids), weights_out=_lib.ptr(weights), workspace=ws.data_ptr(),
         workspace_bytes=ws.numel(), format=gate_up.fmt, M=M, H=H, I=I, E=E, topk=topk, spin_limit=spin_limit,
-        grid=grid, item_units=item_units)
+        grid=grid, item_units=item_units, recompute_all=int(recompute_all))
     _lib.check(_lib.lib().d3_moe_a8(ctypes.byref(desc), _lib.stream_of(device)), "d3_moe_a8")
     return (out, ids, weights) if routing else out
 
 
 def moe_block(x, gate_up: A8Bank, down: A8Bank, topk, *, router=None, logits=None, shared=None, shared_gate=None,
-              routing=False, return_logits=False, out=None, item_units=0):
+              routing=False, return_logits=False, out=None, item_units=0, spin_limit=0, recompute_all=False):
     """SparseMoeBlock.forward for one decode row (drama3/model.py:107-124) in one launch: x [1, H] bf16 -> [1, H] bf16.
 
     The router: `router` [E, H] bf16 (its logits computed in the launch, model.py:115) or given `logits` [1, E] bf16.
     The shared expert: `shared` = (gate_up, down) A8Banks of one expert in the layer's format and shape, and
     `shared_gate` [H] bf16; it is added as model.py:123 does (both terms bf16). With `routing` also returns ids and
-    weights, with `return_logits` the router's logits [1, E] bf16. `item_units` as for moe_layer."""
+    weights, with `return_logits` the router's logits [1, E] bf16. `item_units`, `spin_limit` and `recompute_all` as
+    for moe_layer."""
     if x.dtype != torch.bfloat16 or x.dim() != 2 or x.shape[0] != 1:
         raise ValueError("x [1, H] bfloat16 expected: the block runs one row")
     H = x.shape[1]
@@ -149,13 +163,13 @@ def moe_block(x, gate_up: A8Bank, down: A8Bank, topk, *, router=None, logits=Non
         x=x.data_ptr(), logits=_lib.ptr(logits), gate_up=gate_up.weight.data_ptr(),
         gate_up_scale=gate_up.scale.data_ptr(), down=down.weight.data_ptr(), down_scale=down.scale.data_ptr(),
         out=out.data_ptr(), ids_out=_lib.ptr(ids), weights_out=_lib.ptr(weights), workspace=ws.data_ptr(),
-        workspace_bytes=ws.numel(), format=gate_up.fmt, M=1, H=H, I=I, E=E, topk=topk, spin_limit=0, grid=0,
+        workspace_bytes=ws.numel(), format=gate_up.fmt, M=1, H=H, I=I, E=E, topk=topk, spin_limit=spin_limit, grid=0,
         router=_lib.ptr(router), logits_out=_lib.ptr(lg_out),
         shared_gate_up=_lib.ptr(sg.weight if sg is not None else None),
         shared_gate_up_scale=_lib.ptr(sg.scale if sg is not None else None),
         shared_down=_lib.ptr(sd.weight if sd is not None else None),
         shared_down_scale=_lib.ptr(sd.scale if sd is not None else None), shared_gate=_lib.ptr(shared_gate),
-        item_units=item_units)
+        item_units=item_units, recompute_all=int(recompute_all))
     _lib.check(_lib.lib().d3_moe_a8(ctypes.byref(desc), _lib.stream_of(device)), "d3_moe_a8")
     res = (out,)
     if routing:

@@ -140,6 +140,10 @@ def routed_decode(x, logits, k, banks, rows, kind, codebooks):
     gate_up launch), else route's own launch and resident_decode."""
     (gate_up, down), (gate_up_rows, down_rows) = banks, rows
     H, I = down_rows, gate_up_rows // 2
+    experts = _rows(kind, gate_up, 1) // gate_up_rows
+    if logits.numel() != experts:
+        raise ValueError(f"{logits.numel()} logits for banks of {experts} experts: a routed id past the banks would be "
+                         f"read out of bounds")
     if (H in (1024, 2048) and I in (512, 768, 1024) and k <= 8 and k <= logits.numel() <= 256
             and x.dtype == torch.bfloat16 and logits.dtype == torch.bfloat16):
         return kernels.resident_decode_routed(x, logits, k, banks, kind, codebooks, H, I)

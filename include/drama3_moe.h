@@ -55,7 +55,8 @@ typedef struct d3_moe_a8_desc {
   int32_t I;               /* expert FFN size: 512 or 768 */
   int32_t E;               /* experts per layer, <= 256 */
   int32_t topk;            /* <= 8 */
-  uint32_t spin_limit;     /* bound on a workgroup's wait for another's result (0: default) */
+  uint32_t spin_limit;     /* polls a workgroup waits for another's result before computing it itself (0: default);
+                            * the output is the same either way (see d3_moe_a8_status) */
   int32_t grid;            /* workgroups (0: as many as the device holds at once, capped by the work) */
   /* The block around the routed experts, SparseMoeBlock.forward (drama3/model.py:107-124), for one row (M = 1, grid
    * 0): with `router` the logits are computed in the launch, bf16(x . router[e]) (model.py:115), and `logits` may be
@@ -71,13 +72,21 @@ typedef struct d3_moe_a8_desc {
   /* One-row schedule (M = 1, grid 0): hidden units per gate_up workgroup, 8 or 16 (0: 8 when the device holds k I / 8
    * workgroups at once, else 16). Both give the same output, bit for bit. */
   int32_t item_units;
+  /* Test hook, never set in production: every wait for another workgroup's result gives up at once, as if the
+   * producer never came, so every waiting workgroup computes what it waited for itself; the output must not change. */
+  int32_t recompute_all;
 } d3_moe_a8_desc;
 
 int64_t d3_moe_a8_workspace_bytes(int32_t M, int32_t topk, int32_t H, int32_t I);
 int d3_moe_a8(const d3_moe_a8_desc* desc, void* stream);
-/* Status word of a workspace after the launches on it completed: 0, or bit 0 if a wait hit spin_limit. Host pointer
- * `status` receives it (synchronous copy). */
-int d3_moe_a8_status(const void* workspace, uint32_t* status);
+/* Status bits of a workspace since the last call, after the launches on it completed (synchronous copies; the bits are
+ * cleared): 0; bit 0 when a wait for another workgroup's result passed spin_limit and the waiting workgroup computed
+ * the result itself (bit for bit what the producer would have published: the output is exact); bit 1 when a wait
+ * still failed after that (that launch's output is not valid). Host pointer `status` receives them.
+ * The workspace carries no state a launch must trust from an earlier one: its hand-off words are tagged with the
+ * launch's epoch (dispatch ID plus a salt from the HSA queue's address), so it may move between streams, a graph
+ * replayed on another stream included. Launches that overlap on one workspace race. */
+int d3_moe_a8_status(void* workspace, uint32_t* status);
 
 /* ---- MoE layer for many rows on A8 banks (prefill, many decode lines) --------------------------------------------
  * Replaces offload.resident_prefill (drama3/offload.py:139-149 -> grouped_int8 / grouped_fp8 / grouped_codes,
@@ -123,6 +132,17 @@ int d3_unpack_rows(int32_t format, const void* rows, int32_t R, int32_t K, void*
 /* d3_cvt_fp8: float -> float8 e4m3fn codes (n a multiple of 4), by the hardware converter the kernels quantize with (hardware 1)
  * or the format-definition conversion (0); round to nearest, ties to even. */
 int d3_cvt_fp8(const float* in, int32_t n, void* out, int32_t hardware, void* stream);
+
+/* ---- FP8 weight with a bf16 scale per output row, bf16 activations ----------------------------------------------
+ * The reference's CPU path for an FP8 weight, dequantize then multiply in bf16: nn.functional.linear(x,
+ * dequantize_fp8(W, scale)) (drama3/offload.py:163-167 dequantize_fp8; the linear as experts_decode, offload.py:192-199,
+ * and FP8Experts.forward's torch branch, offload.py:797-802, run it), with the scale per output row (absmax / 448)
+ * instead of per 128 x 128 block:
+ *   out[r, n] = bf16( sum_k x[r, k] * bf16(e4m3(weight[n, k]) * scale[n]) ),  float32 sums
+ * x [rows, K] bf16 (rows 1..4, 16-byte aligned), weight [N, K] e4m3fn bytes, scale [N] bf16, out [rows, N] bf16;
+ * K one of 512, 1024, 1536, 2048. Any N: k experts' rows stacked are one call (experts_decode's [k * 2I, H]). */
+int d3_gemv_fp8_rows(const void* x, int32_t rows, const void* weight, const void* scale, void* out, int32_t N,
+                     int32_t K, void* stream);
 
 /* ---- The reference's own formats, one kernel per reference kernel (drama3/kernels.py SOURCE) -------------------
  * Float32 activations as in the reference. Slot-cache plans as there: plan [k, 2] int32 = (slot, code) per expert;

@@ -145,17 +145,23 @@ def dequantize(packed, scale_bits, fmt):
 # ------------------------------------------------------------------------------------------------------------- dots
 def group_dots(packed, fmt, act):
     """Per 128-column group dot products of packed rows [R, row_bytes] with activation codes act [C, K]:
-    [R, K / 128, C], int64 exact (I8, W4, W6) or float64 (F8, e4m3 x e4m3)."""
+    [R, K / 128, C], int64 (I8, W4, W6) or float64 (F8, e4m3 x e4m3), exact either way: the sums run in float64
+    (a matrix product per group), which holds them without rounding (int8 x int8 x 128 terms < 2^22; e4m3 products
+    are multiples of 2^-18 below 2^18, 128 of them fit 43 bits), so any order of summation gives the same value."""
     w = codes(packed, fmt)
     R, K = w.shape
     C = act.shape[0]
+    G = K // GROUP
     if fmt == FMT_F8:
-        wv = e4m3_decode(w).astype(np.float64).reshape(R, K // GROUP, GROUP)
-        av = e4m3_decode(act).astype(np.float64).reshape(C, K // GROUP, GROUP)
+        wv = e4m3_decode(w).astype(np.float64)
+        av = e4m3_decode(act).astype(np.float64)
     else:
-        wv = w.astype(np.int64).reshape(R, K // GROUP, GROUP)
-        av = np.asarray(act, dtype=np.int64).reshape(C, K // GROUP, GROUP)
-    return np.einsum("rgk,cgk->rgc", wv, av)
+        wv = w.astype(np.float64)
+        av = np.asarray(act).astype(np.float64)
+    wv = wv.reshape(R, G, GROUP).transpose(1, 0, 2)   # [G, R, 128]
+    av = av.reshape(C, G, GROUP).transpose(1, 2, 0)   # [G, 128, C]
+    dots = np.matmul(wv, av).transpose(1, 0, 2)       # [R, G, C]
+    return dots if fmt == FMT_F8 else np.rint(dots).astype(np.int64)
 
 
 def project(packed, scale_bits, fmt, act_codes, act_scale):
@@ -181,26 +187,40 @@ def expert_output(xq, xs, gu, dn, fmt, I):
     return project(dn[0], dn[1], fmt, hq, hs)[0], h
 
 
-def moe_layer(x_bits, logits_bits, gate_up, down, fmt, topk, fetch):
-    """The fused layer for rows x [M, H] (bf16 bits) and logits [M, E] (bf16 bits).
+def experts_output(xq, xs, gu, dn, fmt, I):
+    """expert_output for C rows of one expert at once (xq [C, H], xs [C]): (out float64 [C, H], hidden [C, I]). Every
+    row's values are those expert_output gives it: the sums are exact and the rest is per row."""
+    y = project(gu[0], gu[1], fmt, xq, xs)  # [C, 2I]
+    g, u = y[:, :I], y[:, I:]
+    h = g / (1.0 + np.exp(-g)) * u
+    hq, hs = quantize_act(h.astype(np.float32), fmt)
+    return project(dn[0], dn[1], fmt, hq, hs), h
+
+
+def moe_layer(x_bits, logits_bits, gate_up, down, fmt, topk, fetch, ids=None, weights=None):
+    """The fused layer for rows x [M, H] (bf16 bits) and logits [M, E] (bf16 bits), or the routing given as ids /
+    weights [M, k] (as Experts.forward receives it, model.py:73).
 
     gate_up / down: (rows, cols) of the banks; fetch(bank, e) -> (packed rows, scale bits) of expert e, so callers can
-    hand over only the experts a test touches. Returns (out bf16 bits [M, H], ids [M, k], weights [M, k],
-    hidden float64 [M, k, I])."""
+    hand over only the experts a test touches. Each expert runs once on all its rows (experts_output). Returns (out
+    bf16 bits [M, H], ids [M, k], weights [M, k], hidden float64 [M, k, I])."""
     x = bf16_bits_to_f32(x_bits)
     M, H = x.shape
-    ids, w = route(logits_bits, topk)
+    if ids is None:
+        ids, w = route(logits_bits, topk)
+    else:
+        ids, w = np.asarray(ids, dtype=np.int64), np.asarray(weights, dtype=np.float32)
     I = down[1]
     xq, xs = quantize_act(x, fmt)
-    out = np.zeros((M, H), dtype=np.float64)
+    parts = np.zeros((M, topk, H), dtype=np.float64)
     hidden = np.zeros((M, topk, I), dtype=np.float64)
-    for m in range(M):
-        acc = 0.0
-        for j in range(topk):
-            e = int(ids[m, j])
-            part, hidden[m, j] = expert_output(xq[m:m + 1], xs[m:m + 1], fetch("gate_up", e), fetch("down", e), fmt, I)
-            acc = acc + float(w[m, j]) * part
-        out[m] = acc
+    for e in np.unique(ids):
+        rows, js = np.nonzero(ids == e)
+        parts[rows, js], hidden[rows, js] = experts_output(xq[rows], xs[rows], fetch("gate_up", int(e)),
+                                                           fetch("down", int(e)), fmt, I)
+    out = np.zeros((M, H), dtype=np.float64)
+    for j in range(topk):  # routing order, as the per-row sum
+        out = out + w[:, j:j + 1].astype(np.float64) * parts[:, j]
     return f32_to_bf16_bits(out.astype(np.float32)), ids, w, hidden
 
 
@@ -223,10 +243,17 @@ def moe_block(x_bits, gate_up, down, fmt, topk, fetch, logits_bits, shared=None,
     x = bf16_bits_to_f32(x_bits)
     xq, xs = quantize_act(x, fmt)
     y, _ = expert_output(xq[0:1], xs[0:1], shared[0], shared[1], fmt, down[1])
-    y = bf16_round(y.astype(np.float32))
-    g = bf16_bits_to_f32(shared_gate_bits).astype(np.float64).reshape(-1)
-    gate = float(np.asarray(bf16_round(np.float32(x[0].astype(np.float64) @ g))).reshape(-1)[0])
-    gw = float(np.asarray(bf16_round(np.float32(1.0 / (1.0 + np.exp(-gate))))).reshape(-1)[0])
-    prod = bf16_round((np.float32(gw) * y).astype(np.float32))
-    out = bf16_bits_to_f32(out_bits).astype(np.float32) + prod
-    return f32_to_bf16_bits(out.astype(np.float32)), ids, w
+    return block_combine(out_bits, f32_to_bf16_bits(y.astype(np.float32))[None, :], x_bits, shared_gate_bits), ids, w
+
+
+def block_combine(routed_bits, shared_bits, x_bits, gate_bits):
+    """model.py:123 on bf16 tensors, rows [M, H]: out = routed + sigmoid(shared_expert_gate(x)) * shared_expert(x),
+    every op rounding to bf16 as torch's bf16 ops do: the gate's linear (float sums, one rounding), its sigmoid, the
+    product with the shared expert's bf16 output, the sum with the routed experts' bf16 output. Returns bf16 bits."""
+    x = bf16_bits_to_f32(x_bits).astype(np.float64)
+    g = bf16_bits_to_f32(gate_bits).astype(np.float64).reshape(-1)
+    gate = bf16_round((x @ g).astype(np.float32))                                      # [M]
+    gw = bf16_round((1.0 / (1.0 + np.exp(-gate.astype(np.float64)))).astype(np.float32))
+    prod = bf16_round((gw[:, None] * bf16_bits_to_f32(shared_bits)).astype(np.float32))
+    out = bf16_bits_to_f32(routed_bits).astype(np.float32) + prod
+    return f32_to_bf16_bits(out.astype(np.float32))

@@ -66,3 +66,10 @@ def grouped_layer(x, ids, weights, gate_up, down, fmt, H, I):
             y = torch.nn.functional.linear(hidden, dequantize_rows(dw, ds, fmt, I)).float()
         out[sel] = y * weights.reshape(-1)[sel].float()[:, None]
     return out.view(T, k, H).sum(1)
+
+
+def fp8_rows_linear(x, weight, scale):
+    """x [rows, K] bf16 times an FP8 weight [N, K] (float8_e4m3fn) with one bf16 scale per output row, dequantized to
+    bf16 on every call and multiplied in bf16 (drama3/offload.py:163-167, then the linear): [rows, N] bf16."""
+    wd = (weight.float() * scale.float()[:, None]).to(torch.bfloat16)
+    return torch.nn.functional.linear(x, wd)

@@ -11,6 +11,9 @@ reference lines it follows. What pins each one (tests/test_oracle_reference.py):
                    bit-plane layout by planting single codes
   gemv_*_ref       brute-force float64 dot products of the decoded rows; plan / fill / late / took_over semantics on
                    hand-built cases
+  fp8_rows_*       the dequantized matrix bit for bit against torch's float8 decode, product and bf16 cast; the
+                   linear against torch's bf16 linear on the CPU (within one bf16 step) and an unquantized float64
+                   product (within the format's error); a planted transposed scale must fail
   grouped_ref      equal to gemv_*_ref row by row
   resident_*_ref   against an unquantized float64 layer within the formats' quantization error, and a planted
                    gate / up swap that must fail
@@ -148,6 +151,33 @@ def fp8_rows(weight, scale):
     kernels.py's decode)."""
     R, C = weight.shape
     return e4m3_ref(weight) * np.repeat(np.repeat(np.asarray(scale, np.float64), FP8_BLOCK, 0), FP8_BLOCK, 1)[:R, :C]
+
+
+def quantize_fp8_rows(w):
+    """Float weights [N, K] -> (e4m3 codes [N, K], bf16 scale bits [N]) with one scale per output row, absmax / 448
+    rounded to bf16, codes = e4m3(w / scale) (round to nearest even)."""
+    w = np.asarray(w, dtype=np.float32)
+    sbits = f32_to_bf16_bits(np.abs(w).max(axis=1) / np.float32(448.0))
+    s = bf16_bits_to_f32(sbits)
+    s = np.where(s == 0, np.float32(1), s).astype(np.float32)
+    return e4m3_encode((w / s[:, None]).astype(np.float32)), f32_to_bf16_bits(s)
+
+
+def fp8_rows_dequant(codes, scale_bits):
+    """The dequantized weight the CPU path multiplies with, as bf16 values (float32 [N, K]): e4m3(code) * scale, each
+    product (exact in float32) rounded to bf16 (offload.py:163-167's .to(dtype), the scale per row)."""
+    s = bf16_bits_to_f32(scale_bits).astype(np.float32)
+    v = (e4m3_ref(codes).astype(np.float32) * s[:, None]).astype(np.float32)
+    return bf16_bits_to_f32(f32_to_bf16_bits(v))
+
+
+def fp8_rows_linear_ref(x_bits, codes, scale_bits):
+    """nn.functional.linear(x, dequantized weight) in bf16 for x [rows, K] (bf16 bits): float64 sums of the bf16
+    inputs, one rounding to bf16 (the CPU's bf16 matmul sums in float32, so within one bf16 step of this).
+    Returns bf16 bits [rows, N]."""
+    x = bf16_bits_to_f32(x_bits).astype(np.float64)
+    wd = fp8_rows_dequant(codes, scale_bits).astype(np.float64)
+    return f32_to_bf16_bits((x @ wd.T).astype(np.float32))
 
 
 def gemv_fp8_ref(x, ids, plan, slot_fields, host_fields, n):

@@ -198,7 +198,8 @@ def test_layer_reference_shape_256_experts(fmt, M):
 
 
 def test_repeated_launches_are_identical():
-    """The kernel leaves its workspace as it found it: back-to-back launches give identical results."""
+    """Back-to-back launches on one workspace (its words tagged with each launch's epoch, never cleared) give identical
+    results."""
     gate_up, down = layer_banks(formats.FMT_I8)
     gen = torch.Generator(device=DEV).manual_seed(9)
     x = torch.randn((4, 2048), generator=gen, device=DEV).to(torch.bfloat16)
@@ -239,6 +240,96 @@ def test_graph_replay_matches_eager():
         assert torch.equal(static_out, eager)
         _ = chain(x0.clone())  # eager work between replays
     assert moe.status(DEV, 2048, 768, stream) == 0
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+@pytest.mark.parametrize("M", [1, 3, 5])
+def test_wait_give_up_recomputes(fmt, M):
+    """A wait for another workgroup's result that gives up leaves the output exact: the waiting workgroup computes
+    what it waited for itself (the chunk's gate_up items; at 3 and 5 rows also the other chunks' partial outputs of its
+    block). Forced from the host with recompute_all (every wait gives up at once, so every down workgroup takes the
+    recovery path) and with spin_limit 1 (waits that find a stale word give up after one more read). Every kernel
+    exits; the output is the normal launch's bit for bit; the status records the recomputation and never an invalid
+    launch; a normal launch on the same workspace afterwards is unaffected (a give-up belongs to its own launch)."""
+    gate_up, down = layer_banks(fmt)
+    gen = torch.Generator(device=DEV).manual_seed(300 + M)
+    x = torch.randn((M, 2048), generator=gen, device=DEV).to(torch.bfloat16)
+    logits = torch.randn((M, 128), generator=gen, device=DEV).to(torch.bfloat16)
+    moe.status(DEV, 2048, 768)  # clears the bits
+    normal = check_layer(fmt, x, logits, gate_up, down)
+    forced = moe.moe_layer(x, logits, gate_up, down, 8, fused=True, recompute_all=True)
+    torch.cuda.synchronize()
+    assert moe.status(DEV, 2048, 768) == moe.STATUS_RECOMPUTED
+    assert torch.equal(forced, normal)
+    for _ in range(2):
+        tiny = moe.moe_layer(x, logits, gate_up, down, 8, fused=True, spin_limit=1)
+        torch.cuda.synchronize()
+        assert moe.status(DEV, 2048, 768) & moe.STATUS_INVALID == 0
+        assert torch.equal(tiny, normal)
+    again = moe.moe_layer(x, logits, gate_up, down, 8, fused=True)
+    torch.cuda.synchronize()
+    assert moe.status(DEV, 2048, 768) == 0
+    assert torch.equal(again, normal)
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+@pytest.mark.parametrize("E,inter,units", [(128, 768, 16), (256, 512, 8)])
+def test_block_wait_give_up_recomputes(fmt, E, inter, units):
+    """The block (router, routed experts, shared expert) with every wait given up at once (recompute_all): the
+    routing waves compute the router logits themselves, the down blocks the gate_up items and the shared expert's
+    output rows, the shared expert's blocks its gate_up items. Same output as the normal launch, bit for bit, with
+    16-unit items (the headline shape, whose block does not fit 8-unit items) and 8-unit ones (the reference model's
+    shape); spin_limit 1 as well."""
+    gate_up, down, x, router, (sg, sd), g = block_inputs(fmt, 33, E=E, I=inter)
+    moe.status(DEV, 2048, inter)
+    normal = moe.moe_block(x, gate_up, down, 8, router=router, shared=(sg, sd), shared_gate=g, item_units=units)
+    torch.cuda.synchronize()
+    assert moe.status(DEV, 2048, inter) == 0
+    forced = moe.moe_block(x, gate_up, down, 8, router=router, shared=(sg, sd), shared_gate=g, item_units=units,
+                           recompute_all=True)
+    torch.cuda.synchronize()
+    assert moe.status(DEV, 2048, inter) == moe.STATUS_RECOMPUTED
+    assert torch.equal(forced, normal)
+    tiny = moe.moe_block(x, gate_up, down, 8, router=router, shared=(sg, sd), shared_gate=g, item_units=units,
+                         spin_limit=1)
+    torch.cuda.synchronize()
+    assert moe.status(DEV, 2048, inter) & moe.STATUS_INVALID == 0
+    assert torch.equal(tiny, normal)
+
+
+def test_graph_replayed_on_another_stream():
+    """A graph captured on one stream and replayed on another (torch replays on the current stream), interleaved with
+    eager launches on a third: the launch epochs carry their queue's salt, so no launch takes another queue's leftover
+    words for its own. Every replay equals the eager chain."""
+    gate_up, down = layer_banks(formats.FMT_W4)
+    gen = torch.Generator(device=DEV).manual_seed(11)
+    x0 = torch.randn((1, 2048), generator=gen, device=DEV).to(torch.bfloat16)
+    logits = [torch.randn((1, 128), generator=gen, device=DEV).to(torch.bfloat16) for _ in range(4)]
+
+    def chain(x):
+        for lg in logits:
+            x = moe.moe_layer(x, lg, gate_up, down, 8)
+        return x
+
+    eager = chain(x0.clone())
+    static_x = x0.clone()
+    capture, replay = torch.cuda.Stream(DEV), torch.cuda.Stream(DEV)
+    capture.wait_stream(torch.cuda.current_stream(DEV))
+    with torch.cuda.stream(capture):
+        moe.prepare(DEV, 2048, 768, capture)
+        chain(static_x)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=capture):
+            static_out = chain(static_x)
+    torch.cuda.synchronize()
+    for _ in range(4):
+        with torch.cuda.stream(replay):
+            graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(static_out, eager)
+        assert torch.equal(chain(x0.clone()), eager)
+        torch.cuda.synchronize()
+    assert moe.status(DEV, 2048, 768, capture) & moe.STATUS_INVALID == 0
 
 
 @pytest.mark.parametrize("M", [1, 3, 4, 5, 6, 16])

@@ -169,3 +169,45 @@ def test_prefill_graph_replays(rows):
         eager = moe.moe_prefill(x_buf, gate_up, down, 8, logits=lg_buf)
         torch.cuda.synchronize()
         assert torch.equal(out, eager)
+
+
+def zipf_logits(T, E, seed):
+    """Router logits [T, E] bf16 drawn as bench.py draws config 5's: log p(rank) with p(rank) ~ rank^-1.1 over a seeded
+    permutation of the experts, plus Gumbel noise, so each row's top-k is k distinct experts drawn from Zipf(1.1)."""
+    gen = torch.Generator(device=DEV).manual_seed(seed)
+    logp = -1.1 * torch.log(torch.arange(1, E + 1, device=DEV, dtype=torch.float32))
+    perm = torch.randperm(E, generator=gen, device=DEV)
+    base = torch.empty(E, device=DEV)
+    base[perm] = logp
+    u = torch.rand((T, E), generator=gen, device=DEV).clamp_(1e-12, 1 - 1e-7)
+    return (base - torch.log(-torch.log(u))).to(torch.bfloat16)
+
+
+def test_prefill_fp8_256_rows_zipf():
+    """The prefill workload the benchmark times: 256 rows, FP8 experts at H 2048 / I 768, 128 experts, top-8 from
+    Zipf(1.1)-skewed logits. The hottest expert holds more than 128 (row, expert) pairs, so it is split into 64-pair
+    work units (at least 3) that share its weight reads; every one of the 256 rows is checked against the oracle."""
+    gate_up, down = banks(formats.FMT_F8, E=128, seed=7)
+    gen = torch.Generator(device=DEV).manual_seed(70)
+    x = torch.randn((256, H), generator=gen, device=DEV).to(torch.bfloat16)
+    logits = zipf_logits(256, 128, seed=71)
+    out, ids, w = check(formats.FMT_F8, x, logits, gate_up, down)
+    counts = np.bincount(ids.cpu().numpy().ravel(), minlength=128)
+    assert counts.max() > 128, counts.max()
+    assert (counts > 0).sum() > 100  # most experts in use, as at this workload
+
+
+@pytest.mark.parametrize("fmt,E,inter,T", [(formats.FMT_I8, 128, 768, 200), (formats.FMT_W4, 128, 768, 260),
+                                           (formats.FMT_W6, 256, 512, 160)])
+def test_prefill_experts_over_many_units(fmt, E, inter, T):
+    """Rows biased onto a few experts: two experts take 150 to 260 pairs (3 to 5 work units of 64 pairs each), the
+    rest spread; against the oracle on every row."""
+    gate_up, down = banks(fmt, E=E, inter=inter, seed=8)
+    gen = torch.Generator(device=DEV).manual_seed(80 + fmt)
+    x = torch.randn((T, H), generator=gen, device=DEV).to(torch.bfloat16)
+    logits = torch.randn((T, E), generator=gen, device=DEV)
+    logits[:, 5] += 20.0
+    logits[: 150, E - 3] += 20.0
+    out, ids, w = check(fmt, x, logits.to(torch.bfloat16), gate_up, down)
+    counts = np.bincount(ids.cpu().numpy().ravel(), minlength=E)
+    assert counts[5] == T and counts[E - 3] >= 150

@@ -350,9 +350,13 @@ def test_resident_decode(layer):
                                       (200, 8, True)])
 def test_resident_decode_routed(layer, n, k, ties):
     """Routing inside the gate_up launch: ids and weights equal kernels.route's and the oracle's route_ref, and the
-    output equals route + resident_decode bitwise. Logits past the first E experts sit far below the rest, so the
-    banks' E experts are the ones routed to, while the launch still ranks all n."""
+    output equals route + resident_decode bitwise. With n > E the banks are padded to n experts (zeros) and the logits
+    past the first E sit far below the rest, so the E real experts are the ones routed to while the launch ranks all
+    n."""
     kind, banks, cbs, dbanks, dcbs = layer
+    if n > E:
+        dbanks = [{name: torch.cat([t, t.new_zeros((t.shape[0] // E * (n - E), *t.shape[1:]))]) for name, t in b.items()}
+                  for b in dbanks]
     rng = np.random.default_rng(13 + n + k)
     x = numerics.f32_to_bf16_bits(rng.standard_normal((1, H)).astype(np.float32))
     lf = rng.integers(-2, 3, n).astype(np.float32) if ties else rng.standard_normal(n).astype(np.float32)
@@ -370,6 +374,15 @@ def test_resident_decode_routed(layer, n, k, ties):
     assert torch.equal(out.view(torch.int16), want.view(torch.int16))
     assert_bf16_close(bits_of(out), ref.resident_decode_ref(x, ids.cpu().numpy()[0], w.cpu().numpy()[0], banks,
                                                             (2 * I, H), kind, cbs))
+
+def test_resident_decode_routed_rejects_logits_past_the_banks(layer):
+    """More logits than the banks hold experts: a routed id could index past them, so the call is refused."""
+    kind, banks, cbs, dbanks, dcbs = layer
+    x = torch.zeros((1, H), dtype=torch.bfloat16, device=DEV)
+    lg = torch.zeros((E + 8,), dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(ValueError, match="logits for banks of"):
+        offload.routed_decode(x, lg, 4, dbanks, (2 * I, H), kind, dcbs)
+
 
 def test_resident_prefill(layer):
     kind, banks, cbs, dbanks, dcbs = layer
@@ -433,3 +446,40 @@ def test_resident_decode_graph_replays(layer):
         eager = offload.resident_decode(x_buf, ids_buf, w, dbanks, (2 * I, H), kind, dcbs)
         torch.cuda.synchronize()
         assert torch.equal(out, eager)
+
+
+@pytest.mark.parametrize("rows,N,K", [(1, 1536, 2048), (3, 1536, 2048), (1, 8 * 1536, 2048), (2, 1024, 512),
+                                      (4, 64, 1536)])
+def test_fp8_linear_per_row_scale(rows, N, K):
+    """An FP8 weight with a bf16 scale per output row (absmax / 448) against bf16 activations, dequantized to bf16 then
+    multiplied, as the CPU path runs it (offload.py:163-167, then the linear). The first case is the benchmark's single
+    GEMV: x [1, 2048] ~ N(0, 1), W [1536, 2048] ~ N(0, 0.02), seed 0; the third stacks 8 experts' rows (one call for
+    experts_decode's gate_up). Every output within one bf16 step of the oracle's float64 sums (the kernel sums in
+    float32 in its own order), and nearly all identical."""
+    bf16_bits_to_f32 = numerics.bf16_bits_to_f32
+    rng = np.random.default_rng(0)
+    x = numerics.f32_to_bf16_bits(rng.standard_normal((rows, K)).astype(np.float32))
+    w = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+    codes, sbits = ref.quantize_fp8_rows(w)
+    xt = torch.from_numpy(x.view(np.int16)).view(torch.bfloat16).to(DEV)
+    wt = torch.from_numpy(codes).to(DEV)
+    st = torch.from_numpy(sbits.view(np.int16)).view(torch.bfloat16).to(DEV)
+    got = kernels.fp8_linear(xt, wt, st)
+    assert got.shape == (rows, N) and got.dtype == torch.bfloat16
+    gv = bf16_bits_to_f32(got.view(torch.int16).cpu().numpy().view(np.uint16)).astype(np.float64)
+    want = bf16_bits_to_f32(ref.fp8_rows_linear_ref(x, codes, sbits)).astype(np.float64)
+    # one bf16 step of v is at most 2^-7 |v| (2^(e-7) for v in [2^e, 2^(e+1)))
+    assert np.all(np.abs(gv - want) <= 2.0 ** -7 * np.abs(want) + 1e-6), np.abs(gv - want).max()
+    assert (gv == want).mean() >= 0.97
+    # the float8 view of the weight is taken as well as its bytes
+    assert torch.equal(kernels.fp8_linear(xt, wt.view(torch.float8_e4m3fn), st), got)
+
+
+def test_fp8_linear_rejects_bad_shapes():
+    x = torch.zeros((5, 2048), dtype=torch.bfloat16, device=DEV)
+    w = torch.zeros((16, 2048), dtype=torch.uint8, device=DEV)
+    s = torch.ones((16,), dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(RuntimeError, match="rows must be"):
+        kernels.fp8_linear(x, w, s)
+    with pytest.raises(RuntimeError, match="K must be"):
+        kernels.fp8_linear(x[:1, :768].contiguous(), w[:, :768].contiguous(), s)

@@ -6,7 +6,7 @@ import pytest
 import torch
 
 from drama3 import formats
-from oracle import a8
+from oracle import a8, numerics
 from oracle.numerics import bf16_bits_to_f32, e4m3_decode, f32_to_bf16_bits
 
 FMTS = [a8.FMT_I8, a8.FMT_W4, a8.FMT_W6, a8.FMT_F8]
@@ -176,3 +176,53 @@ def test_layer_gate_up_order_matters():
     bad, *_ = a8.moe_layer(x, logits, (2 * I, H), (H, I), a8.FMT_I8, k, fetch(swapped))
     a, b = bf16_bits_to_f32(out), bf16_bits_to_f32(bad)
     assert np.linalg.norm(a - b) / np.linalg.norm(a) > 0.3
+
+
+# ------------------------------------------------------------------------------------------------------------ block
+def _bf16(a):
+    return torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).view(torch.bfloat16)
+
+
+def _bits_of(t):
+    return t.contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def test_router_logits_against_torch_bf16_linear():
+    """a8.router_logits is model.py:115's bf16 linear: torch's CPU bf16 linear gives the same bits on nearly every
+    logit (its float32 sums in another order may cross a rounding boundary) and stays within one bf16 step; with the
+    router's rows transposed (a planted index mistake) it does not."""
+    rng = np.random.default_rng(3)
+    x = numerics.f32_to_bf16_bits(rng.standard_normal((16, 2048)).astype(np.float32))
+    r = numerics.f32_to_bf16_bits((rng.standard_normal((128, 2048)) * 0.02).astype(np.float32))
+    got = numerics.bf16_bits_to_f32(a8.router_logits(x, r)).astype(np.float64)
+    lib = torch.nn.functional.linear(_bf16(x), _bf16(r)).float().numpy().astype(np.float64)
+    assert np.all(np.abs(got - lib) <= 2.0 ** -7 * np.abs(lib) + 1e-6)
+    assert (got == lib).mean() >= 0.98
+    planted = numerics.bf16_bits_to_f32(a8.router_logits(x, r.reshape(2048, 128).T.copy().reshape(128, 2048)))
+    assert (planted.astype(np.float64) == lib).mean() < 0.1
+
+
+def test_block_combine_against_torch_bf16_ops():
+    """a8.block_combine is model.py:123 evaluated by torch on bf16 tensors: out + sigmoid(gate(x)) * shared(x). Same
+    bits on nearly every element; taking the sigmoid of the gate before its bf16 rounding (a planted mistake) or
+    skipping the product's rounding changes many more."""
+    rng = np.random.default_rng(4)
+    M, H = 64, 2048
+    x = numerics.f32_to_bf16_bits(rng.standard_normal((M, H)).astype(np.float32))
+    g = numerics.f32_to_bf16_bits((rng.standard_normal(H) * 0.05).astype(np.float32))
+    routed = numerics.f32_to_bf16_bits((rng.standard_normal((M, H)) * 0.1).astype(np.float32))
+    shared = numerics.f32_to_bf16_bits((rng.standard_normal((M, H)) * 0.1).astype(np.float32))
+    got = a8.block_combine(routed, shared, x, g)
+    gate = torch.nn.functional.linear(_bf16(x), _bf16(g)[None, :])                  # [M, 1] bf16
+    lib = _bits_of(_bf16(routed) + torch.sigmoid(gate) * _bf16(shared))
+    same = (got == lib).mean()
+    assert same >= 0.99, same
+    gv, lv = numerics.bf16_bits_to_f32(got), numerics.bf16_bits_to_f32(lib)
+    assert np.all(np.abs(gv - lv) <= 2.0 ** -7 * np.abs(lv) + 1e-6)
+    # planted: the sigmoid of the unrounded float gate, the product unrounded
+    xf = numerics.bf16_bits_to_f32(x).astype(np.float64)
+    gf = numerics.bf16_bits_to_f32(g).astype(np.float64)
+    gw = (1.0 / (1.0 + np.exp(-(xf @ gf)))).astype(np.float32)
+    wrong = numerics.f32_to_bf16_bits((numerics.bf16_bits_to_f32(routed) +
+                                       gw[:, None] * numerics.bf16_bits_to_f32(shared)).astype(np.float32))
+    assert (wrong == lib).mean() < same - 0.05

@@ -266,3 +266,41 @@ def test_resident_prefill_ref_equals_decode_per_row():
         one = ref.resident_decode_ref(x[t:t + 1], idx[t], w[t], banks, (512, 256), "int8", cbs)
         a, b = numerics.bf16_bits_to_f32(got[t]), numerics.bf16_bits_to_f32(one[0])
         assert np.all(np.abs(a - b) <= 2.0 ** -7 * np.abs(b) + 1e-6)
+
+
+# ------------------------------------------------------------------------------------------- FP8 rows (config 1)
+def _fp8_rows_case(N=96, K=512, seed=0):
+    rng = np.random.default_rng(seed)
+    x = numerics.f32_to_bf16_bits(rng.standard_normal((2, K)).astype(np.float32))
+    w = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+    codes, sbits = ref.quantize_fp8_rows(w)
+    return x, w, codes, sbits
+
+
+def test_fp8_rows_dequant_matches_torch_bit_for_bit():
+    """The dequantized bf16 matrix equals torch's: float8 decode, float32 product with the scale, bf16 cast."""
+    _, _, codes, sbits = _fp8_rows_case()
+    got = ref.fp8_rows_dequant(codes, sbits)
+    wt = torch.from_numpy(codes).view(torch.float8_e4m3fn).float()
+    st = torch.from_numpy(sbits.view(np.int16)).view(torch.bfloat16).float()
+    want = (wt * st[:, None]).to(torch.bfloat16).float().numpy()
+    assert np.array_equal(got, want)
+    # the scale is absmax / 448 rounded to bf16: every row's largest code sits at the top of the e4m3 range
+    assert np.all(np.abs(ref.e4m3_ref(codes)).max(axis=1) >= 416.0)
+
+
+def test_fp8_rows_linear_against_torch_and_unquantized():
+    """Within one bf16 step of torch's bf16 linear on the CPU (float32 sums in another order), within the format's
+    error of the unquantized float64 product; rows scaled by their neighbours' scales fail that bar."""
+    x, w, codes, sbits = _fp8_rows_case()
+    got = numerics.bf16_bits_to_f32(ref.fp8_rows_linear_ref(x, codes, sbits)).astype(np.float64)
+    xt = torch.from_numpy(x.view(np.int16)).view(torch.bfloat16)
+    wd = torch.from_numpy(ref.fp8_rows_dequant(codes, sbits)).to(torch.bfloat16)
+    lib = torch.nn.functional.linear(xt, wd).float().numpy().astype(np.float64)
+    assert np.all(np.abs(got - lib) <= 2.0 ** -7 * np.abs(lib) + 1e-6)
+    exact = numerics.bf16_bits_to_f32(x).astype(np.float64) @ w.astype(np.float64).T
+    rel = np.linalg.norm(got - exact) / np.linalg.norm(exact)
+    assert rel < 0.05, rel
+    # a planted mistake: each row scaled by its neighbour's scale
+    planted = numerics.bf16_bits_to_f32(ref.fp8_rows_linear_ref(x, codes, np.roll(sbits, 1))).astype(np.float64)
+    assert np.linalg.norm(planted - exact) / np.linalg.norm(exact) > 2 * rel
