@@ -1381,9 +1381,47 @@ int hip_fail(hipError_t err, const char* what) {
 
 // the header, then (pairs + 1 for the shared expert) hidden rows and tile maxima, the pairs' partial outputs, and for
 // the block's router and shared expert MAX_E logit words and H output words
-int64_t moe_a8_workspace_bytes(int M, int topk, int H, int I) {
-  const int64_t pairs = (int64_t)M * topk;
-  return SYNC_WORDS * 4 + (pairs + 1) * I * 8 + (pairs + 1) * (I / 8) * 8 + pairs * H * 8 + (MAX_E + H) * 8;
+__host__ __device__ constexpr int64_t moe_a8_workspace_bytes(int M, int topk, int H, int I) {
+  return SYNC_WORDS * 4 + ((int64_t)M * topk + 1) * I * 8 + ((int64_t)M * topk + 1) * (I / 8) * 8 +
+         (int64_t)M * topk * H * 8 + (int64_t)(MAX_E + H) * 8;
+}
+
+// ---- The entry that allocates nothing (d3_moe_a8_noalloc) -----------------------------------------------------------
+// Its workspace is this file-scope array, one copy per GPU, sized for the largest layer the fused kernels take: 16
+// rows, top-8, H 2048, I 768 (3.0 MB). In host code `scratch` names a host-side stand-in, not device memory: the
+// device address comes from hipGetSymbolAddress, once per device (scratch_on), and only that address is used.
+constexpr int64_t SCRATCH_BYTES = moe_a8_workspace_bytes(MAX_M, MAX_K, 2048, 768);
+static __device__ __align__(256) uint8_t scratch[SCRATCH_BYTES];
+
+// zeroes n bytes (a multiple of 16) at p: the workspace's words must start with tag 0, which no epoch equals
+__global__ void __launch_bounds__(256) fill_zero_kernel(uint4* p, int64_t n16) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n16; i += (int64_t)gridDim.x * 256)
+    p[i] = uint4{0u, 0u, 0u, 0u};
+}
+
+constexpr int MAX_DEVICES = 64;
+
+// The current device's copy of `scratch`: its address from hipGetSymbolAddress (checked), on the first call on the
+// device also zeroed by a fill kernel on `stream` (a kernel, so that a caller capturing a graph records no memset
+// node). Returns nullptr and sets the error on failure.
+void* scratch_on(hipStream_t stream, int* err) {
+  static std::mutex mu;
+  static void* ptrs[MAX_DEVICES] = {};
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) { *err = hip_fail(e, "hipGetDevice"); return nullptr; }
+  if (dev < 0 || dev >= MAX_DEVICES) { *err = fail("d3_moe_a8_noalloc: device index beyond 64"); return nullptr; }
+  std::lock_guard<std::mutex> lock(mu);
+  if (!ptrs[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) { *err = hip_fail(e, "d3_moe_a8_noalloc: hipGetSymbolAddress"); return nullptr; }
+    hipLaunchKernelGGL(fill_zero_kernel, dim3(768), dim3(256), 0, stream, (uint4*)p, SCRATCH_BYTES / 16);
+    e = hipGetLastError();
+    if (e != hipSuccess) { *err = hip_fail(e, "d3_moe_a8_noalloc: clearing the workspace"); return nullptr; }
+    ptrs[dev] = p;
+  }
+  return ptrs[dev];
 }
 
 using KernelFn = void (*)(MoeA8Args);
@@ -1548,6 +1586,21 @@ int64_t d3_moe_a8_workspace_bytes(int32_t M, int32_t topk, int32_t H, int32_t I)
 }
 
 int d3_moe_a8(const d3_moe_a8_desc* desc, void* stream) { return d3::launch_moe_a8(desc, (hipStream_t)stream); }
+
+int d3_moe_a8_noalloc(const d3_moe_a8_desc* desc, void* stream) {
+  if (!desc) return d3::fail("d3_moe_a8_noalloc: null descriptor");
+  const int64_t need = d3::moe_a8_workspace_bytes(desc->M, desc->topk, desc->H, desc->I);
+  if (desc->M < 1 || desc->topk < 1 || desc->H < 1 || desc->I < 1 || need > d3::SCRATCH_BYTES)
+    return d3::fail("d3_moe_a8_noalloc: the layer needs " + std::to_string(need) + " bytes of workspace, more than the " +
+                    std::to_string(d3::SCRATCH_BYTES) + " of the static one (at most 16 rows, top-8, H 2048, I 768)");
+  int err = 0;
+  void* ws = d3::scratch_on((hipStream_t)stream, &err);
+  if (!ws) return err;
+  d3_moe_a8_desc d = *desc;
+  d.workspace = ws;
+  d.workspace_bytes = d3::SCRATCH_BYTES;
+  return d3::launch_moe_a8(&d, (hipStream_t)stream);
+}
 
 int d3_moe_a8_status(void* workspace, uint32_t* status) {
   if (!workspace || !status) return d3::fail("d3_moe_a8_status: null pointer");

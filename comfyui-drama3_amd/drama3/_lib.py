@@ -49,6 +49,7 @@ SIGNATURES = {
     "d3_version": (c_int32, []),
     "d3_moe_a8_workspace_bytes": (c_int64, [c_int32, c_int32, c_int32, c_int32]),
     "d3_moe_a8": (c_int32, [ctypes.POINTER(MoeA8Desc), c_void_p]),
+    "d3_moe_a8_noalloc": (c_int32, [ctypes.POINTER(MoeA8Desc), c_void_p]),
     "d3_moe_a8_status": (c_int32, [c_void_p, ctypes.POINTER(c_uint32)]),
     "d3_moe_a8_prefill_workspace_bytes": (c_int64, [c_int32, c_int32, c_int32, c_int32, c_int32]),
     "d3_moe_a8_prefill": (c_int32, [ctypes.POINTER(MoeA8PrefillDesc), c_void_p]),

@@ -79,6 +79,13 @@ typedef struct d3_moe_a8_desc {
 
 int64_t d3_moe_a8_workspace_bytes(int32_t M, int32_t topk, int32_t H, int32_t I);
 int d3_moe_a8(const d3_moe_a8_desc* desc, void* stream);
+/* d3_moe_a8 without a caller's workspace, allocating nothing: no counterpart in the reference. For callers that cannot
+ * allocate (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). The workspace is a
+ * static device array of the library, one per GPU, of 3,007,744 bytes: layers up to 16 rows, top-8, H 2048, I 768
+ * (d3_moe_a8_workspace_bytes of the layer must fit, else D3_EINVAL). desc->workspace and workspace_bytes are ignored.
+ * The first call on a device looks the array up and clears it with a kernel on `stream`. Every call on a GPU shares
+ * that GPU's array: calls that overlap on one GPU race; calls in sequence, on any streams, do not. */
+int d3_moe_a8_noalloc(const d3_moe_a8_desc* desc, void* stream);
 /* Status bits of a workspace since the last call, after the launches on it completed (synchronous copies; the bits are
  * cleared): 0; bit 0 when a wait for another workgroup's result passed spin_limit and the waiting workgroup computed
  * the result itself (bit for bit what the producer would have published: the output is exact); bit 1 when a wait

@@ -1,0 +1,64 @@
+"""The entry point that allocates nothing (d3_moe_a8_noalloc): the fused layer with its workspace in a static device
+array of the library, against d3_moe_a8 with a workspace the caller allocated, bit for bit, on two calls in a row
+(the second a smaller layer), and its refusal of a layer larger than the static workspace."""
+import ctypes
+
+import pytest
+import torch
+
+from drama3 import _lib, formats, moe
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda:0")
+
+
+def _noalloc():
+    return _lib.lib().d3_moe_a8_noalloc
+
+
+def _banks(fmt, E, I, seed):
+    gen = torch.Generator(device=DEV).manual_seed(seed)
+    gate_up = formats.quantize(torch.randn((E, 2 * I, 2048), generator=gen, device=DEV) * 0.02, fmt)
+    down = formats.quantize(torch.randn((E, 2048, I), generator=gen, device=DEV) * 0.02, fmt)
+    return gate_up, down
+
+
+def _call(fn, x, logits, gate_up, down, topk, I, E):
+    M = x.shape[0]
+    out = torch.empty((M, 2048), dtype=torch.bfloat16, device=DEV)
+    ids = torch.empty((M, topk), dtype=torch.int64, device=DEV)
+    weights = torch.empty((M, topk), dtype=torch.float32, device=DEV)
+    desc = _lib.MoeA8Desc(
+        x=x.data_ptr(), logits=logits.data_ptr(), gate_up=gate_up.weight.data_ptr(),
+        gate_up_scale=gate_up.scale.data_ptr(), down=down.weight.data_ptr(), down_scale=down.scale.data_ptr(),
+        out=out.data_ptr(), ids_out=ids.data_ptr(), weights_out=weights.data_ptr(), workspace=None,
+        workspace_bytes=0, format=gate_up.fmt, M=M, H=2048, I=I, E=E, topk=topk)
+    rc = fn(ctypes.byref(desc), _lib.stream_of(DEV))
+    return rc, out, ids, weights
+
+
+def test_noalloc_matches_the_allocating_entry():
+    fn = _noalloc()
+    cases = [(formats.FMT_W4, 4, 768, 128, 1), (formats.FMT_I8, 1, 512, 256, 2)]  # the second call: a smaller layer
+    for fmt, M, I, E, seed in cases:
+        gate_up, down = _banks(fmt, E, I, seed)
+        gen = torch.Generator(device=DEV).manual_seed(10 + seed)
+        x = torch.randn((M, 2048), generator=gen, device=DEV).to(torch.bfloat16)
+        logits = torch.randn((M, E), generator=gen, device=DEV).to(torch.bfloat16)
+        want, want_ids, want_w = moe.moe_layer(x, logits, gate_up, down, 8, routing=True, fused=True)
+        rc, out, ids, weights = _call(fn, x, logits, gate_up, down, 8, I, E)
+        _lib.check(rc, "d3_moe_a8_noalloc")
+        torch.cuda.synchronize()
+        assert torch.equal(out, want)
+        assert torch.equal(ids, want_ids) and torch.equal(weights, want_w)
+
+
+def test_noalloc_rejects_layers_beyond_its_workspace():
+    fn = _noalloc()
+    gate_up, down = _banks(formats.FMT_I8, 8, 512, 3)
+    x = torch.zeros((16, 2048), dtype=torch.bfloat16, device=DEV)
+    logits = torch.zeros((16, 8), dtype=torch.bfloat16, device=DEV)
+    # 16 rows at I 1024: more workspace than the static array holds (refused before any launch)
+    rc, *_ = _call(fn, x, logits, gate_up, down, 8, 1024, 8)
+    assert rc != 0
+    assert "static one" in _lib.lib().d3_last_error().decode()
