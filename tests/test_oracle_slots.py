@@ -95,3 +95,36 @@ def test_await_ref():
     assert np.all(out == 0) and took == 1
     out, took = slots.await_ref(plan_gpu, 6, 7, res)
     assert np.all(out == 0) and took == 0
+
+
+def test_slots_taken_are_the_smallest_keys_in_routing_order():
+    """Taking a slot takes only that slot out of the candidates (its new owner is an expert of this layer), so the
+    slots a call hands out are the n smallest (decayed count, slot) keys among the slots that may be taken, free
+    slots first, in the order of the experts that need one. The device kernel selects them that way; here the
+    oracle's sequential scans are checked against it on random traces."""
+    rng = np.random.default_rng(11)
+    for trial in range(200):
+        L, E = int(rng.integers(1, 5)), int(rng.integers(8, 64))
+        k = int(rng.integers(1, min(9, E)))
+        st = slots.new_state(L, E, int(rng.integers(1, 3 * E)), budget=(int(rng.integers(0, 4)), 2))
+        cpu, share = int(rng.integers(0, 2)), float(rng.choice([0.0, 0.5]))
+        for _ in range(6):
+            for layer in range(L):
+                ids = rng.choice(E, k, replace=False)
+                now = (int(st["clock"][0]) + (layer == 0)) * L + layer
+                log2_decay = np.float32(-1.0) / np.float32(np.float32(3.0) * np.float32(L))
+                routed = {layer * E + int(e) for e in ids}
+                keys = []
+                for s, key in enumerate(st["owner"]):
+                    if key < 0:
+                        keys.append((-1.0, s))
+                    elif not st["pending"][s] and int(key) not in routed:
+                        keys.append((float(slots.decayed(st["score"][key], st["at"][key], now, log2_decay)), s))
+                before = st["owner"].copy()
+                plan = slots.resolve_ref(ids, layer, L, E, 3.0, cpu, 2.5, st, share)
+                # slots handed out by this call: each expert's slot that it did not already own, in routing order
+                taken = [int(plan[e, 0]) for e in range(k) if plan[e, 0] >= 0 and before[plan[e, 0]] != layer * E + int(ids[e])]
+                assert taken == [s for _, s in sorted(keys)[:len(taken)]]
+            for s in np.nonzero(st["pending"])[0]:
+                st["pending"][s] = 0
+                st["table"][st["owner"][s]] = s
