@@ -1,20 +1,35 @@
-"""A layer's routed experts in the reference's own formats on an MI355X: the entry points model.py imports from
-drama3/offload.py (FP8Experts, experts_decode, gather_experts, kernel_bank, resident_decode, resident_prefill), with
-the same arguments and results, running the gfx950 kernels of kernels.py.
+"""A layer's routed experts in the reference's own formats on an MI355X: every name drama3/model.py, loader.py and
+generate.py import from drama3/offload.py (FP8Experts, experts_decode, gather_experts, kernel_bank, resident_decode,
+resident_prefill; ExpertStore, HostEmbedding, OffloadedExperts), with the reference's signatures and results, running
+the gfx950 kernels of kernels.py.
 
-Storage is an HBM-resident expert table (`ExpertTable`): every layer's banks stay on the device (288 GB holds a
-40-layer model's experts many times over), so the decode plan is the identity (slot e = expert e, offload.py:113)
-and no lookup or host copy sits on the path. Banks are field dicts of flat tensors, as the reference's kernels read
-them (offload.py:72-90, 264-273):
+Storage. An MI355X holds 288 GB, many times a converted model's experts (every layer's banks of the reference model
+in int8: about 13 GB), so an ExpertStore's session first tries to make the banks resident: every layer copied to
+the device once, expert e of layer l in slot l * E + e, and a decode row or a prompt then runs the resident kernels
+(the plan is the identity: no lookup, no host copy, nothing waits on the host). Only when the banks do not fit the
+budget (a small `cache_bytes`, or other models in the way) does the session keep the reference's host-offload scheme:
+banks in page-locked host memory, a slot cache in HBM kept by kernels.resolve (decayed use counts), the GEMVs reading
+missed experts from host memory and filling their slots, and, for int8 banks and a small cache, the CPU running part
+of the missed experts beside the GPU.
+
+The cache's state (table, owners, use counts, pending copies) stays on the device throughout: the decode kernels keep
+it there, and the host-side lookups (a prompt's pass, formats without kernels) are torch operations on the same
+tensors, so nothing moves it between host and device between passes.
+
+Banks are field dicts of flat tensors, as the kernels read them (offload.py:72-90, 264-273):
   int8   {"_qdata": int8 [E * N, K], "scale": float32 [E * N]}                 ConvRot basis (H256 per 256 columns)
   fp8    {"weight": uint8 e4m3 [E * N, K], "scale": float32 [E * N / 128, K / 128]}
   w4/w6  {"_qdata": uint8 [E * N, K * bits / 8], "scale": uint8 e4m3 [E * N, K / 16], "s_channel": float32 [E * N]},
          plus a float32 [16] codebook per bank at 4 bits                       ConvRot basis
 
-comfy's QuantizedTensor (comfy.quant_ops) is used when it is importable; without it `kernel_bank` and friends accept
-any object with the same `_qdata`, `_params`, `_layout_cls` attributes.
+ComfyUI (comfy.quant_ops, comfy.model_management) is used when it is importable; without it a quantized weight is any
+object with QuantizedTensor's `_qdata`, `_params` and `_layout_cls`, and the memory budget comes from torch.
 """
+import concurrent.futures
+import contextlib
 import dataclasses
+import functools
+import logging
 import time
 
 import torch
@@ -22,21 +37,28 @@ import torch.nn as nn
 
 from . import kernels
 
-FP8_BLOCK = 128             # offload.py:36
-CPU_EXPERT_US, CPU_ROW_US = 60, 13   # offload.py:37-38: the CPU's cost of one int8 expert, first estimate
-PCIE_BYTES_PER_US = 12e3    # offload.py:39
-HALF_LIFE = 128             # offload.py:44
-MAX_EXPERTS_PER_ROW = 8     # offload.py:46
-RESERVE_START, RESERVE_MIN, RESERVE_MAX = 32, 8, 256   # offload.py:49
-ADMIT = 6.0                 # offload.py:51
-AWAIT_US = 5000             # offload.py:53
+# The reference's policy constants (offload.py:30-51), with its names and values.
+RESERVE_BASE = 512 * 1024 ** 2           # device memory a generation needs besides the model and the cache
+RESERVE_PER_ROW = 0.3 * 1024 ** 2        # ... and per row of prompt and frames
+EVICTION_PAUSE = 2.0                     # seconds for comfy's memory reading to catch up after it evicted weights
+FP8_BLOCK = 128
+CPU_EXPERT_US, CPU_ROW_US = 60, 13       # first guess of the CPU's cost of one int8 expert, and per row through it
+PCIE_BYTES_PER_US = 12e3                 # host -> device rate the split assumes for a missed expert
+HALF_LIFE = 128                          # passes over which a use count halves
+MAX_EXPERTS_PER_ROW = 8
+RESERVE_START, RESERVE_MIN, RESERVE_MAX = 32, 8, 256  # slots a decode step may reserve for the CPU's experts
+ADMIT = 6.0                              # ... only for experts used this many times (decayed)
+AWAIT_US = 5000                          # a decode layer's wait for the host's experts before running them itself
 
-try:  # optional: ComfyUI's quantized tensor type
+try:  # optional: ComfyUI
     from comfy.quant_ops import QuantizedTensor
+    import comfy.model_management as _mm
 except ImportError:  # pragma: no cover - comfy is not part of this package
     QuantizedTensor = None
+    _mm = None
 
 
+# ----------------------------------------------------------------------------------------------- format contract
 def _quantized(weight):
     if QuantizedTensor is not None:
         return isinstance(weight, QuantizedTensor)
@@ -44,62 +66,141 @@ def _quantized(weight):
 
 
 def pinned(tensor, pin):
-    """offload.py:56-60: a contiguous copy, in pinned host memory when `pin`."""
+    """A contiguous copy of `tensor`, in page-locked host memory when `pin` (offload.py:54-58)."""
     if not pin:
         return tensor.contiguous()
-    out = torch.empty(tensor.shape, dtype=tensor.dtype, pin_memory=True)
-    return out.copy_(tensor)
+    host = torch.empty(tensor.shape, dtype=tensor.dtype, pin_memory=True)
+    host.copy_(tensor)
+    return host
 
 
 def tensor_fields(weight):
-    """offload.py:63-65: the tensors among a quantized weight's parameters."""
+    """{name: tensor} of a quantized weight's parameters that are tensors (offload.py:61-63)."""
     params = weight._params
-    return {f.name: getattr(params, f.name) for f in dataclasses.fields(params) if torch.is_tensor(getattr(params, f.name))}
+    found = ((f.name, getattr(params, f.name)) for f in dataclasses.fields(params))
+    return {name: value for name, value in found if torch.is_tensor(value)}
 
 
 def per_row_fields(weight):
-    """offload.py:68-71: the bank's tensors holding one entry per weight row (sliced or gathered with the rows)."""
+    """The bank's tensors with one entry per weight row, which move with the rows (offload.py:66-69): the packed rows
+    under "_qdata" and every parameter tensor with as many rows."""
     rows = weight._qdata.shape[0]
-    return {"_qdata": weight._qdata, **{n: v for n, v in tensor_fields(weight).items() if v.ndim >= 1 and v.shape[0] == rows}}
+    fields = {"_qdata": weight._qdata}
+    fields.update((name, t) for name, t in tensor_fields(weight).items() if t.ndim >= 1 and t.shape[0] == rows)
+    return fields
 
 
 def kernel_bank(weight):
-    """offload.py:74-90: (kind, fields) of a flat quantized bank [E * out, ...] the kernels read, or None: "int8"
-    (ConvRot 256) with {"_qdata", "scale"}; "w4" (with codebook) or "w6" (without) with {"_qdata", "scale",
-    "s_channel"}, group 16, ConvRot 256. In-features above 2048 are not taken (the grouped kernels hold 2048)."""
+    """(kind, fields) of a flat quantized bank [E * out, ...] the kernels read, or None (offload.py:72-90): "int8"
+    (ConvRot groups of 256) with {"_qdata", "scale"}; "w4" (with a codebook) or "w6" (without) with {"_qdata",
+    "scale", "s_channel"}, scale groups of 16, ConvRot 256. In-features above 2048 are not taken."""
     if not _quantized(weight) or weight._qdata.ndim != 2:
         return None
     params, fields = weight._params, per_row_fields(weight)
     if params.orig_shape[-1] > 2048:
         return None
+    names = set(fields)
     if weight._layout_cls == "TensorWiseINT8Layout":
-        if getattr(params, "convrot", False) and params.convrot_groupsize == 256 and set(fields) == {"_qdata", "scale"}:
-            return "int8", fields
+        ok = getattr(params, "convrot", False) and params.convrot_groupsize == 256 and names == {"_qdata", "scale"}
+        return ("int8", fields) if ok else None
+    if weight._layout_cls != "AsymW4A8Int8Layout":
         return None
-    if (weight._layout_cls == "AsymW4A8Int8Layout" and params.group_size == 16 and params.convrot_groupsize == 256
-            and params.correction is None and not params.transposed and set(fields) == {"_qdata", "scale", "s_channel"}):
-        bits = weight._qdata.shape[1] * 8 // params.orig_shape[-1]
-        if (bits, params.codebook is not None) in ((4, True), (6, False)):
-            return f"w{bits}", fields
-    return None
+    if (params.group_size, params.convrot_groupsize, params.correction, params.transposed) != (16, 256, None, False):
+        return None
+    if names != {"_qdata", "scale", "s_channel"}:
+        return None
+    bits = weight._qdata.shape[1] * 8 // params.orig_shape[-1]
+    with_codebook = params.codebook is not None
+    return (f"w{bits}", fields) if (bits, with_codebook) in ((4, True), (6, False)) else None
 
 
 def swiglu(y):
-    """SiLU(gate) * up of rows [.., 2I] (gate first), the split comfy.ops._swiglu_eager makes (offload.py:115)."""
-    gate, up = y.chunk(2, dim=-1)
-    return nn.functional.silu(gate) * up
+    """SiLU(gate) * up of rows [..., 2I], the gate half first (the split comfy.ops._swiglu_eager makes)."""
+    half = y.shape[-1] // 2
+    return nn.functional.silu(y[..., :half]) * y[..., half:]
 
 
+@functools.lru_cache(maxsize=4)
+def _rotation(size):
+    h4 = torch.tensor([[1.0, 1, 1, -1], [1, 1, -1, 1], [1, -1, 1, 1], [-1, 1, 1, 1]])
+    levels = max(1, (size.bit_length() - 1) // 2)
+    if 4 ** levels != size:
+        raise ValueError(f"ConvRot sizes are powers of 4, not {size}")
+    return functools.reduce(torch.kron, [h4] * levels) / size ** 0.5
+
+
+def hadamard(size):
+    """ConvRot's rotation of order `size` (a power of 4): the Kronecker power of h4 = [[1,1,1,-1], [1,1,-1,1],
+    [1,-1,1,1], [-1,1,1,1]], normalized to be orthogonal; symmetric, so it is its own inverse (offload.py:170-176)."""
+    return _rotation(size).clone()
+
+
+def dequantize_fp8(weight, scale, dtype):
+    """Float8 rows [R, C] with one float32 scale per 128 x 128 block [R / 128, C / 128] -> dtype (offload.py:163-167):
+    each block's scale is spread over its rows and columns, then multiplied in float32."""
+    rows, cols = weight.shape
+    full = scale.repeat_interleave(FP8_BLOCK, 0)[:rows].repeat_interleave(FP8_BLOCK, 1)[:, :cols]
+    return (weight.float() * full).to(dtype)
+
+
+def gather_experts(weight, ids, num_experts):
+    """Experts `ids` [k] of a flat [E * out, in] bank as one [k * out, in] weight, on the bank's device
+    (offload.py:152-160). A quantized bank keeps its type with its per-row fields gathered; a field dict is gathered
+    field by field (block-scale grids by their own rows per expert)."""
+    def pick(t):
+        return t.unflatten(0, (num_experts, t.shape[0] // num_experts)).index_select(0, ids).flatten(0, 1)
+    if isinstance(weight, dict):
+        return {name: pick(t) for name, t in weight.items()}
+    if not _quantized(weight):
+        return pick(weight)
+    picked = {name: pick(t) for name, t in per_row_fields(weight).items()}
+    qdata = picked.pop("_qdata")
+    params = dataclasses.replace(weight._params, orig_shape=(qdata.shape[0], weight._params.orig_shape[-1]), **picked)
+    return type(weight)(qdata, weight._layout_cls, params)
+
+
+def experts_decode(x, gate_up, down, weights):
+    """One row x [1, H] through k experts (gate_up [k * 2I, H] and down [k * H, I], dense) summed by `weights` [k]
+    (offload.py:192-199): gate_up as one product for all k, then each expert's down projection of its own hidden row
+    as one batched product, [1, H] in x's dtype."""
+    k = weights.shape[0]
+    hidden = swiglu(nn.functional.linear(x, gate_up).view(k, -1))               # [k, I]
+    per_expert = down.view(k, -1, hidden.shape[-1])                             # [k, H, I]
+    out = torch.bmm(per_expert, hidden.unsqueeze(-1).contiguous()).squeeze(-1)  # [k, H]
+    return (weights.to(out.dtype).unsqueeze(-1) * out).sum(0, keepdim=True)
+
+
+def experts_on_cpu(banks, experts, counts, x, rotation):
+    """Rows x [rows, H] (bf16, already in the ConvRot basis; counts[i] rows for experts[i], in turn) through their
+    int8 ConvRot experts on the CPU (offload.py:179-189): [rows, H] float32. The matmuls run expert by expert on each
+    expert's run of rows; SwiGLU and the rotation of the hidden rows run on all the rows at once."""
+    gate_up, down = banks
+    ends = torch.tensor(counts).cumsum(0).tolist()
+    runs = [(e, end - n, end) for e, n, end in zip(experts, counts, ends)]
+    hidden = swiglu(torch.cat([gate_up.cpu_linear(x[a:b], e) for e, a, b in runs]).float())
+    group = rotation.shape[0]
+    hidden = torch.matmul(hidden.unflatten(-1, (-1, group)), rotation).flatten(-2).to(torch.bfloat16)
+    return torch.cat([down.cpu_linear(hidden[a:b], e) for e, a, b in runs]).float()
+
+
+def timed(function, *args):
+    """(function(*args), the seconds it took)."""
+    t0 = time.perf_counter()
+    result = function(*args)
+    return result, time.perf_counter() - t0
+
+
+# ------------------------------------------------------------------------------------------------ kernel dispatch
 def quantized_gemv(kind, x, ids, plan, took_over, late, slot_fields, host_fields, rows, codebook):
-    """offload.py:93-98: [k, rows] of a decode row's experts in an int8, W4A8 or W6A8 bank against x (float32,
-    rotated)."""
+    """[k, rows] of a decode row's experts in an int8, W4A8 or W6A8 bank against x (float32, rotated)
+    (offload.py:93-98)."""
     if kind == "int8":
         return kernels.gemv_int8(x, ids, plan, took_over, late, slot_fields, host_fields, rows)
     return kernels.gemv_codes(x, ids, plan, slot_fields, host_fields, codebook, int(kind[1]), rows)
 
 
 def quantized_grouped(kind, x, groups, slot_fields, host_fields, rows, codebook):
-    """offload.py:101-105: quantized_gemv for a prompt's rows grouped by expert."""
+    """quantized_gemv for a prompt's rows grouped by expert (offload.py:101-105)."""
     if kind == "int8":
         return kernels.grouped_int8(x, groups, slot_fields, host_fields, rows)
     return kernels.grouped_codes(x, groups, slot_fields, host_fields, codebook, int(kind[1]), rows)
@@ -118,29 +219,28 @@ def _constants(device):
     return _consts[key]
 
 
-_FUSED_KINDS = {"int8": 0, "fp8": 1, "w4": 4, "w6": 6}
+def _rows(kind, fields, num_experts):
+    return fields["weight" if kind == "fp8" else "_qdata"].shape[0] // num_experts
 
 
 def resident_decode(x, ids, weights, banks, rows, kind, codebooks):
-    """offload.py:108-123: one row x [1, H] through experts `ids` [k] of banks held whole on the GPU (expert e in
-    slot e, `rows` per expert): fp8 -> gemv, SiLU(gate) * up, gemv; int8 / w4 / w6 -> rotate, gemv, rotate(swiglu),
-    gemv; then the routing-weighted sum, bf16 [1, H]. Nothing waits on the host. Two launches
-    (kernels.resident_decode) where the shapes allow, else the reference's five."""
-    (gate_up, down), (gate_up_rows, down_rows) = banks, rows
+    """One row x [1, H] through experts `ids` [k] of banks held whole on the GPU (expert e in slot e, `rows` per
+    expert) (offload.py:108-123): bf16 [1, H]. Two launches (kernels.resident_decode: gate_up with x rotated in its
+    prologue; down with SwiGLU, the rotation and the weighted sum) where the shapes allow, else the reference's five.
+    Nothing waits on the host."""
+    gate_up_rows, down_rows = rows
     H, I = down_rows, gate_up_rows // 2
     if H in (1024, 2048) and I in (512, 768, 1024) and ids.shape[0] <= 8 and x.dtype == torch.bfloat16:
         return kernels.resident_decode(x, ids, weights.float(), banks, kind, codebooks, H, I)
     return resident_decode_unfused(x, ids, weights, banks, rows, kind, codebooks)
 
 
-
 def routed_decode(x, logits, k, banks, rows, kind, codebooks):
-    """kernels.route(logits, k) then resident_decode (model.py:116-118 then offload.py:108-123) for one row:
-    (out [1, H] bf16, ids [1, k], weights [1, k]). Two launches where the shapes allow (the routing inside the
-    gate_up launch), else route's own launch and resident_decode."""
-    (gate_up, down), (gate_up_rows, down_rows) = banks, rows
+    """kernels.route(logits, k), then resident_decode (model.py:116-118, then offload.py:108-123), for one row:
+    (out [1, H] bf16, ids [1, k], weights [1, k]). The routing runs inside the gate_up launch where the shapes allow."""
+    gate_up_rows, down_rows = rows
     H, I = down_rows, gate_up_rows // 2
-    experts = _rows(kind, gate_up, 1) // gate_up_rows
+    experts = _rows(kind, banks[0], 1) // gate_up_rows
     if logits.numel() != experts:
         raise ValueError(f"{logits.numel()} logits for banks of {experts} experts: a routed id past the banks would be "
                          f"read out of bounds")
@@ -150,28 +250,46 @@ def routed_decode(x, logits, k, banks, rows, kind, codebooks):
     ids, weights = kernels.route(logits.reshape(1, -1), k)
     return resident_decode(x, ids[0], weights[0], banks, rows, kind, codebooks), ids, weights
 
+
 def resident_decode_unfused(x, ids, weights, banks, rows, kind, codebooks):
-    """resident_decode as the reference launches it: rotate, gemv, rotate(SwiGLU), gemv, weighted_sum."""
-    (gate_up, down), (gate_up_rows, down_rows) = banks, rows
+    """resident_decode as the reference launches it: rotate, gemv, rotate (SwiGLU), gemv, weighted_sum (fp8: gemv,
+    SiLU(gate) * up, gemv, weighted_sum)."""
     plan = torch.stack((ids.to(torch.int32), torch.zeros_like(ids, dtype=torch.int32)), dim=-1)
+    return _slot_decode(x, ids, weights.float(), plan, banks, banks, rows, kind, codebooks, _constants(x.device))
+
+
+def _slot_decode(x, ids, weights, plan, slot_banks, host_banks, rows, kind, codebooks, flags, cpu_side=None):
+    """The GEMV chain of a decode row under a resolved `plan`: [1, H]. flags = (took_over, always) on the device.
+    With `cpu_side` = (CpuSide, layer, step) the experts the plan leaves to the CPU come back through its mailbox, or
+    run here if the host is late."""
+    took_over, always = flags
     if kind == "fp8":
-        gate, up = kernels.gemv_fp8(x.float(), ids, plan, gate_up, gate_up, gate_up_rows).chunk(2, dim=-1)
-        out = kernels.gemv_fp8(nn.functional.silu(gate) * up, ids, plan, down, down, down_rows)
-        return kernels.weighted_sum(out, weights.float())
-    took_over, always = _constants(x.device)
-    hidden = quantized_gemv(kind, kernels.rotate(x, always), ids, plan, took_over, False, gate_up, gate_up,
-                            gate_up_rows, codebooks[0])
-    out = quantized_gemv(kind, kernels.rotate(hidden, always, swiglu=True), ids, plan, took_over, False, down, down,
-                         down_rows, codebooks[1])
-    return kernels.weighted_sum(out, weights.float())
+        hidden = swiglu(kernels.gemv_fp8(x.float(), ids, plan, slot_banks[0], host_banks[0], rows[0]))
+        return kernels.weighted_sum(kernels.gemv_fp8(hidden, ids, plan, slot_banks[1], host_banks[1], rows[1]), weights)
+    rotated = kernels.rotate(x, always)
+
+    def chain(late):
+        """Each expert's output [k, H], unweighted; with `late`, only the CPU's experts, once the GPU took them."""
+        hidden = quantized_gemv(kind, rotated, ids, plan, took_over, late, slot_banks[0], host_banks[0], rows[0],
+                                codebooks[0])
+        hidden = kernels.rotate(hidden, took_over if late else always, swiglu=True)
+        return quantized_gemv(kind, hidden, ids, plan, took_over, late, slot_banks[1], host_banks[1], rows[1],
+                              codebooks[1])
+
+    if cpu_side is None:
+        return kernels.weighted_sum(chain(False), weights)
+    side, layer, step = cpu_side
+    side.post(layer, plan, ids, weights, rotated.to(torch.bfloat16), step)
+    total = weights @ chain(False) + side.wait(layer, plan, step, took_over)
+    return (total + weights @ chain(True)).to(x.dtype)
 
 
 def grouped_experts(sorted_x, groups, slot_banks, host_banks, rows, kind, codebooks, always):
-    """offload.py:126-136: [rows, H] float32 of sorted_x's rows through their experts, one grouped kernel per bank;
+    """[rows, H] float32: sorted_x's rows through their experts, one grouped kernel per bank (offload.py:126-136);
     `always` is an int32 1 on the GPU."""
     if kind == "fp8":
-        gate, up = kernels.grouped_fp8(sorted_x.float(), groups, slot_banks[0], host_banks[0], rows[0]).chunk(2, dim=-1)
-        return kernels.grouped_fp8(nn.functional.silu(gate) * up, groups, slot_banks[1], host_banks[1], rows[1])
+        hidden = swiglu(kernels.grouped_fp8(sorted_x.float(), groups, slot_banks[0], host_banks[0], rows[0]))
+        return kernels.grouped_fp8(hidden, groups, slot_banks[1], host_banks[1], rows[1])
     hidden = quantized_grouped(kind, kernels.rotate(sorted_x.float(), always), groups, slot_banks[0], host_banks[0],
                                rows[0], codebooks[0])
     return quantized_grouped(kind, kernels.rotate(hidden, always, swiglu=True), groups, slot_banks[1], host_banks[1],
@@ -179,432 +297,767 @@ def grouped_experts(sorted_x, groups, slot_banks, host_banks, rows, kind, codebo
 
 
 def expert_groups(topk_idx, num_experts):
-    """The rows of a prompt's (token, k) pairs sorted by expert, on the device and without a host sync: (order
-    [T * k] int64, groups [num_experts, 5] int32 = (expert, expert, 0, first, rows)). Experts without rows keep a group
-    of 0 rows, which the grouped kernels skip without reading anything. Replaces offload.py:140-143's
-    bincount().tolist(), so a prompt's pass can be captured in a graph."""
+    """A prompt's (token, k) pairs sorted by expert, on the device and without a host sync: (order [T * k] int64,
+    groups [num_experts, 5] int32 = (expert, expert, 0, first, rows)). Experts without rows keep a group of 0 rows,
+    which the grouped kernels skip without reading anything. In place of offload.py:140-143's bincount().tolist(), so
+    a prompt's pass can be captured in a graph."""
     flat = topk_idx.reshape(-1)
     order = torch.sort(flat, stable=True).indices
-    counts = torch.zeros(num_experts, dtype=torch.int64, device=flat.device)
-    counts.scatter_add_(0, flat, torch.ones_like(flat))
+    counts = torch.zeros(num_experts, dtype=torch.int64, device=flat.device).scatter_add_(0, flat, torch.ones_like(flat))
     first = torch.cumsum(counts, 0) - counts
     experts = torch.arange(num_experts, dtype=torch.int64, device=flat.device)
     groups = torch.stack((experts, experts, torch.zeros_like(experts), first, counts), dim=1).to(torch.int32)
     return order, groups
 
 
+def _combine(sorted_out, order, topk_weight, num_tokens, top_k):
+    """The rows of sorted_out ([T * k, H], in `order`) back in (token, k) order, weighted and summed over k: [T, H]
+    float32. A gather by the inverse permutation, so each output element is one sum over k in k's order."""
+    inverse = torch.empty_like(order)
+    inverse[order] = torch.arange(order.shape[0], device=order.device)
+    pairs = sorted_out.float().index_select(0, inverse) * topk_weight.reshape(-1, 1).float()
+    return pairs.view(num_tokens, top_k, -1).sum(dim=1)
+
+
 def resident_prefill(x, topk_idx, topk_weight, banks, rows, kind, codebooks, num_experts):
-    """offload.py:139-149: many rows x [T, H] through banks held whole on the GPU: one grouped kernel per bank, each
-    product scaled by its routing weight and summed over k, in x's dtype."""
+    """Many rows x [T, H] through banks held whole on the GPU (offload.py:138-149): one grouped kernel per bank over
+    the pairs sorted by expert on the device, each product weighted and summed over k; x's dtype."""
     num_tokens, top_k = topk_idx.shape
     order, groups = expert_groups(topk_idx, num_experts)
     _, always = _constants(x.device)
     sorted_out = grouped_experts(x[order // top_k], groups, banks, banks, rows, kind, codebooks, always)
-    out = torch.empty_like(sorted_out)
-    out[order] = sorted_out * topk_weight.reshape(-1)[order].unsqueeze(1).float()
-    return out.view(num_tokens, top_k, -1).sum(dim=1).to(x.dtype)
+    return _combine(sorted_out, order, topk_weight, num_tokens, top_k).to(x.dtype)
 
 
-def gather_experts(weight, ids, num_experts):
-    """offload.py:152-160: experts `ids` [k] of a flat [E * out, in] bank as one [k * out, in] weight, on the device.
-    A field dict is gathered field by field (per-row fields; block-scale grids by their own row count)."""
-    if isinstance(weight, dict):
-        return {n: v.view(num_experts, -1, *v.shape[1:]).index_select(0, ids).flatten(0, 1) for n, v in weight.items()}
-    if not _quantized(weight):
-        return weight.view(num_experts, -1, weight.shape[-1]).index_select(0, ids).flatten(0, 1)
-    rows = weight._qdata.shape[0] // num_experts
-    picked = {n: v.view(num_experts, rows, *v.shape[1:]).index_select(0, ids).flatten(0, 1)
-              for n, v in per_row_fields(weight).items()}
-    qdata = picked.pop("_qdata")
-    return type(weight)(qdata, weight._layout_cls,
-                        dataclasses.replace(weight._params, orig_shape=(len(ids) * rows, weight._params.orig_shape[-1]), **picked))
-
-
-def dequantize_fp8(weight, scale, dtype):
-    """offload.py:163-167: float8 rows [R, C] with a float32 scale per 128 x 128 block [R / 128, C / 128] -> dtype."""
-    rows, cols = weight.shape
-    blocks = weight.float().view(rows // FP8_BLOCK, FP8_BLOCK, cols // FP8_BLOCK, FP8_BLOCK)
-    return (blocks * scale[:, None, :, None]).view(rows, cols).to(dtype)
-
-
-def hadamard(size):
-    """offload.py:170-176: ConvRot's rotation, the regular Hadamard matrix of `size` (a power of 4), normalized."""
-    h4 = torch.tensor([[1.0, 1, 1, -1], [1, 1, -1, 1], [1, -1, 1, 1], [-1, 1, 1, 1]])
-    h = h4
-    while h.shape[0] < size:
-        h = torch.kron(h, h4)
-    return h / size ** 0.5
-
-
-def experts_decode(x, gate_up, down, weights):
-    """offload.py:192-199: one row x [1, H] through k experts as two matmuls (gate_up [k * 2I, H], down [k * H, I],
-    keeping the diagonal blocks of the second), summed by weights."""
-    k = weights.shape[0]
-    hidden = swiglu(nn.functional.linear(x, gate_up).view(k, -1))
-    out = nn.functional.linear(hidden, down).view(k, k, -1).diagonal(dim1=0, dim2=1).T
-    return (out * weights[:, None].to(out.dtype)).sum(0, keepdim=True)
-
-
-def experts_on_cpu(banks, experts, counts, x, rotation):
-    """offload.py:179-189: rows x [rows, H] (bf16, rotated; counts[i] rows for experts[i], in turn) through their int8
-    ConvRot experts on the CPU (`banks` = (gate_up, down) QuantHostBank): [rows, H] float32."""
-    gate_up, down = banks
-    bounds = []
-    start = 0
-    for expert, n in zip(experts, counts):
-        bounds.append((expert, start, start + n))
-        start += n
-    hidden = swiglu(torch.cat([gate_up.cpu_linear(x[a:b], expert) for expert, a, b in bounds]).float())
-    hidden = (hidden.view(len(x), -1, 256) @ rotation).flatten(1).to(torch.bfloat16)
-    return torch.cat([down.cpu_linear(hidden[a:b], expert) for expert, a, b in bounds]).float()
-
-
-# ------------------------------------------------------------------------------------------------------ storage
+# ----------------------------------------------------------------------------------------------------- host banks
 class HostBank:
-    """offload.py:200-218: one expert bank, tensors whose first dimension holds each expert's rows in turn, pinned
-    in host memory when `pin`. `kernel` names the kernel family that reads it."""
+    """One bank of a layer's experts: field tensors whose first dimension holds expert e's rows at [e * rows,
+    (e + 1) * rows), page-locked in host memory when `pin` so the kernels can read them in place (offload.py:202-219).
+    `kernel` names the kernel family that reads the bank, or None."""
 
     kernel = None
 
     def __init__(self, num_experts, fields, pin):
         self.num_experts = num_experts
-        self.fields = {n: pinned(t, pin) for n, t in fields.items()}
+        self.fields = {name: pinned(t, pin) for name, t in fields.items()}
+        self._per_expert = {name: t.shape[0] // num_experts for name, t in self.fields.items()}
 
     def rows(self, name):
-        return self.fields[name].shape[0] // self.num_experts
+        """Rows of field `name` per expert."""
+        return self._per_expert[name]
 
     def take(self, fields, first, last):
-        """Experts [first, last) of `fields`, laid out like this bank's."""
-        return {n: t[first * self.rows(n):last * self.rows(n)] for n, t in fields.items()}
+        """Experts [first, last) of `fields` (this bank's, or a slot pool's: host or device), as views."""
+        return {name: t.narrow(0, first * self.rows(name), (last - first) * self.rows(name)) for name, t in fields.items()}
 
     def to_device(self, first, last, device):
-        return {n: t.to(device, non_blocking=True) for n, t in self.take(self.fields, first, last).items()}
+        return {name: t.to(device, non_blocking=True) for name, t in self.take(self.fields, first, last).items()}
+
+    def codebook(self, device):
+        """The bank's 4-bit codebook on `device` (W4A8 banks), else None."""
+        return None
+
+    def weight(self, fields, device):
+        """The experts of `fields` as one dense bf16 weight on `device`, in the model's own basis: what
+        nn.functional.linear takes on the paths without kernels."""
+        raise NotImplementedError
 
 
 class QuantHostBank(HostBank):
-    """offload.py:221-261 for a bank given as its kind and field dict (int8 ConvRot, W4A8, W6A8) instead of a comfy
-    module: the CPU's int8 matmul reads it in place."""
+    """A flat quantized bank (int8 ConvRot, W4A8, W6A8) taken from a `comfy.ops.MoEExperts`-like module: `module.weight`
+    a QuantizedTensor (or an object with its `_qdata`, `_params`, `_layout_cls`), `module.num_experts`
+    (offload.py:223-261). The CPU's int8 matmul reads it in place."""
 
-    def __init__(self, num_experts, kind, fields, pin, codebook=None):
-        super().__init__(num_experts, fields, pin)
-        self.kernel = kind
-        self._codebook = codebook
+    def __init__(self, module, pin):
+        weight = module.weight
+        if not _quantized(weight) or weight._qdata.ndim != 2:
+            raise ValueError("Drama 3 keeps only flat quantized or FP8 expert banks in host memory")
+        fields = per_row_fields(weight)
+        found = kernel_bank(weight)
+        self._setup(module.num_experts, None if found is None else found[0], fields, pin,
+                    {name: t for name, t in tensor_fields(weight).items() if name not in fields},
+                    weight._params.orig_shape[-1])
+        self.layout, self.params = weight._layout_cls, weight._params
+
+    @classmethod
+    def from_fields(cls, num_experts, kind, fields, pin, codebook=None):
+        """A bank given as its kernel kind and field dict (a converted file's tensors, drama3/loader.py)."""
+        self = cls.__new__(cls)
+        in_features = fields["_qdata"].shape[1] * 8 // (8 if kind == "int8" else int(kind[1]))
+        self._setup(num_experts, kind, fields, pin, {} if codebook is None else {"codebook": codebook}, in_features)
+        self.layout = self.params = None
+        return self
+
+    def _setup(self, num_experts, kind, fields, pin, shared, in_features):
+        HostBank.__init__(self, num_experts, fields, pin)
+        self.kernel, self.shared, self.in_features = kind, shared, in_features
+        self._shared_on = {}
         if kind == "int8":
-            self.scale_bf16 = self.fields["scale"].view(-1).to(torch.bfloat16)
+            self.scale_bf16 = self.fields["scale"].reshape(-1).to(torch.bfloat16)  # the CPU matmul's scale dtype
+
+    def _shared(self, device):
+        if device not in self._shared_on:
+            self._shared_on[device] = {name: t.to(device) for name, t in self.shared.items()}
+        return self._shared_on[device]
 
     def codebook(self, device):
-        return None if self._codebook is None else self._codebook.to(device)
+        return self._shared(torch.device(device)).get("codebook")
 
     def cpu_linear(self, x, expert):
-        """offload.py:245-249: rows x [M, K] (bf16, rotated) through int8 expert `expert` on the CPU: [M, N]."""
+        """Rows x [M, K] (bf16, rotated) through int8 expert `expert` on the CPU, from host memory: [M, N]."""
         rows = self.rows("_qdata")
-        return torch._weight_int8pack_mm(x, self.fields["_qdata"][expert * rows:(expert + 1) * rows],
-                                         self.scale_bf16[expert * rows:(expert + 1) * rows])
+        return torch._weight_int8pack_mm(x, self.fields["_qdata"].narrow(0, expert * rows, rows),
+                                         self.scale_bf16.narrow(0, expert * rows, rows))
+
+    def weight(self, fields, device):
+        """Dequantized (int8 * scale, or the decoded code grid * s_channel) and rotated out of the ConvRot basis."""
+        fields = {name: t.to(device) for name, t in fields.items()}
+        if self.kernel == "int8":
+            w = fields["_qdata"].float() * fields["scale"].float().reshape(-1, 1)
+        elif self.kernel in ("w4", "w6"):
+            grid = kernels.decode_codes(fields["_qdata"], fields["scale"], self.codebook(device), int(self.kernel[1]))
+            w = grid.float() * fields["s_channel"].float().reshape(-1, 1)
+        else:
+            raise ValueError(f"no dense form for a {self.layout} bank outside the kernels' formats")
+        rot = hadamard(256).to(device)
+        return torch.matmul(w.unflatten(-1, (-1, 256)), rot).flatten(-2).to(torch.bfloat16)
 
 
 class FP8HostBank(HostBank):
-    """offload.py:264-273: experts as Fish ships them, float8 rows [E, N, K] and block scales [E, N / 128, K / 128]."""
+    """Experts as Fish ships them: float8 rows [E, N, K] and 128 x 128 block scales [E, N / 128, K / 128]
+    (offload.py:264-273)."""
 
     kernel = "fp8"
 
     def __init__(self, weight, scale, pin):
-        super().__init__(weight.shape[0], {"weight": weight.view(torch.uint8).flatten(0, 1), "scale": scale.flatten(0, 1)}, pin)
+        fields = {"weight": weight.view(torch.uint8).flatten(0, 1), "scale": scale.flatten(0, 1)}
+        super().__init__(weight.shape[0], fields, pin)
+
+    @classmethod
+    def from_fields(cls, num_experts, fields, pin):
+        """A bank given as its field dict ({"weight" uint8, "scale"}, flat), as drama3/loader.py reads it."""
+        self = cls.__new__(cls)
+        HostBank.__init__(self, num_experts, fields, pin)
+        return self
 
     def weight(self, fields, device):
-        return dequantize_fp8(fields["weight"].view(torch.float8_e4m3fn), fields["scale"], torch.bfloat16)
+        w = fields["weight"].to(device).view(torch.float8_e4m3fn)
+        return dequantize_fp8(w, fields["scale"].to(device), torch.bfloat16)
+
+
+# ------------------------------------------------------------------------------------------------------ slot cache
+def _next_reserve(reserve, lagging):
+    """The reservations the next decode step may make (the reference's rule, offload.py:646): a quarter fewer
+    (rounded down, at least RESERVE_MIN) while the copies lag, a quarter and one more (at most RESERVE_MAX) while they
+    keep up."""
+    if lagging:
+        return max(RESERVE_MIN, reserve * 3 // 4)
+    return min(RESERVE_MAX, reserve * 5 // 4 + 1)
 
 
 class SlotPool:
-    """offload.py:560-700, the device part: `count` expert slots in HBM filled from host banks, the least used expert
-    out first. table [L * E] maps a key (layer * E + expert) to its slot, -1, or -2 - slot while the host copies it in
-    (pending); owner [count] maps a slot to its key. The state lives on the device, where kernels.resolve keeps it
-    (`device_state`); `promote` copies the slots decode steps reserved for the CPU's experts between steps."""
+    """`count` expert slots in HBM filled from host banks, the least used expert out first (offload.py:560-753).
 
-    def __init__(self, banks, count, device):
+    State, all on the device, kept there by kernels.resolve and by the host-side lookups alike: table [L * E] maps a
+    key (layer * E + expert) to its slot, -1 (not cached) or -2 - slot (pending: the host is copying it in); owner
+    [count] maps a slot to its key (-1: free); score / at [L * E] hold each key's use count as of step `at` (pass *
+    layers + layer; -1: never), halving every HALF_LIFE passes; clock counts passes; reads counts decode rows' (hits,
+    fills, CPU experts). `fields` holds the slots in the banks' row layout."""
+
+    def __init__(self, banks, budget, device):
         self.banks = banks
         self.device = torch.device(device)
         self.layers, self.num_experts = len(banks), banks[0][0].num_experts
-        self.rows = [{n: bank.rows(n) for n in bank.fields} for bank in banks[0]]
-        self.expert_bytes = sum(t[:bank.rows(n)].nbytes for bank in banks[0] for n, t in bank.fields.items())
-        self.count = max(8, min(self.layers * self.num_experts, int(count)))
-        self.fields = [{n: torch.zeros((self.count * bank.rows(n), *t.shape[1:]), dtype=t.dtype, device=self.device)
-                        for n, t in bank.fields.items()} for bank in banks[0]]
+        self.rows = [{name: bank.rows(name) for name in bank.fields} for bank in banks[0]]
+        self.expert_bytes = sum(t[:1].nbytes * bank.rows(name) for bank in banks[0] for name, t in bank.fields.items())
         keys = self.layers * self.num_experts
-        dev = self.device
-        self.table = torch.full((keys,), -1, dtype=torch.int32, device=dev)
-        self.owner = torch.full((self.count,), -1, dtype=torch.int32, device=dev)
-        self.score = torch.zeros((keys,), dtype=torch.float32, device=dev)
-        self.at = torch.full((keys,), -1, dtype=torch.int32, device=dev)
-        self.pending = torch.zeros((self.count,), dtype=torch.int32, device=dev)
-        self.clock = torch.zeros((1,), dtype=torch.int32, device=dev)
-        self.reads = torch.zeros((3,), dtype=torch.int32, device=dev)
+        self.count = int(max(8, min(keys, budget // self.expert_bytes)))
+        self.fields = [{name: torch.empty((self.count * bank.rows(name), *t.shape[1:]), dtype=t.dtype,
+                                          device=self.device) for name, t in bank.fields.items()}
+                       for bank in banks[0]]
+        on = dict(device=self.device)
+        self.table = torch.full((keys,), -1, dtype=torch.int32, **on)
+        self.owner = torch.full((self.count,), -1, dtype=torch.int32, **on)
+        self.score = torch.zeros((keys,), dtype=torch.float32, **on)
+        self.at = torch.full((keys,), -1, dtype=torch.int32, **on)
+        self.pending = torch.zeros((self.count,), dtype=torch.int32, **on)
+        self.clock = torch.zeros((1,), dtype=torch.int32, **on)
+        self.reads = torch.zeros((3,), dtype=torch.int32, **on)
         self.reserve = RESERVE_START
-        self.budget = torch.tensor(self._budget(), dtype=torch.int32, device=dev)
-        # a layer's step, whether the GPU took over the CPU's experts, a set flag, the GPU's share of missed experts
-        self.step, self.took_over, self.always = torch.tensor([[0], [0], [1]], dtype=torch.int32, device=dev)
-        self.share = torch.zeros((1,), dtype=torch.float32, device=dev)
-        self.reserved, self.copying = [], []
-        self.copy_stream = None
+        self.budget = torch.tensor(self._budget(), dtype=torch.int32, **on)
+        # a layer's step, whether the GPU took the CPU's experts over, a set flag; the GPU's share of missed experts
+        self.step, self.took_over, self.always = torch.tensor([[0], [0], [1]], dtype=torch.int32, **on)
+        self.share = torch.zeros((1,), dtype=torch.float32, **on)
+        self.reserved = []   # (layer, expert, slot) the CPU's experts reserved since the last promote
+        self._copies = []    # (event, [(key, slot)]) in flight, oldest first
+        self._copy_stream = None
+        self._decoding = False
 
+    # -- the decode kernels' view
     def device_state(self):
-        """(table, owner, score, at, pending, clock, budget, reads, step, share) for kernels.resolve."""
+        """(table, owner, score, at, pending, clock, budget, reads, step, share) for kernels.resolve. From here until
+        the next host-side lookup the pool is in its decode phase, whose reservations `promote` copies in."""
+        self._decoding = True
         return (self.table, self.owner, self.score, self.at, self.pending, self.clock, self.budget, self.reads,
                 self.step, self.share)
 
+    def host(self):
+        """Ready for the host-side lookups, which end a decode phase: the state never leaves the device, so this only
+        lets the phase's copies land and maps them."""
+        if self._decoding:
+            self.settle()
+            self._decoding = False
+
     def _budget(self):
-        """[slots a decode step may reserve, at most per layer] (offload.py:644-646)."""
+        """[slots a decode step may reserve, at most per layer]: spread over the layers, with room for busy ones."""
         return [self.reserve, max(1, -(-2 * self.reserve // self.layers))]
 
     def _fill(self, slot, sources):
         for fields, rows, source in zip(self.fields, self.rows, sources):
             for name, target in fields.items():
-                target[slot * rows[name]:(slot + 1) * rows[name]].copy_(source[name], non_blocking=True)
+                target.narrow(0, slot * rows[name], rows[name]).copy_(source[name], non_blocking=True)
 
     def _map(self, pairs):
-        if pairs:
-            keys, slots = zip(*pairs)
-            keys = torch.tensor(keys, dtype=torch.long, device=self.device)
-            slots = torch.tensor(slots, dtype=torch.long, device=self.device)
-            self.table[keys] = slots.to(torch.int32)
-            self.pending[slots] = 0
+        """Copies landed: their keys now map to their slots, which are no longer pending."""
+        if not pairs:
+            return
+        keys, slots = (torch.tensor(v, dtype=torch.long).to(self.device, non_blocking=True) for v in zip(*pairs))
+        self.table.index_put_((keys,), slots.to(torch.int32))
+        self.pending.index_fill_(0, slots, 0)
 
     def promote(self):
-        """offload.py:624-642: map the slots whose copies landed, copy the experts reserved since the last call into
-        theirs on a copy stream, and let the next step reserve as many as the copies kept up with."""
+        """Between decode steps: map the slots whose copies have landed, start copying the experts reserved since the
+        last call (on a copy stream, behind the steps already launched), and set the next step's reservation budget by
+        whether the copies keep up. Outside a decode phase there is nothing to copy, and the budget stays."""
+        if not self._decoding:
+            return
         landed = []
-        while self.copying and self.copying[0][0].query():
-            landed += self.copying.pop(0)[1]
+        while self._copies and self._copies[0][0].query():
+            landed += self._copies.pop(0)[1]
         self._map(landed)
-        lagging = bool(self.copying)
+        lagging = bool(self._copies)
         if self.reserved:
-            if self.copy_stream is None:
-                self.copy_stream = torch.cuda.Stream(self.device)
-            self.copy_stream.wait_stream(torch.cuda.current_stream(self.device))
-            with torch.cuda.stream(self.copy_stream):
+            if self._copy_stream is None:
+                self._copy_stream = torch.cuda.Stream(self.device)
+            self._copy_stream.wait_stream(torch.cuda.current_stream(self.device))
+            with torch.cuda.stream(self._copy_stream):
                 for layer, expert, slot in self.reserved:
                     self._fill(slot, [bank.take(bank.fields, expert, expert + 1) for bank in self.banks[layer]])
-                event = torch.cuda.Event()
-                event.record()
-            self.copying.append((event, [(layer * self.num_experts + expert, slot)
-                                         for layer, expert, slot in self.reserved]))
+                done = torch.cuda.Event()
+                done.record()
+            self._copies.append((done, [(layer * self.num_experts + e, slot) for layer, e, slot in self.reserved]))
             self.reserved = []
-        self.reserve = max(RESERVE_MIN, self.reserve * 3 // 4) if lagging else min(RESERVE_MAX, self.reserve * 5 // 4 + 1)
+        self.reserve = _next_reserve(self.reserve, lagging)
         self.budget.copy_(torch.tensor(self._budget(), dtype=torch.int32), non_blocking=True)
 
     def settle(self):
         """Every reserved slot copied in and mapped."""
         self.promote()
-        if self.copy_stream is not None:
-            self.copy_stream.synchronize()
-        self._map([pair for _, pairs in self.copying for pair in pairs])
-        self.copying = []
+        if self._copy_stream is not None:
+            self._copy_stream.synchronize()
+        self._map([pair for _, pairs in self._copies for pair in pairs])
+        self._copies = []
+
+    # -- host-side lookups (a prompt's pass, formats without kernels)
+    def _now(self, layer):
+        """`layer`'s step in this pass; the first layer starts a new pass."""
+        if layer == 0:
+            self.clock += 1
+        return int(self.clock.item()) * self.layers + layer
+
+    def _decayed(self, keys, now):
+        """Use counts of `keys` as of step `now`: halved per HALF_LIFE passes since their last use, 0 if never used."""
+        at = self.at[keys]
+        halvings = (now - at).float() / float(HALF_LIFE * self.layers)
+        return torch.where(at < 0, torch.zeros_like(halvings), self.score[keys] * torch.exp2(-halvings))
+
+    def slot_fields(self, index, slot):
+        """Bank `index`'s fields of the expert in `slot`, laid out like a host bank's expert."""
+        rows = self.rows[index]
+        return {name: t.narrow(0, slot * rows[name], rows[name]) for name, t in self.fields[index].items()}
+
+    def use(self, layer, experts):
+        """{expert: slot} of the cached ones among `experts`; each of them counts a use in this pass."""
+        self.host()
+        now = self._now(layer)
+        keys = torch.tensor(experts, dtype=torch.long).to(self.device) + layer * self.num_experts
+        self.score[keys] = self._decayed(keys, now) + 1.0
+        self.at[keys] = now
+        found = self.table[keys].tolist()
+        return {e: s for e, s in zip(experts, found) if s >= 0}
+
+    def free_slots(self):
+        return torch.nonzero(self.owner < 0).flatten().tolist()
+
+    def assign(self, slot, layer, expert):
+        """Give `slot` to an expert of `layer`; its previous expert leaves the table. The caller fills the slot."""
+        key = layer * self.num_experts + expert
+        previous = int(self.owner[slot])
+        if previous >= 0:
+            self.table[previous] = -1
+        self.owner[slot] = key
+        self.table[key] = slot
+        return slot
+
+    def _taken(self, layer):
+        """Per slot: whether it holds an expert `layer` used in this pass (such slots are not given away)."""
+        keys = self.owner.long()
+        return (keys >= 0) & (self.at[keys.clamp(min=0)] == int(self.clock.item()) * self.layers + layer)
+
+    def claim(self, layer, expert):
+        """The slot of the least used cached expert (a free one first) that `layer` has not used in this pass."""
+        keys = self.owner.long()
+        now = int(self.clock.item()) * self.layers + layer
+        uses = torch.where(keys < 0, torch.full(keys.shape, -1.0, device=self.device), self._decayed(keys.clamp(min=0), now))
+        return self.assign(int(torch.argmin(uses.masked_fill(self._taken(layer), float("inf")))), layer, expert)
+
+    def room(self, layer):
+        """How many slots `layer` may still claim in this pass: those not holding an expert it used."""
+        return int((~self._taken(layer)).sum())
+
+    def insert(self, layer, expert, sources):
+        """A slot for an expert `layer` uses in this pass, filled from `sources` (host memory)."""
+        slot = self.claim(layer, expert)
+        self._fill(slot, sources)
+        return slot
+
+    def slots(self, layer, experts, banks):
+        """The host-lookup decode: slots of the row's `experts` [k], the missed ones copied in; int64 on the device."""
+        cached = self.use(layer, experts)
+        placed = [cached[e] if e in cached else self.insert(layer, e, [b.take(b.fields, e, e + 1) for b in banks])
+                  for e in experts]
+        self.reads += torch.tensor([len(cached), len(experts) - len(cached), 0], dtype=torch.int32).to(self.device)
+        return torch.tensor(placed, dtype=torch.long).to(self.device)
+
+    def gather(self, index, slots):
+        """Bank `index`'s fields of the experts in `slots`, one after another."""
+        rows = self.rows[index]
+        return {name: t.unflatten(0, (self.count, rows[name])).index_select(0, slots).flatten(0, 1)
+                for name, t in self.fields[index].items()}
+
+    def report(self):
+        self.host()
+        hits, fills, on_cpu = self.reads.tolist()
+        total = hits + fills + on_cpu
+        if total:
+            gib = sum(t.nbytes for f in self.fields for t in f.values()) / 1024 ** 3
+            logging.info("Drama 3 expert cache: %d experts (%.1f GiB), %.0f%% of %d expert reads hit; of the misses %d "
+                         "were read over PCIe, %d run on the CPU", self.count, gib, 100 * hits / total, total, fills,
+                         on_cpu)
 
 
+# -------------------------------------------------------------------------------------------------------- CPU side
 class CpuSide:
-    """offload.py:276-299: where a decode step's layers hand experts to the CPU. A layer copies its plan, routing,
-    rotated row and step here (pinned host memory) and records posted[layer], then waits on the device
-    (kernels.await_cpu) for flag[layer] to reach that step; the host (HostExperts.after_layer) runs the experts and
-    writes result[layer], then the flag."""
+    """Where a decode step's layers hand experts to the CPU (offload.py:276-299): per layer a mailbox in page-locked
+    host memory. The layer posts its plan, routing, rotated row and step and records posted[layer]; the host
+    (ExpertStore.after_layer) runs the experts the plan left to it, writes the result, then the flag; the layer waits
+    on the device (kernels.await_cpu, at most AWAIT_US) for the flag to reach its step. One mailbox per layer, so the
+    host serves a layer while the next one is already launched."""
 
     def __init__(self, layers, k, hidden):
-        self.plan = torch.empty((layers, k, 2), dtype=torch.int32, pin_memory=True)
-        self.ids = torch.empty((layers, k), dtype=torch.long, pin_memory=True)
-        self.weights = torch.empty((layers, k), dtype=torch.float32, pin_memory=True)
-        self.rows = torch.empty((layers, 1, hidden), dtype=torch.bfloat16, pin_memory=True)
-        self.step = torch.zeros((layers,), dtype=torch.int32, pin_memory=True)
-        self.flag = torch.zeros((layers,), dtype=torch.int32, pin_memory=True)
-        self.result = torch.empty((layers, hidden), dtype=torch.bfloat16, pin_memory=True)
+        def mailbox(shape, dtype):
+            return torch.zeros(shape, dtype=dtype, pin_memory=True)
+        self.plan = mailbox((layers, k, 2), torch.int32)
+        self.ids = mailbox((layers, k), torch.long)
+        self.weights = mailbox((layers, k), torch.float32)
+        self.rows = mailbox((layers, 1, hidden), torch.bfloat16)
+        self.step = mailbox((layers,), torch.int32)
+        self.flag = mailbox((layers,), torch.int32)
+        self.result = mailbox((layers, hidden), torch.bfloat16)
         self.posted = [torch.cuda.Event() for _ in range(layers)]
 
     def post(self, layer, plan, ids, weights, rows, step):
-        for target, source in ((self.plan[layer], plan), (self.ids[layer], ids), (self.weights[layer], weights),
-                               (self.rows[layer], rows), (self.step[layer:layer + 1], step)):
-            target.copy_(source, non_blocking=True)
+        sources = {"plan": plan, "ids": ids, "weights": weights, "rows": rows}
+        for name, source in sources.items():
+            getattr(self, name)[layer].copy_(source, non_blocking=True)
+        self.step.narrow(0, layer, 1).copy_(step, non_blocking=True)
         self.posted[layer].record()
 
     def wait(self, layer, plan, step, took_over):
-        return kernels.await_cpu(plan, self.flag[layer:layer + 1], step, self.result[layer], AWAIT_US, took_over)
+        return kernels.await_cpu(plan, self.flag.narrow(0, layer, 1), step, self.result[layer], AWAIT_US, took_over)
 
 
-class HostExperts:
-    """The host-offload option (offload.py:302-452, ExpertStore's decode): every layer's banks in pinned host memory,
-    a SlotPool of `slots` experts in HBM. A decode row resolves its experts on the device (kernels.resolve), the GEMVs
-    read cached ones from their slots and missed ones straight from host memory, filling their slots on the way; with
-    `cpu_side` (int8 banks) the CPU runs part of the missed experts meanwhile (`after_layer` on the host, bounded by
-    kernels.await_cpu on the device). Nothing on the device waits on the host beyond AWAIT_US."""
+# ----------------------------------------------------------------------------------------------------- the store
+class ExpertStore:
+    """Every layer's experts, added one layer at a time (`add`), held for generations (`session`) (offload.py:302-552).
 
-    def __init__(self, kind, layer_banks, num_experts, slots, device, codebooks=None, cpu_side=False, pin=True):
-        self.kind = kind
-        if kind == "fp8":
-            self.banks = [tuple(_FieldBank(num_experts, "fp8", f, pin) for f in banks) for banks in layer_banks]
-        else:
-            self.banks = [tuple(QuantHostBank(num_experts, kind, f, pin) for f in banks) for banks in layer_banks]
-        self.codebooks = [tuple(None if c is None else c.to(device) for c in cb) for cb in codebooks] \
-            if codebooks is not None else [(None, None)] * len(self.banks)
-        self.cache = SlotPool(self.banks, slots, device)
-        self.cpu_side = None
-        if cpu_side:
-            if kind != "int8":
-                raise ValueError("the CPU side runs int8 experts (torch._weight_int8pack_mm)")
-            hidden = self.banks[0][0].fields["_qdata"].shape[1]
-            self.cpu_side = CpuSide(len(self.banks), MAX_EXPERTS_PER_ROW, hidden)
+    In a session the store is either resident (every bank copied to the device: an MI355X holds them many times over)
+    or a slot cache over page-locked host banks. `forward` runs a decode row or a prompt's rows through a layer's
+    experts; `sync_free` says whether a decode row runs without waiting on the host."""
+
+    def __init__(self, cache_bytes, pin):
+        """`cache_bytes` 0: as much device memory as is free when a session starts. `pin` keeps the banks in
+        page-locked host memory, which the kernels need to read them in place."""
+        self.banks = []
+        self.cache = None
+        self.cache_bytes = cache_bytes
+        self.pin = pin
+        self.sync_free = False   # per session: decode rows run the kernels, never waiting on the host
+        self.resident = None     # per resident session: each layer's banks on the device, expert e in slot e
+        self.codebooks = []      # per session: each layer's (gate_up, down) codebooks on the device
+        self.cpu = concurrent.futures.ThreadPoolExecutor(1, thread_name_prefix="drama3-experts")
+        self.cpu_scale = self.gpu_scale = 1.0   # measured / modelled cost of the CPU's and the GPU's share of a prompt
         self.rotation = hadamard(256)
-        self.cpu_expert_us = CPU_EXPERT_US + CPU_ROW_US
+        self.cpu_experts = False  # per session: the CPU may run part of the missed int8 experts
+        self.cpu_side = None      # per session with cpu_decode: the decode steps' mailboxes
+        self.cpu_expert_us = CPU_EXPERT_US + CPU_ROW_US   # a decode step's expert on the CPU, as measured
+
+    # -- building
+    def add(self, experts):
+        """Take a layer's experts (an FP8Experts, or a module with MoEExperts-like gate_up_proj / down_proj) into host
+        memory; returns the module that stands in for them in the model."""
+        if isinstance(experts, FP8Experts):
+            banks = (FP8HostBank(experts.gate_up_weight, experts.gate_up_scale, self.pin),
+                     FP8HostBank(experts.down_weight, experts.down_scale, self.pin))
+        else:
+            banks = (QuantHostBank(experts.gate_up_proj, self.pin), QuantHostBank(experts.down_proj, self.pin))
+        return self._add(banks)
+
+    def add_fields(self, kind, gate_up, down, num_experts, codebooks=(None, None)):
+        """add() for a layer given as field dicts and codebooks (drama3/loader.py's form of a converted file)."""
+        if kind == "fp8":
+            banks = tuple(FP8HostBank.from_fields(num_experts, f, self.pin) for f in (gate_up, down))
+        else:
+            banks = tuple(QuantHostBank.from_fields(num_experts, kind, f, self.pin, cb)
+                          for f, cb in zip((gate_up, down), codebooks))
+        return self._add(banks)
+
+    def _add(self, banks):
+        if self.banks:
+            first = self.banks[0][0]
+            if (banks[0].kernel, banks[0].num_experts) != (first.kernel, first.num_experts):
+                raise ValueError("every layer of a store holds the same format and expert count")
+        self.banks.append(banks)
+        return OffloadedExperts(self, len(self.banks) - 1)
+
+    @property
+    def bank_bytes(self):
+        """Bytes of every layer's banks."""
+        return sum(t.nbytes for banks in self.banks for bank in banks for t in bank.fields.values())
+
+    # -- sessions
+    def _budget(self, device, patchers, rows):
+        """Device memory the session's cache may take: what is free less what the patchers' weights still need on this
+        device and what the longest take needs for `rows` rows, within `cache_bytes` when that is set."""
+        reserve = RESERVE_BASE + int(RESERVE_PER_ROW * rows)
+        loaded = [p.loaded_size() for p in patchers]
+        pending = sum(p.model_size() - size for p, size in zip(patchers, loaded) if p.load_device == device)
+        if _mm is not None:
+            wanted = self.cache_bytes or self.bank_bytes
+            _mm.free_memory(wanted + pending + reserve, device,
+                            [m for m in _mm.current_loaded_models if m.model in patchers])
+            free = _mm.get_free_memory(device)
+            if sum(p.loaded_size() for p in patchers) < sum(loaded):
+                # comfy evicted weights of this very model to make that room: give its memory reading time to catch
+                # up, then load them again (offload.py:366-372)
+                time.sleep(EVICTION_PAUSE)
+                _mm.load_models_gpu(patchers)
+        else:
+            free = torch.cuda.mem_get_info(device)[0]
+        budget = max(0, free - pending - reserve)
+        return min(budget, self.cache_bytes) if self.cache_bytes else budget
+
+    def _make_resident(self):
+        """Every layer's banks copied into the slot pool, expert e of layer l in slot l * E + e, all mapped: each
+        layer's slots are then its banks, read in place by the resident kernels."""
+        cache, E = self.cache, self.banks[0][0].num_experts
+        for layer, banks in enumerate(self.banks):
+            for fields, rows, bank in zip(cache.fields, cache.rows, banks):
+                for name, target in fields.items():
+                    target.narrow(0, layer * E * rows[name], E * rows[name]).copy_(bank.fields[name], non_blocking=True)
+        keys = torch.arange(len(self.banks) * E, dtype=torch.int32, device=cache.device)
+        cache.table.copy_(keys)
+        cache.owner.copy_(keys)
+        self.resident = [[{name: t.narrow(0, layer * E * rows[name], E * rows[name]) for name, t in fields.items()}
+                          for fields, rows in zip(cache.fields, cache.rows)] for layer in range(len(self.banks))]
+
+    @contextlib.contextmanager
+    def session(self, device, patchers, cpu_decode, rows, cpu_experts=True):
+        """One generation's hold on the experts (offload.py:334-384): resident when every bank fits the budget, else
+        a slot cache of what fits. A session opened inside another shares its state. `cpu_decode`: every decode step
+        calls `after_layer` after each layer; `cpu_experts`: the CPU may run part of the missed int8 experts."""
+        if self.cache is not None:
+            yield
+            return
+        device = torch.device(device)
+        budget = self._budget(device, patchers, rows)
+        self.cache = SlotPool(self.banks, budget, device)
+        first = self.banks[0][0]
+        keys = len(self.banks) * first.num_experts
+        if self.cache.count == keys and budget >= self.bank_bytes:
+            self._make_resident()
+        # on the device before any decode step is captured in a graph, which cannot copy them
+        self.codebooks = [tuple(bank.codebook(device) for bank in banks) for banks in self.banks]
+        self.sync_free = (first.kernel is not None and kernels.available(device)
+                          and (self.pin or self.resident is not None))
+        # the CPU runs part of the missed int8 experts while the cache holds under half of them (offload.py:374-378)
+        self.cpu_experts = (cpu_experts and self.sync_free and self.resident is None and first.kernel == "int8"
+                            and 2 * self.cache.count < keys)
+        if cpu_decode and self.cpu_experts:
+            self.cpu_side = CpuSide(len(self.banks), MAX_EXPERTS_PER_ROW, first.in_features)
+        try:
+            yield
+        finally:
+            self.cache.report()
+            self.cache = self.resident = self.cpu_side = None
+            self.sync_free = self.cpu_experts = False
+            if _mm is not None:
+                _mm.soft_empty_cache()
 
     def between_steps(self):
-        """offload.py:386-391: copy the experts the CPU ran into their reserved slots; give the GPU the share of
-        missed experts that lets both sides finish together."""
+        """Between decode steps with the CPU side: copy the experts it ran into the slots they reserved, and give the
+        GPU the share of missed experts that lets both sides finish together (CPU cost / (CPU cost + PCIe time))."""
         self.cache.promote()
-        pcie = self.cache.expert_bytes / PCIE_BYTES_PER_US
-        self.cache.share.fill_(self.cpu_expert_us / (self.cpu_expert_us + pcie))
+        transfer_us = self.cache.expert_bytes / PCIE_BYTES_PER_US
+        self.cache.share.fill_(self.cpu_expert_us / (self.cpu_expert_us + transfer_us))
 
-    def decode(self, layer, x, ids, weights):
-        """offload.py:403-432: one row x [1, H] through its experts `ids` [k]: [1, H] in x's dtype."""
-        gate_up, down = self.banks[layer]
+    # -- running a layer
+    def _bank_rows(self, layer):
+        return [bank.rows("weight" if bank.kernel == "fp8" else "_qdata") for bank in self.banks[layer]]
+
+    def forward(self, layer, x, topk_idx, topk_weight):
+        """A layer's experts for rows x [M, H] routed by topk_idx / topk_weight [M, k]: [M, H] in x's dtype."""
+        banks = self.banks[layer]
+        on_cache = self.cache is not None and x.device == self.cache.device
+        if self.resident is not None and self.sync_free and on_cache:
+            kind, rows = banks[0].kernel, self._bank_rows(layer)
+            if x.shape[0] == 1:
+                return resident_decode(x, topk_idx[0], topk_weight[0], self.resident[layer], rows, kind,
+                                       self.codebooks[layer])
+            return resident_prefill(x, topk_idx, topk_weight, self.resident[layer], rows, kind, self.codebooks[layer],
+                                    banks[0].num_experts)
+        if x.shape[0] == 1 and self.sync_free and on_cache:
+            return self.decode(layer, banks, x, topk_idx[0], topk_weight[0])
+        if x.shape[0] == 1 and self.cache is not None:
+            slots = self.cache.slots(layer, topk_idx[0].tolist(), banks)
+            gate_up, down = (bank.weight(self.cache.gather(i, slots), x.device).to(x.dtype) for i, bank in enumerate(banks))
+            return experts_decode(x, gate_up, down, topk_weight[0])
+        return self.prefill(layer, banks, x, topk_idx, topk_weight)
+
+    def decode(self, layer, banks, x, ids, weights):
+        """One row x [1, H] through its experts `ids` [k] from the slot cache and the host banks: the cache resolved on
+        the device, then the GEMVs (cached experts from their slots, missed ones from host memory, filling their
+        slots). With the CPU side the experts left to the CPU go to the host (`after_layer`) and come back through
+        kernels.await_cpu; if the host is late, the GEMVs run them too."""
         cache, side = self.cache, self.cpu_side
-        plan = kernels.resolve(ids, layer, len(self.banks), gate_up.num_experts, HALF_LIFE, side is not None, ADMIT,
+        plan = kernels.resolve(ids, layer, len(self.banks), banks[0].num_experts, HALF_LIFE, side is not None, ADMIT,
                                *cache.device_state())
-        slots_gate_up, slots_down = cache.fields
-        weights = weights.float()
-        if self.kind == "fp8":
-            gate, up = kernels.gemv_fp8(x.float(), ids, plan, slots_gate_up, gate_up.fields,
-                                        gate_up.rows("weight")).chunk(2, dim=-1)
-            out = kernels.gemv_fp8(nn.functional.silu(gate) * up, ids, plan, slots_down, down.fields,
-                                   down.rows("weight"))
-            return kernels.weighted_sum(out, weights)
-        cb_gu, cb_dn = self.codebooks[layer]
-
-        def experts(late):
-            hidden = quantized_gemv(self.kind, rotated, ids, plan, cache.took_over, late, slots_gate_up,
-                                    gate_up.fields, gate_up.rows("_qdata"), cb_gu)
-            hidden = kernels.rotate(hidden, cache.took_over if late else cache.always, swiglu=True)
-            return quantized_gemv(self.kind, hidden, ids, plan, cache.took_over, late, slots_down, down.fields,
-                                  down.rows("_qdata"), cb_dn)
-
-        rotated = kernels.rotate(x, cache.always)
-        if side is None:
-            return kernels.weighted_sum(experts(False), weights)
-        side.post(layer, plan, ids, weights, rotated.to(torch.bfloat16), cache.step)
-        out = weights @ experts(False) + side.wait(layer, plan, cache.step, cache.took_over)
-        return (out + weights @ experts(True)).to(x.dtype)
+        return _slot_decode(x, ids, weights.float(), plan, cache.fields, [bank.fields for bank in banks],
+                            self._bank_rows(layer), banks[0].kernel, self.codebooks[layer],
+                            (cache.took_over, cache.always), None if side is None else (side, layer, cache.step))
 
     def after_layer(self, layer):
-        """offload.py:434-452: the host's part of decode layer `layer`, already launched: wait for its routing, run
-        the experts it left to the CPU, and hand the result to the layer."""
+        """The host's part of decode layer `layer`, already launched (offload.py:434-452): wait for its routing, run the
+        experts it left to the CPU, hand the result over (result, then flag), and reserve their slots where the plan
+        gave them one. The measured cost per expert steers the next steps' split."""
         side = self.cpu_side
         side.posted[layer].synchronize()
-        plan = side.plan[layer].tolist()
-        on_cpu = [e for e, (_, code) in enumerate(plan) if code == 2]
-        if not on_cpu:
+        plan = side.plan[layer]
+        mine = torch.nonzero(plan[:, 1] == 2).flatten().tolist()
+        if not mine:
             return
         ids = side.ids[layer].tolist()
-        for e in on_cpu:
-            if plan[e][0] >= 0:
-                self.cache.reserved.append((layer, ids[e], plan[e][0]))
-        started = time.perf_counter()
-        out = experts_on_cpu(self.banks[layer], [ids[e] for e in on_cpu], [1] * len(on_cpu),
-                             side.rows[layer].expand(len(on_cpu), -1), self.rotation)
-        side.result[layer].copy_(side.weights[layer, on_cpu] @ out)
+        self.cache.reserved += [(layer, ids[e], int(plan[e, 0])) for e in mine if int(plan[e, 0]) >= 0]
+        out, seconds = timed(experts_on_cpu, self.banks[layer], [ids[e] for e in mine], [1] * len(mine),
+                             side.rows[layer].expand(len(mine), -1), self.rotation)
+        side.result[layer].copy_(side.weights[layer, mine] @ out)
         side.flag[layer] = int(side.step[layer])
-        self.cpu_expert_us = 0.9 * self.cpu_expert_us + 0.1 * 1e6 * (time.perf_counter() - started) / len(on_cpu)
+        self.cpu_expert_us = 0.9 * self.cpu_expert_us + 0.1 * 1e6 * seconds / len(mine)
 
+    def prefill(self, layer, banks, x, topk_idx, topk_weight):
+        """Many rows: each expert the rows use runs once on its rows (offload.py:454-466)."""
+        num_tokens, top_k = topk_idx.shape
+        flat = topk_idx.reshape(-1)
+        order = torch.sort(flat, stable=True).indices
+        counts = torch.bincount(flat, minlength=banks[0].num_experts).tolist()  # the host plans this pass
+        sorted_x = x[order // top_k]
+        if self.sync_free:
+            sorted_out = self.prefill_kernels(layer, banks, sorted_x, counts)
+        else:
+            sorted_out = self.prefill_host(layer, banks, sorted_x, counts)
+        return _combine(sorted_out, order, topk_weight, num_tokens, top_k).to(x.dtype)
 
-class _FieldBank(HostBank):
-    """A host bank given as its field dict (FP8 {"weight", "scale"} with block scales)."""
+    def split(self, experts, counts, expert_bytes):
+        """(experts for the CPU, the CPU's modelled us, the GPU's modelled us) of `experts` (most rows first)
+        (offload.py:514-526): each goes to the side that would finish it sooner, the GPU reading it over PCIe, the CPU
+        at CPU_EXPERT_US + CPU_ROW_US per row, both costs scaled by what earlier passes measured."""
+        transfer = self.gpu_scale * expert_bytes / PCIE_BYTES_PER_US
+        on_cpu, cpu_us, gpu_us = [], 0.0, 0.0
+        for e in experts:
+            cost = self.cpu_scale * (CPU_EXPERT_US + CPU_ROW_US * counts[e])
+            if cpu_us + cost <= gpu_us + transfer:
+                on_cpu.append(e)
+                cpu_us += cost
+            else:
+                gpu_us += transfer
+        return on_cpu, cpu_us / self.cpu_scale, gpu_us / self.gpu_scale
 
-    def __init__(self, num_experts, kind, fields, pin):
-        super().__init__(num_experts, fields, pin)
-        self.kernel = kind
+    def prefill_kernels(self, layer, banks, sorted_x, counts):
+        """The rows `sorted_x` (sorted by expert, counts[e] rows each) through their experts, unweighted, float32
+        (offload.py:468-512). Cached experts run from their slots; the most used of the others fill free slots on the
+        way (up to the layer's share of the cache); the rest are read from host memory; one grouped kernel per bank
+        runs them all. With the CPU side's split, int8 experts with few rows run on the CPU meanwhile."""
+        cache, kind, device = self.cache, banks[0].kernel, sorted_x.device
+        ends = torch.tensor(counts).cumsum(0).tolist()
+        used = [e for e, n in enumerate(counts) if n]
+        slots = cache.use(layer, used)
+        uncached = sorted((e for e in used if e not in slots), key=lambda e: -counts[e])
+        free = cache.free_slots()
+        fills = uncached[:min(cache.count // len(self.banks), len(free))]
+        for e, slot in zip(fills, free):
+            slots[e] = cache.assign(slot, layer, e)
+        on_cpu, cpu_us, gpu_us = [], 0.0, 0.0
+        if self.cpu_experts:
+            on_cpu, cpu_us, gpu_us = self.split(uncached[len(fills):], counts, cache.expert_bytes)
+        skip, filling = set(on_cpu), set(fills)
+        groups = [(e, slots.get(e, -1), int(e in filling), ends[e] - counts[e], counts[e]) for e in used if e not in skip]
+        job = picked = None
+        if on_cpu:
+            picked = torch.cat([torch.arange(ends[e] - counts[e], ends[e]) for e in on_cpu]).to(device)
+            rows = sorted_x.index_select(0, picked).float()
+            rows = torch.matmul(rows.unflatten(-1, (-1, 256)), hadamard(256).to(device)).flatten(-2)
+            job = self.cpu.submit(timed, experts_on_cpu, banks, on_cpu, [counts[e] for e in on_cpu],
+                                  rows.to(torch.bfloat16).cpu(), self.rotation)
+        out = torch.zeros(sorted_x.shape, dtype=torch.float32, device=device)
+        if groups:
+            started, ended = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            started.record()
+            out = grouped_experts(sorted_x, torch.tensor(groups, dtype=torch.int32).to(device), cache.fields,
+                                  [bank.fields for bank in banks], self._bank_rows(layer), kind, self.codebooks[layer],
+                                  cache.always)
+            ended.record()
+        if job is not None:
+            result, cpu_seconds = job.result()
+            out.index_copy_(0, picked, result.to(device, torch.float32))
+            self.cpu_scale = 0.5 * self.cpu_scale + 0.5 * 1e6 * cpu_seconds / cpu_us
+            if groups and gpu_us:
+                ended.synchronize()
+                self.gpu_scale = 0.5 * self.gpu_scale + 0.5 * 1e3 * started.elapsed_time(ended) / gpu_us
+        return out
+
+    def prefill_host(self, layer, banks, sorted_x, counts):
+        """prefill_kernels without the kernels (unpinned banks, formats without kernels) (offload.py:528-552): expert by
+        expert, dense bf16 products from its slot, from a slot filled for this pass (the experts these rows use most,
+        up to the layer's share of the cache, never a slot this layer reads) or straight from host memory."""
+        cache = self.cache
+        ends = torch.tensor(counts).cumsum(0).tolist()
+        out = torch.empty_like(sorted_x)
+        used = [e for e, n in enumerate(counts) if n]
+        cached = cache.use(layer, used)
+        share = min(cache.count // len(self.banks), cache.room(layer))
+        keep = set(sorted((e for e in used if e not in cached), key=lambda e: -counts[e])[:share])
+        for e in used:
+            if e in cached or e in keep:
+                slot = cached[e] if e in cached else cache.insert(layer, e, [b.take(b.fields, e, e + 1) for b in banks])
+                sources = [cache.slot_fields(i, slot) for i in range(len(banks))]
+            else:
+                sources = [b.to_device(e, e + 1, sorted_x.device) for b in banks]
+            gate_up, down = (bank.weight(src, sorted_x.device).to(sorted_x.dtype) for bank, src in zip(banks, sources))
+            run = slice(ends[e] - counts[e], ends[e])
+            out[run] = nn.functional.linear(swiglu(nn.functional.linear(sorted_x[run], gate_up)), down)
+        return out
 
 
 class ExpertTable:
-    """Every layer's expert banks resident in HBM: the build's replacement for the reference's slot cache
-    (offload.py:560-753). A bank is placed once (`place`); the kernels then read expert e in place (plan (e, 0)).
-    `bytes` is what the table holds; `fits` checks it against the device's memory."""
+    """Banks placed whole in HBM, layer by layer (`place`), read in place by the resident kernels (expert e in slot e):
+    a converted checkpoint's experts on an MI355X without a store (drama3/loader.py). `bytes` is what it holds."""
 
     def __init__(self, device):
         self.device = torch.device(device)
         self.layers = {}
 
     def place(self, layer, kind, gate_up, down, codebooks=(None, None)):
-        on = lambda f: {n: t.to(self.device, non_blocking=True).contiguous() for n, t in f.items()}  # noqa: E731
+        banks = tuple({name: t.to(self.device, non_blocking=True).contiguous() for name, t in f.items()}
+                      for f in (gate_up, down))
         cbs = tuple(None if c is None else c.to(self.device) for c in codebooks)
-        self.layers[layer] = (kind, (on(gate_up), on(down)), cbs)
+        self.layers[layer] = (kind, banks, cbs)
         return self.layers[layer]
 
     @property
     def bytes(self):
-        return sum(t.numel() * t.element_size() for _, banks, _ in self.layers.values() for f in banks for t in f.values())
+        return sum(t.nbytes for _, banks, _ in self.layers.values() for f in banks for t in f.values())
 
     def fits(self, extra=0):
+        """Whether `extra` more bytes fit in the device's free memory."""
         free, _ = torch.cuda.mem_get_info(self.device)
         return extra <= free
 
     def decode(self, layer, x, ids, weights, num_experts):
         kind, banks, cbs = self.layers[layer]
-        rows = [_rows(kind, b, num_experts) for b in banks]
-        return resident_decode(x, ids, weights, banks, rows, kind, cbs)
+        return resident_decode(x, ids, weights, banks, [_rows(kind, b, num_experts) for b in banks], kind, cbs)
 
     def prefill(self, layer, x, topk_idx, topk_weight, num_experts):
         kind, banks, cbs = self.layers[layer]
-        rows = [_rows(kind, b, num_experts) for b in banks]
-        return resident_prefill(x, topk_idx, topk_weight, banks, rows, kind, cbs, num_experts)
+        return resident_prefill(x, topk_idx, topk_weight, banks, [_rows(kind, b, num_experts) for b in banks], kind,
+                                cbs, num_experts)
 
 
-def _rows(kind, fields, num_experts):
-    return fields["weight" if kind == "fp8" else "_qdata"].shape[0] // num_experts
-
-
+# ------------------------------------------------------------------------------------------------- model modules
 class FP8Experts(nn.Module):
-    """offload.py:755-802: routed experts as Fish ships them, float8 e4m3 weights with a float32 scale per 128 x 128
-    block. On a gfx950 GPU a decode row runs resident_decode and a prompt resident_prefill; elsewhere the experts a
-    use needs are dequantized to the compute dtype."""
+    """Routed experts as Fish ships them: float8 e4m3 weights with a float32 scale per 128 x 128 block
+    (offload.py:755-802). A decode row runs resident_decode, a prompt resident_prefill, on the gfx950 kernels; there is
+    no torch path here: on any other device the call raises."""
 
     def __init__(self, num_experts, hidden, intermediate, device=None, dtype=None):
         super().__init__()
         self.num_experts = num_experts
         self.dtype = dtype
         for name, rows, cols in (("gate_up", 2 * intermediate, hidden), ("down", hidden, intermediate)):
-            self.register_parameter(f"{name}_weight", nn.Parameter(
-                torch.empty((num_experts, rows, cols), dtype=torch.float8_e4m3fn, device=device), requires_grad=False))
-            self.register_parameter(f"{name}_scale", nn.Parameter(
-                torch.empty((num_experts, rows // FP8_BLOCK, cols // FP8_BLOCK), dtype=torch.float32, device=device),
-                requires_grad=False))
+            weight = torch.empty((num_experts, rows, cols), dtype=torch.float8_e4m3fn, device=device)
+            scale = torch.empty((num_experts, rows // FP8_BLOCK, cols // FP8_BLOCK), dtype=torch.float32, device=device)
+            self.register_parameter(f"{name}_weight", nn.Parameter(weight, requires_grad=False))
+            self.register_parameter(f"{name}_scale", nn.Parameter(scale, requires_grad=False))
 
     def sync_free(self, device):
-        """Whether a decode row on `device` runs without waiting on the host."""
-        return kernels.available(device)
+        """Whether a decode row on `device` runs without waiting on the host: the kernels run there."""
+        return kernels.available(torch.device(device))
 
     def experts(self, name, ids):
-        weight = getattr(self, f"{name}_weight").view(torch.uint8).index_select(0, ids).view(torch.float8_e4m3fn)
-        return dequantize_fp8(weight.flatten(0, 1), getattr(self, f"{name}_scale").index_select(0, ids).flatten(0, 1),
-                              self.dtype)
+        """Experts `ids` of bank `name` ("gate_up" or "down"), dequantized to the module's dtype, one after another."""
+        weight = getattr(self, f"{name}_weight")
+        picked = weight.view(torch.uint8).index_select(0, ids).flatten(0, 1).view(torch.float8_e4m3fn)
+        return dequantize_fp8(picked, getattr(self, f"{name}_scale").index_select(0, ids).flatten(0, 1), self.dtype)
+
+    def _banks(self):
+        names = ("gate_up", "down")
+        banks = [{"weight": getattr(self, f"{n}_weight").view(torch.uint8).flatten(0, 1),
+                  "scale": getattr(self, f"{n}_scale").flatten(0, 1)} for n in names]
+        return banks, [getattr(self, f"{n}_weight").shape[1] for n in names]
 
     def forward(self, x, topk_idx, topk_weight):
-        if kernels.available(x.device):
-            banks = [{"weight": getattr(self, f"{name}_weight").view(torch.uint8).flatten(0, 1),
-                      "scale": getattr(self, f"{name}_scale").flatten(0, 1)} for name in ("gate_up", "down")]
-            rows = [getattr(self, f"{name}_weight").shape[1] for name in ("gate_up", "down")]
-            if x.shape[0] == 1:
-                return resident_decode(x, topk_idx[0], topk_weight[0], banks, rows, "fp8", (None, None))
-            return resident_prefill(x, topk_idx, topk_weight, banks, rows, "fp8", (None, None), self.num_experts)
+        if not kernels.available(x.device):
+            raise RuntimeError(f"drama3.offload.FP8Experts: the gfx950 kernels do not run on {x.device}")
+        banks, rows = self._banks()
         if x.shape[0] == 1:
-            return experts_decode(x, self.experts("gate_up", topk_idx[0]), self.experts("down", topk_idx[0]), topk_weight[0])
-        num_tokens, top_k = topk_idx.shape
-        order = torch.argsort(topk_idx.reshape(-1))
-        counts = torch.bincount(topk_idx.reshape(-1), minlength=self.num_experts).tolist()
-        sorted_x = x[order // top_k]
-        weight = topk_weight.reshape(-1)[order].unsqueeze(1)
-        sorted_out = torch.empty_like(sorted_x)
-        start = 0
-        for expert, n in enumerate(counts):
-            if n == 0:
-                continue
-            ids = torch.tensor([expert], device=x.device)
-            rows = slice(start, start + n)
-            hidden = swiglu(nn.functional.linear(sorted_x[rows], self.experts("gate_up", ids)))
-            sorted_out[rows] = nn.functional.linear(hidden, self.experts("down", ids)) * weight[rows]
-            start += n
-        out = torch.empty_like(sorted_out)
-        out[order] = sorted_out
-        return out.view(num_tokens, top_k, -1).sum(dim=1)
+            return resident_decode(x, topk_idx[0], topk_weight[0], banks, rows, "fp8", (None, None))
+        return resident_prefill(x, topk_idx, topk_weight, banks, rows, "fp8", (None, None), self.num_experts)
+
+
+class HostEmbedding(nn.Module):
+    """The token embedding table left in host memory beside the experts (offload.py:805-815): a prompt or a frame
+    reads a few of its rows, and the device memory goes to the experts instead."""
+
+    def __init__(self, embedding):
+        super().__init__()
+        self.table = embedding.weight.detach()
+
+    def forward(self, ids, out_dtype=None):
+        rows = self.table.index_select(0, ids.reshape(-1).to(self.table.device))
+        return rows.unflatten(0, ids.shape).to(ids.device, out_dtype)
+
+
+class OffloadedExperts(nn.Module):
+    """Stands in for a layer's experts kept by an ExpertStore (offload.py:817-830)."""
+
+    def __init__(self, store, layer):
+        super().__init__()
+        self.store = store
+        self.layer = layer
+
+    def sync_free(self, device):
+        """Whether a decode row on `device` runs without waiting on the host, in the current session."""
+        store = self.store
+        return bool(store.sync_free and store.cache is not None and torch.device(device) == store.cache.device)
+
+    def forward(self, x, topk_idx, topk_weight):
+        return self.store.forward(self.layer, x, topk_idx, topk_weight)
