@@ -281,6 +281,54 @@ D3_INLINE void decode_group(uint32_t lo, uint32_t hi, uint32_t high, uint32_t sc
   }
 }
 
+// W4 through tables: a 16-column group's codes all share one e4m3 scale byte, so the int8-grid values of the 16 codes at
+// each of the 256 scale bytes make a 4 KB table (decode_group's own arithmetic, entry by entry), kept in LDS as bytes
+// q + 128. A group then costs one 16-byte table read, and four of its codes become four bytes through two byte
+// permutes and a byte mask, instead of a codebook read, a product, a rounding and a clamp per value.
+constexpr int QTAB_WORDS = 256 * 4;  // qtab[4 sb + i]: bytes q + 128 of codes 4i .. 4i + 3 at scale byte sb
+// cb: codebook[4 (threadIdx.x & 3) .. + 3], loaded by the caller (ahead of its weight rows)
+D3_INLINE void build_qtab(uint32_t* qtab, f32x4 cb) {
+  const float c[4] = {cb.x, cb.y, cb.z, cb.w};
+  for (int i = threadIdx.x; i < QTAB_WORDS; i += blockDim.x) {  // i & 3 == threadIdx.x & 3: blockDim.x % 4 == 0
+    const float sc = fp8x2_to_f32<false>((uint32_t)(i >> 2)).x;
+    uint32_t word = 0u;
+#pragma unroll
+    for (int b = 0; b < 4; b++) {
+      const float q = fminf(fmaxf(rintf(c[b] * sc), -127.0f), 127.0f);
+      word |= (uint32_t)((int)q + 128) << (8 * b);
+    }
+    qtab[i] = word;
+  }
+}
+
+// the table bytes (t: entries 0..15, 4 per word) at the four indices held in the low nibbles of sel's bytes
+D3_INLINE uint32_t lookup16(i32x4 t, uint32_t sel) {
+  const uint32_t s3 = sel & 0x07070707u;
+  const uint32_t lo = __builtin_amdgcn_perm((uint32_t)t.y, (uint32_t)t.x, s3);  // entries 0..7
+  const uint32_t hi = __builtin_amdgcn_perm((uint32_t)t.w, (uint32_t)t.z, s3);  // entries 8..15
+  // selector byte 12 gives 0x00, 13 gives 0xFF: a byte mask of the indices >= 8
+  const uint32_t m = __builtin_amdgcn_perm(0u, 0u, ((sel >> 3) & 0x01010101u) | 0x0C0C0C0Cu);
+  return (hi & m) | (lo & ~m);
+}
+
+// sum over one group of (q + 128) * x for its 16 codes (nibble words lo / hi, table row t), x the group's 16 floats
+D3_INLINE float group_dot_w4(uint32_t lo, uint32_t hi, i32x4 t, const float* x) {
+  float acc = 0.0f;
+#pragma unroll
+  for (int d = 0; d < 2; d++) {
+    const uint32_t word = d ? hi : lo;  // values 8 d .. 8 d + 7: byte b holds value 2b (low nibble) and 2b + 1
+#pragma unroll
+    for (int odd = 0; odd < 2; odd++) {
+      const uint32_t q = lookup16(t, (odd ? word >> 4 : word) & 0x0F0F0F0Fu);
+      acc = fmaf((float)(q & 0xFFu), x[8 * d + odd], acc);
+      acc = fmaf((float)((q >> 8) & 0xFFu), x[8 * d + 2 + odd], acc);
+      acc = fmaf((float)((q >> 16) & 0xFFu), x[8 * d + 4 + odd], acc);
+      acc = fmaf((float)((q >> 24) & 0xFFu), x[8 * d + 6 + odd], acc);
+    }
+  }
+  return acc;
+}
+
 // kernels.py:495-536: code rows against x, times the row's channel scale. Lane l takes 16-column groups l, l + 64.
 template <int K, int BITS>
 __global__ void __launch_bounds__(256) gemv_codes_kernel(const float* x, int x_rows, const int64_t* ids, const int* plan,
@@ -548,84 +596,130 @@ template <int KIND> D3_INLINE float row_scale(const void* bs, const float* bc, s
 }
 
 //
-// ROUTED: the row's routing (kernels.py:39-67 on logits [n <= 256] bf16) runs first in every workgroup, on wave 0:
-// the top-k keys and softmax weights as route_kernel computes them (the same key order, the same exponentials summed
-// in rank order), expert j from LDS; workgroup (0, 0) writes ids [k] and weights [k] for the down launch and the
-// caller. `ids` is then unused. This saves route's own launch for callers that pass the router's logits.
-constexpr int ROUTED_MAX_N = 256;
-template <int KIND, int K, bool ROUTED>
+// gate_up: grid (I / 8, k), workgroup (hidden units u0 .. u0 + 7 of expert j): its 8 gate rows and the 8 matching up
+// rows, a gate and an up row of two units per wave, so the workgroup ends with h[j, u] = SiLU(gate) * up itself and
+// the down launch reads I floats per expert instead of 2I (the same float operations as rotate_rows' SwiGLU,
+// kernels.py:236, or torch's silu for fp8, offload.py:115). x (bf16) is loaded first, then the weight rows, and x is
+// rotated into LDS (per 256 columns unless fp8) while the rows stream: a wave's loads return in issue order, so x
+// never waits behind the weights.
+//
+// ROUTED: every wave routes the row itself (kernels.py:39-67 on logits [n <= 256] bf16: the top keys and softmax
+// weights as route_kernel computes them, the same key order, the exponentials summed in rank order), running the
+// rounds up to its workgroup's rank j only; workgroup (0, k - 1), which runs all k, writes ids [k] and weights [k] for
+// the down launch and the caller. `ids` is then unused. This saves route's own launch for callers that pass the
+// router's logits.
+constexpr int ROUTED_MAX_N = 256, GU_UNITS = 8;
+template <int KIND, int K, int KPL, bool ROUTED>
 __global__ void __launch_bounds__(256) resident_gu_kernel(const uint16_t* x, const int64_t* ids,
                                                           const uint16_t* logits, int n, int k, int64_t* ids_out,
                                                           float* w_out, const uint8_t* bw, const void* bs,
-                                                          const float* bc, const float* codebook, float* gu, int N) {
-  constexpr int RW = RPB / 4;  // rows per wave
+                                                          const float* bc, const float* codebook, float* h, int I) {
+  constexpr int CH = K / 256 / 4;  // 256-column chunks of x per wave
   __shared__ float xs[K];
-  __shared__ float lut[16];
-  __shared__ int routed_id;
-  const int j = blockIdx.y, lane = threadIdx.x & 63, w = threadIdx.x >> 6, n0 = blockIdx.x * RPB;
+  __shared__ float lut[1];  // (row_dot reads a codebook only at 4 bits, which go through qtab here)
+  __shared__ uint32_t qtab[KIND == 4 ? QTAB_WORDS : 1];
+  const int j = blockIdx.y, lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int unit = blockIdx.x * GU_UNITS + 2 * w;  // this wave's units: unit, unit + 1
+  i32x2 xr[CH];
+#pragma unroll
+  for (int c = 0; c < CH; c++) xr[c] = *(const i32x2*)(x + 256 * (w + 4 * c) + 4 * lane);
+  f32x4 cb = {0.0f, 0.0f, 0.0f, 0.0f};
+  if constexpr (KIND == 4) cb = *(const f32x4*)(codebook + 4 * (threadIdx.x & 3));
   size_t e;
   if constexpr (ROUTED) {
-    if (w == 0) {
-      constexpr int KPL = ROUTED_MAX_N / 64;
-      uint32_t lb[KPL];
+    uint32_t lb[KPL];
 #pragma unroll
-      for (int q = 0; q < KPL; q++) lb[q] = logits[min(lane + 64 * q, n - 1)];  // lanes past n masked by top_keys
-      const uint32_t mine = top_keys<KPL>(lb, lane, n, k);
-      if (lane == j) routed_id = route_key_index(mine);
-      if (blockIdx.x == 0 && j == 0) {  // uniform over the wave: route_weight reads lanes 0 .. k-1
-        const float wt = route_weight(mine, lane, k);
-        if (lane < k) {
-          ids_out[lane] = route_key_index(mine);
-          w_out[lane] = wt;
-        }
+    for (int q = 0; q < KPL; q++) lb[q] = logits[min(lane + 64 * q, n - 1)];  // lanes past n masked by TopKeys
+    const bool writer = blockIdx.x == 0 && j == k - 1;
+    TopKeys<KPL> tk(lb, lane, n);
+    tk.rounds(lane, 0, j + 1);
+    e = (size_t)route_key_index((uint32_t)__builtin_amdgcn_readlane((int)tk.mine, j));
+    if (writer && w == 0) {  // uniform over the wave: route_weight reads lanes 0 .. k-1
+      const float wt = route_weight(tk.mine, lane, k);
+      if (lane < k) {
+        ids_out[lane] = route_key_index(tk.mine);
+        w_out[lane] = wt;
       }
     }
-    __syncthreads();
-    e = (size_t)routed_id;
   } else {
     e = (size_t)ids[j];
   }
-  RowBytes<KIND, K> rb[RW];
-  float sc[RW];
+  // rows: gate unit, gate unit + 1, up unit, up unit + 1
+  const size_t N = 2 * (size_t)I;
+  size_t rows[4] = {e * N + unit, e * N + unit + 1, e * N + I + unit, e * N + I + unit + 1};
+  RowBytes<KIND, K> rb[4];
+  float sc[4];
 #pragma unroll
-  for (int r = 0; r < RW; r++) {
-    const size_t row = e * N + n0 + w * RW + r;
-    load_row<KIND, K>(rb[r], bw, (const uint8_t*)bs, row, lane);
-    sc[r] = row_scale<KIND>(bs, bc, row);
+  for (int r = 0; r < 4; r++) {
+    load_row<KIND, K>(rb[r], bw, (const uint8_t*)bs, rows[r], lane);
+    sc[r] = row_scale<KIND>(bs, bc, rows[r]);
   }
-  for (int g = w; g < K / 256; g += 4) {
-    const int c0 = 256 * g + 4 * lane;
-    const i32x2 raw = *(const i32x2*)(x + c0);
-    float v[4] = {bf16_to_f32((uint32_t)raw.x & 0xFFFFu), bf16_to_f32((uint32_t)raw.x >> 16),
-                  bf16_to_f32((uint32_t)raw.y & 0xFFFFu), bf16_to_f32((uint32_t)raw.y >> 16)};
+#pragma unroll
+  for (int c = 0; c < CH; c++) {
+    float v[4] = {bf16_to_f32((uint32_t)xr[c].x & 0xFFFFu), bf16_to_f32((uint32_t)xr[c].x >> 16),
+                  bf16_to_f32((uint32_t)xr[c].y & 0xFFFFu), bf16_to_f32((uint32_t)xr[c].y >> 16)};
     if constexpr (KIND != 1) fwht256(v);
-    *(f32x4*)(xs + c0) = f32x4{v[0], v[1], v[2], v[3]};
+    *(f32x4*)(xs + 256 * (w + 4 * c) + 4 * lane) = f32x4{v[0], v[1], v[2], v[3]};
   }
-  if (KIND == 4 && threadIdx.x < 16) lut[threadIdx.x] = codebook[threadIdx.x];
+  if constexpr (KIND == 4) build_qtab(qtab, cb);
   __syncthreads();
-  const float* sblock = KIND == 1 ? (const float*)bs + ((e * N + n0) / 128) * (K / 128) : nullptr;
+  float y[4];
+  if constexpr (KIND == 4) {
+    // the lane's groups v = lane + 64 i of x, once for the four rows, and their sum (values enter as q + 128)
+    using R = RowBytes<KIND, K>;
+    float xv[R::GPL][16];
+    float xsum = 0.0f;
 #pragma unroll
-  for (int r = 0; r < RW; r++) {
-    const float acc = wave_sum_f32(row_dot<KIND, K>(rb[r], xs, sblock, lut, lane));
-    if (lane == 0) gu[(size_t)j * N + n0 + w * RW + r] = acc * sc[r];
+    for (int i = 0; i < R::GPL; i++) xsum += load_slice<16>(xs + 16 * 64 * i, lane, xv[i]);
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      float acc = 0.0f;
+#pragma unroll
+      for (int i = 0; i < R::GPL; i++) {
+        const i32x4 t = *(const i32x4*)(qtab + 4 * rb[r].sb[i]);
+        acc += group_dot_w4((uint32_t)rb[r].lw[i].x, (uint32_t)rb[r].lw[i].y, t, xv[i]);
+      }
+      y[r] = wave_sum_f32(fmaf(-128.0f, xsum, acc)) * sc[r];
+    }
+  } else {
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const float* sblock = KIND == 1 ? (const float*)bs + (rows[r] / 128) * (K / 128) : nullptr;
+      y[r] = wave_sum_f32(row_dot<KIND, K>(rb[r], xs, sblock, lut, lane)) * sc[r];
+    }
+  }
+  if (lane < 2) {
+    const float g = lane ? y[1] : y[0], u = lane ? y[3] : y[2];
+    // fp8: torch's silu as offload.py:115 applies it; the others: rotate_rows' SwiGLU (kernels.py:236)
+    const float sig = KIND == 1 ? 1.0f + expf(-g) : 1.0f + __expf(-g);
+    h[(size_t)j * I + unit + lane] = g / sig * u;
   }
 }
 
 // down: grid (H / 4), workgroup (output rows m0 .. m0 + 3) for all k experts, so the routing-weighted sum stays in the
-// workgroup. The rows' bytes for every expert are loaded first; then each expert's hidden row h_j = SiLU(gate) * up
-// of gu[j] (rotated per 256 unless fp8) goes into LDS, and a row per wave gives out[m] = bf16(sum_j w_j *
-// (row . h_j) * scale), experts in order as weighted_sum sums them. (8 rows per workgroup, H / 8 = 256 of them,
-// left one workgroup per CU: int8 25.5 against 24.2 us per layer, W4A8 30.7 against 26.8, fp8 26.9 against 25.0;
-// 2 rows, in workgroups of two waves that each recompute the hidden rows: int8 27.7, W4A8 30.3, fp8 27.6.)
+// workgroup. Each wave first loads its share of the k hidden rows h_j (I floats each, 256-column chunks), then its
+// output row's bytes for every expert; the hidden chunks are rotated (unless fp8) into LDS while the rows stream, and
+// a row per wave gives out[m] = bf16(sum_j w_j * (row . h_j) * scale), experts in order as weighted_sum sums them.
+// (8 rows per workgroup, H / 8 = 256 of them, left one workgroup per CU: int8 25.5 against 24.2 us per layer, W4A8
+// 30.7 against 26.8, fp8 26.9 against 25.0; 2 rows, in workgroups of two waves that each recompute the hidden rows:
+// int8 27.7, W4A8 30.3, fp8 27.6.)
 constexpr int DN_ROWS = 4, MAX_K_RES = 8;
 template <int KIND, int K>
-__global__ void __launch_bounds__(256) resident_dn_kernel(const float* gu, const int64_t* ids, const float* wts, int k,
+__global__ void __launch_bounds__(256) resident_dn_kernel(const float* h, const int64_t* ids, const float* wts, int k,
                                                           const uint8_t* bw, const void* bs, const float* bc,
                                                           const float* codebook, uint16_t* out, int H) {
-  constexpr int RW = DN_ROWS / 4;
+  constexpr int RW = DN_ROWS / 4, CPE = K / 256, CH = MAX_K_RES * CPE / 4;  // chunks per expert, per wave
   __shared__ float hs[MAX_K_RES][K];
   __shared__ float lut[16];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, m0 = blockIdx.x * DN_ROWS;
+  // the hidden chunks first (chunk c = w + 4 i: expert c / CPE, columns 256 (c % CPE) ..; past k: the last expert's,
+  // loaded but not stored), so they return ahead of the weight rows
+  f32x4 hv[CH];
+#pragma unroll
+  for (int i = 0; i < CH; i++) {
+    const int c = w + 4 * i, jj = min(c / CPE, k - 1);
+    hv[i] = *(const f32x4*)(h + (size_t)jj * K + 256 * (c % CPE) + 4 * lane);
+  }
   RowBytes<KIND, K> rb[RW][MAX_K_RES];
   float sc[RW][MAX_K_RES];
   size_t ex[MAX_K_RES];
@@ -641,19 +735,14 @@ __global__ void __launch_bounds__(256) resident_dn_kernel(const float* gu, const
       load_row<KIND, K>(rb[r][j], bw, (const uint8_t*)bs, row, lane);
       sc[r][j] = row_scale<KIND>(bs, bc, row);
     }
-  for (int c = w; c < k * (K / 256); c += 4) {
-    const int jj = c / (K / 256), c0 = 256 * (c % (K / 256)) + 4 * lane;
-    const f32x4 g = *(const f32x4*)(gu + (size_t)jj * 2 * K + c0), u = *(const f32x4*)(gu + (size_t)jj * 2 * K + K + c0);
-    const float gg[4] = {g.x, g.y, g.z, g.w}, uu[4] = {u.x, u.y, u.z, u.w};
-    float v[4];
 #pragma unroll
-    for (int t = 0; t < 4; t++) {
-      // fp8: torch's silu as offload.py:115 applies it; the others: rotate_rows' SwiGLU (kernels.py:236)
-      const float sig = KIND == 1 ? 1.0f + expf(-gg[t]) : 1.0f + __expf(-gg[t]);
-      v[t] = gg[t] / sig * uu[t];
+  for (int i = 0; i < CH; i++) {
+    const int c = w + 4 * i;
+    if (c < k * CPE) {
+      float v[4] = {hv[i].x, hv[i].y, hv[i].z, hv[i].w};
+      if constexpr (KIND != 1) fwht256(v);
+      *(f32x4*)(&hs[c / CPE][256 * (c % CPE) + 4 * lane]) = f32x4{v[0], v[1], v[2], v[3]};
     }
-    if constexpr (KIND != 1) fwht256(v);
-    *(f32x4*)(&hs[jj][c0]) = f32x4{v[0], v[1], v[2], v[3]};
   }
   if (KIND == 4 && threadIdx.x < 16) lut[threadIdx.x] = codebook[threadIdx.x];
   __syncthreads();
@@ -673,12 +762,104 @@ __global__ void __launch_bounds__(256) resident_dn_kernel(const float* gu, const
   }
 }
 
-// Check of the decode above on its own: one thread per (row, 16-column group) writes the int8-grid values.
-template <int BITS>
+// down for the code formats: W4 / W6 rows are short (I / 2 or 3I / 4 bytes, I / 16 scale groups), so a row takes 16
+// lanes, each holding I / 256 of its groups, and a wave covers four experts' rows of its output row at once, in two
+// passes over eight experts; a 16-lane row sum is four DPP steps. The hidden rows arrive and are rotated as in
+// resident_dn_kernel; W4 decodes through qtab.
+template <int KIND, int K>
+__global__ void __launch_bounds__(256) resident_dn_codes_kernel(const float* h, const int64_t* ids, const float* wts,
+                                                                int k, const uint8_t* bw, const uint8_t* bs,
+                                                                const float* bc, const float* codebook,
+                                                                uint16_t* out, int H) {
+  constexpr int CPE = K / 256, CH = MAX_K_RES * CPE / 4, G = K / 16, GS = G / 16, RB = K * KIND / 8;
+  static_assert(DN_ROWS == 4, "one output row per wave");
+  __shared__ float hs[MAX_K_RES][K];
+  __shared__ uint32_t qtab[KIND == 4 ? QTAB_WORDS : 1];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, seg = lane >> 4, li = lane & 15;
+  const int m = blockIdx.x * DN_ROWS + w;
+  f32x4 hv[CH];
+#pragma unroll
+  for (int i = 0; i < CH; i++) {
+    const int c = w + 4 * i, jj = min(c / CPE, k - 1);
+    hv[i] = *(const f32x4*)(h + (size_t)jj * K + 256 * (c % CPE) + 4 * lane);
+  }
+  f32x4 cb = {0.0f, 0.0f, 0.0f, 0.0f};
+  if constexpr (KIND == 4) cb = *(const f32x4*)(codebook + 4 * (threadIdx.x & 3));
+  // pass p: this lane's expert is 4 p + seg (the last routed one again past k), its groups li + 16 i
+  size_t row[2];
+#pragma unroll
+  for (int p = 0; p < 2; p++) row[p] = (size_t)ids[min(4 * p + seg, k - 1)] * H + m;
+  i32x2 lw[2][GS];
+  uint32_t high[2][GS], sb[2][GS];
+  float sc[2];
+#pragma unroll
+  for (int p = 0; p < 2; p++) {
+    const uint8_t* r = bw + row[p] * RB;
+#pragma unroll
+    for (int i = 0; i < GS; i++) {
+      const int v = li + 16 * i;
+      lw[p][i] = *(const i32x2*)(r + 8 * v);
+      high[p][i] = KIND == 6 ? *(const uint32_t*)(r + K / 2 + 4 * v) : 0u;
+      sb[p][i] = bs[row[p] * G + v];
+    }
+    sc[p] = bc[row[p]];
+  }
+#pragma unroll
+  for (int i = 0; i < CH; i++) {
+    const int c = w + 4 * i;
+    if (c < k * CPE) {
+      float v[4] = {hv[i].x, hv[i].y, hv[i].z, hv[i].w};
+      fwht256(v);
+      *(f32x4*)(&hs[c / CPE][256 * (c % CPE) + 4 * lane]) = f32x4{v[0], v[1], v[2], v[3]};
+    }
+  }
+  if constexpr (KIND == 4) build_qtab(qtab, cb);
+  __syncthreads();
+  float y[2];
+#pragma unroll
+  for (int p = 0; p < 2; p++) {
+    const float* hr = hs[min(4 * p + seg, k - 1)];
+    float acc = 0.0f;
+#pragma unroll
+    for (int i = 0; i < GS; i++) {
+      float xv[16];
+      const float xsum = load_slice<16>(hr + 256 * i, li, xv);  // values 16 (li + 16 i) ..
+      if constexpr (KIND == 4) {
+        const i32x4 t = *(const i32x4*)(qtab + 4 * sb[p][i]);
+        acc += fmaf(-128.0f, xsum, group_dot_w4((uint32_t)lw[p][i].x, (uint32_t)lw[p][i].y, t, xv));
+      } else {
+        float q[16];
+        decode_group<KIND>((uint32_t)lw[p][i].x, (uint32_t)lw[p][i].y, high[p][i], sb[p][i], nullptr, q);
+#pragma unroll
+        for (int t = 0; t < 16; t++) acc = fmaf(q[t], xv[t], acc);
+      }
+    }
+    // the row's sum over its 16 lanes, in every lane of the row
+    acc += __int_as_float(dpp_i32(__float_as_int(acc), 0xB1));
+    acc += __int_as_float(dpp_i32(__float_as_int(acc), 0x4E));
+    acc += __int_as_float(dpp_i32(__float_as_int(acc), 0x141));
+    acc += __int_as_float(dpp_i32(__float_as_int(acc), 0x140));
+    y[p] = acc * sc[p];
+  }
+  // out[m] = bf16(sum over the routed experts, in order, of w_j * y_j)
+  float total = 0.0f;
+#pragma unroll
+  for (int j = 0; j < MAX_K_RES; j++) {
+    if (j < k) total = fmaf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(y[j / 4]), 16 * (j % 4))), wts[j], total);
+  }
+  if (lane == 0) out[m] = (uint16_t)f32_to_bf16(total);
+}
+
+// Check of the decodes above on their own: one thread per (row, 16-column group) writes the int8-grid values, through
+// decode_group (TABLE false: the GEMVs' and grouped products' decode) or through qtab (TABLE true, 4 bits: the resident
+// kernels' decode).
+template <int BITS, bool TABLE>
 __global__ void __launch_bounds__(256) decode_codes_kernel(const uint8_t* rows, const uint8_t* scales,
                                                            const float* codebook, int R, int K, int8_t* out) {
   __shared__ float lut[16];
+  __shared__ uint32_t qtab[TABLE ? QTAB_WORDS : 1];
   if (BITS == 4 && threadIdx.x < 16) lut[threadIdx.x] = codebook[threadIdx.x];
+  if constexpr (TABLE) build_qtab(qtab, *(const f32x4*)(codebook + 4 * (threadIdx.x & 3)));
   __syncthreads();
   const int G = K / 16;
   const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
@@ -686,11 +867,25 @@ __global__ void __launch_bounds__(256) decode_codes_kernel(const uint8_t* rows, 
   const int r = (int)(idx / G), v = (int)(idx % G);
   const uint8_t* row = rows + (size_t)r * (K * BITS / 8);
   const i32x2 lw = *(const i32x2*)(row + 8 * v);
-  const uint32_t high = BITS == 6 ? *(const uint32_t*)(row + K / 2 + 4 * v) : 0u;
-  float q[16];
-  decode_group<BITS>((uint32_t)lw.x, (uint32_t)lw.y, high, scales[(size_t)r * G + v], lut, q);
+  const uint32_t sb = scales[(size_t)r * G + v];
+  int8_t* o = out + (size_t)r * K + 16 * v;
+  if constexpr (TABLE) {
+    const i32x4 t = *(const i32x4*)(qtab + 4 * sb);
 #pragma unroll
-  for (int j = 0; j < 16; j++) out[(size_t)r * K + 16 * v + j] = (int8_t)(int)q[j];
+    for (int d = 0; d < 2; d++) {
+      const uint32_t word = d ? (uint32_t)lw.y : (uint32_t)lw.x;
+      const uint32_t ev = lookup16(t, word & 0x0F0F0F0Fu) ^ 0x80808080u;  // values 8d + 0, 2, 4, 6 as int8
+      const uint32_t od = lookup16(t, (word >> 4) & 0x0F0F0F0Fu) ^ 0x80808080u;
+      *(uint32_t*)(o + 8 * d) = __builtin_amdgcn_perm(od, ev, 0x05010400u);
+      *(uint32_t*)(o + 8 * d + 4) = __builtin_amdgcn_perm(od, ev, 0x07030602u);
+    }
+  } else {
+    const uint32_t high = BITS == 6 ? *(const uint32_t*)(row + K / 2 + 4 * v) : 0u;
+    float q[16];
+    decode_group<BITS>((uint32_t)lw.x, (uint32_t)lw.y, high, sb, lut, q);
+#pragma unroll
+    for (int j = 0; j < 16; j++) o[j] = (int8_t)(int)q[j];
+  }
 }
 
 }  // namespace d3
@@ -843,7 +1038,7 @@ static int resident_launch(const char* name, int32_t kind, const void* x, const 
   if ((H != 2048 && H != 1024) || (I != 512 && I != 768 && I != 1024) || H % DN_ROWS)
     return fail(std::string(name) + ": H 1024 or 2048, I 512, 768 or 1024");
   const hipStream_t s = (hipStream_t)stream;
-  const dim3 ggrid(2 * I / RPB, k), dgrid(H / DN_ROWS);
+  const dim3 ggrid(I / GU_UNITS, k), dgrid(H / DN_ROWS);
   const uint16_t *xb = (const uint16_t*)x, *lg = (const uint16_t*)logits;
   const uint8_t *gw = (const uint8_t*)gu_w, *dw = (const uint8_t*)dn_w;
   int64_t* ids_out = const_cast<int64_t*>(ids);
@@ -851,30 +1046,39 @@ static int resident_launch(const char* name, int32_t kind, const void* x, const 
   uint16_t* o = (uint16_t*)out;
 #define D3_GU(KIND, K)                                                                                               \
   do {                                                                                                               \
-    if (lg) hipLaunchKernelGGL((resident_gu_kernel<KIND, K, true>), ggrid, dim3(256), 0, s, xb, nullptr, lg, n, k,   \
-                               ids_out, w_out, gw, gu_s, gu_c, gu_codebook, gu, 2 * I);                              \
-    else hipLaunchKernelGGL((resident_gu_kernel<KIND, K, false>), ggrid, dim3(256), 0, s, xb, ids, nullptr, 0, k,    \
-                            nullptr, nullptr, gw, gu_s, gu_c, gu_codebook, gu, 2 * I);                               \
+    if (!lg) hipLaunchKernelGGL((resident_gu_kernel<KIND, K, 1, false>), ggrid, dim3(256), 0, s, xb, ids, nullptr, 0, \
+                                k, nullptr, nullptr, gw, gu_s, gu_c, gu_codebook, gu, I);                            \
+    else if (n <= 64) hipLaunchKernelGGL((resident_gu_kernel<KIND, K, 1, true>), ggrid, dim3(256), 0, s, xb, nullptr, \
+                                         lg, n, k, ids_out, w_out, gw, gu_s, gu_c, gu_codebook, gu, I);              \
+    else if (n <= 128) hipLaunchKernelGGL((resident_gu_kernel<KIND, K, 2, true>), ggrid, dim3(256), 0, s, xb,        \
+                                          nullptr, lg, n, k, ids_out, w_out, gw, gu_s, gu_c, gu_codebook, gu, I);    \
+    else hipLaunchKernelGGL((resident_gu_kernel<KIND, K, 4, true>), ggrid, dim3(256), 0, s, xb, nullptr, lg, n, k,   \
+                            ids_out, w_out, gw, gu_s, gu_c, gu_codebook, gu, I);                                     \
   } while (0)
-#define D3_RES(KIND)                                                                                                 \
+#define D3_DN(KERNEL, KIND, ST)                                                                                     \
+  do {                                                                                                               \
+    if (I == 768) hipLaunchKernelGGL((KERNEL<KIND, 768>), dgrid, dim3(256), 0, s, gu, ids, weights, k, dw, (ST)dn_s, \
+                                     dn_c, dn_codebook, o, H);                                                       \
+    else if (I == 512) hipLaunchKernelGGL((KERNEL<KIND, 512>), dgrid, dim3(256), 0, s, gu, ids, weights, k, dw,     \
+                                          (ST)dn_s, dn_c, dn_codebook, o, H);                                        \
+    else hipLaunchKernelGGL((KERNEL<KIND, 1024>), dgrid, dim3(256), 0, s, gu, ids, weights, k, dw, (ST)dn_s, dn_c,   \
+                            dn_codebook, o, H);                                                                      \
+  } while (0)
+#define D3_RES(KIND, DN_KERNEL, ST)                                                                                  \
   do {                                                                                                               \
     if (H == 2048) D3_GU(KIND, 2048);                                                                                \
     else D3_GU(KIND, 1024);                                                                                          \
-    if (I == 768) hipLaunchKernelGGL((resident_dn_kernel<KIND, 768>), dgrid, dim3(256), 0, s, gu, ids, weights, k,  \
-                                     dw, dn_s, dn_c, dn_codebook, o, H);                                             \
-    else if (I == 512) hipLaunchKernelGGL((resident_dn_kernel<KIND, 512>), dgrid, dim3(256), 0, s, gu, ids, weights, \
-                                          k, dw, dn_s, dn_c, dn_codebook, o, H);                                    \
-    else hipLaunchKernelGGL((resident_dn_kernel<KIND, 1024>), dgrid, dim3(256), 0, s, gu, ids, weights, k, dw, dn_s, \
-                            dn_c, dn_codebook, o, H);                                                                \
+    D3_DN(DN_KERNEL, KIND, ST);                                                                                      \
   } while (0)
   switch (kind) {
-    case 0: D3_RES(0); break;
-    case 1: D3_RES(1); break;
-    case 4: D3_RES(4); break;
-    case 6: D3_RES(6); break;
+    case 0: D3_RES(0, resident_dn_kernel, const void*); break;
+    case 1: D3_RES(1, resident_dn_kernel, const void*); break;
+    case 4: D3_RES(4, resident_dn_codes_kernel, const uint8_t*); break;
+    case 6: D3_RES(6, resident_dn_codes_kernel, const uint8_t*); break;
     default: return fail(std::string(name) + ": kind 0, 1, 4 or 6");
   }
 #undef D3_RES
+#undef D3_DN
 #undef D3_GU
   return done(name);
 }
@@ -901,16 +1105,18 @@ int d3_resident_decode_routed(int32_t kind, const void* x, const void* logits, i
 int d3_decode_codes(int32_t bits, const void* rows, const void* scales, const float* codebook, int32_t R, int32_t K,
                     void* out, void* stream) {
   if (!rows || !scales || !out) return fail("d3_decode_codes: null pointer");
+  const bool table = bits == D3_DECODE_TABLE_W4;
+  if (table) bits = 4;
   if (bits == 4 && !codebook) return fail("d3_decode_codes: 4 bits need a codebook");
   if ((bits != 4 && bits != 6) || R < 1 || K < 32 || K % 32) return fail("d3_decode_codes: bits 4 or 6, K % 32 == 0");
   const int64_t threads = (int64_t)R * (K / 16);
   const dim3 grid((unsigned)((threads + 255) / 256));
-  if (bits == 4)
-    hipLaunchKernelGGL(decode_codes_kernel<4>, grid, dim3(256), 0, (hipStream_t)stream, (const uint8_t*)rows,
-                       (const uint8_t*)scales, codebook, R, K, (int8_t*)out);
-  else
-    hipLaunchKernelGGL(decode_codes_kernel<6>, grid, dim3(256), 0, (hipStream_t)stream, (const uint8_t*)rows,
-                       (const uint8_t*)scales, codebook, R, K, (int8_t*)out);
+  const hipStream_t s = (hipStream_t)stream;
+  const uint8_t *rb = (const uint8_t*)rows, *sb = (const uint8_t*)scales;
+  int8_t* o = (int8_t*)out;
+  if (table) hipLaunchKernelGGL((decode_codes_kernel<4, true>), grid, dim3(256), 0, s, rb, sb, codebook, R, K, o);
+  else if (bits == 4) hipLaunchKernelGGL((decode_codes_kernel<4, false>), grid, dim3(256), 0, s, rb, sb, codebook, R, K, o);
+  else hipLaunchKernelGGL((decode_codes_kernel<6, false>), grid, dim3(256), 0, s, rb, sb, codebook, R, K, o);
   return done("d3_decode_codes");
 }
 

@@ -16,6 +16,7 @@ import threading
 import torch
 
 LIB_PATH = pathlib.Path(__file__).resolve().parent / "_lib" / "libdrama3_moe.so"
+DECODE_TABLE_W4 = 0x104  # d3_decode_codes: 4-bit rows through the resident kernels' tables (D3_DECODE_TABLE_W4)
 
 c_int32, c_int64, c_uint32, c_void_p = ctypes.c_int32, ctypes.c_int64, ctypes.c_uint32, ctypes.c_void_p
 

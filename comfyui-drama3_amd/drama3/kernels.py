@@ -168,13 +168,13 @@ _RESIDENT_KINDS = {"int8": (0, "_qdata"), "fp8": (1, "weight"), "w4": (4, "_qdat
 
 
 def resident_decode(x, ids, weights, banks, kind, codebooks, H, I):
-    """[1, H] bfloat16: offload.resident_decode's product in two launches (gate_up with x rotated in its prologue;
-    down with SiLU(gate) * up rotated in its prologue and the routing-weighted sum), banks resident, expert e in slot
-    e. weights float32 [k]."""
+    """[1, H] bfloat16: offload.resident_decode's product in two launches (gate_up with x rotated in its prologue and
+    SiLU(gate) * up in its epilogue; down with the hidden rows rotated in its prologue and the routing-weighted sum),
+    banks resident, expert e in slot e. weights float32 [k]."""
     code, wkey = _RESIDENT_KINDS[kind]
     gate_up, down = banks
     k = ids.shape[0]
-    gu = torch.empty((k, 2 * I), dtype=torch.float32, device=x.device)
+    gu = torch.empty((k, I), dtype=torch.float32, device=x.device)  # the hidden rows
     out = torch.empty((1, H), dtype=torch.bfloat16, device=x.device)
     _call("d3_resident_decode", code, _p(x.contiguous()), _p(ids.contiguous()), _p(weights.contiguous()), k,
           _p(gate_up[wkey]), _p(gate_up["scale"]), _p(gate_up.get("s_channel")), _p(down[wkey]), _p(down["scale"]),
@@ -194,7 +194,7 @@ def resident_decode_routed(x, logits, k, banks, kind, codebooks, H, I):
     if lg.shape[0] != experts or down[wkey].shape[0] != experts * H:
         raise ValueError(f"{lg.shape[0]} logits for banks of {experts} experts: a routed id past the banks would be "
                          f"read out of bounds")
-    gu = torch.empty((k, 2 * I), dtype=torch.float32, device=x.device)
+    gu = torch.empty((k, I), dtype=torch.float32, device=x.device)  # the hidden rows
     out = torch.empty((1, H), dtype=torch.bfloat16, device=x.device)
     ids = torch.empty((1, k), dtype=torch.int64, device=x.device)
     weights = torch.empty((1, k), dtype=torch.float32, device=x.device)
@@ -221,12 +221,16 @@ def fp8_linear(x, weight, scale):
     return out
 
 
-def decode_codes(qdata, scale, codebook, bits):
+def decode_codes(qdata, scale, codebook, bits, table=False):
     """int8 [R, K]: W4A8 / W6A8 rows decoded to the int8 grid exactly as gemv_codes / grouped_codes decode them
-    (a check of kernels.py:466-483's decode_codes; no counterpart in the reference's call surface)."""
+    (a check of kernels.py:466-483's decode_codes; no counterpart in the reference's call surface). table: 4-bit rows
+    through the per-scale-byte tables of the resident decode kernels instead."""
     R = qdata.shape[0]
     K = qdata.shape[1] * 8 // bits
     out = torch.empty((R, K), dtype=torch.int8, device=qdata.device)
-    _call("d3_decode_codes", int(bits), _p(qdata.contiguous()), _p(scale.contiguous()), _p(codebook), R, K, _p(out),
+    mode = _lib.DECODE_TABLE_W4 if table else int(bits)
+    if table and bits != 4:
+        raise ValueError("the table decode is for 4-bit rows")
+    _call("d3_decode_codes", mode, _p(qdata.contiguous()), _p(scale.contiguous()), _p(codebook), R, K, _p(out),
           _stream(qdata))
     return out

@@ -222,7 +222,7 @@ int d3_await_cpu(const int32_t* plan, int32_t k, const int32_t* flag, const int3
 /* resident_decode in two launches (offload.py:108-123, which launches rotate, gemv, rotate(SwiGLU), gemv and
  * weighted_sum): kind 0 int8 (ConvRot), 1 fp8, 4 / 6 codes; banks resident (expert e in slot e) with the fields of
  * d3_gemv_* (gu_c / dn_c: channel scales, codes only). x [H] bf16, ids [k] int64, weights [k] float32 (k <= 8),
- * gu [k, 2I] float32 scratch (the gate_up products), out [H] bf16. H 1024 or 2048, I 512, 768 or 1024. */
+ * gu [k, I] float32 scratch (the hidden rows SiLU(gate) * up), out [H] bf16. H 1024 or 2048, I 512, 768 or 1024. */
 int d3_resident_decode(int32_t kind, const void* x, const int64_t* ids, const float* weights, int32_t k,
                        const void* gu_w, const void* gu_s, const float* gu_c, const void* dn_w, const void* dn_s,
                        const float* dn_c, const float* gu_codebook, const float* dn_codebook, float* gu, void* out,
@@ -239,7 +239,10 @@ int d3_resident_decode_routed(int32_t kind, const void* x, const void* logits, i
                               float* gu, void* out, int32_t H, int32_t I, void* stream);
 
 /* Check of the W4A8 / W6A8 decode on its own (kernels.py:466-483 decode_codes; no entry point of its own there):
- * codes [R, K] int8 of rows [R, K * bits / 8] with scales [R, K / 16]; K % 32 == 0. */
+ * codes [R, K] int8 of rows [R, K * bits / 8] with scales [R, K / 16]; K % 32 == 0. bits 4 or 6 decode as the GEMVs
+ * and grouped products do; bits D3_DECODE_TABLE_W4 decodes 4-bit rows through the per-scale-byte tables the resident
+ * decode kernels use. */
+#define D3_DECODE_TABLE_W4 0x104
 int d3_decode_codes(int32_t bits, const void* rows, const void* scales, const float* codebook, int32_t R, int32_t K,
                     void* out, void* stream);
 

@@ -129,6 +129,28 @@ def test_decode_codes_bit_exact_exhaustive(bits):
     assert np.array_equal(got, ref.decode_codes_ref(qr, sr, bits, codebook))
 
 
+def test_decode_table_w4_bit_exact_exhaustive():
+    """The resident kernels' 4-bit decode (a table per e4m3 scale byte, byte permutes) against the oracle: every
+    (code, scale byte) pair in every position of a 16-code group, NaN scale bytes included (they decode as the
+    per-value path decodes them), and random rows."""
+    codebook = ref.default_codebook()
+    K = 16 * 256
+    # row s: group g holds codes (g + s + j) % 16 at its position j, so every code meets every position and scale byte
+    code = np.array([[(g + s + j) % 16 for g in range(256) for j in range(16)] for s in range(16)], dtype=np.uint32)
+    scale = np.tile(np.arange(256, dtype=np.uint8), (16, 1))
+    q = ref.pack_codes(code, 4)
+    got = kernels.decode_codes(dev(q), dev(scale), dev(codebook), 4, table=True).cpu().numpy()
+    per_value = kernels.decode_codes(dev(q), dev(scale), dev(codebook), 4).cpu().numpy()
+    assert np.array_equal(got, per_value)
+    finite = np.repeat((scale & 0x7F) != 0x7F, 16, axis=1)
+    assert np.array_equal(got[finite], ref.decode_codes_ref(q, scale, 4, codebook)[finite])
+    rng = np.random.default_rng(40)
+    qr = rng.integers(0, 256, size=(64, 1024)).astype(np.uint8)
+    sr = no_nan_fp8(rng, (64, 2048 // 16))
+    got = kernels.decode_codes(dev(qr), dev(sr), dev(codebook), 4, table=True).cpu().numpy()
+    assert np.array_equal(got, ref.decode_codes_ref(qr, sr, 4, codebook))
+
+
 # ------------------------------------------------------------------------------------------------------ GEMVs
 def int8_bank(rng, E, N, K):
     return {"_qdata": rng.integers(-127, 128, size=(E * N, K), dtype=np.int8),
