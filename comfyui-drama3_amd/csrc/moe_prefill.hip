@@ -7,11 +7,12 @@
 // moe_layer): per-row int8 or e4m3 activations, SiLU(gate) * up quantized per (row, expert) pair, routing-weighted sum.
 //
 // Launches, all stream-ordered and graph-capturable (no host sync; the grouping happens on the device):
-//   route      top-k per row (d3_route's kernel), unless the caller hands ids / weights in
+//   route      a wave per row: its top-k (as d3_route computes it), or the caller's ids / weights, and its
+//              activations quantized once, by row, in the format's storage order
 //   group      one workgroup: per-expert counts (LDS atomics), offsets, and the pairs in expert order
-//   quantize   activations per pair, straight into the pairs' expert order, in the format's storage order
 //   gate_up    grid (I / 16, E): 16 hidden units of one expert (16 gate + 16 up rows), K split over 4 waves per
-//              tile, the weights held in registers while the expert's pairs go by 16 at a time; SiLU(gate) * up
+//              tile, the weights held in registers while the expert's pairs go by 16 at a time, each pair's row of
+//              activations read through perm; SiLU(gate) * up
 //   quantize   the hidden rows, per pair
 //   down       grid (H / 32, E): 32 output rows of one expert against its pairs; the product, scaled by the pair's
 //              routing weight, lands in the pair's own row
@@ -31,7 +32,7 @@ int hip_fail(hipError_t err, const char* what);
 namespace {
 
 constexpr int MAX_EXPERTS = 1024;
-constexpr int UNIT_PAIRS = 64;  // pairs per work unit: bounds an item's time, so hot experts spread over workgroups
+constexpr int UNIT_PAIRS = 128;  // pairs per work unit (see the grouped products)
 
 struct PrefillArgs {
   const int64_t* ids;     // [P] pair p = t * k + j -> expert
@@ -39,8 +40,8 @@ struct PrefillArgs {
   const int* counts;      // [E]
   const int* offsets;     // [E + 1]
   const int* perm;        // [P] sorted position -> pair
-  const uint8_t* xq;      // [P, H] storage order, by sorted position (row perm[s] / k of x)
-  const float* xs;        // [P]
+  const uint8_t* xq;      // [T, H] storage order, by row
+  const float* xs;        // [T]
   float* h;               // [P, I] by sorted position
   const uint8_t* hq;      // [P, I]
   const float* hs;        // [P] the hidden row's scale times the pair's routing weight
@@ -142,11 +143,90 @@ __global__ void __launch_bounds__(1024) group_kernel(const int64_t* ids, int P, 
   group_pairs(ids, P, E, counts, offsets, perm, units, meta);
 }
 
+// One row of x (bf16, H columns; lane l holds columns 512 c + 8 l .. + 7 in xr[c]) quantized per row: codes in the
+// format's storage order at q, the row's scale (absmax / QMAX) at scale.
+template <int F, int H>
+D3_INLINE void quantize_row(const i32x4* xr, int lane, uint8_t* q, float* scale) {
+  constexpr float QMAX = act_qmax<F>();
+  float v[H / 512][8];
+  float amax = 0.0f;
+#pragma unroll
+  for (int c = 0; c < H / 512; c++) {
+    const uint32_t w4[4] = {(uint32_t)xr[c].x, (uint32_t)xr[c].y, (uint32_t)xr[c].z, (uint32_t)xr[c].w};
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      v[c][2 * j] = bf16_to_f32(w4[j] & 0xFFFFu);
+      v[c][2 * j + 1] = bf16_to_f32(w4[j] >> 16);
+      amax = fmaxf(amax, fmaxf(fabsf(v[c][2 * j]), fabsf(v[c][2 * j + 1])));
+    }
+  }
+  amax = wave_max_f32(amax);
+  const float inv = amax > 0.0f ? QMAX / amax : 0.0f;
+#pragma unroll
+  for (int c = 0; c < H / 512; c++) store_act8<F>(q + 512 * c + 8 * lane, v[c], inv);
+  if (lane == 0) *scale = amax / QMAX;
+}
+
+// ----------------------------------------------------------------------------------------------- route + quantize
+// A wave per row: the row's top-k of E <= 64 KPL bf16 logits (kernels.py:39-67 as d3_route's kernel computes it: keys
+// by value then lower index, k rounds of a wave max, the softmax's exponentials summed in rank order, bf16-rounded),
+// or the caller's ids / weights; then the row's activations quantized once (quantize_row).
+template <int F, int H, int KPL>
+__global__ void __launch_bounds__(256) route_quant_kernel(const uint16_t* logits, const int64_t* ids_in,
+                                                          const float* weights_in, const uint16_t* x, int T, int E,
+                                                          int k, int64_t* ids, float* weights, int64_t* ids_out,
+                                                          float* weights_out, uint8_t* xq, float* xs) {
+  const int lane = threadIdx.x & 63, t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= T) return;
+  i32x4 xr[H / 512];
+#pragma unroll
+  for (int c = 0; c < H / 512; c++) xr[c] = *(const i32x4*)(x + (size_t)t * H + 512 * c + 8 * lane);
+  if (logits) {
+    uint32_t key[KPL];
+#pragma unroll
+    for (int j = 0; j < KPL; j++) {
+      const int e = lane + 64 * j;
+      const uint32_t raw = logits[(size_t)t * E + min(e, E - 1)];  // branch-free: every load in flight at once
+      key[j] = e < E ? route_key(raw, e) : 0u;
+    }
+    int id = 0;  // lane r keeps round r's expert and logit
+    float top = 0.0f;
+    for (int r = 0; r < k; r++) {
+      uint32_t m = key[0];
+#pragma unroll
+      for (int j = 1; j < KPL; j++) m = max(m, key[j]);
+      m = wave_max_u32_v(m);
+#pragma unroll
+      for (int j = 0; j < KPL; j++) key[j] = key[j] == m ? 0u : key[j];
+      if (lane == r) {
+        id = route_key_index(m);
+        top = route_key_value(m);
+      }
+    }
+    const float top0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(top), 0));
+    const float ex = lane < k ? expf(top - top0) : 0.0f;
+    float total = 0.0f;
+    for (int r = 0; r < k; r++) total += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ex), r));
+    if (lane < k) {
+      const float wt = bf16_round(ex / total);
+      ids[(size_t)t * k + lane] = id;
+      weights[(size_t)t * k + lane] = wt;
+      if (ids_out) ids_out[(size_t)t * k + lane] = id;
+      if (weights_out) weights_out[(size_t)t * k + lane] = wt;
+    }
+  } else {
+    for (int j = lane; j < k; j += 64) {
+      ids[(size_t)t * k + j] = ids_in[(size_t)t * k + j];
+      weights[(size_t)t * k + j] = weights_in[(size_t)t * k + j];
+    }
+  }
+  quantize_row<F, H>(xr, lane, xq + (size_t)t * H, xs + t);
+}
+
 // ----------------------------------------------------------------------------------------- few rows, one launch
-// T <= 16 rows in one workgroup of 16 waves, the steps route, group and quantize x of the many-row path in one
-// launch: wave t routes row t (the fused layer's TopKeys, kernels.py:39-67's rule; or copies the given ids and
-// weights), the workgroup groups the pairs (group_pairs), then wave t quantizes row t once (loaded with the logits)
-// and stores its codes at each of its k pairs' sorted positions.
+// T <= 16 rows in one workgroup of 16 waves, the steps route and group of the many-row path in one launch: wave t
+// routes row t (the fused layer's TopKeys, kernels.py:39-67's rule; or copies the given ids and weights) and
+// quantizes it (loaded with the logits), the workgroup groups the pairs (group_pairs).
 struct SmallPrepArgs {
   const uint16_t* logits;   // [T, E] bf16, or null with ids_in / weights_in
   const int64_t* ids_in;
@@ -162,15 +242,14 @@ struct SmallPrepArgs {
   int* perm;
   int4* units;
   int* meta;
-  uint8_t* xq;              // [P, H] by sorted position
-  float* xs;                // [P]
+  uint8_t* xq;              // [T, H] by row
+  float* xs;                // [T]
 };
 
 template <int F, int H, int KPL>
 __global__ void __launch_bounds__(1024) small_prep_kernel(SmallPrepArgs a) {
   constexpr float QMAX = act_qmax<F>();
   __shared__ int64_t lids[16 * 8];
-  __shared__ int linv[16 * 8];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int T = a.T, E = a.E, k = a.k, P = T * k;
   i32x4 xr[H / 512];
@@ -200,30 +279,9 @@ __global__ void __launch_bounds__(1024) small_prep_kernel(SmallPrepArgs a) {
     }
   }
   __syncthreads();
-  group_pairs(lids, P, E, a.counts, a.offsets, a.perm, a.units, a.meta, linv);
+  group_pairs(lids, P, E, a.counts, a.offsets, a.perm, a.units, a.meta);
   __syncthreads();
-  if (w < T) {
-    float v[H / 512][8];
-    float amax = 0.0f;
-#pragma unroll
-    for (int c = 0; c < H / 512; c++) {
-      const uint32_t w4[4] = {(uint32_t)xr[c].x, (uint32_t)xr[c].y, (uint32_t)xr[c].z, (uint32_t)xr[c].w};
-#pragma unroll
-      for (int j = 0; j < 4; j++) {
-        v[c][2 * j] = bf16_to_f32(w4[j] & 0xFFFFu);
-        v[c][2 * j + 1] = bf16_to_f32(w4[j] >> 16);
-        amax = fmaxf(amax, fmaxf(fabsf(v[c][2 * j]), fabsf(v[c][2 * j + 1])));
-      }
-    }
-    amax = wave_max_f32(amax);
-    const float inv = amax > 0.0f ? QMAX / amax : 0.0f;
-    for (int j = 0; j < k; j++) {
-      const int sp = linv[w * k + j];
-#pragma unroll
-      for (int c = 0; c < H / 512; c++) store_act8<F>(a.xq + (size_t)sp * H + 512 * c + 8 * lane, v[c], inv);
-      if (lane == 0) a.xs[sp] = amax / QMAX;
-    }
-  }
+  if (w < T) quantize_row<F, H>(xr, lane, a.xq + (size_t)w * H, a.xs + w);
 }
 
 // ------------------------------------------------------------------------------------------------------- quantize
@@ -345,10 +403,11 @@ D3_INLINE void load_weights(Weights<F, Geometry<F, H, I, MODE>::SW>& wt, const P
 // products are never stored). colv / colp: per column (pair) of a tile, its epilogue scale and (down) its pair index,
 // staged in LDS by wave 0.
 template <int F, int H, int I, int MODE>
-D3_INLINE void compute_tile(const PrefillArgs& a, const Weights<F, Geometry<F, H, I, MODE>::SW>& wt,
+D3_INLINE void compute_tile(const PrefillArgs& a, const int* __restrict__ perm,
+                            const Weights<F, Geometry<F, H, I, MODE>::SW>& wt,
                             Weights<F, Geometry<F, H, I, MODE>::SW>* pref, int4 unit_n, int it_n, int4 unit, int it,
                             int c0, const float* gs, float (*part)[Geometry<F, H, I, MODE>::KS][16][17], float* colv,
-                            int* colp) {
+                            int* colp, int& pr) {
   using G = Geometry<F, H, I, MODE>;
   constexpr int SW = G::SW, KS = G::KS, K = G::K, STEPS = K / 128;
   constexpr int SHIFT = unpack_shift(F);
@@ -357,7 +416,17 @@ D3_INLINE void compute_tile(const PrefillArgs& a, const Weights<F, Geometry<F, H
   const int first = unit.y, n = unit.z;
   const bool valid = c0 + col < n;
   const int sp = first + (valid ? c0 + col : 0);
-  const uint8_t* act = (MODE == 0 ? a.xq : a.hq) + (size_t)sp * K + 32 * q;
+  // gate_up reads the pair's own row of x (row pr / k, pr = perm[sp], loaded a tile ahead); the next tile's pair
+  // (this item's, or the next item's first) is requested before this tile's activations, so it is back by then
+  size_t arow = (size_t)sp;
+  int pr_next = 0;
+  if constexpr (MODE == 0) {
+    const bool more = c0 + 16 < n;
+    const int nfirst = more ? first : unit_n.y, nn = more ? n : unit_n.z, nc0 = more ? c0 + 16 : 0;
+    pr_next = perm[nfirst + min(nc0 + col, nn - 1)];
+    arow = (size_t)(pr / a.k);
+  }
+  const uint8_t* act = (MODE == 0 ? a.xq : a.hq) + arow * K + 32 * q;
   i32x4 lo[SW], hi[SW];
 #pragma unroll
   for (int j = 0; j < SW; j++) {
@@ -365,7 +434,7 @@ D3_INLINE void compute_tile(const PrefillArgs& a, const Weights<F, Geometry<F, H
     hi[j] = *(const i32x4*)(act + 128 * (ks * SW + j) + 16);
   }
   if (w == 0 && lane < 16) {
-    colv[col] = valid ? (MODE == 0 ? a.xs[sp] : a.hs[sp]) : 0.0f;
+    colv[col] = valid ? (MODE == 0 ? a.xs[arow] : a.hs[sp]) : 0.0f;
     if constexpr (MODE == 1) colp[col] = valid ? a.perm[sp] : 0;
   }
   if (pref) load_weights<F, H, I, MODE>(*pref, a, unit_n.x, it_n, tp, ks, lane);
@@ -433,12 +502,15 @@ D3_INLINE void compute_tile(const PrefillArgs& a, const Weights<F, Geometry<F, H
     }
   }
   __syncthreads();
+  if constexpr (MODE == 0) pr = pr_next;
 }
 
 template <int F, int H, int I, int MODE>
-D3_INLINE void compute_item(const PrefillArgs& a, const Weights<F, Geometry<F, H, I, MODE>::SW>& wt,
+D3_INLINE void compute_item(const PrefillArgs& a, const int* __restrict__ perm,
+                            const Weights<F, Geometry<F, H, I, MODE>::SW>& wt,
                             Weights<F, Geometry<F, H, I, MODE>::SW>& pref, int4 unit_n, int it_n, int4 unit, int it,
-                            float* gs, float (*part)[Geometry<F, H, I, MODE>::KS][16][17], float* colv, int* colp) {
+                            float* gs, float (*part)[Geometry<F, H, I, MODE>::KS][16][17], float* colv, int* colp,
+                            int& pr) {
   using G = Geometry<F, H, I, MODE>;
   constexpr int STEPS = G::K / 128;
   const int tid = threadIdx.x;
@@ -453,15 +525,15 @@ D3_INLINE void compute_item(const PrefillArgs& a, const Weights<F, Geometry<F, H
   }
   const int last = (unit.z - 1) & ~15;
   for (int c0 = 0; c0 < last; c0 += 16)
-    compute_tile<F, H, I, MODE>(a, wt, nullptr, unit_n, it_n, unit, it, c0, gs, part, colv, colp);
-  compute_tile<F, H, I, MODE>(a, wt, &pref, unit_n, it_n, unit, it, last, gs, part, colv, colp);
+    compute_tile<F, H, I, MODE>(a, perm, wt, nullptr, unit_n, it_n, unit, it, c0, gs, part, colv, colp, pr);
+  compute_tile<F, H, I, MODE>(a, perm, wt, &pref, unit_n, it_n, unit, it, last, gs, part, colv, colp, pr);
 }
 
-// units / meta come as separate read-only kernel arguments so that their (uniform) loads are scalar loads: those
-// complete apart from the waves' vector loads, so reading the next unit never waits for a weight prefetch.
+// units / meta / perm come as separate read-only kernel arguments so that their (uniform) loads are scalar loads:
+// those complete apart from the waves' vector loads, so reading the next unit never waits for a weight prefetch.
 template <int F, int H, int I, int MODE>
 __global__ void __launch_bounds__(256) grouped_kernel(PrefillArgs a, const int4* __restrict__ units,
-                                                      const int* __restrict__ meta) {
+                                                      const int* __restrict__ meta, const int* __restrict__ perm) {
   using G = Geometry<F, H, I, MODE>;
   __shared__ float part[G::TILES][G::KS][16][17];
   __shared__ float gs[group_scaled(F) ? G::TILES * 16 * (G::K / 128) : 1];
@@ -475,6 +547,8 @@ __global__ void __launch_bounds__(256) grouped_kernel(PrefillArgs a, const int4*
   int it = i % G::PER_EXPERT;
   // two weight buffers in turn (no copy between them, so nothing waits for a prefetch before its data is needed)
   Weights<F, G::SW> buf0, buf1;
+  // gate_up: this lane's pair (column lane % 16) of the first tile, ahead of the weights
+  int pr = MODE == 0 ? perm[unit.y + min(lane & 15, unit.z - 1)] : 0;
   load_weights<F, H, I, MODE>(buf0, a, unit.x, it, tp, ks, lane);
   while (true) {
     // the next item (this one again at the end: its rows are in the cache)
@@ -482,7 +556,7 @@ __global__ void __launch_bounds__(256) grouped_kernel(PrefillArgs a, const int4*
     bool more = in < n_items;
     int4 unit_n = units[(more ? in : i) / G::PER_EXPERT];
     int it_n = (more ? in : i) % G::PER_EXPERT;
-    compute_item<F, H, I, MODE>(a, buf0, buf1, unit_n, it_n, unit, it, gs, part, colv, colp);
+    compute_item<F, H, I, MODE>(a, perm, buf0, buf1, unit_n, it_n, unit, it, gs, part, colv, colp, pr);
     if (!more) break;
     i = in;
     unit = unit_n;
@@ -491,7 +565,7 @@ __global__ void __launch_bounds__(256) grouped_kernel(PrefillArgs a, const int4*
     more = in < n_items;
     unit_n = units[(more ? in : i) / G::PER_EXPERT];
     it_n = (more ? in : i) % G::PER_EXPERT;
-    compute_item<F, H, I, MODE>(a, buf1, buf0, unit_n, it_n, unit, it, gs, part, colv, colp);
+    compute_item<F, H, I, MODE>(a, perm, buf1, buf0, unit_n, it_n, unit, it, gs, part, colv, colp, pr);
     if (!more) break;
     i = in;
     unit = unit_n;
@@ -530,8 +604,8 @@ Layout layout(int64_t T, int64_t k, int64_t H, int64_t I, int64_t E) {
   L.perm = take(P * 4);
   L.units = take((E + P / UNIT_PAIRS + 1) * 16);
   L.meta = take(16);
-  L.xq = take(P * H);
-  L.xs = take(P * 4);
+  L.xq = take(T * H);
+  L.xs = take(T * 4);
   L.h = take(P * I * 4);
   L.hq = take(P * I);
   L.hs = take(P * 4);
@@ -556,15 +630,28 @@ template <int F, int H, int I, int MODE> int resident_grid() {
 }
 template <int F, int H, int I> void launch_products(const PrefillArgs& pa, int max_units, hipStream_t s) {
   const int grid = std::min(resident_grid<F, H, I, 0>(), max_units * (I / 16));
-  hipLaunchKernelGGL((grouped_kernel<F, H, I, 0>), dim3(grid), dim3(256), 0, s, pa, pa.units, pa.meta);
+  hipLaunchKernelGGL((grouped_kernel<F, H, I, 0>), dim3(grid), dim3(256), 0, s, pa, pa.units, pa.meta, pa.perm);
 }
 template <int F, int H, int I> void launch_down(const PrefillArgs& pa, int max_units, hipStream_t s) {
   const int grid = std::min(resident_grid<F, H, I, 1>(), max_units * (H / 64));
-  hipLaunchKernelGGL((grouped_kernel<F, H, I, 1>), dim3(grid), dim3(256), 0, s, pa, pa.units, pa.meta);
+  hipLaunchKernelGGL((grouped_kernel<F, H, I, 1>), dim3(grid), dim3(256), 0, s, pa, pa.units, pa.meta, pa.perm);
 }
 
 template <int F, int KPL> void launch_small(const SmallPrepArgs& sa, hipStream_t s) {
   hipLaunchKernelGGL((small_prep_kernel<F, 2048, KPL>), dim3(1), dim3(1024), 0, s, sa);
+}
+
+template <int F, int KPL> void launch_route_quant(const d3_moe_a8_prefill_desc& d, int64_t* ids, float* weights,
+                                                 uint8_t* xq, float* xs, hipStream_t s) {
+  hipLaunchKernelGGL((route_quant_kernel<F, 2048, KPL>), dim3((d.T + 3) / 4), dim3(256), 0, s,
+                     (const uint16_t*)d.logits, d.ids_in, d.weights_in, (const uint16_t*)d.x, d.T, d.E, d.topk, ids,
+                     weights, d.logits ? d.ids_out : nullptr, d.logits ? d.weights_out : nullptr, xq, xs);
+}
+template <int F> void route_quant(const d3_moe_a8_prefill_desc& d, int64_t* ids, float* weights, uint8_t* xq,
+                                  float* xs, hipStream_t s) {
+  if (d.E <= 128) launch_route_quant<F, 2>(d, ids, weights, xq, xs, s);
+  else if (d.E <= 256) launch_route_quant<F, 4>(d, ids, weights, xq, xs, s);
+  else launch_route_quant<F, 16>(d, ids, weights, xq, xs, s);
 }
 
 template <int F, bool BF16, int WIDTH> void launch_quantize(const void* src, int rows, uint8_t* q, float* scale,
@@ -575,12 +662,9 @@ template <int F, bool BF16, int WIDTH> void launch_quantize(const void* src, int
 }
 
 template <int F, int H, int I> void run(const PrefillArgs& pa, const d3_moe_a8_prefill_desc& d, const Layout& L,
-                                        uint8_t* ws, hipStream_t s, bool x_done) {
+                                        uint8_t* ws, hipStream_t s) {
   const int P = d.T * d.topk;
   const int max_units = std::min(d.E, P) + P / UNIT_PAIRS;
-  // activations quantized straight into the pairs' sorted order (row perm[s] / k of x for position s)
-  if (!x_done)
-    launch_quantize<F, true, H>(d.x, P, ws + L.xq, (float*)(ws + L.xs), pa.perm, d.topk, nullptr, nullptr, s);
   launch_products<F, H, I>(pa, max_units, s);
   launch_quantize<F, false, I>(ws + L.h, P, ws + L.hq, (float*)(ws + L.hs), nullptr, 1, pa.weights, pa.perm, s);
   launch_down<F, H, I>(pa, max_units, s);
@@ -592,8 +676,6 @@ template <int F, int H, int I> void run(const PrefillArgs& pa, const d3_moe_a8_p
 using namespace d3;
 
 extern "C" {
-
-int d3_route(const void* logits, int32_t rows, int32_t n, int32_t k, int64_t* ids, float* weights, void* stream);
 
 int64_t d3_moe_a8_prefill_workspace_bytes(int32_t T, int32_t topk, int32_t H, int32_t I, int32_t E) {
   if (T < 1 || topk < 1 || H < 1 || I < 1 || E < 1) return -1;
@@ -616,9 +698,8 @@ int d3_moe_a8_prefill(const d3_moe_a8_prefill_desc* d, void* stream) {
   const int P = d->T * d->topk;
   int64_t* ids = (int64_t*)(ws + L.ids);
   float* weights = (float*)(ws + L.weights);
-  // up to 16 rows: routing, grouping and x's quantization in one launch (one workgroup; each row quantized once and
-  // its codes stored at its k sorted positions). Measured on a 2048 x 768, 128-expert layer, us per layer against the
-  // three wide launches: int8 66.6 / 70.8 at 7 rows, 70.2 / 74.0 at 8, 84.2 / 87.1 at 12, 97.2 / 98.6 at 16; W4A8
+  // up to 16 rows: routing, x's quantization and the grouping in one launch (one workgroup). Measured on a 2048 x
+  // 768, 128-expert layer, us per layer against the wide launches (then route, group and quantize): int8 66.6 / 70.8 at 7 rows, 70.2 / 74.0 at 8, 84.2 / 87.1 at 12, 97.2 / 98.6 at 16; W4A8
   // 52.1 / 56.6, 55.5 / 59.8, 64.3 / 67.3, 73.6 / 75.3.
   const bool small = d->T <= 16 && d->topk <= 8 && d->E <= 256;
   if (small) {
@@ -648,19 +729,16 @@ int d3_moe_a8_prefill(const d3_moe_a8_prefill_desc* d, void* stream) {
       case D3_FMT_W6: kpl2 ? launch_small<FMT_W6, 2>(sa, s) : launch_small<FMT_W6, 4>(sa, s); break;
       default: kpl2 ? launch_small<FMT_F8, 2>(sa, s) : launch_small<FMT_F8, 4>(sa, s); break;
     }
-  } else if (d->logits) {
-    const int rc = d3_route(d->logits, d->T, d->E, d->topk, ids, weights, stream);
-    if (rc) return rc;
   } else {
-    hipError_t err = hipMemcpyAsync(ids, d->ids_in, (size_t)P * 8, hipMemcpyDeviceToDevice, s);
-    if (err == hipSuccess) err = hipMemcpyAsync(weights, d->weights_in, (size_t)P * 4, hipMemcpyDeviceToDevice, s);
-    if (err != hipSuccess) return hip_fail(err, "d3_moe_a8_prefill: copy routing");
-  }
-  if (d->ids_out && d->logits && !small) {
-    hipError_t err = hipMemcpyAsync(d->ids_out, ids, (size_t)P * 8, hipMemcpyDeviceToDevice, s);
-    if (err == hipSuccess && d->weights_out)
-      err = hipMemcpyAsync(d->weights_out, weights, (size_t)P * 4, hipMemcpyDeviceToDevice, s);
-    if (err != hipSuccess) return hip_fail(err, "d3_moe_a8_prefill: copy routing out");
+    // routing (or the caller's) and x quantized by row, a wave per row
+    uint8_t* xq = ws + L.xq;
+    float* xs = (float*)(ws + L.xs);
+    switch (d->format) {
+      case D3_FMT_I8: route_quant<FMT_I8>(*d, ids, weights, xq, xs, s); break;
+      case D3_FMT_W4: route_quant<FMT_W4>(*d, ids, weights, xq, xs, s); break;
+      case D3_FMT_W6: route_quant<FMT_W6>(*d, ids, weights, xq, xs, s); break;
+      default: route_quant<FMT_F8>(*d, ids, weights, xq, xs, s); break;
+    }
   }
   if (!small)
     hipLaunchKernelGGL(group_kernel, dim3(1), dim3(1024), 0, s, (const int64_t*)ids, P, d->E, (int*)(ws + L.counts),
@@ -687,10 +765,10 @@ int d3_moe_a8_prefill(const d3_moe_a8_prefill_desc* d, void* stream) {
   pa.inter = d->I;
   const bool i768 = d->I == 768;
   switch (d->format) {
-    case D3_FMT_I8: i768 ? run<FMT_I8, 2048, 768>(pa, *d, L, ws, s, small) : run<FMT_I8, 2048, 512>(pa, *d, L, ws, s, small); break;
-    case D3_FMT_W4: i768 ? run<FMT_W4, 2048, 768>(pa, *d, L, ws, s, small) : run<FMT_W4, 2048, 512>(pa, *d, L, ws, s, small); break;
-    case D3_FMT_W6: i768 ? run<FMT_W6, 2048, 768>(pa, *d, L, ws, s, small) : run<FMT_W6, 2048, 512>(pa, *d, L, ws, s, small); break;
-    default: i768 ? run<FMT_F8, 2048, 768>(pa, *d, L, ws, s, small) : run<FMT_F8, 2048, 512>(pa, *d, L, ws, s, small); break;
+    case D3_FMT_I8: i768 ? run<FMT_I8, 2048, 768>(pa, *d, L, ws, s) : run<FMT_I8, 2048, 512>(pa, *d, L, ws, s); break;
+    case D3_FMT_W4: i768 ? run<FMT_W4, 2048, 768>(pa, *d, L, ws, s) : run<FMT_W4, 2048, 512>(pa, *d, L, ws, s); break;
+    case D3_FMT_W6: i768 ? run<FMT_W6, 2048, 768>(pa, *d, L, ws, s) : run<FMT_W6, 2048, 512>(pa, *d, L, ws, s); break;
+    default: i768 ? run<FMT_F8, 2048, 768>(pa, *d, L, ws, s) : run<FMT_F8, 2048, 512>(pa, *d, L, ws, s); break;
   }
   const int64_t threads = (int64_t)d->T * (d->H / 2);
   hipLaunchKernelGGL(reduce_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s, (const float*)pa.parts,
