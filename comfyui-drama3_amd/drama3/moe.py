@@ -118,15 +118,34 @@ def moe_layer(x, logits, gate_up: A8Bank, down: A8Bank, topk, *, routing=False, 
 
 def moe_block(x, gate_up: A8Bank, down: A8Bank, topk, *, router=None, logits=None, shared=None, shared_gate=None,
               routing=False, return_logits=False, out=None, item_units=0, spin_limit=0, recompute_all=False):
-    """SparseMoeBlock.forward for one decode row (drama3/model.py:107-124) in one launch: x [1, H] bf16 -> [1, H] bf16.
+    """SparseMoeBlock.forward (drama3/model.py:107-124) for decode rows: x [M, H] bf16 -> [M, H] bf16, each row in one
+    launch (the rows of the block are independent: a row's router logits, routing, experts and shared expert read
+    only that row).
 
-    The router: `router` [E, H] bf16 (its logits computed in the launch, model.py:115) or given `logits` [1, E] bf16.
+    The router: `router` [E, H] bf16 (its logits computed in the launch, model.py:115) or given `logits` [M, E] bf16.
     The shared expert: `shared` = (gate_up, down) A8Banks of one expert in the layer's format and shape, and
     `shared_gate` [H] bf16; it is added as model.py:123 does (both terms bf16). With `routing` also returns ids and
-    weights, with `return_logits` the router's logits [1, E] bf16. `item_units`, `spin_limit` and `recompute_all` as
-    for moe_layer."""
-    if x.dtype != torch.bfloat16 or x.dim() != 2 or x.shape[0] != 1:
-        raise ValueError("x [1, H] bfloat16 expected: the block runs one row")
+    weights [M, topk], with `return_logits` the router's logits [M, E] bf16. `item_units`, `spin_limit` and
+    `recompute_all` as for moe_layer."""
+    if x.dtype != torch.bfloat16 or x.dim() != 2 or x.shape[0] < 1:
+        raise ValueError("x [M, H] bfloat16 expected")
+    M = x.shape[0]
+    if M > 1:
+        E = gate_up.experts
+        if logits is not None and (logits.dtype != torch.bfloat16 or logits.shape != (M, E)):
+            raise ValueError("logits [M, E] bfloat16 expected")
+        if out is not None and (out.shape != x.shape or out.dtype != torch.bfloat16 or not out.is_contiguous()):
+            raise ValueError("out [M, H] bfloat16, contiguous, expected")
+        out = torch.empty_like(x) if out is None else out
+        rows = [moe_block(x[m:m + 1], gate_up, down, topk, router=router,
+                          logits=None if logits is None else logits[m:m + 1], shared=shared,
+                          shared_gate=shared_gate, routing=routing, return_logits=return_logits, out=out[m:m + 1],
+                          item_units=item_units, spin_limit=spin_limit, recompute_all=recompute_all)
+                for m in range(M)]
+        if not (routing or return_logits):
+            return out
+        res = (out,) + tuple(torch.cat(parts) for parts in zip(*(r[1:] for r in rows)))
+        return res
     H = x.shape[1]
     E = gate_up.experts
     if gate_up.fmt != down.fmt or down.experts != E or gate_up.cols != H or down.rows != H or gate_up.rows != 2 * down.cols:

@@ -3,8 +3,13 @@
 Bars: unpacked W4 / W6 codes and int8 x int8 group sums bit-exact; F8 group sums (e4m3 x e4m3) within 1e-4 of the
 largest sum (the f8f6f4 MFMA does not keep full float32 precision inside its 128-term sum: measured 1.6e-5 on random
 codes spanning 2^-9 .. 448); routing ids exact and weights within one bf16 ulp; layer outputs (bf16) within max-abs
-2e-2 * max|ref| and rel-L2 1e-2 (the kernel computes SiLU(gate) * up in float32 with a fast exp before quantizing it,
-the oracle in float64; a hidden code at a rounding boundary can differ by one step).
+8e-3 * max|ref| (one bf16 step of any element) and rel-L2 3e-3 for
+int8 / W4A8 / W6A8, 1.5e-2 and 6e-3 for FP8 (the kernel computes SiLU(gate) * up
+in float32 with a fast exp before quantizing it, the oracle in float64, so a hidden code at a rounding boundary can
+differ by one step, which moves a whole output row by about 1e-3 in rel-L2; FP8 adds the MFMA's inner precision and
+e4m3's coarser steps). Measured on 4 seeds per case at H 2048, I 768, 128 experts, top-8 (max-abs / max|ref|, rel-L2):
+int8 1.3e-6 / 1.0e-7 at M=1, 6.3e-4 / 1.4e-5 at M=16; W4A8 0 / 0 at M=1, 1.1e-3 / 2.9e-5 at M=16; W6A8 8.6e-5 /
+6.5e-6 and 1.1e-3 / 4.0e-5; FP8 5.7e-3 / 1.9e-3 and 5.0e-3 / 1.7e-3; one flipped code: int8 M=5, rel-L2 1.1e-3.
 """
 import numpy as np
 import pytest
@@ -119,10 +124,15 @@ def check_layer(fmt, x, logits, gate_up, down, topk=8, fused=True, grid=0, item_
     assert np.all(np.abs(got_w - want_w) <= np.abs(want_w) * 2.0 ** -8 + 1e-30)
     got = bf16_bits_to_f32(bits(out)).astype(np.float64)
     ref = bf16_bits_to_f32(want).astype(np.float64)
-    err = np.abs(got - ref)
-    assert err.max() <= 2e-2 * np.abs(ref).max(), (err.max(), np.abs(ref).max())
-    assert np.linalg.norm(got - ref) <= 1e-2 * np.linalg.norm(ref)
+    assert_layer_close(fmt, got, ref)
     return out
+
+
+def assert_layer_close(fmt, got, ref):
+    max_bar, l2_bar = (1.5e-2, 6e-3) if fmt == formats.FMT_F8 else (8e-3, 3e-3)
+    err = np.abs(got - ref)
+    assert err.max() <= max_bar * np.abs(ref).max(), (err.max(), np.abs(ref).max())
+    assert np.linalg.norm(got - ref) <= l2_bar * np.linalg.norm(ref), np.linalg.norm(got - ref) / np.linalg.norm(ref)
 
 
 @pytest.mark.parametrize("fmt", FMTS)
@@ -387,6 +397,28 @@ def test_block_router_and_shared_expert(fmt):
         assert torch.equal(moe.moe_block(x, gate_up, down, 8, router=router, item_units=units), layer)
 
 
+@pytest.mark.parametrize("fmt", [formats.FMT_I8, formats.FMT_W4])
+def test_block_batched_rows(fmt):
+    """The block for several decode rows (model.py:107-124 over a batch): each row equals the one-row block on that
+    row, bit for bit, with the router's logits computed in the launches or given, and the routing and logits of
+    every row returned in row order."""
+    gate_up, down, _, router, (sg, sd), g = block_inputs(fmt, 37)
+    gen = torch.Generator(device=DEV).manual_seed(38)
+    x = torch.randn((3, 2048), generator=gen, device=DEV).to(torch.bfloat16)
+    out, ids, w, lg = moe.moe_block(x, gate_up, down, 8, router=router, shared=(sg, sd), shared_gate=g, routing=True,
+                                    return_logits=True)
+    assert out.shape == (3, 2048) and ids.shape == (3, 8) and w.shape == (3, 8) and lg.shape == (3, 128)
+    for m in range(3):
+        o1, i1, w1, l1 = moe.moe_block(x[m:m + 1].clone(), gate_up, down, 8, router=router, shared=(sg, sd),
+                                       shared_gate=g, routing=True, return_logits=True)
+        assert torch.equal(out[m:m + 1], o1) and torch.equal(ids[m:m + 1], i1) and torch.equal(w[m:m + 1], w1)
+        assert torch.equal(lg[m:m + 1], l1)
+    given = moe.moe_block(x, gate_up, down, 8, logits=lg, shared=(sg, sd), shared_gate=g)
+    assert torch.equal(given, out)
+    torch.cuda.synchronize()
+    assert moe.status(DEV, 2048, 768) == 0
+
+
 @pytest.mark.parametrize("fmt", FMTS)
 def test_block_reference_shape(fmt):
     """The block at the reference model's shape (256 experts, FFN 512): 256 router workgroups, 512 routed 8-unit
@@ -413,7 +445,11 @@ def test_block_reference_shape(fmt):
     assert np.linalg.norm(got - ref) <= 1e-2 * np.linalg.norm(ref)
 
 
-def test_block_rejects_more_rows():
+def test_block_rejects_bad_shapes():
+    """Logits for another number of rows, or x without a row dimension, are refused before any launch."""
     gate_up, down, x, router, shared, g = block_inputs(formats.FMT_I8, 32)
+    lg = torch.zeros((1, 128), dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(ValueError, match="logits"):
+        moe.moe_block(torch.cat([x, x]), gate_up, down, 8, logits=lg)
     with pytest.raises(ValueError):
-        moe.moe_block(torch.cat([x, x]), gate_up, down, 8, router=router)
+        moe.moe_block(x[0], gate_up, down, 8, router=router)

@@ -2,8 +2,10 @@
 oracle's layer (oracle/a8.py moe_layer), for all four A8 formats.
 
 Bars as for the fused decode layer: routing ids exact and weights within one bf16 ulp; outputs (bf16) within max-abs
-2e-2 * max|ref| and rel-L2 1e-2 (SiLU(gate) * up in float32 with a fast exp before its quantization, the oracle in
-float64: a hidden code on a rounding boundary can differ by one step)."""
+8e-3 * max|ref| (one bf16 step of any element) and rel-L2 3e-3 for
+int8 / W4A8 / W6A8, 1.5e-2 and 6e-3 for FP8 (SiLU(gate) * up in float32 with a
+fast exp before its quantization, the oracle in float64: a hidden code on a rounding boundary can differ by one step;
+FP8 adds the MFMA's inner precision)."""
 import numpy as np
 import pytest
 import torch
@@ -57,10 +59,15 @@ def check(fmt, x, logits, gate_up, down, topk=8):
     got = bf16_bits_to_f32(bits(out)).astype(np.float64)
     ref = bf16_bits_to_f32(want).astype(np.float64)
     assert np.all(np.isfinite(got))
-    err = np.abs(got - ref)
-    assert err.max() <= 2e-2 * np.abs(ref).max(), (err.max(), np.abs(ref).max())
-    assert np.linalg.norm(got - ref) <= 1e-2 * np.linalg.norm(ref)
+    assert_layer_close(fmt, got, ref)
     return out, ids, w
+
+
+def assert_layer_close(fmt, got, ref):
+    max_bar, l2_bar = (1.5e-2, 6e-3) if fmt == formats.FMT_F8 else (8e-3, 3e-3)
+    err = np.abs(got - ref)
+    assert err.max() <= max_bar * np.abs(ref).max(), (err.max(), np.abs(ref).max())
+    assert np.linalg.norm(got - ref) <= l2_bar * np.linalg.norm(ref), np.linalg.norm(got - ref) / np.linalg.norm(ref)
 
 
 @pytest.mark.parametrize("fmt", FMTS)
@@ -95,10 +102,9 @@ def test_prefill_single_row_and_reference_shape():
 
 @pytest.mark.parametrize("fmt", FMTS)
 def test_few_rows_prep_in_one_launch(fmt):
-    """Up to 16 rows route, group and quantize x in one launch (each row quantized once, its codes stored at its
-    pairs' sorted positions); 17 rows take the three wide launches. Each output row depends on its own row only, so
-    T rows and the first T of 17 agree bit for bit; 1, 3, 7 and 16 rows match the oracle, with the routing given as
-    well as computed."""
+    """Up to 16 rows route, quantize x and group in one launch; 17 rows take the wide launches (routing with x's
+    quantization, then the grouping). Each output row depends on its own row only, so T rows and the first T of 17
+    agree bit for bit; 1, 3, 7 and 16 rows match the oracle, with the routing given as well as computed."""
     gate_up, down = banks(fmt)
     gen = torch.Generator(device=DEV).manual_seed(40 + fmt)
     x = torch.randn((17, H), generator=gen, device=DEV).to(torch.bfloat16)
