@@ -85,6 +85,32 @@ def unpack_w6(packed):
     return torch.where(c >= 32, c - 64, c).to(torch.int8).flatten(-2)
 
 
+def pack_w6_le3(q):
+    """int codes [..., K] in [-32, 31] -> uint8 [..., 3K / 4] packed 4 per 3 bytes along K, little-endian, low bits
+    first: value 4j + i at bits 6i .. 6i + 5 of the 24-bit word in bytes 3j .. 3j + 2 (the layout BASELINE's W6A8
+    config names; the A8 W6 bank itself packs 16 per 12 bytes, pack_w6)."""
+    c = (q.to(torch.int32) & 63).unflatten(-1, (-1, 4))
+    word = c[..., 0] | (c[..., 1] << 6) | (c[..., 2] << 12) | (c[..., 3] << 18)
+    return torch.stack((word & 0xFF, (word >> 8) & 0xFF, word >> 16), dim=-1).to(torch.uint8).flatten(-2)
+
+
+def unpack_w6_le3(packed):
+    b = packed.to(torch.int32).unflatten(-1, (-1, 3))
+    word = b[..., 0] | (b[..., 1] << 8) | (b[..., 2] << 16)
+    c = torch.stack([(word >> (6 * i)) & 63 for i in range(4)], dim=-1)
+    return torch.where(c >= 32, c - 64, c).to(torch.int8).flatten(-2)
+
+
+def w6_from_le3(packed):
+    """Rows packed 4 per 3 bytes (pack_w6_le3) -> the A8 W6 layout the kernels read (pack_w6): same codes."""
+    return pack_w6(unpack_w6_le3(packed))
+
+
+def w6_to_le3(packed):
+    """The A8 W6 layout -> rows packed 4 per 3 bytes: same codes."""
+    return pack_w6_le3(unpack_w6(packed))
+
+
 def quantize(w, fmt):
     """Float weights [E, rows, cols] -> A8Bank (on w's device)."""
     experts, rows, cols = w.shape

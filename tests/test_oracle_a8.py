@@ -40,6 +40,23 @@ def test_w6_unit_layout():
     assert all(b[i] == 0 for i in range(12) if i not in (0, 4, 8))
 
 
+def test_w6_le3_layout_and_conversion():
+    """The "4 per 3 bytes, little-endian, low bits first" W6 layout: values 1, -1, 5, -32 are the 24-bit word
+    1 | 63 << 6 | 5 << 12 | 32 << 18; converting it to the A8 W6 layout and back keeps every code, for every byte
+    pattern of the A8 layout."""
+    q = torch.tensor([[1, -1, 5, -32]])
+    word = 1 | 63 << 6 | 5 << 12 | 32 << 18
+    assert formats.pack_w6_le3(q).tolist() == [[word & 0xFF, (word >> 8) & 0xFF, word >> 16]]
+    rng = np.random.default_rng(6)
+    codes = torch.from_numpy(rng.integers(-32, 32, size=(5, 256)))
+    le3 = formats.pack_w6_le3(codes)
+    assert torch.equal(formats.unpack_w6_le3(le3).long(), codes)
+    a8_rows = formats.w6_from_le3(le3)
+    assert np.array_equal(a8.codes(a8_rows.numpy(), a8.FMT_W6), codes.numpy())
+    raw = torch.from_numpy(rng.integers(0, 256, size=(4, 192), dtype=np.uint8))
+    assert torch.equal(formats.w6_from_le3(formats.w6_to_le3(raw)), raw)
+
+
 @pytest.mark.parametrize("fmt", FMTS)
 def test_oracle_quantizer_matches_product_quantizer(fmt):
     """Two independent implementations of each format (numpy here, torch in drama3/formats.py) agree bit for bit."""
