@@ -458,6 +458,7 @@ def run_resident(args, fmt, device):
     gemv, weighted sum; FP8 without the rotations), one row, layers chained in HIP graphs."""
     from drama3 import kernels, offload
     L = args.layers
+    offload.RESIDENT_LAUNCHES = args.launches
     log(f"building {L} layers of {args.format} experts in the reference's layouts")
     layers = make_reference_banks(args.format, L, device)
     logits = make_logits(args.routing, GRAPH_TOKENS, L, 1, device)
@@ -491,8 +492,12 @@ def run_resident(args, fmt, device):
             graphs.append(g)
         ms = timed_replays(graphs, stream, args.steps, args.warmup)
     torch.cuda.synchronize()
-    what = ("routed_decode (2 launches: gate_up with the routing, down)" if args.routed else
-            "route + resident_decode (3 launches: route, gate_up, down)")
+    if args.launches == 1:
+        what = ("routed_decode (1 launch: the routing, gate_up, down)" if args.routed else
+                "route + resident_decode (2 launches: route, then gate_up and down)")
+    else:
+        what = ("routed_decode (2 launches: gate_up with the routing, down)" if args.routed else
+                "route + resident_decode (3 launches: route, gate_up, down)")
     config = {"workload": f"routed-expert MoE layer in the reference's {args.format} layout (float activations, "
                           f"{'routed_decode' if args.routed else 'route + resident_decode'}), decode M=1, hidden {H}, "
                           f"FFN {I}, {E} experts top-{TOPK}, {L} layers chained per token", "rows": 1, "layers": L,
@@ -507,6 +512,8 @@ def main():
     p.add_argument("--warmup", type=int, default=None)
     p.add_argument("--mode", default="decode", choices=["decode", "prefill", "resident", "block", "gemv"])
     p.add_argument("--routed", action="store_true", help="--mode resident: route inside the gate_up launch")
+    p.add_argument("--launches", type=int, default=2, choices=[1, 2],
+                   help="--mode resident: the two-launch decode (default) or the one-launch one")
     p.add_argument("--format", default=None, choices=sorted(FORMATS))
     p.add_argument("--rows", type=int, default=None)
     p.add_argument("--layers", type=int, default=None)

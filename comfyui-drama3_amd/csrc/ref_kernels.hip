@@ -16,6 +16,7 @@
 #include "common.hpp"
 #include "../../include/drama3_moe.h"
 
+#include <algorithm>
 #include <string>
 
 namespace d3 {
@@ -602,6 +603,116 @@ template <int KIND> D3_INLINE float row_scale(const void* bs, const float* bc, s
 // kernels.py:236, or torch's silu for fp8, offload.py:115). x (bf16) is loaded first, then the weight rows, and x is
 // rotated into LDS (per 256 columns unless fp8) while the rows stream: a wave's loads return in issue order, so x
 // never waits behind the weights.
+// A gate_up item's rows for one wave: the gate rows of units `unit`, `unit` + 1 of expert e and the matching up rows
+// (rows e 2I + unit, + 1, e 2I + I + unit, + 1), their bytes and row scales, loaded before anything waits.
+template <int KIND, int K> struct GuRows {
+  RowBytes<KIND, K> rb[4];
+  float sc[4];
+  size_t rows[4];
+};
+template <int KIND, int K>
+D3_INLINE void gu_load(GuRows<KIND, K>& g, const uint8_t* bw, const void* bs, const float* bc, size_t e, int I,
+                       int unit, int lane) {
+  const size_t N = 2 * (size_t)I;
+  g.rows[0] = e * N + unit;
+  g.rows[1] = e * N + unit + 1;
+  g.rows[2] = e * N + I + unit;
+  g.rows[3] = e * N + I + unit + 1;
+#pragma unroll
+  for (int r = 0; r < 4; r++) {
+    load_row<KIND, K>(g.rb[r], bw, (const uint8_t*)bs, g.rows[r], lane);
+    g.sc[r] = row_scale<KIND>(bs, bc, g.rows[r]);
+  }
+}
+
+// x (bf16, this wave's 256-column chunks w, w + 4, ... in xr: lane l holds columns 4l .. 4l + 3 of each) into LDS as
+// float, rotated per 256 columns unless fp8
+template <int KIND, int K>
+D3_INLINE void x_to_lds(const i32x2* xr, float* xs, int w, int lane) {
+#pragma unroll
+  for (int c = 0; c < K / 1024; c++) {
+    float v[4] = {bf16_to_f32((uint32_t)xr[c].x & 0xFFFFu), bf16_to_f32((uint32_t)xr[c].x >> 16),
+                  bf16_to_f32((uint32_t)xr[c].y & 0xFFFFu), bf16_to_f32((uint32_t)xr[c].y >> 16)};
+    if constexpr (KIND != 1) fwht256(v);
+    *(f32x4*)(xs + 256 * (w + 4 * c) + 4 * lane) = f32x4{v[0], v[1], v[2], v[3]};
+  }
+}
+
+// The item's hidden units: lane 0 gets SiLU(gate) * up of unit `unit`, lane 1 of unit + 1 (fp8: torch's silu as
+// offload.py:115 applies it; the others: rotate_rows' SwiGLU, kernels.py:236). x is in LDS (xs), and at 4 bits the
+// gate_up bank's code tables (qtab).
+template <int KIND, int K>
+D3_INLINE float gu_hidden(const GuRows<KIND, K>& g, const float* xs, const uint32_t* qtab, const float* lut,
+                          const void* bs, int lane) {
+  float y[4];
+  if constexpr (KIND == 4) {
+    // the lane's groups v = lane + 64 i of x, once for the four rows, and their sum (values enter as q + 128)
+    using R = RowBytes<KIND, K>;
+    float xv[R::GPL][16];
+    float xsum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < R::GPL; i++) xsum += load_slice<16>(xs + 16 * 64 * i, lane, xv[i]);
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      float acc = 0.0f;
+#pragma unroll
+      for (int i = 0; i < R::GPL; i++) {
+        const i32x4 t = *(const i32x4*)(qtab + 4 * g.rb[r].sb[i]);
+        acc += group_dot_w4((uint32_t)g.rb[r].lw[i].x, (uint32_t)g.rb[r].lw[i].y, t, xv[i]);
+      }
+      y[r] = wave_sum_f32(fmaf(-128.0f, xsum, acc)) * g.sc[r];
+    }
+  } else {
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const float* sblock = KIND == 1 ? (const float*)bs + (g.rows[r] / 128) * (K / 128) : nullptr;
+      y[r] = wave_sum_f32(row_dot<KIND, K>(g.rb[r], xs, sblock, lut, lane)) * g.sc[r];
+    }
+  }
+  const float gt = lane ? y[1] : y[0], up = lane ? y[3] : y[2];
+  const float sig = KIND == 1 ? 1.0f + expf(-gt) : 1.0f + __expf(-gt);
+  return gt / sig * up;
+}
+
+// gu_hidden computed one row at a time (the same operations per row, so the same value, bit for bit), for a caller
+// that holds other registers meanwhile; the rows are loaded here
+template <int KIND, int K>
+D3_INLINE float gu_hidden_lean(const uint8_t* bw, const void* bs, const float* bc, size_t e, int I, int unit,
+                               const float* xs, const uint32_t* qtab, const float* lut, int lane) {
+  const size_t N = 2 * (size_t)I;
+  float y0 = 0.0f, y1 = 0.0f, y2 = 0.0f, y3 = 0.0f;
+#pragma unroll 1
+  for (int r = 0; r < 4; r++) {
+    const size_t row = e * N + (r >= 2 ? I : 0) + unit + (r & 1);
+    RowBytes<KIND, K> rb;
+    load_row<KIND, K>(rb, bw, (const uint8_t*)bs, row, lane);
+    const float sc = row_scale<KIND>(bs, bc, row);
+    float v;
+    if constexpr (KIND == 4) {
+      using R = RowBytes<KIND, K>;
+      float xsum = 0.0f, acc = 0.0f;
+#pragma unroll
+      for (int i = 0; i < R::GPL; i++) {
+        float xv[16];
+        xsum += load_slice<16>(xs + 16 * 64 * i, lane, xv);
+        const i32x4 t = *(const i32x4*)(qtab + 4 * rb.sb[i]);
+        acc += group_dot_w4((uint32_t)rb.lw[i].x, (uint32_t)rb.lw[i].y, t, xv);
+      }
+      v = wave_sum_f32(fmaf(-128.0f, xsum, acc)) * sc;
+    } else {
+      const float* sblock = KIND == 1 ? (const float*)bs + (row / 128) * (K / 128) : nullptr;
+      v = wave_sum_f32(row_dot<KIND, K>(rb, xs, sblock, lut, lane)) * sc;
+    }
+    if (r == 0) y0 = v;
+    else if (r == 1) y1 = v;
+    else if (r == 2) y2 = v;
+    else y3 = v;
+  }
+  const float gt = lane ? y1 : y0, up = lane ? y3 : y2;
+  const float sig = KIND == 1 ? 1.0f + expf(-gt) : 1.0f + __expf(-gt);
+  return gt / sig * up;
+}
+
 //
 // ROUTED: every wave routes the row itself (kernels.py:39-67 on logits [n <= 256] bf16: the top keys and softmax
 // weights as route_kernel computes them, the same key order, the exponentials summed in rank order), running the
@@ -644,56 +755,13 @@ __global__ void __launch_bounds__(256) resident_gu_kernel(const uint16_t* x, con
   } else {
     e = (size_t)ids[j];
   }
-  // rows: gate unit, gate unit + 1, up unit, up unit + 1
-  const size_t N = 2 * (size_t)I;
-  size_t rows[4] = {e * N + unit, e * N + unit + 1, e * N + I + unit, e * N + I + unit + 1};
-  RowBytes<KIND, K> rb[4];
-  float sc[4];
-#pragma unroll
-  for (int r = 0; r < 4; r++) {
-    load_row<KIND, K>(rb[r], bw, (const uint8_t*)bs, rows[r], lane);
-    sc[r] = row_scale<KIND>(bs, bc, rows[r]);
-  }
-#pragma unroll
-  for (int c = 0; c < CH; c++) {
-    float v[4] = {bf16_to_f32((uint32_t)xr[c].x & 0xFFFFu), bf16_to_f32((uint32_t)xr[c].x >> 16),
-                  bf16_to_f32((uint32_t)xr[c].y & 0xFFFFu), bf16_to_f32((uint32_t)xr[c].y >> 16)};
-    if constexpr (KIND != 1) fwht256(v);
-    *(f32x4*)(xs + 256 * (w + 4 * c) + 4 * lane) = f32x4{v[0], v[1], v[2], v[3]};
-  }
+  GuRows<KIND, K> g;
+  gu_load<KIND, K>(g, bw, bs, bc, e, I, unit, lane);
+  x_to_lds<KIND, K>(xr, xs, w, lane);
   if constexpr (KIND == 4) build_qtab(qtab, cb);
   __syncthreads();
-  float y[4];
-  if constexpr (KIND == 4) {
-    // the lane's groups v = lane + 64 i of x, once for the four rows, and their sum (values enter as q + 128)
-    using R = RowBytes<KIND, K>;
-    float xv[R::GPL][16];
-    float xsum = 0.0f;
-#pragma unroll
-    for (int i = 0; i < R::GPL; i++) xsum += load_slice<16>(xs + 16 * 64 * i, lane, xv[i]);
-#pragma unroll
-    for (int r = 0; r < 4; r++) {
-      float acc = 0.0f;
-#pragma unroll
-      for (int i = 0; i < R::GPL; i++) {
-        const i32x4 t = *(const i32x4*)(qtab + 4 * rb[r].sb[i]);
-        acc += group_dot_w4((uint32_t)rb[r].lw[i].x, (uint32_t)rb[r].lw[i].y, t, xv[i]);
-      }
-      y[r] = wave_sum_f32(fmaf(-128.0f, xsum, acc)) * sc[r];
-    }
-  } else {
-#pragma unroll
-    for (int r = 0; r < 4; r++) {
-      const float* sblock = KIND == 1 ? (const float*)bs + (rows[r] / 128) * (K / 128) : nullptr;
-      y[r] = wave_sum_f32(row_dot<KIND, K>(rb[r], xs, sblock, lut, lane)) * sc[r];
-    }
-  }
-  if (lane < 2) {
-    const float g = lane ? y[1] : y[0], u = lane ? y[3] : y[2];
-    // fp8: torch's silu as offload.py:115 applies it; the others: rotate_rows' SwiGLU (kernels.py:236)
-    const float sig = KIND == 1 ? 1.0f + expf(-g) : 1.0f + __expf(-g);
-    h[(size_t)j * I + unit + lane] = g / sig * u;
-  }
+  const float hv = gu_hidden<KIND, K>(g, xs, qtab, lut, bs, lane);
+  if (lane < 2) h[(size_t)j * I + unit + lane] = hv;
 }
 
 // down: grid (H / 4), workgroup (output rows m0 .. m0 + 3) for all k experts, so the routing-weighted sum stays in the
@@ -848,6 +916,310 @@ __global__ void __launch_bounds__(256) resident_dn_codes_kernel(const float* h, 
     if (j < k) total = fmaf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(y[j / 4]), 16 * (j % 4))), wts[j], total);
   }
   if (lane == 0) out[m] = (uint16_t)f32_to_bf16(total);
+}
+
+// ----------------------------------------------------------------------------- resident decode in one launch
+// d3_resident_decode_fused: the resident decode (offload.py:108-123, after route, kernels.py:39-67, when routed) in one
+// launch, with the two launches' arithmetic, bit for bit.
+//   Workgroup i < k I / 8 computes the gate_up item (rank i / (I / 8), units 8 (i % (I / 8)) .. + 7) as
+//   resident_gu_kernel does and publishes each wave's two hidden units as tagged words (value, launch epoch), written
+//   and read device-coherently (common.hpp's hand-off: no counter or flag; a word's epoch tells a current one from a
+//   stale one).
+//   The last H / (4 RW) workgroups of the grid then each take a down block: output rows 4 RW b .. + 4 RW - 1 of every
+//   routed expert, RW per wave. A down block requests its rows' bytes, then gathers the k hidden rows (stale words
+//   read again, coherently, within spin_limit polls), rotates them into LDS and writes out[m] = bf16(sum_j w_j (row .
+//   h_j) scale), experts in order, as resident_dn_kernel / resident_dn_codes_kernel do.
+// No wait can block forever: the down blocks come last in the grid and every workgroup before a down block is a
+// producer that waits for nothing, so each has started (workgroups start in grid order) and will finish. Waits are
+// bounded anyway: one that gives up (the spin limit) makes its down block compute every hidden row itself with the
+// gate_up items' own code (gu_load / gu_hidden), so the output is the same bit for bit; the launch's give-up word
+// stops the other waits soon, and a sticky bit records it (d3_resident_status).
+struct ResidentArgs {
+  const uint16_t* x;
+  const int64_t* ids;     // [k] (not routed)
+  const float* wts;       // [k] (not routed)
+  const uint16_t* logits; // [n] (routed)
+  int n, k;
+  int64_t* ids_out;       // [k] (routed)
+  float* w_out;           // [k] (routed)
+  const uint8_t* gw;
+  const void* gs;
+  const float* gc;
+  const float* gcb;
+  const uint8_t* dw;
+  const void* ds;
+  const float* dc;
+  const float* dcb;
+  uint16_t* out;
+  int H, I;
+  uint64_t* hidden;       // [k, I] tagged words
+  uint64_t* status;       // the launch give-up word
+  uint32_t* sticky;       // bit 0: a wait gave up and the block recomputed (output exact)
+  uint32_t spin_limit;    // 0: every wait gives up at once (test hook)
+  int items, dn_first;    // gate_up items (k I / 8); first down block
+};
+// workspace: the give-up word at byte 0, the sticky bits at byte 256, the hidden words from byte RES_HEADER
+constexpr int RES_HEADER = 512, RES_STICKY = 256;
+
+// one wave's down rows for the int8 / fp8 banks: RW output rows x MAX_K_RES experts (every slot loads a valid row, the
+// last routed expert's again past k)
+template <int KIND, int KI, int RW> struct DnRowsRef {
+  RowBytes<KIND, KI> rb[RW][MAX_K_RES];
+  float sc[RW][MAX_K_RES];
+};
+// the code formats: 2 RW passes of four 16-lane row segments (pass p: output row p / 2, expert 4 (p % 2) + lane / 16),
+// each lane KI / 256 groups of its row
+template <int KIND, int KI, int RW> struct DnRowsCodes {
+  static constexpr int GS = KI / 256;
+  i32x2 lw[2 * RW][GS];
+  uint32_t high[2 * RW][GS], sb[2 * RW][GS];
+  float sc[2 * RW];
+};
+
+template <int KIND, int K, int KI, int RW, int KPL, bool ROUTED>
+__global__ void __launch_bounds__(256, 3) resident_fused_kernel(ResidentArgs a) {
+  constexpr int CH = K / 1024, CPE = KI / 256, HCH = MAX_K_RES * CPE / 4;  // x chunks, hidden chunks per wave
+  constexpr bool CODES = KIND == 4 || KIND == 6;
+  __shared__ float xs[K];
+  __shared__ float lut[1];  // (row_dot reads a codebook only at 4 bits, which go through qtab here)
+  __shared__ uint32_t qtab[KIND == 4 ? QTAB_WORDS : 1];
+  __shared__ float hs[MAX_K_RES][KI];
+  __shared__ int gave_w[4];  // per wave: its wait gave up
+  const int i = blockIdx.x, lane = threadIdx.x & 63, w = threadIdx.x >> 6, k = a.k;
+  const int T = KI / GU_UNITS, u = i / T, unit = (i % T) * GU_UNITS + 2 * w;
+  const uint32_t epoch = launch_epoch();
+  const int hb = i - a.dn_first;
+  const bool has_item = i < a.items, has_down = hb >= 0;
+  // ---- the gate_up item (x first, so it returns ahead of the weight rows)
+  i32x2 xr[CH];
+#pragma unroll
+  for (int c = 0; c < CH; c++) xr[c] = *(const i32x2*)(a.x + 256 * (w + 4 * c) + 4 * lane);
+  f32x4 cb = {0.0f, 0.0f, 0.0f, 0.0f};
+  if constexpr (KIND == 4) cb = *(const f32x4*)(a.gcb + 4 * (threadIdx.x & 3));
+  size_t e = 0;
+  size_t ex[MAX_K_RES];  // the routed experts and their weights (down blocks)
+  float wt[MAX_K_RES];
+  int e_lane = 0;        // lane l: the expert of rank min(l % 8, k - 1) (down blocks)
+  if constexpr (ROUTED) {
+    uint32_t lb[KPL];
+#pragma unroll
+    for (int q = 0; q < KPL; q++) lb[q] = a.logits[min(lane + 64 * q, a.n - 1)];  // lanes past n masked by TopKeys
+    TopKeys<KPL> tk(lb, lane, a.n);
+    const int ur = has_item ? u : -1;
+    tk.rounds(lane, 0, has_down ? k : ur + 1);
+    if (has_item) e = (size_t)route_key_index((uint32_t)__builtin_amdgcn_readlane((int)tk.mine, u));
+    if (has_down) {
+      const float wl = route_weight(tk.mine, lane, k);  // uniform over the wave: reads lanes 0 .. k-1
+#pragma unroll
+      for (int j = 0; j < MAX_K_RES; j++) {
+        ex[j] = (size_t)route_key_index((uint32_t)__builtin_amdgcn_readlane((int)tk.mine, min(j, k - 1)));
+        wt[j] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wl), min(j, k - 1)));
+      }
+      e_lane = route_key_index((uint32_t)__shfl((int)tk.mine, min(lane & 7, k - 1)));
+      if (hb == 0 && w == 0 && lane < k) {
+        a.ids_out[lane] = route_key_index(tk.mine);
+        a.w_out[lane] = wl;
+      }
+    }
+  } else {
+    if (has_item) e = (size_t)a.ids[u];
+    if (has_down) {
+#pragma unroll
+      for (int j = 0; j < MAX_K_RES; j++) {
+        ex[j] = (size_t)a.ids[min(j, k - 1)];
+        wt[j] = a.wts[min(j, k - 1)];
+      }
+      e_lane = (int)a.ids[min(lane & 7, k - 1)];
+    }
+  }
+  if (has_item) {
+    GuRows<KIND, K> g;
+    gu_load<KIND, K>(g, a.gw, a.gs, a.gc, e, KI, unit, lane);
+    x_to_lds<KIND, K>(xr, xs, w, lane);
+    if constexpr (KIND == 4) build_qtab(qtab, cb);
+    __syncthreads();
+    const float hv = gu_hidden<KIND, K>(g, xs, qtab, lut, a.gs, lane);
+    if (lane < 2) put_tagged(a.hidden + (size_t)u * KI + unit + lane, hv, epoch);
+  } else {
+    x_to_lds<KIND, K>(xr, xs, w, lane);  // for a recomputation
+    if constexpr (KIND == 4) build_qtab(qtab, cb);
+  }
+  if (!has_down) return;
+  // ---- the down block: this wave's rows, requested once the gate_up item is done (requested earlier, they
+  // compete with the items' rows, which every down block waits for: measured slower)
+  const int m0 = 4 * RW * hb + RW * w;  // this wave's output rows m0 .. m0 + RW - 1
+  const int seg = lane >> 4, li = lane & 15;
+  DnRowsRef<KIND, KI, RW> dr;
+  DnRowsCodes<KIND, KI, RW> dc;
+  auto load_down = [&]() {
+    if constexpr (CODES) {
+      constexpr int RB = KI * KIND / 8, G = KI / 16;
+#pragma unroll
+      for (int p = 0; p < 2 * RW; p++) {
+        const size_t ej = (size_t)__shfl(e_lane, 4 * (p & 1) + seg);  // this segment's expert
+        const size_t row = ej * a.H + m0 + (p >> 1);
+        const uint8_t* r = a.dw + row * RB;
+#pragma unroll
+        for (int g = 0; g < DnRowsCodes<KIND, KI, RW>::GS; g++) {
+          const int v = li + 16 * g;
+          dc.lw[p][g] = *(const i32x2*)(r + 8 * v);
+          dc.high[p][g] = KIND == 6 ? *(const uint32_t*)(r + KI / 2 + 4 * v) : 0u;
+          dc.sb[p][g] = ((const uint8_t*)a.ds)[row * G + v];
+        }
+        dc.sc[p] = a.dc[row];
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < RW; r++)
+#pragma unroll
+        for (int j = 0; j < MAX_K_RES; j++) {
+          const size_t row = ex[j] * a.H + m0 + r;
+          load_row<KIND, KI>(dr.rb[r][j], a.dw, (const uint8_t*)a.ds, row, lane);
+          dr.sc[r][j] = row_scale<KIND>(a.ds, a.dc, row);
+        }
+    }
+  };
+  load_down();
+  // ---- this wave's hidden chunks c = w + 4 q: expert c / CPE, columns 256 (c % CPE) + 4 lane .. + 3 (chunks past k
+  // read the last expert's again and are not stored); values kept, tags reduced to one stale bit per word
+  auto hidden_src = [&](int q) {
+    const int c = w + 4 * q, jj = min(c / CPE, k - 1);
+    return a.hidden + (size_t)jj * KI + 256 * (c % CPE) + 4 * lane;
+  };
+  float hv[HCH][4];
+  uint32_t stale = 0;
+#pragma unroll
+  for (int q = 0; q < HCH; q++) {
+    const uint64_t* src = hidden_src(q);
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+      const uint64_t word = get_tagged_cached(src + t);
+      hv[q][t] = tagged_value(word);
+      stale |= tag_is(word, epoch) ? 0u : 1u << (4 * q + t);
+    }
+  }
+  bool gave = a.spin_limit == 0u;
+  if (!gave) {
+    uint32_t polls = 0;
+    while (!__all(stale == 0u)) {
+      if (!keep_polling(polls, a.status, a.spin_limit, epoch)) {
+        gave = true;
+        break;
+      }
+#pragma unroll
+      for (int q = 0; q < HCH; q++) {
+        const uint64_t* src = hidden_src(q);
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+          if (stale & (1u << (4 * q + t))) {
+            const uint64_t word = get_tagged(src + t);
+            hv[q][t] = tagged_value(word);
+            stale &= tag_is(word, epoch) ? ~(1u << (4 * q + t)) : ~0u;
+          }
+        }
+      }
+    }
+  }
+  if (lane == 0) gave_w[w] = gave;
+  __syncthreads();
+  if (gave_w[0] | gave_w[1] | gave_w[2] | gave_w[3]) {
+    // a producer did not come in time: every hidden row this block needs, computed here with the gate_up items' own
+    // code (x, and at 4 bits the gate_up bank's tables, are still in LDS), raw into hs, then rotated in place
+    if (threadIdx.x == 0) __hip_atomic_fetch_or(a.sticky, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll 1
+    for (int j = 0; j < k; j++) {
+      size_t ej = ex[0];  // (selected, not indexed: ex stays in registers)
+#pragma unroll
+      for (int q = 1; q < MAX_K_RES; q++) ej = j == q ? ex[q] : ej;
+#pragma unroll 1
+      for (int t = 0; t < T; t++) {
+        const float h = gu_hidden_lean<KIND, K>(a.gw, a.gs, a.gc, ej, KI, t * GU_UNITS + 2 * w, xs, qtab, lut, lane);
+        if (lane < 2) hs[j][t * GU_UNITS + 2 * w + lane] = h;
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < HCH; q++) {
+      const int c = w + 4 * q;
+      if (c < k * CPE) {
+        float* dst = &hs[c / CPE][256 * (c % CPE) + 4 * lane];
+        const f32x4 r = *(const f32x4*)dst;
+        float v[4] = {r.x, r.y, r.z, r.w};
+        if constexpr (KIND != 1) fwht256(v);
+        *(f32x4*)dst = f32x4{v[0], v[1], v[2], v[3]};
+      }
+    }
+  } else {
+#pragma unroll
+    for (int q = 0; q < HCH; q++) {
+      const int c = w + 4 * q;
+      if (c < k * CPE) {
+        float v[4] = {hv[q][0], hv[q][1], hv[q][2], hv[q][3]};
+        if constexpr (KIND != 1) fwht256(v);
+        *(f32x4*)(&hs[c / CPE][256 * (c % CPE) + 4 * lane]) = f32x4{v[0], v[1], v[2], v[3]};
+      }
+    }
+  }
+  __syncthreads();  // every hidden row in hs; the gate_up bank's tables no longer read
+  if constexpr (KIND == 4) {
+    build_qtab(qtab, *(const f32x4*)(a.dcb + 4 * (threadIdx.x & 3)));
+    __syncthreads();
+  }
+  // ---- the products and the weighted sum, as the two-launch down kernels compute them
+  if constexpr (CODES) {
+    constexpr int GS = DnRowsCodes<KIND, KI, RW>::GS;
+    float y[2 * RW];
+#pragma unroll
+    for (int p = 0; p < 2 * RW; p++) {
+      const float* hr = hs[min(4 * (p & 1) + seg, k - 1)];
+      float acc = 0.0f;
+#pragma unroll
+      for (int g = 0; g < GS; g++) {
+        float xv[16];
+        const float xsum = load_slice<16>(hr + 256 * g, li, xv);
+        if constexpr (KIND == 4) {
+          const i32x4 t = *(const i32x4*)(qtab + 4 * dc.sb[p][g]);
+          acc += fmaf(-128.0f, xsum, group_dot_w4((uint32_t)dc.lw[p][g].x, (uint32_t)dc.lw[p][g].y, t, xv));
+        } else {
+          float qv[16];
+          decode_group<KIND>((uint32_t)dc.lw[p][g].x, (uint32_t)dc.lw[p][g].y, dc.high[p][g], dc.sb[p][g], nullptr,
+                             qv);
+#pragma unroll
+          for (int t = 0; t < 16; t++) acc = fmaf(qv[t], xv[t], acc);
+        }
+      }
+      acc += __int_as_float(dpp_i32(__float_as_int(acc), 0xB1));
+      acc += __int_as_float(dpp_i32(__float_as_int(acc), 0x4E));
+      acc += __int_as_float(dpp_i32(__float_as_int(acc), 0x141));
+      acc += __int_as_float(dpp_i32(__float_as_int(acc), 0x140));
+      y[p] = acc * dc.sc[p];
+    }
+#pragma unroll
+    for (int r = 0; r < RW; r++) {
+      float total = 0.0f;
+#pragma unroll
+      for (int j = 0; j < MAX_K_RES; j++)
+        if (j < k)
+          total = fmaf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(y[2 * r + j / 4]), 16 * (j % 4))),
+                       wt[j], total);
+      if (lane == 0) a.out[m0 + r] = (uint16_t)f32_to_bf16(total);
+    }
+  } else {
+#pragma unroll
+    for (int r = 0; r < RW; r++) {
+      float total = 0.0f;
+#pragma unroll
+      for (int j = 0; j < MAX_K_RES; j++) {
+        if (j < k) {
+          const float* sblock =
+              KIND == 1 ? (const float*)a.ds + ((ex[j] * a.H + m0 + r) / 128) * (KI / 128) : nullptr;
+          const float y = wave_sum_f32(row_dot<KIND, KI>(dr.rb[r][j], hs[j], sblock, lut, lane)) * dr.sc[r][j];
+          total = fmaf(y, wt[j], total);
+        }
+      }
+      if (lane == 0) a.out[m0 + r] = (uint16_t)f32_to_bf16(total);
+    }
+  }
 }
 
 // Check of the decodes above on their own: one thread per (row, 16-column group) writes the int8-grid values, through
@@ -1100,6 +1472,93 @@ int d3_resident_decode_routed(int32_t kind, const void* x, const void* logits, i
   if (!logits) return fail("d3_resident_decode_routed: null pointer");
   return resident_launch("d3_resident_decode_routed", kind, x, ids, weights, logits, n, k, gu_w, gu_s, gu_c, dn_w,
                          dn_s, dn_c, gu_codebook, dn_codebook, gu, out, H, I, stream);
+}
+
+int64_t d3_resident_workspace_bytes(int32_t k, int32_t I) {
+  if (k < 1 || k > MAX_K_RES || I < 1) return -1;
+  return RES_HEADER + (int64_t)k * I * 8;
+}
+
+int d3_resident_decode_fused(int32_t kind, const void* x, const void* logits, int32_t n, int32_t k, int64_t* ids,
+                             float* weights, const void* gu_w, const void* gu_s, const float* gu_c, const void* dn_w,
+                             const void* dn_s, const float* dn_c, const float* gu_codebook, const float* dn_codebook,
+                             void* workspace, int64_t workspace_bytes, uint32_t spin_limit, int32_t block_rows,
+                             int32_t recompute_all, void* out, int32_t H, int32_t I, void* stream) {
+  const char* name = "d3_resident_decode_fused";
+  if (!x || !ids || !weights || !gu_w || !gu_s || !dn_w || !dn_s || !workspace || !out)
+    return fail(std::string(name) + ": null pointer");
+  if ((kind == 4 || kind == 6) && (!gu_c || !dn_c)) return fail(std::string(name) + ": codes need channel scales");
+  if (kind == 4 && (!gu_codebook || !dn_codebook)) return fail(std::string(name) + ": 4 bits need codebooks");
+  if (k < 1 || k > MAX_K_RES) return fail(std::string(name) + ": 1 <= k <= 8");
+  if (logits && (n < k || n > ROUTED_MAX_N)) return fail(std::string(name) + ": k <= n <= 256 logits");
+  if (H != 2048 || (I != 512 && I != 768)) return fail(std::string(name) + ": H 2048, I 512 or 768");
+  if (block_rows == 0) block_rows = 4;
+  if (block_rows != 4 && block_rows != 8) return fail(std::string(name) + ": block_rows 4 or 8");
+  if (workspace_bytes < d3_resident_workspace_bytes(k, I)) return fail(std::string(name) + ": workspace too small");
+  if ((uintptr_t)workspace & 255u) return fail(std::string(name) + ": workspace must be 256-byte aligned");
+  ResidentArgs a{};
+  a.x = (const uint16_t*)x;
+  a.ids = ids;
+  a.wts = weights;
+  a.logits = (const uint16_t*)logits;
+  a.n = n;
+  a.k = k;
+  a.ids_out = ids;
+  a.w_out = weights;
+  a.gw = (const uint8_t*)gu_w;
+  a.gs = gu_s;
+  a.gc = gu_c;
+  a.gcb = gu_codebook;
+  a.dw = (const uint8_t*)dn_w;
+  a.ds = dn_s;
+  a.dc = dn_c;
+  a.dcb = dn_codebook;
+  a.out = (uint16_t*)out;
+  a.H = H;
+  a.I = I;
+  a.status = (uint64_t*)workspace;
+  a.sticky = (uint32_t*)((uint8_t*)workspace + RES_STICKY);
+  a.hidden = (uint64_t*)((uint8_t*)workspace + RES_HEADER);
+  a.spin_limit = recompute_all ? 0u : spin_limit ? spin_limit : (1u << 20);
+  a.items = k * (I / GU_UNITS);
+  const int blocks = H / block_rows, grid = std::max(a.items, blocks);
+  a.dn_first = grid - blocks;
+  const hipStream_t s = (hipStream_t)stream;
+#define D3_FUSED_ROUTE(KIND, KI, RW)                                                                                   \
+  do {                                                                                                                 \
+    if (!logits) hipLaunchKernelGGL((resident_fused_kernel<KIND, 2048, KI, RW, 1, false>), dim3(grid), dim3(256), 0, s, a); \
+    else if (n <= 64) hipLaunchKernelGGL((resident_fused_kernel<KIND, 2048, KI, RW, 1, true>), dim3(grid), dim3(256), 0, s, a); \
+    else if (n <= 128) hipLaunchKernelGGL((resident_fused_kernel<KIND, 2048, KI, RW, 2, true>), dim3(grid), dim3(256), 0, s, a); \
+    else hipLaunchKernelGGL((resident_fused_kernel<KIND, 2048, KI, RW, 4, true>), dim3(grid), dim3(256), 0, s, a);      \
+  } while (0)
+#define D3_FUSED(KIND)                                                                                                 \
+  do {                                                                                                                 \
+    if (I == 768 && block_rows == 8) D3_FUSED_ROUTE(KIND, 768, 2);                                                     \
+    else if (I == 768) D3_FUSED_ROUTE(KIND, 768, 1);                                                                   \
+    else if (block_rows == 8) D3_FUSED_ROUTE(KIND, 512, 2);                                                            \
+    else D3_FUSED_ROUTE(KIND, 512, 1);                                                                                 \
+  } while (0)
+  switch (kind) {
+    case 0: D3_FUSED(0); break;
+    case 1: D3_FUSED(1); break;
+    case 4: D3_FUSED(4); break;
+    case 6: D3_FUSED(6); break;
+    default: return fail(std::string(name) + ": kind 0, 1, 4 or 6");
+  }
+#undef D3_FUSED
+#undef D3_FUSED_ROUTE
+  return done(name);
+}
+
+int d3_resident_status(void* workspace, uint32_t* status) {
+  if (!workspace || !status) return fail("d3_resident_status: null pointer");
+  uint8_t* sticky = (uint8_t*)workspace + RES_STICKY;
+  hipError_t e = hipMemcpy(status, sticky, 4, hipMemcpyDeviceToHost);
+  if (e != hipSuccess) return hip_fail(e, "d3_resident_status");
+  const uint32_t zero = 0;
+  e = hipMemcpy(sticky, &zero, 4, hipMemcpyHostToDevice);
+  if (e != hipSuccess) return hip_fail(e, "d3_resident_status");
+  return 0;
 }
 
 int d3_decode_codes(int32_t bits, const void* rows, const void* scales, const float* codebook, int32_t R, int32_t K,

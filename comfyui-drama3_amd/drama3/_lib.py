@@ -76,6 +76,12 @@ SIGNATURES = {
     "d3_resident_decode_routed": (c_int32, [c_int32, c_void_p, c_void_p, c_int32, c_int32, c_void_p, c_void_p,
                                             c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                             c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_void_p]),
+    "d3_resident_workspace_bytes": (c_int64, [c_int32, c_int32]),
+    "d3_resident_decode_fused": (c_int32, [c_int32, c_void_p, c_void_p, c_int32, c_int32, c_void_p, c_void_p,
+                                           c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+                                           c_void_p, c_void_p, c_int64, ctypes.c_uint32, c_int32, c_int32, c_void_p,
+                                           c_int32, c_int32, c_void_p]),
+    "d3_resident_status": (c_int32, [c_void_p, c_void_p]),
     "d3_resolve": (c_int32, [c_void_p, c_int32, c_int32, c_int32, c_int32, c_void_p, c_void_p, c_void_p, c_void_p,
                              c_void_p, c_int32, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                              ctypes.c_double, c_int32, ctypes.c_double, c_void_p]),

@@ -203,6 +203,77 @@ def resident_decode_routed(x, logits, k, banks, kind, codebooks, H, I):
           _p(down.get("s_channel")), _p(codebooks[0]), _p(codebooks[1]), _p(gu), _p(out), H, I, _stream(x))
     return out, ids, weights
 
+# The one-launch resident decode hands the hidden rows between its workgroups through a workspace per (device,
+# stream): zeroed once, never cleared again (every word carries its launch's epoch). One first met under graph capture
+# is allocated and zeroed in the graph (a fill kernel, so each replay clears it again, which changes nothing).
+RESIDENT_MAX_K = 8
+_resident_ws = {}
+
+
+def resident_workspace(device, I, stream=None):
+    """The zeroed workspace of the one-launch resident decode for (device, stream) and FFN size I."""
+    device = torch.device(device)
+    stream = stream if stream is not None else torch.cuda.current_stream(device)
+    key = (device.index, stream.cuda_stream, I)
+    ws = _resident_ws.get(key)
+    if ws is None:
+        with torch.cuda.stream(stream):
+            ws = torch.empty(int(_lib.lib().d3_resident_workspace_bytes(RESIDENT_MAX_K, I)), dtype=torch.uint8,
+                             device=device).zero_()
+        _resident_ws[key] = ws
+    return ws
+
+
+RESIDENT_RECOMPUTED = 1  # a down workgroup stopped waiting and computed the hidden rows itself (the output is exact)
+
+
+def resident_status(device, I, stream=None):
+    """The resident workspace's status bits since the last call (synchronizes, then clears them): 0 or
+    RESIDENT_RECOMPUTED."""
+    import ctypes
+    ws = resident_workspace(device, I, stream)
+    torch.cuda.synchronize(ws.device)
+    value = ctypes.c_uint32(0)
+    _lib.check(_lib.lib().d3_resident_status(ctypes.c_void_p(ws.data_ptr()), ctypes.byref(value)),
+               "d3_resident_status")
+    return value.value
+
+
+def resident_fused_fits(kind, H, I, k):
+    """Whether resident_decode_fused takes this layer shape."""
+    return kind in _RESIDENT_KINDS and H == 2048 and I in (512, 768) and 1 <= k <= RESIDENT_MAX_K
+
+
+def resident_decode_fused(x, banks, kind, codebooks, H, I, ids=None, weights=None, logits=None, k=None,
+                          spin_limit=0, block_rows=0, recompute_all=False):
+    """resident_decode (ids [k] int64, weights [k] float32 given) or resident_decode_routed (logits [n] or [1, n]
+    bfloat16 and k given) in one launch, with the same output, ids and weights bit for bit. Returns out [1, H]
+    bfloat16, or (out, ids [1, k], weights [1, k]) when routed."""
+    code, wkey = _RESIDENT_KINDS[kind]
+    gate_up, down = banks
+    routed = logits is not None
+    out = torch.empty((1, H), dtype=torch.bfloat16, device=x.device)
+    if routed:
+        lg = logits.reshape(-1).contiguous()
+        experts = gate_up[wkey].shape[0] // (2 * I)
+        if lg.shape[0] != experts or down[wkey].shape[0] != experts * H:
+            raise ValueError(f"{lg.shape[0]} logits for banks of {experts} experts: a routed id past the banks would "
+                             f"be read out of bounds")
+        n = lg.shape[0]
+        ids = torch.empty((1, k), dtype=torch.int64, device=x.device)
+        weights = torch.empty((1, k), dtype=torch.float32, device=x.device)
+    else:
+        lg, n = None, 0
+        ids, weights = ids.contiguous(), weights.contiguous()
+        k = ids.shape[-1]
+    ws = resident_workspace(x.device, I)
+    _call("d3_resident_decode_fused", code, _p(x.contiguous()), _p(lg), n, k, _p(ids), _p(weights),
+          _p(gate_up[wkey]), _p(gate_up["scale"]), _p(gate_up.get("s_channel")), _p(down[wkey]), _p(down["scale"]),
+          _p(down.get("s_channel")), _p(codebooks[0]), _p(codebooks[1]), _p(ws), ws.numel(), int(spin_limit),
+          int(block_rows), int(bool(recompute_all)), _p(out), H, I, _stream(x))
+    return (out, ids, weights) if routed else out
+
+
 def fp8_linear(x, weight, scale):
     """nn.functional.linear(x, dequantized weight) for an FP8 weight with one bf16 scale per output row, as the CPU
     path computes it (offload.py:163-167 dequantize_fp8, then the bf16 linear): x [rows, K] bf16 (rows <= 4), weight

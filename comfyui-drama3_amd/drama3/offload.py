@@ -223,21 +223,33 @@ def _rows(kind, fields, num_experts):
     return fields["weight" if kind == "fp8" else "_qdata"].shape[0] // num_experts
 
 
+# Launches of the resident decode where the layer's shape allows: 2 (kernels.resident_decode / resident_decode_routed)
+# or 1 (kernels.resident_decode_fused, the hidden rows handed between workgroups of one launch). Both give the same
+# output, ids and weights, bit for bit. Two is the default: measured on MI355X (us per routed layer, hidden 2048,
+# FFN 768, top-8, layers chained in HIP graphs; two launches / one): int8 17.2 / 17.4, fp8 17.0 / 17.6, W4A8 18.1 /
+# 18.4, W6A8 21.3 / 21.1. The one launch saves the second launch's gap but its down workgroups wait for the hidden
+# rows through device-coherent memory, which costs about as much.
+RESIDENT_LAUNCHES = 2
+
+
 def resident_decode(x, ids, weights, banks, rows, kind, codebooks):
     """One row x [1, H] through experts `ids` [k] of banks held whole on the GPU (expert e in slot e, `rows` per
-    expert) (offload.py:108-123): bf16 [1, H]. Two launches (kernels.resident_decode: gate_up with x rotated in its
-    prologue; down with SwiGLU, the rotation and the weighted sum) where the shapes allow, else the reference's five.
-    Nothing waits on the host."""
+    expert) (offload.py:108-123): bf16 [1, H]. One launch (kernels.resident_decode_fused) or two (gate_up with x
+    rotated in its prologue; down with SwiGLU, the rotation and the weighted sum) where the shapes allow, else the
+    reference's five. Nothing waits on the host."""
     gate_up_rows, down_rows = rows
     H, I = down_rows, gate_up_rows // 2
     if H in (1024, 2048) and I in (512, 768, 1024) and ids.shape[0] <= 8 and x.dtype == torch.bfloat16:
+        if RESIDENT_LAUNCHES == 1 and kernels.resident_fused_fits(kind, H, I, ids.shape[0]):
+            return kernels.resident_decode_fused(x, banks, kind, codebooks, H, I, ids=ids, weights=weights.float())
         return kernels.resident_decode(x, ids, weights.float(), banks, kind, codebooks, H, I)
     return resident_decode_unfused(x, ids, weights, banks, rows, kind, codebooks)
 
 
 def routed_decode(x, logits, k, banks, rows, kind, codebooks):
     """kernels.route(logits, k), then resident_decode (model.py:116-118, then offload.py:108-123), for one row:
-    (out [1, H] bf16, ids [1, k], weights [1, k]). The routing runs inside the gate_up launch where the shapes allow."""
+    (out [1, H] bf16, ids [1, k], weights [1, k]). The routing runs inside the (gate_up) launch where the shapes
+    allow."""
     gate_up_rows, down_rows = rows
     H, I = down_rows, gate_up_rows // 2
     experts = _rows(kind, banks[0], 1) // gate_up_rows
@@ -246,6 +258,8 @@ def routed_decode(x, logits, k, banks, rows, kind, codebooks):
                          f"read out of bounds")
     if (H in (1024, 2048) and I in (512, 768, 1024) and k <= 8 and k <= logits.numel() <= 256
             and x.dtype == torch.bfloat16 and logits.dtype == torch.bfloat16):
+        if RESIDENT_LAUNCHES == 1 and kernels.resident_fused_fits(kind, H, I, k):
+            return kernels.resident_decode_fused(x, banks, kind, codebooks, H, I, logits=logits, k=k)
         return kernels.resident_decode_routed(x, logits, k, banks, kind, codebooks, H, I)
     ids, weights = kernels.route(logits.reshape(1, -1), k)
     return resident_decode(x, ids[0], weights[0], banks, rows, kind, codebooks), ids, weights

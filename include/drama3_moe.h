@@ -238,6 +238,26 @@ int d3_resident_decode_routed(int32_t kind, const void* x, const void* logits, i
                               const void* dn_s, const float* dn_c, const float* gu_codebook, const float* dn_codebook,
                               float* gu, void* out, int32_t H, int32_t I, void* stream);
 
+/* resident_decode in one launch (offload.py:108-123, and with `logits` the routing of kernels.py:39-67 as
+ * d3_resident_decode_routed does it): the same output, ids and weights as the two-launch entries, bit for bit. Each
+ * gate_up workgroup hands its hidden units to the down workgroups of the same launch through `workspace`
+ * (d3_resident_workspace_bytes(k, I) bytes, 256-byte aligned, zeroed once before first use; its words carry the
+ * launch's epoch, so it needs no clearing between launches, on any stream). logits NULL: ids [k] and weights [k] are
+ * inputs; else outputs. H 2048, I 512 or 768. spin_limit: polls a down workgroup waits for a hidden row before it
+ * computes the row itself (0: default; the output is the same either way, see d3_resident_status). block_rows: output
+ * rows per down workgroup, 4 or 8 (0: 4). recompute_all (test hook): every down workgroup computes the hidden rows
+ * itself. Launches that overlap on one workspace race. */
+int64_t d3_resident_workspace_bytes(int32_t k, int32_t I);
+int d3_resident_decode_fused(int32_t kind, const void* x, const void* logits, int32_t n, int32_t k, int64_t* ids,
+                             float* weights, const void* gu_w, const void* gu_s, const float* gu_c, const void* dn_w,
+                             const void* dn_s, const float* dn_c, const float* gu_codebook, const float* dn_codebook,
+                             void* workspace, int64_t workspace_bytes, uint32_t spin_limit, int32_t block_rows,
+                             int32_t recompute_all, void* out, int32_t H, int32_t I, void* stream);
+/* Status bits of a resident workspace since the last call, after its launches completed (synchronous copies; the bits
+ * are cleared): 0, or bit 0 when a down workgroup stopped waiting and computed the hidden rows itself (the output is
+ * exact either way). */
+int d3_resident_status(void* workspace, uint32_t* status);
+
 /* Check of the W4A8 / W6A8 decode on its own (kernels.py:466-483 decode_codes; no entry point of its own there):
  * codes [R, K] int8 of rows [R, K * bits / 8] with scales [R, K / 16]; K % 32 == 0. bits 4 or 6 decode as the GEMVs
  * and grouped products do; bits D3_DECODE_TABLE_W4 decodes 4-bit rows through the per-scale-byte tables the resident

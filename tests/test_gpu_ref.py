@@ -470,6 +470,127 @@ def test_resident_decode_graph_replays(layer):
         assert torch.equal(out, eager)
 
 
+# ------------------------------------------------------------------------------ resident decode in one launch
+def _same_bits(a, b):
+    return torch.equal(a.view(torch.int16), b.view(torch.int16))
+
+
+@pytest.mark.parametrize("block_rows", [4, 8])
+@pytest.mark.parametrize("k", [1, 4, 8])
+def test_resident_decode_fused(layer, k, block_rows):
+    """One launch (the hidden rows handed between its workgroups) against the two launches: the same output bit for
+    bit, with no wait given up, and the oracle's result within the layer bar."""
+    kind, banks, cbs, dbanks, dcbs = layer
+    rng = np.random.default_rng(17 + k)
+    x = numerics.f32_to_bf16_bits(rng.standard_normal((1, H)).astype(np.float32))
+    ids = rng.choice(E, k, replace=False)
+    w = numerics.bf16_round(rng.dirichlet(np.ones(k)).astype(np.float32))
+    xd, idd, wd = dev(x).view(torch.bfloat16), dev(ids), dev(w)
+    want = kernels.resident_decode(xd, idd, wd, dbanks, kind, dcbs, H, I)
+    kernels.resident_status(DEV, I)
+    got = kernels.resident_decode_fused(xd, dbanks, kind, dcbs, H, I, ids=idd, weights=wd, block_rows=block_rows)
+    assert _same_bits(got, want)
+    assert kernels.resident_status(DEV, I) == 0
+    assert_bf16_close(bits_of(got), ref.resident_decode_ref(x, ids, w, banks, (2 * I, H), kind, cbs))
+
+
+@pytest.mark.parametrize("n,k,ties", [(E, 4, False), (E, 8, True), (E, 1, False), (256, 6, False), (100, 8, True)])
+def test_resident_decode_fused_routed(layer, n, k, ties):
+    """The routing inside the one launch: ids, weights and output equal the two-launch routed decode's bit for bit
+    (banks padded to n experts with zeros and logits past the first E far below, as in the two-launch test)."""
+    kind, banks, cbs, dbanks, dcbs = layer
+    if n > E:
+        dbanks = [{name: torch.cat([t, t.new_zeros((t.shape[0] // E * (n - E), *t.shape[1:]))]) for name, t in b.items()}
+                  for b in dbanks]
+    rng = np.random.default_rng(29 + n + k)
+    x = numerics.f32_to_bf16_bits(rng.standard_normal((1, H)).astype(np.float32))
+    lf = rng.integers(-2, 3, n).astype(np.float32) if ties else rng.standard_normal(n).astype(np.float32)
+    lf[E:] = -30.0
+    xd, lg = dev(x).view(torch.bfloat16), dev(numerics.f32_to_bf16_bits(lf)).view(torch.bfloat16)
+    want, wid, ww = kernels.resident_decode_routed(xd, lg, k, dbanks, kind, dcbs, H, I)
+    got, gid, gw = kernels.resident_decode_fused(xd, dbanks, kind, dcbs, H, I, logits=lg, k=k)
+    assert torch.equal(gid, wid) and torch.equal(gw, ww)
+    assert _same_bits(got, want)
+    rid, rw = kernels.route(lg.view(1, n), k)
+    assert torch.equal(gid, rid) and torch.equal(gw, rw)
+
+
+@pytest.mark.parametrize("routed", [False, True])
+def test_resident_decode_fused_recomputes_exactly(layer, routed):
+    """Every wait given up at once (the test hook), and a tiny spin limit: each down workgroup computes the hidden
+    rows itself, and the output is still the two launches' bit for bit; the status reports the recomputation."""
+    kind, banks, cbs, dbanks, dcbs = layer
+    rng = np.random.default_rng(41)
+    x = numerics.f32_to_bf16_bits(rng.standard_normal((1, H)).astype(np.float32))
+    xd = dev(x).view(torch.bfloat16)
+    if routed:
+        lg = dev(numerics.f32_to_bf16_bits(rng.standard_normal(E).astype(np.float32))).view(torch.bfloat16)
+        want = kernels.resident_decode_routed(xd, lg, 6, dbanks, kind, dcbs, H, I)
+        call = dict(logits=lg, k=6)
+    else:
+        ids = dev(rng.choice(E, 5, replace=False))
+        wts = dev(numerics.bf16_round(rng.dirichlet(np.ones(5)).astype(np.float32)))
+        want = (kernels.resident_decode(xd, ids, wts, dbanks, kind, dcbs, H, I),)
+        call = dict(ids=ids, weights=wts)
+    kernels.resident_status(DEV, I)
+    for extra in (dict(recompute_all=True), dict(spin_limit=1, block_rows=8)):
+        got = kernels.resident_decode_fused(xd, dbanks, kind, dcbs, H, I, **call, **extra)
+        got = got if routed else (got,)
+        for a, b in zip(got, want):
+            assert _same_bits(a, b) if a.dtype == torch.bfloat16 else torch.equal(a, b)
+        status = kernels.resident_status(DEV, I)
+        assert status == kernels.RESIDENT_RECOMPUTED if "recompute_all" in extra else status in (0, 1)
+
+
+def test_resident_decode_fused_graph_replays(layer):
+    """The routed one-launch decode captured in a HIP graph: every replay, with new x and logits in place, equals the
+    eager two-launch result (the workspace is not cleared between replays: its words carry each launch's epoch)."""
+    kind, banks, cbs, dbanks, dcbs = layer
+    rng = np.random.default_rng(43)
+    xs = [numerics.f32_to_bf16_bits(rng.standard_normal((1, H)).astype(np.float32)) for _ in range(4)]
+    ls = [numerics.f32_to_bf16_bits(rng.standard_normal(E).astype(np.float32)) for _ in range(4)]
+    x_buf = dev(xs[0]).view(torch.bfloat16).clone()
+    l_buf = dev(ls[0]).view(torch.bfloat16).clone()
+    stream = torch.cuda.Stream(DEV)
+    kernels.resident_workspace(DEV, I, stream)  # before capture
+    stream.wait_stream(torch.cuda.current_stream(DEV))
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        with torch.cuda.graph(g, stream=stream):
+            out, ids, w = kernels.resident_decode_fused(x_buf, dbanks, kind, dcbs, H, I, logits=l_buf, k=4)
+    torch.cuda.current_stream(DEV).wait_stream(stream)
+    for x, lgt in zip(xs, ls):
+        x_buf.copy_(dev(x).view(torch.bfloat16))
+        l_buf.copy_(dev(lgt).view(torch.bfloat16))
+        g.replay()
+        torch.cuda.synchronize()
+        want, wid, ww = kernels.resident_decode_routed(x_buf, l_buf, 4, dbanks, kind, dcbs, H, I)
+        torch.cuda.synchronize()
+        assert _same_bits(out, want) and torch.equal(ids, wid) and torch.equal(w, ww)
+
+
+@pytest.mark.parametrize("kind", ["int8", "w4"])
+def test_resident_decode_fused_ffn_512(kind):
+    """The reference model's own layer shape (FFN 512): one launch against two, bit for bit."""
+    inter = 512
+    rng = np.random.default_rng(47)
+    gu = rng.standard_normal((E, 2 * inter, H)).astype(np.float32) * 0.02
+    dn = rng.standard_normal((E, H, inter)).astype(np.float32) * 0.02
+    if kind == "int8":
+        banks, cbs = (ref.quantize_int8_convrot(gu), ref.quantize_int8_convrot(dn)), (None, None)
+    else:
+        (a, ca), (b, cb) = ref.quantize_codes(gu, 4), ref.quantize_codes(dn, 4)
+        banks, cbs = (a, b), (ca, cb)
+    dbanks = [fields_on(b) for b in banks]
+    dcbs = tuple(None if c is None else dev(c) for c in cbs)
+    x = dev(numerics.f32_to_bf16_bits(rng.standard_normal((1, H)).astype(np.float32))).view(torch.bfloat16)
+    lg = dev(numerics.f32_to_bf16_bits(rng.standard_normal(E).astype(np.float32))).view(torch.bfloat16)
+    want = kernels.resident_decode_routed(x, lg, 8, dbanks, kind, dcbs, H, inter)
+    for block_rows in (4, 8):
+        got = kernels.resident_decode_fused(x, dbanks, kind, dcbs, H, inter, logits=lg, k=8, block_rows=block_rows)
+        assert _same_bits(got[0], want[0]) and torch.equal(got[1], want[1]) and torch.equal(got[2], want[2])
+
+
 @pytest.mark.parametrize("rows,N,K", [(1, 1536, 2048), (3, 1536, 2048), (1, 8 * 1536, 2048), (2, 1024, 512),
                                       (4, 64, 1536)])
 def test_fp8_linear_per_row_scale(rows, N, K):
