@@ -335,9 +335,10 @@ __global__ void __launch_bounds__(256) quantize_rows_kernel(const void* src, int
 
 // ------------------------------------------------------------------------------------------- grouped MFMA products
 // The grouped products, persistent: a work item is (unit, tile): a run of at most UNIT_PAIRS of one expert's pairs
-// against the expert's 16 hidden units (gate_up: its 16 gate and 16 up rows) or 64 output rows (down). A workgroup
-// walks items i, i + grid, ... (experts with most pairs first), loading the next item's weights while it computes
-// the current one. Its 4 waves split K into KS
+// against the expert's 16 hidden units (gate_up: its 16 gate and 16 up rows) or 64 output rows (down). Items come
+// experts with most pairs first; workgroup b of G takes items b, 2G - 1 - b, 2G + b, 4G - 1 - b, ... (rounds of G
+// in alternating direction, so that the workgroups that draw a round's heaviest items draw the next round's
+// lightest). Its 4 waves split K into KS
 // slices (SW steps of 128 columns each) and 16-row tile pairs: a wave holds its two tiles' bytes of its slice in
 // registers and walks the expert's pairs 16 at a time (one MFMA per tile and step; lane l reads weight row l % 16
 // and pair l % 16, lane group l / 16 covers 32 columns of a step); the slices' partial products meet in LDS.
@@ -395,19 +396,15 @@ D3_INLINE void load_weights(Weights<F, Geometry<F, H, I, MODE>::SW>& wt, const P
   }
 }
 
-// One item: the unit's pairs 16 at a time against the weights in `wt`. The next item's weights go into `pref` in the
-// first tile, after that tile's own loads, unconditionally (the current item's rows again when there is no next item,
-// which the cache serves). A wave's vector loads complete in issue order, so the later tiles' activation loads then
-// return behind the prefetch; the prefetch in the last tile instead left each workgroup with no weight rows in
-// flight while its hot items' tiles ran (FP8, 256 rows, Zipf: 172.3 -> 170.9 us per layer with the first tile). The
-// compiler counts loads per path, so a prefetch on one path only would make the products wait for it. For the
-// same reason activation rows are read without a branch (columns past the unit's pairs read its first pair and their
-// products are never stored). colv / colp: per column (pair) of a tile, its epilogue scale and (down) its pair index,
-// staged in LDS by wave 0.
+// One item: the unit's pairs 16 at a time against the weights in `wt`, loaded at the item's start. (A prefetch of the
+// next item's weights into a second buffer during this one held twice the registers and left two workgroups per CU
+// instead of three; without it, FP8 / int8 / W4A8 / W6A8 at 256 rows and Zipf routing ran 168.1 / 167.6 / 127.6 /
+// 160.7 us per layer against 171.0 / 169.0 / 131.9 / 166.7.) Activation rows are read without a branch (columns
+// past the unit's pairs read its first pair and their products are never stored). colv / colp: per column (pair)
+// of a tile, its epilogue scale and (down) its pair index, staged in LDS by wave 0.
 template <int F, int H, int I, int MODE>
 D3_INLINE void compute_tile(const PrefillArgs& a, const int* __restrict__ perm,
-                            const Weights<F, Geometry<F, H, I, MODE>::SW>& wt,
-                            Weights<F, Geometry<F, H, I, MODE>::SW>* pref, int4 unit_n, int it_n, int4 unit, int it,
+                            const Weights<F, Geometry<F, H, I, MODE>::SW>& wt, int4 unit_n, int4 unit, int it,
                             int c0, const float* gs, float (*part)[Geometry<F, H, I, MODE>::KS][16][17], float* colv,
                             int* colp, int& pr) {
   using G = Geometry<F, H, I, MODE>;
@@ -439,7 +436,6 @@ D3_INLINE void compute_tile(const PrefillArgs& a, const int* __restrict__ perm,
     colv[col] = valid ? (MODE == 0 ? a.xs[arow] : a.hs[sp]) : 0.0f;
     if constexpr (MODE == 1) colp[col] = valid ? a.perm[sp] : 0;
   }
-  if (pref) load_weights<F, H, I, MODE>(*pref, a, unit_n.x, it_n, tp, ks, lane);
 #pragma unroll
   for (int t = 0; t < 2; t++) {
     f32x4 y;
@@ -509,8 +505,7 @@ D3_INLINE void compute_tile(const PrefillArgs& a, const int* __restrict__ perm,
 
 template <int F, int H, int I, int MODE>
 D3_INLINE void compute_item(const PrefillArgs& a, const int* __restrict__ perm,
-                            const Weights<F, Geometry<F, H, I, MODE>::SW>& wt,
-                            Weights<F, Geometry<F, H, I, MODE>::SW>& pref, int4 unit_n, int it_n, int4 unit, int it,
+                            const Weights<F, Geometry<F, H, I, MODE>::SW>& wt, int4 unit_n, int4 unit, int it,
                             float* gs, float (*part)[Geometry<F, H, I, MODE>::KS][16][17], float* colv, int* colp,
                             int& pr) {
   using G = Geometry<F, H, I, MODE>;
@@ -526,13 +521,12 @@ D3_INLINE void compute_item(const PrefillArgs& a, const int* __restrict__ perm,
     __syncthreads();
   }
   const int last = (unit.z - 1) & ~15;
-  compute_tile<F, H, I, MODE>(a, perm, wt, &pref, unit_n, it_n, unit, it, 0, gs, part, colv, colp, pr);
-  for (int c0 = 16; c0 <= last; c0 += 16)
-    compute_tile<F, H, I, MODE>(a, perm, wt, nullptr, unit_n, it_n, unit, it, c0, gs, part, colv, colp, pr);
+  for (int c0 = 0; c0 <= last; c0 += 16)
+    compute_tile<F, H, I, MODE>(a, perm, wt, unit_n, unit, it, c0, gs, part, colv, colp, pr);
 }
 
 // units / meta / perm come as separate read-only kernel arguments so that their (uniform) loads are scalar loads:
-// those complete apart from the waves' vector loads, so reading the next unit never waits for a weight prefetch.
+// those complete apart from the waves' vector loads.
 template <int F, int H, int I, int MODE>
 __global__ void __launch_bounds__(256) grouped_kernel(PrefillArgs a, const int4* __restrict__ units,
                                                       const int* __restrict__ meta, const int* __restrict__ perm) {
@@ -547,29 +541,23 @@ __global__ void __launch_bounds__(256) grouped_kernel(PrefillArgs a, const int4*
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, ks = w % G::KS, tp = w / G::KS;
   int4 unit = units[i / G::PER_EXPERT];
   int it = i % G::PER_EXPERT;
-  // two weight buffers in turn (no copy between them, so nothing waits for a prefetch before its data is needed)
-  Weights<F, G::SW> buf0, buf1;
+  const int g = (int)gridDim.x, b = (int)blockIdx.x;
+  int rnd = 0;  // the round of item i
+  auto item_of = [&](int r) { return r * g + ((r & 1) ? g - 1 - b : b); };
+  Weights<F, G::SW> wt;
   // gate_up: this lane's pair (column lane % 16) of the first tile, ahead of the weights
   int pr = MODE == 0 ? perm[unit.y + min(lane & 15, unit.z - 1)] : 0;
-  load_weights<F, H, I, MODE>(buf0, a, unit.x, it, tp, ks, lane);
   while (true) {
-    // the next item (this one again at the end: its rows are in the cache)
-    int in = i + (int)gridDim.x;
-    bool more = in < n_items;
-    int4 unit_n = units[(more ? in : i) / G::PER_EXPERT];
-    int it_n = (more ? in : i) % G::PER_EXPERT;
-    compute_item<F, H, I, MODE>(a, perm, buf0, buf1, unit_n, it_n, unit, it, gs, part, colv, colp, pr);
+    load_weights<F, H, I, MODE>(wt, a, unit.x, it, tp, ks, lane);
+    // the next item (this one again after the last: the next tile's pair is read from it)
+    const int in = item_of(rnd + 1);
+    const bool more = in < n_items;
+    const int4 unit_n = units[(more ? in : i) / G::PER_EXPERT];
+    const int it_n = (more ? in : i) % G::PER_EXPERT;
+    compute_item<F, H, I, MODE>(a, perm, wt, unit_n, unit, it, gs, part, colv, colp, pr);
     if (!more) break;
     i = in;
-    unit = unit_n;
-    it = it_n;
-    in = i + (int)gridDim.x;
-    more = in < n_items;
-    unit_n = units[(more ? in : i) / G::PER_EXPERT];
-    it_n = (more ? in : i) % G::PER_EXPERT;
-    compute_item<F, H, I, MODE>(a, perm, buf1, buf0, unit_n, it_n, unit, it, gs, part, colv, colp, pr);
-    if (!more) break;
-    i = in;
+    rnd++;
     unit = unit_n;
     it = it_n;
   }
