@@ -396,17 +396,21 @@ D3_INLINE void load_weights(Weights<F, Geometry<F, H, I, MODE>::SW>& wt, const P
   }
 }
 
-// One item: the unit's pairs 16 at a time against the weights in `wt`, loaded at the item's start. (A prefetch of the
-// next item's weights into a second buffer during this one held twice the registers and left two workgroups per CU
-// instead of three; without it, FP8 / int8 / W4A8 / W6A8 at 256 rows and Zipf routing ran 168.1 / 167.6 / 127.6 /
-// 160.7 us per layer against 171.0 / 169.0 / 131.9 / 166.7.) Activation rows are read without a branch (columns
-// past the unit's pairs read its first pair and their products are never stored). colv / colp: per column (pair)
-// of a tile, its epilogue scale and (down) its pair index, staged in LDS by wave 0.
+// One item: the unit's pairs 16 at a time against the weights in `wt`. (A prefetch of the next item's weights into a
+// second buffer during this one held twice the registers and left two workgroups per CU instead of three; without
+// it, FP8 / int8 / W4A8 / W6A8 at 256 rows and Zipf routing ran 168.1 / 167.6 / 127.6 / 160.7 us per layer against
+// 171.0 / 169.0 / 131.9 / 166.7.) With row-scaled weights (int8, FP8) the next item's weights go into the same
+// registers in the item's last tile, once its products have read them (`next_wt`), and stream during that tile's
+// epilogue and barriers: 164.6 / 164.3 us against 167.8 / 167.7. (Group-scaled weights kept two workgroups per CU
+// that way: W4A8 128.2 against 125.8.) Activation rows are read without a branch (columns past the unit's pairs
+// read its first pair and their products are never stored). colv / colp: per column (pair) of a tile, its epilogue
+// scale and (down) its pair index, staged in LDS by wave 0.
+constexpr bool late_weights(int F) { return !group_scaled(F); }
 template <int F, int H, int I, int MODE>
 D3_INLINE void compute_tile(const PrefillArgs& a, const int* __restrict__ perm,
                             const Weights<F, Geometry<F, H, I, MODE>::SW>& wt, int4 unit_n, int4 unit, int it,
                             int c0, const float* gs, float (*part)[Geometry<F, H, I, MODE>::KS][16][17], float* colv,
-                            int* colp, int& pr) {
+                            int* colp, int& pr, Weights<F, Geometry<F, H, I, MODE>::SW>* next_wt, int it_n) {
   using G = Geometry<F, H, I, MODE>;
   constexpr int SW = G::SW, KS = G::KS, K = G::K, STEPS = K / 128;
   constexpr int SHIFT = unpack_shift(F);
@@ -470,6 +474,7 @@ D3_INLINE void compute_tile(const PrefillArgs& a, const int* __restrict__ perm,
 #pragma unroll
     for (int i = 0; i < 4; i++) part[2 * tp + t][ks][4 * q + i][col] = y[i];
   }
+  if (next_wt) load_weights<F, H, I, MODE>(*next_wt, a, unit_n.x, it_n, tp, ks, lane);
   __syncthreads();
   if constexpr (MODE == 0) {
     // 16 units x 16 pairs, one per thread
@@ -505,9 +510,9 @@ D3_INLINE void compute_tile(const PrefillArgs& a, const int* __restrict__ perm,
 
 template <int F, int H, int I, int MODE>
 D3_INLINE void compute_item(const PrefillArgs& a, const int* __restrict__ perm,
-                            const Weights<F, Geometry<F, H, I, MODE>::SW>& wt, int4 unit_n, int4 unit, int it,
+                            Weights<F, Geometry<F, H, I, MODE>::SW>& wt, int4 unit_n, int4 unit, int it,
                             float* gs, float (*part)[Geometry<F, H, I, MODE>::KS][16][17], float* colv, int* colp,
-                            int& pr) {
+                            int& pr, bool more, int it_n) {
   using G = Geometry<F, H, I, MODE>;
   constexpr int STEPS = G::K / 128;
   const int tid = threadIdx.x;
@@ -521,8 +526,15 @@ D3_INLINE void compute_item(const PrefillArgs& a, const int* __restrict__ perm,
     __syncthreads();
   }
   const int last = (unit.z - 1) & ~15;
-  for (int c0 = 0; c0 <= last; c0 += 16)
-    compute_tile<F, H, I, MODE>(a, perm, wt, unit_n, unit, it, c0, gs, part, colv, colp, pr);
+  if constexpr (late_weights(F)) {
+    for (int c0 = 0; c0 < last; c0 += 16)
+      compute_tile<F, H, I, MODE>(a, perm, wt, unit_n, unit, it, c0, gs, part, colv, colp, pr, nullptr, 0);
+    compute_tile<F, H, I, MODE>(a, perm, wt, unit_n, unit, it, last, gs, part, colv, colp, pr, more ? &wt : nullptr,
+                                it_n);
+  } else {
+    for (int c0 = 0; c0 <= last; c0 += 16)
+      compute_tile<F, H, I, MODE>(a, perm, wt, unit_n, unit, it, c0, gs, part, colv, colp, pr, nullptr, 0);
+  }
 }
 
 // units / meta / perm come as separate read-only kernel arguments so that their (uniform) loads are scalar loads:
@@ -547,14 +559,15 @@ __global__ void __launch_bounds__(256) grouped_kernel(PrefillArgs a, const int4*
   Weights<F, G::SW> wt;
   // gate_up: this lane's pair (column lane % 16) of the first tile, ahead of the weights
   int pr = MODE == 0 ? perm[unit.y + min(lane & 15, unit.z - 1)] : 0;
+  if (late_weights(F)) load_weights<F, H, I, MODE>(wt, a, unit.x, it, tp, ks, lane);
   while (true) {
-    load_weights<F, H, I, MODE>(wt, a, unit.x, it, tp, ks, lane);
+    if (!late_weights(F)) load_weights<F, H, I, MODE>(wt, a, unit.x, it, tp, ks, lane);
     // the next item (this one again after the last: the next tile's pair is read from it)
     const int in = item_of(rnd + 1);
     const bool more = in < n_items;
     const int4 unit_n = units[(more ? in : i) / G::PER_EXPERT];
     const int it_n = (more ? in : i) % G::PER_EXPERT;
-    compute_item<F, H, I, MODE>(a, perm, wt, unit_n, unit, it, gs, part, colv, colp, pr);
+    compute_item<F, H, I, MODE>(a, perm, wt, unit_n, unit, it, gs, part, colv, colp, pr, more, it_n);
     if (!more) break;
     i = in;
     rnd++;
