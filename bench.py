@@ -246,7 +246,7 @@ def run_decode(args, fmt, device):
               "rows": M, "layers": L, "unique_experts_per_launch": round(sum(unique) / len(unique), 2),
               "waits_recomputed": bool(status & moe.STATUS_RECOMPUTED)}
     kernel = "d3::moe_a8_one_row_kernel" if M == 1 else "d3::moe_a8_kernel" if M < moe.GROUPED_FROM_ROWS else \
-        "d3_moe_a8_prefill (7 launches)"
+        "d3_moe_a8_prefill (6 launches)"
     return ms, total_bytes, launches, args.steps * M, config, kernel, cpu
 
 
@@ -295,7 +295,8 @@ def run_block(args, fmt, device):
     total_bytes = sum(bytes_per_token[i % GRAPH_TOKENS] for i in range(args.steps))
     config = {"workload": f"MoE block (router {E}x{H} bf16, routed {args.format} experts top-{TOPK}, shared expert "
                           f"of FFN {I} with its gate), decode M=1, hidden {H}, FFN {I}, {L} layers chained per token",
-              "rows": 1, "layers": L, "unique_experts_per_launch": round(sum(unique) / len(unique), 2)}
+              "rows": 1, "layers": L, "unique_experts_per_launch": round(sum(unique) / len(unique), 2),
+              "waits_recomputed": bool(status & moe.STATUS_RECOMPUTED)}
     return ms, total_bytes, args.steps * L, args.steps, config, "d3::moe_a8_one_row_kernel (block)", None
 
 
@@ -337,7 +338,7 @@ def run_prefill(args, fmt, device):
               "rows": T, "layers": L, "unique_experts_per_launch": round(sum(unique) / len(unique), 2),
               "mfma_tflops": round(flops * L * args.steps / (ms * 1e-3) / 1e12, 2),
               "mfma_frac_fp8_peak": round(flops * L * args.steps / (ms * 1e-3) / 1e12 / PEAK_FP8_TFLOPS, 5)}
-    return ms, step_bytes * args.steps, args.steps * L, args.steps * T, config, "d3_moe_a8_prefill (7 launches)", cpu
+    return ms, step_bytes * args.steps, args.steps * L, args.steps * T, config, "d3_moe_a8_prefill (6 launches)", cpu
 
 
 def run_gemv(args, fmt, device):

@@ -1142,10 +1142,16 @@ D3_INLINE void one_row_layer(Ctx& cx, int i) {
 
 // The one-row schedule as its own kernel: k I / UT + I / UT + H / 64 workgroups (UT = 8 NSUB hidden units per
 // gate_up item). Compiled for three workgroups per CU (168 registers a lane), which the 8-unit items need (768 of them
-// at k 8, I 768) and the 16-unit ones keep for latency; the recovery calls (recover_down, recover_shared) are held to
-// the same bound, so their registers cost the fast path nothing.
+// at k 8, I 768) and the 16-unit ones keep for latency. The recovery calls (recover_down, recover_shared) keep the
+// recovery's own registers out of the fast path, but the call convention still costs it: with the calls the int8
+// kernel spills some 80 registers a lane (149 without them), one-row int8 14.42 -> 14.71 us. Inlined instead, the
+// recovery spilled more (FP8 one row 14.4 -> 20.5 us).
+// (int8 with 16-unit items, the block's schedule, at two workgroups per CU instead: its 464 workgroups fit either way,
+// and then nothing spills; block int8 25.4 -> 22.0 us. FP8 / W4A8 / W6A8 measured 21.2 / 16.7 / 19.5 us at three
+// and 22.1 / 17.1 / 19.3 at two.)
+constexpr int one_row_blocks_per_cu(int F, int NSUB) { return NSUB == 2 && F == FMT_I8 ? 2 : 3; }
 template <int F, int H, int I, int NSUB>
-__global__ void __launch_bounds__(256, 3) moe_a8_one_row_kernel(MoeA8Args a) {
+__global__ void __launch_bounds__(256, one_row_blocks_per_cu(F, NSUB)) moe_a8_one_row_kernel(MoeA8Args a) {
   Ctx cx = make_ctx(a, H, I);
   if (a.E <= 128) one_row_layer<F, H, I, NSUB, 2>(cx, (int)blockIdx.x);
   else one_row_layer<F, H, I, NSUB, 4>(cx, (int)blockIdx.x);
