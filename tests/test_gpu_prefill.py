@@ -191,8 +191,8 @@ def zipf_logits(T, E, seed):
 
 def test_prefill_fp8_256_rows_zipf():
     """The prefill workload the benchmark times: 256 rows, FP8 experts at H 2048 / I 768, 128 experts, top-8 from
-    Zipf(1.1)-skewed logits. The hottest expert holds more than 128 (row, expert) pairs, so it is split into 64-pair
-    work units (at least 3) that share its weight reads; every one of the 256 rows is checked against the oracle."""
+    Zipf(1.1)-skewed logits. The hottest expert holds more than 128 (row, expert) pairs, so it is split into work
+    units of at most 128 pairs (the multi-unit path); every one of the 256 rows is checked against the oracle."""
     gate_up, down = banks(formats.FMT_F8, E=128, seed=7)
     gen = torch.Generator(device=DEV).manual_seed(70)
     x = torch.randn((256, H), generator=gen, device=DEV).to(torch.bfloat16)
@@ -206,8 +206,8 @@ def test_prefill_fp8_256_rows_zipf():
 @pytest.mark.parametrize("fmt,E,inter,T", [(formats.FMT_I8, 128, 768, 200), (formats.FMT_W4, 128, 768, 260),
                                            (formats.FMT_W6, 256, 512, 160)])
 def test_prefill_experts_over_many_units(fmt, E, inter, T):
-    """Rows biased onto a few experts: two experts take 150 to 260 pairs (3 to 5 work units of 64 pairs each), the
-    rest spread; against the oracle on every row."""
+    """Rows biased onto a few experts: two experts take 150 to 260 pairs (2 or 3 work units of at most 128 pairs),
+    the rest spread; against the oracle on every row."""
     gate_up, down = banks(fmt, E=E, inter=inter, seed=8)
     gen = torch.Generator(device=DEV).manual_seed(80 + fmt)
     x = torch.randn((T, H), generator=gen, device=DEV).to(torch.bfloat16)
