@@ -100,13 +100,21 @@ D3_INLINE void group_pairs(const int64_t* ids, int P, int E, int* counts, int* o
     }
     if (tid == 0) offsets[E] = total;
   }
-  // each used expert's rank (most pairs first), and its unit count at that rank
-  for (int e = tid; e < E; e += 1024) {
-    const int c = cnt[e];
-    if (c > 0) {
+  // each used expert's rank (most pairs first, then lower id): S consecutive lanes per expert, each comparing its
+  // count with E2 / S of the others (E2: E rounded up to a power of two), the partial ranks summed across the S lanes
+  // (a loop over all E per thread was a serial chain of E LDS reads)
+  {
+    int e2 = 1;
+    while (e2 < E) e2 <<= 1;
+    const int S = min(64, min(1024 / e2, e2)), span = e2 / S;
+    const int e = tid / S, s = tid % S;
+    const int c = e < E ? cnt[e] : 0;
+    int rank = 0;
+    for (int f = s * span; f < s * span + span; f++)
+      if (f < E) rank += cnt[f] > c || (cnt[f] == c && f < e);
+    for (int off = S >> 1; off > 0; off >>= 1) rank += __shfl_xor(rank, off);
+    if (e < E && s == 0 && c > 0) {
       atomicAdd(&used, 1);
-      int rank = 0;
-      for (int f = 0; f < E; f++) rank += cnt[f] > c || (cnt[f] == c && f < e);
       by_rank[rank] = e;
     }
   }
