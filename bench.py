@@ -26,7 +26,9 @@ Other workloads of the same layer shape:
 Prints one JSON line: metric (expert-weight GB/s), tokens/s, the roofline of the layer (algorithmic bytes per launch
 / average launch time from HIP events on the replay stream, against 8 TB/s HBM) and the reference's CPU path timed on
 a bounded sample of the same workload on this host. The default run (int8, one row) also times the other formats'
-one-row layers (W4A8 and FP8 with normal routing, W6A8 with Zipf routing) and reports them under config.other_formats.
+one-row layers (W4A8 and FP8 with normal routing, W6A8 with Zipf routing) under config.other_formats, and the other
+workloads of the same layer under config.other_workloads: the single FP8 GEMV, W4A8 with 4 and 16 batched lines,
+and the 256-row FP8 prefill (shorter runs than their own modes; no CPU leg).
 """
 import argparse
 import json
@@ -245,8 +247,9 @@ def run_decode(args, fmt, device):
                           f"{E} experts top-{TOPK} ({args.routing} routing), {L} layers chained per token",
               "rows": M, "layers": L, "unique_experts_per_launch": round(sum(unique) / len(unique), 2),
               "waits_recomputed": bool(status & moe.STATUS_RECOMPUTED)}
+    # the grouped path routes, quantizes and groups up to 16 rows in one launch
     kernel = "d3::moe_a8_one_row_kernel" if M == 1 else "d3::moe_a8_kernel" if M < moe.GROUPED_FROM_ROWS else \
-        "d3_moe_a8_prefill (6 launches)"
+        f"d3_moe_a8_prefill ({5 if M <= 16 else 6} launches)"
     return ms, total_bytes, launches, args.steps * M, config, kernel, cpu
 
 
@@ -338,7 +341,8 @@ def run_prefill(args, fmt, device):
               "rows": T, "layers": L, "unique_experts_per_launch": round(sum(unique) / len(unique), 2),
               "mfma_tflops": round(flops * L * args.steps / (ms * 1e-3) / 1e12, 2),
               "mfma_frac_fp8_peak": round(flops * L * args.steps / (ms * 1e-3) / 1e12 / PEAK_FP8_TFLOPS, 5)}
-    return ms, step_bytes * args.steps, args.steps * L, args.steps * T, config, "d3_moe_a8_prefill (6 launches)", cpu
+    return (ms, step_bytes * args.steps, args.steps * L, args.steps * T, config,
+            f"d3_moe_a8_prefill ({5 if T <= 16 else 6} launches)", cpu)
 
 
 def run_gemv(args, fmt, device):
@@ -418,6 +422,23 @@ def decode_summary(args, fmt_name, routing, device):
             "bytes_per_launch": int(total_bytes / launches),
             "unique_experts_per_launch": config["unique_experts_per_launch"],
             "traffic": measured_traffic("decode", fmt_name, 1)}
+
+
+def workload_summary(args, device, mode, fmt_name, rows, routing, layers, steps):
+    """Another workload of the layer (run as its own mode runs it, with `layers` and `steps`): a dict for
+    config.other_workloads."""
+    sub = argparse.Namespace(**vars(args))
+    sub.mode, sub.format, sub.rows, sub.routing = mode, fmt_name, rows, routing
+    sub.layers, sub.steps, sub.warmup, sub.no_cpu_baseline = layers, steps, 2, True
+    run = {"prefill": run_prefill, "gemv": run_gemv}.get(mode, run_decode)
+    ms, total_bytes, launches, tokens, config, kernel, _ = run(sub, FORMATS[fmt_name], device)
+    torch.cuda.empty_cache()
+    launch_us = ms * 1e3 / launches
+    gbs = total_bytes / launches / (launch_us * 1e-6) / 1e9
+    return {"workload": config["workload"], "mode": mode, "format": fmt_name, "rows": rows, "routing": routing,
+            "us_per_launch": round(launch_us, 3), "gbs": round(gbs, 1), "frac_of_peak": round(gbs / PEAK_GBS, 4),
+            "calls_per_s" if mode == "gemv" else "rows_per_s": round(tokens / (ms * 1e-3), 2),
+            "bytes_per_launch": int(total_bytes / launches), "kernel": kernel}
 
 
 def make_reference_banks(fmt_name, layers, device, seed=3):
@@ -558,6 +579,15 @@ def main():
         for fmt_name, routing in (("w4a8", "normal"), ("fp8", "normal"), ("w6a8", "zipf")):
             log(f"timing {fmt_name} one-row decode ({routing} routing)")
             config["other_formats"].append(decode_summary(args, fmt_name, routing, device))
+        # the other workloads of the layer: the single FP8 GEMV, W4A8 batched lines, the FP8 prefill
+        config["other_workloads"] = []
+        for mode, fmt_name, rows, routing, layers, steps in (("gemv", "fp8", 1, "normal", 128, 50),
+                                                             ("decode", "w4a8", 4, "normal", 48, 30),
+                                                             ("decode", "w4a8", 16, "normal", 48, 30),
+                                                             ("prefill", "fp8", 256, "zipf", 16, 10)):
+            log(f"timing {mode} {fmt_name}, {rows} rows")
+            config["other_workloads"].append(workload_summary(args, device, mode, fmt_name, rows, routing, layers,
+                                                              steps))
     gbs = total_bytes / (ms * 1e-3) / 1e9
     launch_us = ms * 1e3 / launches
     bytes_per_launch = total_bytes / launches
