@@ -1161,7 +1161,7 @@ __global__ void __launch_bounds__(256, one_row_blocks_per_cu(F, NSUB)) moe_a8_on
 // five rows run faster with two per CU (the registers of 256 a lane hold a down item's gathered rows without spills),
 // three rows and six or more with three (more workgroups on the items). Measured (int8, us per layer, two / three per
 // CU): 2 rows 25.4 / 29.4, 3 rows 40.8 / 39.5, 4 rows 45.8 / 49.4, 5 rows 58.6 / 61.9.
-template <int F, int H, int I, int WPC>
+template <int F, int H, int I, int WPC, bool BALANCED>
 __global__ void __launch_bounds__(256, WPC) moe_a8_kernel(MoeA8Args a) {
   constexpr int T = I / 16;
   constexpr int NHB = H / 8;
@@ -1343,6 +1343,40 @@ __global__ void __launch_bounds__(256, WPC) moe_a8_kernel(MoeA8Args a) {
   // rows 45.9 / 43.5; int8 25.2 / 38.8 / 44.6 / 55.8 against 26.3 / 40.3 / 45.3 / 56.7 with the 4-bit choice.
   // (EARLY and LAG are set at the top of the kernel.)
   int parity = 0;
+  if constexpr (BALANCED) {
+    // (four and five rows) The schedule's order is gate_up(chunk c), then down(chunk c - LAG), for c = 0, 1, ... Gate_up
+    // item k (k-th in that order among the gate_up items) and down item k go to workgroup k mod G, so that every
+    // workgroup holds as many down items as any other (round-robin over the merged order gave some three and others
+    // one, and the workgroups with three set the layer's end); each workgroup takes its items in their order in the
+    // schedule, so every wait is still on items of lower index. Measured, us per layer, round-robin / this: 4 rows
+    // int8 43.7 / 42.5, W4A8 33.5 / 32.6, FP8 42.9 / 41.8, W6A8 42.4 / 40.2; 5 rows int8 53.4 / 53.2, W4A8 44.7 /
+    // 40.7, FP8 52.8 / 52.5, W6A8 53.3 / 49.4. With two and three rows it was slower (int8 24.8 / 25.0 and 41.1 /
+    // 53.2; W4A8 20.3 / 23.1 and 31.7 / 37.2): round-robin stays there (the loop below), in a kernel of its own.
+    const int G = (int)gridDim.x, n_gu = U * T;
+    // gate_up items of chunks 0 .. c
+    auto gu_through = [&](int c) { return (cx.chunk_first[min(c, cx.nch - 1) + 1] - cx.chunk_first[0]) * T; };
+    int kg = blockIdx.x, kd = blockIdx.x;
+    while (kg < n_gu || kd < cx.n_dn) {
+      // the two candidates' places in the schedule (units are numbered chunk by chunk)
+      int ig = 0x7fffffff, id = 0x7fffffff;
+      if (kg < n_gu) {
+        int cg = 0;
+        while (cx.chunk_first[cg + 1] <= kg / T) cg++;
+        ig = kg + max(0, cg - LAG) * NHB;
+      }
+      if (kd < cx.n_dn) id = gu_through(kd / NHB + LAG) + kd;
+      if (ig < id) {
+        const int u = kg / T;
+        gate_up_item<F, H, I>(cx, u, kg % T, parity, cx.ulist[u], cx.ucount[u], [] {}, [] {}, a.gu_w, a.gu_s);
+        parity ^= 1;
+        kg += G;
+      } else {
+        down_item<F, H, I, EARLY>(cx, kd / NHB, kd % NHB);
+        kd += G;
+      }
+    }
+    return;
+  }
   for (int item = blockIdx.x; item < n_items; item += gridDim.x) {
     // segments: gate_up(chunk c), then down(chunk c - LAG)
     int base = 0;
@@ -1435,7 +1469,8 @@ using KernelFn = void (*)(MoeA8Args);
 template <int F, int H, int I> KernelFn kernel_of(int unit, int M) {
   if (unit == 8) return moe_a8_one_row_kernel<F, H, I, 1>;
   if (unit == 16) return moe_a8_one_row_kernel<F, H, I, 2>;
-  return (M == 2 || M == 4 || M == 5) ? moe_a8_kernel<F, H, I, 2> : moe_a8_kernel<F, H, I, 3>;
+  if (M == 4 || M == 5) return moe_a8_kernel<F, H, I, 2, true>;
+  return M == 2 ? moe_a8_kernel<F, H, I, 2, false> : moe_a8_kernel<F, H, I, 3, false>;
 }
 
 // the fused layer's kernel for a format, shape and row count: the general schedule (unit 0) or the one-row schedule
