@@ -9,7 +9,7 @@
 // Work decomposition. Every workgroup (4 waves) first routes all M rows (top-k of the router logits, softmax over the
 // k, bf16-rounded weights: kernels.py:39-67's semantics), builds the sorted union of their experts (U of them) and
 // groups it into down chunks of at most 8 experts and 32 (expert, row) pairs. It quantizes the activations into LDS.
-// Then it takes work items round-robin (item, item + gridDim, ...):
+// Then it takes its work items (persistent; the dealing is described below):
 //   gate_up item (u, tile): gate rows 16 tile .. 16 tile + 15 and the matching up rows of expert u, two 16-row MFMA
 //     tiles over K = H (the 4 waves split K); the expert's rows are the MFMA columns. The epilogue applies the scales
 //     and SiLU(gate) * up and publishes 16 hidden units per row.
@@ -18,9 +18,11 @@
 //     weights first, then collects the chunk's hidden rows as they are published, quantizes them into LDS and runs.
 //     When the chunk holds every expert (always for M = 1) it writes the weighted sum straight to `out`; otherwise it
 //     publishes its partial outputs and the last chunk's item for block b sums them.
-// Items are ordered gate_up(chunk 0), gate_up(chunk 1), down(chunk 0), gate_up(chunk 2), down(chunk 1), ...: every
-// wait is on items of lower index. The grid is at most what the device holds at once, so every workgroup is resident
-// and the lowest unfinished item can always run: no wait can block forever. Waits are bounded anyway (spin_limit).
+// Items are ordered every gate_up item, then the down items chunk by chunk, and gate_up item k and down item k go to
+// workgroup k mod gridDim, which takes its items in that order (W4A8 at two rows: gate_up(chunk 0), gate_up(chunk 1),
+// down(chunk 0), gate_up(chunk 2), ..., round-robin): every wait is on items of lower index. The grid is at most what
+// the device holds at once, so every workgroup is resident and the lowest unfinished item can always run: no wait
+// can block forever. Waits are bounded anyway (spin_limit).
 // A wait that gives up (a producer that is not resident, because another kernel holds part of the device, or a
 // spin_limit hit) does not leave the output wrong: its workgroup computes what it waited for itself, with the same
 // code on the same inputs, so the words it uses are the ones the producers would have published, bit for bit. The
@@ -1157,10 +1159,11 @@ __global__ void __launch_bounds__(256, one_row_blocks_per_cu(F, NSUB)) moe_a8_on
   else one_row_layer<F, H, I, NSUB, 4>(cx, (int)blockIdx.x);
 }
 
-// The general schedule, persistent: compiled for WPC workgroups per CU, the grid being as many as fit. Two, four and
-// five rows run faster with two per CU (the registers of 256 a lane hold a down item's gathered rows without spills),
-// three rows and six or more with three (more workgroups on the items). Measured (int8, us per layer, two / three per
-// CU): 2 rows 25.4 / 29.4, 3 rows 40.8 / 39.5, 4 rows 45.8 / 49.4, 5 rows 58.6 / 61.9.
+// The general schedule, persistent: compiled for WPC workgroups per CU, the grid being as many as fit. Two per CU
+// (the registers of 256 a lane hold a down item's gathered rows without spills): with the items dealt by kind
+// (BALANCED, see the item loops at the end) two beat three at every row count measured (int8 3 rows 32.4 / 36.0 us
+// per layer, 6 rows 57.6 / 64.5, 16 rows 143 / 164). (Round-robin, int8, two / three per CU: 2 rows 25.4 / 29.4,
+// 3 rows 40.8 / 39.5, 4 rows 45.8 / 49.4, 5 rows 58.6 / 61.9.)
 template <int F, int H, int I, int WPC, bool BALANCED>
 __global__ void __launch_bounds__(256, WPC) moe_a8_kernel(MoeA8Args a) {
   constexpr int T = I / 16;
@@ -1344,37 +1347,25 @@ __global__ void __launch_bounds__(256, WPC) moe_a8_kernel(MoeA8Args a) {
   // (EARLY and LAG are set at the top of the kernel.)
   int parity = 0;
   if constexpr (BALANCED) {
-    // (four and five rows) The schedule's order is gate_up(chunk c), then down(chunk c - LAG), for c = 0, 1, ... Gate_up
-    // item k (k-th in that order among the gate_up items) and down item k go to workgroup k mod G, so that every
-    // workgroup holds as many down items as any other (round-robin over the merged order gave some three and others
-    // one, and the workgroups with three set the layer's end); each workgroup takes its items in their order in the
-    // schedule, so every wait is still on items of lower index. Measured, us per layer, round-robin / this: 4 rows
-    // int8 43.7 / 42.5, W4A8 33.5 / 32.6, FP8 42.9 / 41.8, W6A8 42.4 / 40.2; 5 rows int8 53.4 / 53.2, W4A8 44.7 /
-    // 40.7, FP8 52.8 / 52.5, W6A8 53.3 / 49.4. With two and three rows it was slower (int8 24.8 / 25.0 and 41.1 /
-    // 53.2; W4A8 20.3 / 23.1 and 31.7 / 37.2): round-robin stays there (the loop below), in a kernel of its own.
-    const int G = (int)gridDim.x, n_gu = U * T;
-    // gate_up items of chunks 0 .. c
-    auto gu_through = [&](int c) { return (cx.chunk_first[min(c, cx.nch - 1) + 1] - cx.chunk_first[0]) * T; };
-    int kg = blockIdx.x, kd = blockIdx.x;
-    while (kg < n_gu || kd < cx.n_dn) {
-      // the two candidates' places in the schedule (units are numbered chunk by chunk)
-      int ig = 0x7fffffff, id = 0x7fffffff;
-      if (kg < n_gu) {
-        int cg = 0;
-        while (cx.chunk_first[cg + 1] <= kg / T) cg++;
-        ig = kg + max(0, cg - LAG) * NHB;
-      }
-      if (kd < cx.n_dn) id = gu_through(kd / NHB + LAG) + kd;
-      if (ig < id) {
-        const int u = kg / T;
-        gate_up_item<F, H, I>(cx, u, kg % T, parity, cx.ulist[u], cx.ucount[u], [] {}, [] {}, a.gu_w, a.gu_s);
-        parity ^= 1;
-        kg += G;
-      } else {
-        down_item<F, H, I, EARLY>(cx, kd / NHB, kd % NHB);
-        kd += G;
-      }
+    // Every gate_up item first, then the down items chunk by chunk; gate_up item k and down item k go to workgroup
+    // k mod G, so that every workgroup holds as many down items as any other, and each workgroup takes its gate_up
+    // items, then its down items (every wait is on items of lower index). Measured, us per layer, the round-robin
+    // schedule below / this: 3 rows int8 41.1 / 32.4, W4A8 31.7 / 25.9, FP8 40.1 / 32.2, W6A8 41.5 / 31.9 (two
+    // workgroups per CU; three with this: 36.0 / 31.1 / 34.2 / 34.2); 4 rows
+    // int8 43.7 / 40.4, W4A8 33.5 / 30.4, FP8 42.9 / 39.6, W6A8 42.4 / 38.3; 5 rows int8 53.4 / 49.8, W4A8 44.7 /
+    // 39.0, FP8 52.8 / 48.9, W6A8 53.3 / 46.9; 2 rows int8 24.8 / 24.1, FP8 24.5 / 23.9, W6A8 24.5 / 24.5, but W4A8
+    // 20.4 / 21.3, which keeps the round-robin; with more rows than the layer runs fused by default (moe_layer
+    // with fused=True, d3_moe_a8_noalloc), int8 6 rows 73.4 / 57.6, 8 rows 88.3 / 69.6, 16 rows 185 / 143; W4A8 6
+    // rows 61.0 / 44.5, 16 rows 149 / 116. (Round-robin over that same order, gate_up items first: 2 rows int8 29.8,
+    // 3 rows 41.3. Dealt as here with each chunk's down items after the next one or two chunks' gate_up items, as
+    // below: 4 rows int8 42.3, W4A8 32.6.)
+    const int G = (int)gridDim.x;
+    for (int k = blockIdx.x; k < U * T; k += G) {
+      const int u = k / T;  // units are numbered chunk by chunk
+      gate_up_item<F, H, I>(cx, u, k % T, parity, cx.ulist[u], cx.ucount[u], [] {}, [] {}, a.gu_w, a.gu_s);
+      parity ^= 1;
     }
+    for (int k = blockIdx.x; k < cx.n_dn; k += G) down_item<F, H, I, EARLY>(cx, k / NHB, k % NHB);
     return;
   }
   for (int item = blockIdx.x; item < n_items; item += gridDim.x) {
@@ -1469,8 +1460,9 @@ using KernelFn = void (*)(MoeA8Args);
 template <int F, int H, int I> KernelFn kernel_of(int unit, int M) {
   if (unit == 8) return moe_a8_one_row_kernel<F, H, I, 1>;
   if (unit == 16) return moe_a8_one_row_kernel<F, H, I, 2>;
-  if (M == 4 || M == 5) return moe_a8_kernel<F, H, I, 2, true>;
-  return M == 2 ? moe_a8_kernel<F, H, I, 2, false> : moe_a8_kernel<F, H, I, 3, false>;
+  // two workgroups per CU, items dealt by kind (BALANCED), except W4A8 at two rows (round-robin)
+  if (M == 2 && F == FMT_W4) return moe_a8_kernel<F, H, I, 2, false>;
+  return moe_a8_kernel<F, H, I, 2, true>;
 }
 
 // the fused layer's kernel for a format, shape and row count: the general schedule (unit 0) or the one-row schedule
