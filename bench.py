@@ -248,7 +248,7 @@ def run_decode(args, fmt, device):
               "rows": M, "layers": L, "unique_experts_per_launch": round(sum(unique) / len(unique), 2),
               "waits_recomputed": bool(status & moe.STATUS_RECOMPUTED)}
     # the grouped path routes, quantizes and groups up to 16 rows in one launch
-    kernel = "d3::moe_a8_one_row_kernel" if M == 1 else "d3::moe_a8_kernel" if M < moe.GROUPED_FROM_ROWS else \
+    kernel = "d3::moe_a8_one_row_kernel" if M == 1 else "d3::moe_a8_kernel" if M < moe.grouped_from_rows(fmt) else \
         f"d3_moe_a8_prefill ({5 if M <= 16 else 6} launches)"
     return ms, total_bytes, launches, args.steps * M, config, kernel, cpu
 

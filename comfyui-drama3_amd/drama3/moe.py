@@ -21,7 +21,7 @@ import threading
 import torch
 
 from . import _lib
-from .formats import A8Bank
+from .formats import FMT_W4, FMT_W6, A8Bank
 
 MAX_ROWS = 16
 MAX_TOPK = 8
@@ -70,21 +70,29 @@ def status(device, H, I, stream=None):
 
 # From this many rows on, moe_layer runs the grouped path (d3_moe_a8_prefill): its persistent grouped products read
 # each expert once for all rows and keep the memory busy, where the fused kernel's items for several rows queue up
-# behind each other. Measured on MI355X (us per layer, fused / grouped): int8 4 rows 42.1 / 52.8, 5 rows 52.5 / 58.3,
-# 6 rows 69.4 / 63.1, 16 rows 171 / 100; W4A8 4 rows 33.4 / 43.0, 5 rows 43.9 / 46.7, 6 rows 55.9 / 49.5.
+# behind each other. Measured on MI355X (us per layer, fused / grouped): int8 5 rows 49.8 / 58.3, 6 rows 57.4 /
+# 56.7, 7 rows 63.0 / 60.9, 8 rows 69.4 / 65.3, 16 rows 143 / 92; FP8 6 rows 56.5 / 56.4, 7 rows 61.7 / 60.8; W4A8
+# 6 rows 44.4 / 46.1, 7 rows 48.1 / 49.2, 8 rows 52.8 / 52.6, 16 rows 116 / 70; W6A8 6 rows 53.7 / 56.5, 7 rows
+# 59.1 / 60.9, 8 rows 63.9 / 66.1. GROUPED_FROM_ROWS holds for int8 and FP8; the 4- and 6-bit formats switch later.
 GROUPED_FROM_ROWS = 6
+GROUPED_FROM_ROWS_BY_FORMAT = {FMT_W4: 8, FMT_W6: 9}
+
+
+def grouped_from_rows(fmt):
+    """The row count from which moe_layer runs the grouped path for banks of format `fmt`."""
+    return GROUPED_FROM_ROWS_BY_FORMAT.get(fmt, GROUPED_FROM_ROWS)
 
 
 def moe_layer(x, logits, gate_up: A8Bank, down: A8Bank, topk, *, routing=False, spin_limit=0, grid=0, out=None,
               fused=None, item_units=0, recompute_all=False):
     """x [M, H] bf16 and router logits [M, E] bf16 (M <= 16) through the routed experts: [M, H] bf16, and with
     `routing` also (ids [M, topk] int64 in descending logit order, weights [M, topk] float32). Fewer than
-    GROUPED_FROM_ROWS rows run the fused one-launch kernel (d3_moe_a8), more the grouped path (moe_prefill); `fused`
-    forces either. `item_units` (8 or 16; 0 picks) sets the one-row schedule's hidden units per gate_up workgroup.
+    grouped_from_rows(format) rows run the fused one-launch kernel (d3_moe_a8), more the grouped path (moe_prefill);
+    `fused` forces either. `item_units` (8 or 16; 0 picks) sets the one-row schedule's hidden units per gate_up workgroup.
     `spin_limit` bounds a workgroup's wait for another's result (0: the library's default; see the module's
     docstring for what happens past it). `recompute_all` is a test hook: every such wait gives up at once."""
     if fused is None:
-        fused = x.shape[0] < GROUPED_FROM_ROWS
+        fused = x.shape[0] < grouped_from_rows(gate_up.fmt)
     if not fused:
         return moe_prefill(x, gate_up, down, topk, logits=logits, routing=routing, out=out)
     if x.dtype != torch.bfloat16 or logits.dtype != torch.bfloat16:

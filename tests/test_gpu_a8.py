@@ -342,10 +342,11 @@ def test_graph_replayed_on_another_stream():
     assert moe.status(DEV, 2048, 768, capture) & moe.STATUS_INVALID == 0
 
 
-@pytest.mark.parametrize("M", [1, 3, 4, 5, 6, 16])
+@pytest.mark.parametrize("M", [1, 3, 4, 5, 6, 7, 8, 16])
 def test_layer_dispatch_matches_oracle(M):
-    """moe_layer's own choice of path (fused below GROUPED_FROM_ROWS rows, grouped from there on) against the
-    oracle."""
+    """moe_layer's own choice of path (fused below grouped_from_rows(format) rows, grouped from there on: W4A8 fused
+    up to 7 rows) against the oracle."""
+    assert moe.grouped_from_rows(formats.FMT_W4) == 8
     gate_up, down = layer_banks(formats.FMT_W4)
     gen = torch.Generator(device=DEV).manual_seed(200 + M)
     x = torch.randn((M, 2048), generator=gen, device=DEV).to(torch.bfloat16)
