@@ -53,7 +53,9 @@ METRIC = "MoE-layer expert-weight HBM GB/s (% of peak) at M=1; decode tokens/s"
 TRAFFIC_PROFILES = {("decode", "int8", 1): ROOT / "profiles" / "moe_a8_int8_m1.md",
                     ("decode", "w4a8", 1): ROOT / "profiles" / "moe_a8_w4a8_m1.md",
                     ("decode", "fp8", 1): ROOT / "profiles" / "moe_a8_fp8_m1.md",
-                    ("decode", "w6a8", 1): ROOT / "profiles" / "moe_a8_w6a8_m1_zipf.md"}
+                    ("decode", "w6a8", 1): ROOT / "profiles" / "moe_a8_w6a8_m1_zipf.md",
+                    ("decode", "w4a8", 4): ROOT / "profiles" / "moe_a8_w4a8_m4.md",
+                    ("prefill", "fp8", 256): ROOT / "profiles" / "moe_a8_prefill_fp8_t256.md"}
 PEAK_GBS = 8000.0
 PEAK_FP8_TFLOPS = 5000.0
 FORMATS = {"int8": formats.FMT_I8, "w4a8": formats.FMT_W4, "w6a8": formats.FMT_W6, "fp8": formats.FMT_F8}
@@ -438,7 +440,8 @@ def workload_summary(args, device, mode, fmt_name, rows, routing, layers, steps)
     return {"workload": config["workload"], "mode": mode, "format": fmt_name, "rows": rows, "routing": routing,
             "us_per_launch": round(launch_us, 3), "gbs": round(gbs, 1), "frac_of_peak": round(gbs / PEAK_GBS, 4),
             "calls_per_s" if mode == "gemv" else "rows_per_s": round(tokens / (ms * 1e-3), 2),
-            "bytes_per_launch": int(total_bytes / launches), "kernel": kernel}
+            "bytes_per_launch": int(total_bytes / launches), "kernel": kernel,
+            "traffic": measured_traffic(mode, fmt_name, rows)}
 
 
 def make_reference_banks(fmt_name, layers, device, seed=3):
