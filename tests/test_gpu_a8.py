@@ -136,7 +136,7 @@ def assert_layer_close(fmt, got, ref):
 
 
 @pytest.mark.parametrize("fmt", FMTS)
-@pytest.mark.parametrize("M", [1, 2, 4, 5, 16])
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 5, 16])
 def test_layer_matches_oracle(fmt, M):
     gate_up, down = layer_banks(fmt)
     gen = torch.Generator(device=DEV).manual_seed(100 + M)
