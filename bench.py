@@ -28,7 +28,7 @@ Prints one JSON line: metric (expert-weight GB/s), tokens/s, the roofline of the
 a bounded sample of the same workload on this host. The default run (int8, one row) also times the other formats'
 one-row layers (W4A8 and FP8 with normal routing, W6A8 with Zipf routing) under config.other_formats, and the other
 workloads of the same layer under config.other_workloads: the single FP8 GEMV, W4A8 with 4 and 16 batched lines,
-and the 256-row FP8 prefill (shorter runs than their own modes; no CPU leg).
+and the 256-row FP8 prefill (as their own modes run them, without the CPU leg).
 """
 import argparse
 import json
@@ -426,12 +426,12 @@ def decode_summary(args, fmt_name, routing, device):
             "traffic": measured_traffic("decode", fmt_name, 1)}
 
 
-def workload_summary(args, device, mode, fmt_name, rows, routing, layers, steps):
-    """Another workload of the layer (run as its own mode runs it, with `layers` and `steps`): a dict for
+def workload_summary(args, device, mode, fmt_name, rows, routing, layers, steps, warmup):
+    """Another workload of the layer, run as its own mode runs it by default (layers, steps, warmup): a dict for
     config.other_workloads."""
     sub = argparse.Namespace(**vars(args))
     sub.mode, sub.format, sub.rows, sub.routing = mode, fmt_name, rows, routing
-    sub.layers, sub.steps, sub.warmup, sub.no_cpu_baseline = layers, steps, 2, True
+    sub.layers, sub.steps, sub.warmup, sub.no_cpu_baseline = layers, steps, warmup, True
     run = {"prefill": run_prefill, "gemv": run_gemv}.get(mode, run_decode)
     ms, total_bytes, launches, tokens, config, kernel, _ = run(sub, FORMATS[fmt_name], device)
     torch.cuda.empty_cache()
@@ -584,13 +584,13 @@ def main():
             config["other_formats"].append(decode_summary(args, fmt_name, routing, device))
         # the other workloads of the layer: the single FP8 GEMV, W4A8 batched lines, the FP8 prefill
         config["other_workloads"] = []
-        for mode, fmt_name, rows, routing, layers, steps in (("gemv", "fp8", 1, "normal", 128, 50),
-                                                             ("decode", "w4a8", 4, "normal", 48, 30),
-                                                             ("decode", "w4a8", 16, "normal", 48, 30),
-                                                             ("prefill", "fp8", 256, "zipf", 16, 10)):
+        for mode, fmt_name, rows, routing, layers, steps, warmup in (("gemv", "fp8", 1, "normal", 128, 100, 8),
+                                                                     ("decode", "w4a8", 4, "normal", 48, 100, 8),
+                                                                     ("decode", "w4a8", 16, "normal", 48, 100, 8),
+                                                                     ("prefill", "fp8", 256, "zipf", 16, 20, 3)):
             log(f"timing {mode} {fmt_name}, {rows} rows")
             config["other_workloads"].append(workload_summary(args, device, mode, fmt_name, rows, routing, layers,
-                                                              steps))
+                                                              steps, warmup))
     gbs = total_bytes / (ms * 1e-3) / 1e9
     launch_us = ms * 1e3 / launches
     bytes_per_launch = total_bytes / launches
