@@ -1350,15 +1350,16 @@ __global__ void __launch_bounds__(256, WPC) moe_a8_kernel(MoeA8Args a) {
     // Every gate_up item first, then the down items chunk by chunk; gate_up item k and down item k go to workgroup
     // k mod G, so that every workgroup holds as many down items as any other, and each workgroup takes its gate_up
     // items, then its down items (every wait is on items of lower index). Measured, us per layer, the round-robin
-    // schedule below / this: 3 rows int8 41.1 / 32.4, W4A8 31.7 / 25.9, FP8 40.1 / 32.2, W6A8 41.5 / 31.9 (two
-    // workgroups per CU; three with this: 36.0 / 31.1 / 34.2 / 34.2); 4 rows
-    // int8 43.7 / 40.4, W4A8 33.5 / 30.4, FP8 42.9 / 39.6, W6A8 42.4 / 38.3; 5 rows int8 53.4 / 49.8, W4A8 44.7 /
-    // 39.0, FP8 52.8 / 48.9, W6A8 53.3 / 46.9; 2 rows int8 24.8 / 24.1, FP8 24.5 / 23.9, W6A8 24.5 / 24.5, but W4A8
-    // 20.4 / 21.3, which keeps the round-robin; with more rows than the layer runs fused by default (moe_layer
-    // with fused=True, d3_moe_a8_noalloc), int8 6 rows 73.4 / 57.6, 8 rows 88.3 / 69.6, 16 rows 185 / 143; W4A8 6
-    // rows 61.0 / 44.5, 16 rows 149 / 116. (Round-robin over that same order, gate_up items first: 2 rows int8 29.8,
-    // 3 rows 41.3. Dealt as here with each chunk's down items after the next one or two chunks' gate_up items, as
-    // below: 4 rows int8 42.3, W4A8 32.6.)
+    // schedule below / this, two workgroups per CU:
+    //   3 rows: int8 41.1 / 32.4, W4A8 31.7 / 25.9, FP8 40.1 / 32.2, W6A8 41.5 / 31.9 (three per CU: 36.0, 31.1,
+    //           34.2, 34.2);
+    //   4 rows: int8 43.7 / 40.4, W4A8 33.5 / 30.4, FP8 42.9 / 39.6, W6A8 42.4 / 38.3;
+    //   5 rows: int8 53.4 / 49.8, W4A8 44.7 / 39.0, FP8 52.8 / 48.9, W6A8 53.3 / 46.9;
+    //   2 rows: int8 24.8 / 24.1, FP8 24.5 / 23.9, W6A8 24.5 / 24.5, but W4A8 20.4 / 21.3 (it keeps the round-robin);
+    //   rows the layer runs fused only when asked (moe_layer with fused=True, d3_moe_a8_noalloc): int8 6 rows
+    //           73.4 / 57.6, 8 rows 88.3 / 69.6, 16 rows 185 / 143; W4A8 6 rows 61.0 / 44.5, 16 rows 149 / 116.
+    // (Round-robin over this same order: 2 rows int8 29.8, 3 rows 41.3. Dealt as here but with each chunk's down
+    // items after the next one or two chunks' gate_up items, as below: 4 rows int8 42.3, W4A8 32.6.)
     const int G = (int)gridDim.x;
     for (int k = blockIdx.x; k < U * T; k += G) {
       const int u = k / T;  // units are numbered chunk by chunk
