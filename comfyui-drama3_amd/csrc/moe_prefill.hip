@@ -293,18 +293,16 @@ __global__ void __launch_bounds__(1024) small_prep_kernel(SmallPrepArgs a) {
 }
 
 // ------------------------------------------------------------------------------------------------------- quantize
-// One wave per output row of WIDTH values (float, or bf16 with BF16), read once into registers: absmax, then codes in
-// the format's storage order and the row's scale. With a row map, output row s reads source row rowmap[s] / k; with
-// pair weights, the scale is multiplied by pair_weight[rowmap2[s]] (the down products then need no other factor).
-template <int F, bool BF16, int WIDTH>
-__global__ void __launch_bounds__(256) quantize_rows_kernel(const void* src, int rows, uint8_t* q, float* scale,
-                                                            const int* rowmap, int k, const float* pair_weight,
-                                                            const int* rowmap2) {
+// The hidden rows h [P, WIDTH] float (by sorted position) quantized for the down products, one wave per row, read once
+// into registers: absmax, then codes in the format's storage order, and the row's scale times the routing weight of
+// its pair (pair_weight[perm[row]]), so that the down products need no other factor.
+template <int F, int WIDTH>
+__global__ void __launch_bounds__(256) quantize_rows_kernel(const float* src, int rows, uint8_t* q, float* scale,
+                                                            const float* pair_weight, const int* perm) {
   constexpr float QMAX = act_qmax<F>();
   constexpr int CHUNKS = WIDTH / 8, CPL = (CHUNKS + 63) / 64;  // 8-value chunks, per lane
-  const int lane = threadIdx.x & 63, out_row = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (out_row >= rows) return;
-  const int row = rowmap ? rowmap[out_row] / k : out_row;  // source row
+  const int lane = threadIdx.x & 63, row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
   float v[CPL][8];
   float amax = 0.0f;
 #pragma unroll
@@ -313,20 +311,10 @@ __global__ void __launch_bounds__(256) quantize_rows_kernel(const void* src, int
 #pragma unroll
     for (int j = 0; j < 8; j++) v[i][j] = 0.0f;
     if (c < CHUNKS) {
-      if constexpr (BF16) {
-        const i32x4 r = *(const i32x4*)((const uint16_t*)src + (size_t)row * WIDTH + 8 * c);
-        const uint32_t w4[4] = {(uint32_t)r.x, (uint32_t)r.y, (uint32_t)r.z, (uint32_t)r.w};
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-          v[i][2 * j] = bf16_to_f32(w4[j] & 0xFFFFu);
-          v[i][2 * j + 1] = bf16_to_f32(w4[j] >> 16);
-        }
-      } else {
-        const f32x4 a = *(const f32x4*)((const float*)src + (size_t)row * WIDTH + 8 * c);
-        const f32x4 b = *(const f32x4*)((const float*)src + (size_t)row * WIDTH + 8 * c + 4);
-        v[i][0] = a.x; v[i][1] = a.y; v[i][2] = a.z; v[i][3] = a.w;
-        v[i][4] = b.x; v[i][5] = b.y; v[i][6] = b.z; v[i][7] = b.w;
-      }
+      const f32x4 a = *(const f32x4*)(src + (size_t)row * WIDTH + 8 * c);
+      const f32x4 b = *(const f32x4*)(src + (size_t)row * WIDTH + 8 * c + 4);
+      v[i][0] = a.x; v[i][1] = a.y; v[i][2] = a.z; v[i][3] = a.w;
+      v[i][4] = b.x; v[i][5] = b.y; v[i][6] = b.z; v[i][7] = b.w;
     }
 #pragma unroll
     for (int j = 0; j < 8; j++) amax = fmaxf(amax, fabsf(v[i][j]));
@@ -336,9 +324,9 @@ __global__ void __launch_bounds__(256) quantize_rows_kernel(const void* src, int
 #pragma unroll
   for (int i = 0; i < CPL; i++) {
     const int c = lane + 64 * i;
-    if (c < CHUNKS) store_act8<F>(q + (size_t)out_row * WIDTH + 8 * c, v[i], inv);
+    if (c < CHUNKS) store_act8<F>(q + (size_t)row * WIDTH + 8 * c, v[i], inv);
   }
-  if (lane == 0) scale[out_row] = amax / QMAX * (pair_weight ? pair_weight[rowmap2[out_row]] : 1.0f);
+  if (lane == 0) scale[row] = amax / QMAX * pair_weight[perm[row]];
 }
 
 // ------------------------------------------------------------------------------------------- grouped MFMA products
@@ -665,11 +653,10 @@ template <int F> void route_quant(const d3_moe_a8_prefill_desc& d, int64_t* ids,
   else launch_route_quant<F, 16>(d, ids, weights, xq, xs, s);
 }
 
-template <int F, bool BF16, int WIDTH> void launch_quantize(const void* src, int rows, uint8_t* q, float* scale,
-                                                             const int* rowmap, int k, const float* pair_weight,
-                                                             const int* rowmap2, hipStream_t s) {
-  hipLaunchKernelGGL((quantize_rows_kernel<F, BF16, WIDTH>), dim3((rows + 3) / 4), dim3(256), 0, s, src, rows, q,
-                     scale, rowmap, k, pair_weight, rowmap2);
+template <int F, int WIDTH> void launch_quantize(const float* src, int rows, uint8_t* q, float* scale,
+                                                 const float* pair_weight, const int* perm, hipStream_t s) {
+  hipLaunchKernelGGL((quantize_rows_kernel<F, WIDTH>), dim3((rows + 3) / 4), dim3(256), 0, s, src, rows, q, scale,
+                     pair_weight, perm);
 }
 
 template <int F, int H, int I> void run(const PrefillArgs& pa, const d3_moe_a8_prefill_desc& d, const Layout& L,
@@ -677,7 +664,7 @@ template <int F, int H, int I> void run(const PrefillArgs& pa, const d3_moe_a8_p
   const int P = d.T * d.topk;
   const int max_units = std::min(d.E, P) + P / UNIT_PAIRS;
   launch_products<F, H, I>(pa, max_units, s);
-  launch_quantize<F, false, I>(ws + L.h, P, ws + L.hq, (float*)(ws + L.hs), nullptr, 1, pa.weights, pa.perm, s);
+  launch_quantize<F, I>((const float*)(ws + L.h), P, ws + L.hq, (float*)(ws + L.hs), pa.weights, pa.perm, s);
   launch_down<F, H, I>(pa, max_units, s);
 }
 
