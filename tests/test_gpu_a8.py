@@ -183,14 +183,28 @@ def test_item_units_checked():
     with pytest.raises(RuntimeError, match="one-row schedule"):
         moe.moe_layer(x, logits, gate_up, down, 8, item_units=8)
 
+@pytest.mark.parametrize("fmt,M", [(formats.FMT_I8, 4), (formats.FMT_W4, 2), (formats.FMT_W6, 5)])
+def test_layer_small_grid(fmt, M):
+    """The general schedule on a grid of 37 workgroups (the caller's `grid`): every workgroup takes many items of both
+    kinds, dealt k mod 37 (W4A8 at two rows: round-robin)."""
+    gate_up, down = layer_banks(fmt)
+    gen = torch.Generator(device=DEV).manual_seed(300 + M)
+    x = torch.randn((M, 2048), generator=gen, device=DEV).to(torch.bfloat16)
+    logits = torch.randn((M, 128), generator=gen, device=DEV).to(torch.bfloat16)
+    full = check_layer(fmt, x, logits, gate_up, down)
+    assert torch.equal(check_layer(fmt, x, logits, gate_up, down, grid=37), full)
+
+
 @pytest.mark.parametrize("fmt", [formats.FMT_I8, formats.FMT_W4])
-def test_layer_shared_experts(fmt):
-    """All 16 rows route to the same 8 experts: each expert has 16 rows as MFMA columns and two experts of a wave
-    exceed 16 columns together (two passes)."""
+@pytest.mark.parametrize("M", [2, 3, 16])
+def test_layer_shared_experts(fmt, M):
+    """All rows route to the same 8 experts: one chunk, so fewer down items than workgroups and every gate_up item
+    carrying several rows; at 16 rows each expert has 16 rows as MFMA columns and two experts of a wave exceed 16
+    columns together (two passes)."""
     gate_up, down = layer_banks(fmt)
     gen = torch.Generator(device=DEV).manual_seed(7)
-    x = torch.randn((16, 2048), generator=gen, device=DEV).to(torch.bfloat16)
-    logits = torch.randn((16, 128), generator=gen, device=DEV)
+    x = torch.randn((M, 2048), generator=gen, device=DEV).to(torch.bfloat16)
+    logits = torch.randn((M, 128), generator=gen, device=DEV)
     logits[:, 40:48] += 20.0
     check_layer(fmt, x, logits.to(torch.bfloat16), gate_up, down)
 
