@@ -63,3 +63,14 @@ def test_descriptor_layout_matches_header(struct, cname, tmp_path):
     assert int(got["size"]) == ctypes.sizeof(struct)
     for f in fields:
         assert int(got[f]) == getattr(struct, f).offset, f
+
+
+def test_grouped_switch_per_format():
+    """moe_layer's switch to the grouped path (host logic): int8 and FP8 from 6 rows, W4A8 from 8, W6A8 from 9, and
+    a row count past the fused kernel's 16 rows always grouped."""
+    from drama3 import formats, moe
+    assert moe.grouped_from_rows(formats.FMT_I8) == moe.GROUPED_FROM_ROWS == 6
+    assert moe.grouped_from_rows(formats.FMT_F8) == 6
+    assert moe.grouped_from_rows(formats.FMT_W4) == 8
+    assert moe.grouped_from_rows(formats.FMT_W6) == 9
+    assert all(moe.grouped_from_rows(f) <= moe.MAX_ROWS + 1 for f in range(4))
