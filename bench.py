@@ -28,7 +28,8 @@ Prints one JSON line: metric (expert-weight GB/s), tokens/s, the roofline of the
 a bounded sample of the same workload on this host. The default run (int8, one row) also times the other formats'
 one-row layers (W4A8 and FP8 with normal routing, W6A8 with Zipf routing) under config.other_formats, and the other
 workloads of the same layer under config.other_workloads: the single FP8 GEMV, W4A8 with 4 and 16 batched lines,
-and the 256-row FP8 prefill (as their own modes run them, without the CPU leg).
+the 256-row FP8 prefill, the reference-format resident decode in the four formats and the int8 block (as their own
+modes run them, without the CPU leg).
 """
 import argparse
 import json
@@ -432,7 +433,8 @@ def workload_summary(args, device, mode, fmt_name, rows, routing, layers, steps,
     sub = argparse.Namespace(**vars(args))
     sub.mode, sub.format, sub.rows, sub.routing = mode, fmt_name, rows, routing
     sub.layers, sub.steps, sub.warmup, sub.no_cpu_baseline = layers, steps, warmup, True
-    run = {"prefill": run_prefill, "gemv": run_gemv}.get(mode, run_decode)
+    sub.routed, sub.launches = True, 2  # resident: the routing in the gate_up launch, as `--routed`
+    run = {"prefill": run_prefill, "gemv": run_gemv, "resident": run_resident, "block": run_block}.get(mode, run_decode)
     ms, total_bytes, launches, tokens, config, kernel, _ = run(sub, FORMATS[fmt_name], device)
     torch.cuda.empty_cache()
     launch_us = ms * 1e3 / launches
@@ -582,12 +584,19 @@ def main():
         for fmt_name, routing in (("w4a8", "normal"), ("fp8", "normal"), ("w6a8", "zipf")):
             log(f"timing {fmt_name} one-row decode ({routing} routing)")
             config["other_formats"].append(decode_summary(args, fmt_name, routing, device))
-        # the other workloads of the layer: the single FP8 GEMV, W4A8 batched lines, the FP8 prefill
+        # the other workloads of the layer: the single FP8 GEMV, W4A8 batched lines, the FP8 prefill; and the drop-in
+        # paths around it: the reference-format resident decode (routing in the gate_up launch) in every format, and
+        # the block with the router and the shared expert
         config["other_workloads"] = []
         for mode, fmt_name, rows, routing, layers, steps, warmup in (("gemv", "fp8", 1, "normal", 128, 100, 8),
                                                                      ("decode", "w4a8", 4, "normal", 48, 100, 8),
                                                                      ("decode", "w4a8", 16, "normal", 48, 100, 8),
-                                                                     ("prefill", "fp8", 256, "zipf", 16, 20, 3)):
+                                                                     ("prefill", "fp8", 256, "zipf", 16, 20, 3),
+                                                                     ("resident", "int8", 1, "normal", 48, 100, 8),
+                                                                     ("resident", "fp8", 1, "normal", 48, 100, 8),
+                                                                     ("resident", "w4a8", 1, "normal", 48, 100, 8),
+                                                                     ("resident", "w6a8", 1, "normal", 48, 100, 8),
+                                                                     ("block", "int8", 1, "normal", 48, 100, 8)):
             log(f"timing {mode} {fmt_name}, {rows} rows")
             config["other_workloads"].append(workload_summary(args, device, mode, fmt_name, rows, routing, layers,
                                                               steps, warmup))
