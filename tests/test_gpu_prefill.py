@@ -217,3 +217,30 @@ def test_prefill_experts_over_many_units(fmt, E, inter, T):
     out, ids, w = check(fmt, x, logits.to(torch.bfloat16), gate_up, down)
     counts = np.bincount(ids.cpu().numpy().ravel(), minlength=E)
     assert counts[5] == T and counts[E - 3] >= 150
+
+
+@pytest.mark.parametrize("fmt", [formats.FMT_F8, formats.FMT_I8])
+def test_prefill_rows_independent_at_1024_rows(fmt):
+    """A size-independent check past the oracle's sizes: each output row depends only on its own row (its routing,
+    its pairs' hidden rows quantized per pair, each MFMA column its own dot products, its k partial outputs summed in
+    routing order), so 1024 rows at once (experts of up to ~900 pairs, split into many work units) equal, bit for
+    bit, the same rows run 16 at a time (the one-launch prep) and one at a time."""
+    gate_up, down = banks(fmt, E=128, seed=11)
+    gen = torch.Generator(device=DEV).manual_seed(110 + fmt)
+    T = 1024
+    x = torch.randn((T, H), generator=gen, device=DEV).to(torch.bfloat16)
+    logits = zipf_logits(T, 128, seed=111 + fmt)
+    out, ids, w = moe.moe_prefill(x, gate_up, down, 8, logits=logits, routing=True)
+    counts = np.bincount(ids.cpu().numpy().ravel(), minlength=128)
+    assert counts.max() > 4 * 128  # the hottest expert spans five or more work units
+    hot = int(np.argmax(counts))
+    hot_rows = torch.nonzero((ids == hot).any(dim=1)).flatten()[:16]
+    pick = torch.randperm(T, generator=torch.Generator().manual_seed(5))[:16].to(DEV)
+    for rows in (torch.arange(16, device=DEV), pick, hot_rows):
+        part, pids, pw = moe.moe_prefill(x[rows].contiguous(), gate_up, down, 8, logits=logits[rows].contiguous(),
+                                         routing=True)
+        assert torch.equal(pids, ids[rows]) and torch.equal(pw, w[rows])
+        assert torch.equal(part, out[rows])
+    for r in (0, int(hot_rows[0])):
+        one = moe.moe_prefill(x[r:r + 1], gate_up, down, 8, logits=logits[r:r + 1])
+        assert torch.equal(one, out[r:r + 1])
