@@ -87,8 +87,8 @@ def unpack_w6(packed):
 
 def pack_w6_le3(q):
     """int codes [..., K] in [-32, 31] -> uint8 [..., 3K / 4] packed 4 per 3 bytes along K, little-endian, low bits
-    first: value 4j + i at bits 6i .. 6i + 5 of the 24-bit word in bytes 3j .. 3j + 2 (the layout BASELINE's W6A8
-    config names; the A8 W6 bank itself packs 16 per 12 bytes, pack_w6)."""
+    first: value 4j + i at bits 6i .. 6i + 5 of the 24-bit word in bytes 3j .. 3j + 2 (the layout the W6A8 sweep
+    workload is described with; the A8 W6 bank itself packs 16 per 12 bytes, pack_w6)."""
     c = (q.to(torch.int32) & 63).unflatten(-1, (-1, 4))
     word = c[..., 0] | (c[..., 1] << 6) | (c[..., 2] << 12) | (c[..., 3] << 18)
     return torch.stack((word & 0xFF, (word >> 8) & 0xFF, word >> 16), dim=-1).to(torch.uint8).flatten(-2)

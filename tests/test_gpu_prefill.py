@@ -178,8 +178,9 @@ def test_prefill_graph_replays(rows):
 
 
 def zipf_logits(T, E, seed):
-    """Router logits [T, E] bf16 drawn as bench.py draws config 5's: log p(rank) with p(rank) ~ rank^-1.1 over a seeded
-    permutation of the experts, plus Gumbel noise, so each row's top-k is k distinct experts drawn from Zipf(1.1)."""
+    """Router logits [T, E] bf16 drawn as bench.py draws the 256-row prefill's: log p(rank) with p(rank) ~ rank^-1.1
+    over a seeded permutation of the experts, plus Gumbel noise, so each row's top-k is k distinct experts drawn from
+    Zipf(1.1)."""
     gen = torch.Generator(device=DEV).manual_seed(seed)
     logp = -1.1 * torch.log(torch.arange(1, E + 1, device=DEV, dtype=torch.float32))
     perm = torch.randperm(E, generator=gen, device=DEV)

@@ -268,7 +268,7 @@ def test_resident_prefill_ref_equals_decode_per_row():
         assert np.all(np.abs(a - b) <= 2.0 ** -7 * np.abs(b) + 1e-6)
 
 
-# ------------------------------------------------------------------------------------------- FP8 rows (config 1)
+# ---------------------------------------------------------- FP8 rows (one e4m3 weight, a bf16 scale per output row)
 def _fp8_rows_case(N=96, K=512, seed=0):
     rng = np.random.default_rng(seed)
     x = numerics.f32_to_bf16_bits(rng.standard_normal((2, K)).astype(np.float32))
