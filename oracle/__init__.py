@@ -1,4 +1,4 @@
-"""Oracle: CPU restatements of the routed-expert path's arithmetic, used only as the checker.
+"""Oracle: CPU restatements of the routed-expert path's arithmetic, used only to check results.
 
 Test infrastructure. Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg import anything from here,
 and only to check results or to time the reference's CPU path; the product (comfyui-drama3_amd/drama3) never does.

@@ -1,7 +1,7 @@
 """Oracle for the reference's own expert kernels and formats (test infrastructure only): drama3/kernels.py's SOURCE
 and drama3/offload.py's resident decode / prefill, restated in numpy (float64 sums unless a step is exact in float32).
 
-Only tests/, __graft_entry__.smoke() and bench.py's CPU leg import this, as the checker. Every function cites the
+Only tests/, __graft_entry__.smoke() and bench.py's CPU leg import this, to check results. Every function cites the
 reference lines it follows. What pins each one (tests/test_oracle_reference.py):
   e4m3_ref         exhaustive over 256 codes against OCP e4m3fn (torch.float8_e4m3fn) except the NaN codes, which the
                    reference's bit placement reads as +-480 (checked as such)
