@@ -1161,8 +1161,8 @@ __global__ void __launch_bounds__(256, one_row_blocks_per_cu(F, NSUB)) moe_a8_on
 
 // The general schedule, persistent: compiled for WPC workgroups per CU, the grid being as many as fit. Two per CU
 // (the registers of 256 a lane hold a down item's gathered rows without spills): with the items dealt by kind
-// (BALANCED, see the item loops at the end) two beat three at every row count measured (int8 3 rows 32.4 / 36.0 us
-// per layer, 6 rows 57.6 / 64.5, 16 rows 143 / 164). (Round-robin, int8, two / three per CU: 2 rows 25.4 / 29.4,
+// (BALANCED, see the item loops at the end) two beat three at every row count measured (int8 2 rows 24.1 / 27.9 us
+// per layer, 3 rows 32.4 / 36.0, 6 rows 57.6 / 64.5, 16 rows 143 / 164). (Round-robin, int8, two / three per CU: 2 rows 25.4 / 29.4,
 // 3 rows 40.8 / 39.5, 4 rows 45.8 / 49.4, 5 rows 58.6 / 61.9.)
 template <int F, int H, int I, int WPC, bool BALANCED>
 __global__ void __launch_bounds__(256, WPC) moe_a8_kernel(MoeA8Args a) {
