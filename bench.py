@@ -32,6 +32,7 @@ the 256-row FP8 prefill, the reference-format resident decode in the four format
 modes run them, without the CPU leg).
 """
 import argparse
+import ctypes
 import json
 import math
 import os
@@ -411,6 +412,87 @@ def run_gemv(args, fmt, device):
     return ms, bytes_per_call * launches, launches, launches, config, "d3::gemv_fp8_rows_kernel", cpu
 
 
+STREAM_BYTES = 2 << 30            # the streaming-read buffer: 2 GiB, far beyond the 256 MB Infinity Cache
+STREAM_GRIDS = (2048, 8192, 16384, 32768, 65536)
+ONE_SHOT_BYTES = {"w4a8 layer (19.5 MB)": 8 * 2_433_024, "int8 layer (37.8 MB)": 8 * 4_725_760}
+EMPTY_GRID = 768                  # the one-row layer's grid
+
+
+def measure_ceiling(device, layers=48, steps=50, warmup=5):
+    """What the device allows a layer, measured with the library's probe kernels (d3_stream_read, d3_empty_launch):
+    - stream_read_gbs: one 2 GiB buffer read once per launch, the best of a few grids, 10 launches timed;
+    - one_shot: `layers` distinct buffers of a layer's bytes, one read launch each, chained in a graph as the layers
+      are: us per launch (the gap between graph nodes included) and GB/s, at grids of one, four and eight 16-byte
+      loads per thread;
+    - empty_launch_us: `layers` empty launches of the one-row layer's grid in a graph, us per node."""
+    from drama3 import _lib
+    lib = _lib.lib()
+    sink = torch.zeros(4, dtype=torch.int32, device=device)
+    stream = torch.cuda.Stream(device)
+    stream.wait_stream(torch.cuda.current_stream(device))
+    handle = ctypes.c_void_p(stream.cuda_stream)
+    out = {}
+    with torch.cuda.stream(stream):
+        big = torch.ones(STREAM_BYTES // 4, dtype=torch.int32, device=device)
+        best = None
+        per_grid = {}
+        for grid in STREAM_GRIDS:
+            for _ in range(3):
+                _lib.check(lib.d3_stream_read(big.data_ptr(), STREAM_BYTES, sink.data_ptr(), grid, handle), "read")
+            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            start.record(stream)
+            for _ in range(10):
+                _lib.check(lib.d3_stream_read(big.data_ptr(), STREAM_BYTES, sink.data_ptr(), grid, handle), "read")
+            end.record(stream)
+            end.synchronize()
+            gbs = 10 * STREAM_BYTES / (start.elapsed_time(end) * 1e-3) / 1e9
+            per_grid[grid] = round(gbs, 1)
+            best = gbs if best is None else max(best, gbs)
+        del big
+        out["stream_read_gbs"] = round(best, 1)
+        out["stream_read_gbs_by_grid"] = per_grid
+        one_shot = {}
+        for name, nbytes in ONE_SHOT_BYTES.items():
+            nbytes -= nbytes % 16
+            bufs = [torch.ones(nbytes // 4, dtype=torch.int32, device=device) for _ in range(layers)]
+            runs = {}
+            for loads in (1, 4, 8):
+                grid = -(-nbytes // (16 * 256 * loads))
+                for b in bufs:  # outside capture first, as the graph will run it
+                    _lib.check(lib.d3_stream_read(b.data_ptr(), nbytes, sink.data_ptr(), grid, handle), "read")
+                g = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(g, stream=stream):
+                    for b in bufs:
+                        _lib.check(lib.d3_stream_read(b.data_ptr(), nbytes, sink.data_ptr(), grid, handle), "read")
+                ms = timed_replays([g], stream, steps, warmup)
+                us = ms * 1e3 / (steps * layers)
+                runs[f"grid {grid}"] = {"us_per_launch": round(us, 3), "gbs": round(nbytes / (us * 1e-6) / 1e9, 1)}
+                del g
+            del bufs
+            torch.cuda.empty_cache()
+            one_shot[name] = runs
+        out["one_shot"] = one_shot
+        _lib.check(lib.d3_empty_launch(EMPTY_GRID, handle), "empty")
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream):
+            for _ in range(layers):
+                _lib.check(lib.d3_empty_launch(EMPTY_GRID, handle), "empty")
+        ms = timed_replays([g], stream, steps, warmup)
+        out["empty_launch_us"] = round(ms * 1e3 / (steps * layers), 3)
+        out["empty_launch_grid"] = EMPTY_GRID
+    torch.cuda.synchronize()
+    return out
+
+
+def run_ceiling(args, fmt, device):
+    """--mode ceiling: measure_ceiling alone, one JSON line."""
+    ceiling = measure_ceiling(device, layers=args.layers, steps=args.steps, warmup=args.warmup)
+    print(json.dumps({"metric": "device ceiling: streaming HBM read, one-shot layer reads, empty launches",
+                      "value": ceiling["stream_read_gbs"], "unit": "GB/s", "n_gpus": 1, "higher_is_better": True,
+                      "peak": PEAK_GBS, "data": "synthetic", "config": {"workload": "probe kernels", **ceiling}}),
+          flush=True)
+
+
 def decode_summary(args, fmt_name, routing, device):
     """One-row decode of another format (same shape, 48 layers), as run_decode measures it: a dict for
     config.other_formats."""
@@ -537,7 +619,7 @@ def main():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=None)
     p.add_argument("--warmup", type=int, default=None)
-    p.add_argument("--mode", default="decode", choices=["decode", "prefill", "resident", "block", "gemv"])
+    p.add_argument("--mode", default="decode", choices=["decode", "prefill", "resident", "block", "gemv", "ceiling"])
     p.add_argument("--routed", action="store_true", help="--mode resident: route inside the gate_up launch")
     p.add_argument("--launches", type=int, default=2, choices=[1, 2],
                    help="--mode resident: the two-launch decode (default) or the one-launch one")
@@ -574,10 +656,18 @@ def main():
     if args.calibrate_copy:
         calibrate_copy(device)
         return
+    if args.mode == "ceiling":
+        run_ceiling(args, fmt, device)
+        return
 
     run = {"prefill": run_prefill, "resident": run_resident, "block": run_block, "gemv": run_gemv}.get(args.mode,
                                                                                                      run_decode)
     ms, total_bytes, launches, tokens, config, kernel, cpu = run(args, fmt, device)
+    ceiling = None
+    if default_run and args.shape == "config":
+        log("measuring the device's ceiling (streaming read, one-shot layer reads, empty launches)")
+        ceiling = measure_ceiling(device, steps=20, warmup=3)
+        config["ceiling"] = ceiling
     if default_run and args.shape == "config" and not args.headline_only:
         # the north star's target formats at one row, and the 48-layer Zipf sweep of W6A8
         config["other_formats"] = []
@@ -616,7 +706,10 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / PEAK_GBS, 4), "traffic": measured_traffic(args.mode, args.format, args.rows)
                      if args.shape == "config" else None,
-                     "kernel": kernel, "launch_us": round(launch_us, 3)},
+                     "kernel": kernel, "launch_us": round(launch_us, 3),
+                     "measured_peak": None if ceiling is None else ceiling["stream_read_gbs"],
+                     "frac_of_measured_peak": None if ceiling is None else
+                     round(achieved / ceiling["stream_read_gbs"], 4)},
         "cpu_baseline": cpu,
     }
     if not math.isfinite(gbs):

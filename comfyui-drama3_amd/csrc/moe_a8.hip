@@ -1433,12 +1433,14 @@ __global__ void __launch_bounds__(256) fill_zero_kernel(uint4* p, int64_t n16) {
 
 constexpr int MAX_DEVICES = 64;
 
-// The current device's copy of `scratch`: its address from hipGetSymbolAddress (checked), on the first call on the
-// device also zeroed by a fill kernel on `stream` (a kernel, so that a caller capturing a graph records no memset
-// node). Returns nullptr and sets the error on failure.
-void* scratch_on(hipStream_t stream, int* err) {
+// The current device's copy of `scratch`: its address from hipGetSymbolAddress (checked), looked up once per device
+// with that device current. With `clear`, the first call on the device also zeroes it by a fill kernel on `stream` (a
+// kernel, so that no memset node is recorded) unless `stream` is capturing a graph: the array is zero when the library
+// loads, and a clear recorded into a graph would run on every replay. Returns nullptr and sets the error on failure.
+void* scratch_on(hipStream_t stream, bool clear, int* err) {
   static std::mutex mu;
   static void* ptrs[MAX_DEVICES] = {};
+  static bool cleared[MAX_DEVICES] = {};
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) { *err = hip_fail(e, "hipGetDevice"); return nullptr; }
@@ -1448,10 +1450,18 @@ void* scratch_on(hipStream_t stream, int* err) {
     void* p = nullptr;
     e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
     if (e != hipSuccess) { *err = hip_fail(e, "d3_moe_a8_noalloc: hipGetSymbolAddress"); return nullptr; }
-    hipLaunchKernelGGL(fill_zero_kernel, dim3(768), dim3(256), 0, stream, (uint4*)p, SCRATCH_BYTES / 16);
-    e = hipGetLastError();
-    if (e != hipSuccess) { *err = hip_fail(e, "d3_moe_a8_noalloc: clearing the workspace"); return nullptr; }
     ptrs[dev] = p;
+  }
+  if (clear && !cleared[dev]) {
+    hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+    e = hipStreamIsCapturing(stream, &capture);
+    if (e != hipSuccess) { *err = hip_fail(e, "d3_moe_a8_noalloc: hipStreamIsCapturing"); return nullptr; }
+    if (capture == hipStreamCaptureStatusNone) {
+      hipLaunchKernelGGL(fill_zero_kernel, dim3(768), dim3(256), 0, stream, (uint4*)ptrs[dev], SCRATCH_BYTES / 16);
+      e = hipGetLastError();
+      if (e != hipSuccess) { *err = hip_fail(e, "d3_moe_a8_noalloc: clearing the workspace"); return nullptr; }
+    }
+    cleared[dev] = true;
   }
   return ptrs[dev];
 }
@@ -1628,7 +1638,7 @@ int d3_moe_a8_noalloc(const d3_moe_a8_desc* desc, void* stream) {
     return d3::fail("d3_moe_a8_noalloc: the layer needs " + std::to_string(need) + " bytes of workspace, more than the " +
                     std::to_string(d3::SCRATCH_BYTES) + " of the static one (at most 16 rows, top-8, H 2048, I 768)");
   int err = 0;
-  void* ws = d3::scratch_on((hipStream_t)stream, &err);
+  void* ws = d3::scratch_on((hipStream_t)stream, true, &err);
   if (!ws) return err;
   d3_moe_a8_desc d = *desc;
   d.workspace = ws;
@@ -1645,6 +1655,14 @@ int d3_moe_a8_status(void* workspace, uint32_t* status) {
   e = hipMemcpy(sticky, &zero, 4, hipMemcpyHostToDevice);
   if (e != hipSuccess) return d3::hip_fail(e, "d3_moe_a8_status");
   return 0;
+}
+
+int d3_moe_a8_noalloc_status(uint32_t* status) {
+  if (!status) return d3::fail("d3_moe_a8_noalloc_status: null pointer");
+  int err = 0;
+  void* ws = d3::scratch_on(nullptr, false, &err);
+  if (!ws) return err;
+  return d3_moe_a8_status(ws, status);
 }
 
 }  // extern "C"

@@ -52,11 +52,14 @@ SIGNATURES = {
     "d3_moe_a8": (c_int32, [ctypes.POINTER(MoeA8Desc), c_void_p]),
     "d3_moe_a8_noalloc": (c_int32, [ctypes.POINTER(MoeA8Desc), c_void_p]),
     "d3_moe_a8_status": (c_int32, [c_void_p, ctypes.POINTER(c_uint32)]),
+    "d3_moe_a8_noalloc_status": (c_int32, [ctypes.POINTER(c_uint32)]),
     "d3_moe_a8_prefill_workspace_bytes": (c_int64, [c_int32, c_int32, c_int32, c_int32, c_int32]),
     "d3_moe_a8_prefill": (c_int32, [ctypes.POINTER(MoeA8PrefillDesc), c_void_p]),
     "d3_gemv_a8_groups": (c_int32, [c_int32, c_void_p, c_int32, c_int32, c_void_p, c_int32, c_void_p, c_void_p]),
     "d3_unpack_rows": (c_int32, [c_int32, c_void_p, c_int32, c_int32, c_void_p, c_void_p]),
     "d3_cvt_fp8": (c_int32, [c_void_p, c_int32, c_void_p, c_int32, c_void_p]),
+    "d3_stream_read": (c_int32, [c_void_p, c_int64, c_void_p, c_int32, c_void_p]),
+    "d3_empty_launch": (c_int32, [c_int32, c_void_p]),
     "d3_gemv_fp8_rows": (c_int32, [c_void_p, c_int32, c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_void_p]),
     "d3_route": (c_int32, [c_void_p, c_int32, c_int32, c_int32, c_void_p, c_void_p, c_void_p]),
     "d3_weighted_sum": (c_int32, [c_void_p, c_void_p, c_int32, c_int32, c_void_p, c_void_p]),

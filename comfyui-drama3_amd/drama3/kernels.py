@@ -281,6 +281,10 @@ def fp8_linear(x, weight, scale):
     scale, as the dequantized matrix holds it; sums in float32."""
     if x.dtype != torch.bfloat16 or scale.dtype != torch.bfloat16:
         raise TypeError("x and scale must be bfloat16")
+    if weight.dtype not in (torch.float8_e4m3fn, torch.uint8):
+        raise TypeError(f"weight must be float8_e4m3fn (or its uint8 bytes), not {weight.dtype}")
+    if x.device.type != "cuda" or weight.device != x.device or scale.device != x.device:
+        raise ValueError(f"x, weight and scale must be on one GPU (got {x.device}, {weight.device}, {scale.device})")
     rows, K = x.shape
     N = weight.shape[0]
     if weight.shape != (N, K) or scale.numel() != N:

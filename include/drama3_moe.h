@@ -83,9 +83,16 @@ int d3_moe_a8(const d3_moe_a8_desc* desc, void* stream);
  * allocate (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). The workspace is a
  * static device array of the library, one per GPU, of 3,007,744 bytes: layers up to 16 rows, top-8, H 2048, I 768
  * (d3_moe_a8_workspace_bytes of the layer must fit, else D3_EINVAL). desc->workspace and workspace_bytes are ignored.
- * The first call on a device looks the array up and clears it with a kernel on `stream`. Every call on a GPU shares
- * that GPU's array: calls that overlap on one GPU race; calls in sequence, on any streams, do not. */
+ * The first call on a device looks the array up; unless `stream` is capturing a graph it also clears the array with a
+ * kernel on `stream` (the array starts zeroed when the library loads, so a first call under capture records no
+ * clear). Every call on a GPU shares that GPU's array, which keeps the last call's contents. Calls must be ordered on
+ * the device: on one stream, or across streams through an event dependency. Calls whose launches can overlap on the
+ * device race on the array, host-ordered calls on two unordered streams included. */
 int d3_moe_a8_noalloc(const d3_moe_a8_desc* desc, void* stream);
+/* d3_moe_a8_status for the current device's static workspace of d3_moe_a8_noalloc (no counterpart in the reference;
+ * for the same callers): the status bits since the last read, cleared. Synchronous; call it outside graph capture,
+ * after the launches completed. Before any d3_moe_a8_noalloc call on the device it reports 0. */
+int d3_moe_a8_noalloc_status(uint32_t* status);
 /* Status bits of a workspace since the last call, after the launches on it completed (synchronous copies; the bits are
  * cleared): 0; bit 0 when a wait for another workgroup's result passed spin_limit and the waiting workgroup computed
  * the result itself (bit for bit what the producer would have published: the output is exact); bit 1 when a wait
@@ -139,6 +146,14 @@ int d3_unpack_rows(int32_t format, const void* rows, int32_t R, int32_t K, void*
 /* d3_cvt_fp8: float -> float8 e4m3fn codes (n a multiple of 4), by the hardware converter the kernels quantize with (hardware 1)
  * or the format-definition conversion (0); round to nearest, ties to even. */
 int d3_cvt_fp8(const float* in, int32_t n, void* out, int32_t hardware, void* stream);
+
+/* ---- Measurement of the device's ceiling (no reference counterpart) ---------------------------------------------
+ * d3_stream_read: `grid` workgroups of 256 threads read `bytes` (a multiple of 16) at src once, 16 bytes a load;
+ * nothing is written in practice (sink [1] receives a word only if the loads' xor equals a fixed constant). Timed
+ * over a large buffer it gives the streaming HBM rate; over a layer's bytes, one launch's one-shot read time.
+ * d3_empty_launch: a kernel of `grid` workgroups of 256 threads that does nothing: the fixed cost of a launch. */
+int d3_stream_read(const void* src, int64_t bytes, uint32_t* sink, int32_t grid, void* stream);
+int d3_empty_launch(int32_t grid, void* stream);
 
 /* ---- FP8 weight with a bf16 scale per output row, bf16 activations ----------------------------------------------
  * The reference's CPU path for an FP8 weight, dequantize then multiply in bf16: nn.functional.linear(x,

@@ -1,6 +1,7 @@
 """The entry point that allocates nothing (d3_moe_a8_noalloc): the fused layer with its workspace in a static device
 array of the library, against d3_moe_a8 with a workspace the caller allocated, bit for bit, on two calls in a row
-(the second a smaller layer), and its refusal of a layer larger than the static workspace."""
+(the second a smaller layer), its refusal of a layer larger than the static workspace, the call captured in a graph
+and replayed, and its status reader."""
 import ctypes
 
 import pytest
@@ -62,3 +63,46 @@ def test_noalloc_rejects_layers_beyond_its_workspace():
     rc, *_ = _call(fn, x, logits, gate_up, down, 8, 1024, 8)
     assert rc != 0
     assert "static one" in _lib.lib().d3_last_error().decode()
+
+
+def test_noalloc_captured_in_a_graph_and_replayed():
+    """The call recorded into a graph (the first noalloc call of the process when this test runs alone) and replayed
+    four times, with eager work and synchronizations between the replays: every replay equals the allocating entry's
+    output bit for bit, and the noalloc status reads no failed wait."""
+    fn = _lib.lib().d3_moe_a8_noalloc
+    E, I, M = 128, 768, 1
+    gate_up, down = _banks(formats.FMT_I8, E, I, 21)
+    gen = torch.Generator(device=DEV).manual_seed(22)
+    xs = [torch.randn((M, 2048), generator=gen, device=DEV).to(torch.bfloat16) for _ in range(4)]
+    logits = [torch.randn((M, E), generator=gen, device=DEV).to(torch.bfloat16) for _ in range(4)]
+    wants = [moe.moe_layer(x, lg, gate_up, down, 8, fused=True) for x, lg in zip(xs, logits)]
+    x_buf, lg_buf = xs[0].clone(), logits[0].clone()
+    out = torch.empty((M, 2048), dtype=torch.bfloat16, device=DEV)
+    desc = _lib.MoeA8Desc(
+        x=x_buf.data_ptr(), logits=lg_buf.data_ptr(), gate_up=gate_up.weight.data_ptr(),
+        gate_up_scale=gate_up.scale.data_ptr(), down=down.weight.data_ptr(), down_scale=down.scale.data_ptr(),
+        out=out.data_ptr(), ids_out=None, weights_out=None, workspace=None, workspace_bytes=0, format=gate_up.fmt,
+        M=M, H=2048, I=I, E=E, topk=8)
+    stream = torch.cuda.Stream(DEV)
+    stream.wait_stream(torch.cuda.current_stream(DEV))
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        with torch.cuda.graph(graph, stream=stream):
+            _lib.check(fn(ctypes.byref(desc), ctypes.c_void_p(stream.cuda_stream)), "d3_moe_a8_noalloc")
+    torch.cuda.synchronize()
+    for i in range(4):
+        x_buf.copy_(xs[i])
+        lg_buf.copy_(logits[i])
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, wants[i]), i
+        scratch = torch.randn((1 << 16,), device=DEV).sum()   # eager work between the replays
+        torch.cuda.synchronize()
+        del scratch
+    status = ctypes.c_uint32(0xFFFFFFFF)
+    _lib.check(_lib.lib().d3_moe_a8_noalloc_status(ctypes.byref(status)), "d3_moe_a8_noalloc_status")
+    assert status.value & moe.STATUS_INVALID == 0
+    again = ctypes.c_uint32(0xFFFFFFFF)
+    _lib.check(_lib.lib().d3_moe_a8_noalloc_status(ctypes.byref(again)), "d3_moe_a8_noalloc_status")
+    assert again.value == 0   # read and cleared
