@@ -162,6 +162,47 @@ def test_slot_prefill_equals_resident_prefill(kind):
         assert (owner >= 0).sum() > 0   # the passes filled slots
 
 
+@pytest.mark.parametrize("kind", ["int8", "w4"])
+def test_slot_prefill_captured_in_a_graph(kind):
+    """Without the CPU side a prompt's pass through the slot cache waits on nothing on the host (the pass's plan, fills
+    and groups are made on the device), so it can be captured in a HIP graph: both layers' passes captured once and
+    replayed five times with new rows and routing copied in between, each output equal to the resident prefill's bits
+    while the cache fills across replays."""
+    layers = make_layers(kind, 2, 15)
+    store = make_store(kind, layers, 10)
+    resident, rcbs = on_device(layers)
+    rng = np.random.default_rng(16)
+    T, k = 20, 4
+    with store.session(DEV, [], False, 0, cpu_experts=False):
+        x, idx, w = prompt(rng, T, k)
+        xs, idxs, ws = dev_bf16_bits(x), torch.from_numpy(idx).to(DEV), bf16(w)
+        stream = torch.cuda.Stream(DEV)
+        stream.wait_stream(torch.cuda.current_stream(DEV))
+        with torch.cuda.stream(stream):
+            for layer in range(2):   # eager first: kernels' constants, allocator pools
+                store.forward(layer, xs, idxs, ws)
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph, stream=stream):
+                outs = [store.forward(layer, xs, idxs, ws) for layer in range(2)]
+        torch.cuda.synchronize()
+        for rep in range(5):
+            x, idx, w = prompt(rng, T, k)
+            xs.copy_(dev_bf16_bits(x))
+            idxs.copy_(torch.from_numpy(idx).to(DEV))
+            ws.copy_(bf16(w))
+            torch.cuda.synchronize()
+            graph.replay()
+            torch.cuda.synchronize()
+            for layer in range(2):
+                want = offload.resident_prefill(xs, idxs, ws, resident[layer], (2 * I, H), kind, rcbs[layer], E)
+                assert torch.equal(outs[layer].view(torch.int16), want.view(torch.int16)), (rep, layer)
+        torch.cuda.synchronize()
+        table, owner = store.cache.table.cpu().numpy(), store.cache.owner.cpu().numpy()
+        assert (owner >= 0).sum() > 0 and int(store.cache.clock) == 6   # one eager pass, five replayed
+        for s, key in enumerate(owner):
+            assert key < 0 or table[key] == s
+
+
 def test_cpu_side_decode():
     """int8 with the CPU side: the missed experts the GPU leaves to the CPU come back through the host mailbox (or, if
     the host is late, the GPU runs them itself); the slots the CPU's experts reserved are copied in between steps."""

@@ -128,3 +128,63 @@ def test_slots_taken_are_the_smallest_keys_in_routing_order():
             for s in np.nonzero(st["pending"])[0]:
                 st["pending"][s] = 0
                 st["table"][st["owner"][s]] = s
+
+
+# ---- the host-side rules (host_*_ref, prompt_*_ref, split_ref)
+def test_host_claims_evict_the_least_used_worked_by_hand():
+    """8 slots, one layer of 12 experts: pass 1 uses 0-7 (free slots 0-7 in order); passes 2 and 3 use 0-6 again, so
+    expert 7 is the least used; pass 4's miss (9) takes its slot 7, and expert 7 leaves the table."""
+    st = slots.new_state(1, 12, 8)
+    assert slots.host_decode_ref(st, 0, 1, list(range(8)), 128, 12) == list(range(8))
+    for _ in range(2):
+        assert slots.host_decode_ref(st, 0, 1, list(range(7)), 128, 12) == list(range(7))
+    assert slots.host_decode_ref(st, 0, 1, [9], 128, 12) == [7]
+    assert st["table"][7] == -1 and st["table"][9] == 7 and st["owner"][7] == 9
+    assert list(st["reads"]) == [14, 9, 0] and st["clock"][0] == 4
+
+
+def test_host_claim_is_the_brute_force_minimum():
+    rng = np.random.default_rng(3)
+    for _ in range(100):
+        L, E, S = 2, 12, int(rng.integers(4, 20))
+        st = slots.new_state(L, E, S)
+        for _ in range(int(rng.integers(1, 6))):
+            for layer in range(L):
+                slots.host_use_ref(st, layer, L, list(rng.choice(E, 3, replace=False)), 2.0, E)
+        layer = int(rng.integers(0, L))
+        now = int(st["clock"][0]) * L + layer
+        d = np.float32(-1.0) / np.float32(np.float32(2.0) * np.float32(L))
+        vals = [(-1.0 if k < 0 else np.inf if st["at"][k] == now else float(slots.decayed(st["score"][k], st["at"][k],
+                                                                                          now, d)), s)
+                for s, k in enumerate(st["owner"])]
+        if min(vals)[0] == np.inf:
+            continue
+        want = min(vals)[1]
+        assert slots.host_claim_ref(st, layer, L, 11, 2.0, E) == want
+
+
+def test_prompt_fill_worked_by_hand():
+    """8 slots, 2 layers (share 4): rows 1, 5, 2, 5, 0, 3; the four uncached experts with most rows (1, 3, 5, 2; ties to
+    the lower expert) fill the free slots 0-3 in that order, and expert 0 is the rest."""
+    st = slots.new_state(2, 6, 8)
+    got, fills, rest = slots.prompt_fill_ref(st, 0, 2, [1, 5, 2, 5, 0, 3], 128)
+    assert got == {1: 0, 3: 1, 5: 2, 2: 3} and fills == [1, 3, 5, 2] and rest == [0]
+
+
+def test_prompt_keep_never_takes_a_slot_the_layer_reads():
+    """4 slots, 2 layers (share 2): layer 0's experts 0 and 1 cached in slots 0 and 1, slots 2 and 3 free. A pass using
+    0, 1 (cached) and 2, 3, 4 (rows 3, 9, 9): room is 2 (slots 0 and 1 are read), so the two with most rows, 3 and 4,
+    claim the free slots 2 and 3 in ascending expert order; 2 is read from host memory."""
+    st = slots.new_state(2, 6, 4)
+    slots.host_decode_ref(st, 0, 2, [0, 1], 128, 6)
+    got = slots.prompt_keep_ref(st, 0, 2, [1, 1, 3, 9, 9, 0], 128)
+    assert got == {0: 0, 1: 1, 3: 2, 4: 3}
+
+
+def test_split_worked_by_hand():
+    """PCIe 100 us per expert; the CPU 60 + 13 per row: costs 190, 99, 73, 73 for rows 10, 3, 1, 1. e0 goes to the GPU
+    (190 > 0 + 100), e1 to the CPU (99 <= 100 + 100), e2 to the CPU (172 <= 200), e3 to the GPU (245 > 200)."""
+    counts = {0: 10, 1: 3, 2: 1, 3: 1}
+    assert slots.split_ref([0, 1, 2, 3], counts, 1_200_000, 1.0, 1.0, 60, 13, 12e3) == ([1, 2], 172.0, 200.0)
+    # a CPU twice as slow as modelled: only e1 (198 <= 200); the modelled times come back unscaled
+    assert slots.split_ref([0, 1, 2, 3], counts, 1_200_000, 2.0, 1.0, 60, 13, 12e3) == ([1], 99.0, 300.0)
