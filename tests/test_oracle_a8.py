@@ -243,3 +243,57 @@ def test_block_combine_against_torch_bf16_ops():
     wrong = numerics.f32_to_bf16_bits((numerics.bf16_bits_to_f32(routed) +
                                        gw[:, None] * numerics.bf16_bits_to_f32(shared)).astype(np.float32))
     assert (wrong == lib).mean() < same - 0.05
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+def test_layer_equals_dense_math_on_its_own_operands(fmt):
+    """The oracle layer against the same layer written as dense float64 algebra on its own quantized operands: each
+    weight row decoded on its own (a8.codes, then times the bf16 scale of its row or its 128-column group, written
+    here from the format's definition), the activations dequantized, plain matrix products, SiLU(gate) * up, the hidden
+    rows quantized again, the routing-weighted sum. This path shares no arithmetic with the oracle's grouped integer
+    sums, so a misplaced scale group, a dropped activation scale or a wrong hidden quantization fails it; the two agree
+    to rounding: the same bf16 bits on at least 99% of the outputs, within one bf16 step on all. A planted mistake, the group scales shifted by one group (a row scale
+    format: each row's scale taken from the next row), moves the result far beyond the bar."""
+    rng = np.random.default_rng(19)
+    E, H, I, k, M = 8, 512, 256, 4, 3
+    gu = (rng.standard_normal((E, 2 * I, H)) * 0.05).astype(np.float32)
+    dn = (rng.standard_normal((E, H, I)) * 0.05).astype(np.float32)
+    x = f32_to_bf16_bits(rng.standard_normal((M, H)).astype(np.float32))
+    logits = f32_to_bf16_bits(rng.standard_normal((M, E)).astype(np.float32))
+    banks = {"gate_up": [a8.quantize_weights(gu[e], fmt) for e in range(E)],
+             "down": [a8.quantize_weights(dn[e], fmt) for e in range(E)]}
+    out, ids, w, _ = a8.moe_layer(x, logits, (2 * I, H), (H, I), fmt, k, lambda b, e: banks[b][e])
+
+    def dense(packed, scale_bits, shift=0):
+        rows, cols = packed.shape[0], (packed.shape[1] if fmt in (a8.FMT_I8, a8.FMT_F8) else
+                                       packed.shape[1] * (2 if fmt == a8.FMT_W4 else 4) // (1 if fmt == a8.FMT_W4 else 3))
+        if fmt == a8.FMT_F8:
+            v = e4m3_decode(packed).astype(np.float64)
+        elif fmt == a8.FMT_I8:
+            v = packed.view(np.int8).astype(np.float64)
+        else:
+            v = a8.codes(packed, fmt).astype(np.float64)
+        s = bf16_bits_to_f32(scale_bits).astype(np.float64).reshape(rows, -1)
+        s = np.roll(s, shift, axis=1 if s.shape[1] > 1 else 0)
+        return v * np.repeat(s, cols // s.shape[1], axis=1)
+
+    def layer(shift):
+        xq, xs = a8.quantize_act(bf16_bits_to_f32(x), fmt)
+        xd = (e4m3_decode(xq) if fmt == a8.FMT_F8 else xq).astype(np.float64) * xs.astype(np.float64)[:, None]
+        res = np.zeros((M, H))
+        for m in range(M):
+            for j in range(k):
+                e = ids[m, j]
+                y = dense(*banks["gate_up"][e], shift) @ xd[m]
+                h = (y[:I] / (1.0 + np.exp(-y[:I])) * y[I:]).astype(np.float32)
+                hq, hs = a8.quantize_act(h[None], fmt)
+                hd = (e4m3_decode(hq) if fmt == a8.FMT_F8 else hq).astype(np.float64)[0] * np.float64(hs[0])
+                res[m] += np.float64(w[m, j]) * (dense(*banks["down"][e], shift) @ hd)
+        return res
+
+    got = bf16_bits_to_f32(out).astype(np.float64)
+    ref = bf16_bits_to_f32(f32_to_bf16_bits(layer(0).astype(np.float32))).astype(np.float64)   # the output's rounding
+    assert (got == ref).mean() >= 0.99, (got == ref).mean()
+    assert np.all(np.abs(got - ref) <= 2.0 ** -8 * np.abs(ref))
+    planted = layer(1)
+    assert np.linalg.norm(got - planted) > 0.05 * np.linalg.norm(planted)
