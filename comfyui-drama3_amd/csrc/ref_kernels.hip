@@ -519,6 +519,443 @@ __global__ void __launch_bounds__(256) grouped_kernel(const float* x, const int*
   }
 }
 
+// -------------------------------------------------------------------------- grouped (prefill) on the matrix cores
+// grouped_kernel's products (kernels.py:365-464,538-587) on the bf16 MFMA. Every weight of these formats is a bf16
+// value exactly (int8 and the codes' int8 grid are integers |q| <= 127; e4m3 has 3 mantissa bits). The float32
+// activations are split once, before the products, into three bf16 planes x = hi + mid + lo (split3_kernel: hi =
+// bf16(x), mid = bf16(x - hi), lo = bf16(x - hi - mid); what is left is below 2^-24 |x|), so every product w * term
+// is exact and the MFMA's float32 sums keep float32 accuracy, as the vector unit's FMAs would.
+// Work: grouped_plan_kernel cuts every group into passes of up to 64 rows, the passes with most rows first; a
+// workgroup takes one pass against 64 RA weight rows. Wave w holds RA tiles of 16 rows, n0 + 16 RA w + 16 a + (l & 15)
+// for lane l, as the MFMA's A rows. Per 128-column chunk the workgroup stages the pass's activation rows (all three
+// planes) in LDS, the next chunk's rows and weight bytes loading meanwhile; lane group q = l >> 4 takes columns
+// 32 q .. 32 q + 31 of the chunk in 4 steps of 8, decodes its rows' 32 weights once and runs them against the pass's
+// 16-row tiles as the B columns (lane l: row l & 15 of the tile, the same 32 columns of each plane). A and B take a
+// step's columns in the same lane order, so each sum pairs the right weight and activation whatever order the MFMA
+// adds them in. fp8: the 128 x 128 block scale multiplies each chunk's sums, as the reference's block sums are
+// scaled. A pass's rows past a multiple of 16 read its last row and are not stored.
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+constexpr int GM_ROWS = 64;   // activation rows per pass (4 tiles of 16)
+constexpr int GM_PAD = 136;   // LDS row stride in bf16: 128 columns + 8, so the 16 rows of a tile start 4 banks apart
+
+// x [n] float32 (n % 8 == 0) -> planes hi, mid, lo [n] bf16, x == hi + mid + lo to within 2^-24 |x|
+__global__ void __launch_bounds__(256) split3_kernel(const float* x, int64_t n8, bf16x8* hi, bf16x8* mid, bf16x8* lo) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n8; i += (int64_t)gridDim.x * 256) {
+    const f32x4 a = ((const f32x4*)x)[2 * i], b = ((const f32x4*)x)[2 * i + 1];
+    const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    bf16x8 h, m, l;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      h[j] = (__bf16)v[j];
+      const float r = v[j] - (float)h[j];
+      m[j] = (__bf16)r;
+      l[j] = (__bf16)(r - (float)m[j]);
+    }
+    hi[i] = h;
+    mid[i] = m;
+    lo[i] = l;
+  }
+}
+
+// work [2 + 2 cap] int32: [0] the number of passes, [1] how many of them are first passes (a group's rows 0 .. 63),
+// then (group, first row of the pass) per pass: the first passes, then the others; within each, the passes of 4 tiles
+// first, then those of 3, 2, 1. Groups that are empty or whose rows lie outside [0, T) get none; no more than cap
+// passes are listed. One workgroup.
+__global__ void __launch_bounds__(256) grouped_plan_kernel(const int* groups, int n_groups, int T, int* work, int cap) {
+  __shared__ int count[8], cursor[8];  // bucket 4 - tiles (first passes), 8 - tiles (later passes)
+  if (threadIdx.x < 8) count[threadIdx.x] = 0;
+  __syncthreads();
+  auto tiles_of = [](int n) { return (min(n, GM_ROWS) + 15) / 16; };
+  for (int g = threadIdx.x; g < n_groups; g += 256) {
+    const int first = groups[5 * g + 3], rows = groups[5 * g + 4];
+    if (rows <= 0 || first < 0 || rows > T - first) continue;
+    atomicAdd(&count[4 - tiles_of(rows)], 1);
+    if (rows > GM_ROWS) {
+      atomicAdd(&count[4], (rows - GM_ROWS) / GM_ROWS);
+      if (rows % GM_ROWS) atomicAdd(&count[8 - tiles_of(rows % GM_ROWS)], 1);
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int at = 0;
+    for (int b = 0; b < 8; b++) {
+      cursor[b] = at;
+      at += count[b];
+      if (b == 3) work[1] = min(at, cap);
+    }
+    work[0] = min(at, cap);
+  }
+  __syncthreads();
+  auto put = [&](int bucket, int g, int m0) {
+    const int at = atomicAdd(&cursor[bucket], 1);
+    if (at < cap) {
+      work[2 + 2 * at] = g;
+      work[3 + 2 * at] = m0;
+    }
+  };
+  for (int g = threadIdx.x; g < n_groups; g += 256) {
+    const int first = groups[5 * g + 3], rows = groups[5 * g + 4];
+    if (rows <= 0 || first < 0 || rows > T - first) continue;
+    put(4 - tiles_of(rows), g, 0);
+    for (int m0 = GM_ROWS; m0 < rows; m0 += GM_ROWS) put(8 - tiles_of(rows - m0), g, m0);
+  }
+}
+
+// ------------------------------------------------------------------------------- a prompt's pairs and rows
+// The prompt's (token, k) pairs grouped by expert (offload.py:140-143 sorts them and counts each expert's rows): one
+// workgroup counts the experts' pairs in LDS, takes the exclusive prefix as each group's first row, and deals every
+// pair a place in its expert's range. Within a group the pairs' order is the order of their atomic adds: every output
+// row is computed from its own activation row alone, so no result depends on it. ids outside [0, E) take the places
+// after every group, inverse -1.
+constexpr int GROUPS_MAX_E = 1024;
+__global__ void __launch_bounds__(1024) expert_groups_kernel(const int64_t* ids, int P, int E, int64_t* order,
+                                                             int* inverse, int* groups) {
+  __shared__ int count[GROUPS_MAX_E + 1], cursor[GROUPS_MAX_E + 1], wave_total[16];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  for (int e = tid; e <= E; e += 1024) count[e] = 0;
+  __syncthreads();
+  for (int p = tid; p < P; p += 1024) {
+    const int64_t e = ids[p];
+    atomicAdd(&count[e >= 0 && e < E ? (int)e : E], 1);
+  }
+  __syncthreads();
+  // exclusive prefix over count[0 .. E] (E + 1 <= 1025 entries: thread t takes entry t, thread 0 also entry 1024)
+  const int v = tid <= E ? count[tid] : 0;
+  int incl = v;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int u = __shfl_up(incl, d);
+    if (lane >= d) incl += u;
+  }
+  if (lane == 63) wave_total[w] = incl;
+  __syncthreads();
+  int before = 0;
+  for (int i = 0; i < w; i++) before += wave_total[i];
+  const int first = before + incl - v;
+  if (tid <= E) cursor[tid] = first;
+  if (tid < E) {
+    int* gp = groups + 5 * tid;
+    gp[0] = tid;
+    gp[1] = tid;
+    gp[2] = 0;
+    gp[3] = first;
+    gp[4] = v;
+  }
+  if (E == GROUPS_MAX_E && tid == 0) {  // entry 1024: after all 1024 threads' entries
+    int all = 0;
+    for (int i = 0; i < 16; i++) all += wave_total[i];
+    cursor[E] = all;
+  }
+  __syncthreads();
+  for (int p = tid; p < P; p += 1024) {
+    const int64_t e = ids[p];
+    const bool valid = e >= 0 && e < E;
+    const int at = atomicAdd(&cursor[valid ? (int)e : E], 1);
+    order[at] = p;
+    inverse[p] = valid ? at : -1;
+  }
+}
+
+// Planes hi, mid, lo [P, K] of the rows the grouped products read (split3_kernel's split): row p is x's row
+// order[p] / k (x's row p without order); SRC 0 float32 rows [., K], 1 bf16 rows, 2 float32 gate | up rows [., 2K]
+// through SiLU(gate) * up (kernels.py:222-258's SwiGLU); ROT: in the ConvRot basis (H256 on every 256 columns, / 16).
+template <int SRC, bool ROT>
+__global__ void __launch_bounds__(256) prep_planes_kernel(const void* x, const int64_t* order, int k, int K,
+                                                          __bf16* planes, int64_t plane) {
+  const int p = blockIdx.x, lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const size_t row = order ? (size_t)(order[p] / k) : (size_t)p;
+  for (int g = w; g < K / 256; g += 4) {
+    const int c0 = 256 * g + 4 * lane;
+    float v[4];
+    if constexpr (SRC == 0) {
+      const f32x4 a = *(const f32x4*)((const float*)x + row * K + c0);
+      v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+    } else if constexpr (SRC == 1) {
+      const i32x2 a = *(const i32x2*)((const uint16_t*)x + row * K + c0);
+      v[0] = bf16_to_f32((uint32_t)a.x & 0xFFFFu); v[1] = bf16_to_f32((uint32_t)a.x >> 16);
+      v[2] = bf16_to_f32((uint32_t)a.y & 0xFFFFu); v[3] = bf16_to_f32((uint32_t)a.y >> 16);
+    } else {
+      const float* f = (const float*)x + row * 2 * K;
+      const f32x4 gt = *(const f32x4*)(f + c0), up = *(const f32x4*)(f + K + c0);
+      const float gg[4] = {gt.x, gt.y, gt.z, gt.w}, uu[4] = {up.x, up.y, up.z, up.w};
+#pragma unroll
+      for (int j = 0; j < 4; j++) v[j] = gg[j] / (1.0f + __expf(-gg[j])) * uu[j];
+    }
+    if constexpr (ROT) fwht256(v);
+    typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+    bf16x4 h, m, l;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      h[j] = (__bf16)v[j];
+      const float r = v[j] - (float)h[j];
+      m[j] = (__bf16)r;
+      l[j] = (__bf16)(r - (float)m[j]);
+    }
+    const size_t at = (size_t)p * K + c0;
+    *(bf16x4*)(planes + at) = h;
+    *(bf16x4*)(planes + plane + at) = m;
+    *(bf16x4*)(planes + 2 * plane + at) = l;
+  }
+}
+
+// out[t, h] = sum over j in order of w[t, j] * sorted_out[inverse[t k + j], h] (pairs with inverse -1 left out), in
+// float32, stored as float32 / bf16 / fp16 (out_type 0 / 1 / 2): offload.py:144-149's weighted sum over k.
+template <bool WBF16>
+__global__ void __launch_bounds__(256) combine_rows_kernel(const float* sorted_out, const int* inverse,
+                                                           const void* weights, int k, int H, void* out, int out_type) {
+  const int t = blockIdx.y, h = 4 * (blockIdx.x * 256 + threadIdx.x);
+  if (h >= H) return;
+  f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int j = 0; j < k; j++) {
+    const int at = inverse[(size_t)t * k + j];
+    if (at < 0) continue;
+    const float wj = WBF16 ? bf16_to_f32(((const uint16_t*)weights)[(size_t)t * k + j])
+                           : ((const float*)weights)[(size_t)t * k + j];
+    const f32x4 y = *(const f32x4*)(sorted_out + (size_t)at * H + h);
+    acc.x = fmaf(y.x, wj, acc.x);
+    acc.y = fmaf(y.y, wj, acc.y);
+    acc.z = fmaf(y.z, wj, acc.z);
+    acc.w = fmaf(y.w, wj, acc.w);
+  }
+  const size_t o = (size_t)t * H + h;
+  if (out_type == 0) {
+    *(f32x4*)((float*)out + o) = acc;
+  } else if (out_type == 1) {
+    uint16_t* d = (uint16_t*)out + o;
+    const uint32_t lo = f32_to_bf16(acc.x) | (f32_to_bf16(acc.y) << 16), hi = f32_to_bf16(acc.z) | (f32_to_bf16(acc.w) << 16);
+    *(i32x2*)d = i32x2{(int)lo, (int)hi};
+  } else {
+    _Float16* d = (_Float16*)out + o;
+    d[0] = (_Float16)acc.x; d[1] = (_Float16)acc.y; d[2] = (_Float16)acc.z; d[3] = (_Float16)acc.w;
+  }
+}
+
+// a lane's 32 weights of one row in a chunk as they come from memory (int8 / fp8: 32 bytes in b0, b1; codes: b0 the
+// 16 nibble bytes, b1.x / b1.y the W6 high plane's 8 bytes, sb0 / sb1 the two group scale bytes)
+struct ChunkBytes {
+  i32x4 b0, b1;
+  uint32_t sb0, sb1;
+};
+
+// eight int8 weights (two words, byte i = column i) or eight e4m3 weights as bf16
+template <int KIND> D3_INLINE bf16x8 weights8(uint32_t w0, uint32_t w1) {
+  bf16x8 a;
+  if constexpr (KIND == 0) {
+#pragma unroll
+    for (int j = 0; j < 8; j++) a[j] = (__bf16)(float)(int8_t)(((j < 4 ? w0 : w1) >> (8 * (j & 3))) & 0xFFu);
+  } else {
+    const f32x2 p0 = fp8x2_to_f32<false>(w0), p1 = fp8x2_to_f32<true>(w0);
+    const f32x2 p2 = fp8x2_to_f32<false>(w1), p3 = fp8x2_to_f32<true>(w1);
+    a[0] = (__bf16)p0.x; a[1] = (__bf16)p0.y; a[2] = (__bf16)p1.x; a[3] = (__bf16)p1.y;
+    a[4] = (__bf16)p2.x; a[5] = (__bf16)p2.y; a[6] = (__bf16)p3.x; a[7] = (__bf16)p3.y;
+  }
+  return a;
+}
+
+// grid (N / (64 RA), a multiple of 8 rows): the workgroups of one pass run on one XCD (the dispatcher deals
+// workgroup i to XCD i % 8), where its activation rows stay in that XCD's L2. PHASE 2 runs every pass of the plan;
+// PHASE 0 the first passes, PHASE 1 the others, a filled group's then read from its slot (the first passes filled it).
+template <int KIND, int K, int RA>  // KIND 0 int8, 1 fp8, 4 / 6 codes; RA row tiles per wave
+__global__ void __launch_bounds__(256, 2) grouped_mfma_kernel(const __bf16* xs, int64_t plane, const int* groups,
+                                                              const int* work, int phase, uint8_t* slot_w, void* slot_s,
+                                                              void* slot_c, const uint8_t* host_w, const void* host_s,
+                                                              const void* host_c, const float* codebook, float* out,
+                                                              int N) {
+  constexpr int RB = KIND <= 1 ? K : K * KIND / 8;  // row bytes
+  constexpr int G = K / 16;                          // codes: 16-column scale groups per row
+  constexpr int CHUNKS = K / 128, MT = GM_ROWS / 16;
+  constexpr int STAGE = MT * 3;                      // 16-byte pieces each thread stages per chunk
+  __shared__ float lut[16];
+  __shared__ __attribute__((aligned(16))) __bf16 bt[MT * 3 * 16 * GM_PAD];
+  // XCD-aware order: workgroup i of the launch runs on XCD i % 8; passes p with p % 8 == xcd are dealt to it
+  const int nx = gridDim.x, lin = blockIdx.x + nx * blockIdx.y, xcd = lin & 7, k = lin >> 3;
+  const int item = (k / nx) * 8 + xcd + (phase == 1 ? work[1] : 0), xb = k % nx;
+  if (item >= work[phase == 0 ? 1 : 0]) return;
+  const int g = work[2 + 2 * item], m0 = work[3 + 2 * item];
+  const int* gp = groups + 5 * g;
+  const int expert = gp[0], slot = gp[1], fill = gp[2] && phase != 1, first = gp[3], rows = gp[4];
+  const bool host = slot < 0 || fill, filler = fill && m0 == 0;  // the group's first pass copies it into its slot
+  const int tiles = min(MT, (rows - m0 + 15) / 16);
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, q = lane >> 4, c = lane & 15;
+  const int nw = xb * 64 * RA + 16 * RA * w;  // the wave's first row
+  if (KIND == 4 && tid < 16) lut[tid] = codebook[tid];
+  const size_t src = host ? (size_t)expert : (size_t)slot;  // the expert's index in the fields it is read from
+  const uint8_t* arow = (host ? host_w : slot_w) + (src * N + nw + c) * RB;      // this lane's row of tile 0
+  uint8_t* frow = filler ? slot_w + ((size_t)slot * N + nw + c) * RB : slot_w;  // its slot row (fill)
+  const uint8_t* srow = nullptr;                                                 // codes: its scale bytes
+  if constexpr (KIND >= 4) srow = (const uint8_t*)(host ? host_s : slot_s) + (src * N + nw + c) * G;
+  auto load_chunk = [&](int ch, ChunkBytes (&cb)[RA]) {
+    const int k0 = 128 * ch + 32 * q;
+#pragma unroll
+    for (int a = 0; a < RA; a++) {
+      const uint8_t* r = arow + (size_t)16 * a * RB;
+      if constexpr (KIND <= 1) {
+        cb[a].b0 = *(const i32x4*)(r + k0);
+        cb[a].b1 = *(const i32x4*)(r + k0 + 16);
+      } else {
+        cb[a].b0 = *(const i32x4*)(r + k0 / 2);
+        cb[a].b1 = i32x4{0, 0, 0, 0};
+        if constexpr (KIND == 6) {
+          const i32x2 hw = *(const i32x2*)(r + K / 2 + k0 / 4);
+          cb[a].b1.x = hw.x;
+          cb[a].b1.y = hw.y;
+        }
+        cb[a].sb0 = srow[16 * a * G + k0 / 16];
+        cb[a].sb1 = srow[16 * a * G + k0 / 16 + 1];
+      }
+    }
+  };
+  // staging: piece j of thread tid is tile j / 3, plane j % 3, row (tid >> 4) & 15, 16 bytes at column 8 (tid & 15)
+  const int srow_t = (tid >> 4) & 15, sseg = tid & 15;
+  i32x4 stg[STAGE];
+  auto stage_load = [&](int ch) {
+#pragma unroll
+    for (int j = 0; j < STAGE; j++) {
+      const int mt = j / 3, t = j % 3;
+      if (mt < tiles) {
+        const int r = min(m0 + 16 * mt + srow_t, rows - 1);
+        stg[j] = *(const i32x4*)(xs + t * plane + (size_t)(first + r) * K + 128 * ch + 8 * sseg);
+      }
+    }
+  };
+  auto stage_store = [&]() {
+#pragma unroll
+    for (int j = 0; j < STAGE; j++)
+      if (j / 3 < tiles) *(i32x4*)(bt + ((j / 3 * 3 + j % 3) * 16 + srow_t) * GM_PAD + 8 * sseg) = stg[j];
+  };
+  // the epilogue's scales of rows nw + 16 a + 4 q .. + 3: int8 row scales, codes channel scales
+  float es[RA][4];
+#pragma unroll
+  for (int a = 0; a < RA; a++)
+#pragma unroll
+    for (int r = 0; r < 4; r++) es[a][r] = 1.0f;
+  if constexpr (KIND != 1) {
+    const float* s = (const float*)(KIND == 0 ? (host ? host_s : slot_s) : (host ? host_c : slot_c)) + src * N;
+    float* fs = (float*)(KIND == 0 ? slot_s : slot_c) + (size_t)slot * N;
+#pragma unroll
+    for (int a = 0; a < RA; a++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        es[a][r] = s[nw + 16 * a + 4 * q + r];
+        if (filler && c == 0) fs[nw + 16 * a + 4 * q + r] = es[a][r];
+      }
+  }
+  // fp8: the 128 x 128 block scales of the wave's row block (its 16 RA <= 64 rows lie in one), one per chunk
+  const float* sblk = nullptr;
+  if constexpr (KIND == 1) {
+    const size_t srows = (size_t)(N / 128) * CHUNKS, boff = (size_t)(nw / 128) * CHUNKS;
+    sblk = (const float*)(host ? host_s : slot_s) + src * srows + boff;
+    if (filler && nw % 128 == 0 && lane < CHUNKS) ((float*)slot_s)[(size_t)slot * srows + boff + lane] = sblk[lane];
+  }
+  f32x4 acc[RA][MT];
+#pragma unroll
+  for (int a = 0; a < RA; a++)
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++) acc[a][mt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  ChunkBytes cur[RA], nxt[RA];
+  load_chunk(0, cur);
+  stage_load(0);
+  stage_store();
+  __syncthreads();
+  for (int ch = 0; ch < CHUNKS; ch++) {
+    if (ch + 1 < CHUNKS) {
+      load_chunk(ch + 1, nxt);
+      stage_load(ch + 1);
+    }
+    const int k0 = 128 * ch + 32 * q;
+    if (filler) {  // the expert's bytes copied into its slot as they are read
+#pragma unroll
+      for (int a = 0; a < RA; a++) {
+        uint8_t* f = frow + (size_t)16 * a * RB;
+        if constexpr (KIND <= 1) {
+          *(i32x4*)(f + k0) = cur[a].b0;
+          *(i32x4*)(f + k0 + 16) = cur[a].b1;
+        } else {
+          *(i32x4*)(f + k0 / 2) = cur[a].b0;
+          if constexpr (KIND == 6) *(i32x2*)(f + K / 2 + k0 / 4) = i32x2{cur[a].b1.x, cur[a].b1.y};
+          uint8_t* fsb = (uint8_t*)slot_s + ((size_t)slot * N + nw + 16 * a + c) * G;
+          fsb[k0 / 16] = (uint8_t)cur[a].sb0;
+          fsb[k0 / 16 + 1] = (uint8_t)cur[a].sb1;
+        }
+      }
+    }
+    bf16x8 wa[RA][4];
+#pragma unroll
+    for (int a = 0; a < RA; a++) {
+      if constexpr (KIND <= 1) {
+        wa[a][0] = weights8<KIND>((uint32_t)cur[a].b0.x, (uint32_t)cur[a].b0.y);
+        wa[a][1] = weights8<KIND>((uint32_t)cur[a].b0.z, (uint32_t)cur[a].b0.w);
+        wa[a][2] = weights8<KIND>((uint32_t)cur[a].b1.x, (uint32_t)cur[a].b1.y);
+        wa[a][3] = weights8<KIND>((uint32_t)cur[a].b1.z, (uint32_t)cur[a].b1.w);
+      } else {
+        float qv[32];
+        decode_group<KIND>((uint32_t)cur[a].b0.x, (uint32_t)cur[a].b0.y, (uint32_t)cur[a].b1.x, cur[a].sb0, lut, qv);
+        decode_group<KIND>((uint32_t)cur[a].b0.z, (uint32_t)cur[a].b0.w, (uint32_t)cur[a].b1.y, cur[a].sb1, lut,
+                           qv + 16);
+#pragma unroll
+        for (int st = 0; st < 4; st++)
+#pragma unroll
+          for (int j = 0; j < 8; j++) wa[a][st][j] = (__bf16)qv[8 * st + j];
+      }
+    }
+    f32x4 part[RA][MT];  // fp8: this chunk's sums before its block scale
+#pragma unroll
+    for (int a = 0; a < RA; a++)
+#pragma unroll
+      for (int mt = 0; mt < MT; mt++) part[a][mt] = KIND == 1 ? f32x4{0.0f, 0.0f, 0.0f, 0.0f} : acc[a][mt];
+#pragma unroll
+    for (int st = 0; st < 4; st++)
+#pragma unroll
+      for (int mt = 0; mt < MT; mt++) {
+        if (mt < tiles) {
+          const __bf16* bp = bt + (mt * 3 * 16 + c) * GM_PAD + 32 * q + 8 * st;
+          const bf16x8 b0 = *(const bf16x8*)bp, b1 = *(const bf16x8*)(bp + 16 * GM_PAD),
+                       b2 = *(const bf16x8*)(bp + 32 * GM_PAD);
+#pragma unroll
+          for (int a = 0; a < RA; a++) {
+            part[a][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa[a][st], b0, part[a][mt], 0, 0, 0);
+            part[a][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa[a][st], b1, part[a][mt], 0, 0, 0);
+            part[a][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa[a][st], b2, part[a][mt], 0, 0, 0);
+          }
+        }
+      }
+    if constexpr (KIND == 1) {
+      const float sc = sblk[ch];
+#pragma unroll
+      for (int a = 0; a < RA; a++)
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+          for (int i = 0; i < 4; i++) acc[a][mt][i] = fmaf(sc, part[a][mt][i], acc[a][mt][i]);
+    } else {
+#pragma unroll
+      for (int a = 0; a < RA; a++)
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++) acc[a][mt] = part[a][mt];
+    }
+    if (ch + 1 < CHUNKS) {
+      __syncthreads();  // every wave is done with this chunk's rows
+      stage_store();
+      __syncthreads();
+#pragma unroll
+      for (int a = 0; a < RA; a++) cur[a] = nxt[a];
+    }
+  }
+  // lane l holds rows nw + 16 a + 4 q .. + 3 of activation row m0 + 16 mt + (l & 15)
+#pragma unroll
+  for (int mt = 0; mt < MT; mt++) {
+    const int r = m0 + 16 * mt + c;
+    if (mt < tiles && r < rows) {
+#pragma unroll
+      for (int a = 0; a < RA; a++) {
+        const f32x4 o = {acc[a][mt].x * es[a][0], acc[a][mt].y * es[a][1], acc[a][mt].z * es[a][2],
+                         acc[a][mt].w * es[a][3]};
+        *(f32x4*)(out + (size_t)(first + r) * N + nw + 16 * a + 4 * q) = o;
+      }
+    }
+  }
+}
+
 // ------------------------------------------------------------------------------------ fused resident decode
 // offload.py:108-123 resident_decode in two launches instead of five (rotate, gemv, rotate(SwiGLU), gemv,
 // weighted_sum): banks held whole on the device (expert e in slot e), KIND 0 int8 (ConvRot), 1 fp8 (128 x 128 block
@@ -1379,10 +1816,10 @@ int d3_grouped(int32_t kind, const float* x, const int32_t* groups, int32_t n_gr
   if (n_groups < 1) return 0;
   if (N < RPB || N % (kind == 1 ? 128 : RPB) || !supported_k(K))
     return fail("d3_grouped: N % 16 == 0 (N % 128 == 0 for fp8), K in {256..2048}");
-  const dim3 grid(N / RPB, n_groups);
   const hipStream_t s = (hipStream_t)stream;
   const uint8_t* hw = (const uint8_t*)host_w;
   uint8_t* sw = (uint8_t*)slot_w;
+  const dim3 grid(N / RPB, n_groups);
   switch (kind) {
     case 0: D3_K_SWITCH(K, hipLaunchKernelGGL((grouped_kernel<0, KK>), grid, dim3(256), 0, s, x, groups, sw, slot_s, slot_c, hw, host_s, host_c, codebook, out, N)); break;
     case 1: D3_K_SWITCH(K, hipLaunchKernelGGL((grouped_kernel<1, KK>), grid, dim3(256), 0, s, x, groups, sw, slot_s, slot_c, hw, host_s, host_c, codebook, out, N)); break;
@@ -1391,6 +1828,109 @@ int d3_grouped(int32_t kind, const float* x, const int32_t* groups, int32_t n_gr
     default: return fail("d3_grouped: kind 0, 1, 4 or 6");
   }
   return done("d3_grouped");
+}
+
+int d3_split_bf16x3(const float* x, int64_t n, void* planes, void* stream) {
+  if (!x || !planes) return fail("d3_split_bf16x3: null pointer");
+  if (n < 8 || n % 8) return fail("d3_split_bf16x3: n a positive multiple of 8");
+  const int64_t n8 = n / 8;
+  const int grid = (int)std::min<int64_t>((n8 + 255) / 256, 8192);
+  bf16x8* p = (bf16x8*)planes;
+  hipLaunchKernelGGL(split3_kernel, dim3(grid), dim3(256), 0, (hipStream_t)stream, x, n8, p, p + n8, p + 2 * n8);
+  return done("d3_split_bf16x3");
+}
+
+int64_t d3_grouped_mfma_work_ints(int32_t n_groups, int64_t rows) {
+  const int64_t cap = (rows + GM_ROWS - 1) / GM_ROWS + std::max(n_groups, 0);
+  return 2 + 2 * ((cap + 7) / 8 * 8);
+}
+
+int d3_grouped_mfma(int32_t kind, const void* planes, int64_t plane, const int32_t* groups, int32_t n_groups,
+                    int32_t* work, int64_t work_ints, int32_t fills_first, void* slot_w, void* slot_s, void* slot_c,
+                    const void* host_w, const void* host_s, const void* host_c, const float* codebook, float* out,
+                    int32_t N, int32_t K, void* stream) {
+  if (!planes || !groups || !work || !slot_w || !slot_s || !host_w || !host_s || !out)
+    return fail("d3_grouped_mfma: null pointer");
+  if ((kind == 4 || kind == 6) && (!slot_c || !host_c)) return fail("d3_grouped_mfma: codes need channel scales");
+  if (kind == 4 && !codebook) return fail("d3_grouped_mfma: 4 bits need a codebook");
+  if (n_groups < 1) return 0;
+  if (N < 64 || N % (kind == 1 ? 128 : 64) || !supported_k(K) || plane < K || plane % K)
+    return fail("d3_grouped_mfma: N % 64 == 0 (N % 128 == 0 for fp8), K in {256..2048}, plane a multiple of K");
+  const int64_t T = plane / K;
+  if (T > INT32_MAX) return fail("d3_grouped_mfma: more than 2^31 rows");
+  const int64_t need = d3_grouped_mfma_work_ints(n_groups, T);
+  if (work_ints < need) return fail("d3_grouped_mfma: work holds fewer than d3_grouped_mfma_work_ints ints");
+  const int cap = (int)((need - 2) / 2), firsts = (n_groups + 7) / 8 * 8;
+  const hipStream_t s = (hipStream_t)stream;
+  hipLaunchKernelGGL(grouped_plan_kernel, dim3(1), dim3(256), 0, s, groups, n_groups, (int)T, work, cap);
+  const __bf16* xs = (const __bf16*)planes;
+  const uint8_t* hw = (const uint8_t*)host_w;
+  uint8_t* sw = (uint8_t*)slot_w;
+#define D3_GM(KD, RA, PH, Y) D3_K_SWITCH(K, hipLaunchKernelGGL((grouped_mfma_kernel<KD, KK, RA>), dim3(N / (64 * RA), Y), dim3(256), 0, s, xs, plane, groups, work, PH, sw, slot_s, slot_c, hw, host_s, host_c, codebook, out, N))
+#define D3_GM_RA(KD, PH, Y) if (N % 128 == 0) { D3_GM(KD, 2, PH, Y); } else { D3_GM(KD, 1, PH, Y); }
+#define D3_GM_KIND(PH, Y)                          \
+  switch (kind) {                                  \
+    case 0: D3_GM_RA(0, PH, Y); break;             \
+    case 1: D3_GM_RA(1, PH, Y); break;             \
+    case 4: D3_GM_RA(4, PH, Y); break;             \
+    case 6: D3_GM_RA(6, PH, Y); break;             \
+    default: return fail("d3_grouped_mfma: kind 0, 1, 4 or 6"); \
+  }
+  if (fills_first) {
+    D3_GM_KIND(0, firsts);
+    D3_GM_KIND(1, cap);
+  } else {
+    D3_GM_KIND(2, cap);
+  }
+#undef D3_GM_KIND
+#undef D3_GM_RA
+#undef D3_GM
+  return done("d3_grouped_mfma");
+}
+
+int d3_expert_groups(const int64_t* ids, int32_t P, int32_t E, int64_t* order, int32_t* inverse, int32_t* groups,
+                     void* stream) {
+  if (!groups || (P > 0 && (!ids || !order || !inverse))) return fail("d3_expert_groups: null pointer");
+  if (P < 0 || E < 1 || E > GROUPS_MAX_E) return fail("d3_expert_groups: 1 <= E <= 1024, P >= 0");
+  hipLaunchKernelGGL(expert_groups_kernel, dim3(1), dim3(1024), 0, (hipStream_t)stream, ids, P, E, order, inverse,
+                     groups);
+  return done("d3_expert_groups");
+}
+
+int d3_prep_planes(int32_t mode, int32_t rotate, const void* x, const int64_t* order, int32_t k, int32_t P, int32_t K,
+                   void* planes, void* stream) {
+  if (!x || !planes) return fail("d3_prep_planes: null pointer");
+  if (mode < 0 || mode > 2 || P < 0 || k < 1 || !supported_k(K)) return fail("d3_prep_planes: mode 0-2, K in {256..2048}");
+  if (P == 0) return 0;
+  const hipStream_t s = (hipStream_t)stream;
+  const int64_t plane = (int64_t)P * K;
+  __bf16* out = (__bf16*)planes;
+#define D3_PREP(M, R) hipLaunchKernelGGL((prep_planes_kernel<M, R>), dim3(P), dim3(256), 0, s, x, order, k, K, out, plane)
+  switch (mode * 2 + (rotate ? 1 : 0)) {
+    case 0: D3_PREP(0, false); break;
+    case 1: D3_PREP(0, true); break;
+    case 2: D3_PREP(1, false); break;
+    case 3: D3_PREP(1, true); break;
+    case 4: D3_PREP(2, false); break;
+    default: D3_PREP(2, true); break;
+  }
+#undef D3_PREP
+  return done("d3_prep_planes");
+}
+
+int d3_combine_rows(const float* sorted_out, const int32_t* inverse, const void* weights, int32_t weights_bf16,
+                    int32_t T, int32_t k, int32_t H, void* out, int32_t out_type, void* stream) {
+  if (!sorted_out || !inverse || !weights || !out) return fail("d3_combine_rows: null pointer");
+  if (T < 0 || k < 1 || H < 4 || H % 4 || out_type < 0 || out_type > 2)
+    return fail("d3_combine_rows: H % 4 == 0, out_type 0 float32, 1 bf16, 2 fp16");
+  if (T == 0) return 0;
+  const dim3 grid((H / 4 + 255) / 256, T);
+  const hipStream_t s = (hipStream_t)stream;
+  if (weights_bf16)
+    hipLaunchKernelGGL(combine_rows_kernel<true>, grid, dim3(256), 0, s, sorted_out, inverse, weights, k, H, out, out_type);
+  else
+    hipLaunchKernelGGL(combine_rows_kernel<false>, grid, dim3(256), 0, s, sorted_out, inverse, weights, k, H, out, out_type);
+  return done("d3_combine_rows");
 }
 
 }  // extern "C"

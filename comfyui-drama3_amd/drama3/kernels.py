@@ -139,12 +139,94 @@ def gemv_codes(x, ids, plan, slot_fields, host_fields, codebook, bits, n):
     return out
 
 
-def _grouped(kind, x, groups, slot_fields, host_fields, codebook, n, wkey):
+GROUPED_KINDS = {"int8": (0, "_qdata"), "fp8": (1, "weight"), "w4": (4, "_qdata"), "w6": (6, "_qdata")}
+
+
+def _grouped_fields(slot_fields, host_fields, codebook, wkey):
+    return (_p(slot_fields[wkey]), _p(slot_fields["scale"]), _p(slot_fields.get("s_channel")), _p(host_fields[wkey]),
+            _p(host_fields["scale"]), _p(host_fields.get("s_channel")), _p(codebook))
+
+
+def grouped_planes(kind, planes, rows, width, groups, slot_fields, host_fields, codebook, n, fills_first=False):
+    """[rows, n] float32: the grouped products on the matrix cores over planes [3, rows * width] bf16 (prep_planes /
+    split); kind "int8", "fp8", "w4" or "w6". fills_first: every group's first pass before the others, which then
+    read a filled group from its slot."""
+    code, wkey = GROUPED_KINDS[kind]
+    out = torch.empty((rows, n), dtype=torch.float32, device=planes.device)
+    if rows == 0:
+        return out
+    ints = _lib.lib().d3_grouped_mfma_work_ints(groups.shape[0], rows)
+    work = torch.empty(ints, dtype=torch.int32, device=planes.device)
+    _call("d3_grouped_mfma", code, _p(planes), rows * width, _p(groups), groups.shape[0], _p(work), ints,
+          int(fills_first), *_grouped_fields(slot_fields, host_fields, codebook, wkey), _p(out), n, width,
+          _stream(planes))
+    return out
+
+
+def _grouped(kind, x, groups, slot_fields, host_fields, codebook, n, wkey, matrix=None):
+    """The grouped products on the bf16 matrix cores (x split into three bf16 planes first) when n % 64 == 0 or
+    `matrix`, else on the vector unit."""
     x = x.contiguous()
+    if (matrix if matrix is not None else n % 64 == 0) and x.numel():
+        planes = torch.empty((3, x.numel()), dtype=torch.bfloat16, device=x.device)
+        _call("d3_split_bf16x3", _p(x), x.numel(), _p(planes), _stream(x))
+        name = {0: "int8", 1: "fp8", 4: "w4", 6: "w6"}[kind]
+        return grouped_planes(name, planes, x.shape[0], x.shape[1], groups, slot_fields, host_fields, codebook, n)
     out = torch.empty((x.shape[0], n), dtype=torch.float32, device=x.device)
-    _call("d3_grouped", kind, _p(x), _p(groups), groups.shape[0], _p(slot_fields[wkey]), _p(slot_fields["scale"]),
-          _p(slot_fields.get("s_channel")), _p(host_fields[wkey]), _p(host_fields["scale"]),
-          _p(host_fields.get("s_channel")), _p(codebook), _p(out), n, x.shape[1], _stream(x))
+    if x.numel():
+        _call("d3_grouped", kind, _p(x), _p(groups), groups.shape[0],
+              *_grouped_fields(slot_fields, host_fields, codebook, wkey), _p(out), n, x.shape[1], _stream(x))
+    return out
+
+
+def expert_groups(topk_idx, num_experts):
+    """(order [P] int64, inverse [P] int32, groups [num_experts, 5] int32) of a prompt's pairs topk_idx [T, k] int64:
+    each expert's pairs together, experts ascending; inverse = each pair's place in order; groups (e, e, 0, first,
+    rows). On the device, no host sync."""
+    ids = topk_idx.reshape(-1).contiguous()
+    if ids.dtype != torch.int64:
+        ids = ids.long()
+    P = ids.shape[0]
+    order = torch.empty(P, dtype=torch.int64, device=ids.device)
+    inverse = torch.empty(P, dtype=torch.int32, device=ids.device)
+    groups = torch.empty((num_experts, 5), dtype=torch.int32, device=ids.device)
+    _call("d3_expert_groups", _p(ids), P, num_experts, _p(order), _p(inverse), _p(groups), _stream(ids))
+    return order, inverse, groups
+
+
+def prep_planes(x, rotate, order=None, k=1, swiglu=False):
+    """planes [3, P * K] bf16 for grouped_planes: row p is x's row order[p] // k (x's row p without order), through
+    SiLU(gate) * up first with `swiglu` (x float32 gate | up [., 2K]), in the ConvRot basis with `rotate`."""
+    x = x.contiguous()
+    width = x.shape[1] // 2 if swiglu else x.shape[1]
+    if swiglu:
+        if x.dtype != torch.float32:
+            raise TypeError("prep_planes(swiglu=True) takes float32 gate | up rows")
+        mode = 2
+    elif x.dtype == torch.bfloat16:
+        mode = 1
+    else:
+        x, mode = x.float(), 0
+    P = order.shape[0] if order is not None else x.shape[0]
+    planes = torch.empty((3, P * width), dtype=torch.bfloat16, device=x.device)
+    _call("d3_prep_planes", mode, int(rotate), _p(x), _p(order), int(k), P, width, _p(planes), _stream(x))
+    return planes
+
+
+_OUT_TYPES = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
+
+
+def combine_rows(sorted_out, inverse, topk_weight, dtype):
+    """[T, H] of `dtype` (float32, bfloat16 or float16): sum over j of topk_weight[t, j] * sorted_out[inverse[t k +
+    j]], in float32, j in order."""
+    T, k = topk_weight.shape
+    H = sorted_out.shape[1]
+    w = topk_weight.contiguous()
+    if w.dtype not in (torch.bfloat16, torch.float32):
+        w = w.float()
+    out = torch.empty((T, H), dtype=dtype, device=sorted_out.device)
+    _call("d3_combine_rows", _p(sorted_out.contiguous()), _p(inverse), _p(w), int(w.dtype == torch.bfloat16), T, k,
+          H, _p(out), _OUT_TYPES[dtype], _stream(sorted_out))
     return out
 
 
@@ -164,7 +246,7 @@ def grouped_codes(x, groups, slot_fields, host_fields, codebook, bits, n):
     return _grouped(int(bits), x, groups, slot_fields, host_fields, codebook, n, "_qdata")
 
 
-_RESIDENT_KINDS = {"int8": (0, "_qdata"), "fp8": (1, "weight"), "w4": (4, "_qdata"), "w6": (6, "_qdata")}
+_RESIDENT_KINDS = GROUPED_KINDS
 
 
 def resident_decode(x, ids, weights, banks, kind, codebooks, H, I):

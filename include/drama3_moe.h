@@ -209,10 +209,47 @@ int d3_gemv_codes(const float* x, int32_t x_rows, const int64_t* ids, const int3
 /* grouped_int8 / grouped_fp8 / grouped_codes (kernels.py:365-464,538-587, wrappers kernels.py:684-700,716-724):
  * kind 0 int8, 1 fp8, 4 / 6 codes. x [T, K] float32 rows sorted by expert; groups [n_groups, 5] int32 = (expert, slot,
  * fill, first row, rows); a group reads its slot, or the host fields when slot < 0 or fill (then copying the expert
- * into the slot). out [T, N] float32 rows of the groups (others untouched); a group with 0 rows reads nothing. */
+ * into the slot). out [T, N] float32 rows of the groups (others untouched); a group with 0 rows reads nothing. The
+ * products run on the vector unit in float32. */
 int d3_grouped(int32_t kind, const float* x, const int32_t* groups, int32_t n_groups, void* slot_w, void* slot_s,
                void* slot_c, const void* host_w, const void* host_s, const void* host_c, const float* codebook,
                float* out, int32_t N, int32_t K, void* stream);
+
+/* The same products on the bf16 matrix cores (same replacement, same fields and groups). The float32 rows are first
+ * split into three bf16 planes, by d3_split_bf16x3 (x [n] float32, n % 8 == 0 -> planes bf16 [3, n] = hi, mid, lo)
+ * or d3_prep_planes: x == hi + mid + lo to within 2^-24 |x|, and every weight of these formats is a bf16 value
+ * exactly, so each product is exact and the sums float32. d3_grouped_mfma reads planes [3, plane] holding x [T, K]
+ * (plane = T * K elements per plane); N % 64 == 0 (N % 128 == 0 for fp8). work: int32 device memory of
+ * d3_grouped_mfma_work_ints(n_groups, T) ints, where the call lists its passes of up to 64 rows over the groups (a
+ * group whose rows lie outside [0, T) is skipped). fills_first: the groups' first passes run first, then the others
+ * read a filled group from its slot, so an expert copied in crosses the bus once however many rows it has. */
+int d3_split_bf16x3(const float* x, int64_t n, void* planes, void* stream);
+int64_t d3_grouped_mfma_work_ints(int32_t n_groups, int64_t rows);
+int d3_grouped_mfma(int32_t kind, const void* planes, int64_t plane, const int32_t* groups, int32_t n_groups,
+                    int32_t* work, int64_t work_ints, int32_t fills_first, void* slot_w, void* slot_s, void* slot_c,
+                    const void* host_w, const void* host_s, const void* host_c, const float* codebook, float* out,
+                    int32_t N, int32_t K, void* stream);
+
+/* A prompt's (token, k) pairs grouped by expert (offload.py:140-143, which sorts ids and counts each expert's pairs):
+ * ids [P] int64 (P = T * k, row-major); order [P] int64 = the pairs' indices, each expert's pairs together and the
+ * experts in ascending order; inverse [P] int32 = each pair's place in order (-1 for an id outside [0, E), which is
+ * placed after every group); groups [E, 5] int32 = (e, e, 0, first, rows). Within a group the pairs' order is not
+ * fixed: each output row of the grouped products depends on its own row alone. E <= 1024; one workgroup. */
+int d3_expert_groups(const int64_t* ids, int32_t P, int32_t E, int64_t* order, int32_t* inverse, int32_t* groups,
+                     void* stream);
+
+/* The planes d3_grouped_mfma reads, from the rows themselves: planes bf16 [3, P * K]; row p is x's row order[p] / k
+ * (x's row p when order is NULL). mode 0: x float32 [., K]; 1: bf16 [., K]; 2: float32 gate | up [., 2K] through
+ * SiLU(gate) * up (the SwiGLU between the banks, kernels.py:222-258). rotate: in the ConvRot basis first (int8 and the
+ * codes; d3_rotate's transform). K in {256, 512, 768, 1024, 1536, 2048}. */
+int d3_prep_planes(int32_t mode, int32_t rotate, const void* x, const int64_t* order, int32_t k, int32_t P, int32_t K,
+                   void* planes, void* stream);
+
+/* The weighted sum over k (offload.py:144-149): out [T, H] = sum over j in order of weights[t, j] *
+ * sorted_out[inverse[t k + j]] in float32 (pairs with inverse -1 left out), stored as float32 / bf16 / fp16
+ * (out_type 0 / 1 / 2); weights [T, k] bf16 (weights_bf16) or float32. H % 4 == 0. */
+int d3_combine_rows(const float* sorted_out, const int32_t* inverse, const void* weights, int32_t weights_bf16,
+                    int32_t T, int32_t k, int32_t H, void* out, int32_t out_type, void* stream);
 
 /* resolve_experts (kernels.py:78-191, wrapper resolve kernels.py:617-625): the slot cache's lookup and eviction for
  * one decode row's experts ids [k] (int64, k <= 32) of `layer`, on the device. State (device memory, updated in

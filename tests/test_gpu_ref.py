@@ -107,6 +107,90 @@ def test_rotate_only_if_zero_writes_nothing():
     assert torch.all(out == 7.0)
 
 
+def split3_np(v):
+    """hi, mid, lo float32 arrays: bf16(v), bf16(v - hi), bf16(v - hi - mid) with float32 differences."""
+    v = np.asarray(v, np.float32)
+    hi = numerics.bf16_bits_to_f32(numerics.f32_to_bf16_bits(v))
+    r = (v - hi).astype(np.float32)
+    mid = numerics.bf16_bits_to_f32(numerics.f32_to_bf16_bits(r))
+    lo = numerics.bf16_bits_to_f32(numerics.f32_to_bf16_bits((r - mid).astype(np.float32)))
+    return hi, mid, lo
+
+
+def planes_np(planes, P, K):
+    return [planes[t].float().cpu().numpy().reshape(P, K) for t in range(3)]
+
+
+@pytest.mark.parametrize("mode, rotate", [("f32", False), ("bf16", True), ("bf16", False), ("swiglu", True),
+                                          ("swiglu", False)])
+def test_prep_planes(mode, rotate):
+    """d3_prep_planes: the gathered (row order[p] // k), SwiGLU'd and rotated rows as the oracle's rotate_ref gives
+    them (within 2e-6 of the largest, the float32 transform's reordering), split into planes bit for bit as numpy
+    splits the kernel's own float32 rows (d3_rotate's, the same transform), and hi + mid + lo within 2^-24 |x|."""
+    rng = np.random.default_rng(len(mode) + rotate)
+    T, k, K = 37, 3, 768
+    order = rng.permutation(T * k)
+    if mode == "swiglu":
+        x = rng.standard_normal((T * k, 2 * K)).astype(np.float32)
+        planes = kernels.prep_planes(dev(x), rotate, swiglu=True)
+        rows = x
+        want = ref.rotate_ref(x, swiglu=True) if rotate else None
+        if not rotate:
+            g, u = x[:, :K].astype(np.float64), x[:, K:].astype(np.float64)
+            want = g / (1 + np.exp(-g)) * u
+        dev_rows = kernels.rotate(dev(x), torch.ones(1, dtype=torch.int32, device=DEV), swiglu=True) if rotate \
+            else None
+        P = T * k
+    else:
+        if mode == "bf16":
+            bits = numerics.f32_to_bf16_bits(rng.standard_normal((T, K)).astype(np.float32))
+            xd, x = dev(bits).view(torch.bfloat16), numerics.bf16_bits_to_f32(bits)
+        else:
+            x = rng.standard_normal((T, K)).astype(np.float32)
+            xd = dev(x)
+        planes = kernels.prep_planes(xd, rotate, dev(order.astype(np.int64)), k)
+        rows = x[order // k]
+        want = ref.rotate_ref(rows) if rotate else rows
+        dev_rows = kernels.rotate(dev(rows.astype(np.float32)), torch.ones(1, dtype=torch.int32, device=DEV)) \
+            if rotate else None
+        P = T * k
+    hi, mid, lo = planes_np(planes, P, K)
+    total = hi.astype(np.float64) + mid + lo
+    assert np.abs(total - want).max() <= 2e-6 * np.abs(want).max()
+    if dev_rows is not None or mode != "swiglu":
+        exact = dev_rows.cpu().numpy() if dev_rows is not None else want.astype(np.float32)
+        h, m, l = split3_np(exact)
+        assert np.array_equal(hi, h) and np.array_equal(mid, m) and np.array_equal(lo, l)
+        assert np.all(np.abs(total - exact) <= 2.0 ** -24 * np.abs(exact))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("wdtype", [torch.bfloat16, torch.float32])
+def test_combine_rows(dtype, wdtype):
+    """d3_combine_rows against numpy: sum over j of w[t, j] * rows[inverse[t k + j]] (float64 sum, then the output
+    dtype), within float32 rounding of the sum of |terms| before the output's own rounding; pairs with inverse -1 left
+    out."""
+    rng = np.random.default_rng(3)
+    T, k, H = 29, 8, 2048
+    rows = rng.standard_normal((T * k, H)).astype(np.float32)
+    inverse = rng.permutation(T * k).astype(np.int32)
+    inverse[5] = -1
+    w = rng.dirichlet(np.ones(k), T).astype(np.float32)
+    wt = torch.from_numpy(w).to(DEV, wdtype)
+    wv = wt.float().cpu().numpy().astype(np.float64)
+    got = kernels.combine_rows(dev(rows), dev(inverse), wt, dtype).float().cpu().numpy()
+    terms = np.zeros((T, k, H))
+    for t in range(T):
+        for j in range(k):
+            at = inverse[t * k + j]
+            if at >= 0:
+                terms[t, j] = wv[t, j] * rows[at]
+    want = terms.sum(1)
+    bound = 1e-6 * np.abs(terms).sum(1) + (0 if dtype == torch.float32 else
+                                          (2.0 ** -8 if dtype == torch.bfloat16 else 2.0 ** -11) * np.abs(want))
+    assert np.all(np.abs(got - want) <= bound + 1e-30)
+
+
 # ----------------------------------------------------------------------------------------------------- decode
 @pytest.mark.parametrize("bits", [4, 6])
 def test_decode_codes_bit_exact_exhaustive(bits):
@@ -292,29 +376,25 @@ def test_gemv_codes_fill(bits):
 
 
 # --------------------------------------------------------------------------------------------------- grouped
-@pytest.mark.parametrize("kind", ["int8", "fp8", "w4", "w6"])
-def test_grouped(kind):
-    rng = np.random.default_rng(len(kind) + 40)
-    E, N, K, slots = 6, 256, 768, 3
+def _bank(kind, rng, E, N, K):
     if kind == "int8":
-        host = int8_bank(rng, E, N, K)
-    elif kind == "fp8":
-        host = fp8_bank(rng, E, N, K)
-    else:
-        host = codes_bank(rng, E, N, K, int(kind[1]))
+        return int8_bank(rng, E, N, K)
+    if kind == "fp8":
+        return fp8_bank(rng, E, N, K)
+    return codes_bank(rng, E, N, K, int(kind[1]))
+
+
+def _check_grouped(kind, rng, E, N, K, slots, groups, T, matrix):
+    host = _bank(kind, rng, E, N, K)
     slot = {n: np.zeros(((slots * v.shape[0]) // E, *v.shape[1:]), v.dtype) for n, v in host.items()}
     for n, v in host.items():  # expert 2 cached in slot 0
         r = v.shape[0] // E
         slot[n][0:r] = v[2 * r:3 * r]
     cb = ref.default_codebook()
-    # (expert, slot, fill, first, rows): cached, filling slot 2, slot-less, empty, cached again with fill 0
-    groups = np.array([[2, 0, 0, 0, 5], [4, 2, 1, 5, 7], [1, -1, 0, 12, 3], [5, 1, 0, 15, 0], [0, -1, 0, 15, 9]],
-                      np.int32)
-    T = 24
     x = rng.standard_normal((T, K)).astype(np.float32)
     sf, hf = fields_on(slot), fields_on(host)
     out = kernels._grouped({"int8": 0, "fp8": 1, "w4": 4, "w6": 6}[kind], dev(x), dev(groups), sf, hf,
-                           dev(cb) if kind == "w4" else None, N, "weight" if kind == "fp8" else "_qdata")
+                           dev(cb) if kind == "w4" else None, N, "weight" if kind == "fp8" else "_qdata", matrix)
     expect = ref.grouped_ref(kind, x, groups, slot, host, cb, N)
     if kind == "int8":
         absw = np.abs(host["_qdata"].astype(np.float64)) * host["scale"][:, None]
@@ -325,12 +405,43 @@ def test_grouped(kind):
         absw *= host["s_channel"][:, None]
     got = out.cpu().numpy().astype(np.float64)
     for e, _, _, first, rows in groups:
-        for t in range(first, first + rows):
-            bound = 3e-5 * (absw[e * N:(e + 1) * N] @ np.abs(x[t])) + 1e-30
-            assert np.all(np.abs(got[t] - expect[t]) <= bound), (kind, e, t)
+        t = slice(first, first + rows)
+        bound = 3e-5 * (np.abs(x[t]) @ absw[e * N:(e + 1) * N].T) + 1e-30
+        assert np.all(np.abs(got[t] - expect[t]) <= bound), (kind, e)
+    # the filled slots hold their experts' fields, the others are untouched
+    want = {n: v.copy() for n, v in slot.items()}
+    for e, s, f, _, rows in groups:
+        if f:
+            for n, v in host.items():
+                r = v.shape[0] // E
+                want[n][s * r:(s + 1) * r] = v[e * r:(e + 1) * r]
     for n in slot:
-        assert np.array_equal(sf[n].cpu().numpy(), slot[n]), n
+        assert np.array_equal(sf[n].cpu().numpy(), want[n]), n
 
+
+@pytest.mark.parametrize("matrix", [False, True], ids=["valu", "mfma"])
+@pytest.mark.parametrize("kind", ["int8", "fp8", "w4", "w6"])
+def test_grouped(kind, matrix):
+    """Small groups: cached, filling a slot, slot-less, empty, a slot-less one after it."""
+    rng = np.random.default_rng(len(kind) + 40)
+    # (expert, slot, fill, first, rows): cached, filling slot 2, slot-less, empty, cached again with fill 0
+    groups = np.array([[2, 0, 0, 0, 5], [4, 2, 1, 5, 7], [1, -1, 0, 12, 3], [5, 1, 0, 15, 0], [0, -1, 0, 15, 9]],
+                      np.int32)
+    _check_grouped(kind, rng, 6, 256, 768, 3, groups, 24, matrix)
+
+
+@pytest.mark.parametrize("N", [128, 256])
+@pytest.mark.parametrize("kind", ["int8", "fp8", "w4", "w6"])
+def test_grouped_mfma_many_rows(kind, N):
+    """The matrix-core path over groups of 0 to 300 rows (several passes over the rows, a fill read on the first pass
+    only, ragged last tiles) at K 2048, the prompt's gate_up width; N 128 runs one 16-row tile per wave, N 256 four."""
+    rng = np.random.default_rng(len(kind) + 90)
+    rows = [300, 1, 17, 129, 0, 64]
+    first = np.concatenate([[0], np.cumsum(rows)[:-1]])
+    groups = np.array([[2, 0, 0, first[0], rows[0]], [4, 2, 1, first[1], rows[1]], [3, 1, 1, first[2], rows[2]],
+                       [1, -1, 0, first[3], rows[3]], [5, -1, 0, first[4], rows[4]], [0, 3, 1, first[5], rows[5]]],
+                      np.int32)
+    _check_grouped(kind, rng, 6, N, 2048, 4, groups, int(sum(rows)), True)
 
 # ---------------------------------------------------------------------------------------------- the layer
 H, I, E = 2048, 768, 8
@@ -421,10 +532,43 @@ def test_resident_prefill(layer):
 
 def test_expert_groups_without_host_sync():
     idx = torch.tensor([[3, 1], [1, 0], [3, 3]], device=DEV)
-    order, groups = offload.expert_groups(idx, 5)
+    order, inverse, groups = offload.expert_groups(idx, 5)
     g = groups.cpu().numpy()
     assert g[:, 4].tolist() == [1, 2, 0, 3, 0] and g[:, 3].tolist() == [0, 1, 3, 3, 6]
     assert idx.reshape(-1)[order].cpu().tolist() == [0, 1, 1, 3, 3, 3]
+    assert sorted(order.cpu().tolist()) == list(range(6)) and inverse[order].cpu().tolist() == list(range(6))
+
+
+@pytest.mark.parametrize("E, T, k, zipf", [(128, 256, 8, True), (256, 2048, 8, True), (1024, 300, 4, False),
+                                           (7, 1, 1, False), (64, 0, 8, False)])
+def test_expert_groups_kernel(E, T, k, zipf):
+    """The counting sort against numpy's stable argsort: the same groups, each group holding the same pairs (in any
+    order), order and inverse each other's inverse; ids outside [0, E) after every group with inverse -1."""
+    rng = np.random.default_rng(E + T)
+    if zipf:
+        p = np.arange(1, E + 1) ** -1.1
+        idx = np.stack([rng.choice(E, k, replace=False, p=p / p.sum()) for _ in range(T)]).reshape(T, k)
+    else:
+        idx = rng.integers(0, E, (T, k))
+    order, inverse, groups = offload.expert_groups(dev(idx.astype(np.int64)), E)
+    order, inverse, g = order.cpu().numpy(), inverse.cpu().numpy(), groups.cpu().numpy()
+    flat = idx.reshape(-1)
+    counts = np.bincount(flat, minlength=E)
+    assert g[:, 0].tolist() == list(range(E)) and g[:, 1].tolist() == list(range(E)) and not g[:, 2].any()
+    assert g[:, 4].tolist() == counts.tolist() and g[:, 3].tolist() == (np.cumsum(counts) - counts).tolist()
+    want = np.argsort(flat, kind="stable")
+    for e in range(E):
+        f, r = g[e, 3], g[e, 4]
+        assert sorted(order[f:f + r].tolist()) == want[f:f + r].tolist(), e
+    assert np.array_equal(inverse[order], np.arange(flat.shape[0]))
+    if T:   # out-of-range ids: placed last, inverse -1
+        bad = idx.copy()
+        bad[0, 0], bad[-1, -1] = -3, E + 5
+        order, inverse, groups = offload.expert_groups(dev(bad.astype(np.int64)), E)
+        order, inverse, g = order.cpu().numpy(), inverse.cpu().numpy(), groups.cpu().numpy()
+        n = flat.shape[0]
+        assert sorted(order.tolist()) == list(range(n)) and g[:, 4].sum() == n - (2 if n > 1 else 1)
+        assert inverse[0] == -1 and inverse[n - 1] == -1 and set(order[g[:, 4].sum():].tolist()) == {0, n - 1}
 
 
 def test_fp8_experts_module():
