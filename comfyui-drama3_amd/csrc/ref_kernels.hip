@@ -535,7 +535,7 @@ __global__ void __launch_bounds__(256) grouped_kernel(const float* x, const int*
 // adds them in. fp8: the 128 x 128 block scale multiplies each chunk's sums, as the reference's block sums are
 // scaled. A pass's rows past a multiple of 16 read its last row and are not stored.
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-constexpr int GM_ROWS = 64;   // activation rows per pass (4 tiles of 16)
+constexpr int GM_ROWS = 32;   // activation rows per pass (2 tiles of 16)
 constexpr int GM_PAD = 136;   // LDS row stride in bf16: 128 columns + 8, so the 16 rows of a tile start 4 banks apart
 
 // x [n] float32 (n % 8 == 0) -> planes hi, mid, lo [n] bf16, x == hi + mid + lo to within 2^-24 |x|
@@ -562,6 +562,7 @@ __global__ void __launch_bounds__(256) split3_kernel(const float* x, int64_t n8,
 // first, then those of 3, 2, 1. Groups that are empty or whose rows lie outside [0, T) get none; no more than cap
 // passes are listed. One workgroup.
 __global__ void __launch_bounds__(256) grouped_plan_kernel(const int* groups, int n_groups, int T, int* work, int cap) {
+  static_assert(GM_ROWS % 16 == 0 && GM_ROWS <= 64, "passes of 1 to 4 tiles");
   __shared__ int count[8], cursor[8];  // bucket 4 - tiles (first passes), 8 - tiles (later passes)
   if (threadIdx.x < 8) count[threadIdx.x] = 0;
   __syncthreads();
@@ -571,7 +572,7 @@ __global__ void __launch_bounds__(256) grouped_plan_kernel(const int* groups, in
     if (rows <= 0 || first < 0 || rows > T - first) continue;
     atomicAdd(&count[4 - tiles_of(rows)], 1);
     if (rows > GM_ROWS) {
-      atomicAdd(&count[4], (rows - GM_ROWS) / GM_ROWS);
+      atomicAdd(&count[8 - GM_ROWS / 16], (rows - GM_ROWS) / GM_ROWS);
       if (rows % GM_ROWS) atomicAdd(&count[8 - tiles_of(rows % GM_ROWS)], 1);
     }
   }
@@ -659,7 +660,7 @@ __global__ void __launch_bounds__(1024) expert_groups_kernel(const int64_t* ids,
 // Planes hi, mid, lo [P, K] of the rows the grouped products read (split3_kernel's split): row p is x's row
 // order[p] / k (x's row p without order); SRC 0 float32 rows [., K], 1 bf16 rows, 2 float32 gate | up rows [., 2K]
 // through SiLU(gate) * up (kernels.py:222-258's SwiGLU); ROT: in the ConvRot basis (H256 on every 256 columns, / 16).
-template <int SRC, bool ROT>
+template <int SRC, bool ROT, int PL>
 __global__ void __launch_bounds__(256) prep_planes_kernel(const void* x, const int64_t* order, int k, int K,
                                                           __bf16* planes, int64_t plane) {
   const int p = blockIdx.x, lane = threadIdx.x & 63, w = threadIdx.x >> 6;
@@ -693,8 +694,10 @@ __global__ void __launch_bounds__(256) prep_planes_kernel(const void* x, const i
     }
     const size_t at = (size_t)p * K + c0;
     *(bf16x4*)(planes + at) = h;
-    *(bf16x4*)(planes + plane + at) = m;
-    *(bf16x4*)(planes + 2 * plane + at) = l;
+    if constexpr (PL == 3) {
+      *(bf16x4*)(planes + plane + at) = m;
+      *(bf16x4*)(planes + 2 * plane + at) = l;
+    }
   }
 }
 
@@ -752,10 +755,44 @@ template <int KIND> D3_INLINE bf16x8 weights8(uint32_t w0, uint32_t w1) {
   return a;
 }
 
+// W6: one 16-code group's int8-grid values (decode_group<6>'s arithmetic: clamp(rint((code - 32) * s), +-127), with
+// (code - 32) * s formed exactly as code * s - 32 s) as bf16, codes 0-7 in a0, 8-15 in a1. lo / hi: the nibble words
+// of codes 0-7 / 8-15 (code j's low nibble at bits 4 (j & 7)); high: code j's top two bits at bits 2j. Codes k, k + 4,
+// k + 8, k + 12 are assembled together, one per byte: their nibbles by one byte permute, their top bits by a shift.
+D3_INLINE void w6_group(uint32_t lo, uint32_t hi, uint32_t high, float s, bf16x8& a0, bf16x8& a1) {
+  const float ms = -32.0f * s;
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    const uint32_t h = k >> 1, sel = h | ((h + 2) << 8) | ((h + 4) << 16) | ((h + 6) << 24);
+    const uint32_t p = __builtin_amdgcn_perm(hi, lo, sel);  // bytes: lo[h], lo[h + 2], hi[h], hi[h + 2]
+    const uint32_t code = ((k & 1 ? p >> 4 : p) & 0x0F0F0F0Fu) | (((high >> (2 * k)) & 0x03030303u) << 4);
+#pragma unroll
+    for (int b = 0; b < 4; b++) {
+      const float q = fminf(fmaxf(rintf(fmaf((float)((code >> (8 * b)) & 0xFFu), s, ms)), -127.0f), 127.0f);
+      if (b < 2) a0[k + 4 * b] = (__bf16)q;
+      else a1[k + 4 * (b - 2)] = (__bf16)q;
+    }
+  }
+}
+
+// W4: one 16-code group's int8-grid values as bf16 through the group's scale-byte row t of the LDS table (build_qtab:
+// decode_group<4>'s values, entry by entry), codes 0-7 in a0, 8-15 in a1; lo / hi the nibble words as for w6_group.
+D3_INLINE void w4_group(uint32_t lo, uint32_t hi, i32x4 t, bf16x8& a0, bf16x8& a1) {
+  const uint32_t w[4] = {lookup16(t, lo) ^ 0x80808080u, lookup16(t, lo >> 4) ^ 0x80808080u,   // codes 0,2,4,6 / 1,3,5,7
+                         lookup16(t, hi) ^ 0x80808080u, lookup16(t, hi >> 4) ^ 0x80808080u};  // 8,10,.. / 9,11,..
+#pragma unroll
+  for (int b = 0; b < 4; b++) {
+    a0[2 * b] = (__bf16)(float)(int8_t)(w[0] >> (8 * b));
+    a0[2 * b + 1] = (__bf16)(float)(int8_t)(w[1] >> (8 * b));
+    a1[2 * b] = (__bf16)(float)(int8_t)(w[2] >> (8 * b));
+    a1[2 * b + 1] = (__bf16)(float)(int8_t)(w[3] >> (8 * b));
+  }
+}
+
 // grid (N / (64 RA), a multiple of 8 rows): the workgroups of one pass run on one XCD (the dispatcher deals
 // workgroup i to XCD i % 8), where its activation rows stay in that XCD's L2. PHASE 2 runs every pass of the plan;
 // PHASE 0 the first passes, PHASE 1 the others, a filled group's then read from its slot (the first passes filled it).
-template <int KIND, int K, int RA>  // KIND 0 int8, 1 fp8, 4 / 6 codes; RA row tiles per wave
+template <int KIND, int K, int RA, int PL>  // KIND 0 int8, 1 fp8, 4 / 6 codes; RA row tiles per wave; PL planes
 __global__ void __launch_bounds__(256, 2) grouped_mfma_kernel(const __bf16* xs, int64_t plane, const int* groups,
                                                               const int* work, int phase, uint8_t* slot_w, void* slot_s,
                                                               void* slot_c, const uint8_t* host_w, const void* host_s,
@@ -764,9 +801,13 @@ __global__ void __launch_bounds__(256, 2) grouped_mfma_kernel(const __bf16* xs, 
   constexpr int RB = KIND <= 1 ? K : K * KIND / 8;  // row bytes
   constexpr int G = K / 16;                          // codes: 16-column scale groups per row
   constexpr int CHUNKS = K / 128, MT = GM_ROWS / 16;
-  constexpr int STAGE = MT * 3;                      // 16-byte pieces each thread stages per chunk
-  __shared__ float lut[16];
-  __shared__ __attribute__((aligned(16))) __bf16 bt[MT * 3 * 16 * GM_PAD];
+  constexpr int STAGE = MT * PL;   // 16-byte pieces each thread stages per chunk
+  // chunks whose weights are on their way while one is multiplied (more gain nothing: the loads complete in order,
+  // and each chunk waits for the next chunk's rows, requested after the weights one chunk ahead)
+  constexpr int GM_AHEAD = 2;
+  static_assert(CHUNKS % GM_AHEAD == 0, "K a multiple of 256");
+  __shared__ uint32_t qtab[KIND == 4 ? QTAB_WORDS : 1];
+  __shared__ __attribute__((aligned(16))) __bf16 bt[MT * PL * 16 * GM_PAD];
   // XCD-aware order: workgroup i of the launch runs on XCD i % 8; passes p with p % 8 == xcd are dealt to it
   const int nx = gridDim.x, lin = blockIdx.x + nx * blockIdx.y, xcd = lin & 7, k = lin >> 3;
   const int item = (k / nx) * 8 + xcd + (phase == 1 ? work[1] : 0), xb = k % nx;
@@ -778,7 +819,7 @@ __global__ void __launch_bounds__(256, 2) grouped_mfma_kernel(const __bf16* xs, 
   const int tiles = min(MT, (rows - m0 + 15) / 16);
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, q = lane >> 4, c = lane & 15;
   const int nw = xb * 64 * RA + 16 * RA * w;  // the wave's first row
-  if (KIND == 4 && tid < 16) lut[tid] = codebook[tid];
+  if constexpr (KIND == 4) build_qtab(qtab, *(const f32x4*)(codebook + 4 * (tid & 3)));
   const size_t src = host ? (size_t)expert : (size_t)slot;  // the expert's index in the fields it is read from
   const uint8_t* arow = (host ? host_w : slot_w) + (src * N + nw + c) * RB;      // this lane's row of tile 0
   uint8_t* frow = filler ? slot_w + ((size_t)slot * N + nw + c) * RB : slot_w;  // its slot row (fill)
@@ -805,23 +846,26 @@ __global__ void __launch_bounds__(256, 2) grouped_mfma_kernel(const __bf16* xs, 
       }
     }
   };
-  // staging: piece j of thread tid is tile j / 3, plane j % 3, row (tid >> 4) & 15, 16 bytes at column 8 (tid & 15)
+  // staging: piece j of thread tid is tile j / PL, plane j % PL, row (tid >> 4) & 15, the 16 bytes at column
+  // 8 (tid & 15)
   const int srow_t = (tid >> 4) & 15, sseg = tid & 15;
+  const size_t srow_at = (size_t)first * K + 8 * sseg;
   i32x4 stg[STAGE];
   auto stage_load = [&](int ch) {
 #pragma unroll
     for (int j = 0; j < STAGE; j++) {
-      const int mt = j / 3, t = j % 3;
+      const int mt = j / PL, t = j % PL;
       if (mt < tiles) {
         const int r = min(m0 + 16 * mt + srow_t, rows - 1);
-        stg[j] = *(const i32x4*)(xs + t * plane + (size_t)(first + r) * K + 128 * ch + 8 * sseg);
+        stg[j] = *(const i32x4*)(xs + t * plane + srow_at + (size_t)r * K + 128 * ch);
       }
     }
   };
   auto stage_store = [&]() {
 #pragma unroll
-    for (int j = 0; j < STAGE; j++)
-      if (j / 3 < tiles) *(i32x4*)(bt + ((j / 3 * 3 + j % 3) * 16 + srow_t) * GM_PAD + 8 * sseg) = stg[j];
+    for (int j = 0; j < STAGE; j++) {
+      if (j < PL * tiles) *(i32x4*)(bt + (j * 16 + srow_t) * GM_PAD + 8 * sseg) = stg[j];
+    }
   };
   // the epilogue's scales of rows nw + 16 a + 4 q .. + 3: int8 row scales, codes channel scales
   float es[RA][4];
@@ -852,30 +896,24 @@ __global__ void __launch_bounds__(256, 2) grouped_mfma_kernel(const __bf16* xs, 
   for (int a = 0; a < RA; a++)
 #pragma unroll
     for (int mt = 0; mt < MT; mt++) acc[a][mt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-  ChunkBytes cur[RA], nxt[RA];
-  load_chunk(0, cur);
-  stage_load(0);
-  stage_store();
-  __syncthreads();
-  for (int ch = 0; ch < CHUNKS; ch++) {
-    if (ch + 1 < CHUNKS) {
-      load_chunk(ch + 1, nxt);
-      stage_load(ch + 1);
-    }
+  // one chunk: its weights (loaded GM_AHEAD chunks ahead into `bytes`, which then take chunk ch + GM_AHEAD's)
+  // decoded, the slot filled, the next chunk's rows on their way, the products from LDS, then the next chunk's rows
+  // into LDS
+  auto chunk = [&](int ch, ChunkBytes (&bytes)[RA]) {
     const int k0 = 128 * ch + 32 * q;
     if (filler) {  // the expert's bytes copied into its slot as they are read
 #pragma unroll
       for (int a = 0; a < RA; a++) {
         uint8_t* f = frow + (size_t)16 * a * RB;
         if constexpr (KIND <= 1) {
-          *(i32x4*)(f + k0) = cur[a].b0;
-          *(i32x4*)(f + k0 + 16) = cur[a].b1;
+          *(i32x4*)(f + k0) = bytes[a].b0;
+          *(i32x4*)(f + k0 + 16) = bytes[a].b1;
         } else {
-          *(i32x4*)(f + k0 / 2) = cur[a].b0;
-          if constexpr (KIND == 6) *(i32x2*)(f + K / 2 + k0 / 4) = i32x2{cur[a].b1.x, cur[a].b1.y};
+          *(i32x4*)(f + k0 / 2) = bytes[a].b0;
+          if constexpr (KIND == 6) *(i32x2*)(f + K / 2 + k0 / 4) = i32x2{bytes[a].b1.x, bytes[a].b1.y};
           uint8_t* fsb = (uint8_t*)slot_s + ((size_t)slot * N + nw + 16 * a + c) * G;
-          fsb[k0 / 16] = (uint8_t)cur[a].sb0;
-          fsb[k0 / 16 + 1] = (uint8_t)cur[a].sb1;
+          fsb[k0 / 16] = (uint8_t)bytes[a].sb0;
+          fsb[k0 / 16 + 1] = (uint8_t)bytes[a].sb1;
         }
       }
     }
@@ -883,21 +921,24 @@ __global__ void __launch_bounds__(256, 2) grouped_mfma_kernel(const __bf16* xs, 
 #pragma unroll
     for (int a = 0; a < RA; a++) {
       if constexpr (KIND <= 1) {
-        wa[a][0] = weights8<KIND>((uint32_t)cur[a].b0.x, (uint32_t)cur[a].b0.y);
-        wa[a][1] = weights8<KIND>((uint32_t)cur[a].b0.z, (uint32_t)cur[a].b0.w);
-        wa[a][2] = weights8<KIND>((uint32_t)cur[a].b1.x, (uint32_t)cur[a].b1.y);
-        wa[a][3] = weights8<KIND>((uint32_t)cur[a].b1.z, (uint32_t)cur[a].b1.w);
+        wa[a][0] = weights8<KIND>((uint32_t)bytes[a].b0.x, (uint32_t)bytes[a].b0.y);
+        wa[a][1] = weights8<KIND>((uint32_t)bytes[a].b0.z, (uint32_t)bytes[a].b0.w);
+        wa[a][2] = weights8<KIND>((uint32_t)bytes[a].b1.x, (uint32_t)bytes[a].b1.y);
+        wa[a][3] = weights8<KIND>((uint32_t)bytes[a].b1.z, (uint32_t)bytes[a].b1.w);
+      } else if constexpr (KIND == 4) {
+        w4_group((uint32_t)bytes[a].b0.x, (uint32_t)bytes[a].b0.y, *(const i32x4*)(qtab + 4 * bytes[a].sb0),
+                 wa[a][0], wa[a][1]);
+        w4_group((uint32_t)bytes[a].b0.z, (uint32_t)bytes[a].b0.w, *(const i32x4*)(qtab + 4 * bytes[a].sb1),
+                 wa[a][2], wa[a][3]);
       } else {
-        float qv[32];
-        decode_group<KIND>((uint32_t)cur[a].b0.x, (uint32_t)cur[a].b0.y, (uint32_t)cur[a].b1.x, cur[a].sb0, lut, qv);
-        decode_group<KIND>((uint32_t)cur[a].b0.z, (uint32_t)cur[a].b0.w, (uint32_t)cur[a].b1.y, cur[a].sb1, lut,
-                           qv + 16);
-#pragma unroll
-        for (int st = 0; st < 4; st++)
-#pragma unroll
-          for (int j = 0; j < 8; j++) wa[a][st][j] = (__bf16)qv[8 * st + j];
+        w6_group((uint32_t)bytes[a].b0.x, (uint32_t)bytes[a].b0.y, (uint32_t)bytes[a].b1.x,
+                 fp8x2_to_f32<false>(bytes[a].sb0).x, wa[a][0], wa[a][1]);
+        w6_group((uint32_t)bytes[a].b0.z, (uint32_t)bytes[a].b0.w, (uint32_t)bytes[a].b1.y,
+                 fp8x2_to_f32<false>(bytes[a].sb1).x, wa[a][2], wa[a][3]);
       }
     }
+    if (ch + GM_AHEAD < CHUNKS) load_chunk(ch + GM_AHEAD, bytes);
+    if (ch + 1 < CHUNKS) stage_load(ch + 1);
     f32x4 part[RA][MT];  // fp8: this chunk's sums before its block scale
 #pragma unroll
     for (int a = 0; a < RA; a++)
@@ -908,15 +949,15 @@ __global__ void __launch_bounds__(256, 2) grouped_mfma_kernel(const __bf16* xs, 
 #pragma unroll
       for (int mt = 0; mt < MT; mt++) {
         if (mt < tiles) {
-          const __bf16* bp = bt + (mt * 3 * 16 + c) * GM_PAD + 32 * q + 8 * st;
-          const bf16x8 b0 = *(const bf16x8*)bp, b1 = *(const bf16x8*)(bp + 16 * GM_PAD),
-                       b2 = *(const bf16x8*)(bp + 32 * GM_PAD);
+          const __bf16* bp = bt + (mt * PL * 16 + c) * GM_PAD + 32 * q + 8 * st;
+          bf16x8 b[PL];
 #pragma unroll
-          for (int a = 0; a < RA; a++) {
-            part[a][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa[a][st], b0, part[a][mt], 0, 0, 0);
-            part[a][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa[a][st], b1, part[a][mt], 0, 0, 0);
-            part[a][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa[a][st], b2, part[a][mt], 0, 0, 0);
-          }
+          for (int t = 0; t < PL; t++) b[t] = *(const bf16x8*)(bp + 16 * t * GM_PAD);
+#pragma unroll
+          for (int a = 0; a < RA; a++)
+#pragma unroll
+            for (int t = 0; t < PL; t++)
+              part[a][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa[a][st], b[t], part[a][mt], 0, 0, 0);
         }
       }
     if constexpr (KIND == 1) {
@@ -937,9 +978,17 @@ __global__ void __launch_bounds__(256, 2) grouped_mfma_kernel(const __bf16* xs, 
       __syncthreads();  // every wave is done with this chunk's rows
       stage_store();
       __syncthreads();
-#pragma unroll
-      for (int a = 0; a < RA; a++) cur[a] = nxt[a];
     }
+  };
+  ChunkBytes ring[GM_AHEAD][RA];  // chunk ch's weight bytes in ring[ch % GM_AHEAD]
+#pragma unroll
+  for (int d = 0; d < GM_AHEAD; d++) load_chunk(d, ring[d]);
+  stage_load(0);
+  stage_store();
+  __syncthreads();
+  for (int ch = 0; ch < CHUNKS; ch += GM_AHEAD) {
+#pragma unroll
+    for (int d = 0; d < GM_AHEAD; d++) chunk(ch + d, ring[d]);
   }
   // lane l holds rows nw + 16 a + 4 q .. + 3 of activation row m0 + 16 mt + (l & 15)
 #pragma unroll
@@ -1845,14 +1894,26 @@ int64_t d3_grouped_mfma_work_ints(int32_t n_groups, int64_t rows) {
   return 2 + 2 * ((cap + 7) / 8 * 8);
 }
 
-int d3_grouped_mfma(int32_t kind, const void* planes, int64_t plane, const int32_t* groups, int32_t n_groups,
-                    int32_t* work, int64_t work_ints, int32_t fills_first, void* slot_w, void* slot_s, void* slot_c,
-                    const void* host_w, const void* host_s, const void* host_c, const float* codebook, float* out,
-                    int32_t N, int32_t K, void* stream) {
+int d3_grouped_plan(const int32_t* groups, int32_t n_groups, int64_t rows, int32_t* work, int64_t work_ints,
+                    void* stream) {
+  if (!groups || !work) return fail("d3_grouped_plan: null pointer");
+  if (n_groups < 1 || rows < 0 || rows > INT32_MAX) return fail("d3_grouped_plan: n_groups >= 1, 0 <= rows < 2^31");
+  const int64_t need = d3_grouped_mfma_work_ints(n_groups, rows);
+  if (work_ints < need) return fail("d3_grouped_plan: work holds fewer than d3_grouped_mfma_work_ints ints");
+  hipLaunchKernelGGL(grouped_plan_kernel, dim3(1), dim3(256), 0, (hipStream_t)stream, groups, n_groups, (int)rows,
+                     work, (int)((need - 2) / 2));
+  return done("d3_grouped_plan");
+}
+
+int d3_grouped_mfma(int32_t kind, const void* planes, int32_t n_planes, int64_t plane, const int32_t* groups,
+                    int32_t n_groups, const int32_t* work, int64_t work_ints, int32_t fills_first, void* slot_w,
+                    void* slot_s, void* slot_c, const void* host_w, const void* host_s, const void* host_c,
+                    const float* codebook, float* out, int32_t N, int32_t K, void* stream) {
   if (!planes || !groups || !work || !slot_w || !slot_s || !host_w || !host_s || !out)
     return fail("d3_grouped_mfma: null pointer");
   if ((kind == 4 || kind == 6) && (!slot_c || !host_c)) return fail("d3_grouped_mfma: codes need channel scales");
   if (kind == 4 && !codebook) return fail("d3_grouped_mfma: 4 bits need a codebook");
+  if (n_planes != 1 && n_planes != 3) return fail("d3_grouped_mfma: 1 or 3 planes");
   if (n_groups < 1) return 0;
   if (N < 64 || N % (kind == 1 ? 128 : 64) || !supported_k(K) || plane < K || plane % K)
     return fail("d3_grouped_mfma: N % 64 == 0 (N % 128 == 0 for fp8), K in {256..2048}, plane a multiple of K");
@@ -1862,12 +1923,16 @@ int d3_grouped_mfma(int32_t kind, const void* planes, int64_t plane, const int32
   if (work_ints < need) return fail("d3_grouped_mfma: work holds fewer than d3_grouped_mfma_work_ints ints");
   const int cap = (int)((need - 2) / 2), firsts = (n_groups + 7) / 8 * 8;
   const hipStream_t s = (hipStream_t)stream;
-  hipLaunchKernelGGL(grouped_plan_kernel, dim3(1), dim3(256), 0, s, groups, n_groups, (int)T, work, cap);
   const __bf16* xs = (const __bf16*)planes;
   const uint8_t* hw = (const uint8_t*)host_w;
   uint8_t* sw = (uint8_t*)slot_w;
-#define D3_GM(KD, RA, PH, Y) D3_K_SWITCH(K, hipLaunchKernelGGL((grouped_mfma_kernel<KD, KK, RA>), dim3(N / (64 * RA), Y), dim3(256), 0, s, xs, plane, groups, work, PH, sw, slot_s, slot_c, hw, host_s, host_c, codebook, out, N))
-#define D3_GM_RA(KD, PH, Y) if (N % 128 == 0) { D3_GM(KD, 2, PH, Y); } else { D3_GM(KD, 1, PH, Y); }
+#define D3_GM(KD, RA, PL, PH, Y) D3_K_SWITCH(K, hipLaunchKernelGGL((grouped_mfma_kernel<KD, KK, RA, PL>), dim3(N / (64 * RA), Y), dim3(256), 0, s, xs, plane, groups, work, PH, sw, slot_s, slot_c, hw, host_s, host_c, codebook, out, N))
+#define D3_GM_RA(KD, PH, Y)                                                                            \
+  if (n_planes == 1) {                                                                                 \
+    if (N % 128 == 0) { D3_GM(KD, 2, 1, PH, Y); } else { D3_GM(KD, 1, 1, PH, Y); }                     \
+  } else {                                                                                             \
+    if (N % 128 == 0) { D3_GM(KD, 2, 3, PH, Y); } else { D3_GM(KD, 1, 3, PH, Y); }                     \
+  }
 #define D3_GM_KIND(PH, Y)                          \
   switch (kind) {                                  \
     case 0: D3_GM_RA(0, PH, Y); break;             \
@@ -1897,22 +1962,28 @@ int d3_expert_groups(const int64_t* ids, int32_t P, int32_t E, int64_t* order, i
   return done("d3_expert_groups");
 }
 
-int d3_prep_planes(int32_t mode, int32_t rotate, const void* x, const int64_t* order, int32_t k, int32_t P, int32_t K,
-                   void* planes, void* stream) {
+int d3_prep_planes(int32_t mode, int32_t rotate, int32_t n_planes, const void* x, const int64_t* order, int32_t k,
+                   int32_t P, int32_t K, void* planes, void* stream) {
   if (!x || !planes) return fail("d3_prep_planes: null pointer");
   if (mode < 0 || mode > 2 || P < 0 || k < 1 || !supported_k(K)) return fail("d3_prep_planes: mode 0-2, K in {256..2048}");
+  if (n_planes != 3 && !(n_planes == 1 && mode == 1 && !rotate))
+    return fail("d3_prep_planes: 3 planes, or 1 for bf16 rows taken as they are");
   if (P == 0) return 0;
   const hipStream_t s = (hipStream_t)stream;
   const int64_t plane = (int64_t)P * K;
   __bf16* out = (__bf16*)planes;
-#define D3_PREP(M, R) hipLaunchKernelGGL((prep_planes_kernel<M, R>), dim3(P), dim3(256), 0, s, x, order, k, K, out, plane)
-  switch (mode * 2 + (rotate ? 1 : 0)) {
-    case 0: D3_PREP(0, false); break;
-    case 1: D3_PREP(0, true); break;
-    case 2: D3_PREP(1, false); break;
-    case 3: D3_PREP(1, true); break;
-    case 4: D3_PREP(2, false); break;
-    default: D3_PREP(2, true); break;
+#define D3_PREP(M, R, PL) hipLaunchKernelGGL((prep_planes_kernel<M, R, PL>), dim3(P), dim3(256), 0, s, x, order, k, K, out, plane)
+  if (n_planes == 1) {
+    D3_PREP(1, false, 1);
+  } else {
+    switch (mode * 2 + (rotate ? 1 : 0)) {
+      case 0: D3_PREP(0, false, 3); break;
+      case 1: D3_PREP(0, true, 3); break;
+      case 2: D3_PREP(1, false, 3); break;
+      case 3: D3_PREP(1, true, 3); break;
+      case 4: D3_PREP(2, false, 3); break;
+      default: D3_PREP(2, true, 3); break;
+    }
   }
 #undef D3_PREP
   return done("d3_prep_planes");

@@ -147,19 +147,26 @@ def _grouped_fields(slot_fields, host_fields, codebook, wkey):
             _p(host_fields["scale"]), _p(host_fields.get("s_channel")), _p(codebook))
 
 
-def grouped_planes(kind, planes, rows, width, groups, slot_fields, host_fields, codebook, n, fills_first=False):
-    """[rows, n] float32: the grouped products on the matrix cores over planes [3, rows * width] bf16 (prep_planes /
-    split); kind "int8", "fp8", "w4" or "w6". fills_first: every group's first pass before the others, which then
-    read a filled group from its slot."""
+def grouped_plan(groups, rows):
+    """The work list of the grouped products over `rows` sorted rows in `groups` [g, 5] int32: passes of up to 32
+    rows, on the device. One plan serves every bank the same rows and groups go through."""
+    ints = _lib.lib().d3_grouped_mfma_work_ints(groups.shape[0], rows)
+    work = torch.empty(ints, dtype=torch.int32, device=groups.device)
+    _call("d3_grouped_plan", _p(groups), groups.shape[0], rows, _p(work), ints, _stream(groups))
+    return work
+
+
+def grouped_planes(kind, planes, rows, width, groups, work, slot_fields, host_fields, codebook, n, fills_first=False):
+    """[rows, n] float32: the grouped products on the matrix cores over planes [1 or 3, rows * width] bf16
+    (prep_planes / split) and the plan `work` (grouped_plan); kind "int8", "fp8", "w4" or "w6". fills_first: every
+    group's first pass before the others, which then read a filled group from its slot."""
     code, wkey = GROUPED_KINDS[kind]
     out = torch.empty((rows, n), dtype=torch.float32, device=planes.device)
     if rows == 0:
         return out
-    ints = _lib.lib().d3_grouped_mfma_work_ints(groups.shape[0], rows)
-    work = torch.empty(ints, dtype=torch.int32, device=planes.device)
-    _call("d3_grouped_mfma", code, _p(planes), rows * width, _p(groups), groups.shape[0], _p(work), ints,
-          int(fills_first), *_grouped_fields(slot_fields, host_fields, codebook, wkey), _p(out), n, width,
-          _stream(planes))
+    _call("d3_grouped_mfma", code, _p(planes), planes.shape[0], rows * width, _p(groups), groups.shape[0], _p(work),
+          work.shape[0], int(fills_first), *_grouped_fields(slot_fields, host_fields, codebook, wkey), _p(out), n,
+          width, _stream(planes))
     return out
 
 
@@ -171,7 +178,8 @@ def _grouped(kind, x, groups, slot_fields, host_fields, codebook, n, wkey, matri
         planes = torch.empty((3, x.numel()), dtype=torch.bfloat16, device=x.device)
         _call("d3_split_bf16x3", _p(x), x.numel(), _p(planes), _stream(x))
         name = {0: "int8", 1: "fp8", 4: "w4", 6: "w6"}[kind]
-        return grouped_planes(name, planes, x.shape[0], x.shape[1], groups, slot_fields, host_fields, codebook, n)
+        return grouped_planes(name, planes, x.shape[0], x.shape[1], groups, grouped_plan(groups, x.shape[0]),
+                              slot_fields, host_fields, codebook, n)
     out = torch.empty((x.shape[0], n), dtype=torch.float32, device=x.device)
     if x.numel():
         _call("d3_grouped", kind, _p(x), _p(groups), groups.shape[0],
@@ -194,9 +202,10 @@ def expert_groups(topk_idx, num_experts):
     return order, inverse, groups
 
 
-def prep_planes(x, rotate, order=None, k=1, swiglu=False):
-    """planes [3, P * K] bf16 for grouped_planes: row p is x's row order[p] // k (x's row p without order), through
-    SiLU(gate) * up first with `swiglu` (x float32 gate | up [., 2K]), in the ConvRot basis with `rotate`."""
+def prep_planes(x, rotate, order=None, k=1, swiglu=False, n_planes=3):
+    """planes [n_planes, P * K] bf16 for grouped_planes: row p is x's row order[p] // k (x's row p without order),
+    through SiLU(gate) * up first with `swiglu` (x float32 gate | up [., 2K]), in the ConvRot basis with `rotate`.
+    n_planes 1 takes bf16 rows as they are (no rotation, no SwiGLU); 3 splits float32 values into hi + mid + lo."""
     x = x.contiguous()
     width = x.shape[1] // 2 if swiglu else x.shape[1]
     if swiglu:
@@ -208,8 +217,8 @@ def prep_planes(x, rotate, order=None, k=1, swiglu=False):
     else:
         x, mode = x.float(), 0
     P = order.shape[0] if order is not None else x.shape[0]
-    planes = torch.empty((3, P * width), dtype=torch.bfloat16, device=x.device)
-    _call("d3_prep_planes", mode, int(rotate), _p(x), _p(order), int(k), P, width, _p(planes), _stream(x))
+    planes = torch.empty((n_planes, P * width), dtype=torch.bfloat16, device=x.device)
+    _call("d3_prep_planes", mode, int(rotate), n_planes, _p(x), _p(order), int(k), P, width, _p(planes), _stream(x))
     return planes
 
 

@@ -218,17 +218,20 @@ int d3_grouped(int32_t kind, const float* x, const int32_t* groups, int32_t n_gr
 /* The same products on the bf16 matrix cores (same replacement, same fields and groups). The float32 rows are first
  * split into three bf16 planes, by d3_split_bf16x3 (x [n] float32, n % 8 == 0 -> planes bf16 [3, n] = hi, mid, lo)
  * or d3_prep_planes: x == hi + mid + lo to within 2^-24 |x|, and every weight of these formats is a bf16 value
- * exactly, so each product is exact and the sums float32. d3_grouped_mfma reads planes [3, plane] holding x [T, K]
- * (plane = T * K elements per plane); N % 64 == 0 (N % 128 == 0 for fp8). work: int32 device memory of
- * d3_grouped_mfma_work_ints(n_groups, T) ints, where the call lists its passes of up to 64 rows over the groups (a
- * group whose rows lie outside [0, T) is skipped). fills_first: the groups' first passes run first, then the others
- * read a filled group from its slot, so an expert copied in crosses the bus once however many rows it has. */
+ * exactly, so each product is exact and the sums float32. Rows that are bf16 already take one plane (n_planes 1).
+ * d3_grouped_mfma reads planes [n_planes, plane] holding x [T, K] (plane = T * K elements per plane); N % 64 == 0
+ * (N % 128 == 0 for fp8). work: int32 device memory of d3_grouped_mfma_work_ints(n_groups, T) ints, filled by
+ * d3_grouped_plan for these groups and T (one plan serves both banks of a layer): passes of up to 32 rows, a group
+ * whose rows lie outside [0, T) skipped. fills_first: the groups' first passes run first, then the others read a
+ * filled group from its slot, so an expert copied in crosses the bus once however many rows it has. */
 int d3_split_bf16x3(const float* x, int64_t n, void* planes, void* stream);
 int64_t d3_grouped_mfma_work_ints(int32_t n_groups, int64_t rows);
-int d3_grouped_mfma(int32_t kind, const void* planes, int64_t plane, const int32_t* groups, int32_t n_groups,
-                    int32_t* work, int64_t work_ints, int32_t fills_first, void* slot_w, void* slot_s, void* slot_c,
-                    const void* host_w, const void* host_s, const void* host_c, const float* codebook, float* out,
-                    int32_t N, int32_t K, void* stream);
+int d3_grouped_plan(const int32_t* groups, int32_t n_groups, int64_t rows, int32_t* work, int64_t work_ints,
+                    void* stream);
+int d3_grouped_mfma(int32_t kind, const void* planes, int32_t n_planes, int64_t plane, const int32_t* groups,
+                    int32_t n_groups, const int32_t* work, int64_t work_ints, int32_t fills_first, void* slot_w,
+                    void* slot_s, void* slot_c, const void* host_w, const void* host_s, const void* host_c,
+                    const float* codebook, float* out, int32_t N, int32_t K, void* stream);
 
 /* A prompt's (token, k) pairs grouped by expert (offload.py:140-143, which sorts ids and counts each expert's pairs):
  * ids [P] int64 (P = T * k, row-major); order [P] int64 = the pairs' indices, each expert's pairs together and the
@@ -238,12 +241,13 @@ int d3_grouped_mfma(int32_t kind, const void* planes, int64_t plane, const int32
 int d3_expert_groups(const int64_t* ids, int32_t P, int32_t E, int64_t* order, int32_t* inverse, int32_t* groups,
                      void* stream);
 
-/* The planes d3_grouped_mfma reads, from the rows themselves: planes bf16 [3, P * K]; row p is x's row order[p] / k
- * (x's row p when order is NULL). mode 0: x float32 [., K]; 1: bf16 [., K]; 2: float32 gate | up [., 2K] through
- * SiLU(gate) * up (the SwiGLU between the banks, kernels.py:222-258). rotate: in the ConvRot basis first (int8 and the
- * codes; d3_rotate's transform). K in {256, 512, 768, 1024, 1536, 2048}. */
-int d3_prep_planes(int32_t mode, int32_t rotate, const void* x, const int64_t* order, int32_t k, int32_t P, int32_t K,
-                   void* planes, void* stream);
+/* The planes d3_grouped_mfma reads, from the rows themselves: planes bf16 [n_planes, P * K]; row p is x's row
+ * order[p] / k (x's row p when order is NULL). mode 0: x float32 [., K]; 1: bf16 [., K]; 2: float32 gate | up
+ * [., 2K] through SiLU(gate) * up (the SwiGLU between the banks, kernels.py:222-258). rotate: in the ConvRot basis
+ * first (int8 and the codes; d3_rotate's transform). n_planes 3, or 1 for bf16 rows taken as they are (mode 1, no
+ * rotation: the one plane holds them exactly). K in {256, 512, 768, 1024, 1536, 2048}. */
+int d3_prep_planes(int32_t mode, int32_t rotate, int32_t n_planes, const void* x, const int64_t* order, int32_t k,
+                   int32_t P, int32_t K, void* planes, void* stream);
 
 /* The weighted sum over k (offload.py:144-149): out [T, H] = sum over j in order of weights[t, j] *
  * sorted_out[inverse[t k + j]] in float32 (pairs with inverse -1 left out), stored as float32 / bf16 / fp16

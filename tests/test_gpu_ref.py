@@ -121,6 +121,19 @@ def planes_np(planes, P, K):
     return [planes[t].float().cpu().numpy().reshape(P, K) for t in range(3)]
 
 
+def test_prep_planes_one_plane_holds_bf16_rows():
+    """n_planes 1: the gathered bf16 rows themselves, bit for bit."""
+    rng = np.random.default_rng(12)
+    T, k, K = 19, 4, 2048
+    bits = numerics.f32_to_bf16_bits(rng.standard_normal((T, K)).astype(np.float32))
+    order = rng.permutation(T * k)
+    planes = kernels.prep_planes(dev(bits).view(torch.bfloat16), False, dev(order.astype(np.int64)), k, n_planes=1)
+    assert planes.shape == (1, T * k * K)
+    assert np.array_equal(planes.view(torch.int16).cpu().numpy().reshape(T * k, K).view(np.uint16), bits[order // k])
+    with pytest.raises(RuntimeError, match="1 for bf16 rows"):
+        kernels.prep_planes(dev(bits).view(torch.bfloat16), True, n_planes=1)
+
+
 @pytest.mark.parametrize("mode, rotate", [("f32", False), ("bf16", True), ("bf16", False), ("swiglu", True),
                                           ("swiglu", False)])
 def test_prep_planes(mode, rotate):
@@ -445,6 +458,38 @@ def test_grouped_mfma_many_rows(kind, N):
 
 # ---------------------------------------------------------------------------------------------- the layer
 H, I, E = 2048, 768, 8
+
+
+@pytest.mark.parametrize("matrix", [False, True], ids=["valu", "mfma"])
+@pytest.mark.parametrize("kind", ["int8", "fp8", "w4", "w6"])
+def test_grouped_decodes_exactly(kind, matrix):
+    """One-hot activation rows (x = [I; I], K = 256 rows per expert) make each output one weight: out[t, n] = the
+    dequantized weight of row n at column t, a single product rounded once to float32, so it must equal the oracle's
+    weights (the int8 grid times the row or channel scale, e4m3 times the block scale) bit for bit. Pins the decode
+    (every code and scale byte the banks hold) through the grouped products, whatever the summation order."""
+    rng = np.random.default_rng(len(kind) + 7)
+    E, N, K = 2, 128, 256
+    host = _bank(kind, rng, E, N, K)
+    if kind in ("w4", "w6"):   # every finite e4m3 scale byte, tiny (all codes to 0) to huge (all clamped to +-127)
+        finite = np.array([b for b in range(256) if b & 0x7F != 0x7F], np.uint8)
+        host["scale"] = rng.choice(finite, size=host["scale"].shape)
+    x = np.concatenate([np.eye(K, dtype=np.float32)] * E)
+    groups = np.array([[e, -1, 0, e * K, K] for e in range(E)], np.int32)
+    cb = ref.default_codebook()
+    sf = fields_on({n: np.zeros_like(v) for n, v in host.items()})
+    out = kernels._grouped({"int8": 0, "fp8": 1, "w4": 4, "w6": 6}[kind], dev(x), dev(groups), sf, fields_on(host),
+                           dev(cb) if kind == "w4" else None, N, "weight" if kind == "fp8" else "_qdata", matrix)
+    got = out.cpu().numpy()
+    if kind == "int8":
+        w = host["_qdata"].astype(np.float32) * host["scale"].reshape(-1, 1)
+    elif kind == "fp8":
+        w = ref.fp8_rows(host["weight"], host["scale"]).astype(np.float32)
+    else:
+        w = ref.decode_codes_ref(host["_qdata"], host["scale"], int(kind[1]), cb).astype(np.float32)
+        w = w * host["s_channel"].reshape(-1, 1).astype(np.float32)
+    for e in range(E):
+        want = w[e * N:(e + 1) * N].T
+        assert np.array_equal(got[e * K:(e + 1) * K], want), (kind, e, int((got[e * K:(e + 1) * K] != want).sum()))
 
 
 def layer_banks(kind, seed):
