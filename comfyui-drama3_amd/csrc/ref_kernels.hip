@@ -1927,11 +1927,13 @@ int d3_grouped_mfma(int32_t kind, const void* planes, int32_t n_planes, int64_t 
   const uint8_t* hw = (const uint8_t*)host_w;
   uint8_t* sw = (uint8_t*)slot_w;
 #define D3_GM(KD, RA, PL, PH, Y) D3_K_SWITCH(K, hipLaunchKernelGGL((grouped_mfma_kernel<KD, KK, RA, PL>), dim3(N / (64 * RA), Y), dim3(256), 0, s, xs, plane, groups, work, PH, sw, slot_s, slot_c, hw, host_s, host_c, codebook, out, N))
+// two 16-row tiles per wave where N allows, one for W6 (its decode is the heaviest: at 128 registers a SIMD holds
+// twice the waves, so one's decode overlaps another's loads and products)
 #define D3_GM_RA(KD, PH, Y)                                                                            \
   if (n_planes == 1) {                                                                                 \
-    if (N % 128 == 0) { D3_GM(KD, 2, 1, PH, Y); } else { D3_GM(KD, 1, 1, PH, Y); }                     \
+    if (N % 128 == 0 && KD != 6) { D3_GM(KD, 2, 1, PH, Y); } else { D3_GM(KD, 1, 1, PH, Y); }          \
   } else {                                                                                             \
-    if (N % 128 == 0) { D3_GM(KD, 2, 3, PH, Y); } else { D3_GM(KD, 1, 3, PH, Y); }                     \
+    if (N % 128 == 0 && KD != 6) { D3_GM(KD, 2, 3, PH, Y); } else { D3_GM(KD, 1, 3, PH, Y); }          \
   }
 #define D3_GM_KIND(PH, Y)                          \
   switch (kind) {                                  \

@@ -279,28 +279,28 @@ def resident_decode_ref(x_bits, ids, weights, banks, rows, kind, codebooks):
 
 def resident_prefill_ref(x_bits, topk_idx, topk_weight, banks, rows, kind, codebooks):
     """offload.py:126-149 resident_prefill: rows x [T, H] (bf16 bits) through their top-k experts, each product scaled
-    by its weight and summed over k -> bf16 bits [T, H]."""
+    by its weight and summed over k in k's order -> bf16 bits [T, H]. Each expert's rows go through it together (one
+    float64 matrix product per bank), each pair's row as resident_decode_ref computes it."""
     topk_idx = np.asarray(topk_idx)
     T, k = topk_idx.shape
     (gate_up, down), (gu_rows, dn_rows) = banks, rows
     x = bf16_bits_to_f32(x_bits).astype(np.float64)
     xin = x if kind == "fp8" else rotate_ref(x)
     w = np.asarray(topk_weight, np.float64)
+    pairs = np.zeros((T, k, dn_rows))
+    I = gu_rows // 2
+    for e in np.unique(topk_idx):
+        ts, js = np.nonzero(topk_idx == e)
+        wg = expert_rows(kind, gate_up, int(e), gu_rows, codebooks[0])
+        wd = expert_rows(kind, down, int(e), dn_rows, codebooks[1])
+        gu = xin[ts] @ wg.T
+        h = silu(gu[:, :I]) * gu[:, I:]
+        if kind != "fp8":
+            h = rotate_ref(h)
+        pairs[ts, js] = h @ wd.T
     out = np.zeros((T, dn_rows))
-    mats = {}
-    for t in range(T):
-        for j in range(k):
-            e = int(topk_idx[t, j])
-            if e not in mats:
-                mats[e] = (expert_rows(kind, gate_up, e, gu_rows, codebooks[0]),
-                           expert_rows(kind, down, e, dn_rows, codebooks[1]))
-            wg, wd = mats[e]
-            gu = wg @ xin[t]
-            I = gu_rows // 2
-            h = silu(gu[:I]) * gu[I:]
-            if kind != "fp8":
-                h = rotate_ref(h[None])[0]
-            out[t] += (wd @ h) * w[t, j]
+    for j in range(k):
+        out += pairs[:, j] * w[:, j:j + 1]
     return f32_to_bf16_bits(out.astype(np.float32))
 
 

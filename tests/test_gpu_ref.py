@@ -575,6 +575,38 @@ def test_resident_prefill(layer):
     assert_bf16_close(bits_of(got), ref.resident_prefill_ref(x, idx, w, banks, (2 * I, H), kind, cbs))
 
 
+def zipf_topk(rng, T, E, k, s=1.1):
+    """[T, k] expert ids: per row a draw of k distinct experts without replacement from Zipf(s) over a random ranking of
+    the experts (Gumbel-top-k over log p(rank), p(rank) ~ rank^-s), the prompt routing of the 256-row workload."""
+    logp = np.empty(E)
+    logp[rng.permutation(E)] = -s * np.log(np.arange(1, E + 1))
+    g = logp - np.log(-np.log(rng.uniform(1e-12, 1 - 1e-7, (T, E))))
+    return np.argsort(-g, axis=1, kind="stable")[:, :k]
+
+
+@pytest.mark.parametrize("kind", ["int8", "fp8", "w4", "w6"])
+def test_resident_prefill_256_rows_zipf(kind):
+    """The prompt workload: 256 rows, top-8 of Zipf(1.1) routing, the layer's shape (H 2048, I 768) over 32 experts
+    (random fields of each format: the oracle's dequantization of 64 experts per format would take minutes), so the
+    hottest experts take well over 64 rows (several passes of the grouped products) and the coldest one or two.
+    Against the oracle's resident layer, at the bf16 bar of the other layer tests."""
+    rng = np.random.default_rng(300 + len(kind))
+    E, T, k = 32, 256, 8
+    banks = (_bank(kind, rng, E, 2 * I, H), _bank(kind, rng, E, H, I))
+    cb = ref.default_codebook()
+    cbs = (cb, cb) if kind == "w4" else (None, None)
+    idx = zipf_topk(rng, T, E, k)
+    counts = np.bincount(idx.reshape(-1), minlength=E)
+    assert counts.max() > 128 and (counts > 0).sum() >= 24
+    w = numerics.bf16_round(rng.dirichlet(np.ones(k), T).astype(np.float32))
+    x = numerics.f32_to_bf16_bits(rng.standard_normal((T, H)).astype(np.float32))
+    dbanks = [fields_on(b) for b in banks]
+    dcbs = tuple(None if c is None else dev(c) for c in cbs)
+    got = offload.resident_prefill(dev(x).view(torch.bfloat16), dev(idx.astype(np.int64)), dev(w).to(torch.bfloat16),
+                                   dbanks, (2 * I, H), kind, dcbs, E)
+    assert_bf16_close(bits_of(got), ref.resident_prefill_ref(x, idx, w, banks, (2 * I, H), kind, cbs))
+
+
 def test_expert_groups_without_host_sync():
     idx = torch.tensor([[3, 1], [1, 0], [3, 3]], device=DEV)
     order, inverse, groups = offload.expert_groups(idx, 5)
