@@ -13,6 +13,7 @@ Other workloads of the same layer shape:
                                                 MFMA path (d3_moe_a8_prefill), 16 layers chained
     --mode resident --format fp8                the reference's own layouts and float activations (kernels.route +
                                                 offload.resident_decode), the drop-in path for converted files
+    --mode resident --rows 256 --routing zipf   its prompt path (offload.resident_prefill: grouped bf16 MFMA products)
     --mode gemv                                 one FP8 expert weight [1536, 2048] with a bf16 scale per output row
                                                 against one bf16 row, dequantize-then-matmul semantics
                                                 (kernels.fp8_linear): 128 distinct weights, one launch each
@@ -28,8 +29,8 @@ Prints one JSON line: metric (expert-weight GB/s), tokens/s, the roofline of the
 a bounded sample of the same workload on this host. The default run (int8, one row) also times the other formats'
 one-row layers (W4A8 and FP8 with normal routing, W6A8 with Zipf routing) under config.other_formats, and the other
 workloads of the same layer under config.other_workloads: the single FP8 GEMV, W4A8 with 4 and 16 batched lines,
-the 256-row FP8 prefill, the reference-format resident decode in the four formats and the int8 block (as their own
-modes run them, without the CPU leg).
+the 256-row FP8 prefill, the reference-format resident decode and 256-row prompt in the four formats and the int8
+block (as their own modes run them, without the CPU leg).
 """
 import argparse
 import ctypes
@@ -562,10 +563,56 @@ def bank_bytes(fields):
     return sum(t.numel() * t.element_size() for t in fields.values()) // E
 
 
+def run_resident_prompt(args, fmt, device):
+    """The reference-format prompt path (kernels.route + offload.resident_prefill: the pairs grouped by expert, the
+    rows gathered, rotated and split into bf16 planes, the grouped products on the matrix cores per bank, the SwiGLU
+    between them, the weighted sum) over args.rows rows, L layers in one HIP graph, each layer over the same rows."""
+    from drama3 import kernels, offload
+    T, L = args.rows, args.layers
+    log(f"building {L} layers of {args.format} experts in the reference's layouts")
+    layers = make_reference_banks(args.format, L, device)
+    logits = make_logits(args.routing, 1, L, T, device)[0]
+    gen = torch.Generator(device=device).manual_seed(2)
+    x0 = torch.randn((T, H), generator=gen, device=device).to(torch.bfloat16)
+    rows = (2 * I, H)
+
+    def layer_step(x, layer):
+        kind, banks, cbs = layers[layer]
+        ids, w = kernels.route(logits[layer], TOPK)
+        return offload.resident_prefill(x, ids, w, banks, rows, kind, cbs, E)
+
+    unique = [len(torch.unique(kernels.route(logits[layer], TOPK)[0])) for layer in range(L)]
+    per_expert = sum(bank_bytes(f) for f in layers[0][1])
+    step_bytes = sum(unique) * per_expert + L * T * (2 * H * 2 + E * 2)
+    stream = torch.cuda.Stream(device)
+    stream.wait_stream(torch.cuda.current_stream(device))
+    with torch.cuda.stream(stream):
+        for layer in range(L):  # constants and allocator pools before capture
+            layer_step(x0, layer)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream):
+            for layer in range(L):
+                layer_step(x0, layer)
+        ms = timed_replays([g], stream, args.steps, args.warmup)
+    torch.cuda.synchronize()
+    flops = 2 * TOPK * T * (2 * I * H + H * I)
+    config = {"workload": f"routed-expert MoE layer in the reference's {args.format} layout (float activations, "
+                          f"route + resident_prefill), {T} rows at once (prefill), hidden {H}, FFN {I}, {E} experts "
+                          f"top-{TOPK} ({args.routing} routing), {L} layers", "rows": T, "layers": L,
+              "unique_experts_per_launch": round(sum(unique) / len(unique), 2),
+              "us_per_layer": round(ms * 1e3 / (args.steps * L), 2),
+              "mfma_bf16_tflops": round(3 * flops * L * args.steps / (ms * 1e-3) / 1e12, 2)}
+    return (ms, step_bytes * args.steps, args.steps * L, args.steps * T, config,
+            "route + resident_prefill (d3::grouped_mfma_kernel per bank, 9 launches)", None)
+
+
 def run_resident(args, fmt, device):
     """The reference-format decode path (kernels.route + offload.resident_decode: rotate, gemv, rotate(SwiGLU),
-    gemv, weighted sum; FP8 without the rotations), one row, layers chained in HIP graphs."""
+    gemv, weighted sum; FP8 without the rotations), one row, layers chained in HIP graphs; with more rows, the prompt
+    path (run_resident_prompt)."""
     from drama3 import kernels, offload
+    if args.rows > 1:
+        return run_resident_prompt(args, fmt, device)
     L = args.layers
     offload.RESIDENT_LAUNCHES = args.launches
     log(f"building {L} layers of {args.format} experts in the reference's layouts")
@@ -643,9 +690,10 @@ def main():
     default_run = args.mode == "decode" and args.format is None and args.rows is None and args.routing is None
     args.format = args.format or ("fp8" if prefill or args.mode == "gemv" else "int8")
     args.rows = args.rows or (256 if prefill else 1)
-    args.layers = args.layers or (16 if prefill else 128 if args.mode == "gemv" else 48)
-    args.routing = args.routing or ("zipf" if prefill else "normal")
-    args.steps = args.steps or (20 if prefill else 100)
+    prompt = prefill or (args.mode == "resident" and args.rows > 1)
+    args.layers = args.layers or (16 if prefill else 8 if prompt else 128 if args.mode == "gemv" else 48)
+    args.routing = args.routing or ("zipf" if prompt else "normal")
+    args.steps = args.steps or (20 if prefill else 10 if prompt else 100)
     args.warmup = args.warmup if args.warmup is not None else (3 if prefill else 8)
     fmt = FORMATS[args.format]
     global E, I
@@ -686,6 +734,10 @@ def main():
                                                                      ("resident", "fp8", 1, "normal", 48, 100, 8),
                                                                      ("resident", "w4a8", 1, "normal", 48, 100, 8),
                                                                      ("resident", "w6a8", 1, "normal", 48, 100, 8),
+                                                                     ("resident", "int8", 256, "zipf", 8, 10, 2),
+                                                                     ("resident", "fp8", 256, "zipf", 8, 10, 2),
+                                                                     ("resident", "w4a8", 256, "zipf", 8, 10, 2),
+                                                                     ("resident", "w6a8", 256, "zipf", 8, 10, 2),
                                                                      ("block", "int8", 1, "normal", 48, 100, 8)):
             log(f"timing {mode} {fmt_name}, {rows} rows")
             config["other_workloads"].append(workload_summary(args, device, mode, fmt_name, rows, routing, layers,
