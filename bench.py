@@ -595,13 +595,14 @@ def run_resident_prompt(args, fmt, device):
                 layer_step(x0, layer)
         ms = timed_replays([g], stream, args.steps, args.warmup)
     torch.cuda.synchronize()
-    flops = 2 * TOPK * T * (2 * I * H + H * I)
+    # the bf16 products as issued: three planes of float32 rows, one for fp8's gate_up (its rows are bf16 already)
+    flops = 2 * TOPK * T * ((1 if args.format == "fp8" else 3) * 2 * I * H + 3 * H * I)
     config = {"workload": f"routed-expert MoE layer in the reference's {args.format} layout (float activations, "
                           f"route + resident_prefill), {T} rows at once (prefill), hidden {H}, FFN {I}, {E} experts "
                           f"top-{TOPK} ({args.routing} routing), {L} layers", "rows": T, "layers": L,
               "unique_experts_per_launch": round(sum(unique) / len(unique), 2),
               "us_per_layer": round(ms * 1e3 / (args.steps * L), 2),
-              "mfma_bf16_tflops": round(3 * flops * L * args.steps / (ms * 1e-3) / 1e12, 2)}
+              "mfma_bf16_tflops": round(flops * L * args.steps / (ms * 1e-3) / 1e12, 2)}
     return (ms, step_bytes * args.steps, args.steps * L, args.steps * T, config,
             "route + resident_prefill (d3::grouped_mfma_kernel per bank, 9 launches)", None)
 
