@@ -259,17 +259,18 @@ def run_decode(args, fmt, device):
 
 
 def run_block(args, fmt, device):
-    """SparseMoeBlock.forward for one decode row in one launch (moe.moe_block): the router's logits from its bf16
-    weights [E, H], the routed experts, and a shared expert of the layer's format and shape with its gate, per layer.
-    Algorithmic bytes: the routed experts read, the shared expert, the router and gate rows, x and out."""
-    L = args.layers
+    """SparseMoeBlock.forward for M decode rows (moe.moe_block; one row in one launch, more in four): the router's
+    logits from its bf16 weights [E, H], the routed experts, and a shared expert of the layer's format and shape with
+    its gate, per layer. Algorithmic bytes: the routed experts read (once for all rows), the shared expert, the router
+    and gate rows, x and out."""
+    L, M = args.layers, args.rows
     log(f"building {L} layers of {args.format} experts, routers and shared experts")
     banks = make_layers(fmt, L, device)
     shared = make_layers(fmt, L, device, seed=5, experts=1)
     gen = torch.Generator(device=device).manual_seed(4)
     routers = [(torch.randn((E, H), generator=gen, device=device) * 0.02).to(torch.bfloat16) for _ in range(L)]
     gates = [(torch.randn((H,), generator=gen, device=device) * 0.05).to(torch.bfloat16) for _ in range(L)]
-    x0 = torch.randn((GRAPH_TOKENS, 1, H), generator=gen, device=device).to(torch.bfloat16)
+    x0 = torch.randn((GRAPH_TOKENS, M, H), generator=gen, device=device).to(torch.bfloat16)
     unique = []
     for t in range(GRAPH_TOKENS):
         x = x0[t]
@@ -279,7 +280,7 @@ def run_block(args, fmt, device):
             unique.append(len(torch.unique(ids)))
     torch.cuda.synchronize()
     per_expert = expert_bytes(*banks[0])
-    fixed = expert_bytes(*shared[0]) + E * H * 2 + H * 2 + 2 * H * 2
+    fixed = expert_bytes(*shared[0]) + E * H * 2 + H * 2 + M * 2 * H * 2
     bytes_per_token = [sum(unique[t * L:(t + 1) * L]) * per_expert + L * fixed for t in range(GRAPH_TOKENS)]
     stream = torch.cuda.Stream(device)
     stream.wait_stream(torch.cuda.current_stream(device))
@@ -302,10 +303,12 @@ def run_block(args, fmt, device):
         raise RuntimeError(f"fused layer reported status {status}")
     total_bytes = sum(bytes_per_token[i % GRAPH_TOKENS] for i in range(args.steps))
     config = {"workload": f"MoE block (router {E}x{H} bf16, routed {args.format} experts top-{TOPK}, shared expert "
-                          f"of FFN {I} with its gate), decode M=1, hidden {H}, FFN {I}, {L} layers chained per token",
-              "rows": 1, "layers": L, "unique_experts_per_launch": round(sum(unique) / len(unique), 2),
+                          f"of FFN {I} with its gate), decode M={M}, hidden {H}, FFN {I}, {L} layers chained per token",
+              "rows": M, "layers": L, "unique_experts_per_launch": round(sum(unique) / len(unique), 2),
               "waits_recomputed": bool(status & moe.STATUS_RECOMPUTED)}
-    return ms, total_bytes, args.steps * L, args.steps, config, "d3::moe_a8_one_row_kernel (block)", None
+    kernel = ("d3::moe_a8_one_row_kernel (block)" if M == 1 else
+              "router_logits_kernel, d3_moe_a8 (routed, one expert for the shared), block_combine_kernel")
+    return ms, total_bytes, args.steps * L, args.steps * M, config, kernel, None
 
 
 def run_prefill(args, fmt, device):
@@ -739,7 +742,8 @@ def main():
                                                                      ("resident", "fp8", 256, "zipf", 8, 10, 2),
                                                                      ("resident", "w4a8", 256, "zipf", 8, 10, 2),
                                                                      ("resident", "w6a8", 256, "zipf", 8, 10, 2),
-                                                                     ("block", "int8", 1, "normal", 48, 100, 8)):
+                                                                     ("block", "int8", 1, "normal", 48, 100, 8),
+                                                                     ("block", "int8", 4, "normal", 48, 100, 8)):
             log(f"timing {mode} {fmt_name}, {rows} rows")
             config["other_workloads"].append(workload_summary(args, device, mode, fmt_name, rows, routing, layers,
                                                               steps, warmup))

@@ -779,13 +779,13 @@ D3_INLINE void down_item(const Ctx& cx, int c, int hb) {
 
 // The router's logit e for one row, as bf16 bits: bf16(x . router[e]) with float sums (model.py:115), x as every wave
 // holds it (lane l: columns 512 k + 8 l .. + 7 of chunk k); the same in every lane.
+// bf16(x . v) with float sums in the block's order: lane l takes columns 512 k + 8 l .. + 7, then a wave sum
 template <int H>
-D3_INLINE uint32_t router_dot(const MoeA8Args& a, int e, const i32x4* xraw, int lane) {
-  const uint16_t* wr = a.router + (size_t)e * H;
+D3_INLINE float row_dot(const uint16_t* v, const i32x4* xraw, int lane) {
   float acc = 0.0f;
 #pragma unroll
   for (int k = 0; k < H / 512; k++) {
-    const i32x4 wv = *(const i32x4*)(wr + 512 * k + 8 * lane);
+    const i32x4 wv = *(const i32x4*)(v + 512 * k + 8 * lane);
     const uint32_t xs[4] = {(uint32_t)xraw[k].x, (uint32_t)xraw[k].y, (uint32_t)xraw[k].z, (uint32_t)xraw[k].w};
     const uint32_t ws[4] = {(uint32_t)wv.x, (uint32_t)wv.y, (uint32_t)wv.z, (uint32_t)wv.w};
 #pragma unroll
@@ -794,7 +794,19 @@ D3_INLINE uint32_t router_dot(const MoeA8Args& a, int e, const i32x4* xraw, int 
       acc = fmaf(bf16_to_f32(xs[j] >> 16), bf16_to_f32(ws[j] >> 16), acc);
     }
   }
-  return f32_to_bf16(wave_sum_f32(acc));
+  return wave_sum_f32(acc);
+}
+
+template <int H>
+D3_INLINE uint32_t router_dot(const MoeA8Args& a, int e, const i32x4* xraw, int lane) {
+  return f32_to_bf16(row_dot<H>(a.router + (size_t)e * H, xraw, lane));
+}
+
+// the shared expert's gate weight of a row: bf16(sigmoid(bf16(x . gate))), as model.py:123's bf16 ops round it
+template <int H>
+D3_INLINE float shared_gate_weight(const uint16_t* gate, const i32x4* xraw, int lane) {
+  const float g = bf16_round(row_dot<H>(gate, xraw, lane));
+  return bf16_round(1.0f / (1.0f + expf(-g)));
 }
 
 // router_dot published as a tagged word (its bf16 bits) for every routing wave
@@ -968,20 +980,7 @@ D3_INLINE bool shared_down_block(const Ctx& cx, int b, const i32x4* xraw) {
   }
   auto half = [&](int k) { return bf16_to_f32((k & 1) ? sw[k >> 1] >> 16 : sw[k >> 1] & 0xFFFFu); };
   // the gate: x . shared_gate (model.py:123), then its sigmoid, each rounded to bf16 as the block's ops round them
-  float gsum = 0.0f;
-#pragma unroll
-  for (int k = 0; k < H / 512; k++) {
-    const i32x4 gv = *(const i32x4*)(a.sh_gate + 512 * k + 8 * lane);
-    const uint32_t xs[4] = {(uint32_t)xraw[k].x, (uint32_t)xraw[k].y, (uint32_t)xraw[k].z, (uint32_t)xraw[k].w};
-    const uint32_t gs[4] = {(uint32_t)gv.x, (uint32_t)gv.y, (uint32_t)gv.z, (uint32_t)gv.w};
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-      gsum = fmaf(bf16_to_f32(xs[j] & 0xFFFFu), bf16_to_f32(gs[j] & 0xFFFFu), gsum);
-      gsum = fmaf(bf16_to_f32(xs[j] >> 16), bf16_to_f32(gs[j] >> 16), gsum);
-    }
-  }
-  const float gate = bf16_round(wave_sum_f32(gsum));
-  const float gw = bf16_round(1.0f / (1.0f + expf(-gate)));
+  const float gw = shared_gate_weight<H>(a.sh_gate, xraw, lane);
   // the shared hidden row, gathered once this wave's rows have landed
   settle();
   uint64_t mw[TPW], vw[HPW];
@@ -1426,6 +1425,45 @@ constexpr int64_t SCRATCH_BYTES = moe_a8_workspace_bytes(MAX_M, MAX_K, 2048, 768
 static __device__ __align__(256) uint8_t scratch[SCRATCH_BYTES];
 
 // zeroes n bytes (a multiple of 16) at p: the workspace's words must start with tag 0, which no epoch equals
+// The block for several rows around the routed layer (model.py:107-124): the router's logits of M rows (self.gate(flat),
+// model.py:115), a wave per (row, expert), with router_dot's arithmetic, so each row's logits equal the one-row block's
+template <int H>
+__global__ void __launch_bounds__(256) router_logits_kernel(const uint16_t* x, const uint16_t* router, int M, int E,
+                                                            uint16_t* logits) {
+  const int lane = threadIdx.x & 63, g = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (g >= M * E) return;
+  const int t = g / E, e = g - t * E;
+  i32x4 xraw[H / 512];
+#pragma unroll
+  for (int k = 0; k < H / 512; k++) xraw[k] = *(const i32x4*)(x + (size_t)t * H + 512 * k + 8 * lane);
+  const uint32_t bits = f32_to_bf16(row_dot<H>(router + (size_t)e * H, xraw, lane));
+  if (lane == 0) logits[g] = (uint16_t)bits;
+}
+
+// out[t] = routed[t] + bf16(gw_t * shared[t]) rounded to bf16 (model.py:123: the shared expert's output scaled by
+// bf16(sigmoid(bf16(x . gate))), added to the routed output, each a bf16 tensor), as the one-row block's down blocks
+// combine them. A workgroup per row: wave 0 computes the row's gate weight.
+template <int H>
+__global__ void __launch_bounds__(256) block_combine_kernel(const uint16_t* x, const uint16_t* gate,
+                                                            const uint16_t* routed, const uint16_t* shared,
+                                                            uint16_t* out) {
+  __shared__ float gw;
+  const int t = blockIdx.x, lane = threadIdx.x & 63;
+  if (threadIdx.x < 64) {
+    i32x4 xraw[H / 512];
+#pragma unroll
+    for (int k = 0; k < H / 512; k++) xraw[k] = *(const i32x4*)(x + (size_t)t * H + 512 * k + 8 * lane);
+    const float w = shared_gate_weight<H>(gate, xraw, lane);
+    if (lane == 0) gw = w;
+  }
+  __syncthreads();
+  for (int h = threadIdx.x; h < H; h += 256) {
+    const size_t i = (size_t)t * H + h;
+    const float y = bf16_to_f32(routed[i]) + bf16_round(gw * bf16_to_f32(shared[i]));
+    out[i] = (uint16_t)f32_to_bf16(y);
+  }
+}
+
 __global__ void __launch_bounds__(256) fill_zero_kernel(uint4* p, int64_t n16) {
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n16; i += (int64_t)gridDim.x * 256)
     p[i] = uint4{0u, 0u, 0u, 0u};
@@ -1624,6 +1662,29 @@ extern "C" {
 
 const char* d3_last_error(void) { return d3::g_error.c_str(); }
 int d3_version(void) { return 1; }
+
+int d3_router_logits(const void* x, const void* router, int32_t M, int32_t H, int32_t E, void* logits, void* stream) {
+  if (!x || !router || !logits) return d3::fail("d3_router_logits: null pointer");
+  if (H != 2048) return d3::fail("d3_router_logits: H = 2048");
+  if (M < 0 || E < 1 || E > d3::MAX_E) return d3::fail("d3_router_logits: M >= 0, 1 <= E <= 256");
+  if (M == 0) return 0;
+  hipLaunchKernelGGL(d3::router_logits_kernel<2048>, dim3((M * E + 3) / 4), dim3(256), 0, (hipStream_t)stream,
+                     (const uint16_t*)x, (const uint16_t*)router, M, E, (uint16_t*)logits);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? 0 : d3::hip_fail(e, "d3_router_logits launch");
+}
+
+int d3_block_combine(const void* x, const void* gate, const void* routed, const void* shared, int32_t M, int32_t H,
+                     void* out, void* stream) {
+  if (!x || !gate || !routed || !shared || !out) return d3::fail("d3_block_combine: null pointer");
+  if (H != 2048) return d3::fail("d3_block_combine: H = 2048");
+  if (M < 0) return d3::fail("d3_block_combine: M >= 0");
+  if (M == 0) return 0;
+  hipLaunchKernelGGL(d3::block_combine_kernel<2048>, dim3(M), dim3(256), 0, (hipStream_t)stream, (const uint16_t*)x,
+                     (const uint16_t*)gate, (const uint16_t*)routed, (const uint16_t*)shared, (uint16_t*)out);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? 0 : d3::hip_fail(e, "d3_block_combine launch");
+}
 
 int64_t d3_moe_a8_workspace_bytes(int32_t M, int32_t topk, int32_t H, int32_t I) {
   return d3::moe_a8_workspace_bytes(M, topk, H, I);

@@ -59,6 +59,8 @@ SIGNATURES = {
     "d3_unpack_rows": (c_int32, [c_int32, c_void_p, c_int32, c_int32, c_void_p, c_void_p]),
     "d3_cvt_fp8": (c_int32, [c_void_p, c_int32, c_void_p, c_int32, c_void_p]),
     "d3_stream_read": (c_int32, [c_void_p, c_int64, c_void_p, c_int32, c_void_p]),
+    "d3_router_logits": (c_int32, [c_void_p, c_void_p, c_int32, c_int32, c_int32, c_void_p, c_void_p]),
+    "d3_block_combine": (c_int32, [c_void_p, c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_void_p, c_void_p]),
     "d3_empty_launch": (c_int32, [c_int32, c_void_p]),
     "d3_gemv_fp8_rows": (c_int32, [c_void_p, c_int32, c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_void_p]),
     "d3_route": (c_int32, [c_void_p, c_int32, c_int32, c_int32, c_void_p, c_void_p, c_void_p]),

@@ -124,37 +124,62 @@ def moe_layer(x, logits, gate_up: A8Bank, down: A8Bank, topk, *, routing=False, 
     return (out, ids, weights) if routing else out
 
 
+def _check_shared(shared, shared_gate, gate_up, H, I):
+    if shared is None:
+        return None, None, None
+    sg, sd = shared
+    if (sg.fmt, sd.fmt) != (gate_up.fmt, gate_up.fmt) or sg.experts != 1 or sd.experts != 1 or \
+            (sg.rows, sg.cols, sd.rows, sd.cols) != (2 * I, H, H, I):
+        raise ValueError("the shared expert: one expert of the layer's format and shape")
+    if shared_gate is None or shared_gate.dtype != torch.bfloat16 or shared_gate.numel() != H:
+        raise ValueError("shared_gate [H] bfloat16 expected")
+    return sg, sd, shared_gate.contiguous()
+
+
+_ZERO_LOGITS = {}
+
+
+def _one_expert_logits(device, M):
+    """[M, 1] bf16 zeros: every row's only expert, at weight 1. Kept per (device, M) once made outside a graph
+    capture (a tensor first made inside one is filled only when the graph replays)."""
+    key = (device.type, device.index, M)
+    t = _ZERO_LOGITS.get(key)
+    if t is None:
+        t = torch.zeros((M, 1), dtype=torch.bfloat16, device=device)
+        if not torch.cuda.is_current_stream_capturing():
+            _ZERO_LOGITS[key] = t
+    return t
+
+
+def router_logits(x, router):
+    """The router's logits of every row, model.py:115's self.gate(flat): [M, E] bf16 from x [M, H] and router [E, H]
+    bf16, float sums in the one-row block's order, so each row's logits equal what that block computes."""
+    M, H = x.shape
+    out = torch.empty((M, router.shape[0]), dtype=torch.bfloat16, device=x.device)
+    _lib.check(_lib.lib().d3_router_logits(x.data_ptr(), router.data_ptr(), M, H, router.shape[0], out.data_ptr(),
+                                           _lib.stream_of(x.device)), "d3_router_logits")
+    return out
+
+
 def moe_block(x, gate_up: A8Bank, down: A8Bank, topk, *, router=None, logits=None, shared=None, shared_gate=None,
               routing=False, return_logits=False, out=None, item_units=0, spin_limit=0, recompute_all=False):
-    """SparseMoeBlock.forward (drama3/model.py:107-124) for decode rows: x [M, H] bf16 -> [M, H] bf16, each row in one
-    launch (the rows of the block are independent: a row's router logits, routing, experts and shared expert read
-    only that row).
+    """SparseMoeBlock.forward (drama3/model.py:107-124) for decode rows: x [M, H] bf16 -> [M, H] bf16.
 
-    The router: `router` [E, H] bf16 (its logits computed in the launch, model.py:115) or given `logits` [M, E] bf16.
+    The router: `router` [E, H] bf16 (its logits computed on the device, model.py:115) or given `logits` [M, E] bf16.
     The shared expert: `shared` = (gate_up, down) A8Banks of one expert in the layer's format and shape, and
     `shared_gate` [H] bf16; it is added as model.py:123 does (both terms bf16). With `routing` also returns ids and
     weights [M, topk], with `return_logits` the router's logits [M, E] bf16. `item_units`, `spin_limit` and
-    `recompute_all` as for moe_layer."""
+    `recompute_all` as for moe_layer.
+
+    One row runs in one launch (router, routed experts, shared expert, sum). More rows run in four, each over all the
+    rows at once: the router's logits (router_logits), the routed layer (moe_layer: one launch, each expert read
+    once), the shared expert as a layer of one expert at weight 1 (its banks read once), and the sum
+    (d3_block_combine). Each row's output, routing and logits equal the one-row block's on that row bit for bit
+    while the routed layer runs fused (fewer than grouped_from_rows(format) rows); from there on the grouped path's
+    own summation order applies."""
     if x.dtype != torch.bfloat16 or x.dim() != 2 or x.shape[0] < 1:
         raise ValueError("x [M, H] bfloat16 expected")
-    M = x.shape[0]
-    if M > 1:
-        E = gate_up.experts
-        if logits is not None and (logits.dtype != torch.bfloat16 or logits.shape != (M, E)):
-            raise ValueError("logits [M, E] bfloat16 expected")
-        if out is not None and (out.shape != x.shape or out.dtype != torch.bfloat16 or not out.is_contiguous()):
-            raise ValueError("out [M, H] bfloat16, contiguous, expected")
-        out = torch.empty_like(x) if out is None else out
-        rows = [moe_block(x[m:m + 1], gate_up, down, topk, router=router,
-                          logits=None if logits is None else logits[m:m + 1], shared=shared,
-                          shared_gate=shared_gate, routing=routing, return_logits=return_logits, out=out[m:m + 1],
-                          item_units=item_units, spin_limit=spin_limit, recompute_all=recompute_all)
-                for m in range(M)]
-        if not (routing or return_logits):
-            return out
-        res = (out,) + tuple(torch.cat(parts) for parts in zip(*(r[1:] for r in rows)))
-        return res
-    H = x.shape[1]
+    M, H = x.shape
     E = gate_up.experts
     if gate_up.fmt != down.fmt or down.experts != E or gate_up.cols != H or down.rows != H or gate_up.rows != 2 * down.cols:
         raise ValueError("gate_up [E * 2I, H] and down [E * H, I] of one format expected")
@@ -167,19 +192,33 @@ def moe_block(x, gate_up: A8Bank, down: A8Bank, topk, *, router=None, logits=Non
             raise ValueError("router [E, H] bfloat16 expected")
         router = router.contiguous()
     else:
-        if logits.dtype != torch.bfloat16 or logits.shape != (1, E):
-            raise ValueError("logits [1, E] bfloat16 expected")
+        if logits.dtype != torch.bfloat16 or logits.shape != (M, E):
+            raise ValueError(f"logits [{M}, {E}] bfloat16 expected")
         logits = logits.contiguous()
-    sg = sd = None
-    if shared is not None:
-        sg, sd = shared
-        if (sg.fmt, sd.fmt) != (gate_up.fmt, gate_up.fmt) or sg.experts != 1 or sd.experts != 1 or \
-                (sg.rows, sg.cols, sd.rows, sd.cols) != (2 * I, H, H, I):
-            raise ValueError("the shared expert: one expert of the layer's format and shape")
-        if shared_gate is None or shared_gate.dtype != torch.bfloat16 or shared_gate.numel() != H:
-            raise ValueError("shared_gate [H] bfloat16 expected")
-        shared_gate = shared_gate.contiguous()
+    sg, sd, shared_gate = _check_shared(shared, shared_gate, gate_up, H, I)
+    if out is not None and (out.shape != x.shape or out.dtype != torch.bfloat16 or not out.is_contiguous()):
+        raise ValueError("out [M, H] bfloat16, contiguous, expected")
     x = x.contiguous()
+    if M > 1:
+        lg = router_logits(x, router) if router is not None else logits
+        res = moe_layer(x, lg, gate_up, down, topk, routing=routing, spin_limit=spin_limit,
+                        out=None if sg is not None else out, recompute_all=recompute_all)
+        routed, ids, weights = res if routing else (res, None, None)
+        if sg is None:
+            out = routed
+        else:
+            ys = moe_layer(x, _one_expert_logits(device, M), sg, sd, 1, spin_limit=spin_limit,
+                           recompute_all=recompute_all)
+            out = torch.empty_like(x) if out is None else out
+            _lib.check(_lib.lib().d3_block_combine(x.data_ptr(), shared_gate.data_ptr(), routed.data_ptr(),
+                                                   ys.data_ptr(), M, H, out.data_ptr(), _lib.stream_of(device)),
+                       "d3_block_combine")
+        res = (out,)
+        if routing:
+            res += (ids, weights)
+        if return_logits:
+            res += (lg if router is not None else logits,)
+        return res if len(res) > 1 else out
     if out is None:
         out = torch.empty((1, H), dtype=torch.bfloat16, device=device)
     ids = torch.empty((1, topk), dtype=torch.int64, device=device) if routing else None

@@ -102,6 +102,19 @@ int d3_moe_a8_noalloc_status(uint32_t* status);
  * replayed on another stream included. Launches that overlap on one workspace race. */
 int d3_moe_a8_status(void* workspace, uint32_t* status);
 
+/* ---- The block for several rows (SparseMoeBlock.forward over a batch, drama3/model.py:107-124) -------------------
+ * With d3_moe_a8 on all rows and a one-expert d3_moe_a8 for the shared expert, four launches run the block for M
+ * rows, each over all of them:
+ * d3_router_logits (model.py:115, self.gate(flat)): logits [M, E] bf16 = bf16(x . router[e]) with float sums in
+ * the one-row block's order, so each row's logits equal what that block computes; x [M, H], router [E, H] bf16.
+ * d3_block_combine (model.py:123): out[t] = bf16(routed[t] + bf16(gw_t * shared[t])), gw_t =
+ * bf16(sigmoid(bf16(x[t] . gate))), as the one-row block's down blocks add the shared expert; routed, shared [M, H]
+ * bf16 (the routed layer's output and the shared expert's, run as a layer of one expert at weight 1), gate [H] bf16.
+ * H = 2048. */
+int d3_router_logits(const void* x, const void* router, int32_t M, int32_t H, int32_t E, void* logits, void* stream);
+int d3_block_combine(const void* x, const void* gate, const void* routed, const void* shared, int32_t M, int32_t H,
+                     void* out, void* stream);
+
 /* ---- MoE layer for many rows on A8 banks (prefill, many decode lines) --------------------------------------------
  * Replaces offload.resident_prefill (drama3/offload.py:139-149 -> grouped_int8 / grouped_fp8 / grouped_codes,
  * kernels.py:365-464,538-587) and FP8Experts.forward's prompt branch (offload.py:775-802) for A8 banks: the rows'

@@ -430,24 +430,34 @@ def test_block_router_and_shared_expert(fmt):
         assert torch.equal(moe.moe_block(x, gate_up, down, 8, router=router, item_units=units), layer)
 
 
-@pytest.mark.parametrize("fmt", [formats.FMT_I8, formats.FMT_W4])
-def test_block_batched_rows(fmt):
-    """The block for several decode rows (model.py:107-124 over a batch): each row equals the one-row block on that
-    row, bit for bit, with the router's logits computed in the launches or given, and the routing and logits of
-    every row returned in row order."""
+@pytest.mark.parametrize("M", [2, 3, 5, 8, 16])
+@pytest.mark.parametrize("fmt", FMTS)
+def test_block_batched_rows(fmt, M):
+    """The block for several decode rows (model.py:107-124 over a batch; four launches, each over every row): each row
+    equals the one-row block on that row, bit for bit, while the routed layer runs fused (M below
+    grouped_from_rows(format)), with the router's logits computed or given, and the routing and logits of every row
+    returned in row order. Past that the grouped path sums in its own order: each row within the layer's bar of the
+    one-row block, the routing still exact."""
     gate_up, down, _, router, (sg, sd), g = block_inputs(fmt, 37)
-    gen = torch.Generator(device=DEV).manual_seed(38)
-    x = torch.randn((3, 2048), generator=gen, device=DEV).to(torch.bfloat16)
+    gen = torch.Generator(device=DEV).manual_seed(38 + M)
+    x = torch.randn((M, 2048), generator=gen, device=DEV).to(torch.bfloat16)
     out, ids, w, lg = moe.moe_block(x, gate_up, down, 8, router=router, shared=(sg, sd), shared_gate=g, routing=True,
                                     return_logits=True)
-    assert out.shape == (3, 2048) and ids.shape == (3, 8) and w.shape == (3, 8) and lg.shape == (3, 128)
-    for m in range(3):
+    assert out.shape == (M, 2048) and ids.shape == (M, 8) and w.shape == (M, 8) and lg.shape == (M, 128)
+    fused = M < moe.grouped_from_rows(fmt)
+    for m in range(M):
         o1, i1, w1, l1 = moe.moe_block(x[m:m + 1].clone(), gate_up, down, 8, router=router, shared=(sg, sd),
                                        shared_gate=g, routing=True, return_logits=True)
-        assert torch.equal(out[m:m + 1], o1) and torch.equal(ids[m:m + 1], i1) and torch.equal(w[m:m + 1], w1)
-        assert torch.equal(lg[m:m + 1], l1)
+        assert torch.equal(lg[m:m + 1], l1) and torch.equal(ids[m:m + 1], i1)
+        if fused:
+            assert torch.equal(out[m:m + 1], o1) and torch.equal(w[m:m + 1], w1), m
+        else:
+            a, b = out[m].float().cpu().numpy(), o1[0].float().cpu().numpy()
+            assert np.abs(a - b).max() <= 8e-3 * np.abs(b).max() and np.linalg.norm(a - b) <= 3e-3 * np.linalg.norm(b)
     given = moe.moe_block(x, gate_up, down, 8, logits=lg, shared=(sg, sd), shared_gate=g)
     assert torch.equal(given, out)
+    # without the shared expert the block is the routed layer on the router's logits
+    assert torch.equal(moe.moe_block(x, gate_up, down, 8, router=router), moe.moe_layer(x, lg, gate_up, down, 8))
     torch.cuda.synchronize()
     assert moe.status(DEV, 2048, 768) == 0
 
