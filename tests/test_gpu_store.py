@@ -162,6 +162,38 @@ def test_slot_prefill_equals_resident_prefill(kind):
         assert (owner >= 0).sum() > 0   # the passes filled slots
 
 
+@pytest.mark.parametrize("kind", ["int8", "fp8", "w4", "w6"])
+def test_slot_prefill_hot_experts_fill_once(kind):
+    """Experts with many rows (100 and 70 rows: four and three 32-row passes of the grouped products) that are not
+    cached: the first pass of each reads it from host memory and copies it into its slot, the later passes read the
+    slot once the first passes are done (fills_first). The output equals the resident prefill's bits, the filled slots
+    hold the experts' bytes, and the next pass finds them cached."""
+    layers = make_layers(kind, 2, 9)
+    store = make_store(kind, layers, 12)
+    resident, rcbs = on_device(layers)
+    rng = np.random.default_rng(10)
+    T, k, hot = 100, 4, (5, 11)
+    with store.session(DEV, [], False, 0, cpu_experts=False):
+        for rep in range(2):
+            x, idx, w = prompt(rng, T, k)
+            others = [e for e in range(E) if e not in hot]
+            for t in range(T):   # expert 5 in every row, expert 11 in 70 of them
+                fixed = [hot[0]] + ([hot[1]] if t < 70 else [])
+                idx[t] = fixed + list(rng.choice(others, k - len(fixed), replace=False))
+            xd, idxd, wd = dev_bf16_bits(x), torch.from_numpy(idx).to(DEV), bf16(w)
+            got = store.forward(0, xd, idxd, wd)
+            want = offload.resident_prefill(xd, idxd, wd, resident[0], (2 * I, H), kind, rcbs[0], E)
+            assert torch.equal(got.view(torch.int16), want.view(torch.int16)), rep
+            table = store.cache.table.cpu().numpy()
+            for e in hot:
+                s = int(table[e])
+                assert s >= 0, (rep, e)   # layer 0's key of expert e: its slot
+                for i, bank in enumerate(store.banks[0]):
+                    want_fields = bank.take(bank.fields, e, e + 1)
+                    for name, t in store.cache.slot_fields(i, s).items():
+                        assert torch.equal(t.cpu(), want_fields[name]), (rep, e, name)
+
+
 @pytest.mark.parametrize("kind", ["int8", "w4"])
 def test_slot_prefill_captured_in_a_graph(kind):
     """Without the CPU side a prompt's pass through the slot cache waits on nothing on the host (the pass's plan, fills
