@@ -598,16 +598,18 @@ def run_resident_prompt(args, fmt, device):
                 layer_step(x0, layer)
         ms = timed_replays([g], stream, args.steps, args.warmup)
     torch.cuda.synchronize()
-    # the bf16 products as issued: three planes of float32 rows, one for fp8's gate_up (its rows are bf16 already)
+    # the matrix-core products as issued: three planes of both banks' rows (int8 planes on the int8 cores for int8 and
+    # the codes; bf16 planes for fp8, one for its gate_up, whose rows are bf16 already)
     flops = 2 * TOPK * T * ((1 if args.format == "fp8" else 3) * 2 * I * H + 3 * H * I)
     config = {"workload": f"routed-expert MoE layer in the reference's {args.format} layout (float activations, "
                           f"route + resident_prefill), {T} rows at once (prefill), hidden {H}, FFN {I}, {E} experts "
                           f"top-{TOPK} ({args.routing} routing), {L} layers", "rows": T, "layers": L,
               "unique_experts_per_launch": round(sum(unique) / len(unique), 2),
               "us_per_layer": round(ms * 1e3 / (args.steps * L), 2),
-              "mfma_bf16_tflops": round(flops * L * args.steps / (ms * 1e-3) / 1e12, 2)}
+              "mfma_ops_per_s_e12": round(flops * L * args.steps / (ms * 1e-3) / 1e12, 2),
+              "mfma_type": "bf16" if args.format == "fp8" else "int8"}
     return (ms, step_bytes * args.steps, args.steps * L, args.steps * T, config,
-            "route + resident_prefill (d3::grouped_mfma_kernel per bank, 9 launches)", None)
+            "route + resident_prefill (d3::grouped_i8_kernel / grouped_mfma_kernel per bank, 9 launches)", None)
 
 
 def run_resident(args, fmt, device):

@@ -287,8 +287,9 @@ D3_INLINE void decode_group(uint32_t lo, uint32_t hi, uint32_t high, uint32_t sc
 // q + 128. A group then costs one 16-byte table read, and four of its codes become four bytes through two byte
 // permutes and a byte mask, instead of a codebook read, a product, a rounding and a clamp per value.
 constexpr int QTAB_WORDS = 256 * 4;  // qtab[4 sb + i]: bytes q + 128 of codes 4i .. 4i + 3 at scale byte sb
-// cb: codebook[4 (threadIdx.x & 3) .. + 3], loaded by the caller (ahead of its weight rows)
-D3_INLINE void build_qtab(uint32_t* qtab, f32x4 cb) {
+// cb: codebook[4 (threadIdx.x & 3) .. + 3], loaded by the caller (ahead of its weight rows); SIGNED: the bytes hold q
+// itself (two's complement) instead of q + 128
+template <bool SIGNED = false> D3_INLINE void build_qtab(uint32_t* qtab, f32x4 cb) {
   const float c[4] = {cb.x, cb.y, cb.z, cb.w};
   for (int i = threadIdx.x; i < QTAB_WORDS; i += blockDim.x) {  // i & 3 == threadIdx.x & 3: blockDim.x % 4 == 0
     const float sc = fp8x2_to_f32<false>((uint32_t)(i >> 2)).x;
@@ -296,7 +297,7 @@ D3_INLINE void build_qtab(uint32_t* qtab, f32x4 cb) {
 #pragma unroll
     for (int b = 0; b < 4; b++) {
       const float q = fminf(fmaxf(rintf(c[b] * sc), -127.0f), 127.0f);
-      word |= (uint32_t)((int)q + 128) << (8 * b);
+      word |= ((uint32_t)((int)q + (SIGNED ? 0 : 128)) & 0xFFu) << (8 * b);
     }
     qtab[i] = word;
   }
@@ -660,6 +661,24 @@ __global__ void __launch_bounds__(1024) expert_groups_kernel(const int64_t* ids,
 // Planes hi, mid, lo [P, K] of the rows the grouped products read (split3_kernel's split): row p is x's row
 // order[p] / k (x's row p without order); SRC 0 float32 rows [., K], 1 bf16 rows, 2 float32 gate | up rows [., 2K]
 // through SiLU(gate) * up (kernels.py:222-258's SwiGLU); ROT: in the ConvRot basis (H256 on every 256 columns, / 16).
+// columns c0 .. c0 + 3 of row `row` of x as float (SRC as for prep_planes_kernel)
+template <int SRC> D3_INLINE void load_row4(const void* x, size_t row, int K, int c0, float* v) {
+  if constexpr (SRC == 0) {
+    const f32x4 a = *(const f32x4*)((const float*)x + row * K + c0);
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+  } else if constexpr (SRC == 1) {
+    const i32x2 a = *(const i32x2*)((const uint16_t*)x + row * K + c0);
+    v[0] = bf16_to_f32((uint32_t)a.x & 0xFFFFu); v[1] = bf16_to_f32((uint32_t)a.x >> 16);
+    v[2] = bf16_to_f32((uint32_t)a.y & 0xFFFFu); v[3] = bf16_to_f32((uint32_t)a.y >> 16);
+  } else {
+    const float* f = (const float*)x + row * 2 * K;
+    const f32x4 gt = *(const f32x4*)(f + c0), up = *(const f32x4*)(f + K + c0);
+    const float gg[4] = {gt.x, gt.y, gt.z, gt.w}, uu[4] = {up.x, up.y, up.z, up.w};
+#pragma unroll
+    for (int j = 0; j < 4; j++) v[j] = gg[j] / (1.0f + __expf(-gg[j])) * uu[j];
+  }
+}
+
 template <int SRC, bool ROT, int PL>
 __global__ void __launch_bounds__(256) prep_planes_kernel(const void* x, const int64_t* order, int k, int K,
                                                           __bf16* planes, int64_t plane) {
@@ -668,20 +687,7 @@ __global__ void __launch_bounds__(256) prep_planes_kernel(const void* x, const i
   for (int g = w; g < K / 256; g += 4) {
     const int c0 = 256 * g + 4 * lane;
     float v[4];
-    if constexpr (SRC == 0) {
-      const f32x4 a = *(const f32x4*)((const float*)x + row * K + c0);
-      v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
-    } else if constexpr (SRC == 1) {
-      const i32x2 a = *(const i32x2*)((const uint16_t*)x + row * K + c0);
-      v[0] = bf16_to_f32((uint32_t)a.x & 0xFFFFu); v[1] = bf16_to_f32((uint32_t)a.x >> 16);
-      v[2] = bf16_to_f32((uint32_t)a.y & 0xFFFFu); v[3] = bf16_to_f32((uint32_t)a.y >> 16);
-    } else {
-      const float* f = (const float*)x + row * 2 * K;
-      const f32x4 gt = *(const f32x4*)(f + c0), up = *(const f32x4*)(f + K + c0);
-      const float gg[4] = {gt.x, gt.y, gt.z, gt.w}, uu[4] = {up.x, up.y, up.z, up.w};
-#pragma unroll
-      for (int j = 0; j < 4; j++) v[j] = gg[j] / (1.0f + __expf(-gg[j])) * uu[j];
-    }
+    load_row4<SRC>(x, row, K, c0, v);
     if constexpr (ROT) fwht256(v);
     typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
     bf16x4 h, m, l;
@@ -697,6 +703,70 @@ __global__ void __launch_bounds__(256) prep_planes_kernel(const void* x, const i
     if constexpr (PL == 3) {
       *(bf16x4*)(planes + plane + at) = m;
       *(bf16x4*)(planes + 2 * plane + at) = l;
+    }
+  }
+}
+
+// The same rows (SRC, ROT as for prep_planes_kernel) as three int8 planes a0, a1, a2 [P, K] and a row scale S
+// (scales[p]) for the products on the int8 matrix cores: S is the smallest power of two with max |v| <= 127 S, and
+//   v / S = a0 + a1 / 254 + a2 / 254^2 + r,  every a in [-127, 127], |r| <= 0.5 / 254^2 + 2^-24
+// (v / S and d = v / S - a0 are exact; a1 = rint(254 d rounded), a2 = rint(254 (254 d - a1) rounded), the inner
+// difference from the exact product, rounded once). So the planes hold v to within (0.5 / 254^2 + 2^-24) S <
+// 1.25e-7 max |v|, and a row of integers times a power of two (such as a one-hot row) exactly in a0. An all-zero row
+// gets S = 0, a row holding a non-finite value S = NaN (planes 0 both ways); below 2^-143, S stays 2^-149.
+constexpr float I8_RATIO = 254.0f;  // the int8 planes' ratio
+
+template <int SRC, bool ROT>
+__global__ void __launch_bounds__(256) prep_i8_kernel(const void* x, const int64_t* order, int k, int K,
+                                                      int8_t* planes, int64_t plane, float* scales) {
+  __shared__ uint32_t wmax[4];
+  const int p = blockIdx.x, lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const size_t row = order ? (size_t)(order[p] / k) : (size_t)p;
+  float v[2][4];  // wave w's columns 256 g + 4 lane .. + 3 of g = w, w + 4 (K <= 2048)
+  uint32_t m = 0u;  // the bits of max |v|: non-negative floats order as their bits, inf and NaN above every finite
+#pragma unroll
+  for (int i = 0; i < 2; i++) {
+    const int g = w + 4 * i;
+    if (g < K / 256) {
+      load_row4<SRC>(x, row, K, 256 * g + 4 * lane, v[i]);
+      if constexpr (ROT) fwht256(v[i]);
+#pragma unroll
+      for (int j = 0; j < 4; j++) m = max(m, __float_as_uint(v[i][j]) & 0x7FFFFFFFu);
+    }
+  }
+  m = wave_max_u32(m);
+  if (lane == 0) wmax[w] = m;
+  __syncthreads();
+  m = max(max(wmax[0], wmax[1]), max(wmax[2], wmax[3]));
+  const bool split = m != 0u && m < 0x7F800000u;
+  int e = 0;  // S = 2^e
+  if (split) {
+    const float mf = __uint_as_float(m);
+    e = max(ilogbf(mf) - 6, -149);  // mf / 2^e in [64, 128) (or below 64 for tiny rows)
+    if (mf > ldexpf(127.0f, e)) e += 1;
+  }
+  if (threadIdx.x == 0) scales[p] = split ? ldexpf(1.0f, e) : m == 0u ? 0.0f : __uint_as_float(0x7FC00000u);
+#pragma unroll
+  for (int i = 0; i < 2; i++) {
+    const int g = w + 4 * i;
+    if (g < K / 256) {
+      uint32_t q0 = 0u, q1 = 0u, q2 = 0u;
+      if (split) {
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          // explicit roundings (no contraction to choose them): a1 from the rounded 254 d, the remainder of the exact
+          // product after a1 by one fused step
+          const float a = ldexpf(v[i][j], -e), a0 = rintf(a), d = a - a0;
+          const float a1 = rintf(__fmul_rn(d, I8_RATIO)), a2 = rintf(__fmul_rn(fmaf(d, I8_RATIO, -a1), I8_RATIO));
+          q0 |= ((uint32_t)(int)a0 & 0xFFu) << (8 * j);
+          q1 |= ((uint32_t)(int)a1 & 0xFFu) << (8 * j);
+          q2 |= ((uint32_t)(int)a2 & 0xFFu) << (8 * j);
+        }
+      }
+      uint32_t* d = (uint32_t*)(planes + (size_t)p * K + 256 * g + 4 * lane);
+      d[0] = q0;
+      d[plane / 4] = q1;
+      d[plane / 2] = q2;
     }
   }
 }
@@ -999,6 +1069,240 @@ __global__ void __launch_bounds__(256, 2) grouped_mfma_kernel(const __bf16* xs, 
       for (int a = 0; a < RA; a++) {
         const f32x4 o = {acc[a][mt].x * es[a][0], acc[a][mt].y * es[a][1], acc[a][mt].z * es[a][2],
                          acc[a][mt].w * es[a][3]};
+        *(f32x4*)(out + (size_t)(first + r) * N + nw + 16 * a + 4 * q) = o;
+      }
+    }
+  }
+}
+
+// ----------------------------------------------------------------------------- grouped products on the int8 cores
+// The grouped products of the formats whose weights are integers |q| <= 127 before their row or channel scale (int8
+// ConvRot, W4 and W6 codes on the int8 grid) on the int8 matrix cores, v_mfma_i32_16x16x64_i8 (twice the bf16 rate
+// and 64 columns a step), against the rows as three int8 planes (prep_i8_kernel). The weight bytes go in as they are
+// (int8) or as decoded bytes (codes); each plane's sums are exact int32 (|sum| <= 2048 * 127 * 127 < 2^25), and the
+// epilogue adds the planes in float32: out = es * (S * (A0 + (A1 + A2 / 254) / 254)). The work list, placement,
+// slot fill and weight ring are grouped_mfma_kernel's; lane group q takes columns 32 q .. 32 q + 31 of each
+// 128-column chunk in 2 steps of 16 bytes, weights and rows alike.
+
+// W4: one 16-code group's int8-grid values as bytes in column order (word d: codes 4d .. 4d + 3) through the
+// group's scale-byte row t of a signed table (build_qtab<true>); lo / hi as for w4_group
+D3_INLINE i32x4 w4_group_i8(uint32_t lo, uint32_t hi, i32x4 t) {
+  const uint32_t e0 = lookup16(t, lo), o0 = lookup16(t, lo >> 4);  // codes 0, 2, 4, 6 / 1, 3, 5, 7
+  const uint32_t e1 = lookup16(t, hi), o1 = lookup16(t, hi >> 4);  // codes 8, 10, 12, 14 / 9, 11, 13, 15
+  return i32x4{(int)__builtin_amdgcn_perm(o0, e0, 0x05010400u), (int)__builtin_amdgcn_perm(o0, e0, 0x07030602u),
+               (int)__builtin_amdgcn_perm(o1, e1, 0x05010400u), (int)__builtin_amdgcn_perm(o1, e1, 0x07030602u)};
+}
+
+// W6: one 16-code group's values (w6_group's arithmetic) as bytes in column order. rint(t) for |t| < 2^22 is the
+// low mantissa bits of t + 1.5 * 2^23 (round to nearest even, as rintf), two's complement; the clamp to +-127
+// happens on the biased value (NaN -> -127, as fmaxf / fminf give in w6_group).
+D3_INLINE i32x4 w6_group_i8(uint32_t lo, uint32_t hi, uint32_t high, float s) {
+  constexpr float MAGIC = 12582912.0f;
+  const float ms = -32.0f * s;
+  uint32_t u[4][4];  // u[k][b]: code k + 4b
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    const uint32_t h = k >> 1, sel = h | ((h + 2) << 8) | ((h + 4) << 16) | ((h + 6) << 24);
+    const uint32_t p = __builtin_amdgcn_perm(hi, lo, sel);
+    const uint32_t code = ((k & 1 ? p >> 4 : p) & 0x0F0F0F0Fu) | (((high >> (2 * k)) & 0x03030303u) << 4);
+#pragma unroll
+    for (int b = 0; b < 4; b++) {
+      const float t = fmaf((float)((code >> (8 * b)) & 0xFFu), s, ms) + MAGIC;
+      u[k][b] = __float_as_uint(fminf(fmaxf(t, MAGIC - 127.0f), MAGIC + 127.0f));
+    }
+  }
+  i32x4 r;
+#pragma unroll
+  for (int d = 0; d < 4; d++) {
+    const uint32_t p01 = __builtin_amdgcn_perm(u[1][d], u[0][d], 0x0C0C0400u);  // bytes u0, u1, 0, 0
+    const uint32_t p23 = __builtin_amdgcn_perm(u[3][d], u[2][d], 0x04000C0Cu);  // bytes 0, 0, u2, u3
+    r[d] = (int)(p01 | p23);
+  }
+  return r;
+}
+
+constexpr int GI_SC = 2;                   // chunks staged together: 256 columns of each row per stage
+constexpr int GI_PITCH = 128 * GI_SC + 16;  // LDS row stride in bytes: the 16 rows of a tile start 4 banks apart
+
+template <int KIND, int K, int RA>  // KIND 0 int8, 4 / 6 codes; RA row tiles per wave
+__global__ void __launch_bounds__(256, 2) grouped_i8_kernel(const int8_t* xs, int64_t plane, const float* xscale,
+                                                            const int* groups, const int* work, int phase,
+                                                            uint8_t* slot_w, void* slot_s, void* slot_c,
+                                                            const uint8_t* host_w, const void* host_s,
+                                                            const void* host_c, const float* codebook, float* out,
+                                                            int N) {
+  static_assert(KIND == 0 || KIND == 4 || KIND == 6, "integer formats");
+  constexpr int RB = KIND == 0 ? K : K * KIND / 8;  // row bytes
+  constexpr int G = K / 16;                          // codes: 16-column scale groups per row
+  constexpr int CHUNKS = K / 128, MT = GM_ROWS / 16, PL = 3;
+  constexpr int STAGE = MT * PL * GI_SC / 2;  // 16-byte pieces each thread stages per stage
+  constexpr int GM_AHEAD = 2;                 // chunks of weights on their way (one stage)
+  static_assert(GM_AHEAD == GI_SC && CHUNKS % GI_SC == 0, "K a multiple of 256");
+  __shared__ uint32_t qtab[KIND == 4 ? QTAB_WORDS : 1];
+  __shared__ __attribute__((aligned(16))) int8_t bt[MT * PL * 16 * GI_PITCH];
+  // XCD-aware order: workgroup i of the launch runs on XCD i % 8; passes p with p % 8 == xcd are dealt to it
+  const int nx = gridDim.x, lin = blockIdx.x + nx * blockIdx.y, xcd = lin & 7, k = lin >> 3;
+  const int item = (k / nx) * 8 + xcd + (phase == 1 ? work[1] : 0), xb = k % nx;
+  if (item >= work[phase == 0 ? 1 : 0]) return;
+  const int g = work[2 + 2 * item], m0 = work[3 + 2 * item];
+  const int* gp = groups + 5 * g;
+  const int expert = gp[0], slot = gp[1], fill = gp[2] && phase != 1, first = gp[3], rows = gp[4];
+  const bool host = slot < 0 || fill, filler = fill && m0 == 0;  // the group's first pass copies it into its slot
+  const int tiles = min(MT, (rows - m0 + 15) / 16);
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, q = lane >> 4, c = lane & 15;
+  const int nw = xb * 64 * RA + 16 * RA * w;  // the wave's first row
+  if constexpr (KIND == 4) build_qtab<true>(qtab, *(const f32x4*)(codebook + 4 * (tid & 3)));
+  const size_t src = host ? (size_t)expert : (size_t)slot;  // the expert's index in the fields it is read from
+  const uint8_t* arow = (host ? host_w : slot_w) + (src * N + nw + c) * RB;      // this lane's row of tile 0
+  uint8_t* frow = filler ? slot_w + ((size_t)slot * N + nw + c) * RB : slot_w;  // its slot row (fill)
+  const uint8_t* srow = nullptr;                                                 // codes: its scale bytes
+  if constexpr (KIND >= 4) srow = (const uint8_t*)(host ? host_s : slot_s) + (src * N + nw + c) * G;
+  auto load_chunk = [&](int ch, ChunkBytes (&cb)[RA]) {
+    const int k0 = 128 * ch + 32 * q;
+#pragma unroll
+    for (int a = 0; a < RA; a++) {
+      const uint8_t* r = arow + (size_t)16 * a * RB;
+      if constexpr (KIND == 0) {
+        cb[a].b0 = *(const i32x4*)(r + k0);
+        cb[a].b1 = *(const i32x4*)(r + k0 + 16);
+      } else {
+        cb[a].b0 = *(const i32x4*)(r + k0 / 2);
+        cb[a].b1 = i32x4{0, 0, 0, 0};
+        if constexpr (KIND == 6) {
+          const i32x2 hw = *(const i32x2*)(r + K / 2 + k0 / 4);
+          cb[a].b1.x = hw.x;
+          cb[a].b1.y = hw.y;
+        }
+        cb[a].sb0 = srow[16 * a * G + k0 / 16];
+        cb[a].sb1 = srow[16 * a * G + k0 / 16 + 1];
+      }
+    }
+  };
+  // staging: piece j of thread tid is tile j / PL, plane j % PL, row tid >> 4, the 16 bytes at column 16 (tid & 15)
+  // of the stage's 256
+  const int srow_t = tid >> 4, sseg = tid & 15;
+  const size_t srow_at = (size_t)first * K + 16 * sseg;
+  i32x4 stg[STAGE];
+  auto stage_load = [&](int s) {
+#pragma unroll
+    for (int j = 0; j < STAGE; j++) {
+      const int mt = j / PL, t = j % PL;
+      if (mt < tiles) {
+        const int r = min(m0 + 16 * mt + srow_t, rows - 1);
+        stg[j] = *(const i32x4*)(xs + t * plane + srow_at + (size_t)r * K + 128 * GI_SC * s);
+      }
+    }
+  };
+  auto stage_store = [&]() {
+#pragma unroll
+    for (int j = 0; j < STAGE; j++) {
+      if (j < PL * tiles) *(i32x4*)(bt + (j * 16 + srow_t) * GI_PITCH + 16 * sseg) = stg[j];
+    }
+  };
+  // the epilogue's scales of rows nw + 16 a + 4 q .. + 3: int8 row scales, codes channel scales
+  float es[RA][4];
+  {
+    const float* s = (const float*)(KIND == 0 ? (host ? host_s : slot_s) : (host ? host_c : slot_c)) + src * N;
+    float* fs = (float*)(KIND == 0 ? slot_s : slot_c) + (size_t)slot * N;
+#pragma unroll
+    for (int a = 0; a < RA; a++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        es[a][r] = s[nw + 16 * a + 4 * q + r];
+        if (filler && c == 0) fs[nw + 16 * a + 4 * q + r] = es[a][r];
+      }
+  }
+  i32x4 acc[RA][MT][PL];
+#pragma unroll
+  for (int a = 0; a < RA; a++)
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+      for (int t = 0; t < PL; t++) acc[a][mt][t] = i32x4{0, 0, 0, 0};
+  // one chunk (half `h` of its stage): its weights (loaded GM_AHEAD chunks ahead into `bytes`, which then take chunk
+  // ch + GM_AHEAD's) as int8 operands, the slot filled, the products from LDS; after the stage's second chunk the
+  // next stage's rows (requested with the first chunk) go into LDS
+  auto chunk = [&](int ch, int h, ChunkBytes (&bytes)[RA]) {
+    const int k0 = 128 * ch + 32 * q;
+    if (filler) {  // the expert's bytes copied into its slot as they are read
+#pragma unroll
+      for (int a = 0; a < RA; a++) {
+        uint8_t* f = frow + (size_t)16 * a * RB;
+        if constexpr (KIND == 0) {
+          *(i32x4*)(f + k0) = bytes[a].b0;
+          *(i32x4*)(f + k0 + 16) = bytes[a].b1;
+        } else {
+          *(i32x4*)(f + k0 / 2) = bytes[a].b0;
+          if constexpr (KIND == 6) *(i32x2*)(f + K / 2 + k0 / 4) = i32x2{bytes[a].b1.x, bytes[a].b1.y};
+          uint8_t* fsb = (uint8_t*)slot_s + ((size_t)slot * N + nw + 16 * a + c) * G;
+          fsb[k0 / 16] = (uint8_t)bytes[a].sb0;
+          fsb[k0 / 16 + 1] = (uint8_t)bytes[a].sb1;
+        }
+      }
+    }
+    i32x4 wa[RA][2];
+#pragma unroll
+    for (int a = 0; a < RA; a++) {
+      if constexpr (KIND == 0) {
+        wa[a][0] = bytes[a].b0;
+        wa[a][1] = bytes[a].b1;
+      } else if constexpr (KIND == 4) {
+        wa[a][0] = w4_group_i8((uint32_t)bytes[a].b0.x, (uint32_t)bytes[a].b0.y, *(const i32x4*)(qtab + 4 * bytes[a].sb0));
+        wa[a][1] = w4_group_i8((uint32_t)bytes[a].b0.z, (uint32_t)bytes[a].b0.w, *(const i32x4*)(qtab + 4 * bytes[a].sb1));
+      } else {
+        wa[a][0] = w6_group_i8((uint32_t)bytes[a].b0.x, (uint32_t)bytes[a].b0.y, (uint32_t)bytes[a].b1.x,
+                               fp8x2_to_f32<false>(bytes[a].sb0).x);
+        wa[a][1] = w6_group_i8((uint32_t)bytes[a].b0.z, (uint32_t)bytes[a].b0.w, (uint32_t)bytes[a].b1.y,
+                               fp8x2_to_f32<false>(bytes[a].sb1).x);
+      }
+    }
+    if (h == 0 && ch + GI_SC < CHUNKS) stage_load(ch / GI_SC + 1);
+    if (ch + GM_AHEAD < CHUNKS) load_chunk(ch + GM_AHEAD, bytes);
+#pragma unroll
+    for (int st = 0; st < 2; st++)
+#pragma unroll
+      for (int mt = 0; mt < MT; mt++) {
+        if (mt < tiles) {
+          const int8_t* bp = bt + (mt * PL * 16 + c) * GI_PITCH + 128 * h + 32 * q + 16 * st;
+          i32x4 b[PL];
+#pragma unroll
+          for (int t = 0; t < PL; t++) b[t] = *(const i32x4*)(bp + 16 * t * GI_PITCH);
+#pragma unroll
+          for (int a = 0; a < RA; a++)
+#pragma unroll
+            for (int t = 0; t < PL; t++) acc[a][mt][t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wa[a][st], b[t], acc[a][mt][t], 0, 0, 0);
+        }
+      }
+    if (h == GI_SC - 1 && ch + 1 < CHUNKS) {
+      __syncthreads();  // every wave is done with this stage's rows
+      stage_store();
+      __syncthreads();
+    }
+  };
+  ChunkBytes ring[GM_AHEAD][RA];  // chunk ch's weight bytes in ring[ch % GM_AHEAD]
+  stage_load(0);
+#pragma unroll
+  for (int d = 0; d < GM_AHEAD; d++) load_chunk(d, ring[d]);
+  stage_store();
+  __syncthreads();
+  for (int ch = 0; ch < CHUNKS; ch += GM_AHEAD) {
+#pragma unroll
+    for (int d = 0; d < GM_AHEAD; d++) chunk(ch + d, d, ring[d]);
+  }
+  // lane l holds rows nw + 16 a + 4 q .. + 3 of activation row m0 + 16 mt + (l & 15)
+#pragma unroll
+  for (int mt = 0; mt < MT; mt++) {
+    const int r = m0 + 16 * mt + c;
+    if (mt < tiles && r < rows) {
+      const float sx = xscale[first + r];
+#pragma unroll
+      for (int a = 0; a < RA; a++) {
+        f32x4 o;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          const float mid = (float)acc[a][mt][1][i] + (float)acc[a][mt][2][i] / I8_RATIO;
+          o[i] = es[a][i] * (sx * ((float)acc[a][mt][0][i] + mid / I8_RATIO));
+        }
         *(f32x4*)(out + (size_t)(first + r) * N + nw + 16 * a + 4 * q) = o;
       }
     }
@@ -1989,6 +2293,71 @@ int d3_prep_planes(int32_t mode, int32_t rotate, int32_t n_planes, const void* x
   }
 #undef D3_PREP
   return done("d3_prep_planes");
+}
+
+int d3_prep_planes_i8(int32_t mode, int32_t rotate, const void* x, const int64_t* order, int32_t k, int32_t P,
+                      int32_t K, void* planes, float* scales, void* stream) {
+  if (!x || !planes || !scales) return fail("d3_prep_planes_i8: null pointer");
+  if (mode < 0 || mode > 2 || P < 0 || k < 1 || !supported_k(K))
+    return fail("d3_prep_planes_i8: mode 0-2, K in {256..2048}");
+  if (P == 0) return 0;
+  const hipStream_t s = (hipStream_t)stream;
+  const int64_t plane = (int64_t)P * K;
+  int8_t* out = (int8_t*)planes;
+#define D3_PREP(M, R) hipLaunchKernelGGL((prep_i8_kernel<M, R>), dim3(P), dim3(256), 0, s, x, order, k, K, out, plane, scales)
+  switch (mode * 2 + (rotate ? 1 : 0)) {
+    case 0: D3_PREP(0, false); break;
+    case 1: D3_PREP(0, true); break;
+    case 2: D3_PREP(1, false); break;
+    case 3: D3_PREP(1, true); break;
+    case 4: D3_PREP(2, false); break;
+    default: D3_PREP(2, true); break;
+  }
+#undef D3_PREP
+  return done("d3_prep_planes_i8");
+}
+
+int d3_grouped_i8(int32_t kind, const void* planes, const float* scales, int64_t plane, const int32_t* groups,
+                  int32_t n_groups, const int32_t* work, int64_t work_ints, int32_t fills_first, void* slot_w,
+                  void* slot_s, void* slot_c, const void* host_w, const void* host_s, const void* host_c,
+                  const float* codebook, float* out, int32_t N, int32_t K, void* stream) {
+  if (!planes || !scales || !groups || !work || !slot_w || !slot_s || !host_w || !host_s || !out)
+    return fail("d3_grouped_i8: null pointer");
+  if (kind != 0 && kind != 4 && kind != 6) return fail("d3_grouped_i8: kind 0, 4 or 6");
+  if (kind != 0 && (!slot_c || !host_c)) return fail("d3_grouped_i8: codes need channel scales");
+  if (kind == 4 && !codebook) return fail("d3_grouped_i8: 4 bits need a codebook");
+  if (n_groups < 1) return 0;
+  if (N < 64 || N % 64 || !supported_k(K) || plane < K || plane % K)
+    return fail("d3_grouped_i8: N % 64 == 0, K in {256..2048}, plane a multiple of K");
+  const int64_t T = plane / K;
+  if (T > INT32_MAX) return fail("d3_grouped_i8: more than 2^31 rows");
+  const int64_t need = d3_grouped_mfma_work_ints(n_groups, T);
+  if (work_ints < need) return fail("d3_grouped_i8: work holds fewer than d3_grouped_mfma_work_ints ints");
+  const int cap = (int)((need - 2) / 2), firsts = (n_groups + 7) / 8 * 8;
+  const hipStream_t s = (hipStream_t)stream;
+  const int8_t* xs = (const int8_t*)planes;
+  const uint8_t* hw = (const uint8_t*)host_w;
+  uint8_t* sw = (uint8_t*)slot_w;
+#define D3_GI(KD, RA, PH, Y) D3_K_SWITCH(K, hipLaunchKernelGGL((grouped_i8_kernel<KD, KK, RA>), dim3(N / (64 * RA), Y), dim3(256), 0, s, xs, plane, scales, groups, work, PH, sw, slot_s, slot_c, hw, host_s, host_c, codebook, out, N))
+// two 16-row tiles per wave where N allows
+#define D3_GI_RA(KD, PH, Y) \
+  if (N % 128 == 0) { D3_GI(KD, 2, PH, Y); } else { D3_GI(KD, 1, PH, Y); }
+#define D3_GI_KIND(PH, Y)                        \
+  switch (kind) {                                \
+    case 0: D3_GI_RA(0, PH, Y); break;           \
+    case 4: D3_GI_RA(4, PH, Y); break;           \
+    default: D3_GI_RA(6, PH, Y); break;          \
+  }
+  if (fills_first) {
+    D3_GI_KIND(0, firsts);
+    D3_GI_KIND(1, cap);
+  } else {
+    D3_GI_KIND(2, cap);
+  }
+#undef D3_GI_KIND
+#undef D3_GI_RA
+#undef D3_GI
+  return done("d3_grouped_i8");
 }
 
 int d3_combine_rows(const float* sorted_out, const int32_t* inverse, const void* weights, int32_t weights_bf16,

@@ -83,6 +83,11 @@ SIGNATURES = {
     "d3_expert_groups": (c_int32, [c_void_p, c_int32, c_int32, c_void_p, c_void_p, c_void_p, c_void_p]),
     "d3_prep_planes": (c_int32, [c_int32, c_int32, c_int32, c_void_p, c_void_p, c_int32, c_int32, c_int32, c_void_p,
                                  c_void_p]),
+    "d3_prep_planes_i8": (c_int32, [c_int32, c_int32, c_void_p, c_void_p, c_int32, c_int32, c_int32, c_void_p,
+                                    c_void_p, c_void_p]),
+    "d3_grouped_i8": (c_int32, [c_int32, c_void_p, c_void_p, c_int64, c_void_p, c_int32, c_void_p, c_int64, c_int32,
+                                c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+                                c_int32, c_int32, c_void_p]),
     "d3_combine_rows": (c_int32, [c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_int32, c_int32, c_void_p,
                                   c_int32, c_void_p]),
     "d3_decode_codes": (c_int32, [c_int32, c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_void_p, c_void_p]),

@@ -170,16 +170,35 @@ def grouped_planes(kind, planes, rows, width, groups, work, slot_fields, host_fi
     return out
 
 
+def grouped_i8(kind, planes, scales, rows, width, groups, work, slot_fields, host_fields, codebook, n,
+               fills_first=False):
+    """grouped_planes on the int8 matrix cores for kind "int8", "w4" or "w6", over (planes [3, rows * width] int8,
+    scales [rows] float32) from prep_planes_i8."""
+    code, wkey = GROUPED_KINDS[kind]
+    out = torch.empty((rows, n), dtype=torch.float32, device=planes.device)
+    if rows == 0:
+        return out
+    _call("d3_grouped_i8", code, _p(planes), _p(scales), rows * width, _p(groups), groups.shape[0], _p(work),
+          work.shape[0], int(fills_first), *_grouped_fields(slot_fields, host_fields, codebook, wkey), _p(out), n,
+          width, _stream(planes))
+    return out
+
+
 def _grouped(kind, x, groups, slot_fields, host_fields, codebook, n, wkey, matrix=None):
-    """The grouped products on the bf16 matrix cores (x split into three bf16 planes first) when n % 64 == 0 or
-    `matrix`, else on the vector unit."""
+    """The grouped products on the matrix cores when n % 64 == 0 or `matrix` (int8 and the codes on the int8 cores
+    against x as three int8 planes, fp8 on the bf16 cores against three bf16 planes), else on the vector unit."""
     x = x.contiguous()
     if (matrix if matrix is not None else n % 64 == 0) and x.numel():
+        name = {0: "int8", 1: "fp8", 4: "w4", 6: "w6"}[kind]
+        work = grouped_plan(groups, x.shape[0])
+        if kind != 1:
+            planes, scales = prep_planes_i8(x, False)
+            return grouped_i8(name, planes, scales, x.shape[0], x.shape[1], groups, work, slot_fields, host_fields,
+                              codebook, n)
         planes = torch.empty((3, x.numel()), dtype=torch.bfloat16, device=x.device)
         _call("d3_split_bf16x3", _p(x), x.numel(), _p(planes), _stream(x))
-        name = {0: "int8", 1: "fp8", 4: "w4", 6: "w6"}[kind]
-        return grouped_planes(name, planes, x.shape[0], x.shape[1], groups, grouped_plan(groups, x.shape[0]),
-                              slot_fields, host_fields, codebook, n)
+        return grouped_planes(name, planes, x.shape[0], x.shape[1], groups, work, slot_fields, host_fields, codebook,
+                              n)
     out = torch.empty((x.shape[0], n), dtype=torch.float32, device=x.device)
     if x.numel():
         _call("d3_grouped", kind, _p(x), _p(groups), groups.shape[0],
@@ -220,6 +239,27 @@ def prep_planes(x, rotate, order=None, k=1, swiglu=False, n_planes=3):
     planes = torch.empty((n_planes, P * width), dtype=torch.bfloat16, device=x.device)
     _call("d3_prep_planes", mode, int(rotate), n_planes, _p(x), _p(order), int(k), P, width, _p(planes), _stream(x))
     return planes
+
+
+def prep_planes_i8(x, rotate, order=None, k=1, swiglu=False):
+    """(planes [3, P * K] int8, scales [P] float32) for grouped_i8, rows as for prep_planes: v / S = a0 + a1 / 254 +
+    a2 / 254^2 to within 0.5 / 254^2, S the row's power-of-two scale (max |v| <= 127 S)."""
+    x = x.contiguous()
+    width = x.shape[1] // 2 if swiglu else x.shape[1]
+    if swiglu:
+        if x.dtype != torch.float32:
+            raise TypeError("prep_planes_i8(swiglu=True) takes float32 gate | up rows")
+        mode = 2
+    elif x.dtype == torch.bfloat16:
+        mode = 1
+    else:
+        x, mode = x.float(), 0
+    P = order.shape[0] if order is not None else x.shape[0]
+    planes = torch.empty((3, P * width), dtype=torch.int8, device=x.device)
+    scales = torch.empty(P, dtype=torch.float32, device=x.device)
+    _call("d3_prep_planes_i8", mode, int(rotate), _p(x), _p(order), int(k), P, width, _p(planes), _p(scales),
+          _stream(x))
+    return planes, scales
 
 
 _OUT_TYPES = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}

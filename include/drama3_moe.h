@@ -262,6 +262,23 @@ int d3_expert_groups(const int64_t* ids, int32_t P, int32_t E, int64_t* order, i
 int d3_prep_planes(int32_t mode, int32_t rotate, int32_t n_planes, const void* x, const int64_t* order, int32_t k,
                    int32_t P, int32_t K, void* planes, void* stream);
 
+/* The int8 formats' products (kind 0 int8, 4 / 6 codes; the same replacement: kernels.py:365-464,538-587 as called
+ * from offload.py:126-149) on the int8 matrix cores. Their weights are integers |q| <= 127 before the row or channel
+ * scale, so they enter the int8 products as bytes; the float32 rows enter as three int8 planes and a power-of-two row
+ * scale S. d3_prep_planes_i8 takes the rows as d3_prep_planes does (mode, rotate, order, k) and writes planes int8
+ * [3, P * K] = a0, a1, a2 and scales [P] float32: v / S = a0 + a1 / 254 + a2 / 254^2 + r with every a in
+ * [-127, 127] and |r| < 0.5 / 254^2 + 2^-24, S the smallest power of two with max |v| <= 127 S, so the planes hold each row
+ * to within 1.25e-7 of its largest magnitude, and rows of integers times a power of two exactly. A row holding inf or
+ * NaN gets S = NaN (its products NaN), an all-zero row S = 0. d3_grouped_i8 is d3_grouped_mfma over those planes
+ * (plane = T * K bytes per plane, the same groups, work plan, fields and fills_first); each plane's sums are exact
+ * int32, added in float32 at the end: out = scale * (S * (A0 + (A1 + A2 / 254) / 254)). N % 64 == 0. */
+int d3_prep_planes_i8(int32_t mode, int32_t rotate, const void* x, const int64_t* order, int32_t k, int32_t P,
+                      int32_t K, void* planes, float* scales, void* stream);
+int d3_grouped_i8(int32_t kind, const void* planes, const float* scales, int64_t plane, const int32_t* groups,
+                  int32_t n_groups, const int32_t* work, int64_t work_ints, int32_t fills_first, void* slot_w,
+                  void* slot_s, void* slot_c, const void* host_w, const void* host_s, const void* host_c,
+                  const float* codebook, float* out, int32_t N, int32_t K, void* stream);
+
 /* The weighted sum over k (offload.py:144-149): out [T, H] = sum over j in order of weights[t, j] *
  * sorted_out[inverse[t k + j]] in float32 (pairs with inverse -1 left out), stored as float32 / bf16 / fp16
  * (out_type 0 / 1 / 2); weights [T, k] bf16 (weights_bf16) or float32. H % 4 == 0. */

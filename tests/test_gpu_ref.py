@@ -177,6 +177,93 @@ def test_prep_planes(mode, rotate):
         assert np.all(np.abs(total - exact) <= 2.0 ** -24 * np.abs(exact))
 
 
+def split_i8_np(v):
+    """(a0, a1, a2 float32 [P, K], S [P]) of float32 rows v [P, K] as d3_prep_planes_i8 splits them: S the smallest
+    power of two with max |v| <= 127 S, a0 = rint(v / S), d = v / S - a0, a1 = rint(f32(254 d)), a2 = rint(f32(254
+    f32(254 d - a1))) with 254 d - a1 from the exact product (float64 holds it)."""
+    v = np.asarray(v, np.float32)
+    m = np.abs(v).max(axis=1)
+    e = np.frexp(m)[1].astype(np.int64) - 7
+    e = np.maximum(e, -149)
+    e = np.where(m > np.ldexp(np.float32(127), e).astype(np.float32), e + 1, e)
+    a = np.ldexp(v, -e[:, None]).astype(np.float32)
+    a0 = np.rint(a)
+    d = (a - a0).astype(np.float32)
+    a1 = np.rint((d * np.float32(254)).astype(np.float32))
+    r2 = (d.astype(np.float64) * 254 - a1).astype(np.float32)
+    a2 = np.rint((r2 * np.float32(254)).astype(np.float32))
+    return a0, a1, a2, np.ldexp(np.float32(1), e).astype(np.float32)
+
+
+@pytest.mark.parametrize("mode, rotate", [("f32", False), ("bf16", True), ("f32", True), ("swiglu", True),
+                                          ("swiglu", False)])
+def test_prep_planes_i8(mode, rotate):
+    """d3_prep_planes_i8: the rows prep_planes gathers, SwiGLUs and rotates, as three int8 planes and a power-of-two
+    scale S. Pinned by what the split must satisfy whatever its arithmetic: every plane value in [-127, 127], S the
+    smallest power of two with max |v| <= 127 S, and S (a0 + a1 / 254 + a2 / 254^2) within (0.5 / 254^2 + 2^-24) S,
+    so 1.25e-7 max |v|, of each value (float64); the planes also equal a numpy split of the kernel's own float32 rows
+    (d3_rotate's transform)."""
+    rng = np.random.default_rng(60 + len(mode) + rotate)
+    T, k, K = 29, 3, 768 if mode != "f32" else 2048
+    order = rng.permutation(T * k)
+    if mode == "swiglu":
+        x = rng.standard_normal((T * k, 2 * K)).astype(np.float32)
+        planes, scales = kernels.prep_planes_i8(dev(x), rotate, swiglu=True)
+        if rotate:
+            rows = kernels.rotate(dev(x), torch.ones(1, dtype=torch.int32, device=DEV), swiglu=True).cpu().numpy()
+        else:
+            g, u = x[:, :K].astype(np.float64), x[:, K:].astype(np.float64)
+            rows = g / (1 + np.exp(-g)) * u
+    else:
+        if mode == "bf16":
+            bits = numerics.f32_to_bf16_bits(rng.standard_normal((T, K)).astype(np.float32))
+            xd, x = dev(bits).view(torch.bfloat16), numerics.bf16_bits_to_f32(bits)
+        else:
+            x = (rng.standard_normal((T, K)) * np.exp(rng.uniform(-20, 20, (T, 1)))).astype(np.float32)
+            xd = dev(x)
+        planes, scales = kernels.prep_planes_i8(xd, rotate, dev(order.astype(np.int64)), k)
+        rows = x[order // k]
+        if rotate:
+            rows = kernels.rotate(dev(rows.astype(np.float32)), torch.ones(1, dtype=torch.int32, device=DEV)).cpu().numpy()
+    P = T * k
+    a = [planes[t].cpu().numpy().reshape(P, K).astype(np.float64) for t in range(3)]
+    S = scales.cpu().numpy().astype(np.float64)
+    assert all(np.abs(p).max() <= 127 for p in a)
+    m = np.abs(rows).max(axis=1)
+    exact = mode != "swiglu" or rotate   # rows as the kernel computes them (else numpy's exp against the kernel's)
+    assert np.all(np.log2(S) == np.round(np.log2(S)))
+    if exact:
+        assert np.all(m <= 127 * S) and np.all(m > 63.5 * S)
+    held = S[:, None] * (a[0] + (a[1] + a[2] / 254) / 254)
+    if exact:
+        assert np.all(np.abs(held - rows) <= (0.5 / 254 ** 2 + 2.0 ** -24) * S[:, None])
+    assert np.all(np.abs(held - rows) <= (1.25e-7 if exact else 2e-6) * m[:, None])
+    if exact:
+        want = split_i8_np(rows)
+        for t in range(3):
+            assert np.array_equal(a[t], want[t]), t
+        assert np.array_equal(S, want[3])
+
+
+def test_prep_planes_i8_special_rows():
+    """A row of integers times a power of two lies in a0 alone (so one-hot rows are exact); an all-zero row gets
+    S = 0 and a row holding inf or NaN S = NaN, with zero planes; the other rows are unaffected."""
+    K = 256
+    x = np.zeros((5, K), np.float32)
+    x[0] = np.arange(K) % 255 - 127            # integers up to 127: S = 1
+    x[1, 7] = 3.0                              # one-hot times 3: S = 2^-5, a0 = 96
+    x[2, 3], x[2, 9] = np.inf, 1.0
+    x[3, 5] = np.nan
+    planes, scales = kernels.prep_planes_i8(dev(x), False)
+    a = [planes[t].cpu().numpy().reshape(5, K) for t in range(3)]
+    S = scales.cpu().numpy()
+    assert S[0] == 1.0 and np.array_equal(a[0][0], x[0]) and not a[1][0].any() and not a[2][0].any()
+    assert S[1] == 2.0 ** -5 and a[0][1, 7] == 96 and np.count_nonzero(a[0][1]) == 1 and not a[1][1].any()
+    assert np.isnan(S[2]) and np.isnan(S[3]) and S[4] == 0.0
+    for r in (2, 3, 4):
+        assert not any(p[r].any() for p in a), r
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("wdtype", [torch.bfloat16, torch.float32])
 def test_combine_rows(dtype, wdtype):
