@@ -562,45 +562,52 @@ __global__ void __launch_bounds__(256) split3_kernel(const float* x, int64_t n8,
 // then (group, first row of the pass) per pass: the first passes, then the others; within each, the passes of 4 tiles
 // first, then those of 3, 2, 1. Groups that are empty or whose rows lie outside [0, T) get none; no more than cap
 // passes are listed. One workgroup.
-__global__ void __launch_bounds__(256) grouped_plan_kernel(const int* groups, int n_groups, int T, int* work, int cap) {
-  static_assert(GM_ROWS % 16 == 0 && GM_ROWS <= 64, "passes of 1 to 4 tiles");
-  __shared__ int count[8], cursor[8];  // bucket 4 - tiles (first passes), 8 - tiles (later passes)
-  if (threadIdx.x < 8) count[threadIdx.x] = 0;
-  __syncthreads();
-  auto tiles_of = [](int n) { return (min(n, GM_ROWS) + 15) / 16; };
-  for (int g = threadIdx.x; g < n_groups; g += 256) {
-    const int first = groups[5 * g + 3], rows = groups[5 * g + 4];
-    if (rows <= 0 || first < 0 || rows > T - first) continue;
-    atomicAdd(&count[4 - tiles_of(rows)], 1);
-    if (rows > GM_ROWS) {
-      atomicAdd(&count[8 - GM_ROWS / 16], (rows - GM_ROWS) / GM_ROWS);
-      if (rows % GM_ROWS) atomicAdd(&count[8 - tiles_of(rows % GM_ROWS)], 1);
-    }
+// The plan in three steps for a workgroup: every group counted into its buckets (plan_count), the buckets' offsets
+// by one thread (plan_offsets), every group's passes put in place (plan_put), a barrier between the steps. count /
+// cursor: 8 LDS ints, bucket 4 - tiles (first passes), 8 - tiles (later passes).
+static_assert(GM_ROWS % 16 == 0 && GM_ROWS <= 64, "passes of 1 to 4 tiles");
+D3_INLINE int plan_tiles(int n) { return (min(n, GM_ROWS) + 15) / 16; }
+D3_INLINE bool plan_valid(int first, int rows, int T) { return rows > 0 && first >= 0 && rows <= T - first; }
+D3_INLINE void plan_count(int first, int rows, int T, int* count) {
+  if (!plan_valid(first, rows, T)) return;
+  atomicAdd(&count[4 - plan_tiles(rows)], 1);
+  if (rows > GM_ROWS) {
+    atomicAdd(&count[8 - GM_ROWS / 16], (rows - GM_ROWS) / GM_ROWS);
+    if (rows % GM_ROWS) atomicAdd(&count[8 - plan_tiles(rows % GM_ROWS)], 1);
   }
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    int at = 0;
-    for (int b = 0; b < 8; b++) {
-      cursor[b] = at;
-      at += count[b];
-      if (b == 3) work[1] = min(at, cap);
-    }
-    work[0] = min(at, cap);
+}
+D3_INLINE void plan_offsets(const int* count, int* cursor, int* work, int cap) {
+  int at = 0;
+  for (int b = 0; b < 8; b++) {
+    cursor[b] = at;
+    at += count[b];
+    if (b == 3) work[1] = min(at, cap);
   }
-  __syncthreads();
-  auto put = [&](int bucket, int g, int m0) {
+  work[0] = min(at, cap);
+}
+D3_INLINE void plan_put(int g, int first, int rows, int T, int* cursor, int* work, int cap) {
+  if (!plan_valid(first, rows, T)) return;
+  auto put = [&](int bucket, int m0) {
     const int at = atomicAdd(&cursor[bucket], 1);
     if (at < cap) {
       work[2 + 2 * at] = g;
       work[3 + 2 * at] = m0;
     }
   };
-  for (int g = threadIdx.x; g < n_groups; g += 256) {
-    const int first = groups[5 * g + 3], rows = groups[5 * g + 4];
-    if (rows <= 0 || first < 0 || rows > T - first) continue;
-    put(4 - tiles_of(rows), g, 0);
-    for (int m0 = GM_ROWS; m0 < rows; m0 += GM_ROWS) put(8 - tiles_of(rows - m0), g, m0);
-  }
+  put(4 - plan_tiles(rows), 0);
+  for (int m0 = GM_ROWS; m0 < rows; m0 += GM_ROWS) put(8 - plan_tiles(rows - m0), m0);
+}
+
+__global__ void __launch_bounds__(256) grouped_plan_kernel(const int* groups, int n_groups, int T, int* work, int cap) {
+  __shared__ int count[8], cursor[8];
+  if (threadIdx.x < 8) count[threadIdx.x] = 0;
+  __syncthreads();
+  for (int g = threadIdx.x; g < n_groups; g += 256) plan_count(groups[5 * g + 3], groups[5 * g + 4], T, count);
+  __syncthreads();
+  if (threadIdx.x == 0) plan_offsets(count, cursor, work, cap);
+  __syncthreads();
+  for (int g = threadIdx.x; g < n_groups; g += 256)
+    plan_put(g, groups[5 * g + 3], groups[5 * g + 4], T, cursor, work, cap);
 }
 
 // ------------------------------------------------------------------------------- a prompt's pairs and rows
@@ -608,13 +615,15 @@ __global__ void __launch_bounds__(256) grouped_plan_kernel(const int* groups, in
 // workgroup counts the experts' pairs in LDS, takes the exclusive prefix as each group's first row, and deals every
 // pair a place in its expert's range. Within a group the pairs' order is the order of their atomic adds: every output
 // row is computed from its own activation row alone, so no result depends on it. ids outside [0, E) take the places
-// after every group, inverse -1.
+// after every group, inverse -1. With `work`, the same workgroup also plans the grouped products' passes over the
+// groups (grouped_plan_kernel's plan, from the counts it holds), so that takes no launch of its own.
 constexpr int GROUPS_MAX_E = 1024;
 __global__ void __launch_bounds__(1024) expert_groups_kernel(const int64_t* ids, int P, int E, int64_t* order,
-                                                             int* inverse, int* groups) {
-  __shared__ int count[GROUPS_MAX_E + 1], cursor[GROUPS_MAX_E + 1], wave_total[16];
+                                                             int* inverse, int* groups, int* work, int cap) {
+  __shared__ int count[GROUPS_MAX_E + 1], cursor[GROUPS_MAX_E + 1], wave_total[16], pcount[8], pcursor[8];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   for (int e = tid; e <= E; e += 1024) count[e] = 0;
+  if (tid < 8) pcount[tid] = 0;
   __syncthreads();
   for (int p = tid; p < P; p += 1024) {
     const int64_t e = ids[p];
@@ -648,6 +657,13 @@ __global__ void __launch_bounds__(1024) expert_groups_kernel(const int64_t* ids,
     for (int i = 0; i < 16; i++) all += wave_total[i];
     cursor[E] = all;
   }
+  if (work) {  // thread e < E holds group e's (first, rows)
+    if (tid < E) plan_count(first, v, P, pcount);
+    __syncthreads();
+    if (tid == 0) plan_offsets(pcount, pcursor, work, cap);
+    __syncthreads();
+    if (tid < E) plan_put(tid, first, v, P, pcursor, work, cap);
+  }
   __syncthreads();
   for (int p = tid; p < P; p += 1024) {
     const int64_t e = ids[p];
@@ -658,9 +674,6 @@ __global__ void __launch_bounds__(1024) expert_groups_kernel(const int64_t* ids,
   }
 }
 
-// Planes hi, mid, lo [P, K] of the rows the grouped products read (split3_kernel's split): row p is x's row
-// order[p] / k (x's row p without order); SRC 0 float32 rows [., K], 1 bf16 rows, 2 float32 gate | up rows [., 2K]
-// through SiLU(gate) * up (kernels.py:222-258's SwiGLU); ROT: in the ConvRot basis (H256 on every 256 columns, / 16).
 // columns c0 .. c0 + 3 of row `row` of x as float (SRC as for prep_planes_kernel)
 template <int SRC> D3_INLINE void load_row4(const void* x, size_t row, int K, int c0, float* v) {
   if constexpr (SRC == 0) {
@@ -679,6 +692,9 @@ template <int SRC> D3_INLINE void load_row4(const void* x, size_t row, int K, in
   }
 }
 
+// Planes hi, mid, lo [P, K] of the rows the grouped products read (split3_kernel's split): row p is x's row
+// order[p] / k (x's row p without order); SRC 0 float32 rows [., K], 1 bf16 rows, 2 float32 gate | up rows [., 2K]
+// through SiLU(gate) * up (kernels.py:222-258's SwiGLU); ROT: in the ConvRot basis (H256 on every 256 columns, / 16).
 template <int SRC, bool ROT, int PL>
 __global__ void __launch_bounds__(256) prep_planes_kernel(const void* x, const int64_t* order, int k, int K,
                                                           __bf16* planes, int64_t plane) {
@@ -859,11 +875,18 @@ D3_INLINE void w4_group(uint32_t lo, uint32_t hi, i32x4 t, bf16x8& a0, bf16x8& a
   }
 }
 
+// The row of the planes that row p of the passes reads: p itself, or with `order` x's row order[p] / k (the rows of
+// a prompt's pairs taken from its token rows, so no gathered copy is made), kept within the planes' xrows rows.
+D3_INLINE size_t plane_row(const int64_t* order, int k, int xrows, int p) {
+  return order ? (size_t)min(max((int)order[p], 0) / k, xrows - 1) : (size_t)p;
+}
+
 // grid (N / (64 RA), a multiple of 8 rows): the workgroups of one pass run on one XCD (the dispatcher deals
 // workgroup i to XCD i % 8), where its activation rows stay in that XCD's L2. PHASE 2 runs every pass of the plan;
 // PHASE 0 the first passes, PHASE 1 the others, a filled group's then read from its slot (the first passes filled it).
 template <int KIND, int K, int RA, int PL>  // KIND 0 int8, 1 fp8, 4 / 6 codes; RA row tiles per wave; PL planes
-__global__ void __launch_bounds__(256, 2) grouped_mfma_kernel(const __bf16* xs, int64_t plane, const int* groups,
+__global__ void __launch_bounds__(256, 2) grouped_mfma_kernel(const __bf16* xs, int64_t plane, const int64_t* order,
+                                                              int k_order, int xrows, const int* groups,
                                                               const int* work, int phase, uint8_t* slot_w, void* slot_s,
                                                               void* slot_c, const uint8_t* host_w, const void* host_s,
                                                               const void* host_c, const float* codebook, float* out,
@@ -919,16 +942,16 @@ __global__ void __launch_bounds__(256, 2) grouped_mfma_kernel(const __bf16* xs, 
   // staging: piece j of thread tid is tile j / PL, plane j % PL, row (tid >> 4) & 15, the 16 bytes at column
   // 8 (tid & 15)
   const int srow_t = (tid >> 4) & 15, sseg = tid & 15;
-  const size_t srow_at = (size_t)first * K + 8 * sseg;
+  size_t xr[MT];  // where each tile's staged row starts in a plane
+#pragma unroll
+  for (int mt = 0; mt < MT; mt++)
+    xr[mt] = plane_row(order, k_order, xrows, first + min(m0 + 16 * mt + srow_t, rows - 1)) * K + 8 * sseg;
   i32x4 stg[STAGE];
   auto stage_load = [&](int ch) {
 #pragma unroll
     for (int j = 0; j < STAGE; j++) {
       const int mt = j / PL, t = j % PL;
-      if (mt < tiles) {
-        const int r = min(m0 + 16 * mt + srow_t, rows - 1);
-        stg[j] = *(const i32x4*)(xs + t * plane + srow_at + (size_t)r * K + 128 * ch);
-      }
+      if (mt < tiles) stg[j] = *(const i32x4*)(xs + t * plane + xr[mt] + 128 * ch);
     }
   };
   auto stage_store = [&]() {
@@ -1124,8 +1147,12 @@ D3_INLINE i32x4 w6_group_i8(uint32_t lo, uint32_t hi, uint32_t high, float s) {
 constexpr int GI_SC = 2;                   // chunks staged together: 256 columns of each row per stage
 constexpr int GI_PITCH = 128 * GI_SC + 16;  // LDS row stride in bytes: the 16 rows of a tile start 4 banks apart
 
-template <int KIND, int K, int RA>  // KIND 0 int8, 4 / 6 codes; RA row tiles per wave
-__global__ void __launch_bounds__(256, 2) grouped_i8_kernel(const int8_t* xs, int64_t plane, const float* xscale,
+// KIND 0 int8, 4 / 6 codes; RA row tiles per wave; AHEAD chunks of weights on their way while one is multiplied
+// (a multiple of the stage's GI_SC: each stage's rows are requested before the weights, so the wait for them at the
+// stage's end leaves the weights in flight)
+template <int KIND, int K, int RA, int AHEAD, int OCC = 2>
+__global__ void __launch_bounds__(256, OCC) grouped_i8_kernel(const int8_t* xs, int64_t plane, const float* xscale,
+                                                            const int64_t* order, int k_order, int xrows,
                                                             const int* groups, const int* work, int phase,
                                                             uint8_t* slot_w, void* slot_s, void* slot_c,
                                                             const uint8_t* host_w, const void* host_s,
@@ -1136,8 +1163,7 @@ __global__ void __launch_bounds__(256, 2) grouped_i8_kernel(const int8_t* xs, in
   constexpr int G = K / 16;                          // codes: 16-column scale groups per row
   constexpr int CHUNKS = K / 128, MT = GM_ROWS / 16, PL = 3;
   constexpr int STAGE = MT * PL * GI_SC / 2;  // 16-byte pieces each thread stages per stage
-  constexpr int GM_AHEAD = 2;                 // chunks of weights on their way (one stage)
-  static_assert(GM_AHEAD == GI_SC && CHUNKS % GI_SC == 0, "K a multiple of 256");
+  static_assert(AHEAD % GI_SC == 0 && CHUNKS % GI_SC == 0, "K a multiple of 256");
   __shared__ uint32_t qtab[KIND == 4 ? QTAB_WORDS : 1];
   __shared__ __attribute__((aligned(16))) int8_t bt[MT * PL * 16 * GI_PITCH];
   // XCD-aware order: workgroup i of the launch runs on XCD i % 8; passes p with p % 8 == xcd are dealt to it
@@ -1181,16 +1207,16 @@ __global__ void __launch_bounds__(256, 2) grouped_i8_kernel(const int8_t* xs, in
   // staging: piece j of thread tid is tile j / PL, plane j % PL, row tid >> 4, the 16 bytes at column 16 (tid & 15)
   // of the stage's 256
   const int srow_t = tid >> 4, sseg = tid & 15;
-  const size_t srow_at = (size_t)first * K + 16 * sseg;
+  size_t xr[MT];  // where each tile's staged row starts in a plane
+#pragma unroll
+  for (int mt = 0; mt < MT; mt++)
+    xr[mt] = plane_row(order, k_order, xrows, first + min(m0 + 16 * mt + srow_t, rows - 1)) * K + 16 * sseg;
   i32x4 stg[STAGE];
   auto stage_load = [&](int s) {
 #pragma unroll
     for (int j = 0; j < STAGE; j++) {
       const int mt = j / PL, t = j % PL;
-      if (mt < tiles) {
-        const int r = min(m0 + 16 * mt + srow_t, rows - 1);
-        stg[j] = *(const i32x4*)(xs + t * plane + srow_at + (size_t)r * K + 128 * GI_SC * s);
-      }
+      if (mt < tiles) stg[j] = *(const i32x4*)(xs + t * plane + xr[mt] + 128 * GI_SC * s);
     }
   };
   auto stage_store = [&]() {
@@ -1219,9 +1245,9 @@ __global__ void __launch_bounds__(256, 2) grouped_i8_kernel(const int8_t* xs, in
     for (int mt = 0; mt < MT; mt++)
 #pragma unroll
       for (int t = 0; t < PL; t++) acc[a][mt][t] = i32x4{0, 0, 0, 0};
-  // one chunk (half `h` of its stage): its weights (loaded GM_AHEAD chunks ahead into `bytes`, which then take chunk
-  // ch + GM_AHEAD's) as int8 operands, the slot filled, the products from LDS; after the stage's second chunk the
-  // next stage's rows (requested with the first chunk) go into LDS
+  // one chunk (half `h` of its stage): its weights (loaded AHEAD chunks ahead into `bytes`, which then take chunk
+  // ch + AHEAD's) as int8 operands, the slot filled, the products from LDS; after the stage's second chunk the next
+  // stage's rows (requested with the first chunk) go into LDS
   auto chunk = [&](int ch, int h, ChunkBytes (&bytes)[RA]) {
     const int k0 = 128 * ch + 32 * q;
     if (filler) {  // the expert's bytes copied into its slot as they are read
@@ -1257,7 +1283,7 @@ __global__ void __launch_bounds__(256, 2) grouped_i8_kernel(const int8_t* xs, in
       }
     }
     if (h == 0 && ch + GI_SC < CHUNKS) stage_load(ch / GI_SC + 1);
-    if (ch + GM_AHEAD < CHUNKS) load_chunk(ch + GM_AHEAD, bytes);
+    if (ch + AHEAD < CHUNKS) load_chunk(ch + AHEAD, bytes);
 #pragma unroll
     for (int st = 0; st < 2; st++)
 #pragma unroll
@@ -1279,22 +1305,24 @@ __global__ void __launch_bounds__(256, 2) grouped_i8_kernel(const int8_t* xs, in
       __syncthreads();
     }
   };
-  ChunkBytes ring[GM_AHEAD][RA];  // chunk ch's weight bytes in ring[ch % GM_AHEAD]
+  ChunkBytes ring[AHEAD][RA];  // chunk ch's weight bytes in ring[ch % AHEAD]
   stage_load(0);
 #pragma unroll
-  for (int d = 0; d < GM_AHEAD; d++) load_chunk(d, ring[d]);
+  for (int d = 0; d < AHEAD; d++)
+    if (d < CHUNKS) load_chunk(d, ring[d]);
   stage_store();
   __syncthreads();
-  for (int ch = 0; ch < CHUNKS; ch += GM_AHEAD) {
+  for (int ch = 0; ch < CHUNKS; ch += AHEAD) {
 #pragma unroll
-    for (int d = 0; d < GM_AHEAD; d++) chunk(ch + d, d, ring[d]);
+    for (int d = 0; d < AHEAD; d++)
+      if (ch + d < CHUNKS) chunk(ch + d, d % GI_SC, ring[d]);
   }
   // lane l holds rows nw + 16 a + 4 q .. + 3 of activation row m0 + 16 mt + (l & 15)
 #pragma unroll
   for (int mt = 0; mt < MT; mt++) {
     const int r = m0 + 16 * mt + c;
     if (mt < tiles && r < rows) {
-      const float sx = xscale[first + r];
+      const float sx = xscale[plane_row(order, k_order, xrows, first + r)];
 #pragma unroll
       for (int a = 0; a < RA; a++) {
         f32x4 o;
@@ -2209,28 +2237,37 @@ int d3_grouped_plan(const int32_t* groups, int32_t n_groups, int64_t rows, int32
   return done("d3_grouped_plan");
 }
 
-int d3_grouped_mfma(int32_t kind, const void* planes, int32_t n_planes, int64_t plane, const int32_t* groups,
-                    int32_t n_groups, const int32_t* work, int64_t work_ints, int32_t fills_first, void* slot_w,
-                    void* slot_s, void* slot_c, const void* host_w, const void* host_s, const void* host_c,
-                    const float* codebook, float* out, int32_t N, int32_t K, void* stream) {
+// the planes' rows and the pass rows' checks shared by d3_grouped_mfma and d3_grouped_i8; 0 when they fit
+static int check_rows(const char* what, int64_t plane, int32_t K, const int64_t* order, int32_t k, int32_t rows) {
+  if (!supported_k(K) || plane < K || plane % K || plane / K > INT32_MAX)
+    return fail(std::string(what) + ": K in {256..2048}, plane a multiple of K, under 2^31 rows");
+  if (rows < 1 || (order ? k < 1 : rows > plane / K))
+    return fail(std::string(what) + ": 1 <= rows (<= plane / K without order), k >= 1 with order");
+  return 0;
+}
+
+int d3_grouped_mfma(int32_t kind, const void* planes, int32_t n_planes, int64_t plane, const int64_t* order,
+                    int32_t k, int32_t rows, const int32_t* groups, int32_t n_groups, const int32_t* work,
+                    int64_t work_ints, int32_t fills_first, void* slot_w, void* slot_s, void* slot_c,
+                    const void* host_w, const void* host_s, const void* host_c, const float* codebook, float* out,
+                    int32_t N, int32_t K, void* stream) {
   if (!planes || !groups || !work || !slot_w || !slot_s || !host_w || !host_s || !out)
     return fail("d3_grouped_mfma: null pointer");
   if ((kind == 4 || kind == 6) && (!slot_c || !host_c)) return fail("d3_grouped_mfma: codes need channel scales");
   if (kind == 4 && !codebook) return fail("d3_grouped_mfma: 4 bits need a codebook");
   if (n_planes != 1 && n_planes != 3) return fail("d3_grouped_mfma: 1 or 3 planes");
   if (n_groups < 1) return 0;
-  if (N < 64 || N % (kind == 1 ? 128 : 64) || !supported_k(K) || plane < K || plane % K)
-    return fail("d3_grouped_mfma: N % 64 == 0 (N % 128 == 0 for fp8), K in {256..2048}, plane a multiple of K");
-  const int64_t T = plane / K;
-  if (T > INT32_MAX) return fail("d3_grouped_mfma: more than 2^31 rows");
-  const int64_t need = d3_grouped_mfma_work_ints(n_groups, T);
+  if (N < 64 || N % (kind == 1 ? 128 : 64)) return fail("d3_grouped_mfma: N % 64 == 0 (N % 128 == 0 for fp8)");
+  if (const int e = check_rows("d3_grouped_mfma", plane, K, order, k, rows)) return e;
+  const int xrows = (int)(plane / K);
+  const int64_t need = d3_grouped_mfma_work_ints(n_groups, rows);
   if (work_ints < need) return fail("d3_grouped_mfma: work holds fewer than d3_grouped_mfma_work_ints ints");
   const int cap = (int)((need - 2) / 2), firsts = (n_groups + 7) / 8 * 8;
   const hipStream_t s = (hipStream_t)stream;
   const __bf16* xs = (const __bf16*)planes;
   const uint8_t* hw = (const uint8_t*)host_w;
   uint8_t* sw = (uint8_t*)slot_w;
-#define D3_GM(KD, RA, PL, PH, Y) D3_K_SWITCH(K, hipLaunchKernelGGL((grouped_mfma_kernel<KD, KK, RA, PL>), dim3(N / (64 * RA), Y), dim3(256), 0, s, xs, plane, groups, work, PH, sw, slot_s, slot_c, hw, host_s, host_c, codebook, out, N))
+#define D3_GM(KD, RA, PL, PH, Y) D3_K_SWITCH(K, hipLaunchKernelGGL((grouped_mfma_kernel<KD, KK, RA, PL>), dim3(N / (64 * RA), Y), dim3(256), 0, s, xs, plane, order, k, xrows, groups, work, PH, sw, slot_s, slot_c, hw, host_s, host_c, codebook, out, N))
 // two 16-row tiles per wave where N allows, one for W6 (its decode is the heaviest: at 128 registers a SIMD holds
 // twice the waves, so one's decode overlaps another's loads and products)
 #define D3_GM_RA(KD, PH, Y)                                                                            \
@@ -2260,11 +2297,17 @@ int d3_grouped_mfma(int32_t kind, const void* planes, int32_t n_planes, int64_t 
 }
 
 int d3_expert_groups(const int64_t* ids, int32_t P, int32_t E, int64_t* order, int32_t* inverse, int32_t* groups,
-                     void* stream) {
+                     int32_t* work, int64_t work_ints, void* stream) {
   if (!groups || (P > 0 && (!ids || !order || !inverse))) return fail("d3_expert_groups: null pointer");
   if (P < 0 || E < 1 || E > GROUPS_MAX_E) return fail("d3_expert_groups: 1 <= E <= 1024, P >= 0");
+  int cap = 0;
+  if (work) {
+    const int64_t need = d3_grouped_mfma_work_ints(E, P);
+    if (work_ints < need) return fail("d3_expert_groups: work holds fewer than d3_grouped_mfma_work_ints ints");
+    cap = (int)((need - 2) / 2);
+  }
   hipLaunchKernelGGL(expert_groups_kernel, dim3(1), dim3(1024), 0, (hipStream_t)stream, ids, P, E, order, inverse,
-                     groups);
+                     groups, work, cap);
   return done("d3_expert_groups");
 }
 
@@ -2317,36 +2360,37 @@ int d3_prep_planes_i8(int32_t mode, int32_t rotate, const void* x, const int64_t
   return done("d3_prep_planes_i8");
 }
 
-int d3_grouped_i8(int32_t kind, const void* planes, const float* scales, int64_t plane, const int32_t* groups,
-                  int32_t n_groups, const int32_t* work, int64_t work_ints, int32_t fills_first, void* slot_w,
-                  void* slot_s, void* slot_c, const void* host_w, const void* host_s, const void* host_c,
-                  const float* codebook, float* out, int32_t N, int32_t K, void* stream) {
+int d3_grouped_i8(int32_t kind, const void* planes, const float* scales, int64_t plane, const int64_t* order,
+                  int32_t k, int32_t rows, const int32_t* groups, int32_t n_groups, const int32_t* work,
+                  int64_t work_ints, int32_t fills_first, void* slot_w, void* slot_s, void* slot_c,
+                  const void* host_w, const void* host_s, const void* host_c, const float* codebook, float* out,
+                  int32_t N, int32_t K, void* stream) {
   if (!planes || !scales || !groups || !work || !slot_w || !slot_s || !host_w || !host_s || !out)
     return fail("d3_grouped_i8: null pointer");
   if (kind != 0 && kind != 4 && kind != 6) return fail("d3_grouped_i8: kind 0, 4 or 6");
   if (kind != 0 && (!slot_c || !host_c)) return fail("d3_grouped_i8: codes need channel scales");
   if (kind == 4 && !codebook) return fail("d3_grouped_i8: 4 bits need a codebook");
   if (n_groups < 1) return 0;
-  if (N < 64 || N % 64 || !supported_k(K) || plane < K || plane % K)
-    return fail("d3_grouped_i8: N % 64 == 0, K in {256..2048}, plane a multiple of K");
-  const int64_t T = plane / K;
-  if (T > INT32_MAX) return fail("d3_grouped_i8: more than 2^31 rows");
-  const int64_t need = d3_grouped_mfma_work_ints(n_groups, T);
+  if (N < 64 || N % 64) return fail("d3_grouped_i8: N % 64 == 0");
+  if (const int e = check_rows("d3_grouped_i8", plane, K, order, k, rows)) return e;
+  const int xrows = (int)(plane / K);
+  const int64_t need = d3_grouped_mfma_work_ints(n_groups, rows);
   if (work_ints < need) return fail("d3_grouped_i8: work holds fewer than d3_grouped_mfma_work_ints ints");
   const int cap = (int)((need - 2) / 2), firsts = (n_groups + 7) / 8 * 8;
   const hipStream_t s = (hipStream_t)stream;
   const int8_t* xs = (const int8_t*)planes;
   const uint8_t* hw = (const uint8_t*)host_w;
   uint8_t* sw = (uint8_t*)slot_w;
-#define D3_GI(KD, RA, PH, Y) D3_K_SWITCH(K, hipLaunchKernelGGL((grouped_i8_kernel<KD, KK, RA>), dim3(N / (64 * RA), Y), dim3(256), 0, s, xs, plane, scales, groups, work, PH, sw, slot_s, slot_c, hw, host_s, host_c, codebook, out, N))
-// two 16-row tiles per wave where N allows
-#define D3_GI_RA(KD, PH, Y) \
-  if (N % 128 == 0) { D3_GI(KD, 2, PH, Y); } else { D3_GI(KD, 1, PH, Y); }
-#define D3_GI_KIND(PH, Y)                        \
-  switch (kind) {                                \
-    case 0: D3_GI_RA(0, PH, Y); break;           \
-    case 4: D3_GI_RA(4, PH, Y); break;           \
-    default: D3_GI_RA(6, PH, Y); break;          \
+#define D3_GI(KD, RA, PH, Y) D3_K_SWITCH(K, hipLaunchKernelGGL((grouped_i8_kernel<KD, KK, RA, 2>), dim3(N / (64 * RA), Y), dim3(256), 0, s, xs, plane, scales, order, k, xrows, groups, work, PH, sw, slot_s, slot_c, hw, host_s, host_c, codebook, out, N))
+// int8: two 16-row tiles per wave where N allows; the codes one (their decode takes the registers and the vector
+// unit: more waves per SIMD hide it better)
+#define D3_GI_KIND(PH, Y)                                                           \
+  switch (kind) {                                                                   \
+    case 0:                                                                         \
+      if (N % 128 == 0) { D3_GI(0, 2, PH, Y); } else { D3_GI(0, 1, PH, Y); }         \
+      break;                                                                        \
+    case 4: D3_GI(4, 1, PH, Y); break;                                              \
+    default: D3_GI(6, 1, PH, Y); break;                                             \
   }
   if (fills_first) {
     D3_GI_KIND(0, firsts);
@@ -2355,7 +2399,6 @@ int d3_grouped_i8(int32_t kind, const void* planes, const float* scales, int64_t
     D3_GI_KIND(2, cap);
   }
 #undef D3_GI_KIND
-#undef D3_GI_RA
 #undef D3_GI
   return done("d3_grouped_i8");
 }

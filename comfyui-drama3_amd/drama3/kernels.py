@@ -156,31 +156,34 @@ def grouped_plan(groups, rows):
     return work
 
 
-def grouped_planes(kind, planes, rows, width, groups, work, slot_fields, host_fields, codebook, n, fills_first=False):
-    """[rows, n] float32: the grouped products on the matrix cores over planes [1 or 3, rows * width] bf16
-    (prep_planes / split) and the plan `work` (grouped_plan); kind "int8", "fp8", "w4" or "w6". fills_first: every
-    group's first pass before the others, which then read a filled group from its slot."""
+def grouped_planes(kind, planes, rows, width, groups, work, slot_fields, host_fields, codebook, n, fills_first=False,
+                   order=None, k=1):
+    """[rows, n] float32: the grouped products on the matrix cores over planes [1 or 3, R * width] bf16
+    (prep_planes / split, or bf16 rows themselves as one plane) and the plan `work` (grouped_plan); kind "int8",
+    "fp8", "w4" or "w6". Row p of the groups' rows is the planes' row p, or with `order` [rows] int64 their row
+    order[p] // k. fills_first: every group's first pass before the others, which then read a filled group from its
+    slot."""
     code, wkey = GROUPED_KINDS[kind]
     out = torch.empty((rows, n), dtype=torch.float32, device=planes.device)
     if rows == 0:
         return out
-    _call("d3_grouped_mfma", code, _p(planes), planes.shape[0], rows * width, _p(groups), groups.shape[0], _p(work),
-          work.shape[0], int(fills_first), *_grouped_fields(slot_fields, host_fields, codebook, wkey), _p(out), n,
-          width, _stream(planes))
+    _call("d3_grouped_mfma", code, _p(planes), planes.shape[0], planes.shape[1], _p(order), int(k), rows,
+          _p(groups), groups.shape[0], _p(work), work.shape[0], int(fills_first),
+          *_grouped_fields(slot_fields, host_fields, codebook, wkey), _p(out), n, width, _stream(planes))
     return out
 
 
 def grouped_i8(kind, planes, scales, rows, width, groups, work, slot_fields, host_fields, codebook, n,
-               fills_first=False):
-    """grouped_planes on the int8 matrix cores for kind "int8", "w4" or "w6", over (planes [3, rows * width] int8,
-    scales [rows] float32) from prep_planes_i8."""
+               fills_first=False, order=None, k=1):
+    """grouped_planes on the int8 matrix cores for kind "int8", "w4" or "w6", over (planes [3, R * width] int8,
+    scales [R] float32) from prep_planes_i8."""
     code, wkey = GROUPED_KINDS[kind]
     out = torch.empty((rows, n), dtype=torch.float32, device=planes.device)
     if rows == 0:
         return out
-    _call("d3_grouped_i8", code, _p(planes), _p(scales), rows * width, _p(groups), groups.shape[0], _p(work),
-          work.shape[0], int(fills_first), *_grouped_fields(slot_fields, host_fields, codebook, wkey), _p(out), n,
-          width, _stream(planes))
+    _call("d3_grouped_i8", code, _p(planes), _p(scales), planes.shape[1], _p(order), int(k), rows, _p(groups),
+          groups.shape[0], _p(work), work.shape[0], int(fills_first),
+          *_grouped_fields(slot_fields, host_fields, codebook, wkey), _p(out), n, width, _stream(planes))
     return out
 
 
@@ -206,10 +209,11 @@ def _grouped(kind, x, groups, slot_fields, host_fields, codebook, n, wkey, matri
     return out
 
 
-def expert_groups(topk_idx, num_experts):
+def expert_groups(topk_idx, num_experts, plan=False):
     """(order [P] int64, inverse [P] int32, groups [num_experts, 5] int32) of a prompt's pairs topk_idx [T, k] int64:
     each expert's pairs together, experts ascending; inverse = each pair's place in order; groups (e, e, 0, first,
-    rows). On the device, no host sync."""
+    rows). With `plan`, also the grouped products' work list over them (grouped_plan's) from the same launch. On the
+    device, no host sync."""
     ids = topk_idx.reshape(-1).contiguous()
     if ids.dtype != torch.int64:
         ids = ids.long()
@@ -217,8 +221,13 @@ def expert_groups(topk_idx, num_experts):
     order = torch.empty(P, dtype=torch.int64, device=ids.device)
     inverse = torch.empty(P, dtype=torch.int32, device=ids.device)
     groups = torch.empty((num_experts, 5), dtype=torch.int32, device=ids.device)
-    _call("d3_expert_groups", _p(ids), P, num_experts, _p(order), _p(inverse), _p(groups), _stream(ids))
-    return order, inverse, groups
+    work, ints = None, 0
+    if plan:
+        ints = _lib.lib().d3_grouped_mfma_work_ints(num_experts, P)
+        work = torch.empty(ints, dtype=torch.int32, device=ids.device)
+    _call("d3_expert_groups", _p(ids), P, num_experts, _p(order), _p(inverse), _p(groups), _p(work), ints,
+          _stream(ids))
+    return (order, inverse, groups, work) if plan else (order, inverse, groups)
 
 
 def prep_planes(x, rotate, order=None, k=1, swiglu=False, n_planes=3):

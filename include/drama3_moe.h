@@ -232,27 +232,33 @@ int d3_grouped(int32_t kind, const float* x, const int32_t* groups, int32_t n_gr
  * split into three bf16 planes, by d3_split_bf16x3 (x [n] float32, n % 8 == 0 -> planes bf16 [3, n] = hi, mid, lo)
  * or d3_prep_planes: x == hi + mid + lo to within 2^-24 |x|, and every weight of these formats is a bf16 value
  * exactly, so each product is exact and the sums float32. Rows that are bf16 already take one plane (n_planes 1).
- * d3_grouped_mfma reads planes [n_planes, plane] holding x [T, K] (plane = T * K elements per plane); N % 64 == 0
- * (N % 128 == 0 for fp8). work: int32 device memory of d3_grouped_mfma_work_ints(n_groups, T) ints, filled by
- * d3_grouped_plan for these groups and T (one plan serves both banks of a layer): passes of up to 32 rows, a group
- * whose rows lie outside [0, T) skipped. fills_first: the groups' first passes run first, then the others read a
- * filled group from its slot, so an expert copied in crosses the bus once however many rows it has. */
+ * d3_grouped_mfma reads planes [n_planes, plane] (plane a multiple of K: plane / K rows of K elements per plane) and
+ * writes out [rows, N]: row p of the groups' rows is the planes' row p (order NULL, rows <= plane / K), or with
+ * order [rows] int64 the planes' row order[p] / k (a prompt's pairs read from its token rows, no gathered copy; kept
+ * below plane / K). N % 64 == 0 (N % 128 == 0 for fp8). work: int32 device memory of
+ * d3_grouped_mfma_work_ints(n_groups, rows) ints, filled by d3_grouped_plan (or d3_expert_groups) for these groups
+ * and rows (one plan serves both banks of a layer): passes of up to 32 rows, a group whose rows lie outside
+ * [0, rows) skipped. fills_first: the groups' first passes run first, then the others read a filled group from its
+ * slot, so an expert copied in crosses the bus once however many rows it has. */
 int d3_split_bf16x3(const float* x, int64_t n, void* planes, void* stream);
 int64_t d3_grouped_mfma_work_ints(int32_t n_groups, int64_t rows);
 int d3_grouped_plan(const int32_t* groups, int32_t n_groups, int64_t rows, int32_t* work, int64_t work_ints,
                     void* stream);
-int d3_grouped_mfma(int32_t kind, const void* planes, int32_t n_planes, int64_t plane, const int32_t* groups,
-                    int32_t n_groups, const int32_t* work, int64_t work_ints, int32_t fills_first, void* slot_w,
-                    void* slot_s, void* slot_c, const void* host_w, const void* host_s, const void* host_c,
-                    const float* codebook, float* out, int32_t N, int32_t K, void* stream);
+int d3_grouped_mfma(int32_t kind, const void* planes, int32_t n_planes, int64_t plane, const int64_t* order,
+                    int32_t k, int32_t rows, const int32_t* groups, int32_t n_groups, const int32_t* work,
+                    int64_t work_ints, int32_t fills_first, void* slot_w, void* slot_s, void* slot_c,
+                    const void* host_w, const void* host_s, const void* host_c, const float* codebook, float* out,
+                    int32_t N, int32_t K, void* stream);
 
 /* A prompt's (token, k) pairs grouped by expert (offload.py:140-143, which sorts ids and counts each expert's pairs):
  * ids [P] int64 (P = T * k, row-major); order [P] int64 = the pairs' indices, each expert's pairs together and the
  * experts in ascending order; inverse [P] int32 = each pair's place in order (-1 for an id outside [0, E), which is
  * placed after every group); groups [E, 5] int32 = (e, e, 0, first, rows). Within a group the pairs' order is not
- * fixed: each output row of the grouped products depends on its own row alone. E <= 1024; one workgroup. */
+ * fixed: each output row of the grouped products depends on its own row alone. E <= 1024; one workgroup. work (or
+ * NULL): the same launch also writes d3_grouped_plan's plan for these groups and P rows (work_ints >=
+ * d3_grouped_mfma_work_ints(E, P)), which no later change of the groups' slot and fill fields alters. */
 int d3_expert_groups(const int64_t* ids, int32_t P, int32_t E, int64_t* order, int32_t* inverse, int32_t* groups,
-                     void* stream);
+                     int32_t* work, int64_t work_ints, void* stream);
 
 /* The planes d3_grouped_mfma reads, from the rows themselves: planes bf16 [n_planes, P * K]; row p is x's row
  * order[p] / k (x's row p when order is NULL). mode 0: x float32 [., K]; 1: bf16 [., K]; 2: float32 gate | up
@@ -270,14 +276,16 @@ int d3_prep_planes(int32_t mode, int32_t rotate, int32_t n_planes, const void* x
  * [-127, 127] and |r| < 0.5 / 254^2 + 2^-24, S the smallest power of two with max |v| <= 127 S, so the planes hold each row
  * to within 1.25e-7 of its largest magnitude, and rows of integers times a power of two exactly. A row holding inf or
  * NaN gets S = NaN (its products NaN), an all-zero row S = 0. d3_grouped_i8 is d3_grouped_mfma over those planes
- * (plane = T * K bytes per plane, the same groups, work plan, fields and fills_first); each plane's sums are exact
+ * (plane bytes per plane, rows / order / k, groups, work plan, fields and fills_first alike; row p's scale is that
+ * of the planes' row it reads); each plane's sums are exact
  * int32, added in float32 at the end: out = scale * (S * (A0 + (A1 + A2 / 254) / 254)). N % 64 == 0. */
 int d3_prep_planes_i8(int32_t mode, int32_t rotate, const void* x, const int64_t* order, int32_t k, int32_t P,
                       int32_t K, void* planes, float* scales, void* stream);
-int d3_grouped_i8(int32_t kind, const void* planes, const float* scales, int64_t plane, const int32_t* groups,
-                  int32_t n_groups, const int32_t* work, int64_t work_ints, int32_t fills_first, void* slot_w,
-                  void* slot_s, void* slot_c, const void* host_w, const void* host_s, const void* host_c,
-                  const float* codebook, float* out, int32_t N, int32_t K, void* stream);
+int d3_grouped_i8(int32_t kind, const void* planes, const float* scales, int64_t plane, const int64_t* order,
+                  int32_t k, int32_t rows, const int32_t* groups, int32_t n_groups, const int32_t* work,
+                  int64_t work_ints, int32_t fills_first, void* slot_w, void* slot_s, void* slot_c,
+                  const void* host_w, const void* host_s, const void* host_c, const float* codebook, float* out,
+                  int32_t N, int32_t K, void* stream);
 
 /* The weighted sum over k (offload.py:144-149): out [T, H] = sum over j in order of weights[t, j] *
  * sorted_out[inverse[t k + j]] in float32 (pairs with inverse -1 left out), stored as float32 / bf16 / fp16

@@ -543,6 +543,31 @@ def test_grouped_mfma_many_rows(kind, N):
                       np.int32)
     _check_grouped(kind, rng, 6, N, 2048, 4, groups, int(sum(rows)), True)
 
+@pytest.mark.parametrize("kind", ["int8", "fp8", "w4", "w6"])
+def test_grouped_rows_through_order(kind):
+    """Pair p reading x's row order[p] // k through the products' `order` gives, bit for bit, what the same products
+    give over a gathered copy of the rows (a row's planes and scale depend on that row alone); with the plan from
+    the grouping's own launch."""
+    rng = np.random.default_rng(70 + len(kind))
+    E, N, K, T, k = 6, 256, 768, 40, 3
+    hf = fields_on(_bank(kind, rng, E, N, K))   # groups (e, e, ..): every expert read from "slot" e
+    idx = rng.integers(0, E, (T, k))
+    order, inverse, groups, work = kernels.expert_groups(dev(idx.astype(np.int64)), E, plan=True)
+    x = dev(rng.standard_normal((T, K)).astype(np.float32))
+    cb = dev(ref.default_codebook()) if kind == "w4" else None
+    P = T * k
+    if kind == "fp8":
+        x = x.to(torch.bfloat16)
+        got = kernels.grouped_planes(kind, x.view(1, -1), P, K, groups, work, hf, hf, None, N, order=order, k=k)
+        want = kernels.grouped_planes(kind, x[order // k].view(1, -1), P, K, groups, work, hf, hf, None, N)
+    else:
+        planes, scales = kernels.prep_planes_i8(x, True)
+        got = kernels.grouped_i8(kind, planes, scales, P, K, groups, work, hf, hf, cb, N, order=order, k=k)
+        planes, scales = kernels.prep_planes_i8(x[order // k], True)
+        want = kernels.grouped_i8(kind, planes, scales, P, K, groups, work, hf, hf, cb, N)
+    assert torch.equal(got, want)
+
+
 # ---------------------------------------------------------------------------------------------- the layer
 H, I, E = 2048, 768, 8
 
@@ -703,6 +728,23 @@ def test_expert_groups_without_host_sync():
     assert sorted(order.cpu().tolist()) == list(range(6)) and inverse[order].cpu().tolist() == list(range(6))
 
 
+def check_plan(work, groups, P, rows=32):
+    """work [2 + 2 cap] holds the plan of groups [g, 5] over P rows: every group with rows cut into passes (g, m0),
+    m0 = 0, 32, ..; work[0] passes, the work[1] first passes (m0 = 0) listed first, each part by tiles (1 to 2 of
+    16 rows), most first."""
+    tiles = lambda n: (min(n, rows) + 15) // 16  # noqa: E731
+    passes = [(g, m0) for g, (_, _, _, f, r) in enumerate(groups) if r > 0 and f >= 0 and f + r <= P
+              for m0 in range(0, r, rows)]
+    firsts = sorted(p for p in passes if p[1] == 0)
+    n, nf = int(work[0]), int(work[1])
+    assert n == len(passes) and nf == len(firsts)
+    got = [(int(work[2 + 2 * i]), int(work[3 + 2 * i])) for i in range(n)]
+    assert sorted(got[:nf]) == firsts and sorted(got[nf:]) == sorted(p for p in passes if p[1])
+    for part in (got[:nf], got[nf:]):
+        t = [tiles(groups[g][4] - m0) for g, m0 in part]
+        assert t == sorted(t, reverse=True)
+
+
 @pytest.mark.parametrize("E, T, k, zipf", [(128, 256, 8, True), (256, 2048, 8, True), (1024, 300, 4, False),
                                            (7, 1, 1, False), (64, 0, 8, False)])
 def test_expert_groups_kernel(E, T, k, zipf):
@@ -725,6 +767,11 @@ def test_expert_groups_kernel(E, T, k, zipf):
         f, r = g[e, 3], g[e, 4]
         assert sorted(order[f:f + r].tolist()) == want[f:f + r].tolist(), e
     assert np.array_equal(inverse[order], np.arange(flat.shape[0]))
+    # the plan from the same launch: what d3_grouped_plan makes of these groups, and the plan's own rule
+    o2, i2, g2, work = kernels.expert_groups(dev(idx.astype(np.int64)), E, plan=True)
+    assert np.array_equal(g2.cpu().numpy(), g)
+    check_plan(work.cpu().numpy(), g, flat.shape[0])
+    check_plan(kernels.grouped_plan(g2, flat.shape[0]).cpu().numpy(), g, flat.shape[0])
     if T:   # out-of-range ids: placed last, inverse -1
         bad = idx.copy()
         bad[0, 0], bad[-1, -1] = -3, E + 5
