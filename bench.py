@@ -609,7 +609,7 @@ def run_resident_prompt(args, fmt, device):
               "mfma_ops_per_s_e12": round(flops * L * args.steps / (ms * 1e-3) / 1e12, 2),
               "mfma_type": "bf16" if args.format == "fp8" else "int8"}
     return (ms, step_bytes * args.steps, args.steps * L, args.steps * T, config,
-            "route + resident_prefill (d3::grouped_i8_kernel / grouped_mfma_kernel per bank, 9 launches)", None)
+            "route + resident_prefill (d3::grouped_i8_kernel / grouped_fp8_kernel per bank, 7 launches)", None)
 
 
 def run_resident(args, fmt, device):

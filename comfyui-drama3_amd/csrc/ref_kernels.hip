@@ -826,53 +826,14 @@ struct ChunkBytes {
   uint32_t sb0, sb1;
 };
 
-// eight int8 weights (two words, byte i = column i) or eight e4m3 weights as bf16
-template <int KIND> D3_INLINE bf16x8 weights8(uint32_t w0, uint32_t w1) {
+// eight e4m3 weights (two words, byte i = column i) as bf16: exact, e4m3 has 3 mantissa bits
+D3_INLINE bf16x8 fp8x8_to_bf16(uint32_t w0, uint32_t w1) {
+  const f32x2 p0 = fp8x2_to_f32<false>(w0), p1 = fp8x2_to_f32<true>(w0);
+  const f32x2 p2 = fp8x2_to_f32<false>(w1), p3 = fp8x2_to_f32<true>(w1);
   bf16x8 a;
-  if constexpr (KIND == 0) {
-#pragma unroll
-    for (int j = 0; j < 8; j++) a[j] = (__bf16)(float)(int8_t)(((j < 4 ? w0 : w1) >> (8 * (j & 3))) & 0xFFu);
-  } else {
-    const f32x2 p0 = fp8x2_to_f32<false>(w0), p1 = fp8x2_to_f32<true>(w0);
-    const f32x2 p2 = fp8x2_to_f32<false>(w1), p3 = fp8x2_to_f32<true>(w1);
-    a[0] = (__bf16)p0.x; a[1] = (__bf16)p0.y; a[2] = (__bf16)p1.x; a[3] = (__bf16)p1.y;
-    a[4] = (__bf16)p2.x; a[5] = (__bf16)p2.y; a[6] = (__bf16)p3.x; a[7] = (__bf16)p3.y;
-  }
+  a[0] = (__bf16)p0.x; a[1] = (__bf16)p0.y; a[2] = (__bf16)p1.x; a[3] = (__bf16)p1.y;
+  a[4] = (__bf16)p2.x; a[5] = (__bf16)p2.y; a[6] = (__bf16)p3.x; a[7] = (__bf16)p3.y;
   return a;
-}
-
-// W6: one 16-code group's int8-grid values (decode_group<6>'s arithmetic: clamp(rint((code - 32) * s), +-127), with
-// (code - 32) * s formed exactly as code * s - 32 s) as bf16, codes 0-7 in a0, 8-15 in a1. lo / hi: the nibble words
-// of codes 0-7 / 8-15 (code j's low nibble at bits 4 (j & 7)); high: code j's top two bits at bits 2j. Codes k, k + 4,
-// k + 8, k + 12 are assembled together, one per byte: their nibbles by one byte permute, their top bits by a shift.
-D3_INLINE void w6_group(uint32_t lo, uint32_t hi, uint32_t high, float s, bf16x8& a0, bf16x8& a1) {
-  const float ms = -32.0f * s;
-#pragma unroll
-  for (int k = 0; k < 4; k++) {
-    const uint32_t h = k >> 1, sel = h | ((h + 2) << 8) | ((h + 4) << 16) | ((h + 6) << 24);
-    const uint32_t p = __builtin_amdgcn_perm(hi, lo, sel);  // bytes: lo[h], lo[h + 2], hi[h], hi[h + 2]
-    const uint32_t code = ((k & 1 ? p >> 4 : p) & 0x0F0F0F0Fu) | (((high >> (2 * k)) & 0x03030303u) << 4);
-#pragma unroll
-    for (int b = 0; b < 4; b++) {
-      const float q = fminf(fmaxf(rintf(fmaf((float)((code >> (8 * b)) & 0xFFu), s, ms)), -127.0f), 127.0f);
-      if (b < 2) a0[k + 4 * b] = (__bf16)q;
-      else a1[k + 4 * (b - 2)] = (__bf16)q;
-    }
-  }
-}
-
-// W4: one 16-code group's int8-grid values as bf16 through the group's scale-byte row t of the LDS table (build_qtab:
-// decode_group<4>'s values, entry by entry), codes 0-7 in a0, 8-15 in a1; lo / hi the nibble words as for w6_group.
-D3_INLINE void w4_group(uint32_t lo, uint32_t hi, i32x4 t, bf16x8& a0, bf16x8& a1) {
-  const uint32_t w[4] = {lookup16(t, lo) ^ 0x80808080u, lookup16(t, lo >> 4) ^ 0x80808080u,   // codes 0,2,4,6 / 1,3,5,7
-                         lookup16(t, hi) ^ 0x80808080u, lookup16(t, hi >> 4) ^ 0x80808080u};  // 8,10,.. / 9,11,..
-#pragma unroll
-  for (int b = 0; b < 4; b++) {
-    a0[2 * b] = (__bf16)(float)(int8_t)(w[0] >> (8 * b));
-    a0[2 * b + 1] = (__bf16)(float)(int8_t)(w[1] >> (8 * b));
-    a1[2 * b] = (__bf16)(float)(int8_t)(w[2] >> (8 * b));
-    a1[2 * b + 1] = (__bf16)(float)(int8_t)(w[3] >> (8 * b));
-  }
 }
 
 // The row of the planes that row p of the passes reads: p itself, or with `order` x's row order[p] / k (the rows of
@@ -881,25 +842,22 @@ D3_INLINE size_t plane_row(const int64_t* order, int k, int xrows, int p) {
   return order ? (size_t)min(max((int)order[p], 0) / k, xrows - 1) : (size_t)p;
 }
 
+// The fp8 grouped products on the bf16 matrix cores, over PL bf16 planes of the rows (1: bf16 rows as they are).
 // grid (N / (64 RA), a multiple of 8 rows): the workgroups of one pass run on one XCD (the dispatcher deals
 // workgroup i to XCD i % 8), where its activation rows stay in that XCD's L2. PHASE 2 runs every pass of the plan;
 // PHASE 0 the first passes, PHASE 1 the others, a filled group's then read from its slot (the first passes filled it).
-template <int KIND, int K, int RA, int PL>  // KIND 0 int8, 1 fp8, 4 / 6 codes; RA row tiles per wave; PL planes
-__global__ void __launch_bounds__(256, 2) grouped_mfma_kernel(const __bf16* xs, int64_t plane, const int64_t* order,
-                                                              int k_order, int xrows, const int* groups,
-                                                              const int* work, int phase, uint8_t* slot_w, void* slot_s,
-                                                              void* slot_c, const uint8_t* host_w, const void* host_s,
-                                                              const void* host_c, const float* codebook, float* out,
-                                                              int N) {
-  constexpr int RB = KIND <= 1 ? K : K * KIND / 8;  // row bytes
-  constexpr int G = K / 16;                          // codes: 16-column scale groups per row
+template <int K, int RA, int PL>  // RA row tiles per wave; PL planes
+__global__ void __launch_bounds__(256, 2) grouped_fp8_kernel(const __bf16* xs, int64_t plane, const int64_t* order,
+                                                             int k_order, int xrows, const int* groups,
+                                                             const int* work, int phase, uint8_t* slot_w,
+                                                             float* slot_s, const uint8_t* host_w,
+                                                             const float* host_s, float* out, int N) {
   constexpr int CHUNKS = K / 128, MT = GM_ROWS / 16;
   constexpr int STAGE = MT * PL;   // 16-byte pieces each thread stages per chunk
   // chunks whose weights are on their way while one is multiplied (more gain nothing: the loads complete in order,
   // and each chunk waits for the next chunk's rows, requested after the weights one chunk ahead)
   constexpr int GM_AHEAD = 2;
   static_assert(CHUNKS % GM_AHEAD == 0, "K a multiple of 256");
-  __shared__ uint32_t qtab[KIND == 4 ? QTAB_WORDS : 1];
   __shared__ __attribute__((aligned(16))) __bf16 bt[MT * PL * 16 * GM_PAD];
   // XCD-aware order: workgroup i of the launch runs on XCD i % 8; passes p with p % 8 == xcd are dealt to it
   const int nx = gridDim.x, lin = blockIdx.x + nx * blockIdx.y, xcd = lin & 7, k = lin >> 3;
@@ -912,31 +870,16 @@ __global__ void __launch_bounds__(256, 2) grouped_mfma_kernel(const __bf16* xs, 
   const int tiles = min(MT, (rows - m0 + 15) / 16);
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, q = lane >> 4, c = lane & 15;
   const int nw = xb * 64 * RA + 16 * RA * w;  // the wave's first row
-  if constexpr (KIND == 4) build_qtab(qtab, *(const f32x4*)(codebook + 4 * (tid & 3)));
   const size_t src = host ? (size_t)expert : (size_t)slot;  // the expert's index in the fields it is read from
-  const uint8_t* arow = (host ? host_w : slot_w) + (src * N + nw + c) * RB;      // this lane's row of tile 0
-  uint8_t* frow = filler ? slot_w + ((size_t)slot * N + nw + c) * RB : slot_w;  // its slot row (fill)
-  const uint8_t* srow = nullptr;                                                 // codes: its scale bytes
-  if constexpr (KIND >= 4) srow = (const uint8_t*)(host ? host_s : slot_s) + (src * N + nw + c) * G;
+  const uint8_t* arow = (host ? host_w : slot_w) + (src * N + nw + c) * K;      // this lane's row of tile 0
+  uint8_t* frow = filler ? slot_w + ((size_t)slot * N + nw + c) * K : slot_w;  // its slot row (fill)
   auto load_chunk = [&](int ch, ChunkBytes (&cb)[RA]) {
     const int k0 = 128 * ch + 32 * q;
 #pragma unroll
     for (int a = 0; a < RA; a++) {
-      const uint8_t* r = arow + (size_t)16 * a * RB;
-      if constexpr (KIND <= 1) {
-        cb[a].b0 = *(const i32x4*)(r + k0);
-        cb[a].b1 = *(const i32x4*)(r + k0 + 16);
-      } else {
-        cb[a].b0 = *(const i32x4*)(r + k0 / 2);
-        cb[a].b1 = i32x4{0, 0, 0, 0};
-        if constexpr (KIND == 6) {
-          const i32x2 hw = *(const i32x2*)(r + K / 2 + k0 / 4);
-          cb[a].b1.x = hw.x;
-          cb[a].b1.y = hw.y;
-        }
-        cb[a].sb0 = srow[16 * a * G + k0 / 16];
-        cb[a].sb1 = srow[16 * a * G + k0 / 16 + 1];
-      }
+      const uint8_t* r = arow + (size_t)16 * a * K;
+      cb[a].b0 = *(const i32x4*)(r + k0);
+      cb[a].b1 = *(const i32x4*)(r + k0 + 16);
     }
   };
   // staging: piece j of thread tid is tile j / PL, plane j % PL, row (tid >> 4) & 15, the 16 bytes at column
@@ -960,83 +903,43 @@ __global__ void __launch_bounds__(256, 2) grouped_mfma_kernel(const __bf16* xs, 
       if (j < PL * tiles) *(i32x4*)(bt + (j * 16 + srow_t) * GM_PAD + 8 * sseg) = stg[j];
     }
   };
-  // the epilogue's scales of rows nw + 16 a + 4 q .. + 3: int8 row scales, codes channel scales
-  float es[RA][4];
-#pragma unroll
-  for (int a = 0; a < RA; a++)
-#pragma unroll
-    for (int r = 0; r < 4; r++) es[a][r] = 1.0f;
-  if constexpr (KIND != 1) {
-    const float* s = (const float*)(KIND == 0 ? (host ? host_s : slot_s) : (host ? host_c : slot_c)) + src * N;
-    float* fs = (float*)(KIND == 0 ? slot_s : slot_c) + (size_t)slot * N;
-#pragma unroll
-    for (int a = 0; a < RA; a++)
-#pragma unroll
-      for (int r = 0; r < 4; r++) {
-        es[a][r] = s[nw + 16 * a + 4 * q + r];
-        if (filler && c == 0) fs[nw + 16 * a + 4 * q + r] = es[a][r];
-      }
-  }
-  // fp8: the 128 x 128 block scales of the wave's row block (its 16 RA <= 64 rows lie in one), one per chunk
-  const float* sblk = nullptr;
-  if constexpr (KIND == 1) {
-    const size_t srows = (size_t)(N / 128) * CHUNKS, boff = (size_t)(nw / 128) * CHUNKS;
-    sblk = (const float*)(host ? host_s : slot_s) + src * srows + boff;
-    if (filler && nw % 128 == 0 && lane < CHUNKS) ((float*)slot_s)[(size_t)slot * srows + boff + lane] = sblk[lane];
-  }
+  // the 128 x 128 block scales of the wave's row block (its 16 RA <= 64 rows lie in one), one per chunk
+  const size_t srows = (size_t)(N / 128) * CHUNKS, boff = (size_t)(nw / 128) * CHUNKS;
+  const float* sblk = (host ? host_s : slot_s) + src * srows + boff;
+  if (filler && nw % 128 == 0 && lane < CHUNKS) slot_s[(size_t)slot * srows + boff + lane] = sblk[lane];
   f32x4 acc[RA][MT];
 #pragma unroll
   for (int a = 0; a < RA; a++)
 #pragma unroll
     for (int mt = 0; mt < MT; mt++) acc[a][mt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   // one chunk: its weights (loaded GM_AHEAD chunks ahead into `bytes`, which then take chunk ch + GM_AHEAD's)
-  // decoded, the slot filled, the next chunk's rows on their way, the products from LDS, then the next chunk's rows
-  // into LDS
+  // widened, the slot filled, the next chunk's rows on their way, the products from LDS scaled by the chunk's block
+  // scale, then the next chunk's rows into LDS
   auto chunk = [&](int ch, ChunkBytes (&bytes)[RA]) {
     const int k0 = 128 * ch + 32 * q;
     if (filler) {  // the expert's bytes copied into its slot as they are read
 #pragma unroll
       for (int a = 0; a < RA; a++) {
-        uint8_t* f = frow + (size_t)16 * a * RB;
-        if constexpr (KIND <= 1) {
-          *(i32x4*)(f + k0) = bytes[a].b0;
-          *(i32x4*)(f + k0 + 16) = bytes[a].b1;
-        } else {
-          *(i32x4*)(f + k0 / 2) = bytes[a].b0;
-          if constexpr (KIND == 6) *(i32x2*)(f + K / 2 + k0 / 4) = i32x2{bytes[a].b1.x, bytes[a].b1.y};
-          uint8_t* fsb = (uint8_t*)slot_s + ((size_t)slot * N + nw + 16 * a + c) * G;
-          fsb[k0 / 16] = (uint8_t)bytes[a].sb0;
-          fsb[k0 / 16 + 1] = (uint8_t)bytes[a].sb1;
-        }
+        uint8_t* f = frow + (size_t)16 * a * K;
+        *(i32x4*)(f + k0) = bytes[a].b0;
+        *(i32x4*)(f + k0 + 16) = bytes[a].b1;
       }
     }
     bf16x8 wa[RA][4];
 #pragma unroll
     for (int a = 0; a < RA; a++) {
-      if constexpr (KIND <= 1) {
-        wa[a][0] = weights8<KIND>((uint32_t)bytes[a].b0.x, (uint32_t)bytes[a].b0.y);
-        wa[a][1] = weights8<KIND>((uint32_t)bytes[a].b0.z, (uint32_t)bytes[a].b0.w);
-        wa[a][2] = weights8<KIND>((uint32_t)bytes[a].b1.x, (uint32_t)bytes[a].b1.y);
-        wa[a][3] = weights8<KIND>((uint32_t)bytes[a].b1.z, (uint32_t)bytes[a].b1.w);
-      } else if constexpr (KIND == 4) {
-        w4_group((uint32_t)bytes[a].b0.x, (uint32_t)bytes[a].b0.y, *(const i32x4*)(qtab + 4 * bytes[a].sb0),
-                 wa[a][0], wa[a][1]);
-        w4_group((uint32_t)bytes[a].b0.z, (uint32_t)bytes[a].b0.w, *(const i32x4*)(qtab + 4 * bytes[a].sb1),
-                 wa[a][2], wa[a][3]);
-      } else {
-        w6_group((uint32_t)bytes[a].b0.x, (uint32_t)bytes[a].b0.y, (uint32_t)bytes[a].b1.x,
-                 fp8x2_to_f32<false>(bytes[a].sb0).x, wa[a][0], wa[a][1]);
-        w6_group((uint32_t)bytes[a].b0.z, (uint32_t)bytes[a].b0.w, (uint32_t)bytes[a].b1.y,
-                 fp8x2_to_f32<false>(bytes[a].sb1).x, wa[a][2], wa[a][3]);
-      }
+      wa[a][0] = fp8x8_to_bf16((uint32_t)bytes[a].b0.x, (uint32_t)bytes[a].b0.y);
+      wa[a][1] = fp8x8_to_bf16((uint32_t)bytes[a].b0.z, (uint32_t)bytes[a].b0.w);
+      wa[a][2] = fp8x8_to_bf16((uint32_t)bytes[a].b1.x, (uint32_t)bytes[a].b1.y);
+      wa[a][3] = fp8x8_to_bf16((uint32_t)bytes[a].b1.z, (uint32_t)bytes[a].b1.w);
     }
     if (ch + GM_AHEAD < CHUNKS) load_chunk(ch + GM_AHEAD, bytes);
     if (ch + 1 < CHUNKS) stage_load(ch + 1);
-    f32x4 part[RA][MT];  // fp8: this chunk's sums before its block scale
+    f32x4 part[RA][MT];  // this chunk's sums before its block scale
 #pragma unroll
     for (int a = 0; a < RA; a++)
 #pragma unroll
-      for (int mt = 0; mt < MT; mt++) part[a][mt] = KIND == 1 ? f32x4{0.0f, 0.0f, 0.0f, 0.0f} : acc[a][mt];
+      for (int mt = 0; mt < MT; mt++) part[a][mt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int st = 0; st < 4; st++)
 #pragma unroll
@@ -1053,20 +956,13 @@ __global__ void __launch_bounds__(256, 2) grouped_mfma_kernel(const __bf16* xs, 
               part[a][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa[a][st], b[t], part[a][mt], 0, 0, 0);
         }
       }
-    if constexpr (KIND == 1) {
-      const float sc = sblk[ch];
+    const float sc = sblk[ch];
 #pragma unroll
-      for (int a = 0; a < RA; a++)
+    for (int a = 0; a < RA; a++)
 #pragma unroll
-        for (int mt = 0; mt < MT; mt++)
+      for (int mt = 0; mt < MT; mt++)
 #pragma unroll
-          for (int i = 0; i < 4; i++) acc[a][mt][i] = fmaf(sc, part[a][mt][i], acc[a][mt][i]);
-    } else {
-#pragma unroll
-      for (int a = 0; a < RA; a++)
-#pragma unroll
-        for (int mt = 0; mt < MT; mt++) acc[a][mt] = part[a][mt];
-    }
+        for (int i = 0; i < 4; i++) acc[a][mt][i] = fmaf(sc, part[a][mt][i], acc[a][mt][i]);
     if (ch + 1 < CHUNKS) {
       __syncthreads();  // every wave is done with this chunk's rows
       stage_store();
@@ -1089,11 +985,7 @@ __global__ void __launch_bounds__(256, 2) grouped_mfma_kernel(const __bf16* xs, 
     const int r = m0 + 16 * mt + c;
     if (mt < tiles && r < rows) {
 #pragma unroll
-      for (int a = 0; a < RA; a++) {
-        const f32x4 o = {acc[a][mt].x * es[a][0], acc[a][mt].y * es[a][1], acc[a][mt].z * es[a][2],
-                         acc[a][mt].w * es[a][3]};
-        *(f32x4*)(out + (size_t)(first + r) * N + nw + 16 * a + 4 * q) = o;
-      }
+      for (int a = 0; a < RA; a++) *(f32x4*)(out + (size_t)(first + r) * N + nw + 16 * a + 4 * q) = acc[a][mt];
     }
   }
 }
@@ -1104,11 +996,12 @@ __global__ void __launch_bounds__(256, 2) grouped_mfma_kernel(const __bf16* xs, 
 // and 64 columns a step), against the rows as three int8 planes (prep_i8_kernel). The weight bytes go in as they are
 // (int8) or as decoded bytes (codes); each plane's sums are exact int32 (|sum| <= 2048 * 127 * 127 < 2^25), and the
 // epilogue adds the planes in float32: out = es * (S * (A0 + (A1 + A2 / 254) / 254)). The work list, placement,
-// slot fill and weight ring are grouped_mfma_kernel's; lane group q takes columns 32 q .. 32 q + 31 of each
+// slot fill and weight ring are grouped_fp8_kernel's; lane group q takes columns 32 q .. 32 q + 31 of each
 // 128-column chunk in 2 steps of 16 bytes, weights and rows alike.
 
 // W4: one 16-code group's int8-grid values as bytes in column order (word d: codes 4d .. 4d + 3) through the
-// group's scale-byte row t of a signed table (build_qtab<true>); lo / hi as for w4_group
+// group's scale-byte row t of a signed table (build_qtab<true>); lo / hi: the nibble words of codes 0-7 / 8-15
+// (code j's nibble at bits 4 (j & 7))
 D3_INLINE i32x4 w4_group_i8(uint32_t lo, uint32_t hi, i32x4 t) {
   const uint32_t e0 = lookup16(t, lo), o0 = lookup16(t, lo >> 4);  // codes 0, 2, 4, 6 / 1, 3, 5, 7
   const uint32_t e1 = lookup16(t, hi), o1 = lookup16(t, hi >> 4);  // codes 8, 10, 12, 14 / 9, 11, 13, 15
@@ -1116,9 +1009,12 @@ D3_INLINE i32x4 w4_group_i8(uint32_t lo, uint32_t hi, i32x4 t) {
                (int)__builtin_amdgcn_perm(o1, e1, 0x05010400u), (int)__builtin_amdgcn_perm(o1, e1, 0x07030602u)};
 }
 
-// W6: one 16-code group's values (w6_group's arithmetic) as bytes in column order. rint(t) for |t| < 2^22 is the
-// low mantissa bits of t + 1.5 * 2^23 (round to nearest even, as rintf), two's complement; the clamp to +-127
-// happens on the biased value (NaN -> -127, as fmaxf / fminf give in w6_group).
+// W6: one 16-code group's int8-grid values (decode_group<6>'s arithmetic: clamp(rint((code - 32) * s), +-127), with
+// (code - 32) * s formed exactly as code * s - 32 s) as bytes in column order. lo / hi: the nibble words of codes
+// 0-7 / 8-15 (code j's low nibble at bits 4 (j & 7)); high: code j's top two bits at bits 2j. Codes k, k + 4, k + 8,
+// k + 12 are assembled together, one per byte: their nibbles by one byte permute, their top bits by a shift. rint(t)
+// for |t| < 2^22 is the low mantissa bits of t + 1.5 * 2^23 (round to nearest even, as rintf), two's complement; the
+// clamp to +-127 happens on the biased value (a NaN scale gives -127, as fmaxf / fminf do).
 D3_INLINE i32x4 w6_group_i8(uint32_t lo, uint32_t hi, uint32_t high, float s) {
   constexpr float MAGIC = 12582912.0f;
   const float ms = -32.0f * s;
@@ -2237,7 +2133,7 @@ int d3_grouped_plan(const int32_t* groups, int32_t n_groups, int64_t rows, int32
   return done("d3_grouped_plan");
 }
 
-// the planes' rows and the pass rows' checks shared by d3_grouped_mfma and d3_grouped_i8; 0 when they fit
+// the planes' rows and the pass rows' checks shared by d3_grouped_fp8 and d3_grouped_i8; 0 when they fit
 static int check_rows(const char* what, int64_t plane, int32_t K, const int64_t* order, int32_t k, int32_t rows) {
   if (!supported_k(K) || plane < K || plane % K || plane / K > INT32_MAX)
     return fail(std::string(what) + ": K in {256..2048}, plane a multiple of K, under 2^31 rows");
@@ -2246,54 +2142,39 @@ static int check_rows(const char* what, int64_t plane, int32_t K, const int64_t*
   return 0;
 }
 
-int d3_grouped_mfma(int32_t kind, const void* planes, int32_t n_planes, int64_t plane, const int64_t* order,
-                    int32_t k, int32_t rows, const int32_t* groups, int32_t n_groups, const int32_t* work,
-                    int64_t work_ints, int32_t fills_first, void* slot_w, void* slot_s, void* slot_c,
-                    const void* host_w, const void* host_s, const void* host_c, const float* codebook, float* out,
-                    int32_t N, int32_t K, void* stream) {
+int d3_grouped_fp8(const void* planes, int32_t n_planes, int64_t plane, const int64_t* order, int32_t k,
+                   int32_t rows, const int32_t* groups, int32_t n_groups, const int32_t* work, int64_t work_ints,
+                   int32_t fills_first, void* slot_w, void* slot_s, const void* host_w, const void* host_s,
+                   float* out, int32_t N, int32_t K, void* stream) {
   if (!planes || !groups || !work || !slot_w || !slot_s || !host_w || !host_s || !out)
-    return fail("d3_grouped_mfma: null pointer");
-  if ((kind == 4 || kind == 6) && (!slot_c || !host_c)) return fail("d3_grouped_mfma: codes need channel scales");
-  if (kind == 4 && !codebook) return fail("d3_grouped_mfma: 4 bits need a codebook");
-  if (n_planes != 1 && n_planes != 3) return fail("d3_grouped_mfma: 1 or 3 planes");
+    return fail("d3_grouped_fp8: null pointer");
+  if (n_planes != 1 && n_planes != 3) return fail("d3_grouped_fp8: 1 or 3 planes");
   if (n_groups < 1) return 0;
-  if (N < 64 || N % (kind == 1 ? 128 : 64)) return fail("d3_grouped_mfma: N % 64 == 0 (N % 128 == 0 for fp8)");
-  if (const int e = check_rows("d3_grouped_mfma", plane, K, order, k, rows)) return e;
+  if (N < 128 || N % 128) return fail("d3_grouped_fp8: N % 128 == 0");
+  if (const int e = check_rows("d3_grouped_fp8", plane, K, order, k, rows)) return e;
   const int xrows = (int)(plane / K);
   const int64_t need = d3_grouped_mfma_work_ints(n_groups, rows);
-  if (work_ints < need) return fail("d3_grouped_mfma: work holds fewer than d3_grouped_mfma_work_ints ints");
+  if (work_ints < need) return fail("d3_grouped_fp8: work holds fewer than d3_grouped_mfma_work_ints ints");
   const int cap = (int)((need - 2) / 2), firsts = (n_groups + 7) / 8 * 8;
   const hipStream_t s = (hipStream_t)stream;
   const __bf16* xs = (const __bf16*)planes;
   const uint8_t* hw = (const uint8_t*)host_w;
   uint8_t* sw = (uint8_t*)slot_w;
-#define D3_GM(KD, RA, PL, PH, Y) D3_K_SWITCH(K, hipLaunchKernelGGL((grouped_mfma_kernel<KD, KK, RA, PL>), dim3(N / (64 * RA), Y), dim3(256), 0, s, xs, plane, order, k, xrows, groups, work, PH, sw, slot_s, slot_c, hw, host_s, host_c, codebook, out, N))
-// two 16-row tiles per wave where N allows, one for W6 (its decode is the heaviest: at 128 registers a SIMD holds
-// twice the waves, so one's decode overlaps another's loads and products)
-#define D3_GM_RA(KD, PH, Y)                                                                            \
-  if (n_planes == 1) {                                                                                 \
-    if (N % 128 == 0 && KD != 6) { D3_GM(KD, 2, 1, PH, Y); } else { D3_GM(KD, 1, 1, PH, Y); }          \
-  } else {                                                                                             \
-    if (N % 128 == 0 && KD != 6) { D3_GM(KD, 2, 3, PH, Y); } else { D3_GM(KD, 1, 3, PH, Y); }          \
-  }
-#define D3_GM_KIND(PH, Y)                          \
-  switch (kind) {                                  \
-    case 0: D3_GM_RA(0, PH, Y); break;             \
-    case 1: D3_GM_RA(1, PH, Y); break;             \
-    case 4: D3_GM_RA(4, PH, Y); break;             \
-    case 6: D3_GM_RA(6, PH, Y); break;             \
-    default: return fail("d3_grouped_mfma: kind 0, 1, 4 or 6"); \
-  }
+  float* ss = (float*)slot_s;
+  const float* hs = (const float*)host_s;
+  // two 16-row tiles per wave
+#define D3_GF(PL, PH, Y) D3_K_SWITCH(K, hipLaunchKernelGGL((grouped_fp8_kernel<KK, 2, PL>), dim3(N / 128, Y), dim3(256), 0, s, xs, plane, order, k, xrows, groups, work, PH, sw, ss, hw, hs, out, N))
+#define D3_GF_PL(PH, Y) \
+  if (n_planes == 1) { D3_GF(1, PH, Y); } else { D3_GF(3, PH, Y); }
   if (fills_first) {
-    D3_GM_KIND(0, firsts);
-    D3_GM_KIND(1, cap);
+    D3_GF_PL(0, firsts);
+    D3_GF_PL(1, cap);
   } else {
-    D3_GM_KIND(2, cap);
+    D3_GF_PL(2, cap);
   }
-#undef D3_GM_KIND
-#undef D3_GM_RA
-#undef D3_GM
-  return done("d3_grouped_mfma");
+#undef D3_GF_PL
+#undef D3_GF
+  return done("d3_grouped_fp8");
 }
 
 int d3_expert_groups(const int64_t* ids, int32_t P, int32_t E, int64_t* order, int32_t* inverse, int32_t* groups,

@@ -77,9 +77,9 @@ SIGNATURES = {
     "d3_split_bf16x3": (c_int32, [c_void_p, c_int64, c_void_p, c_void_p]),
     "d3_grouped_mfma_work_ints": (c_int64, [c_int32, c_int64]),
     "d3_grouped_plan": (c_int32, [c_void_p, c_int32, c_int64, c_void_p, c_int64, c_void_p]),
-    "d3_grouped_mfma": (c_int32, [c_int32, c_void_p, c_int32, c_int64, c_void_p, c_int32, c_int32, c_void_p, c_int32,
-                                  c_void_p, c_int64, c_int32, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
-                                  c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_void_p]),
+    "d3_grouped_fp8": (c_int32, [c_void_p, c_int32, c_int64, c_void_p, c_int32, c_int32, c_void_p, c_int32, c_void_p,
+                                 c_int64, c_int32, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int32, c_int32,
+                                 c_void_p]),
     "d3_expert_groups": (c_int32, [c_void_p, c_int32, c_int32, c_void_p, c_void_p, c_void_p, c_void_p, c_int64,
                                    c_void_p]),
     "d3_prep_planes": (c_int32, [c_int32, c_int32, c_int32, c_void_p, c_void_p, c_int32, c_int32, c_int32, c_void_p,

@@ -156,27 +156,26 @@ def grouped_plan(groups, rows):
     return work
 
 
-def grouped_planes(kind, planes, rows, width, groups, work, slot_fields, host_fields, codebook, n, fills_first=False,
-                   order=None, k=1):
-    """[rows, n] float32: the grouped products on the matrix cores over planes [1 or 3, R * width] bf16
-    (prep_planes / split, or bf16 rows themselves as one plane) and the plan `work` (grouped_plan); kind "int8",
-    "fp8", "w4" or "w6". Row p of the groups' rows is the planes' row p, or with `order` [rows] int64 their row
-    order[p] // k. fills_first: every group's first pass before the others, which then read a filled group from its
-    slot."""
-    code, wkey = GROUPED_KINDS[kind]
+def grouped_fp8_planes(planes, rows, width, groups, work, slot_fields, host_fields, n, fills_first=False, order=None,
+                       k=1):
+    """[rows, n] float32: the fp8 grouped products on the bf16 matrix cores over planes [1 or 3, R * width] bf16
+    (prep_planes / split, or bf16 rows themselves as one plane) and the plan `work` (grouped_plan). Row p of the
+    groups' rows is the planes' row p, or with `order` [rows] int64 their row order[p] // k. fills_first: every
+    group's first pass before the others, which then read a filled group from its slot."""
     out = torch.empty((rows, n), dtype=torch.float32, device=planes.device)
     if rows == 0:
         return out
-    _call("d3_grouped_mfma", code, _p(planes), planes.shape[0], planes.shape[1], _p(order), int(k), rows,
-          _p(groups), groups.shape[0], _p(work), work.shape[0], int(fills_first),
-          *_grouped_fields(slot_fields, host_fields, codebook, wkey), _p(out), n, width, _stream(planes))
+    _call("d3_grouped_fp8", _p(planes), planes.shape[0], planes.shape[1], _p(order), int(k), rows, _p(groups),
+          groups.shape[0], _p(work), work.shape[0], int(fills_first), _p(slot_fields["weight"]),
+          _p(slot_fields["scale"]), _p(host_fields["weight"]), _p(host_fields["scale"]), _p(out), n, width,
+          _stream(planes))
     return out
 
 
 def grouped_i8(kind, planes, scales, rows, width, groups, work, slot_fields, host_fields, codebook, n,
                fills_first=False, order=None, k=1):
-    """grouped_planes on the int8 matrix cores for kind "int8", "w4" or "w6", over (planes [3, R * width] int8,
-    scales [R] float32) from prep_planes_i8."""
+    """The grouped products of kind "int8", "w4" or "w6" on the int8 matrix cores, over (planes [3, R * width] int8,
+    scales [R] float32) from prep_planes_i8; rows, order, k, work and fills_first as for grouped_fp8_planes."""
     code, wkey = GROUPED_KINDS[kind]
     out = torch.empty((rows, n), dtype=torch.float32, device=planes.device)
     if rows == 0:
@@ -200,8 +199,7 @@ def _grouped(kind, x, groups, slot_fields, host_fields, codebook, n, wkey, matri
                               codebook, n)
         planes = torch.empty((3, x.numel()), dtype=torch.bfloat16, device=x.device)
         _call("d3_split_bf16x3", _p(x), x.numel(), _p(planes), _stream(x))
-        return grouped_planes(name, planes, x.shape[0], x.shape[1], groups, work, slot_fields, host_fields, codebook,
-                              n)
+        return grouped_fp8_planes(planes, x.shape[0], x.shape[1], groups, work, slot_fields, host_fields, n)
     out = torch.empty((x.shape[0], n), dtype=torch.float32, device=x.device)
     if x.numel():
         _call("d3_grouped", kind, _p(x), _p(groups), groups.shape[0],
@@ -231,7 +229,7 @@ def expert_groups(topk_idx, num_experts, plan=False):
 
 
 def prep_planes(x, rotate, order=None, k=1, swiglu=False, n_planes=3):
-    """planes [n_planes, P * K] bf16 for grouped_planes: row p is x's row order[p] // k (x's row p without order),
+    """planes [n_planes, P * K] bf16 for grouped_fp8_planes: row p is x's row order[p] // k (x's row p without order),
     through SiLU(gate) * up first with `swiglu` (x float32 gate | up [., 2K]), in the ConvRot basis with `rotate`.
     n_planes 1 takes bf16 rows as they are (no rotation, no SwiGLU); 3 splits float32 values into hi + mid + lo."""
     x = x.contiguous()

@@ -228,27 +228,28 @@ int d3_grouped(int32_t kind, const float* x, const int32_t* groups, int32_t n_gr
                void* slot_c, const void* host_w, const void* host_s, const void* host_c, const float* codebook,
                float* out, int32_t N, int32_t K, void* stream);
 
-/* The same products on the bf16 matrix cores (same replacement, same fields and groups). The float32 rows are first
- * split into three bf16 planes, by d3_split_bf16x3 (x [n] float32, n % 8 == 0 -> planes bf16 [3, n] = hi, mid, lo)
- * or d3_prep_planes: x == hi + mid + lo to within 2^-24 |x|, and every weight of these formats is a bf16 value
- * exactly, so each product is exact and the sums float32. Rows that are bf16 already take one plane (n_planes 1).
- * d3_grouped_mfma reads planes [n_planes, plane] (plane a multiple of K: plane / K rows of K elements per plane) and
- * writes out [rows, N]: row p of the groups' rows is the planes' row p (order NULL, rows <= plane / K), or with
- * order [rows] int64 the planes' row order[p] / k (a prompt's pairs read from its token rows, no gathered copy; kept
- * below plane / K). N % 64 == 0 (N % 128 == 0 for fp8). work: int32 device memory of
- * d3_grouped_mfma_work_ints(n_groups, rows) ints, filled by d3_grouped_plan (or d3_expert_groups) for these groups
- * and rows (one plan serves both banks of a layer): passes of up to 32 rows, a group whose rows lie outside
- * [0, rows) skipped. fills_first: the groups' first passes run first, then the others read a filled group from its
- * slot, so an expert copied in crosses the bus once however many rows it has. */
+/* The same products on the matrix cores (same replacement, same fields and groups), for bank widths N % 64 == 0
+ * (fp8: N % 128 == 0): d3_grouped_fp8 for fp8 banks on the bf16 cores, d3_grouped_i8 (below) for int8 and the codes
+ * on the int8 cores. Both read the rows as planes [n_planes, plane] (plane a multiple of K: plane / K rows of K
+ * elements per plane) and write out [rows, N]: row p of the groups' rows is the planes' row p (order NULL, rows <=
+ * plane / K), or with order [rows] int64 the planes' row order[p] / k (a prompt's pairs read from its token rows,
+ * no gathered copy; kept below plane / K). work: int32 device memory of d3_grouped_mfma_work_ints(n_groups, rows)
+ * ints, filled by d3_grouped_plan (or d3_expert_groups) for these groups and rows (one plan serves both banks of a
+ * layer): passes of up to 32 rows, a group whose rows lie outside [0, rows) skipped. fills_first: the groups' first
+ * passes run first, then the others read a filled group from its slot, so an expert copied in crosses the bus once
+ * however many rows it has.
+ * d3_grouped_fp8's planes are bf16: bf16 rows as they are (n_planes 1), or float32 rows split into three bf16
+ * planes by d3_split_bf16x3 (x [n] float32, n % 8 == 0 -> planes bf16 [3, n] = hi, mid, lo) or d3_prep_planes:
+ * x == hi + mid + lo to within 2^-24 |x|, and every e4m3 weight is a bf16 value exactly, so each product is exact and
+ * the sums float32, each 128-column chunk's scaled by its 128 x 128 block scale. */
 int d3_split_bf16x3(const float* x, int64_t n, void* planes, void* stream);
 int64_t d3_grouped_mfma_work_ints(int32_t n_groups, int64_t rows);
 int d3_grouped_plan(const int32_t* groups, int32_t n_groups, int64_t rows, int32_t* work, int64_t work_ints,
                     void* stream);
-int d3_grouped_mfma(int32_t kind, const void* planes, int32_t n_planes, int64_t plane, const int64_t* order,
-                    int32_t k, int32_t rows, const int32_t* groups, int32_t n_groups, const int32_t* work,
-                    int64_t work_ints, int32_t fills_first, void* slot_w, void* slot_s, void* slot_c,
-                    const void* host_w, const void* host_s, const void* host_c, const float* codebook, float* out,
-                    int32_t N, int32_t K, void* stream);
+int d3_grouped_fp8(const void* planes, int32_t n_planes, int64_t plane, const int64_t* order, int32_t k,
+                   int32_t rows, const int32_t* groups, int32_t n_groups, const int32_t* work, int64_t work_ints,
+                   int32_t fills_first, void* slot_w, void* slot_s, const void* host_w, const void* host_s,
+                   float* out, int32_t N, int32_t K, void* stream);
 
 /* A prompt's (token, k) pairs grouped by expert (offload.py:140-143, which sorts ids and counts each expert's pairs):
  * ids [P] int64 (P = T * k, row-major); order [P] int64 = the pairs' indices, each expert's pairs together and the
@@ -260,7 +261,7 @@ int d3_grouped_mfma(int32_t kind, const void* planes, int32_t n_planes, int64_t 
 int d3_expert_groups(const int64_t* ids, int32_t P, int32_t E, int64_t* order, int32_t* inverse, int32_t* groups,
                      int32_t* work, int64_t work_ints, void* stream);
 
-/* The planes d3_grouped_mfma reads, from the rows themselves: planes bf16 [n_planes, P * K]; row p is x's row
+/* The planes d3_grouped_fp8 reads, from the rows themselves: planes bf16 [n_planes, P * K]; row p is x's row
  * order[p] / k (x's row p when order is NULL). mode 0: x float32 [., K]; 1: bf16 [., K]; 2: float32 gate | up
  * [., 2K] through SiLU(gate) * up (the SwiGLU between the banks, kernels.py:222-258). rotate: in the ConvRot basis
  * first (int8 and the codes; d3_rotate's transform). n_planes 3, or 1 for bf16 rows taken as they are (mode 1, no
@@ -273,12 +274,12 @@ int d3_prep_planes(int32_t mode, int32_t rotate, int32_t n_planes, const void* x
  * scale, so they enter the int8 products as bytes; the float32 rows enter as three int8 planes and a power-of-two row
  * scale S. d3_prep_planes_i8 takes the rows as d3_prep_planes does (mode, rotate, order, k) and writes planes int8
  * [3, P * K] = a0, a1, a2 and scales [P] float32: v / S = a0 + a1 / 254 + a2 / 254^2 + r with every a in
- * [-127, 127] and |r| < 0.5 / 254^2 + 2^-24, S the smallest power of two with max |v| <= 127 S, so the planes hold each row
- * to within 1.25e-7 of its largest magnitude, and rows of integers times a power of two exactly. A row holding inf or
- * NaN gets S = NaN (its products NaN), an all-zero row S = 0. d3_grouped_i8 is d3_grouped_mfma over those planes
- * (plane bytes per plane, rows / order / k, groups, work plan, fields and fills_first alike; row p's scale is that
- * of the planes' row it reads); each plane's sums are exact
- * int32, added in float32 at the end: out = scale * (S * (A0 + (A1 + A2 / 254) / 254)). N % 64 == 0. */
+ * [-127, 127] and |r| < 0.5 / 254^2 + 2^-24, S the smallest power of two with max |v| <= 127 S, so the planes hold
+ * each row to within 1.25e-7 of its largest magnitude, and rows of integers times a power of two exactly. A row
+ * holding inf or NaN gets S = NaN (its products NaN), an all-zero row S = 0. d3_grouped_i8 reads those planes (plane
+ * bytes per plane; rows, order, k, groups, work plan and fills_first as for d3_grouped_fp8; row p's scale is that of
+ * the planes' row it reads); each plane's sums are exact int32, added in float32 at the end: out = scale * (S * (A0
+ * + (A1 + A2 / 254) / 254)). N % 64 == 0. */
 int d3_prep_planes_i8(int32_t mode, int32_t rotate, const void* x, const int64_t* order, int32_t k, int32_t P,
                       int32_t K, void* planes, float* scales, void* stream);
 int d3_grouped_i8(int32_t kind, const void* planes, const float* scales, int64_t plane, const int64_t* order,

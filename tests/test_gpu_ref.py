@@ -558,8 +558,8 @@ def test_grouped_rows_through_order(kind):
     P = T * k
     if kind == "fp8":
         x = x.to(torch.bfloat16)
-        got = kernels.grouped_planes(kind, x.view(1, -1), P, K, groups, work, hf, hf, None, N, order=order, k=k)
-        want = kernels.grouped_planes(kind, x[order // k].view(1, -1), P, K, groups, work, hf, hf, None, N)
+        got = kernels.grouped_fp8_planes(x.view(1, -1), P, K, groups, work, hf, hf, N, order=order, k=k)
+        want = kernels.grouped_fp8_planes(x[order // k].view(1, -1), P, K, groups, work, hf, hf, N)
     else:
         planes, scales = kernels.prep_planes_i8(x, True)
         got = kernels.grouped_i8(kind, planes, scales, P, K, groups, work, hf, hf, cb, N, order=order, k=k)
