@@ -572,18 +572,24 @@ def test_grouped_rows_through_order(kind):
 H, I, E = 2048, 768, 8
 
 
-@pytest.mark.parametrize("matrix", [False, True], ids=["valu", "mfma"])
+@pytest.mark.parametrize("matrix, scales", [(False, "all"), (True, "all"), (True, "small")],
+                         ids=["valu", "mfma", "mfma-small-scales"])
 @pytest.mark.parametrize("kind", ["int8", "fp8", "w4", "w6"])
-def test_grouped_decodes_exactly(kind, matrix):
+def test_grouped_decodes_exactly(kind, matrix, scales):
     """One-hot activation rows (x = [I; I], K = 256 rows per expert) make each output one weight: out[t, n] = the
     dequantized weight of row n at column t, a single product rounded once to float32, so it must equal the oracle's
     weights (the int8 grid times the row or channel scale, e4m3 times the block scale) bit for bit. Pins the decode
-    (every code and scale byte the banks hold) through the grouped products, whatever the summation order."""
+    (every code and scale byte the banks hold) through the grouped products, whatever the summation order. "small":
+    the codes' scale bytes all within +-127 / 32, where no value reaches the clamp (a checkpoint's usual scales)."""
+    if scales == "small" and kind not in ("w4", "w6"):
+        pytest.skip("scale bytes of the code formats only")
     rng = np.random.default_rng(len(kind) + 7)
     E, N, K = 2, 128, 256
     host = _bank(kind, rng, E, N, K)
     if kind in ("w4", "w6"):   # every finite e4m3 scale byte, tiny (all codes to 0) to huge (all clamped to +-127)
         finite = np.array([b for b in range(256) if b & 0x7F != 0x7F], np.uint8)
+        if scales == "small":
+            finite = finite[np.abs(numerics.e4m3_decode(finite)) <= 127 / 32]
         host["scale"] = rng.choice(finite, size=host["scale"].shape)
     x = np.concatenate([np.eye(K, dtype=np.float32)] * E)
     groups = np.array([[e, -1, 0, e * K, K] for e in range(E)], np.int32)
@@ -685,6 +691,38 @@ def test_resident_prefill(layer):
                                    (2 * I, H), kind, dcbs, E)
     assert got.shape == (T, H) and got.dtype == torch.bfloat16
     assert_bf16_close(bits_of(got), ref.resident_prefill_ref(x, idx, w, banks, (2 * I, H), kind, cbs))
+
+
+def test_resident_prefill_graph_replays(layer):
+    """The prompt path captured in a HIP graph (grouping with its plan, planes, products, weighted sum; no host sync,
+    no memset) gives the eager result bit for bit on every replay, with new rows and routing copied in between."""
+    kind, banks, cbs, dbanks, dcbs = layer
+    rng = np.random.default_rng(23)
+    T, k = 40, 4
+    inputs = [(numerics.f32_to_bf16_bits(rng.standard_normal((T, H)).astype(np.float32)),
+               np.stack([rng.choice(E, k, replace=False) for _ in range(T)]),
+               numerics.bf16_round(rng.dirichlet(np.ones(k), T).astype(np.float32))) for _ in range(3)]
+    x_buf = dev(inputs[0][0]).view(torch.bfloat16).clone()
+    idx_buf = dev(inputs[0][1]).clone()
+    w_buf = dev(inputs[0][2]).to(torch.bfloat16)
+    run = lambda: offload.resident_prefill(x_buf, idx_buf, w_buf, dbanks, (2 * I, H), kind, dcbs, E)  # noqa: E731
+    run()   # constants exist before capture
+    stream = torch.cuda.Stream(DEV)
+    stream.wait_stream(torch.cuda.current_stream(DEV))
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        with torch.cuda.graph(g, stream=stream):
+            out = run()
+    torch.cuda.current_stream(DEV).wait_stream(stream)
+    for x, idx, w in inputs:
+        x_buf.copy_(dev(x).view(torch.bfloat16))
+        idx_buf.copy_(dev(idx))
+        w_buf.copy_(dev(w).to(torch.bfloat16))
+        g.replay()
+        torch.cuda.synchronize()
+        eager = run()
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), eager.view(torch.int16))
 
 
 def zipf_topk(rng, T, E, k, s=1.1):
