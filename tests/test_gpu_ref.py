@@ -572,17 +572,15 @@ def test_grouped_rows_through_order(kind):
 H, I, E = 2048, 768, 8
 
 
-@pytest.mark.parametrize("matrix, scales", [(False, "all"), (True, "all"), (True, "small")],
-                         ids=["valu", "mfma", "mfma-small-scales"])
-@pytest.mark.parametrize("kind", ["int8", "fp8", "w4", "w6"])
+@pytest.mark.parametrize("kind, matrix, scales",
+                         [(k, m, "all") for k in ("int8", "fp8", "w4", "w6") for m in (False, True)]
+                         + [("w4", True, "small"), ("w6", True, "small")])
 def test_grouped_decodes_exactly(kind, matrix, scales):
     """One-hot activation rows (x = [I; I], K = 256 rows per expert) make each output one weight: out[t, n] = the
     dequantized weight of row n at column t, a single product rounded once to float32, so it must equal the oracle's
     weights (the int8 grid times the row or channel scale, e4m3 times the block scale) bit for bit. Pins the decode
     (every code and scale byte the banks hold) through the grouped products, whatever the summation order. "small":
     the codes' scale bytes all within +-127 / 32, where no value reaches the clamp (a checkpoint's usual scales)."""
-    if scales == "small" and kind not in ("w4", "w6"):
-        pytest.skip("scale bytes of the code formats only")
     rng = np.random.default_rng(len(kind) + 7)
     E, N, K = 2, 128, 256
     host = _bank(kind, rng, E, N, K)
