@@ -1043,11 +1043,8 @@ D3_INLINE i32x4 w6_group_i8(uint32_t lo, uint32_t hi, uint32_t high, float s) {
 constexpr int GI_SC = 2;                   // chunks staged together: 256 columns of each row per stage
 constexpr int GI_PITCH = 128 * GI_SC + 16;  // LDS row stride in bytes: the 16 rows of a tile start 4 banks apart
 
-// KIND 0 int8, 4 / 6 codes; RA row tiles per wave; AHEAD chunks of weights on their way while one is multiplied
-// (a multiple of the stage's GI_SC: each stage's rows are requested before the weights, so the wait for them at the
-// stage's end leaves the weights in flight)
-template <int KIND, int K, int RA, int AHEAD, int OCC = 2>
-__global__ void __launch_bounds__(256, OCC) grouped_i8_kernel(const int8_t* xs, int64_t plane, const float* xscale,
+template <int KIND, int K, int RA>  // KIND 0 int8, 4 / 6 codes; RA row tiles per wave
+__global__ void __launch_bounds__(256, 2) grouped_i8_kernel(const int8_t* xs, int64_t plane, const float* xscale,
                                                             const int64_t* order, int k_order, int xrows,
                                                             const int* groups, const int* work, int phase,
                                                             uint8_t* slot_w, void* slot_s, void* slot_c,
@@ -1059,7 +1056,10 @@ __global__ void __launch_bounds__(256, OCC) grouped_i8_kernel(const int8_t* xs, 
   constexpr int G = K / 16;                          // codes: 16-column scale groups per row
   constexpr int CHUNKS = K / 128, MT = GM_ROWS / 16, PL = 3;
   constexpr int STAGE = MT * PL * GI_SC / 2;  // 16-byte pieces each thread stages per stage
-  static_assert(AHEAD % GI_SC == 0 && CHUNKS % GI_SC == 0, "K a multiple of 256");
+  // chunks of weights on their way while one is multiplied: one stage. Each stage's rows are requested before the
+  // weights, so the wait for them at the stage's end leaves the weights in flight (deeper measured no faster).
+  constexpr int AHEAD = GI_SC;
+  static_assert(CHUNKS % GI_SC == 0, "K a multiple of 256");
   __shared__ uint32_t qtab[KIND == 4 ? QTAB_WORDS : 1];
   __shared__ __attribute__((aligned(16))) int8_t bt[MT * PL * 16 * GI_PITCH];
   // XCD-aware order: workgroup i of the launch runs on XCD i % 8; passes p with p % 8 == xcd are dealt to it
@@ -1204,14 +1204,12 @@ __global__ void __launch_bounds__(256, OCC) grouped_i8_kernel(const int8_t* xs, 
   ChunkBytes ring[AHEAD][RA];  // chunk ch's weight bytes in ring[ch % AHEAD]
   stage_load(0);
 #pragma unroll
-  for (int d = 0; d < AHEAD; d++)
-    if (d < CHUNKS) load_chunk(d, ring[d]);
+  for (int d = 0; d < AHEAD; d++) load_chunk(d, ring[d]);
   stage_store();
   __syncthreads();
   for (int ch = 0; ch < CHUNKS; ch += AHEAD) {
 #pragma unroll
-    for (int d = 0; d < AHEAD; d++)
-      if (ch + d < CHUNKS) chunk(ch + d, d % GI_SC, ring[d]);
+    for (int d = 0; d < AHEAD; d++) chunk(ch + d, d, ring[d]);
   }
   // lane l holds rows nw + 16 a + 4 q .. + 3 of activation row m0 + 16 mt + (l & 15)
 #pragma unroll
@@ -2262,7 +2260,7 @@ int d3_grouped_i8(int32_t kind, const void* planes, const float* scales, int64_t
   const int8_t* xs = (const int8_t*)planes;
   const uint8_t* hw = (const uint8_t*)host_w;
   uint8_t* sw = (uint8_t*)slot_w;
-#define D3_GI(KD, RA, PH, Y) D3_K_SWITCH(K, hipLaunchKernelGGL((grouped_i8_kernel<KD, KK, RA, 2>), dim3(N / (64 * RA), Y), dim3(256), 0, s, xs, plane, scales, order, k, xrows, groups, work, PH, sw, slot_s, slot_c, hw, host_s, host_c, codebook, out, N))
+#define D3_GI(KD, RA, PH, Y) D3_K_SWITCH(K, hipLaunchKernelGGL((grouped_i8_kernel<KD, KK, RA>), dim3(N / (64 * RA), Y), dim3(256), 0, s, xs, plane, scales, order, k, xrows, groups, work, PH, sw, slot_s, slot_c, hw, host_s, host_c, codebook, out, N))
 // int8: two 16-row tiles per wave where N allows; the codes one (their decode takes the registers and the vector
 // unit: more waves per SIMD hide it better)
 #define D3_GI_KIND(PH, Y)                                                           \
