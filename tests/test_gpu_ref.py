@@ -568,6 +568,16 @@ def test_grouped_rows_through_order(kind):
     assert torch.equal(got, want)
 
 
+@pytest.mark.parametrize("K", [256, 512, 1536])
+@pytest.mark.parametrize("kind", ["int8", "w4", "w6"])
+def test_grouped_i8_widths(kind, K):
+    """The int8 cores at bank widths the layer does not use: N = 192 (one row tile per wave for int8 too) and the
+    other supported K, against the oracle at the grouped bar."""
+    rng = np.random.default_rng(len(kind) + K)
+    groups = np.array([[2, 0, 0, 0, 21], [4, 2, 1, 21, 7], [1, -1, 0, 28, 40], [0, -1, 0, 68, 3]], np.int32)
+    _check_grouped(kind, rng, 6, 192, K, 3, groups, 71, True)
+
+
 # ---------------------------------------------------------------------------------------------- the layer
 H, I, E = 2048, 768, 8
 
