@@ -558,10 +558,10 @@ __global__ void __launch_bounds__(256) split3_kernel(const float* x, int64_t n8,
   }
 }
 
-// work [2 + 2 cap] int32: [0] the number of passes, [1] how many of them are first passes (a group's rows 0 .. 63),
-// then (group, first row of the pass) per pass: the first passes, then the others; within each, the passes of 4 tiles
-// first, then those of 3, 2, 1. Groups that are empty or whose rows lie outside [0, T) get none; no more than cap
-// passes are listed. One workgroup.
+// work [2 + 2 cap] int32: [0] the number of passes, [1] how many of them are first passes (a group's rows
+// 0 .. GM_ROWS - 1), then (group, first row of the pass) per pass: the first passes, then the others; within each,
+// the passes with most tiles first. Groups that are empty or whose rows lie outside [0, T) get none; no more than cap
+// passes are listed; the products skip a place whose group is -1. One workgroup.
 // The plan in three steps for a workgroup: every group counted into its buckets (plan_count), the buckets' offsets
 // by one thread (plan_offsets), every group's passes put in place (plan_put), a barrier between the steps. count /
 // cursor: 8 LDS ints, bucket 4 - tiles (first passes), 8 - tiles (later passes).
@@ -864,6 +864,7 @@ __global__ void __launch_bounds__(256, 2) grouped_fp8_kernel(const __bf16* xs, i
   const int item = (k / nx) * 8 + xcd + (phase == 1 ? work[1] : 0), xb = k % nx;
   if (item >= work[phase == 0 ? 1 : 0]) return;
   const int g = work[2 + 2 * item], m0 = work[3 + 2 * item];
+  if (g < 0) return;  // an empty place of the list
   const int* gp = groups + 5 * g;
   const int expert = gp[0], slot = gp[1], fill = gp[2] && phase != 1, first = gp[3], rows = gp[4];
   const bool host = slot < 0 || fill, filler = fill && m0 == 0;  // the group's first pass copies it into its slot
@@ -1067,6 +1068,7 @@ __global__ void __launch_bounds__(256, 2) grouped_i8_kernel(const int8_t* xs, in
   const int item = (k / nx) * 8 + xcd + (phase == 1 ? work[1] : 0), xb = k % nx;
   if (item >= work[phase == 0 ? 1 : 0]) return;
   const int g = work[2 + 2 * item], m0 = work[3 + 2 * item];
+  if (g < 0) return;  // an empty place of the list
   const int* gp = groups + 5 * g;
   const int expert = gp[0], slot = gp[1], fill = gp[2] && phase != 1, first = gp[3], rows = gp[4];
   const bool host = slot < 0 || fill, filler = fill && m0 == 0;  // the group's first pass copies it into its slot
