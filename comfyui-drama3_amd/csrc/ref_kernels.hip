@@ -1056,7 +1056,8 @@ __global__ void __launch_bounds__(256, 2) grouped_i8_kernel(const int8_t* xs, in
   constexpr int RB = KIND == 0 ? K : K * KIND / 8;  // row bytes
   constexpr int G = K / 16;                          // codes: 16-column scale groups per row
   constexpr int CHUNKS = K / 128, MT = GM_ROWS / 16, PL = 3;
-  constexpr int STAGE = MT * PL * GI_SC / 2;  // 16-byte pieces each thread stages per stage
+  static_assert(GI_SC == 2, "a stage's row of 256 bytes is 16 threads' 16-byte pieces");
+  constexpr int STAGE = MT * PL;  // 16-byte pieces each thread stages per stage: tile-plane j, row tid >> 4
   // chunks of weights on their way while one is multiplied: one stage. Each stage's rows are requested before the
   // weights, so the wait for them at the stage's end leaves the weights in flight (deeper measured no faster).
   constexpr int AHEAD = GI_SC;
