@@ -618,8 +618,8 @@ __global__ void __launch_bounds__(256) grouped_plan_kernel(const int* groups, in
 // after every group, inverse -1. With `work`, the same workgroup also plans the grouped products' passes over the
 // groups (grouped_plan_kernel's plan, from the counts it holds), so that takes no launch of its own.
 constexpr int GROUPS_MAX_E = 1024;
-__global__ void __launch_bounds__(1024) expert_groups_kernel(const int64_t* ids, int P, int E, int64_t* order,
-                                                             int* inverse, int* groups, int* work, int cap) {
+D3_INLINE void expert_groups_body(const int64_t* ids, int P, int E, int64_t* order, int* inverse, int* groups,
+                                  int* work, int cap) {
   __shared__ int count[GROUPS_MAX_E + 1], cursor[GROUPS_MAX_E + 1], wave_total[16], pcount[8], pcursor[8];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   for (int e = tid; e <= E; e += 1024) count[e] = 0;
@@ -672,6 +672,11 @@ __global__ void __launch_bounds__(1024) expert_groups_kernel(const int64_t* ids,
     order[at] = p;
     inverse[p] = valid ? at : -1;
   }
+}
+
+__global__ void __launch_bounds__(1024) expert_groups_kernel(const int64_t* ids, int P, int E, int64_t* order,
+                                                             int* inverse, int* groups, int* work, int cap) {
+  expert_groups_body(ids, P, E, order, inverse, groups, work, cap);
 }
 
 // columns c0 .. c0 + 3 of row `row` of x as float (SRC as for prep_planes_kernel)
@@ -732,18 +737,19 @@ __global__ void __launch_bounds__(256) prep_planes_kernel(const void* x, const i
 // gets S = 0, a row holding a non-finite value S = NaN (planes 0 both ways); below 2^-143, S stays 2^-149.
 constexpr float I8_RATIO = 254.0f;  // the int8 planes' ratio
 
+// Row p of the planes by the row's 4 waves (w = 0 .. 3 of them, lane within the wave, tid0: the row's first thread;
+// wmax: 4 LDS words of the row); valid false: a row past the planes' end, which only joins the barrier. Every
+// thread of the workgroup takes the one barrier inside.
 template <int SRC, bool ROT>
-__global__ void __launch_bounds__(256) prep_i8_kernel(const void* x, const int64_t* order, int k, int K,
-                                                      int8_t* planes, int64_t plane, float* scales) {
-  __shared__ uint32_t wmax[4];
-  const int p = blockIdx.x, lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const size_t row = order ? (size_t)(order[p] / k) : (size_t)p;
+D3_INLINE void prep_i8_row(const void* x, const int64_t* order, int k, int K, int8_t* planes, int64_t plane,
+                           float* scales, int p, bool valid, int w, int lane, bool tid0, uint32_t* wmax) {
+  const size_t row = !valid ? 0 : order ? (size_t)(order[p] / k) : (size_t)p;
   float v[2][4];  // wave w's columns 256 g + 4 lane .. + 3 of g = w, w + 4 (K <= 2048)
   uint32_t m = 0u;  // the bits of max |v|: non-negative floats order as their bits, inf and NaN above every finite
 #pragma unroll
   for (int i = 0; i < 2; i++) {
     const int g = w + 4 * i;
-    if (g < K / 256) {
+    if (valid && g < K / 256) {
       load_row4<SRC>(x, row, K, 256 * g + 4 * lane, v[i]);
       if constexpr (ROT) fwht256(v[i]);
 #pragma unroll
@@ -753,6 +759,7 @@ __global__ void __launch_bounds__(256) prep_i8_kernel(const void* x, const int64
   m = wave_max_u32(m);
   if (lane == 0) wmax[w] = m;
   __syncthreads();
+  if (!valid) return;
   m = max(max(wmax[0], wmax[1]), max(wmax[2], wmax[3]));
   const bool split = m != 0u && m < 0x7F800000u;
   int e = 0;  // S = 2^e
@@ -761,7 +768,7 @@ __global__ void __launch_bounds__(256) prep_i8_kernel(const void* x, const int64
     e = max(ilogbf(mf) - 6, -149);  // mf / 2^e in [64, 128) (or below 64 for tiny rows)
     if (mf > ldexpf(127.0f, e)) e += 1;
   }
-  if (threadIdx.x == 0) scales[p] = split ? ldexpf(1.0f, e) : m == 0u ? 0.0f : __uint_as_float(0x7FC00000u);
+  if (tid0) scales[p] = split ? ldexpf(1.0f, e) : m == 0u ? 0.0f : __uint_as_float(0x7FC00000u);
 #pragma unroll
   for (int i = 0; i < 2; i++) {
     const int g = w + 4 * i;
@@ -785,6 +792,31 @@ __global__ void __launch_bounds__(256) prep_i8_kernel(const void* x, const int64
       d[plane / 2] = q2;
     }
   }
+}
+
+template <int SRC, bool ROT>
+__global__ void __launch_bounds__(256) prep_i8_kernel(const void* x, const int64_t* order, int k, int K,
+                                                      int8_t* planes, int64_t plane, float* scales) {
+  __shared__ uint32_t wmax[4];
+  prep_i8_row<SRC, ROT>(x, order, k, K, planes, plane, scales, blockIdx.x, true, threadIdx.x >> 6,
+                        threadIdx.x & 63, threadIdx.x == 0, wmax);
+}
+
+// The grouping (workgroup 0, expert_groups_kernel's) and the token rows' int8 planes (prep_i8_kernel's, 4 rows per
+// later workgroup) in one launch: neither waits for the other, so the planes cost no launch of their own.
+template <int SRC, bool ROT>
+__global__ void __launch_bounds__(1024) groups_prep_kernel(const int64_t* ids, int P, int E, int64_t* order,
+                                                           int* inverse, int* groups, int* work, int cap,
+                                                           const void* x, int T, int K, int8_t* planes,
+                                                           float* scales) {
+  if (blockIdx.x == 0) {
+    expert_groups_body(ids, P, E, order, inverse, groups, work, cap);
+    return;
+  }
+  __shared__ uint32_t wmax[4][4];
+  const int tid = threadIdx.x, r = tid >> 8, p = 4 * ((int)blockIdx.x - 1) + r;
+  prep_i8_row<SRC, ROT>(x, nullptr, 1, K, planes, (int64_t)T * K, scales, p, p < T, (tid >> 6) & 3, tid & 63,
+                        (tid & 255) == 0, wmax[r]);
 }
 
 // out[t, h] = sum over j in order of w[t, j] * sorted_out[inverse[t k + j], h] (pairs with inverse -1 left out), in
@@ -2141,6 +2173,31 @@ static int check_rows(const char* what, int64_t plane, int32_t K, const int64_t*
   if (rows < 1 || (order ? k < 1 : rows > plane / K))
     return fail(std::string(what) + ": 1 <= rows (<= plane / K without order), k >= 1 with order");
   return 0;
+}
+
+int d3_expert_groups_prep_i8(const int64_t* ids, int32_t P, int32_t E, int64_t* order, int32_t* inverse,
+                             int32_t* groups, int32_t* work, int64_t work_ints, int32_t mode, int32_t rotate,
+                             const void* x, int32_t T, int32_t K, void* planes, float* scales, void* stream) {
+  if (!groups || !work || (P > 0 && (!ids || !order || !inverse))) return fail("d3_expert_groups_prep_i8: null pointer");
+  if (P < 0 || E < 1 || E > GROUPS_MAX_E) return fail("d3_expert_groups_prep_i8: 1 <= E <= 1024, P >= 0");
+  if (T > 0 && (!x || !planes || !scales)) return fail("d3_expert_groups_prep_i8: null pointer");
+  if (T < 0 || (mode != 0 && mode != 1) || !supported_k(K))
+    return fail("d3_expert_groups_prep_i8: T >= 0, mode 0 (float32 rows) or 1 (bf16 rows), K in {256..2048}");
+  const int64_t need = d3_grouped_mfma_work_ints(E, P);
+  if (work_ints < need) return fail("d3_expert_groups_prep_i8: work holds fewer than d3_grouped_mfma_work_ints ints");
+  const int cap = (int)((need - 2) / 2);
+  const hipStream_t s = (hipStream_t)stream;
+  const dim3 grid(1 + (T + 3) / 4);
+  int8_t* pl = (int8_t*)planes;
+#define D3_GP(M, R) hipLaunchKernelGGL((groups_prep_kernel<M, R>), grid, dim3(1024), 0, s, ids, P, E, order, inverse, groups, work, cap, x, T, K, pl, scales)
+  switch (mode * 2 + (rotate ? 1 : 0)) {
+    case 0: D3_GP(0, false); break;
+    case 1: D3_GP(0, true); break;
+    case 2: D3_GP(1, false); break;
+    default: D3_GP(1, true); break;
+  }
+#undef D3_GP
+  return done("d3_expert_groups_prep_i8");
 }
 
 int d3_grouped_fp8(const void* planes, int32_t n_planes, int64_t plane, const int64_t* order, int32_t k,

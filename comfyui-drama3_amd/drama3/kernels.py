@@ -269,6 +269,28 @@ def prep_planes_i8(x, rotate, order=None, k=1, swiglu=False):
     return planes, scales
 
 
+def expert_groups_prep_i8(topk_idx, num_experts, x, rotate):
+    """expert_groups(topk_idx, num_experts, plan=True) and prep_planes_i8(x, rotate) (x [T, K] float32 or bf16 token
+    rows) in one launch: (order, inverse, groups, work, planes, scales)."""
+    ids = topk_idx.reshape(-1).contiguous()
+    if ids.dtype != torch.int64:
+        ids = ids.long()
+    x = x.contiguous()
+    if x.dtype != torch.bfloat16:
+        x = x.float()
+    P, (T, K) = ids.shape[0], x.shape
+    order = torch.empty(P, dtype=torch.int64, device=ids.device)
+    inverse = torch.empty(P, dtype=torch.int32, device=ids.device)
+    groups = torch.empty((num_experts, 5), dtype=torch.int32, device=ids.device)
+    ints = _lib.lib().d3_grouped_mfma_work_ints(num_experts, P)
+    work = torch.empty(ints, dtype=torch.int32, device=ids.device)
+    planes = torch.empty((3, T * K), dtype=torch.int8, device=x.device)
+    scales = torch.empty(T, dtype=torch.float32, device=x.device)
+    _call("d3_expert_groups_prep_i8", _p(ids), P, num_experts, _p(order), _p(inverse), _p(groups), _p(work), ints,
+          int(x.dtype == torch.bfloat16), int(rotate), _p(x), T, K, _p(planes), _p(scales), _stream(ids))
+    return order, inverse, groups, work, planes, scales
+
+
 _OUT_TYPES = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
 
 

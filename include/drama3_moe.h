@@ -282,6 +282,12 @@ int d3_prep_planes(int32_t mode, int32_t rotate, int32_t n_planes, const void* x
  * + (A1 + A2 / 254) / 254)). N % 64 == 0. */
 int d3_prep_planes_i8(int32_t mode, int32_t rotate, const void* x, const int64_t* order, int32_t k, int32_t P,
                       int32_t K, void* planes, float* scales, void* stream);
+/* d3_expert_groups (work required) and d3_prep_planes_i8 over x's T token rows (mode 0 float32 or 1 bf16, order
+ * NULL) in one launch, the grouping in its first workgroup and the rows in the others: a prompt's groups, plan,
+ * planes and row scales with no launch between them (offload.py:138-143 and the first bank's rows). */
+int d3_expert_groups_prep_i8(const int64_t* ids, int32_t P, int32_t E, int64_t* order, int32_t* inverse,
+                             int32_t* groups, int32_t* work, int64_t work_ints, int32_t mode, int32_t rotate,
+                             const void* x, int32_t T, int32_t K, void* planes, float* scales, void* stream);
 int d3_grouped_i8(int32_t kind, const void* planes, const float* scales, int64_t plane, const int64_t* order,
                   int32_t k, int32_t rows, const int32_t* groups, int32_t n_groups, const int32_t* work,
                   int64_t work_ints, int32_t fills_first, void* slot_w, void* slot_s, void* slot_c,

@@ -828,6 +828,28 @@ def test_expert_groups_kernel(E, T, k, zipf):
         assert inverse[0] == -1 and inverse[n - 1] == -1 and set(order[g[:, 4].sum():].tolist()) == {0, n - 1}
 
 
+@pytest.mark.parametrize("T, dtype", [(1, torch.bfloat16), (37, torch.float32), (256, torch.bfloat16)])
+def test_expert_groups_prep_i8(T, dtype):
+    """The grouping and the token rows' int8 planes in one launch: the same groups, pairs, plan and planes (bit for
+    bit) as d3_expert_groups and d3_prep_planes_i8 give separately."""
+    rng = np.random.default_rng(T)
+    E, k, K = 128, 8, 2048
+    idx = dev(np.stack([rng.choice(E, k, replace=False) for _ in range(T)]).astype(np.int64))
+    x = dev(rng.standard_normal((T, K)).astype(np.float32)).to(dtype)
+    order, inverse, groups, work, planes, scales = kernels.expert_groups_prep_i8(idx, E, x, True)
+    o2, i2, g2, w2 = kernels.expert_groups(idx, E, plan=True)
+    g = groups.cpu().numpy()
+    assert np.array_equal(g, g2.cpu().numpy())
+    check_plan(work.cpu().numpy(), g, T * k)
+    o, o2 = order.cpu().numpy(), o2.cpu().numpy()
+    for e in range(E):
+        f, r = g[e, 3], g[e, 4]
+        assert sorted(o[f:f + r].tolist()) == sorted(o2[f:f + r].tolist()), e
+    assert np.array_equal(inverse.cpu().numpy()[o], np.arange(T * k))
+    p2, s2 = kernels.prep_planes_i8(x, True)
+    assert torch.equal(planes, p2) and torch.equal(scales.view(torch.int32), s2.view(torch.int32))
+
+
 def test_fp8_experts_module():
     banks, _ = layer_banks("fp8", 90)
     mod = offload.FP8Experts(E, H, I, device=DEV, dtype=torch.bfloat16)
