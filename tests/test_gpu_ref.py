@@ -12,6 +12,7 @@ import torch
 from drama3 import _lib, kernels, offload
 from oracle import numerics
 from oracle import reference as ref
+from tests.planes_np import split_i8_np
 
 pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda:0")
@@ -175,24 +176,6 @@ def test_prep_planes(mode, rotate):
         h, m, l = split3_np(exact)
         assert np.array_equal(hi, h) and np.array_equal(mid, m) and np.array_equal(lo, l)
         assert np.all(np.abs(total - exact) <= 2.0 ** -24 * np.abs(exact))
-
-
-def split_i8_np(v):
-    """(a0, a1, a2 float32 [P, K], S [P]) of float32 rows v [P, K] as d3_prep_planes_i8 splits them: S the smallest
-    power of two with max |v| <= 127 S, a0 = rint(v / S), d = v / S - a0, a1 = rint(f32(254 d)), a2 = rint(f32(254
-    f32(254 d - a1))) with 254 d - a1 from the exact product (float64 holds it)."""
-    v = np.asarray(v, np.float32)
-    m = np.abs(v).max(axis=1)
-    e = np.frexp(m)[1].astype(np.int64) - 7
-    e = np.maximum(e, -149)
-    e = np.where(m > np.ldexp(np.float32(127), e).astype(np.float32), e + 1, e)
-    a = np.ldexp(v, -e[:, None]).astype(np.float32)
-    a0 = np.rint(a)
-    d = (a - a0).astype(np.float32)
-    a1 = np.rint((d * np.float32(254)).astype(np.float32))
-    r2 = (d.astype(np.float64) * 254 - a1).astype(np.float32)
-    a2 = np.rint((r2 * np.float32(254)).astype(np.float32))
-    return a0, a1, a2, np.ldexp(np.float32(1), e).astype(np.float32)
 
 
 @pytest.mark.parametrize("mode, rotate", [("f32", False), ("bf16", True), ("f32", True), ("swiglu", True),
