@@ -2252,7 +2252,7 @@ int d3_expert_groups(const int64_t* ids, int32_t P, int32_t E, int64_t* order, i
 
 int d3_prep_planes(int32_t mode, int32_t rotate, int32_t n_planes, const void* x, const int64_t* order, int32_t k,
                    int32_t P, int32_t K, void* planes, void* stream) {
-  if (!x || !planes) return fail("d3_prep_planes: null pointer");
+  if (P > 0 && (!x || !planes)) return fail("d3_prep_planes: null pointer");
   if (mode < 0 || mode > 2 || P < 0 || k < 1 || !supported_k(K)) return fail("d3_prep_planes: mode 0-2, K in {256..2048}");
   if (n_planes != 3 && !(n_planes == 1 && mode == 1 && !rotate))
     return fail("d3_prep_planes: 3 planes, or 1 for bf16 rows taken as they are");
@@ -2279,7 +2279,7 @@ int d3_prep_planes(int32_t mode, int32_t rotate, int32_t n_planes, const void* x
 
 int d3_prep_planes_i8(int32_t mode, int32_t rotate, const void* x, const int64_t* order, int32_t k, int32_t P,
                       int32_t K, void* planes, float* scales, void* stream) {
-  if (!x || !planes || !scales) return fail("d3_prep_planes_i8: null pointer");
+  if (P > 0 && (!x || !planes || !scales)) return fail("d3_prep_planes_i8: null pointer");
   if (mode < 0 || mode > 2 || P < 0 || k < 1 || !supported_k(K))
     return fail("d3_prep_planes_i8: mode 0-2, K in {256..2048}");
   if (P == 0) return 0;
@@ -2344,7 +2344,7 @@ int d3_grouped_i8(int32_t kind, const void* planes, const float* scales, int64_t
 
 int d3_combine_rows(const float* sorted_out, const int32_t* inverse, const void* weights, int32_t weights_bf16,
                     int32_t T, int32_t k, int32_t H, void* out, int32_t out_type, void* stream) {
-  if (!sorted_out || !inverse || !weights || !out) return fail("d3_combine_rows: null pointer");
+  if (T > 0 && (!sorted_out || !inverse || !weights || !out)) return fail("d3_combine_rows: null pointer");
   if (T < 0 || k < 1 || H < 4 || H % 4 || out_type < 0 || out_type > 2)
     return fail("d3_combine_rows: H % 4 == 0, out_type 0 float32, 1 bf16, 2 fp16");
   if (T == 0) return 0;

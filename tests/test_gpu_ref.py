@@ -684,6 +684,23 @@ def test_resident_prefill(layer):
     assert_bf16_close(bits_of(got), ref.resident_prefill_ref(x, idx, w, banks, (2 * I, H), kind, cbs))
 
 
+@pytest.mark.parametrize("T", [0, 1, 2])
+def test_resident_prefill_few_rows(layer, T):
+    """The prompt path at its edges: no rows (an empty [0, H] result, nothing launched past the grouping), and one or
+    two rows (every group a single partial tile) against the oracle."""
+    kind, banks, cbs, dbanks, dcbs = layer
+    rng = np.random.default_rng(40 + T)
+    k = 4
+    x = numerics.f32_to_bf16_bits(rng.standard_normal((T, H)).astype(np.float32))
+    idx = np.stack([rng.choice(E, k, replace=False) for _ in range(T)]) if T else np.zeros((0, k), np.int64)
+    w = numerics.bf16_round(rng.dirichlet(np.ones(k), T).astype(np.float32)) if T else np.zeros((0, k), np.float32)
+    got = offload.resident_prefill(dev(x).view(torch.bfloat16), dev(idx.astype(np.int64)), dev(w).to(torch.bfloat16),
+                                   dbanks, (2 * I, H), kind, dcbs, E)
+    assert got.shape == (T, H) and got.dtype == torch.bfloat16
+    if T:
+        assert_bf16_close(bits_of(got), ref.resident_prefill_ref(x, idx, w, banks, (2 * I, H), kind, cbs))
+
+
 def test_resident_prefill_graph_replays(layer):
     """The prompt path captured in a HIP graph (grouping with its plan, planes, products, weighted sum; no host sync,
     no memset) gives the eager result bit for bit on every replay, with new rows and routing copied in between."""
