@@ -12,7 +12,9 @@
 // folded into the activation slice, and wave sums go through DPP. The rotation runs in registers: H256 is the 4-fold
 // Kronecker power of h4, whose row r is +1 except -1 at column 3 - r, so each of the four base-4 digits of the column
 // index is one step y = (sum of the 4 values) - 2 * (the value at the mirrored digit), exchanged within a lane, a quad
-// (DPP), a row (DPP rotate / mirror) and the wave (shuffles).
+// (DPP), a row (DPP rotate / mirror) and the wave (shuffles). Many rows (a prompt) run on the matrix cores: int8 and
+// the codes on the int8 cores against the rows as three int8 planes with a power-of-two scale (grouped_i8_kernel),
+// FP8 on the bf16 cores against exact bf16 planes (grouped_fp8_kernel), each weight read once per 32-row pass.
 #include "common.hpp"
 #include "../../include/drama3_moe.h"
 
